@@ -1,0 +1,188 @@
+#!/usr/bin/env python3
+"""LoRA fine-tuning step benchmark on one MI355X.
+
+A step is the reference driver's optimizer step (gpt2_small_lora_finetune/
+src/main.cpp:456-505): for each micro-batch forward → lm_cross_entropy →
+backward with loss scaled by 1/accum, then global grad-norm clip, Adam on the
+LoRA parameters and zero_grad — here one fused device-resident pass in
+libmft_hip.so.  Default workload: BASELINE configs[1], GPT-2 medium,
+batch 2 × seq 128, grad_accum 2, LoRA r=8 α=16 on c_attn + attn c_proj,
+random-init weights N(0,0.02), LoRA A ~ N(0,1/r), B ~ N(0,0.02), token ids
+uniform in [0, vocab) from the seed (synthetic data; no dataset download).
+
+Prints ONE JSON line.  `value` = tokens/s of the whole job (accum·B·S tokens
+per step / measured step time), inputs already resident in HBM.
+`roofline` covers the dominant kernel (the linear-layer GEMM kernel family,
+fwd + dX, LoRA epilogue included), timed live with HIP events on the model's
+stream during the timed region.  `cpu_baseline` times the CPU port (oracle/,
+BLAS-backed GEMMs) on the host on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "LoRA fwd+bwd tokens/sec at 1 GPU; LoRA-linear & attention % of MFMA peak"
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8000.0        # GB/s, MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="gpt2m",
+                    help="gpt2s | gpt2m | gemma270m | qwen05b | gemma1b")
+    ap.add_argument("--seed", type=int, default=1235)
+    ap.add_argument("--lr", type=float, default=2e-4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-timing", action="store_true",
+                    help="skip the per-kernel HIP events (roofline becomes null)")
+    return ap.parse_args()
+
+
+def cpu_baseline(rc, seed, steps, threads):
+    """The CPU port (oracle/) with BLAS GEMMs, timed on the host."""
+    import numpy as np
+
+    import oracle as O
+    n = threads or min(16, os.cpu_count() or 1)
+    O.lib().orc_set_threads(n)
+    O.lib().orc_set_blas(1)
+    backend = O.lib().orc_blas_backend().decode()
+    mc = rc.model
+    om = O.OracleModel(mc)
+    rng = np.random.default_rng(seed)
+    for p in om.params:
+        name = p["name"]
+        if name.endswith("lora_A"):
+            v = rng.standard_normal(p["shape"], dtype=np.float32) / mc.lora_r
+        elif "norm" in name or "ln_" in name:
+            one = name.endswith("weight") and (mc.arch != 2)
+            v = np.ones(p["shape"], np.float32) if one else np.zeros(p["shape"], np.float32)
+        else:
+            v = rng.standard_normal(p["shape"], dtype=np.float32) * 0.02
+        if p["f16"]:
+            v = v.astype(np.float16).view(np.uint16)
+        om.set_param(name, v)
+    B, S, acc = rc.batch, rc.seq, rc.accum
+    ids = rng.integers(0, mc.vocab, (acc, B, S)).astype(np.int32)
+    times = []
+    for it in range(steps + 1):
+        t0 = time.perf_counter()
+        for a in range(acc):
+            om.fwd_bwd(ids[a], None, ids[a], B, S, 1.0 / acc)
+        om.opt_step(2e-4, clip=1.0)
+        dt = time.perf_counter() - t0
+        if it > 0:
+            times.append(dt)
+    med = statistics.median(times)
+    return {"value": rc.tokens_per_step / med, "unit": "tokens/s", "cores": n, "kind": "port",
+            "sample": f"{steps} timed optimizer steps (+1 warm-up) of the same workload "
+                      f"({rc.tokens_per_step} tokens/step), median {med:.3f} s/step; "
+                      f"GEMMs via {backend}, {n} threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+
+    from mobilefinetuner_amd.configs import CONFIGS, step_flops
+    from mobilefinetuner_amd.engine import (CLS_ATTN, CLS_CE, CLS_LINEAR, CLS_LMHEAD, CLS_RANK,
+                                            Model)
+    rc = CONFIGS[args.config]
+    mc = rc.model
+    torch.cuda.set_device(0)
+    tokens = rc.tokens_per_step
+    model = Model(mc, tokens)
+    model.init_params(args.seed, 0.02, 1.0 / mc.lora_r, 0.02)
+    g = torch.Generator(device="cpu").manual_seed(args.seed)
+    ids = torch.randint(0, mc.vocab, (tokens,), generator=g, dtype=torch.int32).cuda()
+    labels = ids.clone()
+
+    def step():
+        model.fwd_bwd(ids, labels, n_micro=rc.accum, seqs_per_micro=rc.batch, S=rc.seq)
+        model.opt_step(args.lr, clip=1.0)
+
+    for _ in range(args.warmup):
+        step()
+    losses = []
+    model.read_stats()
+    torch.cuda.synchronize()
+    timing = not args.no_timing
+    model.reset_timing()
+    model.set_timing(timing)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    model.set_timing(False)
+    loss, n_valid, gnorm = model.read_stats()
+    ms = (t1 - t0) * 1000.0 / args.steps
+    value = tokens / (ms / 1000.0)
+
+    fl = step_flops(rc)
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded uniform token ids; random-init weights)",
+        "config": {"workload": f"{mc.name} LoRA r={mc.lora_r} alpha={mc.lora_alpha:g} "
+                               f"targets_mask={mc.lora_mask:#x} fwd+bwd+clip+Adam",
+                   "config_id": args.config, "batch": rc.batch, "seq_len": rc.seq,
+                   "grad_accum": rc.accum, "tokens_per_step": tokens,
+                   "weights": "fp16-stored frozen W" if mc.w_fp16 else "fp32"},
+        "algorithmic_tflop_per_step": round(sum(fl.values()) / 1e12, 4),
+        "achieved_tflops_step": round(sum(fl.values()) / (ms / 1000.0) / 1e12, 2),
+        "last_loss_mean": loss,
+    }
+    if timing:
+        def cls(c):
+            t_ms, work, n = model.timing(c)
+            return t_ms, work, n
+        t_ms, work, n = cls(CLS_LINEAR)
+        ach = work / (t_ms / 1000.0) / 1e12 if t_ms > 0 else 0.0
+        result["roofline"] = {
+            "kernel": "gemm_kernel (linear fwd + dX, LoRA epilogue)", "bound": "mfma",
+            "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
+            "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": None,
+            "launches": n, "avg_launch_us": round(1000.0 * t_ms / max(n, 1), 2)}
+        br = {}
+        for name, c, unit in (("lm_head_gemm", CLS_LMHEAD, "TFLOP/s"), ("attention", CLS_ATTN, "TFLOP/s"),
+                              ("cross_entropy", CLS_CE, "GB/s"), ("lora_rank_r", CLS_RANK, "TFLOP/s")):
+            t_ms, work, n = cls(c)
+            if n == 0:
+                continue
+            rate = work / (t_ms / 1000.0) / (1e9 if unit == "GB/s" else 1e12)
+            peak = PEAK_HBM if unit == "GB/s" else PEAK_FP32_MFMA
+            br[name] = {"ms_per_step": round(t_ms / args.steps, 4), "achieved": round(rate, 2),
+                        "unit": unit, "frac_of_peak": round(rate / peak, 4), "launches": n}
+        lin_ms = model.timing(CLS_LINEAR)[0]
+        br["linear_gemm"] = {"ms_per_step": round(lin_ms / args.steps, 4)}
+        result["breakdown"] = br
+    else:
+        result["roofline"] = None
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(rc, args.seed, args.cpu_steps, args.cpu_threads)
+    else:
+        result["cpu_baseline"] = None
+    model.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

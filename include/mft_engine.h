@@ -1,0 +1,106 @@
+/*
+ * mft_engine.h — C-ABI of the device-resident LoRA training step
+ * (libmft_hip.so).
+ *
+ * One model object owns every parameter, LoRA optimizer state and saved
+ * activation in HBM and runs the training step of the reference drivers:
+ *   for each micro-batch: model.forward → lm_cross_entropy →
+ *   mul(loss, 1/accum)->backward()   (gpt2_small_lora_finetune/src/main.cpp:471-487)
+ *   clip_and_get_grad_norm → Adam::step → zero_grad   (main.cpp:489-505)
+ * for three graph families: GPT-2 (GPT2Model, main.cpp:202-276), Qwen2
+ * (QwenModel, qwen_lora_finetune/src/wikitext_main.cpp:63-79) and Gemma3
+ * (GemmaModel, gemma_3_270m_lora_finetune/src/main.cpp:326-379).  All
+ * arithmetic runs in libmft_hip's kernels; the host only launches.
+ *
+ * Status codes and mft_last_error() are those of mft_hip.h.
+ */
+#ifndef MFT_ENGINE_H
+#define MFT_ENGINE_H
+#include <stdint.h>
+
+#include "mft_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mft_arch { MFT_ARCH_GPT2 = 0, MFT_ARCH_QWEN2 = 1, MFT_ARCH_GEMMA3 = 2 };
+
+/* LoRA target bits.  GPT-2: bit0 attn.c_attn, bit1 attn.c_proj, bit2 mlp.c_fc,
+ * bit3 mlp.c_proj (LoraTarget::AttnQKV/AttnProj, main.cpp:271-272).
+ * Qwen2/Gemma3: bits 0..6 = q, k, v, o, gate, up, down
+ * (pytorch_alignment/gemma_lora_finetune.py:144-151). */
+typedef struct {
+  int arch, n_layer, d, n_head, n_kv_head, head_dim, d_ff, max_pos;
+  int64_t vocab;
+  int lora_r;
+  float lora_alpha;
+  int lora_mask;
+  float norm_eps;
+  double rope_theta, rope_local_theta;
+  int sliding_pattern; /* Gemma3: layer i is local iff (i+1) % pattern != 0 */
+  int sliding_window;  /* key window of local layers (0 = none) */
+  float attn_scale;    /* 0 → 1/sqrt(head_dim) */
+  int w_fp16;          /* frozen linear + embedding weights stored as fp16 */
+} mft_model_cfg;
+
+typedef struct mft_model_s* mft_model;
+
+/* max_tokens: capacity in tokens of one fused fwd/bwd pass (activations are
+ * sized for it).  stream: hipStream_t or NULL. */
+int mft_model_create(mft_model* out, const mft_model_cfg* cfg,
+                     int64_t max_tokens, void* stream);
+int mft_model_destroy(mft_model m);
+int mft_model_num_params(mft_model m);
+/* Parameter i: name, shape, trainable flag, storage dtype, device pointers
+ * (grad is NULL for frozen parameters). */
+int mft_model_param_info(mft_model m, int i, const char** name, int* ndim,
+                         int64_t* dims, int* trainable, int* is_f16,
+                         void** data, float** grad);
+/* Deterministic on-device init: linear/embedding weights
+ * and biases N(0, std); LayerNorm γ=1, β=0; Qwen RMSNorm w=1; Gemma RMSNorm
+ * stored w=0 (the (1+w) form); LoRA A N(0, a_std), B N(0, b_std). */
+int mft_model_init_params(mft_model m, uint64_t seed, float std, float a_std,
+                          float b_std);
+/* Forward + CE + backward over n_micro micro-batches of seqs_per_micro
+ * sequences of length S, processed as one fused pass of
+ * n_micro*seqs_per_micro sequences.  Each micro-batch's CE is normalised by
+ * its own valid-target count and scaled by `upstream` (1/accum under the
+ * driver's loss scaling), so LoRA gradients equal those of running the
+ * micro-batches one after another.  ids/labels [n_micro*seqs*S] int32 and
+ * mask (nullable, float, 1 = token present) are DEVICE pointers.  LoRA grads
+ * accumulate until mft_model_opt_step.  Asynchronous. */
+int mft_model_fwd_bwd(mft_model m, const int32_t* ids, const float* mask,
+                      const int32_t* labels, int n_micro, int seqs_per_micro,
+                      int S, float upstream);
+/* Forward only: logits [tokens, V] into `logits` (device, nullable) and the
+ * per-micro-batch loss statistics.  Asynchronous. */
+int mft_model_forward(mft_model m, const int32_t* ids, const float* mask,
+                      const int32_t* labels, int n_micro, int seqs_per_micro,
+                      int S, float* logits);
+/* Global grad-norm clip + Adam on the LoRA parameters + zero_grad, entirely
+ * on the device (no host round trip). */
+int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps,
+                       float wd, float clip);
+/* Synchronises, returns the mean over micro-batches of the micro-batch mean
+ * loss since the last call (the driver's accum_loss / accum), the number of
+ * valid targets and the last pre-clip grad norm; resets the loss statistics. */
+int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid,
+                         float* grad_norm);
+
+/* ---- measurement ----------------------------------------------------------
+ * When enabled, HIP events are recorded on the model's stream around every
+ * launch of a kernel class; mft_model_timing returns the summed duration
+ * (ms), algorithmic FLOPs or bytes, and launch count since the last reset.
+ * class 0 = linear GEMMs (LoRA and frozen projections, fwd + dX),
+ * 1 = LM-head GEMMs, 2 = attention kernels (fwd + bwd), 3 = cross-entropy,
+ * 4 = rank-r LoRA kernels. */
+int mft_model_set_timing(mft_model m, int enable);
+int mft_model_timing(mft_model m, int cls, double* ms, double* work,
+                     int64_t* launches);
+int mft_model_reset_timing(mft_model m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,164 @@
+// common.h — shared plumbing for the gfx950 kernel library.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "mft_hip.h"
+
+struct mft_handle_s {
+  hipStream_t stream = nullptr;
+  int device = 0;
+  int num_cu = 256;
+};
+
+namespace mft {
+
+// Thrown inside the library, converted to a status code at the C-ABI.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+
+#define MFT_CHECK_ARG(cond, msg)                                            \
+  do {                                                                      \
+    if (!(cond)) throw ::mft::Error(MFT_EINVAL, std::string(__func__) + ": " + (msg)); \
+  } while (0)
+
+#define MFT_HIP(call)                                                       \
+  do {                                                                      \
+    hipError_t e_ = (call);                                                 \
+    if (e_ != hipSuccess)                                                   \
+      throw ::mft::Error(MFT_EHIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// Kernel launch error check (catches invalid launch configurations).
+#define MFT_LAUNCH_CHECK() MFT_HIP(hipGetLastError())
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- launchers shared by the C-ABI and the step engine ----------------------
+struct GemmEpilogue {
+  const float* bias = nullptr;   // [N]
+  const float* resid = nullptr;  // [M,N] row stride ldc; may alias C
+  float beta = 0.f;              // C = ... + beta * C_old
+  // rank-r update: C += lscale * P[M,r] · Q,  Q(n,j) = Q[n*qsn + j*qsj]
+  const float* P = nullptr;
+  const float* Q = nullptr;
+  int r = 0;
+  int64_t qsn = 0, qsj = 0;
+  float lscale = 0.f;
+};
+
+// Device scratch handed to launchers (split-K partials, rank-r temporaries).
+struct Scratch {
+  float* ptr = nullptr;
+  size_t bytes = 0;
+  Scratch offset(size_t nfloats) const {
+    Scratch s;
+    if (ptr && nfloats * sizeof(float) <= bytes) {
+      s.ptr = ptr + nfloats;
+      s.bytes = bytes - nfloats * sizeof(float);
+    }
+    return s;
+  }
+};
+
+// Optional events recorded immediately around the main GEMM kernel (not the
+// split-K reduction), for live per-kernel timing.
+struct KernelEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+// C[M,N] = A[M,K] · op(B) (+ epilogue).  b_nk=false: B is [K,N] (ldb = row
+// stride); b_nk=true: B is [N,K].  b_f16: B holds IEEE fp16 values.
+void gemm(hipStream_t s, const float* A, int64_t lda, const void* B,
+          int64_t ldb, bool b_nk, bool b_f16, float* C, int64_t ldc, int M,
+          int N, int K, const GemmEpilogue& ep, Scratch ws = Scratch(),
+          const KernelEvents* ev = nullptr);
+// out[M,r] = X[M,K] · Y with Y(k,j) = Y[k*ysk + j*ysj]
+void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y,
+               int64_t ysk, int64_t ysj, int M, int K, int r, float* out);
+// out(j,c) (+)= scale · Σ_m P[m,j] X[m,c];  out(j,c) = out[j*osj + c*osc]
+void rank_outer(hipStream_t s, const float* P, const float* X, int64_t ldx,
+                int M, int C, int r, float scale, float* out, int64_t osj,
+                int64_t osc, bool accumulate, Scratch ws);
+
+void lora_linear_fwd(hipStream_t s, const float* x, int64_t M, int64_t K,
+                     const void* W, bool w_f16, int64_t N, const float* bias,
+                     const float* A, const float* B, int r, float scale,
+                     float* y, float* xa, const float* resid, Scratch ws,
+                     const KernelEvents* ev = nullptr);
+void lora_linear_bwd(hipStream_t s, const float* dy, const float* x,
+                     const void* W, bool w_f16, const float* A, const float* B,
+                     const float* xa, int64_t M, int64_t K, int64_t N, int r,
+                     float scale, float* dx, float* dA, float* dB,
+                     bool accumulate, bool dx_accumulate, Scratch ws,
+                     const KernelEvents* ev = nullptr);
+// Scratch floats lora_linear_bwd needs for its rank-r temporaries.
+size_t lora_bwd_scratch_floats(int64_t M, int64_t K, int64_t N, int r);
+
+struct AttnArgs {
+  const float *q, *k, *v;
+  int64_t q_rs, k_rs, v_rs;
+  int B, Hq, Hkv, S, hd;
+  float scale;
+  int causal, window;
+  const float* kpad;
+};
+void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs,
+              float* lse);
+void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs,
+              const float* dout, int64_t do_rs, const float* lse, float* dq,
+              int64_t dq_rs, float* dk, int64_t dk_rs, float* dv,
+              int64_t dv_rs, float* delta_scratch);
+
+// logits rows have stride ld (>= V); dlogits (may alias logits) uses the same.
+void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
+                int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
+                int64_t norm_count, double* loss_sum, int64_t* n_valid,
+                float* dlogits, float* row_nll, int64_t* count_scratch);
+
+void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n);
+void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n);
+void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
+               int64_t n, float lr, float b1, float b2, float eps, float wd,
+               int t, const float* clip_scale, bool zero_grad);
+void sumsq(hipStream_t s, const float* g, int64_t n, double* out);
+void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,
+                float* norm);
+void layernorm_fwd(hipStream_t s, const float* x, const float* g,
+                   const float* b, int64_t M, int64_t C, float eps, float* y,
+                   float* mean, float* rstd);
+void layernorm_bwd(hipStream_t s, const float* dy, const float* x,
+                   const float* g, const float* mean, const float* rstd,
+                   int64_t M, int64_t C, float* dx, bool accumulate);
+void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
+                 int64_t C, float eps, bool unit_offset, float* y,
+                 float* rstd);
+void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
+                 const float* w, const float* rstd, int64_t M, int64_t C,
+                 bool unit_offset, float* dx, bool accumulate);
+void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
+             int act, float* out);
+void glu_bwd(hipStream_t s, const float* dout, const float* gate,
+             const float* up, int64_t n, int act, float* dgate, float* dup);
+void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
+          double theta, bool inverse);
+void embed(hipStream_t s, const int32_t* ids, int64_t M, int S,
+           const void* wte, bool w_f16, const float* wpe, int64_t C,
+           float scale, float* out);
+void add_inplace(hipStream_t s, float* a, const float* b, int64_t n);
+void fill_normal(hipStream_t s, float* p, int64_t n, uint64_t seed, float std,
+                 float mean);
+void fill_normal_f16(hipStream_t s, uint16_t* p, int64_t n, uint64_t seed,
+                     float std);
+void fill_const(hipStream_t s, float* p, int64_t n, float v);
+void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,
+                      int32_t hi);
+
+}  // namespace mft

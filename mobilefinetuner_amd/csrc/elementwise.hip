@@ -1,0 +1,478 @@
+// elementwise.hip — HBM-bound support kernels of the LoRA step: norms,
+// activations, RoPE, embedding gather, fp16 widening, Adam, grad-norm/clip,
+// and deterministic initialisers.  Row reductions use one wave64 per row
+// (4 rows per 256-thread workgroup) with shuffle reductions; streaming
+// kernels use 128-bit accesses where the tensor length allows.
+#include "common.h"
+
+namespace mft {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Round-to-nearest-even fp32 → fp16 via the hardware conversion
+// (v_cvt_f16_f32 rounds to nearest even under the default rounding mode).
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---- LayerNorm (GPT-2) -------------------------------------------------------
+__global__ __launch_bounds__(256) void layernorm_fwd_kernel(
+    const float* __restrict__ x, const float* __restrict__ g,
+    const float* __restrict__ b, int64_t M, int C, float eps,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* xr = x + row * C;
+  float s = 0.f;
+  for (int j = lane; j < C; j += 64) s += xr[j];
+  const float mu = wave_sum(s) / (float)C;
+  float v = 0.f;
+  for (int j = lane; j < C; j += 64) {
+    const float d = xr[j] - mu;
+    v = fmaf(d, d, v);
+  }
+  const float rs = rsqrtf(wave_sum(v) / (float)C + eps);
+  float* yr = y + row * C;
+  for (int j = lane; j < C; j += 64) yr[j] = fmaf((xr[j] - mu) * rs, g[j], b[j]);
+  if (lane == 0) {
+    if (mean) mean[row] = mu;
+    if (rstd) rstd[row] = rs;
+  }
+}
+
+__global__ __launch_bounds__(256) void layernorm_bwd_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ g, const float* __restrict__ mean,
+    const float* __restrict__ rstd, int64_t M, int C, float* dx,
+    int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* xr = x + row * C;
+  const float* dyr = dy + row * C;
+  const float mu = mean[row], rs = rstd[row];
+  float s1 = 0.f, s2 = 0.f;
+  for (int j = lane; j < C; j += 64) {
+    const float xh = (xr[j] - mu) * rs;
+    const float dxh = dyr[j] * g[j];
+    s1 += dxh;
+    s2 = fmaf(dxh, xh, s2);
+  }
+  s1 = wave_sum(s1) / (float)C;
+  s2 = wave_sum(s2) / (float)C;
+  float* dxr = dx + row * C;
+  for (int j = lane; j < C; j += 64) {
+    const float xh = (xr[j] - mu) * rs;
+    const float r = rs * (dyr[j] * g[j] - s1 - xh * s2);
+    dxr[j] = accumulate ? dxr[j] + r : r;
+  }
+}
+
+// ---- RMSNorm (Qwen2: w; Gemma3: 1+w) ------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, int64_t M, int C,
+    float eps, int unit_offset, float* __restrict__ y, float* __restrict__ rstd) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* xr = x + row * C;
+  float s = 0.f;
+  for (int j = lane; j < C; j += 64) s = fmaf(xr[j], xr[j], s);
+  const float rs = rsqrtf(wave_sum(s) / (float)C + eps);
+  float* yr = y + row * C;
+  for (int j = lane; j < C; j += 64) {
+    const float wj = unit_offset ? 1.f + w[j] : w[j];
+    yr[j] = xr[j] * rs * wj;
+  }
+  if (lane == 0 && rstd) rstd[row] = rs;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ w, const float* __restrict__ rstd, int64_t M,
+    int C, int unit_offset, float* dx, int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* xr = x + row * C;
+  const float* dyr = dy + row * C;
+  const float rs = rstd[row];
+  float s = 0.f;
+  for (int j = lane; j < C; j += 64) {
+    const float wj = unit_offset ? 1.f + w[j] : w[j];
+    s = fmaf(dyr[j] * wj, xr[j] * rs, s);
+  }
+  s = wave_sum(s) / (float)C;
+  float* dxr = dx + row * C;
+  for (int j = lane; j < C; j += 64) {
+    const float wj = unit_offset ? 1.f + w[j] : w[j];
+    const float r = rs * (dyr[j] * wj - xr[j] * rs * s);
+    dxr[j] = accumulate ? dxr[j] + r : r;
+  }
+}
+
+// ---- activations ---------------------------------------------------------------
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;
+  return 0.5f * x * (1.f + tanhf(c * fmaf(0.044715f * x, x * x, x)));
+}
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * fmaf(0.044715f * x, x * x, x));
+  const float du = c * fmaf(3.f * 0.044715f, x * x, 1.f);
+  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * du;
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float silu_grad(float x) {
+  const float s = 1.f / (1.f + expf(-x));
+  return s * (1.f + x * (1.f - s));
+}
+
+__global__ void glu_fwd_kernel(const float* __restrict__ gate,
+                               const float* __restrict__ up, int64_t n, int act,
+                               float* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float a = act == 0 ? gelu_tanh(gate[i]) : silu(gate[i]);
+    out[i] = up ? a * up[i] : a;
+  }
+}
+
+__global__ void glu_bwd_kernel(const float* __restrict__ dout,
+                               const float* __restrict__ gate,
+                               const float* __restrict__ up, int64_t n, int act,
+                               float* __restrict__ dgate, float* __restrict__ dup) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float gv = gate[i];
+    const float a = act == 0 ? gelu_tanh(gv) : silu(gv);
+    const float da = act == 0 ? gelu_tanh_grad(gv) : silu_grad(gv);
+    const float u = up ? up[i] : 1.f;
+    const float d = dout[i];
+    dgate[i] = d * u * da;
+    if (up && dup) dup[i] = d * a;
+  }
+}
+
+// ---- RoPE (HF rotate_half) ---------------------------------------------------
+__global__ void rope_kernel(float* x, int64_t rs, int B, int S, int H, int hd,
+                            double theta, int inverse) {
+  const int half = hd / 2;
+  const int64_t total = (int64_t)B * S * H * half;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(idx % half);
+    const int64_t t = idx / half;
+    const int h = (int)(t % H);
+    const int64_t tok = t / H;  // b*S + s
+    const int s = (int)(tok % S);
+    const double inv = pow(theta, -2.0 * i / (double)hd);
+    double sn, cs;
+    sincos((double)s * inv, &sn, &cs);
+    const float c = (float)cs, sgn = (float)(inverse ? -sn : sn);
+    float* xp = x + tok * rs + (int64_t)h * hd;
+    const float x1 = xp[i], x2 = xp[i + half];
+    xp[i] = x1 * c - x2 * sgn;
+    xp[i + half] = x2 * c + x1 * sgn;
+  }
+}
+
+// ---- embedding ------------------------------------------------------------------
+template <bool F16>
+__global__ void embed_kernel(const int32_t* __restrict__ ids, int64_t M, int S,
+                             const void* __restrict__ wte, const float* __restrict__ wpe,
+                             int C, float scale, float* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;
+  const int64_t id = ids[row];
+  const int s = (int)(row % S);
+  for (int j = threadIdx.x; j < C; j += blockDim.x) {
+    float e;
+    if constexpr (F16)
+      e = half_bits_to_float(reinterpret_cast<const uint16_t*>(wte)[id * C + j]);
+    else
+      e = reinterpret_cast<const float*>(wte)[id * C + j];
+    float v = e * scale;
+    if (wpe) v += wpe[(int64_t)s * C + j];
+    out[row * C + j] = v;
+  }
+}
+
+__global__ void add_kernel(float* a, const float* b, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    a[i] += b[i];
+}
+
+// ---- fp16 <-> fp32 -----------------------------------------------------------
+// 8 halves (16 B) in, 8 floats (32 B) out per thread per iteration.
+__global__ void dequant_f16_kernel(const uint16_t* __restrict__ src,
+                                   float* __restrict__ dst, int64_t n) {
+  const int64_t nvec = n / 8;
+  const uint4* s4 = reinterpret_cast<const uint4*>(src);
+  float4* d4 = reinterpret_cast<float4*>(dst);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint4 u = s4[i];
+    float4 a, b;
+    a.x = half_bits_to_float(u.x & 0xffff); a.y = half_bits_to_float(u.x >> 16);
+    a.z = half_bits_to_float(u.y & 0xffff); a.w = half_bits_to_float(u.y >> 16);
+    b.x = half_bits_to_float(u.z & 0xffff); b.y = half_bits_to_float(u.z >> 16);
+    b.z = half_bits_to_float(u.w & 0xffff); b.w = half_bits_to_float(u.w >> 16);
+    d4[2 * i] = a;
+    d4[2 * i + 1] = b;
+  }
+  for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = half_bits_to_float(src[i]);
+}
+
+__global__ void dequant_f16_scalar_kernel(const uint16_t* __restrict__ src,
+                                          float* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = half_bits_to_float(src[i]);
+}
+
+__global__ void quant_f16_kernel(const float* __restrict__ src,
+                                 uint16_t* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = float_to_half_bits(src[i]);
+}
+
+// ---- Adam / grad norm ------------------------------------------------------------
+__global__ void adam_kernel(float* __restrict__ p, float* __restrict__ g,
+                            float* __restrict__ m, float* __restrict__ v,
+                            int64_t n, float lr, float b1, float b2, float eps,
+                            float wd, double bc1, double bc2,
+                            const float* __restrict__ clip_scale, int zero_grad) {
+  const float cs = clip_scale ? *clip_scale : 1.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float gi = g[i] * cs;
+    const float mi = b1 * m[i] + (1.f - b1) * gi;
+    const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
+    m[i] = mi;
+    v[i] = vi;
+    const double mh = mi / bc1, vh = vi / bc2;
+    double pi = p[i];
+    if (wd != 0.f) pi -= (double)lr * wd * pi;
+    pi -= (double)lr * mh / (sqrt(vh) + eps);
+    p[i] = (float)pi;
+    if (zero_grad) g[i] = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g,
+                                                    int64_t n, double* out) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const double x = g[i];
+    s += x * x;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicAdd(out, red[0] + red[1] + red[2] + red[3]);
+}
+
+__global__ void clip_kernel(const double* ss, float max_norm, float* scale,
+                            float* norm) {
+  float nv = (float)sqrt(*ss);
+  float sc = 1.f;
+  if (max_norm > 0.f && nv > max_norm) {
+    sc = max_norm / (nv + 1e-6f);
+    nv = max_norm;
+  }
+  if (scale) *scale = sc;
+  if (norm) *norm = nv;
+}
+
+// ---- deterministic initialisers (splitmix64 counter hash + Box-Muller) ------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ float normal_at(uint64_t seed, int64_t i) {
+  const uint64_t a = splitmix64(seed ^ splitmix64((uint64_t)i * 2 + 1));
+  const uint64_t b = splitmix64(a);
+  const double u1 = ((a >> 11) + 1) * (1.0 / 9007199254740993.0);  // (0,1]
+  const double u2 = (b >> 11) * (1.0 / 9007199254740992.0);        // [0,1)
+  return (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+}
+
+__global__ void fill_normal_kernel(float* p, int64_t n, uint64_t seed, float std,
+                                   float mean) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = mean + std * normal_at(seed, i);
+}
+__global__ void fill_normal_f16_kernel(uint16_t* p, int64_t n, uint64_t seed,
+                                       float std) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = float_to_half_bits(std * normal_at(seed, i));
+}
+__global__ void fill_const_kernel(float* p, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+__global__ void fill_uniform_int_kernel(int32_t* p, int64_t n, uint64_t seed,
+                                        int32_t hi) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = (int32_t)(splitmix64(seed ^ splitmix64((uint64_t)i)) % (uint64_t)hi);
+}
+
+inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 8192) {
+  int64_t g = cdiv(n, per_block);
+  if (g < 1) g = 1;
+  return (unsigned)(g > cap ? cap : g);
+}
+
+}  // namespace
+
+void layernorm_fwd(hipStream_t s, const float* x, const float* g,
+                   const float* b, int64_t M, int64_t C, float eps, float* y,
+                   float* mean, float* rstd) {
+  MFT_CHECK_ARG(M > 0 && C > 0, "empty");
+  hipLaunchKernelGGL(layernorm_fwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
+                     x, g, b, M, (int)C, eps, y, mean, rstd);
+  MFT_LAUNCH_CHECK();
+}
+void layernorm_bwd(hipStream_t s, const float* dy, const float* x,
+                   const float* g, const float* mean, const float* rstd,
+                   int64_t M, int64_t C, float* dx, bool accumulate) {
+  MFT_CHECK_ARG(M > 0 && C > 0, "empty");
+  hipLaunchKernelGGL(layernorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
+                     dy, x, g, mean, rstd, M, (int)C, dx, accumulate ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
+                 int64_t C, float eps, bool unit_offset, float* y, float* rstd) {
+  MFT_CHECK_ARG(M > 0 && C > 0, "empty");
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
+                     x, w, M, (int)C, eps, unit_offset ? 1 : 0, y, rstd);
+  MFT_LAUNCH_CHECK();
+}
+void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
+                 const float* w, const float* rstd, int64_t M, int64_t C,
+                 bool unit_offset, float* dx, bool accumulate) {
+  MFT_CHECK_ARG(M > 0 && C > 0, "empty");
+  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
+                     dy, x, w, rstd, M, (int)C, unit_offset ? 1 : 0, dx, accumulate ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
+             int act, float* out) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(glu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, act, out);
+  MFT_LAUNCH_CHECK();
+}
+void glu_bwd(hipStream_t s, const float* dout, const float* gate,
+             const float* up, int64_t n, int act, float* dgate, float* dup) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(glu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, dout, gate, up, n, act, dgate, dup);
+  MFT_LAUNCH_CHECK();
+}
+void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
+          double theta, bool inverse) {
+  MFT_CHECK_ARG(hd % 2 == 0, "head_dim must be even");
+  const int64_t n = (int64_t)B * S * H * (hd / 2);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(rope_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, rs, B, S, H, hd, theta,
+                     inverse ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void embed(hipStream_t s, const int32_t* ids, int64_t M, int S,
+           const void* wte, bool w_f16, const float* wpe, int64_t C,
+           float scale, float* out) {
+  MFT_CHECK_ARG(M > 0 && C > 0 && S > 0, "empty");
+  if (w_f16)
+    hipLaunchKernelGGL(embed_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, wpe, (int)C, scale, out);
+  else
+    hipLaunchKernelGGL(embed_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, wpe, (int)C, scale, out);
+  MFT_LAUNCH_CHECK();
+}
+void add_inplace(hipStream_t s, float* a, const float* b, int64_t n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, s, a, b, n);
+  MFT_LAUNCH_CHECK();
+}
+void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n) {
+  if (n <= 0) return;
+  const bool aligned = ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  if (aligned)
+    hipLaunchKernelGGL(dequant_f16_kernel, dim3(grid_for(cdiv(n, 8), 256, 4096)), dim3(256), 0, s, src, dst, n);
+  else
+    hipLaunchKernelGGL(dequant_f16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+  MFT_LAUNCH_CHECK();
+}
+void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(quant_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+  MFT_LAUNCH_CHECK();
+}
+void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
+               int64_t n, float lr, float b1, float b2, float eps, float wd,
+               int t, const float* clip_scale, bool zero_grad) {
+  MFT_CHECK_ARG(t >= 1, "Adam step count is 1-based");
+  if (n <= 0) return;
+  const double bc1 = 1.0 - std::pow((double)b1, t);
+  const double bc2 = 1.0 - std::pow((double)b2, t);
+  hipLaunchKernelGGL(adam_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, lr, b1,
+                     b2, eps, wd, bc1, bc2, clip_scale, zero_grad ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void sumsq(hipStream_t s, const float* g, int64_t n, double* out) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(sumsq_kernel, dim3(grid_for(n, 256, 1024)), dim3(256), 0, s, g, n, out);
+  MFT_LAUNCH_CHECK();
+}
+void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,
+                float* norm) {
+  hipLaunchKernelGGL(clip_kernel, dim3(1), dim3(1), 0, s, ss, max_norm, scale, norm);
+  MFT_LAUNCH_CHECK();
+}
+void fill_normal(hipStream_t s, float* p, int64_t n, uint64_t seed, float std,
+                 float mean) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, seed, std, mean);
+  MFT_LAUNCH_CHECK();
+}
+void fill_normal_f16(hipStream_t s, uint16_t* p, int64_t n, uint64_t seed,
+                     float std) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_normal_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, seed, std);
+  MFT_LAUNCH_CHECK();
+}
+void fill_const(hipStream_t s, float* p, int64_t n, float v) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_const_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
+  MFT_LAUNCH_CHECK();
+}
+void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,
+                      int32_t hi) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_uniform_int_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, seed, hi);
+  MFT_LAUNCH_CHECK();
+}
+
+}  // namespace mft

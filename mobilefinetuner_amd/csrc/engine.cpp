@@ -1,0 +1,865 @@
+// engine.cpp — device-resident LoRA training step for GPT-2, Qwen2 and
+// Gemma3 graphs (C-ABI in include/mft_engine.h).
+//
+// Memory layout in HBM:
+//   * frozen parameters: one arena, each tensor 256-byte aligned, fp32 or
+//     (w_fp16) IEEE fp16 for linear weights and the embedding;
+//   * LoRA parameters: four flat fp32 arrays (value, grad, Adam m, Adam v)
+//     with every A/B tensor at a 64-float-aligned offset, so grad-norm and
+//     Adam are single launches over one contiguous range;
+//   * activations: one arena sized for `max_tokens`, holding what the
+//     backward needs per layer (inputs of every linear, attention output and
+//     lse, norm statistics, MLP pre-activations), plus per-pass scratch;
+//   * logits [tokens, V] — dlogits overwrite them in place.
+// The step never returns to the host: CE normalisation, grad-norm, clip
+// factor and Adam all read device scalars.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "mft_engine.h"
+
+namespace mft {
+namespace {
+
+enum InitKind { INIT_NORMAL, INIT_ONE, INIT_ZERO, INIT_LORA_A, INIT_LORA_B };
+enum { T_Q = 0, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_MAX };
+enum { G_ATTN = 0, G_PROJ, G_FC, G_FC2 };
+enum { CLS_LINEAR = 0, CLS_LMHEAD, CLS_ATTN, CLS_CE, CLS_RANK, CLS_MAX };
+
+struct Param {
+  std::string name;
+  int ndim = 1;
+  int64_t dims[2] = {0, 0};
+  int64_t numel = 0;
+  bool trainable = false, f16 = false;
+  InitKind init = INIT_NORMAL;
+  size_t offset = 0;  // bytes in the frozen arena, or floats in the LoRA arrays
+  void* data = nullptr;
+  float* grad = nullptr;
+};
+
+struct Linear {
+  int W = -1, b = -1, A = -1, B = -1;
+  int K = 0, N = 0;
+};
+
+struct Layer {
+  int n1w = -1, n1b = -1, n2w = -1, n2b = -1, qn = -1, kn = -1, pan = -1, pfn = -1;
+  Linear lin[T_MAX];
+};
+
+struct Acts {
+  float *x, *n1, *mean1, *rstd1;
+  float *q, *k, *v, *qraw, *kraw, *qrs, *krs;
+  int64_t qs, ks, vs;
+  float* xa[T_MAX];
+  float *att, *lse, *o, *ors, *hmid, *n2, *mean2, *rstd2;
+  float *gate, *up, *act, *mo, *mrs;
+};
+
+struct Bump {
+  char* base = nullptr;
+  size_t cap = 0, used = 0;
+  void* take(size_t bytes) {
+    size_t b = (bytes + 255) & ~size_t(255);
+    if (used + b > cap) throw Error(MFT_ENOMEM, "activation arena exhausted");
+    void* p = base + used;
+    used += b;
+    return p;
+  }
+  float* f(int64_t n) { return reinterpret_cast<float*>(take((size_t)n * sizeof(float))); }
+};
+
+struct TimedLaunch {
+  int cls;
+  double work;
+  hipEvent_t a, b;
+};
+
+}  // namespace
+}  // namespace mft
+
+using namespace mft;
+
+struct mft_model_s {
+  mft_model_cfg c{};
+  hipStream_t stream = nullptr;
+  int64_t max_tokens = 0;
+  std::vector<Param> P;
+  std::vector<Layer> L;
+  int wte = -1, wpe = -1, nfw = -1, nfb = -1;
+  // arenas
+  void* frozen = nullptr;
+  size_t frozen_bytes = 0;
+  float *lora_p = nullptr, *lora_g = nullptr, *lora_m = nullptr, *lora_v = nullptr;
+  int64_t lora_n = 0;
+  void* act_mem = nullptr;
+  Bump act;
+  std::vector<Acts> A;
+  float *h_final = nullptr, *hf = nullptr, *fmean = nullptr, *frstd = nullptr;
+  float* logits = nullptr;
+  int64_t ldv = 0;  // logits row stride: vocab rounded up to 4 (zeroed padding)
+  float *dh = nullptr, *dtmp = nullptr, *dn = nullptr, *datt = nullptr;
+  float *dq = nullptr, *dk = nullptr, *dv = nullptr, *dqkv = nullptr;
+  float *dact = nullptr, *dgate = nullptr, *dup = nullptr, *delta = nullptr;
+  float *dtq = nullptr, *dtk = nullptr;
+  float* row_nll = nullptr;
+  Scratch ws;
+  // device scalars: [0..63] per-micro loss sums (double), counts (int64)
+  double* d_loss = nullptr;
+  int64_t* d_cnt = nullptr;
+  int64_t* d_tmpcnt = nullptr;
+  double* d_sumsq = nullptr;
+  float* d_clip = nullptr;  // [0] scale, [1] norm
+  int n_micro_pending = 0;
+  int adam_t = 0;
+  // timing
+  bool timing = false;
+  std::vector<TimedLaunch> launches;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_next = 0;
+  double t_ms[CLS_MAX] = {0}, t_work[CLS_MAX] = {0};
+  int64_t t_n[CLS_MAX] = {0};
+};
+
+namespace {
+
+const char* kGpt2Lin[4] = {"attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"};
+const char* kHfLin[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                         "self_attn.o_proj", "mlp.gate_proj",    "mlp.up_proj",
+                         "mlp.down_proj"};
+
+int add_param(mft_model_s* m, const std::string& name, int64_t d0, int64_t d1, bool trainable,
+              bool f16, InitKind init) {
+  Param p;
+  p.name = name;
+  p.ndim = d1 > 0 ? 2 : 1;
+  p.dims[0] = d0;
+  p.dims[1] = d1 > 0 ? d1 : 0;
+  p.numel = d0 * (d1 > 0 ? d1 : 1);
+  p.trainable = trainable;
+  p.f16 = f16;
+  p.init = init;
+  m->P.push_back(p);
+  return (int)m->P.size() - 1;
+}
+
+void add_linear(mft_model_s* m, Linear& l, const std::string& pfx, const char* nm, int K, int N,
+                bool bias, bool lora) {
+  l.K = K;
+  l.N = N;
+  l.W = add_param(m, pfx + "." + nm + ".weight", K, N, false, m->c.w_fp16 != 0, INIT_NORMAL);
+  if (bias) l.b = add_param(m, pfx + "." + nm + ".bias", N, 0, false, false, INIT_NORMAL);
+  if (lora && m->c.lora_r > 0) {
+    l.A = add_param(m, pfx + "." + nm + ".lora_A", m->c.lora_r, K, true, false, INIT_LORA_A);
+    l.B = add_param(m, pfx + "." + nm + ".lora_B", N, m->c.lora_r, true, false, INIT_LORA_B);
+  }
+}
+
+void build_params(mft_model_s* m) {
+  const mft_model_cfg& c = m->c;
+  const int d = c.d, hd = c.head_dim, H = c.n_head, Hk = c.n_kv_head;
+  const bool f16 = c.w_fp16 != 0;
+  m->L.resize(c.n_layer);
+  if (c.arch == MFT_ARCH_GPT2) {
+    m->wte = add_param(m, "wte", c.vocab, d, false, f16, INIT_NORMAL);
+    m->wpe = add_param(m, "wpe", c.max_pos, d, false, false, INIT_NORMAL);
+    for (int i = 0; i < c.n_layer; ++i) {
+      Layer& L = m->L[i];
+      const std::string pfx = "h." + std::to_string(i);
+      L.n1w = add_param(m, pfx + ".ln_1.weight", d, 0, false, false, INIT_ONE);
+      L.n1b = add_param(m, pfx + ".ln_1.bias", d, 0, false, false, INIT_ZERO);
+      add_linear(m, L.lin[G_ATTN], pfx, kGpt2Lin[0], d, 3 * d, true, c.lora_mask & 1);
+      add_linear(m, L.lin[G_PROJ], pfx, kGpt2Lin[1], d, d, true, c.lora_mask & 2);
+      L.n2w = add_param(m, pfx + ".ln_2.weight", d, 0, false, false, INIT_ONE);
+      L.n2b = add_param(m, pfx + ".ln_2.bias", d, 0, false, false, INIT_ZERO);
+      add_linear(m, L.lin[G_FC], pfx, kGpt2Lin[2], d, c.d_ff, true, c.lora_mask & 4);
+      add_linear(m, L.lin[G_FC2], pfx, kGpt2Lin[3], c.d_ff, d, true, c.lora_mask & 8);
+    }
+    m->nfw = add_param(m, "ln_f.weight", d, 0, false, false, INIT_ONE);
+    m->nfb = add_param(m, "ln_f.bias", d, 0, false, false, INIT_ZERO);
+    return;
+  }
+  const bool qwen = c.arch == MFT_ARCH_QWEN2;
+  const InitKind norm_init = qwen ? INIT_ONE : INIT_ZERO;
+  m->wte = add_param(m, "embed_tokens.weight", c.vocab, d, false, f16, INIT_NORMAL);
+  for (int i = 0; i < c.n_layer; ++i) {
+    Layer& L = m->L[i];
+    const std::string pfx = "layers." + std::to_string(i);
+    L.n1w = add_param(m, pfx + ".input_layernorm.weight", d, 0, false, false, norm_init);
+    const int outs[7] = {H * hd, Hk * hd, Hk * hd, d, c.d_ff, c.d_ff, d};
+    const int ins[7] = {d, d, d, H * hd, d, d, c.d_ff};
+    for (int t = 0; t < 4; ++t)
+      add_linear(m, L.lin[t], pfx, kHfLin[t], ins[t], outs[t], qwen && t < 3, (c.lora_mask >> t) & 1);
+    if (!qwen) {
+      L.qn = add_param(m, pfx + ".self_attn.q_norm.weight", hd, 0, false, false, INIT_ZERO);
+      L.kn = add_param(m, pfx + ".self_attn.k_norm.weight", hd, 0, false, false, INIT_ZERO);
+      L.pan = add_param(m, pfx + ".post_attention_layernorm.weight", d, 0, false, false, INIT_ZERO);
+      L.n2w = add_param(m, pfx + ".pre_feedforward_layernorm.weight", d, 0, false, false, INIT_ZERO);
+      L.pfn = add_param(m, pfx + ".post_feedforward_layernorm.weight", d, 0, false, false, INIT_ZERO);
+    } else {
+      L.n2w = add_param(m, pfx + ".post_attention_layernorm.weight", d, 0, false, false, INIT_ONE);
+    }
+    for (int t = 4; t < 7; ++t)
+      add_linear(m, L.lin[t], pfx, kHfLin[t], ins[t], outs[t], false, (c.lora_mask >> t) & 1);
+  }
+  m->nfw = add_param(m, "norm.weight", d, 0, false, false, norm_init);
+}
+
+void alloc_params(mft_model_s* m) {
+  size_t fb = 0;
+  int64_t ln = 0;
+  for (auto& p : m->P) {
+    if (p.trainable) {
+      p.offset = (size_t)ln;
+      ln += (p.numel + 63) / 64 * 64;
+    } else {
+      p.offset = fb;
+      fb += ((size_t)p.numel * (p.f16 ? 2 : 4) + 255) & ~size_t(255);
+    }
+  }
+  m->frozen_bytes = fb;
+  if (hipMalloc(&m->frozen, fb ? fb : 256) != hipSuccess)
+    throw Error(MFT_ENOMEM, "frozen parameter arena (" + std::to_string(fb) + " bytes)");
+  m->lora_n = ln;
+  const size_t lb = (size_t)(ln ? ln : 64) * sizeof(float);
+  float* arr[4];
+  for (int i = 0; i < 4; ++i) {
+    if (hipMalloc(reinterpret_cast<void**>(&arr[i]), lb) != hipSuccess)
+      throw Error(MFT_ENOMEM, "LoRA arena");
+    MFT_HIP(hipMemset(arr[i], 0, lb));
+  }
+  m->lora_p = arr[0];
+  m->lora_g = arr[1];
+  m->lora_m = arr[2];
+  m->lora_v = arr[3];
+  MFT_HIP(hipMemset(m->frozen, 0, fb ? fb : 256));
+  for (auto& p : m->P) {
+    if (p.trainable) {
+      p.data = m->lora_p + p.offset;
+      p.grad = m->lora_g + p.offset;
+    } else {
+      p.data = static_cast<char*>(m->frozen) + p.offset;
+    }
+  }
+}
+
+bool layer_local(const mft_model_cfg& c, int i) {
+  return c.arch == MFT_ARCH_GEMMA3 && c.sliding_pattern > 0 && ((i + 1) % c.sliding_pattern) != 0;
+}
+float attn_scale(const mft_model_cfg& c) {
+  return c.attn_scale > 0.f ? c.attn_scale : 1.f / std::sqrt((float)c.head_dim);
+}
+
+void alloc_acts(mft_model_s* m) {
+  const mft_model_cfg& c = m->c;
+  const int64_t M = m->max_tokens;
+  const int64_t d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim, ff = c.d_ff, r = c.lora_r;
+  const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
+  // size estimate (floats) — computed by a dry run of the same carve-up
+  auto carve = [&](Bump& b) {
+    m->A.assign(c.n_layer, Acts{});
+    for (int l = 0; l < c.n_layer; ++l) {
+      Acts& a = m->A[l];
+      std::memset(&a, 0, sizeof(a));
+      a.x = b.f(M * d);
+      a.n1 = b.f(M * d);
+      a.rstd1 = b.f(M);
+      if (gpt2) {
+        a.mean1 = b.f(M);
+        a.q = b.f(M * 3 * d);
+        a.k = a.q + d;
+        a.v = a.q + 2 * d;
+        a.qs = a.ks = a.vs = 3 * d;
+      } else {
+        a.q = b.f(M * H * hd);
+        a.k = b.f(M * Hk * hd);
+        a.v = b.f(M * Hk * hd);
+        a.qs = H * hd;
+        a.ks = a.vs = Hk * hd;
+        if (gemma) {
+          a.qraw = b.f(M * H * hd);
+          a.kraw = b.f(M * Hk * hd);
+          a.qrs = b.f(M * H);
+          a.krs = b.f(M * Hk);
+        }
+      }
+      const Layer& L = m->L[l];
+      for (int t = 0; t < T_MAX; ++t)
+        if (L.lin[t].A >= 0) a.xa[t] = b.f(M * r);
+      a.att = b.f(M * H * hd);
+      a.lse = b.f(M * H);
+      a.o = b.f(M * d);
+      if (gemma) a.ors = b.f(M);
+      a.hmid = b.f(M * d);
+      a.n2 = b.f(M * d);
+      a.rstd2 = b.f(M);
+      if (gpt2) a.mean2 = b.f(M);
+      a.gate = b.f(M * ff);
+      if (!gpt2) a.up = b.f(M * ff);
+      a.act = b.f(M * ff);
+      a.mo = b.f(M * d);
+      if (gemma) a.mrs = b.f(M);
+    }
+    m->h_final = b.f(M * d);
+    m->hf = b.f(M * d);
+    m->frstd = b.f(M);
+    m->fmean = b.f(M);
+    m->ldv = (c.vocab + 3) / 4 * 4;
+    m->logits = b.f(M * m->ldv);
+    m->dh = b.f(M * d);
+    m->dtmp = b.f(M * d);
+    m->dn = b.f(M * d);
+    m->datt = b.f(M * H * hd);
+    m->dq = b.f(M * H * hd);
+    m->dk = b.f(M * Hk * hd);
+    m->dv = b.f(M * Hk * hd);
+    m->dtq = b.f(M * H * hd);
+    m->dtk = b.f(M * Hk * hd);
+    if (gpt2) m->dqkv = b.f(M * 3 * d);
+    m->dact = b.f(M * ff);
+    m->dgate = b.f(M * ff);
+    m->dup = b.f(M * ff);
+    m->delta = b.f(M * H);
+    m->row_nll = b.f(M);
+    const int64_t wide = std::max<int64_t>({d, ff, H * hd, 3 * d});
+    const int64_t wsf = M * std::max<int64_t>(r, 1) + 16 * std::max<int64_t>(r, 1) * wide + 8 * M * wide;
+    m->ws.ptr = b.f(wsf);
+    m->ws.bytes = (size_t)wsf * sizeof(float);
+  };
+  Bump dry;
+  dry.base = nullptr;
+  dry.cap = SIZE_MAX / 2;
+  carve(dry);
+  const size_t need = dry.used;
+  if (hipMalloc(&m->act_mem, need) != hipSuccess)
+    throw Error(MFT_ENOMEM, "activation arena (" + std::to_string(need) + " bytes)");
+  m->act.base = static_cast<char*>(m->act_mem);
+  m->act.cap = need;
+  m->act.used = 0;
+  carve(m->act);
+  // logits padding columns are never written and must stay finite (they are
+  // read, times zero rows of E, by the LM-head backward's vector loads).
+  MFT_HIP(hipMemset(m->logits, 0, sizeof(float) * (size_t)M * m->ldv));
+  void* sc = nullptr;
+  MFT_HIP(hipMalloc(&sc, 4096));
+  MFT_HIP(hipMemset(sc, 0, 4096));
+  m->d_loss = reinterpret_cast<double*>(sc);                               // 64 doubles
+  m->d_cnt = reinterpret_cast<int64_t*>(static_cast<char*>(sc) + 512);     // 64 int64
+  m->d_tmpcnt = reinterpret_cast<int64_t*>(static_cast<char*>(sc) + 1024);
+  m->d_sumsq = reinterpret_cast<double*>(static_cast<char*>(sc) + 1280);
+  m->d_clip = reinterpret_cast<float*>(static_cast<char*>(sc) + 1536);
+}
+
+// ---- timing helpers -------------------------------------------------------------
+hipEvent_t next_event(mft_model_s* m) {
+  if (m->ev_next == m->ev_pool.size()) {
+    hipEvent_t e;
+    MFT_HIP(hipEventCreate(&e));
+    m->ev_pool.push_back(e);
+  }
+  return m->ev_pool[m->ev_next++];
+}
+
+struct Timed {
+  mft_model_s* m;
+  KernelEvents ev;
+  int cls;
+  double work;
+  Timed(mft_model_s* mm, int c, double w) : m(mm), cls(c), work(w) {
+    if (m->timing) {
+      ev.start = next_event(m);
+      ev.stop = next_event(m);
+    }
+  }
+  const KernelEvents* events() const { return m->timing ? &ev : nullptr; }
+  void begin() {
+    if (m->timing) MFT_HIP(hipEventRecord(ev.start, m->stream));
+  }
+  void end() {
+    if (m->timing) MFT_HIP(hipEventRecord(ev.stop, m->stream));
+  }
+  ~Timed() {
+    if (m->timing) m->launches.push_back({cls, work, ev.start, ev.stop});
+  }
+};
+
+void collect_timing(mft_model_s* m) {
+  if (m->launches.empty()) return;
+  MFT_HIP(hipStreamSynchronize(m->stream));
+  for (auto& t : m->launches) {
+    float ms = 0.f;
+    MFT_HIP(hipEventElapsedTime(&ms, t.a, t.b));
+    m->t_ms[t.cls] += ms;
+    m->t_work[t.cls] += t.work;
+    m->t_n[t.cls] += 1;
+  }
+  m->launches.clear();
+  m->ev_next = 0;
+}
+
+// ---- building blocks ---------------------------------------------------------------
+float lscale(const mft_model_s* m) { return m->c.lora_alpha / (float)m->c.lora_r; }
+
+void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
+             const float* resid) {
+  const Param& W = m->P[l.W];
+  const bool lora = l.A >= 0;
+  const int r = lora ? m->c.lora_r : 0;
+  GemmEpilogue ep;
+  ep.bias = l.b >= 0 ? static_cast<const float*>(m->P[l.b].data) : nullptr;
+  ep.resid = resid;
+  if (lora) {
+    Timed tr(m, CLS_RANK, 4.0 * M * l.K * r);
+    tr.begin();
+    rank_proj(m->stream, x, l.K, static_cast<const float*>(m->P[l.A].data), 1, l.K, (int)M, l.K, r, xa);
+    tr.end();
+    ep.P = xa;
+    ep.Q = static_cast<const float*>(m->P[l.B].data);
+    ep.r = r;
+    ep.qsn = r;
+    ep.qsj = 1;
+    ep.lscale = lscale(m);
+  }
+  Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
+  gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+}
+
+void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, const float* xa,
+             int64_t M, float* dx) {
+  const Param& W = m->P[l.W];
+  const bool lora = l.A >= 0;
+  const int r = lora ? m->c.lora_r : 0;
+  float* U = m->ws.ptr;
+  Scratch rest = m->ws.offset((size_t)(M * (r > 0 ? r : 1)));
+  if (lora) {
+    Timed tr(m, CLS_RANK, 2.0 * M * l.N * r);
+    tr.begin();
+    rank_proj(m->stream, dy, l.N, static_cast<const float*>(m->P[l.B].data), r, 1, (int)M, l.N, r, U);
+    tr.end();
+  }
+  if (dx) {
+    GemmEpilogue ep;
+    if (lora) {
+      ep.P = U;
+      ep.Q = static_cast<const float*>(m->P[l.A].data);
+      ep.r = r;
+      ep.qsn = 1;
+      ep.qsj = l.K;
+      ep.lscale = lscale(m);
+    }
+    Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.K * r);
+    gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
+  }
+  if (lora) {
+    Timed tr(m, CLS_RANK, 2.0 * M * r * (l.K + l.N));
+    tr.begin();
+    rank_outer(m->stream, U, x, l.K, (int)M, l.K, r, lscale(m), m->P[l.A].grad, l.K, 1, true, rest);
+    rank_outer(m->stream, xa, dy, l.N, (int)M, l.N, r, lscale(m), m->P[l.B].grad, 1, r, true, rest);
+    tr.end();
+  }
+}
+
+template <typename T>
+const T* pd(const mft_model_s* m, int i) {
+  return i < 0 ? nullptr : static_cast<const T*>(m->P[i].data);
+}
+
+void attention_fwd(mft_model_s* m, Acts& a, int li, const float* mask, int nseq, int S) {
+  const mft_model_cfg& c = m->c;
+  AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, c.n_head, c.n_kv_head, S, c.head_dim,
+             attn_scale(c), 1, layer_local(c, li) ? c.sliding_window : 0, mask};
+  const double work = 2.0 * 2.0 * nseq * c.n_head * (double)S * S * c.head_dim * 0.5;
+  Timed t(m, CLS_ATTN, work);
+  t.begin();
+  attn_fwd(m->stream, g, a.att, (int64_t)c.n_head * c.head_dim, a.lse);
+  t.end();
+}
+
+void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S) {
+  const mft_model_cfg& c = m->c;
+  const int64_t M = (int64_t)nseq * S;
+  const int d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim;
+  const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
+  const hipStream_t s = m->stream;
+  const Param& E = m->P[m->wte];
+  embed(s, ids, M, S, E.data, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
+        gemma ? std::sqrt((float)d) : 1.f, m->A[0].x);
+  for (int li = 0; li < c.n_layer; ++li) {
+    const Layer& L = m->L[li];
+    Acts& a = m->A[li];
+    float* hout = li + 1 < c.n_layer ? m->A[li + 1].x : m->h_final;
+    if (gpt2) {
+      layernorm_fwd(s, a.x, pd<float>(m, L.n1w), pd<float>(m, L.n1b), M, d, c.norm_eps, a.n1, a.mean1, a.rstd1);
+      lin_fwd(m, L.lin[G_ATTN], a.n1, M, a.q, a.xa[G_ATTN], nullptr);
+      attention_fwd(m, a, li, mask, nseq, S);
+      lin_fwd(m, L.lin[G_PROJ], a.att, M, a.hmid, a.xa[G_PROJ], a.x);  // residual fused
+      layernorm_fwd(s, a.hmid, pd<float>(m, L.n2w), pd<float>(m, L.n2b), M, d, c.norm_eps, a.n2, a.mean2, a.rstd2);
+      lin_fwd(m, L.lin[G_FC], a.n2, M, a.gate, a.xa[G_FC], nullptr);
+      glu_fwd(s, a.gate, nullptr, M * c.d_ff, 0, a.act);
+      lin_fwd(m, L.lin[G_FC2], a.act, M, hout, a.xa[G_FC2], a.hmid);  // residual fused
+      continue;
+    }
+    rmsnorm_fwd(s, a.x, pd<float>(m, L.n1w), M, d, c.norm_eps, gemma, a.n1, a.rstd1);
+    if (gemma) {
+      lin_fwd(m, L.lin[T_Q], a.n1, M, a.qraw, a.xa[T_Q], nullptr);
+      lin_fwd(m, L.lin[T_K], a.n1, M, a.kraw, a.xa[T_K], nullptr);
+      rmsnorm_fwd(s, a.qraw, pd<float>(m, L.qn), M * H, hd, c.norm_eps, true, a.q, a.qrs);
+      rmsnorm_fwd(s, a.kraw, pd<float>(m, L.kn), M * Hk, hd, c.norm_eps, true, a.k, a.krs);
+    } else {
+      lin_fwd(m, L.lin[T_Q], a.n1, M, a.q, a.xa[T_Q], nullptr);
+      lin_fwd(m, L.lin[T_K], a.n1, M, a.k, a.xa[T_K], nullptr);
+    }
+    lin_fwd(m, L.lin[T_V], a.n1, M, a.v, a.xa[T_V], nullptr);
+    const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
+    rope(s, a.q, a.qs, nseq, S, H, hd, th, false);
+    rope(s, a.k, a.ks, nseq, S, Hk, hd, th, false);
+    attention_fwd(m, a, li, mask, nseq, S);
+    if (gemma) {
+      lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr);
+      rmsnorm_fwd(s, a.o, pd<float>(m, L.pan), M, d, c.norm_eps, true, m->dtmp, a.ors);
+      MFT_HIP(hipMemcpyAsync(a.hmid, a.x, sizeof(float) * M * d, hipMemcpyDeviceToDevice, s));
+      add_inplace(s, a.hmid, m->dtmp, M * d);
+    } else {
+      lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x);
+    }
+    rmsnorm_fwd(s, a.hmid, pd<float>(m, L.n2w), M, d, c.norm_eps, gemma, a.n2, a.rstd2);
+    lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
+    lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
+    glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
+    if (gemma) {
+      lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr);
+      rmsnorm_fwd(s, a.mo, pd<float>(m, L.pfn), M, d, c.norm_eps, true, m->dtmp, a.mrs);
+      MFT_HIP(hipMemcpyAsync(hout, a.hmid, sizeof(float) * M * d, hipMemcpyDeviceToDevice, s));
+      add_inplace(s, hout, m->dtmp, M * d);
+    } else {
+      lin_fwd(m, L.lin[T_DOWN], a.act, M, hout, a.xa[T_DOWN], a.hmid);
+    }
+  }
+  if (gpt2)
+    layernorm_fwd(s, m->h_final, pd<float>(m, m->nfw), pd<float>(m, m->nfb), M, d, c.norm_eps, m->hf, m->fmean, m->frstd);
+  else
+    rmsnorm_fwd(s, m->h_final, pd<float>(m, m->nfw), M, d, c.norm_eps, gemma, m->hf, m->frstd);
+  // LM head: logits = hf · Eᵀ, E [V, d] is the [N, K] operand.
+  Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
+  gemm(s, m->hf, d, E.data, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, GemmEpilogue(),
+       m->ws, t.events());
+}
+
+void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs, int S,
+                   float upstream, bool backward) {
+  const mft_model_cfg& c = m->c;
+  if (m->n_micro_pending + n_micro > 64) throw Error(MFT_EINVAL, "more than 64 micro-batches pending");
+  for (int i = 0; i < n_micro; ++i) {
+    const int64_t row0 = (int64_t)i * seqs * S;
+    float* lg = m->logits + row0 * m->ldv;
+    Timed t(m, CLS_CE, 8.0 * (double)seqs * S * c.vocab);
+    t.begin();
+    ce_fwd_bwd(m->stream, lg, labels + row0, seqs, S, c.vocab, m->ldv, -100, upstream, 0,
+               m->d_loss + m->n_micro_pending, m->d_cnt + m->n_micro_pending, backward ? lg : nullptr,
+               m->row_nll + row0, m->d_tmpcnt);
+    t.end();
+    m->n_micro_pending++;
+  }
+}
+
+void backward(mft_model_s* m, const float* mask, int nseq, int S) {
+  const mft_model_cfg& c = m->c;
+  const int64_t M = (int64_t)nseq * S;
+  const int d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim;
+  const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
+  const hipStream_t s = m->stream;
+  const Param& E = m->P[m->wte];
+  {
+    // dhf = dlogits · E, E [V, d] is the [K, N] operand.
+    Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
+    gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, GemmEpilogue(),
+         m->ws, t.events());
+  }
+  if (gpt2)
+    layernorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->fmean, m->frstd, M, d, m->dh, false);
+  else
+    rmsnorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->frstd, M, d, gemma, m->dh, false);
+  const int64_t nf = M * c.d_ff;
+  for (int li = c.n_layer - 1; li >= 0; --li) {
+    const Layer& L = m->L[li];
+    Acts& a = m->A[li];
+    // ---- MLP block ----
+    const float* dmo = m->dh;
+    if (gemma) {
+      rmsnorm_bwd(s, m->dh, a.mo, pd<float>(m, L.pfn), a.mrs, M, d, true, m->dtmp, false);
+      dmo = m->dtmp;
+    }
+    if (gpt2) {
+      lin_bwd(m, L.lin[G_FC2], dmo, a.act, a.xa[G_FC2], M, m->dact);
+      glu_bwd(s, m->dact, a.gate, nullptr, nf, 0, m->dgate, nullptr);
+      lin_bwd(m, L.lin[G_FC], m->dgate, a.n2, a.xa[G_FC], M, m->dn);
+      layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, m->dh, true);
+    } else {
+      lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
+      glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, m->dgate, m->dup);
+      lin_bwd(m, L.lin[T_GATE], m->dgate, a.n2, a.xa[T_GATE], M, m->dn);
+      lin_bwd(m, L.lin[T_UP], m->dup, a.n2, a.xa[T_UP], M, m->dtmp);
+      add_inplace(s, m->dn, m->dtmp, M * d);
+      rmsnorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.rstd2, M, d, gemma, m->dh, true);
+    }
+    // ---- attention block ----
+    const float* dox = m->dh;
+    if (gemma) {
+      rmsnorm_bwd(s, m->dh, a.o, pd<float>(m, L.pan), a.ors, M, d, true, m->dtmp, false);
+      dox = m->dtmp;
+    }
+    lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
+    AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
+               layer_local(c, li) ? c.sliding_window : 0, mask};
+    const bool need_dx = li > 0;
+    const double awork = 2.0 * 5.0 * nseq * H * (double)S * S * hd * 0.5;
+    if (gpt2) {
+      {
+        Timed t(m, CLS_ATTN, awork);
+        t.begin();
+        attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dqkv, 3 * d, m->dqkv + d,
+                 3 * d, m->dqkv + 2 * d, 3 * d, m->delta);
+        t.end();
+      }
+      lin_bwd(m, L.lin[G_ATTN], m->dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
+      if (need_dx)
+        layernorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.mean1, a.rstd1, M, d, m->dh, true);
+      continue;
+    }
+    {
+      Timed t(m, CLS_ATTN, awork);
+      t.begin();
+      attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dq, (int64_t)H * hd, m->dk,
+               (int64_t)Hk * hd, m->dv, (int64_t)Hk * hd, m->delta);
+      t.end();
+    }
+    const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
+    rope(s, m->dq, (int64_t)H * hd, nseq, S, H, hd, th, true);
+    rope(s, m->dk, (int64_t)Hk * hd, nseq, S, Hk, hd, th, true);
+    const float* dqx = m->dq;
+    const float* dkx = m->dk;
+    if (gemma) {
+      rmsnorm_bwd(s, m->dq, a.qraw, pd<float>(m, L.qn), a.qrs, M * H, hd, true, m->dtq, false);
+      rmsnorm_bwd(s, m->dk, a.kraw, pd<float>(m, L.kn), a.krs, M * Hk, hd, true, m->dtk, false);
+      dqx = m->dtq;
+      dkx = m->dtk;
+    }
+    lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, need_dx ? m->dn : nullptr);
+    lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, need_dx ? m->dtmp : nullptr);
+    if (need_dx) add_inplace(s, m->dn, m->dtmp, M * d);
+    lin_bwd(m, L.lin[T_V], m->dv, a.n1, a.xa[T_V], M, need_dx ? m->dtmp : nullptr);
+    if (need_dx) {
+      add_inplace(s, m->dn, m->dtmp, M * d);
+      rmsnorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.rstd1, M, d, gemma, m->dh, true);
+    }
+  }
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return MFT_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return MFT_EHIP;
+  }
+}
+
+void check_cfg(const mft_model_cfg& c) {
+  MFT_CHECK_ARG(c.arch >= 0 && c.arch <= 2, "unknown arch");
+  MFT_CHECK_ARG(c.n_layer > 0 && c.d > 0 && c.n_head > 0 && c.n_kv_head > 0 && c.head_dim > 0 && c.d_ff > 0 &&
+                    c.vocab > 0,
+                "bad model dims");
+  MFT_CHECK_ARG(c.n_head % c.n_kv_head == 0, "n_head must be a multiple of n_kv_head");
+  MFT_CHECK_ARG(c.arch != MFT_ARCH_GPT2 || c.n_head * c.head_dim == c.d, "GPT-2 needs n_head*head_dim == d");
+  MFT_CHECK_ARG(c.arch != MFT_ARCH_GPT2 || c.n_head == c.n_kv_head, "GPT-2 has no GQA");
+  MFT_CHECK_ARG(c.lora_r >= 0 && c.lora_r <= 32, "lora_r must be in [0,32]");
+  MFT_CHECK_ARG(c.d % 4 == 0 && c.d_ff % 4 == 0 && c.head_dim % 4 == 0, "dims must be multiples of 4");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mft_model_create(mft_model* out, const mft_model_cfg* cfg, int64_t max_tokens, void* stream) {
+  return guarded([&] {
+    if (!out || !cfg) throw Error(MFT_EINVAL, "null argument");
+    check_cfg(*cfg);
+    if (max_tokens <= 0) throw Error(MFT_EINVAL, "max_tokens must be positive");
+    auto* m = new mft_model_s();
+    try {
+      m->c = *cfg;
+      m->stream = reinterpret_cast<hipStream_t>(stream);
+      m->max_tokens = max_tokens;
+      build_params(m);
+      alloc_params(m);
+      alloc_acts(m);
+    } catch (...) {
+      mft_model_destroy(m);
+      throw;
+    }
+    *out = m;
+  });
+}
+
+int mft_model_destroy(mft_model m) {
+  return guarded([&] {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->stream);
+    for (auto e : m->ev_pool) (void)hipEventDestroy(e);
+    void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss};
+    for (void* b : bufs)
+      if (b) (void)hipFree(b);
+    delete m;
+  });
+}
+
+int mft_model_num_params(mft_model m) { return m ? (int)m->P.size() : 0; }
+
+int mft_model_param_info(mft_model m, int i, const char** name, int* ndim, int64_t* dims, int* trainable,
+                         int* is_f16, void** data, float** grad) {
+  return guarded([&] {
+    if (!m || i < 0 || i >= (int)m->P.size()) throw Error(MFT_EINVAL, "param index out of range");
+    const Param& p = m->P[i];
+    if (name) *name = p.name.c_str();
+    if (ndim) *ndim = p.ndim;
+    if (dims) {
+      dims[0] = p.dims[0];
+      dims[1] = p.dims[1];
+    }
+    if (trainable) *trainable = p.trainable;
+    if (is_f16) *is_f16 = p.f16;
+    if (data) *data = p.data;
+    if (grad) *grad = p.grad;
+  });
+}
+
+int mft_model_init_params(mft_model m, uint64_t seed, float std, float a_std, float b_std) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    for (size_t i = 0; i < m->P.size(); ++i) {
+      Param& p = m->P[i];
+      const uint64_t ps = seed * 0x100000001b3ull + i * 0x9e3779b97f4a7c15ull;
+      switch (p.init) {
+        case INIT_NORMAL:
+          if (p.f16) fill_normal_f16(m->stream, static_cast<uint16_t*>(p.data), p.numel, ps, std);
+          else fill_normal(m->stream, static_cast<float*>(p.data), p.numel, ps, std, 0.f);
+          break;
+        case INIT_ONE: fill_const(m->stream, static_cast<float*>(p.data), p.numel, 1.f); break;
+        case INIT_ZERO: fill_const(m->stream, static_cast<float*>(p.data), p.numel, 0.f); break;
+        case INIT_LORA_A: fill_normal(m->stream, static_cast<float*>(p.data), p.numel, ps, a_std, 0.f); break;
+        case INIT_LORA_B: fill_normal(m->stream, static_cast<float*>(p.data), p.numel, ps, b_std, 0.f); break;
+      }
+    }
+    MFT_HIP(hipStreamSynchronize(m->stream));
+  });
+}
+
+int mft_model_fwd_bwd(mft_model m, const int32_t* ids, const float* mask, const int32_t* labels, int n_micro,
+                      int seqs_per_micro, int S, float upstream) {
+  return guarded([&] {
+    if (!m || !ids || !labels) throw Error(MFT_EINVAL, "null argument");
+    const int nseq = n_micro * seqs_per_micro;
+    if (n_micro <= 0 || seqs_per_micro <= 0 || S <= 0) throw Error(MFT_EINVAL, "empty batch");
+    if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
+    if (m->c.arch == MFT_ARCH_GPT2 && S > m->c.max_pos) throw Error(MFT_EINVAL, "seq_len exceeds n_positions");
+    forward(m, ids, mask, nseq, S);
+    cross_entropy(m, labels, n_micro, seqs_per_micro, S, upstream, true);
+    backward(m, mask, nseq, S);
+  });
+}
+
+int mft_model_forward(mft_model m, const int32_t* ids, const float* mask, const int32_t* labels, int n_micro,
+                      int seqs_per_micro, int S, float* logits) {
+  return guarded([&] {
+    if (!m || !ids) throw Error(MFT_EINVAL, "null argument");
+    const int nseq = n_micro * seqs_per_micro;
+    if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
+    forward(m, ids, mask, nseq, S);
+    if (logits)
+      MFT_HIP(hipMemcpy2DAsync(logits, sizeof(float) * m->c.vocab, m->logits, sizeof(float) * m->ldv,
+                               sizeof(float) * m->c.vocab, (size_t)nseq * S, hipMemcpyDeviceToDevice,
+                               m->stream));
+    if (labels) cross_entropy(m, labels, n_micro, seqs_per_micro, S, 1.f, false);
+  });
+}
+
+int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps, float wd, float clip) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    const hipStream_t s = m->stream;
+    fill_const(s, reinterpret_cast<float*>(m->d_sumsq), 2, 0.f);  // one double = two floats
+    sumsq(s, m->lora_g, m->lora_n, m->d_sumsq);
+    clip_scale(s, m->d_sumsq, clip, m->d_clip, m->d_clip + 1);
+    m->adam_t++;
+    adam_step(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, lr, b1, b2, eps, wd, m->adam_t, m->d_clip,
+              true);
+  });
+}
+
+int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid, float* grad_norm) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    MFT_HIP(hipStreamSynchronize(m->stream));
+    double ls[64];
+    int64_t cn[64];
+    float cl[2];
+    const int n = m->n_micro_pending;
+    if (n > 0) {
+      MFT_HIP(hipMemcpy(ls, m->d_loss, sizeof(double) * n, hipMemcpyDeviceToHost));
+      MFT_HIP(hipMemcpy(cn, m->d_cnt, sizeof(int64_t) * n, hipMemcpyDeviceToHost));
+    }
+    MFT_HIP(hipMemcpy(cl, m->d_clip, sizeof(cl), hipMemcpyDeviceToHost));
+    double acc = 0.0;
+    int64_t tot = 0;
+    for (int i = 0; i < n; ++i) {
+      acc += cn[i] > 0 ? ls[i] / (double)cn[i] : 0.0;
+      tot += cn[i];
+    }
+    if (mean_loss) *mean_loss = n > 0 ? (float)(acc / n) : 0.f;
+    if (n_valid) *n_valid = tot;
+    if (grad_norm) *grad_norm = cl[1];
+    MFT_HIP(hipMemset(m->d_loss, 0, 1024));
+    m->n_micro_pending = 0;
+  });
+}
+
+int mft_model_set_timing(mft_model m, int enable) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    if (!enable) collect_timing(m);
+    m->timing = enable != 0;
+  });
+}
+
+int mft_model_timing(mft_model m, int cls, double* ms, double* work, int64_t* launches) {
+  return guarded([&] {
+    if (!m || cls < 0 || cls >= CLS_MAX) throw Error(MFT_EINVAL, "bad class");
+    collect_timing(m);
+    if (ms) *ms = m->t_ms[cls];
+    if (work) *work = m->t_work[cls];
+    if (launches) *launches = m->t_n[cls];
+  });
+}
+
+int mft_model_reset_timing(mft_model m) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    collect_timing(m);
+    for (int i = 0; i < CLS_MAX; ++i) {
+      m->t_ms[i] = m->t_work[i] = 0;
+      m->t_n[i] = 0;
+    }
+  });
+}
+
+}  // extern "C"

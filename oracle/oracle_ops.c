@@ -1,0 +1,658 @@
+/*
+ * oracle_ops.c — CPU restatement of the hot-path operators.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h).
+ */
+#include "oracle.h"
+
+#include <dlfcn.h>
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* BLAS plumbing                                                            */
+/* ------------------------------------------------------------------------ */
+typedef void (*cblas_sgemm_fn)(int, int, int, int, int, int, float,
+                               const float*, int, const float*, int, float,
+                               float*, int);
+typedef void (*cblas_sgemm64_fn)(int, int, int, int64_t, int64_t, int64_t,
+                                 float, const float*, int64_t, const float*,
+                                 int64_t, float, float*, int64_t);
+static cblas_sgemm_fn g_sgemm32 = NULL;
+static cblas_sgemm64_fn g_sgemm64 = NULL;
+static int g_use_blas = 0;
+static const char* g_backend = "builtin(fp64-accumulate)";
+static int g_threads = 0;
+
+static void try_load_blas(void) {
+  static int tried = 0;
+  if (tried) return;
+  tried = 1;
+  const char* force = getenv("ORC_BLAS_LIB");
+  const char* mkl[] = {"libmkl_rt.so", "/opt/conda/lib/libmkl_rt.so",
+                       "libmkl_rt.so.1", NULL};
+  if (!force || strstr(force, "mkl")) {
+    for (int i = 0; mkl[i]; ++i) {
+      void* h = dlopen(force ? force : mkl[i], RTLD_NOW | RTLD_GLOBAL);
+      if (!h) continue;
+      g_sgemm32 = (cblas_sgemm_fn)dlsym(h, "cblas_sgemm");
+      if (g_sgemm32) {
+        typedef void (*setn)(int);
+        setn f = (setn)dlsym(h, "MKL_Set_Num_Threads");
+        if (f && g_threads > 0) f(g_threads);
+        g_backend = "mkl_rt cblas_sgemm";
+        return;
+      }
+    }
+  }
+  /* OpenBLAS with 64-bit ints as shipped inside numpy / scipy wheels. */
+  const char* ob[] = {"libscipy_openblas64_.so", "libopenblas64_.so",
+                      "libopenblas.so", NULL};
+  for (int i = 0; ob[i]; ++i) {
+    void* h = dlopen(force ? force : ob[i], RTLD_NOW | RTLD_GLOBAL);
+    if (!h) continue;
+    g_sgemm64 = (cblas_sgemm64_fn)dlsym(h, "scipy_cblas_sgemm64_");
+    if (!g_sgemm64) g_sgemm64 = (cblas_sgemm64_fn)dlsym(h, "cblas_sgemm64_");
+    if (g_sgemm64) {
+      g_backend = "openblas cblas_sgemm64_";
+      return;
+    }
+    g_sgemm32 = (cblas_sgemm_fn)dlsym(h, "cblas_sgemm");
+    if (g_sgemm32) {
+      g_backend = "openblas cblas_sgemm";
+      return;
+    }
+  }
+}
+
+int orc_set_blas(int use_blas) {
+  if (use_blas) {
+    try_load_blas();
+    g_use_blas = (g_sgemm32 || g_sgemm64) ? 1 : 0;
+  } else {
+    g_use_blas = 0;
+  }
+  return g_use_blas;
+}
+
+const char* orc_blas_backend(void) {
+  return g_use_blas ? g_backend : "builtin(fp64-accumulate)";
+}
+
+void orc_set_threads(int n) {
+  g_threads = n;
+  if (n > 0) omp_set_num_threads(n);
+}
+int orc_get_threads(void) { return g_threads > 0 ? g_threads : omp_get_max_threads(); }
+
+void orc_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
+               float alpha, const float* A, int64_t lda, const float* B,
+               int64_t ldb, float beta, float* C, int64_t ldc) {
+  if (M <= 0 || N <= 0) return;
+  if (g_use_blas && K > 0) {
+    /* CblasRowMajor = 101, NoTrans = 111, Trans = 112 */
+    if (g_sgemm64)
+      g_sgemm64(101, transA ? 112 : 111, transB ? 112 : 111, M, N, K, alpha,
+                A, lda, B, ldb, beta, C, ldc);
+    else
+      g_sgemm32(101, transA ? 112 : 111, transB ? 112 : 111, (int)M, (int)N,
+                (int)K, alpha, A, (int)lda, B, (int)ldb, beta, C, (int)ldc);
+    return;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i) {
+    double* acc = (double*)calloc((size_t)N, sizeof(double));
+    for (int64_t k = 0; k < K; ++k) {
+      double a = transA ? A[k * lda + i] : A[i * lda + k];
+      if (a == 0.0) continue;
+      if (!transB) {
+        const float* brow = B + k * ldb;
+        for (int64_t j = 0; j < N; ++j) acc[j] += a * brow[j];
+      } else {
+        for (int64_t j = 0; j < N; ++j) acc[j] += a * B[j * ldb + k];
+      }
+    }
+    for (int64_t j = 0; j < N; ++j) {
+      double c = beta == 0.0f ? 0.0 : (double)beta * C[i * ldc + j];
+      C[i * ldc + j] = (float)(alpha * acc[j] + c);
+    }
+    free(acc);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a1/a2 LoRA linear.                                                       */
+/* y = x·W + b + s·(x·Aᵀ)·Bᵀ with W [in,out] as loaded with                 */
+/* transpose_linear=false (gpt2_small_lora_finetune/src/main.cpp:211-214)   */
+/* and PEFT A [r,in], B [out,r] (README.md:282,296); the merged-weight      */
+/* equivalence W' = W + s·AᵀBᵀ is what LoraInjector::merge_all relies on    */
+/* (gpt2_small_lora_finetune/src/eval_ppl.cpp:125-127).  s = alpha/r        */
+/* (LoraSpec{rank, alpha}, main.cpp:264-272).                               */
+/* ------------------------------------------------------------------------ */
+void orc_lora_linear_fwd(const float* x, int64_t M, int64_t K, const float* W,
+                         int64_t N, const float* bias, const float* A,
+                         const float* B, int r, float scale, float* y,
+                         float* xa) {
+  orc_sgemm(0, 0, M, N, K, 1.0f, x, K, W, N, 0.0f, y, N);
+  if (bias) {
+#pragma omp parallel for
+    for (int64_t i = 0; i < M; ++i)
+      for (int64_t j = 0; j < N; ++j) y[i * N + j] += bias[j];
+  }
+  if (r > 0 && A && B) {
+    float* t = xa ? xa : (float*)malloc(sizeof(float) * (size_t)(M * r));
+    orc_sgemm(0, 1, M, r, K, 1.0f, x, K, A, K, 0.0f, t, r); /* x·Aᵀ */
+    orc_sgemm(0, 1, M, N, r, scale, t, r, B, r, 1.0f, y, N); /* += s·t·Bᵀ */
+    if (!xa) free(t);
+  }
+}
+
+/* Backward with W frozen (freeze_base, qwen_lora_finetune/src/wikitext_main.cpp:78):
+ *   U  = dy·B                [M,r]
+ *   dx = dy·Wᵀ + s·U·A        (overwritten)
+ *   dA (+)= s·Uᵀ·x           [r,K]
+ *   dB (+)= s·dyᵀ·xa         [N,r]
+ * Grads accumulate across micro-batches (main.cpp:471-487) when
+ * accumulate != 0. */
+void orc_lora_linear_bwd(const float* dy, const float* x, const float* W,
+                         const float* A, const float* B, const float* xa,
+                         int64_t M, int64_t K, int64_t N, int r, float scale,
+                         float* dx, float* dA, float* dB, int accumulate) {
+  float* U = NULL;
+  if (r > 0 && A && B) {
+    U = (float*)malloc(sizeof(float) * (size_t)(M * r));
+    orc_sgemm(0, 0, M, r, N, 1.0f, dy, N, B, r, 0.0f, U, r);
+  }
+  if (dx) {
+    orc_sgemm(0, 1, M, K, N, 1.0f, dy, N, W, N, 0.0f, dx, K);
+    if (U) orc_sgemm(0, 0, M, K, r, scale, U, r, A, K, 1.0f, dx, K);
+  }
+  if (U) {
+    float beta = accumulate ? 1.0f : 0.0f;
+    if (dA) orc_sgemm(1, 0, r, K, M, scale, U, r, x, K, beta, dA, K);
+    if (dB) orc_sgemm(1, 0, N, r, M, scale, dy, N, xa, r, beta, dB, r);
+    free(U);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a7 IEEE binary16 <-> binary32.  The sharder keeps frozen shards as FP16  */
+/* on disk (--shard_fp16_disk, README.md:311,318) and widens them on        */
+/* require(); BASELINE config 5 defines W as N(0,0.02) rounded to fp16.     */
+/* Widening is exact; narrowing is round-to-nearest-even.                    */
+/* ------------------------------------------------------------------------ */
+float orc_half_bits_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1f;
+  uint32_t man = h & 0x3ff;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else { /* subnormal: value = man * 2^-24 */
+      float f = (float)man * (1.0f / 16777216.0f);
+      memcpy(&bits, &f, 4);
+      bits |= sign;
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 112) << 23) | (man << 13);
+  }
+  float out;
+  memcpy(&out, &bits, 4);
+  return out;
+}
+
+uint16_t orc_float_to_half_bits(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t absx = x & 0x7fffffffu;
+  if (absx > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((absx >> 13) & 0x3ff)); /* NaN */
+  if (absx >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* overflow → inf */
+  if (absx < 0x38800000u) { /* below fp16 normal range: subnormal/zero */
+    /* value in units of 2^-24, rounded to nearest even */
+    float a;
+    memcpy(&a, &absx, 4);
+    double q = (double)a * 16777216.0;
+    double fl = floor(q);
+    double rem = q - fl;
+    uint32_t m = (uint32_t)fl;
+    if (rem > 0.5 || (rem == 0.5 && (m & 1u))) m++;
+    return (uint16_t)(sign | m);
+  }
+  uint32_t e = (absx >> 23) - 112;
+  uint32_t mant = absx & 0x7fffffu;
+  uint32_t h = (e << 10) | (mant >> 13);
+  uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+void orc_f16_to_f32(const uint16_t* src, float* dst, int64_t n) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) dst[i] = orc_half_bits_to_float(src[i]);
+}
+void orc_f32_to_f16(const float* src, uint16_t* dst, int64_t n) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) dst[i] = orc_float_to_half_bits(src[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a3/a4 causal attention with GQA.                                         */
+/* P = softmax(scale·Q·Kᵀ + causal + key-padding), O = P·V; the reference    */
+/* materialises scores/probs and repeats K/V heads (repeat_kv_heads,         */
+/* gemma_3_270m_lora_finetune/src/main.cpp:579-580,623-626); a query head h  */
+/* reads KV head h / (Hq/Hkv), which is what the repeat produces.            */
+/* Backward follows the analytical forms restated at main.cpp:605-657:      */
+/*   dV = Pᵀ·dO, dP = dO·Vᵀ, dS = P∘(dP − rowsum(dO∘O)),                    */
+/*   dQ = scale·dS·K, dK = scale·dSᵀ·Q, dK/dV summed over each GQA group.    */
+/* window > 0 adds HF's sliding-window rule (key j visible iff i-j < window).*/
+/* A query row with no visible key yields O = 0, lse = -inf, zero grads.    */
+/* Accumulation is fp64.                                                    */
+/* ------------------------------------------------------------------------ */
+static int visible(int causal, int window, const float* kpad, int b, int S,
+                   int i, int j) {
+  if (causal && j > i) return 0;
+  if (window > 0 && i - j >= window) return 0; /* HF sliding_window */
+  if (kpad && !(kpad[(int64_t)b * S + j] > 0.5f)) return 0;
+  return 1;
+}
+
+void orc_attn_fwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
+                  const float* v, int64_t v_rs, int B, int Hq, int Hkv, int S,
+                  int hd, float scale, int causal, int window,
+                  const float* kpad, float* o, int64_t o_rs, float* lse) {
+  const int grp = Hq / Hkv;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h) {
+      const int kh = h / grp;
+      double* sc = (double*)malloc(sizeof(double) * (size_t)S);
+      double* acc = (double*)malloc(sizeof(double) * (size_t)hd);
+      for (int i = 0; i < S; ++i) {
+        const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
+        double mx = -INFINITY;
+        for (int j = 0; j < S; ++j) {
+          if (!visible(causal, window, kpad, b, S, i, j)) { sc[j] = -INFINITY; continue; }
+          const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
+          double s = 0.0;
+          for (int d = 0; d < hd; ++d) s += (double)qi[d] * kj[d];
+          sc[j] = s * scale;
+          if (sc[j] > mx) mx = sc[j];
+        }
+        float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
+        int64_t li = ((int64_t)b * Hq + h) * S + i;
+        if (mx == -INFINITY) {
+          for (int d = 0; d < hd; ++d) oi[d] = 0.0f;
+          if (lse) lse[li] = -INFINITY;
+          continue;
+        }
+        double sum = 0.0;
+        for (int j = 0; j < S; ++j) {
+          sc[j] = sc[j] == -INFINITY ? 0.0 : exp(sc[j] - mx);
+          sum += sc[j];
+        }
+        for (int d = 0; d < hd; ++d) acc[d] = 0.0;
+        for (int j = 0; j < S; ++j) {
+          if (sc[j] == 0.0) continue;
+          const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
+          double p = sc[j] / sum;
+          for (int d = 0; d < hd; ++d) acc[d] += p * vj[d];
+        }
+        for (int d = 0; d < hd; ++d) oi[d] = (float)acc[d];
+        if (lse) lse[li] = (float)(mx + log(sum));
+      }
+      free(sc);
+      free(acc);
+    }
+}
+
+void orc_attn_bwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
+                  const float* v, int64_t v_rs, const float* o, int64_t o_rs,
+                  const float* dout, int64_t do_rs, const float* lse, int B,
+                  int Hq, int Hkv, int S, int hd, float scale, int causal,
+                  int window, const float* kpad, float* dq, int64_t dq_rs, float* dk,
+                  int64_t dk_rs, float* dv, int64_t dv_rs) {
+  (void)lse;
+  const int grp = Hq / Hkv;
+  /* dk/dv accumulate over the group: do it per (b, kv-head) to stay race-free */
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int b = 0; b < B; ++b)
+    for (int kh = 0; kh < Hkv; ++kh) {
+      double* dK = (double*)calloc((size_t)S * hd, sizeof(double));
+      double* dV = (double*)calloc((size_t)S * hd, sizeof(double));
+      double* P = (double*)malloc(sizeof(double) * (size_t)S);
+      double* dP = (double*)malloc(sizeof(double) * (size_t)S);
+      for (int h = kh * grp; h < (kh + 1) * grp; ++h) {
+        for (int i = 0; i < S; ++i) {
+          const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
+          const float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
+          const float* gi = dout + ((int64_t)b * S + i) * do_rs + (int64_t)h * hd;
+          float* dqi = dq + ((int64_t)b * S + i) * dq_rs + (int64_t)h * hd;
+          double mx = -INFINITY;
+          for (int j = 0; j < S; ++j) {
+            if (!visible(causal, window, kpad, b, S, i, j)) { P[j] = -INFINITY; continue; }
+            const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
+            double s = 0.0;
+            for (int d = 0; d < hd; ++d) s += (double)qi[d] * kj[d];
+            P[j] = s * scale;
+            if (P[j] > mx) mx = P[j];
+          }
+          if (mx == -INFINITY) {
+            for (int d = 0; d < hd; ++d) dqi[d] = 0.0f;
+            continue;
+          }
+          double sum = 0.0;
+          for (int j = 0; j < S; ++j) {
+            P[j] = P[j] == -INFINITY ? 0.0 : exp(P[j] - mx);
+            sum += P[j];
+          }
+          double Di = 0.0; /* rowsum(dO∘O) */
+          for (int d = 0; d < hd; ++d) Di += (double)gi[d] * oi[d];
+          for (int j = 0; j < S; ++j) {
+            P[j] /= sum;
+            if (P[j] == 0.0) { dP[j] = 0.0; continue; }
+            const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
+            double s = 0.0;
+            for (int d = 0; d < hd; ++d) s += (double)gi[d] * vj[d];
+            dP[j] = s;
+          }
+          double* dqa = (double*)calloc((size_t)hd, sizeof(double));
+          for (int j = 0; j < S; ++j) {
+            if (P[j] == 0.0) continue;
+            double ds = P[j] * (dP[j] - Di) * scale;
+            const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
+            for (int d = 0; d < hd; ++d) {
+              dqa[d] += ds * kj[d];
+              dK[(int64_t)j * hd + d] += ds * qi[d];
+              dV[(int64_t)j * hd + d] += P[j] * gi[d];
+            }
+          }
+          for (int d = 0; d < hd; ++d) dqi[d] = (float)dqa[d];
+          free(dqa);
+        }
+      }
+      for (int j = 0; j < S; ++j) {
+        float* dkj = dk + ((int64_t)b * S + j) * dk_rs + (int64_t)kh * hd;
+        float* dvj = dv + ((int64_t)b * S + j) * dv_rs + (int64_t)kh * hd;
+        for (int d = 0; d < hd; ++d) {
+          dkj[d] = (float)dK[(int64_t)j * hd + d];
+          dvj[d] = (float)dV[(int64_t)j * hd + d];
+        }
+      }
+      free(dK); free(dV); free(P); free(dP);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a5/a6 shifted LM cross-entropy, lm_cross_entropy(logits, labels, -100,    */
+/* "mean") (gpt2_small_lora_finetune/src/main.cpp:475).  Per-token NLL as    */
+/* in compute_per_token_nll (gemma_3_270m_lora_finetune/src/main.cpp:100-133):*/
+/* row (b,s), s < S-1, predicts labels[b,s+1]; max-subtracted, fp64 sum of   */
+/* exp.  Mean over non-ignored targets.  Backward: (softmax − onehot)/N      */
+/* times the upstream factor (1/accum under loss scaling, main.cpp:480-485).*/
+/* ------------------------------------------------------------------------ */
+int64_t orc_ce_fwd_bwd(const float* logits, const int32_t* labels, int B,
+                       int S, int64_t V, int ignore_index, float upstream,
+                       int64_t norm_count, double* loss_sum, float* dlogits,
+                       float* row_nll) {
+  int64_t nvalid = 0;
+  for (int b = 0; b < B; ++b)
+    for (int s = 0; s + 1 < S; ++s)
+      if (labels[(int64_t)b * S + s + 1] != ignore_index) nvalid++;
+  const int64_t denom = norm_count > 0 ? norm_count : nvalid;
+  const double g = denom > 0 ? (double)upstream / (double)denom : 0.0;
+  double total = 0.0;
+#pragma omp parallel for reduction(+ : total) schedule(static)
+  for (int64_t row = 0; row < (int64_t)B * S; ++row) {
+    const int b = (int)(row / S), s = (int)(row % S);
+    const float* x = logits + row * V;
+    float* dx = dlogits ? dlogits + row * V : NULL;
+    int label = (s + 1 < S) ? labels[(int64_t)b * S + s + 1] : ignore_index;
+    if (label == ignore_index || label < 0 || label >= V) {
+      if (row_nll) row_nll[row] = 0.0f;
+      if (dx) for (int64_t j = 0; j < V; ++j) dx[j] = 0.0f;
+      continue;
+    }
+    float mx = x[0];
+    for (int64_t j = 1; j < V; ++j) if (x[j] > mx) mx = x[j];
+    double sum = 0.0;
+    for (int64_t j = 0; j < V; ++j) sum += exp((double)(x[j] - mx));
+    double lse = log(sum) + (double)mx;
+    double nll = lse - (double)x[label];
+    total += nll;
+    if (row_nll) row_nll[row] = (float)nll;
+    if (dx) {
+      double xl = (double)x[label];
+      for (int64_t j = 0; j < V; ++j) dx[j] = (float)(exp((double)x[j] - lse) * g);
+      dx[label] = (float)((exp(xl - lse) - 1.0) * g);
+    }
+  }
+  if (loss_sum) *loss_sum = total;
+  return nvalid;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a8 Adam (AdamConfig{lr, β1=.9, β2=.999, ε=1e-8, wd},                      */
+/* gpt2_small_lora_finetune/src/main.cpp:341-348; step at :497-502).  The    */
+/* optim/ source is absent: bias-corrected Adam (Kingma & Ba 2015) is taken, */
+/* with decoupled weight decay as in the mirrors' torch AdamW                */
+/* (pytorch_alignment/gpt2_lora_finetune.py:313).  t is 1-based.             */
+/* ------------------------------------------------------------------------ */
+void orc_adam_step(float* p, const float* g, float* m, float* v, int64_t n,
+                   float lr, float b1, float b2, float eps, float wd, int t) {
+  const double bc1 = 1.0 - pow((double)b1, t);
+  const double bc2 = 1.0 - pow((double)b2, t);
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) {
+    float gi = g[i];
+    m[i] = b1 * m[i] + (1.0f - b1) * gi;
+    v[i] = b2 * v[i] + (1.0f - b2) * gi * gi;
+    double mh = m[i] / bc1;
+    double vh = v[i] / bc2;
+    double pi = p[i];
+    if (wd != 0.0f) pi -= (double)lr * wd * pi;
+    pi -= (double)lr * mh / (sqrt(vh) + eps);
+    p[i] = (float)pi;
+  }
+}
+
+/* a9 global grad norm in fp64 and clip factor                               */
+/* (clip_and_get_grad_norm, gpt2_small_lora_finetune/src/main.cpp:384-409).  */
+double orc_sumsq(const float* g, int64_t n) {
+  double s = 0.0;
+#pragma omp parallel for reduction(+ : s)
+  for (int64_t i = 0; i < n; ++i) s += (double)g[i] * (double)g[i];
+  return s;
+}
+
+float orc_clip_scale(double sumsq, float max_norm, float* norm_out) {
+  float norm = (float)sqrt(sumsq);
+  float scale = 1.0f;
+  if (max_norm > 0.0f && norm > max_norm) {
+    scale = max_norm / (norm + 1e-6f);
+    norm = max_norm;
+  }
+  if (norm_out) *norm_out = norm;
+  return scale;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a10 support ops.  Semantics follow HF GPT-2 / Qwen2 / Gemma3, which the   */
+/* alignment mirrors load (pytorch_alignment/{gpt2,gemma,qwen}_lora_finetune.py) and which */
+/* the reference graphs reproduce (debug names gemma…/main.cpp:562-596).     */
+/* ------------------------------------------------------------------------ */
+void orc_layernorm_fwd(const float* x, const float* g, const float* b,
+                       int64_t M, int64_t C, float eps, float* y, float* mean,
+                       float* rstd) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < M; ++i) {
+    const float* xi = x + i * C;
+    double mu = 0.0;
+    for (int64_t j = 0; j < C; ++j) mu += xi[j];
+    mu /= (double)C;
+    double var = 0.0;
+    for (int64_t j = 0; j < C; ++j) var += ((double)xi[j] - mu) * ((double)xi[j] - mu);
+    var /= (double)C;
+    double rs = 1.0 / sqrt(var + eps);
+    for (int64_t j = 0; j < C; ++j)
+      y[i * C + j] = (float)(((double)xi[j] - mu) * rs * g[j] + b[j]);
+    if (mean) mean[i] = (float)mu;
+    if (rstd) rstd[i] = (float)rs;
+  }
+}
+
+void orc_layernorm_bwd(const float* dy, const float* x, const float* g,
+                       const float* mean, const float* rstd, int64_t M,
+                       int64_t C, float* dx, int accumulate) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < M; ++i) {
+    const float* xi = x + i * C;
+    const float* dyi = dy + i * C;
+    double mu = mean[i], rs = rstd[i];
+    double s1 = 0.0, s2 = 0.0;
+    for (int64_t j = 0; j < C; ++j) {
+      double xh = ((double)xi[j] - mu) * rs;
+      double dxh = (double)dyi[j] * g[j];
+      s1 += dxh;
+      s2 += dxh * xh;
+    }
+    s1 /= (double)C;
+    s2 /= (double)C;
+    for (int64_t j = 0; j < C; ++j) {
+      double xh = ((double)xi[j] - mu) * rs;
+      double dxh = (double)dyi[j] * g[j];
+      float r = (float)(rs * (dxh - s1 - xh * s2));
+      dx[i * C + j] = accumulate ? dx[i * C + j] + r : r;
+    }
+  }
+}
+
+void orc_rmsnorm_fwd(const float* x, const float* w, int64_t M, int64_t C,
+                     float eps, int unit_offset, float* y, float* rstd) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < M; ++i) {
+    const float* xi = x + i * C;
+    double ss = 0.0;
+    for (int64_t j = 0; j < C; ++j) ss += (double)xi[j] * xi[j];
+    double rs = 1.0 / sqrt(ss / (double)C + eps);
+    for (int64_t j = 0; j < C; ++j) {
+      double wj = unit_offset ? 1.0 + (double)w[j] : (double)w[j];
+      y[i * C + j] = (float)((double)xi[j] * rs * wj);
+    }
+    if (rstd) rstd[i] = (float)rs;
+  }
+}
+
+void orc_rmsnorm_bwd(const float* dy, const float* x, const float* w,
+                     const float* rstd, int64_t M, int64_t C, int unit_offset,
+                     float* dx, int accumulate) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < M; ++i) {
+    const float* xi = x + i * C;
+    const float* dyi = dy + i * C;
+    double rs = rstd[i];
+    double s = 0.0;
+    for (int64_t j = 0; j < C; ++j) {
+      double wj = unit_offset ? 1.0 + (double)w[j] : (double)w[j];
+      s += (double)dyi[j] * wj * ((double)xi[j] * rs);
+    }
+    s /= (double)C;
+    for (int64_t j = 0; j < C; ++j) {
+      double wj = unit_offset ? 1.0 + (double)w[j] : (double)w[j];
+      float r = (float)(rs * ((double)dyi[j] * wj - (double)xi[j] * rs * s));
+      dx[i * C + j] = accumulate ? dx[i * C + j] + r : r;
+    }
+  }
+}
+
+/* GELU, tanh approximation (HF "gelu_new" for GPT-2, "gelu_pytorch_tanh"
+ * for Gemma3's hidden_activation). */
+float orc_gelu_tanh(float xf) {
+  double x = xf;
+  double c = 0.7978845608028654; /* sqrt(2/pi) */
+  return (float)(0.5 * x * (1.0 + tanh(c * (x + 0.044715 * x * x * x))));
+}
+float orc_gelu_tanh_grad(float xf) {
+  double x = xf;
+  double c = 0.7978845608028654;
+  double u = c * (x + 0.044715 * x * x * x);
+  double t = tanh(u);
+  double du = c * (1.0 + 3.0 * 0.044715 * x * x);
+  return (float)(0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * du);
+}
+float orc_silu(float xf) {
+  double x = xf;
+  return (float)(x / (1.0 + exp(-x)));
+}
+float orc_silu_grad(float xf) {
+  double x = xf;
+  double s = 1.0 / (1.0 + exp(-x));
+  return (float)(s * (1.0 + x * (1.0 - s)));
+}
+
+void orc_glu_fwd(const float* gate, const float* up, int64_t n, int act,
+                 float* out) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) {
+    float a = act == 0 ? orc_gelu_tanh(gate[i]) : orc_silu(gate[i]);
+    out[i] = up ? a * up[i] : a;
+  }
+}
+
+void orc_glu_bwd(const float* dout, const float* gate, const float* up,
+                 int64_t n, int act, float* dgate, float* dup) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) {
+    float a = act == 0 ? orc_gelu_tanh(gate[i]) : orc_silu(gate[i]);
+    float da = act == 0 ? orc_gelu_tanh_grad(gate[i]) : orc_silu_grad(gate[i]);
+    float u = up ? up[i] : 1.0f;
+    dgate[i] = dout[i] * u * da;
+    if (up && dup) dup[i] = dout[i] * a;
+  }
+}
+
+/* HF rotate_half convention: inv_freq_i = θ^(-2i/hd), i < hd/2; the pair
+ * (x_i, x_{i+hd/2}) is rotated by angle s·inv_freq_i.  inverse=1 applies the
+ * transpose rotation, which is the backward of the forward map. */
+void orc_rope(float* x, int64_t rs, int B, int S, int H, int hd, double theta,
+              int inverse) {
+  const int half = hd / 2;
+#pragma omp parallel for collapse(2)
+  for (int b = 0; b < B; ++b)
+    for (int s = 0; s < S; ++s)
+      for (int h = 0; h < H; ++h) {
+        float* xp = x + ((int64_t)b * S + s) * rs + (int64_t)h * hd;
+        for (int i = 0; i < half; ++i) {
+          double inv = pow(theta, -2.0 * i / (double)hd);
+          double ang = (double)s * inv;
+          double c = cos(ang), sn = sin(ang);
+          if (inverse) sn = -sn;
+          double x1 = xp[i], x2 = xp[i + half];
+          xp[i] = (float)(x1 * c - x2 * sn);
+          xp[i + half] = (float)(x2 * c + x1 * sn);
+        }
+      }
+}
+
+/* Token + (GPT-2) learned position embedding; Gemma3 multiplies the token
+ * embedding by sqrt(hidden) (scale argument). */
+void orc_embed(const int32_t* ids, int64_t M, int S, const float* wte,
+               const uint16_t* wte_f16, const float* wpe, int64_t C,
+               float scale, float* h) {
+#pragma omp parallel for
+  for (int64_t i = 0; i < M; ++i) {
+    int64_t id = ids[i];
+    int s = (int)(i % S);
+    for (int64_t j = 0; j < C; ++j) {
+      float e = wte_f16 ? orc_half_bits_to_float(wte_f16[id * C + j])
+                        : wte[id * C + j];
+      float v = e * scale;
+      if (wpe) v += wpe[(int64_t)s * C + j];
+      h[i * C + j] = v;
+    }
+  }
+}

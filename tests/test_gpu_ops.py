@@ -1,0 +1,306 @@
+"""GPU parity of every C-ABI kernel entry point against the CPU oracle on the
+same seeded inputs.  Tolerances (relative L2 error ‖y−y_ref‖/‖y_ref‖):
+fp32 path ≤ 1e-4; fp16-stored-W path ≤ 2e-3 (the benchmark's bars) —
+fp16 W is widened exactly, so those cases are also held to 1e-4 against an
+oracle fed the same fp16 values; integer/bit work is bit-exact."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+TOL_F16W = 2e-3
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no GPU", allow_module_level=True)
+
+from mobilefinetuner_amd import ops  # noqa: E402
+
+DEV = "cuda"
+RNG = np.random.default_rng(2024)
+
+
+def rn(*shape, std=1.0):
+    return (RNG.standard_normal(shape) * std).astype(np.float32)
+
+
+def g(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def h(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _exact_oracle():
+    O.lib().orc_set_blas(0)  # fp64-accumulating reference loops
+    yield
+
+
+# ------------------------------------------------------------------ LoRA linear
+LIN_SHAPES = [
+    (77, 132, 200, 8, True),     # ragged M/N, K not a multiple of 16
+    (512, 768, 2304, 8, True),   # GPT-2 small c_attn
+    (512, 768, 768, 8, True),    # GPT-2 small attn c_proj (split-K path)
+    (64, 3072, 768, 4, False),   # few tiles, deep K (split-K)
+    (256, 1024, 4096, 16, True), # 128x128 tile path
+    (33, 20, 50, 0, True),       # plain frozen linear (no LoRA)
+]
+
+
+@pytest.mark.parametrize("M,K,N,r,bias", LIN_SHAPES)
+def test_lora_linear_fwd(M, K, N, r, bias):
+    print(f"lora_linear_fwd M={M} K={K} N={N} r={r}", flush=True)
+    x, W, b = rn(M, K), rn(K, N, std=0.05), rn(N) if bias else None
+    A, B = (rn(r, K, std=1 / 8), rn(N, r, std=0.02)) if r else (None, None)
+    s = 16.0 / max(r, 1)
+    y_ref, xa_ref = O.lora_linear_fwd(x, W, b, A, B, s)
+    y, xa = ops.lora_linear_fwd(g(x), g(W), g(b) if bias else None, g(A) if r else None,
+                                g(B) if r else None, s)
+    assert rel_err(h(y), y_ref) < TOL
+    if r:
+        assert rel_err(h(xa), xa_ref) < TOL
+
+
+def test_lora_linear_fwd_fused_residual():
+    M, K, N, r = 96, 256, 256, 8
+    x, W, b, A, B, res = rn(M, K), rn(K, N, std=0.05), rn(N), rn(r, K), rn(N, r), rn(M, N)
+    y_ref, _ = O.lora_linear_fwd(x, W, b, A, B, 2.0)
+    y, _ = ops.lora_linear_fwd(g(x), g(W), g(b), g(A), g(B), 2.0, resid=g(res))
+    assert rel_err(h(y), y_ref + res) < TOL
+
+
+@pytest.mark.parametrize("M,K,N,r", [(77, 132, 200, 8), (512, 768, 2304, 8), (512, 3072, 768, 8),
+                                     (1024, 896, 128, 8), (64, 1024, 1024, 4)])
+def test_lora_linear_bwd(M, K, N, r):
+    print(f"lora_linear_bwd M={M} K={K} N={N} r={r}", flush=True)
+    x, W, A, B, dy = rn(M, K), rn(K, N, std=0.05), rn(r, K, std=1 / 8), rn(N, r, std=0.02), rn(M, N)
+    s = 2.0
+    _, xa = O.lora_linear_fwd(x, W, None, A, B, s)
+    dx_ref, dA_ref, dB_ref = O.lora_linear_bwd(dy, x, W, A, B, xa, s)
+    dx, dA, dB = ops.lora_linear_bwd(g(dy), g(x), g(W), g(A), g(B), g(xa), s)
+    assert rel_err(h(dx), dx_ref) < TOL
+    assert rel_err(h(dA), dA_ref) < TOL
+    assert rel_err(h(dB), dB_ref) < TOL
+    # accumulate semantics: a second call adds
+    ops.lora_linear_bwd(g(dy), g(x), g(W), g(A), g(B), g(xa), s, dA=dA, dB=dB, need_dx=False,
+                        accumulate=True)
+    assert rel_err(h(dA), 2 * dA_ref) < TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 1152, 1024), (200, 640, 2048)])
+def test_lora_linear_fp16_weight(M, K, N):
+    """W stored as fp16 and widened in the GEMM's tile load (config 5)."""
+    r = 8
+    x, A, B, dy = rn(M, K), rn(r, K, std=1 / 8), rn(N, r, std=0.02), rn(M, N)
+    W32 = rn(K, N, std=0.02)
+    W16 = W32.astype(np.float16)
+    Wf = W16.astype(np.float32)
+    y_ref, xa_ref = O.lora_linear_fwd(x, Wf, None, A, B, 4.0)
+    y, xa = ops.lora_linear_fwd(g(x), g(W16), None, g(A), g(B), 4.0)
+    assert rel_err(h(y), y_ref) < TOL  # exact widening: held to the fp32 bar
+    # against the unrounded fp32 weights: the fp16-W bar
+    assert rel_err(h(y), O.lora_linear_fwd(x, W32, None, A, B, 4.0)[0]) < TOL_F16W
+    dx_ref, dA_ref, dB_ref = O.lora_linear_bwd(dy, x, Wf, A, B, xa_ref, 4.0)
+    dx, dA, dB = ops.lora_linear_bwd(g(dy), g(x), g(W16), g(A), g(B), xa, 4.0)
+    assert rel_err(h(dx), dx_ref) < TOL
+    assert rel_err(h(dA), dA_ref) < TOL
+    assert rel_err(h(dB), dB_ref) < TOL
+
+
+def test_lm_head_shapes_odd_vocab():
+    """LM head: logits = h·Eᵀ with E [V,d] and dH = dlogits·E, V odd."""
+    M, d, V = 96, 256, 5003
+    x, E, dl = rn(M, d), rn(V, d, std=0.02), rn(M, V)
+    # forward as a linear with W = Eᵀ
+    y_ref, _ = O.lora_linear_fwd(x, E.T.copy(), None, None, None, 1.0)
+    dx_ref, _, _ = O.lora_linear_bwd(dl, x, E.T.copy(), None, None, None, 1.0)
+    # dX of a linear with W = Eᵀ is dl·E: exercise through the bwd entry point
+    dx, _, _ = ops.lora_linear_bwd(g(dl), g(x), g(E.T.copy()), None, None, None, 1.0)
+    assert rel_err(h(dx), dx_ref) < TOL
+    y, _ = ops.lora_linear_fwd(g(x), g(E.T.copy()), None, None, None, 1.0)
+    assert rel_err(h(y), y_ref) < TOL
+
+
+# ------------------------------------------------------------------ attention
+ATTN = [
+    (4, 12, 12, 128, 64, 0, False),   # GPT-2 small
+    (2, 14, 2, 160, 64, 0, True),     # Qwen-style GQA 7:1, padding mask
+    (2, 4, 1, 96, 256, 0, False),     # Gemma hd=256, GQA 4:1
+    (1, 4, 1, 200, 256, 64, False),   # Gemma sliding window
+    (1, 4, 2, 77, 128, 0, True),      # hd=128, ragged S
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,hd,window,pad", ATTN)
+def test_attention_fwd_bwd(B, Hq, Hkv, S, hd, window, pad):
+    print(f"attention B={B} Hq={Hq} Hkv={Hkv} S={S} hd={hd} win={window}", flush=True)
+    q, k, v = rn(B * S, Hq * hd), rn(B * S, Hkv * hd), rn(B * S, Hkv * hd)
+    scale = hd ** -0.5
+    kpad = None
+    if pad:
+        kpad = np.ones((B, S), np.float32)
+        kpad[-1, S - S // 4:] = 0
+    o_ref, lse_ref = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, True, window, kpad)
+    o, lse = ops.attn_fwd(g(q), g(k), g(v), B, Hq, Hkv, S, hd, scale, True, window,
+                          g(kpad) if pad else None)
+    assert rel_err(h(o), o_ref) < TOL
+    fin = np.isfinite(lse_ref)
+    assert rel_err(h(lse)[fin], lse_ref[fin]) < TOL
+    dout = rn(B * S, Hq * hd)
+    dq_ref, dk_ref, dv_ref = O.attn_bwd(q, k, v, o_ref, dout, lse_ref, B, Hq, Hkv, S, hd, scale,
+                                        True, window, kpad)
+    dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, True,
+                              window, g(kpad) if pad else None)
+    assert rel_err(h(dq), dq_ref) < TOL
+    assert rel_err(h(dk), dk_ref) < TOL
+    assert rel_err(h(dv), dv_ref) < TOL
+
+
+def test_attention_strided_qkv_view():
+    """q/k/v as views into one fused [M, 3d] QKV buffer (GPT-2 c_attn output)."""
+    B, H, S, hd = 2, 4, 64, 64
+    d = H * hd
+    qkv = rn(B * S, 3 * d)
+    q, k, v = qkv[:, :d].copy(), qkv[:, d:2 * d].copy(), qkv[:, 2 * d:].copy()
+    o_ref, _ = O.attn_fwd(q, k, v, B, H, H, S, hd, 0.125)
+    t = g(qkv)
+    o, _ = ops.attn_fwd(t, t[:, d:], t[:, 2 * d:], B, H, H, S, hd, 0.125, q_rs=3 * d, k_rs=3 * d,
+                        v_rs=3 * d)
+    assert rel_err(h(o), o_ref) < TOL
+
+
+# ------------------------------------------------------------------ cross-entropy
+@pytest.mark.parametrize("B,S,V", [(2, 64, 50257), (1, 33, 151936), (2, 16, 262144), (3, 7, 97)])
+def test_cross_entropy(B, S, V):
+    print(f"ce B={B} S={S} V={V}", flush=True)
+    logits = rn(B * S, V, std=2.0)
+    labels = RNG.integers(0, V, (B, S)).astype(np.int32)
+    labels[0, 3] = -100
+    up = 0.5
+    ls_ref, n_ref, dl_ref, nll_ref = O.ce_fwd_bwd(logits, labels, B, S, -100, up)
+    t = g(logits)
+    ls, n, dl, nll = ops.ce_fwd_bwd(t, g(labels), B, S, -100, up, in_place=True)
+    assert int(h(n)[0]) == n_ref
+    assert abs(float(h(ls)[0]) - ls_ref) < TOL * abs(ls_ref)
+    assert rel_err(h(nll), nll_ref) < TOL
+    assert rel_err(h(dl), dl_ref) < TOL
+
+
+def test_cross_entropy_all_ignored_row_zero_grad():
+    B, S, V = 1, 5, 1000
+    logits = rn(B * S, V)
+    labels = np.full((B, S), -100, np.int32)
+    ls, n, dl, _ = ops.ce_fwd_bwd(g(logits), g(labels), B, S)
+    assert int(h(n)[0]) == 0 and float(h(ls)[0]) == 0.0
+    assert np.abs(h(dl)).max() == 0.0
+
+
+# ------------------------------------------------------------------ fp16
+def test_dequant_f16_exhaustive_bit_exact():
+    bits = np.arange(65536, dtype=np.uint16)
+    out = h(ops.dequant_f16(g(bits.view(np.int16))))
+    ref = O.f16_to_f32(bits)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_quant_f16_round_nearest_even_bit_exact():
+    x = np.concatenate([rn(100000, std=0.02), rn(1000, std=1e-6), rn(100, std=3e4)])
+    out = h(ops.quant_f16(g(x))).view(np.uint16)
+    assert np.array_equal(out, O.f32_to_f16(x))
+
+
+def test_dequant_large_and_unaligned():
+    n = (1 << 22) + 3
+    bits = RNG.integers(0, 0x7C00, n).astype(np.uint16)
+    out = h(ops.dequant_f16(g(bits.view(np.int16))))
+    assert np.array_equal(out, O.f16_to_f32(bits))
+    out2 = h(ops.dequant_f16(g(bits.view(np.int16))[1:]))
+    assert np.array_equal(out2, O.f16_to_f32(bits[1:]))
+
+
+# ------------------------------------------------------------------ Adam / clip
+def test_adam_sumsq_clip():
+    n = 100003
+    p, gr = rn(n), rn(n, std=0.1)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    tp, tg, tm, tv = g(p), g(gr), g(m), g(v)
+    ss = ops.sumsq(tg)
+    ss_ref = O.sumsq(gr)
+    assert abs(float(h(ss)[0]) - ss_ref) < 1e-12 * ss_ref
+    sc = ops.clip_scale(ss, 1.0)
+    s_ref, n_ref = O.clip_scale(ss_ref, 1.0)
+    assert abs(float(h(sc)[0]) - s_ref) < 1e-7 and abs(float(h(sc)[1]) - n_ref) < 1e-6
+    gref = (gr * np.float32(s_ref)).astype(np.float32)
+    for t in (1, 2, 3):
+        ops.adam_step(tp, tg, tm, tv, 2e-4, 0.9, 0.999, 1e-8, 0.0, t, clip_scale=sc)
+        O.adam_step(p, gref, m, v, 2e-4, 0.9, 0.999, 1e-8, 0.0, t)
+    assert rel_err(h(tp), p) < 1e-6
+    assert rel_err(h(tm), m) < 1e-6
+    ops.adam_step(tp, tg, tm, tv, 2e-4, 0.9, 0.999, 1e-8, 0.0, 4, zero_grad=True)
+    assert np.abs(h(tg)).max() == 0
+
+
+# ------------------------------------------------------------------ support ops
+def test_layernorm():
+    x, gm, b, dy = rn(300, 1024, std=2), rn(1024), rn(1024), rn(300, 1024)
+    y_ref, mu, rs = O.layernorm_fwd(x, gm, b, 1e-5)
+    y, tmu, trs = ops.layernorm_fwd(g(x), g(gm), g(b), 1e-5)
+    assert rel_err(h(y), y_ref) < TOL
+    assert rel_err(h(ops.layernorm_bwd(g(dy), g(x), g(gm), tmu, trs)),
+                   O.layernorm_bwd(dy, x, gm, mu, rs)) < TOL
+
+
+@pytest.mark.parametrize("C,unit", [(896, 0), (640, 1), (256, 1)])
+def test_rmsnorm(C, unit):
+    x, w, dy = rn(500, C, std=2), rn(C, std=0.3), rn(500, C)
+    y_ref, rs = O.rmsnorm_fwd(x, w, 1e-6, unit)
+    y, trs = ops.rmsnorm_fwd(g(x), g(w), 1e-6, unit)
+    assert rel_err(h(y), y_ref) < TOL
+    assert rel_err(h(ops.rmsnorm_bwd(g(dy), g(x), g(w), trs, unit)),
+                   O.rmsnorm_bwd(dy, x, w, rs, unit)) < TOL
+
+
+@pytest.mark.parametrize("act,gated", [(0, False), (0, True), (1, True)])
+def test_glu(act, gated):
+    n = 300007
+    gate, up, dout = rn(n, std=3), rn(n) if gated else None, rn(n)
+    out = ops.glu_fwd(g(gate), g(up) if gated else None, act)
+    assert rel_err(h(out), O.glu_fwd(gate, up, act)) < TOL
+    dg, du = ops.glu_bwd(g(dout), g(gate), g(up) if gated else None, act)
+    dg_ref, du_ref = O.glu_bwd(dout, gate, up, act)
+    assert rel_err(h(dg), dg_ref) < TOL
+    if gated:
+        assert rel_err(h(du), du_ref) < TOL
+
+
+@pytest.mark.parametrize("S,H,hd,theta", [(1024, 14, 64, 1e6), (256, 4, 256, 1e4)])
+def test_rope(S, H, hd, theta):
+    B = 2
+    x = rn(B * S, H * hd)
+    t = g(x)
+    ops.rope_(t, B, S, H, hd, theta)
+    assert rel_err(h(t), O.rope(x, B, S, H, hd, theta)) < TOL
+    ops.rope_(t, B, S, H, hd, theta, inverse=True)
+    assert rel_err(h(t), x) < TOL
+
+
+def test_embed():
+    V, C, S = 50257, 768, 128
+    wte, wpe = rn(V, C, std=0.02), rn(1024, C, std=0.02)
+    ids = RNG.integers(0, V, (4, S)).astype(np.int32)
+    out = ops.embed(g(ids), S, g(wte), g(wpe), 1.0)
+    assert np.array_equal(h(out), O.embed(ids, S, wte, wpe, 1.0))
+    w16 = wte.astype(np.float16)
+    out16 = ops.embed(g(ids), S, g(w16), None, math.sqrt(640))
+    ref16 = O.embed(ids, S, None, None, math.sqrt(640), wte_f16=w16.view(np.uint16))
+    assert np.array_equal(h(out16), ref16)
