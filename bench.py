@@ -44,6 +44,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the captured step graph instead of launching eagerly (measured "
+                         "slower on ROCm 7.2 for this step; per-kernel timing is unavailable "
+                         "inside graphs, so --graph implies --no-timing)")
     ap.add_argument("--no-timing", action="store_true",
                     help="skip the per-kernel HIP events (roofline becomes null)")
     return ap.parse_args()
@@ -113,17 +117,19 @@ def main():
     labels = ids.clone()
 
     def step():
-        model.fwd_bwd(ids, labels, n_micro=rc.accum, seqs_per_micro=rc.batch, S=rc.seq)
-        model.opt_step(args.lr, clip=1.0)
+        model.train_step(ids, labels, n_micro=rc.accum, seqs_per_micro=rc.batch, S=rc.seq,
+                         lr=args.lr, clip=1.0, graph=args.graph)
 
-    for _ in range(args.warmup):
+    # Timing events are part of the captured step graph, so switch them on
+    # before the warm-up (which captures the graph) and clear their totals
+    # before the timed region.
+    timing = not (args.no_timing or args.graph)
+    model.set_timing(timing)
+    for _ in range(max(1, args.warmup)):
         step()
-    losses = []
     model.read_stats()
     torch.cuda.synchronize()
-    timing = not args.no_timing
     model.reset_timing()
-    model.set_timing(timing)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):

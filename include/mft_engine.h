@@ -82,6 +82,18 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask,
  * on the device (no host round trip). */
 int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps,
                        float wd, float clip);
+/* One complete optimizer step: mft_model_fwd_bwd + mft_model_opt_step with
+ * the loss statistics reset first.  use_graph != 0 captures the whole step
+ * (every kernel of forward, CE, backward, clip and Adam) into a HIP graph on
+ * the first call and replays it on later calls with the same buffers and
+ * shapes; the learning rate and the other Adam scalars are uploaded before
+ * each replay, so a schedule can change them per step.  The caller's
+ * stream is ordered before and after the replay by events. */
+int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask,
+                         const int32_t* labels, int n_micro,
+                         int seqs_per_micro, int S, float upstream, float lr,
+                         float b1, float b2, float eps, float wd, float clip,
+                         int use_graph);
 /* Synchronises, returns the mean over micro-batches of the micro-batch mean
  * loss since the last call (the driver's accum_loss / accum), the number of
  * valid targets and the last pre-clip grad norm; resets the loss statistics. */

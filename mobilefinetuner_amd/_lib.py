@@ -83,6 +83,7 @@ _SIGS = {
     "mft_model_fwd_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _F]),
     "mft_model_forward": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "mft_model_opt_step": (_I, [_P, _F, _F, _F, _F, _F, _F]),
+    "mft_model_train_step": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _F, _F, _F, _F, _F, _F, _I]),
     "mft_model_read_stats": (_I, [_P, C.POINTER(_F), C.POINTER(_L), C.POINTER(_F)]),
     "mft_model_set_timing": (_I, [_P, _I]),
     "mft_model_timing": (_I, [_P, _I, C.POINTER(_D), C.POINTER(_D), C.POINTER(_L)]),

@@ -128,6 +128,14 @@ void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n);
 void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
                int64_t n, float lr, float b1, float b2, float eps, float wd,
                int t, const float* clip_scale, bool zero_grad);
+// Device-parameterised variants for captured step graphs:
+// hp = {lr, b1, b2, eps, wd, max_norm}; *tstep is the 1-based Adam step,
+// advanced by clip_scale_dev.
+void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n,
+                   const float* hp, const int* tstep, const float* clip_scale, bool zero_grad);
+void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,
+                    int* tstep);
+void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n);
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out);
 void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,
                 float* norm);
@@ -143,6 +151,17 @@ void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
 void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
                  const float* w, const float* rstd, int64_t M, int64_t C,
                  bool unit_offset, float* dx, bool accumulate);
+// Row-loop fallbacks of the four norm launchers (elementwise.hip).
+void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g, const float* b,
+                           int64_t M, int64_t C, float eps, float* y, float* mean, float* rstd);
+void layernorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x, const float* g,
+                           const float* mean, const float* rstd, int64_t M, int64_t C,
+                           float* dx, bool accumulate);
+void rmsnorm_fwd_rowloop(hipStream_t s, const float* x, const float* w, int64_t M, int64_t C,
+                         float eps, bool unit_offset, float* y, float* rstd);
+void rmsnorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x, const float* w,
+                         const float* rstd, int64_t M, int64_t C, bool unit_offset, float* dx,
+                         bool accumulate);
 void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
              int act, float* out);
 void glu_bwd(hipStream_t s, const float* dout, const float* gate,

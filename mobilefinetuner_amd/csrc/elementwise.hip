@@ -274,6 +274,56 @@ __global__ void adam_kernel(float* __restrict__ p, float* __restrict__ g,
   }
 }
 
+// Same update with the hyper-parameters and the 1-based step count read
+// from device memory (hp = {lr, b1, b2, eps, wd}), so a captured step graph
+// can be replayed with a new learning rate and step.
+__global__ void adam_dev_kernel(float* __restrict__ p, float* __restrict__ g,
+                                float* __restrict__ m, float* __restrict__ v, int64_t n,
+                                const float* __restrict__ hp, const int* __restrict__ tstep,
+                                const float* __restrict__ clip_scale, int zero_grad) {
+  const float lr = hp[0], b1 = hp[1], b2 = hp[2], eps = hp[3], wd = hp[4];
+  const int t = *tstep;
+  const double bc1 = 1.0 - pow((double)b1, (double)t);
+  const double bc2 = 1.0 - pow((double)b2, (double)t);
+  const float cs = clip_scale ? *clip_scale : 1.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float gi = g[i] * cs;
+    const float mi = b1 * m[i] + (1.f - b1) * gi;
+    const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
+    m[i] = mi;
+    v[i] = vi;
+    const double mh = mi / bc1, vh = vi / bc2;
+    double pi = p[i];
+    if (wd != 0.f) pi -= (double)lr * wd * pi;
+    pi -= (double)lr * mh / (sqrt(vh) + eps);
+    p[i] = (float)pi;
+    if (zero_grad) g[i] = 0.f;
+  }
+}
+
+// Clip factor from Σg² with max_norm = hp[5]; advances the step counter.
+__global__ void clip_dev_kernel(const double* ss, const float* hp, float* scale, float* norm,
+                                int* tstep) {
+  const float max_norm = hp[5];
+  float nv = (float)sqrt(*ss);
+  float sc = 1.f;
+  if (max_norm > 0.f && nv > max_norm) {
+    sc = max_norm / (nv + 1e-6f);
+    nv = max_norm;
+  }
+  *scale = sc;
+  *norm = nv;
+  *tstep += 1;
+}
+
+__global__ void add_out_kernel(float* __restrict__ out, const float* __restrict__ a,
+                               const float* __restrict__ b, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = a[i] + b[i];
+}
+
 __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g,
                                                     int64_t n, double* out) {
   __shared__ double red[4];
@@ -349,32 +399,34 @@ inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 8192) {
 
 }  // namespace
 
-void layernorm_fwd(hipStream_t s, const float* x, const float* g,
-                   const float* b, int64_t M, int64_t C, float eps, float* y,
-                   float* mean, float* rstd) {
+// Row-loop versions for shapes the vectorised kernels (norms.hip) do not
+// take: C not a multiple of 4, unaligned rows, or C > 2048.
+void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g,
+                           const float* b, int64_t M, int64_t C, float eps, float* y,
+                           float* mean, float* rstd) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(layernorm_fwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
                      x, g, b, M, (int)C, eps, y, mean, rstd);
   MFT_LAUNCH_CHECK();
 }
-void layernorm_bwd(hipStream_t s, const float* dy, const float* x,
-                   const float* g, const float* mean, const float* rstd,
-                   int64_t M, int64_t C, float* dx, bool accumulate) {
+void layernorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x,
+                           const float* g, const float* mean, const float* rstd,
+                           int64_t M, int64_t C, float* dx, bool accumulate) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(layernorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
                      dy, x, g, mean, rstd, M, (int)C, dx, accumulate ? 1 : 0);
   MFT_LAUNCH_CHECK();
 }
-void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
-                 int64_t C, float eps, bool unit_offset, float* y, float* rstd) {
+void rmsnorm_fwd_rowloop(hipStream_t s, const float* x, const float* w, int64_t M,
+                         int64_t C, float eps, bool unit_offset, float* y, float* rstd) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
                      x, w, M, (int)C, eps, unit_offset ? 1 : 0, y, rstd);
   MFT_LAUNCH_CHECK();
 }
-void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
-                 const float* w, const float* rstd, int64_t M, int64_t C,
-                 bool unit_offset, float* dx, bool accumulate) {
+void rmsnorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x,
+                         const float* w, const float* rstd, int64_t M, int64_t C,
+                         bool unit_offset, float* dx, bool accumulate) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
                      dy, x, w, rstd, M, (int)C, unit_offset ? 1 : 0, dx, accumulate ? 1 : 0);
@@ -439,6 +491,23 @@ void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
   const double bc2 = 1.0 - std::pow((double)b2, t);
   hipLaunchKernelGGL(adam_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, lr, b1,
                      b2, eps, wd, bc1, bc2, clip_scale, zero_grad ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n,
+                   const float* hp, const int* tstep, const float* clip_scale, bool zero_grad) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(adam_dev_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, hp,
+                     tstep, clip_scale, zero_grad ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,
+                    int* tstep) {
+  hipLaunchKernelGGL(clip_dev_kernel, dim3(1), dim3(1), 0, s, ss, hp, scale, norm, tstep);
+  MFT_LAUNCH_CHECK();
+}
+void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(add_out_kernel, dim3(grid_for(n)), dim3(256), 0, s, out, a, b, n);
   MFT_LAUNCH_CHECK();
 }
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out) {

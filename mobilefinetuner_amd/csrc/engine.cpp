@@ -115,8 +115,25 @@ struct mft_model_s {
   int64_t* d_tmpcnt = nullptr;
   double* d_sumsq = nullptr;
   float* d_clip = nullptr;  // [0] scale, [1] norm
+  float* d_hp = nullptr;    // {lr, b1, b2, eps, wd, max_norm}
+  int* d_t = nullptr;       // Adam step count (advanced on the device)
+  float* h_hp_ring = nullptr;  // pinned staging ring for d_hp uploads
+  int hp_slot = 0;
   int n_micro_pending = 0;
   int adam_t = 0;
+  // captured train-step graph
+  hipStream_t cap_stream = nullptr;
+  hipEvent_t ev_in = nullptr, ev_out = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  bool capturing = false;
+  std::vector<TimedLaunch> graph_timed;  // event pairs recorded by the graph
+  std::vector<hipEvent_t> gev_pool;
+  struct {
+    const void *ids, *mask, *labels;
+    int n_micro, seqs, S;
+    float upstream;
+    bool timing;
+  } graph_key{};
   // timing
   bool timing = false;
   std::vector<TimedLaunch> launches;
@@ -353,10 +370,22 @@ void alloc_acts(mft_model_s* m) {
   m->d_tmpcnt = reinterpret_cast<int64_t*>(static_cast<char*>(sc) + 1024);
   m->d_sumsq = reinterpret_cast<double*>(static_cast<char*>(sc) + 1280);
   m->d_clip = reinterpret_cast<float*>(static_cast<char*>(sc) + 1536);
+  m->d_hp = reinterpret_cast<float*>(static_cast<char*>(sc) + 1792);
+  m->d_t = reinterpret_cast<int*>(static_cast<char*>(sc) + 2048);
+  MFT_HIP(hipHostMalloc(reinterpret_cast<void**>(&m->h_hp_ring), 256 * 8 * sizeof(float)));
+  MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
+  MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
+  MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
 }
 
 // ---- timing helpers -------------------------------------------------------------
 hipEvent_t next_event(mft_model_s* m) {
+  if (m->capturing) {  // events owned by the captured graph
+    hipEvent_t e;
+    MFT_HIP(hipEventCreate(&e));
+    m->gev_pool.push_back(e);
+    return e;
+  }
   if (m->ev_next == m->ev_pool.size()) {
     hipEvent_t e;
     MFT_HIP(hipEventCreate(&e));
@@ -384,7 +413,9 @@ struct Timed {
     if (m->timing) MFT_HIP(hipEventRecord(ev.stop, m->stream));
   }
   ~Timed() {
-    if (m->timing) m->launches.push_back({cls, work, ev.start, ev.stop});
+    if (!m->timing) return;
+    if (m->capturing) m->graph_timed.push_back({cls, work, ev.start, ev.stop});
+    else m->launches.push_back({cls, work, ev.start, ev.stop});
   }
 };
 
@@ -522,8 +553,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     if (gemma) {
       lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr);
       rmsnorm_fwd(s, a.o, pd<float>(m, L.pan), M, d, c.norm_eps, true, m->dtmp, a.ors);
-      MFT_HIP(hipMemcpyAsync(a.hmid, a.x, sizeof(float) * M * d, hipMemcpyDeviceToDevice, s));
-      add_inplace(s, a.hmid, m->dtmp, M * d);
+      add_out(s, a.hmid, a.x, m->dtmp, M * d);
     } else {
       lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x);
     }
@@ -534,8 +564,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     if (gemma) {
       lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr);
       rmsnorm_fwd(s, a.mo, pd<float>(m, L.pfn), M, d, c.norm_eps, true, m->dtmp, a.mrs);
-      MFT_HIP(hipMemcpyAsync(hout, a.hmid, sizeof(float) * M * d, hipMemcpyDeviceToDevice, s));
-      add_inplace(s, hout, m->dtmp, M * d);
+      add_out(s, hout, a.hmid, m->dtmp, M * d);
     } else {
       lin_fwd(m, L.lin[T_DOWN], a.act, M, hout, a.xa[T_DOWN], a.hmid);
     }
@@ -660,6 +689,87 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   }
 }
 
+// Host → device hyper-parameters through a ring of pinned slots (a slot is
+// not rewritten before 255 later steps have been enqueued).
+void upload_hparams(mft_model_s* m, float lr, float b1, float b2, float eps, float wd, float clip) {
+  float* slot = m->h_hp_ring + 8 * (m->hp_slot++ % 256);
+  slot[0] = lr; slot[1] = b1; slot[2] = b2; slot[3] = eps; slot[4] = wd; slot[5] = clip;
+  MFT_HIP(hipMemcpyAsync(m->d_hp, slot, 6 * sizeof(float), hipMemcpyHostToDevice, m->stream));
+}
+
+// clip_and_get_grad_norm + Adam::step + zero_grad on the flat LoRA arrays;
+// reads d_hp / d_t only, so it can live inside a captured graph.
+void opt_device(mft_model_s* m) {
+  const hipStream_t s = m->stream;
+  fill_const(s, reinterpret_cast<float*>(m->d_sumsq), 2, 0.f);  // one double = two floats
+  sumsq(s, m->lora_g, m->lora_n, m->d_sumsq);
+  clip_scale_dev(s, m->d_sumsq, m->d_hp, m->d_clip, m->d_clip + 1, m->d_t);
+  adam_step_dev(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, m->d_hp, m->d_t, m->d_clip, true);
+}
+
+void zero_stats(mft_model_s* m, int n_micro) {
+  // per-micro loss sums (doubles) and counts (int64) are 8 bytes each
+  fill_const(m->stream, reinterpret_cast<float*>(m->d_loss), 2 * n_micro, 0.f);
+  fill_const(m->stream, reinterpret_cast<float*>(m->d_cnt), 2 * n_micro, 0.f);
+}
+
+void drop_graph(mft_model_s* m) {
+  if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+  m->graph_exec = nullptr;
+  for (auto e : m->gev_pool) (void)hipEventDestroy(e);
+  m->gev_pool.clear();
+  m->graph_timed.clear();
+}
+
+void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S);
+void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs, int S, float upstream,
+                   bool backward);
+void backward(mft_model_s* m, const float* mask, int nseq, int S);
+
+// Capture one whole training step (stats reset, fwd, CE, bwd, clip, Adam) on
+// the model's private stream into an executable graph.
+void capture_step(mft_model_s* m, const int32_t* ids, const float* mask, const int32_t* labels, int n_micro,
+                  int seqs, int S, float upstream) {
+  MFT_HIP(hipStreamSynchronize(m->stream));
+  MFT_HIP(hipStreamSynchronize(m->cap_stream));
+  drop_graph(m);
+  const hipStream_t saved = m->stream;
+  m->stream = m->cap_stream;
+  m->capturing = true;
+  hipGraph_t g = nullptr;
+  try {
+    MFT_HIP(hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal));
+    zero_stats(m, n_micro);
+    m->n_micro_pending = 0;
+    forward(m, ids, mask, n_micro * seqs, S);
+    cross_entropy(m, labels, n_micro, seqs, S, upstream, true);
+    backward(m, mask, n_micro * seqs, S);
+    opt_device(m);
+    MFT_HIP(hipStreamEndCapture(m->cap_stream, &g));
+    MFT_HIP(hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0));
+    (void)hipGraphDestroy(g);
+  } catch (...) {
+    hipGraph_t junk = nullptr;
+    (void)hipStreamEndCapture(m->cap_stream, &junk);
+    if (junk) (void)hipGraphDestroy(junk);
+    if (g) (void)hipGraphDestroy(g);
+    m->stream = saved;
+    m->capturing = false;
+    drop_graph(m);
+    throw;
+  }
+  m->stream = saved;
+  m->capturing = false;
+  m->graph_key.ids = ids;
+  m->graph_key.mask = mask;
+  m->graph_key.labels = labels;
+  m->graph_key.n_micro = n_micro;
+  m->graph_key.seqs = seqs;
+  m->graph_key.S = S;
+  m->graph_key.upstream = upstream;
+  m->graph_key.timing = m->timing;
+}
+
 template <typename F>
 int guarded(F&& f) {
   try {
@@ -682,7 +792,8 @@ void check_cfg(const mft_model_cfg& c) {
   MFT_CHECK_ARG(c.n_head % c.n_kv_head == 0, "n_head must be a multiple of n_kv_head");
   MFT_CHECK_ARG(c.arch != MFT_ARCH_GPT2 || c.n_head * c.head_dim == c.d, "GPT-2 needs n_head*head_dim == d");
   MFT_CHECK_ARG(c.arch != MFT_ARCH_GPT2 || c.n_head == c.n_kv_head, "GPT-2 has no GQA");
-  MFT_CHECK_ARG(c.lora_r >= 0 && c.lora_r <= 32, "lora_r must be in [0,32]");
+  MFT_CHECK_ARG(c.lora_r == 0 || c.lora_r == 4 || c.lora_r == 8 || c.lora_r == 16 || c.lora_r == 32,
+                "lora_r must be 0, 4, 8, 16 or 32");
   MFT_CHECK_ARG(c.d % 4 == 0 && c.d_ff % 4 == 0 && c.head_dim % 4 == 0, "dims must be multiples of 4");
 }
 
@@ -715,6 +826,12 @@ int mft_model_destroy(mft_model m) {
   return guarded([&] {
     if (!m) return;
     (void)hipStreamSynchronize(m->stream);
+    if (m->cap_stream) (void)hipStreamSynchronize(m->cap_stream);
+    drop_graph(m);
+    if (m->cap_stream) (void)hipStreamDestroy(m->cap_stream);
+    if (m->ev_in) (void)hipEventDestroy(m->ev_in);
+    if (m->ev_out) (void)hipEventDestroy(m->ev_out);
+    if (m->h_hp_ring) (void)hipHostFree(m->h_hp_ring);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
     void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss};
     for (void* b : bufs)
@@ -796,13 +913,56 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask, const 
 int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps, float wd, float clip) {
   return guarded([&] {
     if (!m) throw Error(MFT_EINVAL, "null model");
-    const hipStream_t s = m->stream;
-    fill_const(s, reinterpret_cast<float*>(m->d_sumsq), 2, 0.f);  // one double = two floats
-    sumsq(s, m->lora_g, m->lora_n, m->d_sumsq);
-    clip_scale(s, m->d_sumsq, clip, m->d_clip, m->d_clip + 1);
+    upload_hparams(m, lr, b1, b2, eps, wd, clip);
+    opt_device(m);
     m->adam_t++;
-    adam_step(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, lr, b1, b2, eps, wd, m->adam_t, m->d_clip,
-              true);
+  });
+}
+
+int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, const int32_t* labels,
+                         int n_micro, int seqs_per_micro, int S, float upstream, float lr, float b1,
+                         float b2, float eps, float wd, float clip, int use_graph) {
+  return guarded([&] {
+    if (!m || !ids || !labels) throw Error(MFT_EINVAL, "null argument");
+    const int nseq = n_micro * seqs_per_micro;
+    if (n_micro <= 0 || seqs_per_micro <= 0 || S <= 0) throw Error(MFT_EINVAL, "empty batch");
+    if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
+    if (m->c.arch == MFT_ARCH_GPT2 && S > m->c.max_pos) throw Error(MFT_EINVAL, "seq_len exceeds n_positions");
+    if (!use_graph) {
+      zero_stats(m, n_micro);
+      m->n_micro_pending = 0;
+      forward(m, ids, mask, nseq, S);
+      cross_entropy(m, labels, n_micro, seqs_per_micro, S, upstream, true);
+      backward(m, mask, nseq, S);
+      upload_hparams(m, lr, b1, b2, eps, wd, clip);
+      opt_device(m);
+      m->adam_t++;
+      return;
+    }
+    const bool same = m->graph_exec && m->graph_key.ids == ids && m->graph_key.mask == mask &&
+                      m->graph_key.labels == labels && m->graph_key.n_micro == n_micro &&
+                      m->graph_key.seqs == seqs_per_micro && m->graph_key.S == S &&
+                      m->graph_key.upstream == upstream && m->graph_key.timing == m->timing;
+    if (!same) capture_step(m, ids, mask, labels, n_micro, seqs_per_micro, S, upstream);
+    upload_hparams(m, lr, b1, b2, eps, wd, clip);
+    MFT_HIP(hipEventRecord(m->ev_in, m->stream));
+    MFT_HIP(hipStreamWaitEvent(m->cap_stream, m->ev_in, 0));
+    MFT_HIP(hipGraphLaunch(m->graph_exec, m->cap_stream));
+    MFT_HIP(hipEventRecord(m->ev_out, m->cap_stream));
+    MFT_HIP(hipStreamWaitEvent(m->stream, m->ev_out, 0));
+    m->n_micro_pending = n_micro;
+    m->adam_t++;
+    if (m->timing) {
+      // The graph re-records the same events on every replay: read them now.
+      MFT_HIP(hipStreamSynchronize(m->cap_stream));
+      for (auto& t : m->graph_timed) {
+        float ms = 0.f;
+        MFT_HIP(hipEventElapsedTime(&ms, t.a, t.b));
+        m->t_ms[t.cls] += ms;
+        m->t_work[t.cls] += t.work;
+        m->t_n[t.cls] += 1;
+      }
+    }
   });
 }
 

@@ -1,19 +1,35 @@
 // gemm.hip — LoRA-linear GEMMs for gfx950 (CDNA4).
 //
-// C[M,N] = A[M,K]·op(B) on the fp32 matrix cores (v_mfma_f32_32x32x2_f32),
-// 256-thread workgroups = 4 wave64s in a 2×2 grid, LDS double-buffered K
-// panels (BK = 16), epilogue fusing bias, the rank-r LoRA term
-// scale·P[M,r]·Q, a residual add, and accumulation into C.  B may be [K,N]
-// (frozen W in the forward, tied embedding in the LM-head backward) or [N,K]
-// (W in dX = dY·Wᵀ, embedding in the LM-head forward), fp32 or fp16; fp16 is
-// widened to fp32 while the tile is staged into LDS, so the frozen weight is
-// read from HBM at 2 bytes/element and never materialised as fp32.
+// C[M,N] = A[M,K]·op(B) on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+// A 256-thread workgroup owns a BM×BN tile; its four wave64s each compute a
+// 64×64 sub-tile as 2×2 MFMA tiles (four independent accumulation chains per
+// wave).  When the workgroup tile is smaller than 2×2 sub-tiles, the waves
+// split every K panel instead (KW-way) and their partial tiles are summed
+// through LDS in a fixed order at the end, so each LDS element is read by one
+// wave only.  K is consumed in panels of BK through a two-stage LDS ring; the
+// global loads of panel k+2 are in flight while panel k is multiplied.  The
+// epilogue fuses bias, the rank-r LoRA term scale·P[M,r]·Q, a residual add
+// and accumulation into C.
 //
-// LDS holds both panels k-contiguous (As[m][k], Bs[n][k], row pitch BK+4
-// floats) so every MFMA operand fetch is a ds_read_b128 without bank
-// conflicts: within one BK=16 panel, lane (i, h) of a 32×32 tile consumes
-// k = 8h .. 8h+7 over eight MFMAs (the k order inside a panel is permuted the
-// same way for A and B, which leaves the sum unchanged).
+// B may be [K,N] (frozen W in the forward, tied embedding in the LM-head
+// backward) or [N,K] (W in dX = dY·Wᵀ, embedding in the LM-head forward),
+// fp32 or fp16; fp16 is widened to fp32 while the panel is staged into LDS,
+// so a frozen fp16 weight is read from HBM at 2 bytes/element and never
+// materialised as fp32.
+//
+// LDS layouts (pitch = row length + 4 floats, conflict-free):
+//   A       As[m][k]  — fragments read as 128-bit rows;
+//   B [N,K] Bs[n][k]  — same;
+//   B [K,N] Bs[k][n]  — global rows land with 128-bit stores, fragments are
+//                       read as 32-bit columns (consecutive n per lane).
+// In-panel k order: wave kw takes k ∈ [kw·KS, (kw+1)·KS) (KS = BK/KW); lane
+// half h of a 32×32 tile supplies k = kw·KS + h·KS/2 + j for its KS/2 MFMAs
+// (A and B permuted identically, so the sum is unchanged).  Interior tiles
+// take an unchecked load path; edge tiles check every element.
+#include <cstdio>
+#include <cstdlib>
+#include <type_traits>
+
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -21,9 +37,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace mft {
 namespace {
-
-constexpr int BK = 16;
-constexpr int PITCH = BK + 4;  // floats per LDS row
 
 struct GemmParams {
   const float* A;
@@ -34,6 +47,7 @@ struct GemmParams {
   int k_chunk;       // K range per split (multiple of BK)
   int tiles_m, tiles_n, tiles_per_xcd;
   float* partial;    // split-K: [splits][M][N] raw accumulators
+  int b_vec;         // B rows allow 128-bit (fp32) / 64-bit (fp16) loads
   GemmEpilogue ep;
 };
 
@@ -41,8 +55,12 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
-__device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep,
-                                                float acc, int m, int n,
+__device__ __forceinline__ floatx4 widen4(uint2 u) {
+  return floatx4{half_bits_to_float(u.x & 0xffff), half_bits_to_float(u.x >> 16),
+                 half_bits_to_float(u.y & 0xffff), half_bits_to_float(u.y >> 16)};
+}
+
+__device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep, float acc, int m, int n,
                                                 const float* C, int64_t ldc) {
   float v = acc;
   if (ep.bias) v += ep.bias[n];
@@ -58,18 +76,27 @@ __device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep,
   return v;
 }
 
-template <int BM, int BN, bool B_NK, bool B_F16>
+template <int BM, int BN, int BK, bool B_NK, bool B_F16>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
-  constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
-  constexpr int TM = WM / 32, TN = WN / 32;    // 32×32 MFMA tiles per wave
-  constexpr int A_ITEMS = BM / 64;             // float4 per thread per panel
-  constexpr int B_ITEMS = BN / 64;
-  __shared__ __attribute__((aligned(16))) float As[2][BM * PITCH];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN * PITCH];
+  constexpr int NWM = BM / 64, NWN = BN / 64;  // 64×64 sub-tiles
+  constexpr int KW = 4 / (NWM * NWN);          // waves sharing a sub-tile (K split)
+  constexpr int KS = BK / KW;                  // k per wave per panel
+  constexpr int HK = KS / 2;                   // k per lane half per panel
+  static_assert(NWM * NWN * KW == 4 && HK % 8 == 0, "tile config");
+  constexpr int PA = BK + 4;
+  constexpr int PB = B_NK ? BK + 4 : BN + 4;
+  constexpr int A_ITEMS = BM * BK / 4 / 256;   // float4 per thread per panel
+  constexpr int B_ITEMS = BN * BK / 4 / 256;
+  constexpr int A_STAGE = BM * PA;
+  constexpr int B_STAGE = B_NK ? BN * PB : BK * PB;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  constexpr int SMEM = (KW > 1 && 4 * 4096 > 2 * STAGE) ? 4 * 4096 : 2 * STAGE;
+  __shared__ __attribute__((aligned(16))) float smem[SMEM];
 
-  // XCD-aware tile order: consecutive workgroup ids land on different XCDs
-  // (round-robin dispatch), so tile = xcd-major chunk + local index keeps the
-  // workgroups that share a B column panel on one XCD's L2.
+  // XCD-aware tile order: workgroup ids are dispatched round-robin over the
+  // 8 XCDs, so tile = (id % 8) * tiles_per_xcd + id / 8 gives every XCD a
+  // contiguous run of tiles (m fastest): the workgroups sharing a B column
+  // panel share one XCD's L2.
   const int wg = blockIdx.x;
   const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
   if (tile >= p.tiles_m * p.tiles_n) return;
@@ -83,167 +110,233 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wave_m = wave & 1, wave_n = wave >> 1;
+  const int kw = wave % KW;                 // K-split index
+  const int sub = wave / KW;                // 64×64 sub-tile index
+  const int wm = (sub % NWM) * 64, wn = (sub / NWM) * 64;
   const int li = lane & 31, lh = lane >> 5;
+  const int klane = kw * KS + lh * HK;      // first in-panel k of this lane
 
-  floatx16 acc[TM][TN];
+  floatx16 acc[2][2];
 #pragma unroll
-  for (int a = 0; a < TM; ++a)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < TN; ++b)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
-  floatx4 ra[A_ITEMS], rb[B_ITEMS];
+  // Two register staging sets: panel p lives in set p%2 from the issue of its
+  // global loads until it is parked in LDS stage p%2.
+  floatx4 ra_set[2][A_ITEMS], rb_set[2][B_ITEMS];
 
-  auto load_panel = [&](int k0) {
+  auto load_panel = [&](auto sc, int k0) {
+    constexpr int S = decltype(sc)::value;
+    floatx4(&ra)[A_ITEMS] = ra_set[S];
+    floatx4(&rb)[B_ITEMS] = rb_set[S];
+    // Branch-free: every address is clamped into its tensor (rows past M or
+    // N only feed outputs that are never stored; an aligned 4-vector at
+    // k < K never crosses a row because the pitches are multiples of 4) and
+    // k ≥ kend elements are zeroed by selects, so the loads sit in the same
+    // basic block as the MFMAs and can be interleaved with them.
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
       const int flat = tid + 256 * it;
-      const int row = flat >> 2, kq = (flat & 3) * 4;
-      const int gm = m0 + row, gk = k0 + kq;
-      ra[it] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (gm < p.M) {
-        const float* src = p.A + (int64_t)gm * p.lda + gk;
-        if (gk + 4 <= kend) {
-          ra[it] = *reinterpret_cast<const floatx4*>(src);
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      const int gm = min(m0 + row, p.M - 1), gk = k0 + kq;
+      floatx4 v = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
+      ra[it] = v;
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      floatx4 v;
+      if constexpr (B_NK) {
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        const int gn = min(n0 + row, p.N - 1), gk = k0 + kq;
+        const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
+        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
+      } else {
+        const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+        const int gk = k0 + k, gn = n0 + nq;
+        const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
+        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
+        const bool ok = gk < kend;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = ok ? v[e] : 0.f;
+      }
+      rb[it] = v;
+    }
+  };
+  auto store_panel = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    const floatx4(&ra)[A_ITEMS] = ra_set[S];
+    const floatx4(&rb)[B_ITEMS] = rb_set[S];
+    float* As = smem + S * STAGE;
+    float* Bs = As + A_STAGE;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = ra[it];
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      if constexpr (B_NK) {
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = rb[it];
+      } else {
+        const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = rb[it];
+      }
+    }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  auto compute = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    const float* as = smem + S * STAGE;
+    const float* bs = as + A_STAGE;
+#pragma unroll
+    for (int c8 = 0; c8 < HK / 8; ++c8) {
+      const int kl = klane + 8 * c8;
+      floatx4 fa[2][2];
+      float fb[2][8];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const float* src = as + (wm + a * 32 + li) * PA + kl;
+        fa[a][0] = *reinterpret_cast<const floatx4*>(src);
+        fa[a][1] = *reinterpret_cast<const floatx4*>(src + 4);
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int col = wn + b * 32 + li;
+        if constexpr (B_NK) {
+          const floatx4 u = *reinterpret_cast<const floatx4*>(bs + col * PB + kl);
+          const floatx4 v = *reinterpret_cast<const floatx4*>(bs + col * PB + kl + 4);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            fb[b][t] = u[t];
+            fb[b][4 + t] = v[t];
+          }
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (gk + e < kend) ra[it][e] = src[e];
+          for (int t = 0; t < 8; ++t) fb[b][t] = bs[(kl + t) * PB + col];
         }
       }
-    }
 #pragma unroll
-    for (int it = 0; it < B_ITEMS; ++it) {
-      const int flat = tid + 256 * it;
-      if constexpr (B_NK) {
-        const int row = flat >> 2, kq = (flat & 3) * 4;
-        const int gn = n0 + row, gk = k0 + kq;
-        rb[it] = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (gn < p.N) {
-          if constexpr (B_F16) {
-            const uint16_t* src = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)gn * p.ldb + gk;
-            if (gk + 4 <= kend) {
-              const uint2 u = *reinterpret_cast<const uint2*>(src);
-              rb[it] = floatx4{half_bits_to_float(u.x & 0xffff), half_bits_to_float(u.x >> 16),
-                               half_bits_to_float(u.y & 0xffff), half_bits_to_float(u.y >> 16)};
-            } else {
+      for (int t = 0; t < 8; ++t)
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (gk + e < kend) rb[it][e] = half_bits_to_float(src[e]);
-            }
-          } else {
-            const float* src = reinterpret_cast<const float*>(p.B) + (int64_t)gn * p.ldb + gk;
-            if (gk + 4 <= kend) {
-              rb[it] = *reinterpret_cast<const floatx4*>(src);
-            } else {
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (gk + e < kend) rb[it][e] = src[e];
-            }
-          }
-        }
-      } else {
-        // [K,N]: lanes walk n (coalesced rows of W); each thread gathers 4 k.
-        const int n = flat % BN, kq = (flat / BN) * 4;
-        const int gn = n0 + n;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int gk = k0 + kq + e;
-          float val = 0.f;
-          if (gn < p.N && gk < kend) {
-            if constexpr (B_F16)
-              val = half_bits_to_float(reinterpret_cast<const uint16_t*>(p.B)[(int64_t)gk * p.ldb + gn]);
-            else
-              val = reinterpret_cast<const float*>(p.B)[(int64_t)gk * p.ldb + gn];
-          }
-          rb[it][e] = val;
-        }
-      }
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[a][t >> 2][t & 3], fb[b][t], acc[a][b], 0, 0, 0);
     }
   };
-  auto store_panel = [&](int buf) {
+  // Iteration kt: put panel kt+2 in flight (its register set was emptied when
+  // panel kt was parked), multiply panel kt, then park panel kt+1 — whose
+  // loads have had two compute phases to land — in the other LDS stage.
+  // Loads and stores are unconditional (past the last panel the clamped,
+  // masked loads fetch nothing that is used), keeping the step one basic
+  // block; the scheduler is then told to put the fragment reads first and to
+  // thread the global loads and the LDS stores through the MFMA stream.
+  constexpr int N_DSR = (HK / 8) * (4 + (B_NK ? 4 : 16));
+  constexpr int N_MFMA = (HK / 8) * 32;
+  constexpr int N_VMEM = A_ITEMS + B_ITEMS;
+  auto step = [&](auto sc, int kt) {
+    constexpr int S = decltype(sc)::value;
+    using SN = std::integral_constant<int, 1 - S>;
+    load_panel(sc, kbeg + (kt + 2) * BK);
+    compute(sc);
+    store_panel(SN{});
+    __builtin_amdgcn_sched_group_barrier(0x100, N_DSR, 0);
 #pragma unroll
-    for (int it = 0; it < A_ITEMS; ++it) {
-      const int flat = tid + 256 * it;
-      const int row = flat >> 2, kq = (flat & 3) * 4;
-      *reinterpret_cast<floatx4*>(&As[buf][row * PITCH + kq]) = ra[it];
+    for (int i = 0; i < N_VMEM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
 #pragma unroll
-    for (int it = 0; it < B_ITEMS; ++it) {
-      const int flat = tid + 256 * it;
-      int row, kq;
-      if constexpr (B_NK) {
-        row = flat >> 2;
-        kq = (flat & 3) * 4;
-      } else {
-        row = flat % BN;
-        kq = (flat / BN) * 4;
-      }
-      *reinterpret_cast<floatx4*>(&Bs[buf][row * PITCH + kq]) = rb[it];
+    for (int i = 0; i < N_VMEM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
     }
-  };
-
-  if (nk > 0) {
-    load_panel(kbeg);
-    store_panel(0);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_panel(kbeg + (kt + 1) * BK);
-    floatx4 fa[TM][2], fb[TN][2];
-#pragma unroll
-    for (int a = 0; a < TM; ++a) {
-      const float* src = &As[buf][(wave_m * WM + a * 32 + li) * PITCH + 8 * lh];
-      fa[a][0] = *reinterpret_cast<const floatx4*>(src);
-      fa[a][1] = *reinterpret_cast<const floatx4*>(src + 4);
-    }
-#pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const float* src = &Bs[buf][(wave_n * WN + b * 32 + li) * PITCH + 8 * lh];
-      fb[b][0] = *reinterpret_cast<const floatx4*>(src);
-      fb[b][1] = *reinterpret_cast<const floatx4*>(src + 4);
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[a][t >> 2][t & 3],
-                                                           fb[b][t >> 2][t & 3],
-                                                           acc[a][b], 0, 0, 0);
-    if (kt + 1 < nk) store_panel(buf ^ 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA - 2 * N_VMEM, 0);
     __syncthreads();
+  };
+  if (nk > 0) load_panel(I0{}, kbeg);
+  if (nk > 1) load_panel(I1{}, kbeg + BK);
+  if (nk > 0) store_panel(I0{});
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(I0{}, kt);
+    if (kt + 1 < nk) step(I1{}, kt + 1);
+  }
+
+  const bool split_out = p.partial != nullptr;
+  // K-split: every wave parks its partial sub-tile in LDS (the ring is free
+  // after the final barrier), then all 256 threads sum the KW partials of
+  // each element in kw order (timing-independent) and run the epilogue with
+  // coalesced row stores.
+  if constexpr (KW > 1) {
+    float* red = smem;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[wave * 4096 + ((a * 2 + b) * 16 + e) * 64 + lane] = acc[a][b][e];
+    __syncthreads();
+#pragma unroll 4
+    for (int i = 0; i < BM * BN / 256; ++i) {
+      const int idx = tid + 256 * i;
+      const int row = idx / BN, col = idx % BN;
+      const int s2 = (col / 64) * NWM + row / 64;   // sub-tile
+      const int rr = row % 64, cc = col % 64;
+      const int a = rr / 32, r = rr % 32, b = cc / 32;
+      const int e = 4 * (r / 8) + (r % 4), lh2 = (r / 4) % 2;
+      const int slot = ((a * 2 + b) * 16 + e) * 64 + (cc % 32) + 32 * lh2;
+      float v = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < KW; ++w2) v += red[(s2 * KW + w2) * 4096 + slot];
+      const int m = m0 + row, n = n0 + col;
+      if (m < p.M && n < p.N) {
+        if (split_out)
+          p.partial[((int64_t)split * p.M + m) * p.N + n] = v;
+        else
+          p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, v, m, n, p.C, p.ldc);
+      }
+    }
+    return;
   }
 
   // Output: lane (li, lh) of a 32×32 tile holds column li, rows
   // 8*(e/4) + 4*lh + e%4 for e = 0..15.
-  const bool split_out = p.partial != nullptr;
 #pragma unroll
-  for (int a = 0; a < TM; ++a)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const int n = n0 + wave_n * WN + b * 32 + li;
+    for (int b = 0; b < 2; ++b) {
+      const int n = n0 + wn + b * 32 + li;
       if (n >= p.N) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wave_m * WM + a * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
+        const int m = m0 + wm + a * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
         if (m >= p.M) continue;
-        if (split_out) {
+        if (split_out)
           p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][e];
-        } else {
+        else
           p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, acc[a][b][e], m, n, p.C, p.ldc);
-        }
       }
     }
 }
 
-__global__ void splitk_reduce_kernel(const float* partial, int splits, int M,
-                                     int N, float* C, int64_t ldc,
-                                     GemmEpilogue ep) {
+__global__ void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M, int N,
+                                     float* C, int64_t ldc, GemmEpilogue ep) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)M * N;
   if (idx >= total) return;
@@ -253,7 +346,7 @@ __global__ void splitk_reduce_kernel(const float* partial, int splits, int M,
   C[(int64_t)m * ldc + n] = epilogue_value(ep, s, m, n, C, ldc);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, BN);
@@ -261,186 +354,102 @@ void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   dim3 grid(p.tiles_per_xcd * 8, splits), block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, true>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, true, false>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, true>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, false>), grid, block, 0, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, false, true>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, false, false>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, true>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, false>), grid, block, 0, s, p);
   }
   MFT_LAUNCH_CHECK();
 }
 
-// ---- skinny rank-r kernels --------------------------------------------------
-// out[m, j] = Σ_k X[m,k] · Y(k,j); one wave per row, lanes stride k.
-template <int R>
-__global__ __launch_bounds__(256) void rank_proj_kernel(const float* X, int64_t ldx,
-                                                         const float* Y, int64_t ysk,
-                                                         int64_t ysj, int M, int K,
-                                                         int r, float* out) {
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (m >= M) return;
-  float acc[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) acc[j] = 0.f;
-  const float* xr = X + (int64_t)m * ldx;
-  for (int k = lane; k < K; k += 64) {
-    const float xv = xr[k];
-    const float* yk = Y + (int64_t)k * ysk;
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-      if (j < r) acc[j] = fmaf(xv, yk[j * ysj], acc[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    float v = acc[j];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    acc[j] = v;
-  }
-  if (lane < r) {
-    float v = 0.f;
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-      if (j == lane) v = acc[j];
-    out[(int64_t)m * r + lane] = v;
-  }
-}
+struct Plan {
+  int bm, bn, splits;
+};
 
-// Partial sums of Σ_m P[m,j] X[m,c] over a row slice; 64 columns × 4 row
-// groups per workgroup.  Writes part[slice][j][c].
-template <int R>
-__global__ __launch_bounds__(256) void rank_outer_kernel(const float* P, const float* X,
-                                                          int64_t ldx, int M, int C, int r,
-                                                          int rows_per_slice, float* part) {
-  __shared__ float red[4][R][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int g = threadIdx.x >> 6;
-  const int slice = blockIdx.y;
-  const int mb = slice * rows_per_slice, me = min(M, mb + rows_per_slice);
-  float acc[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) acc[j] = 0.f;
-  if (c < C) {
-    for (int m = mb + g; m < me; m += 4) {
-      const float xv = X[(int64_t)m * ldx + c];
-      const float* pr = P + (int64_t)m * r;
-#pragma unroll
-      for (int j = 0; j < R; ++j)
-        if (j < r) acc[j] = fmaf(pr[j], xv, acc[j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < R; ++j) red[g][j][threadIdx.x & 63] = acc[j];
-  __syncthreads();
-  if (g == 0 && c < C) {
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      if (j >= r) break;
-      const float v = red[0][j][threadIdx.x] + red[1][j][threadIdx.x] +
-                      red[2][j][threadIdx.x] + red[3][j][threadIdx.x];
-      part[((int64_t)slice * r + j) * C + c] = v;
-    }
-  }
-}
+int plan_bk(int bm, int bn) { return (bm == 64 && bn == 64) ? 64 : 32; }
 
-__global__ void rank_outer_finish(const float* part, int slices, int C, int r,
-                                  float scale, float* out, int64_t osj,
-                                  int64_t osc, int accumulate) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)C * r) return;
-  const int j = (int)(idx / C), c = (int)(idx % C);
-  float s = 0.f;
-  for (int z = 0; z < slices; ++z) s += part[((int64_t)z * r + j) * C + c];
-  float* o = out + (int64_t)j * osj + (int64_t)c * osc;
-  *o = accumulate ? fmaf(scale, s, *o) : scale * s;
+// Tile shape and split-K, from sweeps of the benchmark shapes on MI355X:
+// 64×64 tiles (two resident workgroups per CU), with split-K doubled while
+// the grid has fewer than 512 workgroups (two per CU) and every split keeps
+// at least 512 of K; very large grids (the LM head over the vocabulary) use
+// 128×128 tiles, which halve the operand traffic per FLOP.
+Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
+  if (cdiv(M, 128) * cdiv(N, 128) >= 1024) return {128, 128, 1};
+  const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
+  int sp = 1;
+  while (tiles * sp < 512 && K / (2 * sp) >= 512 && sp < 8 &&
+         (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
+    sp *= 2;
+  return {64, 64, sp};
 }
 
 }  // namespace
 
-void gemm(hipStream_t s, const float* A, int64_t lda, const void* B,
-          int64_t ldb, bool b_nk, bool b_f16, float* C, int64_t ldc, int M,
-          int N, int K, const GemmEpilogue& ep, Scratch ws,
-          const KernelEvents* ev) {
-  float* workspace = ws.ptr;
-  const size_t workspace_bytes = ws.bytes;
+void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb, bool b_nk,
+          bool b_f16, float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep,
+          Scratch ws, const KernelEvents* ev) {
   MFT_CHECK_ARG(M > 0 && N > 0 && K > 0, "empty GEMM");
   MFT_CHECK_ARG(lda % 4 == 0 && lda >= K, "lda must be a multiple of 4 and >= K");
-  MFT_CHECK_ARG(!b_nk || (ldb % 4 == 0 && ldb >= K), "ldb must be a multiple of 4 and >= K for [N,K] B");
+  MFT_CHECK_ARG(!b_nk || ldb >= K, "ldb must be >= K for [N,K] B");
   MFT_CHECK_ARG(b_nk || ldb >= N, "ldb must be >= N for [K,N] B");
   MFT_CHECK_ARG(ldc >= N, "ldc must be >= N");
   MFT_CHECK_ARG(ep.r <= 32, "LoRA rank > 32 unsupported");
   MFT_CHECK_ARG(((uintptr_t)A & 15) == 0, "A must be 16-byte aligned");
-  MFT_CHECK_ARG(!b_nk || ((uintptr_t)B & (b_f16 ? 7 : 15)) == 0, "B misaligned");
   GemmParams p;
   p.A = A; p.B = B; p.C = C;
   p.lda = lda; p.ldb = ldb; p.ldc = ldc;
   p.M = M; p.N = N; p.K = K;
   p.ep = ep;
   p.partial = nullptr;
-
-  // Tile choice: the largest tile that still yields ≥ one workgroup per CU;
-  // otherwise 64×64 plus split-K until the grid covers the 256 CUs.
-  const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
-  const int64_t t64x128 = cdiv(M, 64) * cdiv(N, 128);
-  const int64_t t64 = cdiv(M, 64) * cdiv(N, 64);
-  int bm = 64, bn = 64, splits = 1;
-  if (t128 >= 256) { bm = 128; bn = 128; }
-  else if (t64x128 >= 256) { bm = 64; bn = 128; }
-  else {
-    const int64_t want = cdiv(256, t64);
-    const int64_t kmax = K / 128;  // keep ≥ 128 of K per split
-    splits = (int)std::max<int64_t>(1, std::min<int64_t>(want, kmax));
-    if (splits > 1 && (size_t)splits * M * N * sizeof(float) > workspace_bytes) splits = 1;
+  p.b_vec = (ldb % 4 == 0) && (((uintptr_t)B & (b_f16 ? 7 : 15)) == 0);
+  if (!p.b_vec) {
+    // The kernel reads B as aligned 4-vectors; repack an unaligned or
+    // odd-pitch B into the workspace with a padded pitch first.
+    const size_t esz = b_f16 ? 2 : 4;
+    const int64_t rows = b_nk ? N : K, cols = b_nk ? K : N;
+    const int64_t pitch = (cols + 3) / 4 * 4;
+    const size_t need = (size_t)rows * pitch * esz;
+    MFT_CHECK_ARG(ws.ptr && ws.bytes >= need + 256, "unaligned B needs a workspace for repacking");
+    char* dst = reinterpret_cast<char*>(ws.ptr);
+    MFT_HIP(hipMemcpy2DAsync(dst, pitch * esz, B, ldb * esz, cols * esz, rows, hipMemcpyDeviceToDevice, s));
+    p.B = dst;
+    p.ldb = pitch;
+    p.b_vec = 1;
+    const size_t used = (need + 255) / 256 * 256;
+    ws.ptr = reinterpret_cast<float*>(dst + used);
+    ws.bytes -= used;
   }
-  p.k_chunk = (int)(cdiv(cdiv(K, splits), BK) * BK);
+
+  Plan pl = plan_gemm(M, N, K, ws.ptr ? ws.bytes : 0);
+  // Tuning hook: MFT_GEMM_PLAN="bm,bn,splits" forces the launch shape
+  // (bm×bn ∈ {128×128, 64×128, 64×64}); same arithmetic, other tiling.
+  static const char* forced = getenv("MFT_GEMM_PLAN");
+  if (forced) {
+    int bm = 0, bn = 0, sp = 0;
+    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
+        ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
+        (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
+      pl = {bm, bn, sp};
+  }
+  const int bk = plan_bk(pl.bm, pl.bn);
+  int splits = pl.splits;
+  p.k_chunk = (int)(cdiv(cdiv(K, splits), bk) * bk);
   splits = (int)cdiv(K, p.k_chunk);
-  if (splits > 1) p.partial = workspace;
+  if (splits > 1) p.partial = ws.ptr;
 
   if (ev && ev->start) MFT_HIP(hipEventRecord(ev->start, s));
-  if (bm == 128) launch_tile<128, 128>(s, p, b_nk, b_f16, splits);
-  else if (bn == 128) launch_tile<64, 128>(s, p, b_nk, b_f16, splits);
-  else launch_tile<64, 64>(s, p, b_nk, b_f16, splits);
+  if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
+  else if (pl.bn == 128) launch_tile<64, 128, 32>(s, p, b_nk, b_f16, splits);
+  else launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
 
   if (splits > 1) {
     const int64_t total = (int64_t)M * N;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s,
-                       (const float*)workspace, splits, M, N, C, ldc, ep);
+                       (const float*)ws.ptr, splits, M, N, C, ldc, ep);
     MFT_LAUNCH_CHECK();
   }
-}
-
-void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y,
-               int64_t ysk, int64_t ysj, int M, int K, int r, float* out) {
-  MFT_CHECK_ARG(r >= 1 && r <= 32, "rank must be in [1,32]");
-  dim3 grid((unsigned)cdiv(M, 4)), block(256);
-  if (r <= 8)       hipLaunchKernelGGL(rank_proj_kernel<8>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
-  else if (r <= 16) hipLaunchKernelGGL(rank_proj_kernel<16>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
-  else              hipLaunchKernelGGL(rank_proj_kernel<32>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
-  MFT_LAUNCH_CHECK();
-}
-
-void rank_outer(hipStream_t s, const float* P, const float* X, int64_t ldx,
-                int M, int C, int r, float scale, float* out, int64_t osj,
-                int64_t osc, bool accumulate, Scratch ws) {
-  float* workspace = ws.ptr;
-  const size_t ws_bytes = ws.bytes;
-  MFT_CHECK_ARG(r >= 1 && r <= 32, "rank must be in [1,32]");
-  int slices = (int)std::min<int64_t>(cdiv(M, 64), 16);
-  while (slices > 1 && (size_t)slices * r * C * sizeof(float) > ws_bytes) slices /= 2;
-  if (!workspace) slices = 1;
-  MFT_CHECK_ARG(workspace && (size_t)slices * r * C * sizeof(float) <= ws_bytes,
-                "rank_outer needs a workspace of r*C floats");
-  const int rows = (int)cdiv(M, slices);
-  dim3 grid((unsigned)cdiv(C, 64), slices), block(256);
-  if (r <= 8)       hipLaunchKernelGGL(rank_outer_kernel<8>, grid, block, 0, s, P, X, ldx, M, C, r, rows, workspace);
-  else if (r <= 16) hipLaunchKernelGGL(rank_outer_kernel<16>, grid, block, 0, s, P, X, ldx, M, C, r, rows, workspace);
-  else              hipLaunchKernelGGL(rank_outer_kernel<32>, grid, block, 0, s, P, X, ldx, M, C, r, rows, workspace);
-  MFT_LAUNCH_CHECK();
-  hipLaunchKernelGGL(rank_outer_finish, dim3((unsigned)cdiv((int64_t)C * r, 256)), dim3(256), 0, s,
-                     (const float*)workspace, slices, C, r, scale, out, osj, osc, accumulate ? 1 : 0);
-  MFT_LAUNCH_CHECK();
 }
 
 }  // namespace mft

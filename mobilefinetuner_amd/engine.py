@@ -105,6 +105,21 @@ class Model:
     def opt_step(self, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0):
         call("mft_model_opt_step", self.h, lr, b1, b2, eps, wd, clip)
 
+    def train_step(self, ids, labels, mask=None, n_micro=1, seqs_per_micro=None, S=None,
+                   upstream=None, lr=2e-4, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0,
+                   graph=True):
+        """Whole optimizer step (fwd+CE+bwd over all micro-batches, clip, Adam);
+        graph=True replays a captured HIP graph after the first call."""
+        S = S or ids.shape[-1]
+        nseq = ids.numel() // S
+        seqs_per_micro = seqs_per_micro or nseq // n_micro
+        if upstream is None:
+            upstream = 1.0 / n_micro
+        call("mft_model_train_step", self.h, C.c_void_p(ids.data_ptr()),
+             C.c_void_p(mask.data_ptr()) if mask is not None else None,
+             C.c_void_p(labels.data_ptr()), n_micro, seqs_per_micro, S, upstream, lr, b1, b2, eps,
+             wd, clip, int(graph))
+
     def read_stats(self):
         loss = C.c_float()
         n = C.c_int64()

@@ -2,6 +2,7 @@
  * oracle_ops.c — CPU restatement of the hot-path operators.
  * TEST INFRASTRUCTURE ONLY (see oracle.h).
  */
+#define _GNU_SOURCE
 #include "oracle.h"
 
 #include <dlfcn.h>
@@ -30,6 +31,11 @@ static void try_load_blas(void) {
   if (tried) return;
   tried = 1;
   const char* force = getenv("ORC_BLAS_LIB");
+  /* This library's loops run on libgomp; MKL's default Intel-OpenMP layer
+   * next to an already-loaded libgomp (torch brings one) returns wrong
+   * products, so MKL is pinned to its GNU-OpenMP layer. */
+  setenv("MKL_THREADING_LAYER", "GNU", 0);
+  setenv("MKL_INTERFACE_LAYER", "LP64", 0);
   const char* mkl[] = {"libmkl_rt.so", "/opt/conda/lib/libmkl_rt.so",
                        "libmkl_rt.so.1", NULL};
   if (!force || strstr(force, "mkl")) {

@@ -190,3 +190,25 @@ def test_fp16_storage_model_equals_dequantised_fp32():
     assert la == lb
     n = "layers.1.mlp.down_proj.lora_A"
     assert np.array_equal(a.get(n, grad=True), b.get(n, grad=True))
+
+
+def test_blas_backed_oracle_equals_exact_loops():
+    """The CPU-baseline configuration (GEMMs in a dlopen'd CBLAS, threads on
+    libgomp) computes the same step as the fp64-accumulating loops, also with
+    torch (and its OpenMP runtime) already loaded in the process."""
+    import sys
+    assert "torch" in sys.modules
+    mc = gpt2(2, 256, 4, vocab=5003, max_pos=64, name="gpt2-blas")
+    res = []
+    for blas in (0, 1):
+        O.lib().orc_set_blas(blas)
+        om = O.OracleModel(mc)
+        init_values(om, seed=21)
+        ids = np.random.default_rng(2).integers(0, mc.vocab, (2, 64)).astype(np.int32)
+        loss = om.fwd_bwd(ids, None, ids, 2, 64, 1.0)
+        res.append((loss, om.get("h.0.attn.c_attn.lora_A", grad=True)))
+    O.lib().orc_set_blas(0)
+    if O.lib().orc_blas_backend() is None:
+        pytest.skip("no CBLAS available")
+    assert abs(res[0][0] - res[1][0]) < 1e-5 * res[0][0]
+    assert rel_err(res[1][1], res[0][1]) < 1e-4
