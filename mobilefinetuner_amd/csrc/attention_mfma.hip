@@ -16,9 +16,11 @@
 // (pitch hd+4: conflict-free 128-bit and 32-bit reads).
 //
 // Backward: delta = rowsum(dO∘O) (one pass), then
-//   dK/dV kernel — per wave 16 keys; S and dP formed with keys as columns so
-//     Pᵀ and dSᵀ feed dV += Pᵀ·dO and dK += dSᵀ·Q from registers; loops over
-//     every query head of the GQA group (no repeat_kv copy, no atomics);
+//   dK/dV kernel — per wave 16 keys of one QUERY head; S and dP formed with
+//     keys as columns so Pᵀ and dSᵀ feed dV += Pᵀ·dO and dK += dSᵀ·Q from
+//     registers.  With GQA groups > 1 each query head writes a partial and a
+//     small pass sums the group in head order (no repeat_kv copy, no atomics,
+//     deterministic);
 //   dQ kernel — per wave 16 queries; Sᵀ, dPᵀ transposed as in the forward so
 //     dS feeds dQ += dS·K from registers.
 // P is recomputed from the saved lse in both backward kernels.
@@ -33,6 +35,7 @@ struct AttnP {
   const float *q, *k, *v, *o, *dout, *lse, *delta;
   int64_t q_rs, k_rs, v_rs, o_rs, do_rs;
   float *out, *lse_out, *dq, *dk, *dv, *delta_out;
+  float *pdk, *pdv;  // per-query-head dK/dV partials [B,S,Hq,hd] (GQA groups > 1)
   int64_t out_rs, dq_rs, dk_rs, dv_rs;
   int B, Hq, Hkv, S;
   float scale;
@@ -241,8 +244,12 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int kh = blockIdx.y, b = blockIdx.z;
+  // One workgroup per (key block, QUERY head): a GQA group's query heads
+  // run in parallel and their dK/dV contributions are summed afterwards by
+  // attn_group_sum_kernel in head order.
+  const int h = blockIdx.y, b = blockIdx.z;
   const int grp = p.Hq / p.Hkv;
+  const int kh = h / grp;
   const int k0 = blockIdx.x * BKEYS;
   const int kbase = k0 + 16 * w;
   const int kj = kbase + li;  // this lane's key (as S column)
@@ -260,8 +267,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   const int klast = min(k0 + BKEYS - 1, p.S - 1);
   const int qstart = p.causal ? k0 : 0;
   const int qend = p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1;
-  for (int hh = 0; hh < grp; ++hh) {
-    const int h = kh * grp + hh;
+  {
     for (int qb0 = (qstart / BQ) * BQ; qb0 <= qend; qb0 += BQ) {
       __syncthreads();
       stage_rows<HD, NT>(Qs, p.q, p.q_rs, b, p.S, h, qb0, BQ, tid);
@@ -320,17 +326,47 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
       }
     }
   }
-  // lane holds [key = kbase + 4lg + v][d = 16c + li]
+  // lane holds [key = kbase + 4lg + v][d = 16c + li]; a group of one query
+  // head writes dK/dV directly, larger groups write per-head partials.
+  const bool direct = grp == 1;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int gk = kbase + 4 * lg + v;
     if (gk >= p.S) continue;
-    float* dkr = p.dk + ((int64_t)b * p.S + gk) * p.dk_rs + (int64_t)kh * HD;
-    float* dvr = p.dv + ((int64_t)b * p.S + gk) * p.dv_rs + (int64_t)kh * HD;
+    const int64_t tok = (int64_t)b * p.S + gk;
+    float* dkr = direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + (tok * p.Hq + h) * HD;
+    float* dvr = direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       dkr[16 * c + li] = dkacc[c][v];
       dvr[16 * c + li] = dvacc[c][v];
+    }
+  }
+}
+
+// dK/dV[b,s,kh,:] = Σ_{j<grp} partial[b,s,kh·grp+j,:], in j order.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_group_sum_kernel(AttnP p) {
+  const int grp = p.Hq / p.Hkv;
+  const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c4 = (int)(i % (HD / 4));
+    const int64_t r = i / (HD / 4);
+    const int kh = (int)(r % p.Hkv);
+    const int64_t tok = r / p.Hkv;
+    floatx4 sk = floatx4{0.f, 0.f, 0.f, 0.f}, sv = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < grp; ++j) {
+      const int64_t off = (tok * p.Hq + kh * grp + j) * HD + 4 * c4;
+      sk += *reinterpret_cast<const floatx4*>(p.pdk + off);
+      sv += *reinterpret_cast<const floatx4*>(p.pdv + off);
+    }
+    float* dk = p.dk + tok * p.dk_rs + (int64_t)kh * HD + 4 * c4;
+    float* dv = p.dv + tok * p.dv_rs + (int64_t)kh * HD + 4 * c4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dk[e] = sk[e];
+      dv[e] = sv[e];
     }
   }
 }
@@ -459,24 +495,48 @@ void fwd_launch(hipStream_t s, AttnP& p) {
 }
 
 template <int HD, int NW>
-void bwd_launch(hipStream_t s, AttnP& p) {
+void dkdv_launch(hipStream_t s, AttnP& p) {
   constexpr int P = HD + 4;
-  {
-    constexpr int BQ = Cfg<HD>::BQ;
-    const size_t lds = sizeof(float) * (2 * 16 * NW * P + 2 * BQ * P + 2 * BQ + 16 * NW);
-    auto kern = attn_bwd_dkdv_mfma<HD, NW, BQ>;
-    set_lds(kern, lds);
-    dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hkv, p.B);
-    hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
-    MFT_LAUNCH_CHECK();
+  constexpr int BQ = Cfg<HD>::BQ;
+  const size_t lds = sizeof(float) * (2 * 16 * NW * P + 2 * BQ * P + 2 * BQ + 16 * NW);
+  auto kern = attn_bwd_dkdv_mfma<HD, NW, BQ>;
+  set_lds(kern, lds);
+  dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  MFT_LAUNCH_CHECK();
+}
+
+template <int HD, int NW>
+void dq_launch(hipStream_t s, AttnP& p) {
+  constexpr int P = HD + 4;
+  constexpr int BKV = Cfg<HD>::DQBKV;
+  const size_t lds = sizeof(float) * (2 * BKV * P + BKV);
+  auto kern = attn_bwd_dq_mfma<HD, NW, BKV>;
+  set_lds(kern, lds);
+  dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  MFT_LAUNCH_CHECK();
+}
+
+// Waves per workgroup (16 queries or keys each): the widest that still gives
+// at least two workgroups per CU over the (S-blocks × Hq × B) grid.
+int pick_nw(const AttnArgs& a) {
+  for (int nw : {4, 2}) {
+    if (a.hd == 256 && nw == 4) continue;  // LDS budget at head_dim 256
+    if (cdiv(a.S, 16 * nw) * a.Hq * a.B >= 512) return nw;
   }
-  {
-    constexpr int BKV = Cfg<HD>::DQBKV;
-    const size_t lds = sizeof(float) * (2 * BKV * P + BKV);
-    auto kern = attn_bwd_dq_mfma<HD, NW, BKV>;
-    set_lds(kern, lds);
-    dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
-    hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  return 1;
+}
+
+template <int HD>
+void bwd_launch(hipStream_t s, AttnP& p, int nw) {
+  if (nw == 4) { dkdv_launch<HD, 4>(s, p); dq_launch<HD, 4>(s, p); }
+  else if (nw == 2) { dkdv_launch<HD, 2>(s, p); dq_launch<HD, 2>(s, p); }
+  else { dkdv_launch<HD, 1>(s, p); dq_launch<HD, 1>(s, p); }
+  if (p.Hq != p.Hkv) {
+    const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
+    hipLaunchKernelGGL(attn_group_sum_kernel<HD>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
+                       dim3(256), 0, s, p);
     MFT_LAUNCH_CHECK();
   }
 }
@@ -499,9 +559,6 @@ AttnP make(const AttnArgs& a) {
   return p;
 }
 
-// 4 waves per workgroup when that still gives ≥ 2 workgroups per CU, else 2.
-bool wide(const AttnArgs& a) { return cdiv(a.S, 64) * a.Hq * a.B >= 512; }
-
 }  // namespace
 
 void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* lse) {
@@ -511,19 +568,24 @@ void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* l
   p.out = o;
   p.out_rs = o_rs;
   p.lse_out = lse;
-  const bool w4 = wide(a);
-  switch (a.hd) {
-    case 64: w4 ? fwd_launch<64, 4>(s, p) : fwd_launch<64, 2>(s, p); break;
-    case 128: w4 ? fwd_launch<128, 4>(s, p) : fwd_launch<128, 2>(s, p); break;
-    default: fwd_launch<256, 2>(s, p); break;
+  switch (pick_nw(a)) {
+    case 4: a.hd == 64 ? fwd_launch<64, 4>(s, p) : fwd_launch<128, 4>(s, p); break;
+    case 2:
+      a.hd == 64 ? fwd_launch<64, 2>(s, p) : a.hd == 128 ? fwd_launch<128, 2>(s, p) : fwd_launch<256, 2>(s, p);
+      break;
+    default:
+      a.hd == 64 ? fwd_launch<64, 1>(s, p) : a.hd == 128 ? fwd_launch<128, 1>(s, p) : fwd_launch<256, 1>(s, p);
+      break;
   }
 }
 
 void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, const float* dout,
               int64_t do_rs, const float* lse, float* dq, int64_t dq_rs, float* dk, int64_t dk_rs,
-              float* dv, int64_t dv_rs, float* delta_scratch) {
+              float* dv, int64_t dv_rs, Scratch ws) {
   AttnP p = make(a);
-  MFT_CHECK_ARG(o && dout && lse && dq && dk && dv && delta_scratch, "null tensor");
+  MFT_CHECK_ARG(o && dout && lse && dq && dk && dv, "null tensor");
+  MFT_CHECK_ARG(ws.ptr && ws.bytes >= attn_bwd_scratch_floats(a) * sizeof(float),
+                "attention backward scratch too small");
   MFT_CHECK_ARG(do_rs % 4 == 0 && ((uintptr_t)dout & 15) == 0, "dout must be 16-byte aligned rows");
   p.o = o; p.o_rs = o_rs;
   p.dout = dout; p.do_rs = do_rs;
@@ -531,21 +593,34 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
   p.dq = dq; p.dq_rs = dq_rs;
   p.dk = dk; p.dk_rs = dk_rs;
   p.dv = dv; p.dv_rs = dv_rs;
-  p.delta_out = delta_scratch;
-  p.delta = delta_scratch;
   const int64_t rows = (int64_t)a.B * a.S * a.Hq;
+  p.delta_out = ws.ptr;
+  p.delta = ws.ptr;
+  if (a.Hq != a.Hkv) {
+    // partial rows padded to a 16-byte boundary after delta
+    float* part = ws.ptr + (rows + 3) / 4 * 4;
+    p.pdk = part;
+    p.pdv = part + rows * a.hd;
+  }
   switch (a.hd) {
     case 64: hipLaunchKernelGGL(attn_delta_mfma_kernel<64>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
     case 128: hipLaunchKernelGGL(attn_delta_mfma_kernel<128>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
     default: hipLaunchKernelGGL(attn_delta_mfma_kernel<256>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
   }
   MFT_LAUNCH_CHECK();
-  const bool w4 = wide(a);
+  const int nw = pick_nw(a);
   switch (a.hd) {
-    case 64: w4 ? bwd_launch<64, 4>(s, p) : bwd_launch<64, 2>(s, p); break;
-    case 128: w4 ? bwd_launch<128, 4>(s, p) : bwd_launch<128, 2>(s, p); break;
-    default: bwd_launch<256, 2>(s, p); break;
+    case 64: bwd_launch<64>(s, p, nw); break;
+    case 128: bwd_launch<128>(s, p, nw); break;
+    default: bwd_launch<256>(s, p, nw); break;
   }
+}
+
+size_t attn_bwd_scratch_floats(const AttnArgs& a) {
+  const size_t rows = (size_t)a.B * a.S * a.Hq;
+  size_t n = (rows + 3) / 4 * 4;
+  if (a.Hq != a.Hkv) n += 2 * rows * (size_t)a.hd;
+  return n;
 }
 
 }  // namespace mft

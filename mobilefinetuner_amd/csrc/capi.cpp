@@ -204,9 +204,9 @@ int mft_attn_bwd(mft_handle h, const float* q, int64_t q_rs, const float* k,
   return guarded([&] {
     require_handle(h);
     mft::AttnArgs a{q, k, v, q_rs, k_rs, v_rs, B, Hq, Hkv, S, hd, scale, causal, window, kpad};
-    const size_t ws = (size_t)B * Hq * S * sizeof(float);
-    float* delta = reinterpret_cast<float*>(scratch(h, ws));
-    mft::attn_bwd(h->stream, a, o, o_rs, dout, do_rs, lse, dq, dq_rs, dk, dk_rs, dv, dv_rs, delta);
+    const size_t ws = mft::attn_bwd_scratch_floats(a) * sizeof(float);
+    mft::Scratch s{reinterpret_cast<float*>(scratch(h, ws)), ws};
+    mft::attn_bwd(h->stream, a, o, o_rs, dout, do_rs, lse, dq, dq_rs, dk, dk_rs, dv, dv_rs, s);
   });
 }
 

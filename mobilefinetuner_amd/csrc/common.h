@@ -115,7 +115,10 @@ void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs,
 void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs,
               const float* dout, int64_t do_rs, const float* lse, float* dq,
               int64_t dq_rs, float* dk, int64_t dk_rs, float* dv,
-              int64_t dv_rs, float* delta_scratch);
+              int64_t dv_rs, Scratch ws);
+// Scratch floats attn_bwd needs: delta rows, plus per-query-head dK/dV
+// partials when heads are grouped (Hq != Hkv).
+size_t attn_bwd_scratch_floats(const AttnArgs& a);
 
 // logits rows have stride ld (>= V); dlogits (may alias logits) uses the same.
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
@@ -135,6 +138,8 @@ void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_
                    const float* hp, const int* tstep, const float* clip_scale, bool zero_grad);
 void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,
                     int* tstep);
+void set_hparams(hipStream_t s, float* hp, float lr, float b1, float b2, float eps, float wd,
+                 float max_norm);
 void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n);
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out);
 void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,

@@ -302,6 +302,15 @@ __global__ void adam_dev_kernel(float* __restrict__ p, float* __restrict__ g,
   }
 }
 
+// hp = {lr, b1, b2, eps, wd, max_norm}, written by a kernel that takes the
+// values as arguments (no host staging buffer for the captured graph to read).
+__global__ void set_hparams_kernel(float* hp, float lr, float b1, float b2, float eps, float wd,
+                                   float max_norm) {
+  if (threadIdx.x == 0) {
+    hp[0] = lr; hp[1] = b1; hp[2] = b2; hp[3] = eps; hp[4] = wd; hp[5] = max_norm;
+  }
+}
+
 // Clip factor from Σg² with max_norm = hp[5]; advances the step counter.
 __global__ void clip_dev_kernel(const double* ss, const float* hp, float* scale, float* norm,
                                 int* tstep) {
@@ -498,6 +507,11 @@ void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_
   if (n <= 0) return;
   hipLaunchKernelGGL(adam_dev_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, hp,
                      tstep, clip_scale, zero_grad ? 1 : 0);
+  MFT_LAUNCH_CHECK();
+}
+void set_hparams(hipStream_t s, float* hp, float lr, float b1, float b2, float eps, float wd,
+                 float max_norm) {
+  hipLaunchKernelGGL(set_hparams_kernel, dim3(1), dim3(64), 0, s, hp, lr, b1, b2, eps, wd, max_norm);
   MFT_LAUNCH_CHECK();
 }
 void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,

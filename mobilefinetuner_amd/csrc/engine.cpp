@@ -13,6 +13,7 @@
 //   * logits [tokens, V] — dlogits overwrite them in place.
 // The step never returns to the host: CE normalisation, grad-norm, clip
 // factor and Adam all read device scalars.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -105,7 +106,7 @@ struct mft_model_s {
   int64_t ldv = 0;  // logits row stride: vocab rounded up to 4 (zeroed padding)
   float *dh = nullptr, *dtmp = nullptr, *dn = nullptr, *datt = nullptr;
   float *dq = nullptr, *dk = nullptr, *dv = nullptr, *dqkv = nullptr;
-  float *dact = nullptr, *dgate = nullptr, *dup = nullptr, *delta = nullptr;
+  float *dact = nullptr, *dgate = nullptr, *dup = nullptr;
   float *dtq = nullptr, *dtk = nullptr;
   float* row_nll = nullptr;
   Scratch ws;
@@ -117,8 +118,6 @@ struct mft_model_s {
   float* d_clip = nullptr;  // [0] scale, [1] norm
   float* d_hp = nullptr;    // {lr, b1, b2, eps, wd, max_norm}
   int* d_t = nullptr;       // Adam step count (advanced on the device)
-  float* h_hp_ring = nullptr;  // pinned staging ring for d_hp uploads
-  int hp_slot = 0;
   int n_micro_pending = 0;
   int adam_t = 0;
   // captured train-step graph
@@ -341,7 +340,6 @@ void alloc_acts(mft_model_s* m) {
     m->dact = b.f(M * ff);
     m->dgate = b.f(M * ff);
     m->dup = b.f(M * ff);
-    m->delta = b.f(M * H);
     m->row_nll = b.f(M);
     const int64_t wide = std::max<int64_t>({d, ff, H * hd, 3 * d});
     const int64_t wsf = M * std::max<int64_t>(r, 1) + 16 * std::max<int64_t>(r, 1) * wide + 8 * M * wide;
@@ -372,7 +370,6 @@ void alloc_acts(mft_model_s* m) {
   m->d_clip = reinterpret_cast<float*>(static_cast<char*>(sc) + 1536);
   m->d_hp = reinterpret_cast<float*>(static_cast<char*>(sc) + 1792);
   m->d_t = reinterpret_cast<int*>(static_cast<char*>(sc) + 2048);
-  MFT_HIP(hipHostMalloc(reinterpret_cast<void**>(&m->h_hp_ring), 256 * 8 * sizeof(float)));
   MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
@@ -652,7 +649,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
         Timed t(m, CLS_ATTN, awork);
         t.begin();
         attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dqkv, 3 * d, m->dqkv + d,
-                 3 * d, m->dqkv + 2 * d, 3 * d, m->delta);
+                 3 * d, m->dqkv + 2 * d, 3 * d, m->ws);
         t.end();
       }
       lin_bwd(m, L.lin[G_ATTN], m->dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
@@ -664,7 +661,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       Timed t(m, CLS_ATTN, awork);
       t.begin();
       attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dq, (int64_t)H * hd, m->dk,
-               (int64_t)Hk * hd, m->dv, (int64_t)Hk * hd, m->delta);
+               (int64_t)Hk * hd, m->dv, (int64_t)Hk * hd, m->ws);
       t.end();
     }
     const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
@@ -689,12 +686,11 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   }
 }
 
-// Host → device hyper-parameters through a ring of pinned slots (a slot is
-// not rewritten before 255 later steps have been enqueued).
+// Hyper-parameters reach the device as kernel arguments of a one-block
+// kernel launched ahead of the optimizer (or of the captured step graph), so
+// no host buffer is read by the device.
 void upload_hparams(mft_model_s* m, float lr, float b1, float b2, float eps, float wd, float clip) {
-  float* slot = m->h_hp_ring + 8 * (m->hp_slot++ % 256);
-  slot[0] = lr; slot[1] = b1; slot[2] = b2; slot[3] = eps; slot[4] = wd; slot[5] = clip;
-  MFT_HIP(hipMemcpyAsync(m->d_hp, slot, 6 * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  set_hparams(m->stream, m->d_hp, lr, b1, b2, eps, wd, clip);
 }
 
 // clip_and_get_grad_norm + Adam::step + zero_grad on the flat LoRA arrays;
@@ -831,7 +827,6 @@ int mft_model_destroy(mft_model m) {
     if (m->cap_stream) (void)hipStreamDestroy(m->cap_stream);
     if (m->ev_in) (void)hipEventDestroy(m->ev_in);
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
-    if (m->h_hp_ring) (void)hipHostFree(m->h_hp_ring);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
     void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss};
     for (void* b : bufs)

@@ -11,6 +11,15 @@ from ._lib import call, lib
 from .configs import ModelConfig
 
 
+def _dev(t, dt, what):
+    """Device pointer of a contiguous tensor of dtype `dt` (None passes)."""
+    if t is None:
+        return None
+    if not t.is_cuda or not t.is_contiguous() or t.dtype != dt:
+        raise TypeError(f"{what}: contiguous {dt} device tensor required, got {t.dtype}")
+    return C.c_void_p(t.data_ptr())
+
+
 class Model:
     def __init__(self, cfg: ModelConfig, max_tokens: int, stream=None):
         self.cfg = cfg
@@ -90,17 +99,16 @@ class Model:
         seqs_per_micro = seqs_per_micro or nseq // n_micro
         if upstream is None:
             upstream = 1.0 / n_micro
-        call("mft_model_fwd_bwd", self.h, C.c_void_p(ids.data_ptr()),
-             C.c_void_p(mask.data_ptr()) if mask is not None else None,
-             C.c_void_p(labels.data_ptr()), n_micro, seqs_per_micro, S, upstream)
+        call("mft_model_fwd_bwd", self.h, _dev(ids, torch.int32, "ids"),
+             _dev(mask, torch.float32, "mask"), _dev(labels, torch.int32, "labels"), n_micro,
+             seqs_per_micro, S, upstream)
 
     def forward(self, ids, labels=None, mask=None, logits=None, n_micro=1, S=None):
         S = S or ids.shape[-1]
         nseq = ids.numel() // S
-        call("mft_model_forward", self.h, C.c_void_p(ids.data_ptr()),
-             C.c_void_p(mask.data_ptr()) if mask is not None else None,
-             C.c_void_p(labels.data_ptr()) if labels is not None else None, n_micro,
-             nseq // n_micro, S, C.c_void_p(logits.data_ptr()) if logits is not None else None)
+        call("mft_model_forward", self.h, _dev(ids, torch.int32, "ids"),
+             _dev(mask, torch.float32, "mask"), _dev(labels, torch.int32, "labels"), n_micro,
+             nseq // n_micro, S, _dev(logits, torch.float32, "logits"))
 
     def opt_step(self, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0):
         call("mft_model_opt_step", self.h, lr, b1, b2, eps, wd, clip)
@@ -115,10 +123,9 @@ class Model:
         seqs_per_micro = seqs_per_micro or nseq // n_micro
         if upstream is None:
             upstream = 1.0 / n_micro
-        call("mft_model_train_step", self.h, C.c_void_p(ids.data_ptr()),
-             C.c_void_p(mask.data_ptr()) if mask is not None else None,
-             C.c_void_p(labels.data_ptr()), n_micro, seqs_per_micro, S, upstream, lr, b1, b2, eps,
-             wd, clip, int(graph))
+        call("mft_model_train_step", self.h, _dev(ids, torch.int32, "ids"),
+             _dev(mask, torch.float32, "mask"), _dev(labels, torch.int32, "labels"), n_micro,
+             seqs_per_micro, S, upstream, lr, b1, b2, eps, wd, clip, int(graph))
 
     def read_stats(self):
         loss = C.c_float()

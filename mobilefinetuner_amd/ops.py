@@ -31,14 +31,23 @@ def handle():
     return h
 
 
-def _p(t):
+def _p(t, dt=torch.float32):
+    """Device pointer of a contiguous tensor whose dtype is `dt` (a dtype or a
+    tuple of accepted dtypes): the C-ABI takes raw pointers, so the element
+    type is checked here."""
     if t is None:
         return None
     if not t.is_cuda:
         raise ValueError("device tensor required")
     if not t.is_contiguous():
         raise ValueError("contiguous tensor required")
+    if t.dtype not in (dt if isinstance(dt, tuple) else (dt,)):
+        raise TypeError(f"tensor of dtype {dt} required, got {t.dtype}")
     return C.c_void_p(t.data_ptr())
+
+
+_W = (torch.float32, torch.float16)
+_U16 = (torch.int16, torch.uint16) if hasattr(torch, "uint16") else (torch.int16,)
 
 
 def _wdtype(W):
@@ -56,7 +65,7 @@ def lora_linear_fwd(x, W, bias, A, B, scale, resid=None):
     r = A.shape[0] if A is not None else 0
     y = torch.empty(M, N, device=x.device, dtype=torch.float32)
     xa = torch.empty(M, max(r, 1), device=x.device, dtype=torch.float32) if r else None
-    call("mft_lora_linear_fwd", handle(), _p(x), M, K, _p(W), _wdtype(W), N, _p(bias), _p(A),
+    call("mft_lora_linear_fwd", handle(), _p(x), M, K, _p(W, _W), _wdtype(W), N, _p(bias), _p(A),
          _p(B), r, scale, _p(y), _p(xa), _p(resid))
     return y, xa
 
@@ -72,10 +81,16 @@ def lora_linear_bwd(dy, x, W, A, B, xa, scale, dA=None, dB=None, need_dx=True, a
         dA = torch.zeros_like(A)
     if r and dB is None:
         dB = torch.zeros_like(B)
-    call("mft_lora_linear_bwd", handle(), _p(dy), _p(x), _p(W), _wdtype(W), _p(A), _p(B), _p(xa),
+    call("mft_lora_linear_bwd", handle(), _p(dy), _p(x), _p(W, _W), _wdtype(W), _p(A), _p(B), _p(xa),
          M, K, N, r, scale, _p(dx) if need_dx else None, _p(dA), _p(dB), int(accumulate),
          int(dx_accumulate))
     return dx, dA, dB
+
+
+def _check_f32(*ts):
+    for t in ts:
+        if not t.is_cuda or t.dtype != torch.float32:
+            raise TypeError("float32 device tensors required")
 
 
 def _rs(t, H, hd):
@@ -90,6 +105,7 @@ def attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, causal=True, window=0, kpad=None
     v_rs = v_rs or Hkv * hd
     o = torch.empty(B * S, Hq * hd, device=q.device, dtype=torch.float32)
     lse = torch.empty(B, Hq, S, device=q.device, dtype=torch.float32)
+    _check_f32(q, k, v)
     call("mft_attn_fwd", handle(), C.c_void_p(q.data_ptr()), q_rs, C.c_void_p(k.data_ptr()), k_rs,
          C.c_void_p(v.data_ptr()), v_rs, B, Hq, Hkv, S, hd, scale, int(causal), window, _p(kpad),
          _p(o), Hq * hd, _p(lse))
@@ -104,6 +120,7 @@ def attn_bwd(q, k, v, o, dout, lse, B, Hq, Hkv, S, hd, scale, causal=True, windo
     dq = torch.empty(B * S, Hq * hd, device=q.device, dtype=torch.float32)
     dk = torch.empty(B * S, Hkv * hd, device=q.device, dtype=torch.float32)
     dv = torch.empty(B * S, Hkv * hd, device=q.device, dtype=torch.float32)
+    _check_f32(q, k, v)
     call("mft_attn_bwd", handle(), C.c_void_p(q.data_ptr()), q_rs, C.c_void_p(k.data_ptr()), k_rs,
          C.c_void_p(v.data_ptr()), v_rs, _p(o), Hq * hd, _p(dout), Hq * hd, _p(lse), B, Hq, Hkv, S,
          hd, scale, int(causal), window, _p(kpad), _p(dq), Hq * hd, _p(dk), Hkv * hd, _p(dv),
@@ -121,20 +138,20 @@ def ce_fwd_bwd(logits, labels, B, S, ignore_index=-100, upstream=1.0, norm_count
     dl = None
     if want_grad:
         dl = logits if in_place else torch.empty_like(logits)
-    call("mft_ce_fwd_bwd", handle(), _p(logits), _p(labels), B, S, V, ignore_index, upstream,
-         norm_count, _p(loss), _p(cnt), _p(dl), _p(nll))
+    call("mft_ce_fwd_bwd", handle(), _p(logits), _p(labels, torch.int32), B, S, V, ignore_index,
+         upstream, norm_count, _p(loss, torch.float64), _p(cnt, torch.int64), _p(dl), _p(nll))
     return loss, cnt, dl, nll
 
 
 def dequant_f16(src_u16):
     dst = torch.empty(src_u16.shape, device=src_u16.device, dtype=torch.float32)
-    call("mft_dequant_f16", handle(), _p(src_u16), _p(dst), src_u16.numel())
+    call("mft_dequant_f16", handle(), _p(src_u16, _U16 + (torch.float16,)), _p(dst), src_u16.numel())
     return dst
 
 
 def quant_f16(src):
     dst = torch.empty(src.shape, device=src.device, dtype=torch.int16)
-    call("mft_quant_f16", handle(), _p(src), _p(dst), src.numel())
+    call("mft_quant_f16", handle(), _p(src), _p(dst, torch.int16), src.numel())
     return dst
 
 
@@ -146,13 +163,13 @@ def adam_step(p, g, m, v, lr, b1, b2, eps, wd, t, clip_scale=None, zero_grad=Fal
 def sumsq(g, out=None):
     if out is None:
         out = torch.zeros(1, device=g.device, dtype=torch.float64)
-    call("mft_sumsq", handle(), _p(g), g.numel(), _p(out))
+    call("mft_sumsq", handle(), _p(g), g.numel(), _p(out, torch.float64))
     return out
 
 
 def clip_scale(ss, max_norm):
     out = torch.empty(2, device=ss.device, dtype=torch.float32)
-    call("mft_clip_scale", handle(), _p(ss), max_norm, C.c_void_p(out.data_ptr()),
+    call("mft_clip_scale", handle(), _p(ss, torch.float64), max_norm, C.c_void_p(out.data_ptr()),
          C.c_void_p(out.data_ptr() + 4))
     return out
 
@@ -160,8 +177,8 @@ def clip_scale(ss, max_norm):
 def layernorm_fwd(x, g, b, eps):
     M, Cc = x.shape
     y = torch.empty_like(x)
-    mean = torch.empty(M, device=x.device)
-    rstd = torch.empty(M, device=x.device)
+    mean = torch.empty(M, device=x.device, dtype=torch.float32)
+    rstd = torch.empty(M, device=x.device, dtype=torch.float32)
     call("mft_layernorm_fwd", handle(), _p(x), _p(g), _p(b), M, Cc, eps, _p(y), _p(mean), _p(rstd))
     return y, mean, rstd
 
@@ -178,7 +195,7 @@ def layernorm_bwd(dy, x, g, mean, rstd, dx=None, accumulate=False):
 def rmsnorm_fwd(x, w, eps, unit_offset):
     M, Cc = x.shape
     y = torch.empty_like(x)
-    rstd = torch.empty(M, device=x.device)
+    rstd = torch.empty(M, device=x.device, dtype=torch.float32)
     call("mft_rmsnorm_fwd", handle(), _p(x), _p(w), M, Cc, eps, int(unit_offset), _p(y), _p(rstd))
     return y, rstd
 
@@ -210,11 +227,12 @@ def rope_(x, B, S, H, hd, theta, inverse=False, rs=None):
     return x
 
 
-def embed(ids, S, wte, wpe, scale):
+def embed(ids, S, wte, wpe, scale, out=None):
     M = ids.numel()
     Cc = wte.shape[1]
-    out = torch.empty(M, Cc, device=ids.device)
-    call("mft_embed", handle(), _p(ids), M, S, _p(wte), F16 if wte.dtype == torch.float16 else F32,
+    if out is None:
+        out = torch.empty(M, Cc, device=ids.device, dtype=torch.float32)
+    call("mft_embed", handle(), _p(ids, torch.int32), M, S, _p(wte, _W), _wdtype(wte),
          _p(wpe), Cc, scale, _p(out))
     return out
 

@@ -26,3 +26,18 @@ def rel_err(a, b):
 @pytest.fixture
 def rel():
     return rel_err
+
+
+@pytest.fixture(autouse=True)
+def _torch_default_dtype_untouched():
+    """Process-wide torch state set by one test module would leak into every
+    module collected after it (a float64 default dtype once turned dtype-less
+    allocations float64): fail the test that changes it."""
+    torch = sys.modules.get("torch")
+    before = torch.get_default_dtype() if torch is not None else None
+    yield
+    torch = sys.modules.get("torch")
+    if torch is not None and before is not None:
+        assert torch.get_default_dtype() == before, "test changed torch's default dtype"
+    if torch is not None:
+        assert torch.get_default_dtype() == torch.float32, "torch default dtype is not float32"

@@ -65,3 +65,34 @@ def test_bad_model_config_rejected_without_gpu():
     rc = L.mft_model_create(C.byref(h), C.byref(cfg), 128, None)
     assert rc == 1
     assert b"n_head*head_dim" in L.mft_last_error()
+
+
+class _FakeDev:
+    """Stands in for a contiguous device tensor (no GPU in this process)."""
+
+    def __init__(self, dtype):
+        import torch
+        self.dtype = dtype
+        self.is_cuda = True
+        self._torch = torch
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):
+        return 4096
+
+
+def test_ops_pointer_helper_checks_dtype():
+    """The C-ABI takes raw pointers, so the Python wrappers check element types:
+    a float64 tensor handed to a float32 argument is an error, not a misread."""
+    import torch
+
+    from mobilefinetuner_amd import ops
+    assert ops._p(_FakeDev(torch.float32)).value == 4096
+    with pytest.raises(TypeError):
+        ops._p(_FakeDev(torch.float64))
+    with pytest.raises(TypeError):
+        ops._p(_FakeDev(torch.float32), torch.int32)
+    assert ops._p(_FakeDev(torch.float16), (torch.float32, torch.float16)).value == 4096
+    assert ops._p(None) is None

@@ -141,6 +141,10 @@ ATTN = [
     (2, 4, 1, 96, 256, 0, False),     # Gemma hd=256, GQA 4:1
     (1, 4, 1, 200, 256, 64, False),   # Gemma sliding window
     (1, 4, 2, 77, 128, 0, True),      # hd=128, ragged S
+    # grids large enough for the 4- and 2-wave workgroup variants
+    (8, 16, 4, 256, 64, 0, False),    # 4 waves / workgroup, GQA 4:1
+    (4, 8, 2, 500, 128, 0, True),     # 2 waves / workgroup, ragged S, padding mask
+    (4, 8, 2, 512, 256, 128, False),  # 2 waves / workgroup, hd=256 sliding window
 ]
 
 
@@ -303,9 +307,36 @@ def test_embed():
     V, C, S = 50257, 768, 128
     wte, wpe = rn(V, C, std=0.02), rn(1024, C, std=0.02)
     ids = RNG.integers(0, V, (4, S)).astype(np.int32)
-    out = ops.embed(g(ids), S, g(wte), g(wpe), 1.0)
-    assert np.array_equal(h(out), O.embed(ids, S, wte, wpe, 1.0))
+    # NaN-filled output: a row the kernel never wrote stays NaN
+    out = torch.full((4 * S, C), float("nan"), device=DEV)
+    gi, gw, gp = g(ids), g(wte), g(wpe)
+    ops.embed(gi, S, gw, gp, 1.0, out=out)
+    got, ref = h(out), O.embed(ids, S, wte, wpe, 1.0)
+    exact = np.all(got == ref, axis=1)
+    assert exact.all(), (f"{exact.sum()}/{len(exact)} rows exact, "
+                         f"{np.isnan(got).all(axis=1).sum()} rows unwritten")
     w16 = wte.astype(np.float16)
     out16 = ops.embed(g(ids), S, g(w16), None, math.sqrt(640))
     ref16 = O.embed(ids, S, None, None, math.sqrt(640), wte_f16=w16.view(np.uint16))
     assert np.array_equal(h(out16), ref16)
+
+
+def test_outputs_float32_whatever_the_default_dtype():
+    """Wrapper-allocated outputs are float32 even when torch's default dtype is
+    not (the kernels write fp32 through raw pointers)."""
+    ids = RNG.integers(0, 300, (2, 16)).astype(np.int32)
+    wte, x = rn(300, 64), rn(32, 64)
+    gm, b = rn(64), rn(64)
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    try:
+        out = ops.embed(g(ids), 16, g(wte), None, 1.0)
+        y, mean, rstd = ops.layernorm_fwd(g(x), g(gm), g(b), 1e-5)
+        ry, rr = ops.rmsnorm_fwd(g(x), g(gm), 1e-6, 0)
+    finally:
+        torch.set_default_dtype(old)
+    assert all(t.dtype == torch.float32 for t in (out, y, mean, rstd, ry, rr))
+    assert np.array_equal(h(out), O.embed(ids, 16, wte, None, 1.0))
+    assert rel_err(h(y), O.layernorm_fwd(x, gm, b, 1e-5)[0]) < TOL
+    with pytest.raises(TypeError):
+        ops.embed(g(ids.astype(np.int64)), 16, g(wte), None, 1.0)

@@ -12,8 +12,12 @@ import torch
 import oracle as O
 from conftest import rel_err
 
-torch.set_default_dtype(torch.float64)
 RNG = np.random.default_rng(1234)
+
+
+def T(a, **kw):
+    """fp64 torch tensor of a numpy array (references run in double)."""
+    return torch.tensor(np.asarray(a, dtype=np.float64), **kw)
 
 
 def rn(*shape, std=1.0):
@@ -49,9 +53,9 @@ def test_lora_linear_bwd_autograd(M, K, N, r):
     dy = rn(M, N)
     y, xa = O.lora_linear_fwd(x, W, b, A, B, s)
     dx, dA, dB = O.lora_linear_bwd(dy, x, W, A, B, xa, s)
-    tx, tA, tB = (torch.tensor(v, requires_grad=True) for v in (x, A, B))
-    ty = tx @ torch.tensor(W) + torch.tensor(b) + s * (tx @ tA.T) @ tB.T
-    ty.backward(torch.tensor(dy))
+    tx, tA, tB = (T(v, requires_grad=True) for v in (x, A, B))
+    ty = tx @ T(W) + T(b) + s * (tx @ tA.T) @ tB.T
+    ty.backward(T(dy))
     assert rel_err(dx, tx.grad.numpy()) < 1e-6
     assert rel_err(dA, tA.grad.numpy()) < 1e-6
     assert rel_err(dB, tB.grad.numpy()) < 1e-6
@@ -114,11 +118,11 @@ def test_attention_fwd_bwd_vs_autograd(B, Hq, Hkv, S, hd, window):
     if B > 1:
         kpad[1, -3:] = 0
     o, lse = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, True, window, kpad)
-    tq, tk, tv = (torch.tensor(a, requires_grad=True) for a in (q, k, v))
+    tq, tk, tv = (T(a, requires_grad=True) for a in (q, k, v))
     to = torch_attn(tq, tk, tv, B, Hq, Hkv, S, hd, scale, True, window, kpad)
     assert rel_err(o, to.detach().numpy()) < 1e-6
     g = rn(B * S, Hq * hd)
-    to.backward(torch.tensor(g))
+    to.backward(T(g))
     dq, dk, dv = O.attn_bwd(q, k, v, o, g, lse, B, Hq, Hkv, S, hd, scale, True, window, kpad)
     assert rel_err(dq, tq.grad.numpy()) < 1e-5
     assert rel_err(dk, tk.grad.numpy()) < 1e-5
@@ -129,7 +133,7 @@ def test_attention_matches_sdpa_and_invariants():
     B, H, S, hd = 2, 3, 11, 16
     q, k, v = rn(B * S, H * hd), rn(B * S, H * hd), rn(B * S, H * hd)
     o, lse = O.attn_fwd(q, k, v, B, H, H, S, hd, hd ** -0.5)
-    tq, tk, tv = (torch.tensor(a).reshape(B, S, H, hd).permute(0, 2, 1, 3) for a in (q, k, v))
+    tq, tk, tv = (T(a).reshape(B, S, H, hd).permute(0, 2, 1, 3) for a in (q, k, v))
     ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True)
     assert rel_err(o, ref.permute(0, 2, 1, 3).reshape(B * S, H * hd).numpy()) < 1e-6
     # row 0 attends only to key 0 → O = V[0], lse = scale·q0·k0
@@ -157,7 +161,7 @@ def test_ce_vs_torch_cross_entropy(B, S, V):
     labels[-1, -1] = -100
     up = 0.5
     ls, n, dl, nll = O.ce_fwd_bwd(logits, labels, B, S, -100, up)
-    tl = torch.tensor(logits, requires_grad=True)
+    tl = T(logits, requires_grad=True)
     shift = tl.reshape(B, S, V)[:, :-1].reshape(-1, V)
     tgt = torch.tensor(labels[:, 1:].reshape(-1).astype(np.int64))
     loss = torch.nn.functional.cross_entropy(shift, tgt, ignore_index=-100, reduction="mean")
@@ -238,11 +242,11 @@ def test_sumsq_and_clip():
 def test_layernorm_vs_torch():
     x, g, b = rn(13, 40, std=2.0), rn(40), rn(40)
     y, mean, rstd = O.layernorm_fwd(x, g, b, 1e-5)
-    tx = torch.tensor(x, requires_grad=True)
-    ty = torch.nn.functional.layer_norm(tx, (40,), torch.tensor(g), torch.tensor(b), 1e-5)
+    tx = T(x, requires_grad=True)
+    ty = torch.nn.functional.layer_norm(tx, (40,), T(g), T(b), 1e-5)
     assert rel_err(y, ty.detach().numpy()) < 1e-6
     dy = rn(13, 40)
-    ty.backward(torch.tensor(dy))
+    ty.backward(T(dy))
     assert rel_err(O.layernorm_bwd(dy, x, g, mean, rstd), tx.grad.numpy()) < 1e-5
 
 
@@ -250,31 +254,31 @@ def test_layernorm_vs_torch():
 def test_rmsnorm_vs_autograd(unit):
     x, w = rn(11, 64, std=2.0), rn(64, std=0.3)
     y, rstd = O.rmsnorm_fwd(x, w, 1e-6, unit)
-    tx = torch.tensor(x, requires_grad=True)
-    tw = torch.tensor(w) + (1.0 if unit else 0.0)
+    tx = T(x, requires_grad=True)
+    tw = T(w) + (1.0 if unit else 0.0)
     ty = tx * torch.rsqrt(tx.pow(2).mean(-1, keepdim=True) + 1e-6) * tw
     assert rel_err(y, ty.detach().numpy()) < 1e-6
     dy = rn(11, 64)
-    ty.backward(torch.tensor(dy))
+    ty.backward(T(dy))
     assert rel_err(O.rmsnorm_bwd(dy, x, w, rstd, unit), tx.grad.numpy()) < 1e-5
 
 
 @pytest.mark.parametrize("act", [0, 1])
 def test_glu_vs_torch(act):
     gate, up, dout = rn(500, std=3), rn(500), rn(500)
-    tg = torch.tensor(gate, requires_grad=True)
-    tu = torch.tensor(up, requires_grad=True)
+    tg = T(gate, requires_grad=True)
+    tu = T(up, requires_grad=True)
     a = (torch.nn.functional.gelu(tg, approximate="tanh") if act == 0
          else torch.nn.functional.silu(tg))
     out = a * tu
     assert rel_err(O.glu_fwd(gate, up, act), out.detach().numpy()) < 1e-6
-    out.backward(torch.tensor(dout))
+    out.backward(T(dout))
     dg, du = O.glu_bwd(dout, gate, up, act)
     assert rel_err(dg, tg.grad.numpy()) < 1e-5
     assert rel_err(du, tu.grad.numpy()) < 1e-6
     # GPT-2 MLP: plain activation when up is absent
     assert rel_err(O.glu_fwd(gate, None, 0),
-                   torch.nn.functional.gelu(torch.tensor(gate), approximate="tanh").numpy()) < 1e-6
+                   torch.nn.functional.gelu(T(gate), approximate="tanh").numpy()) < 1e-6
 
 
 def test_rope_vs_hf_apply_rotary():
@@ -286,7 +290,7 @@ def test_rope_vs_hf_apply_rotary():
     freqs = torch.arange(S, dtype=torch.float64)[:, None] * inv[None]
     emb = torch.cat([freqs, freqs], -1)
     cos, sin = emb.cos()[None], emb.sin()[None]
-    tx = torch.tensor(x).reshape(B, S, H, hd).permute(0, 2, 1, 3)
+    tx = T(x).reshape(B, S, H, hd).permute(0, 2, 1, 3)
     ref, _ = apply_rotary_pos_emb(tx, tx, cos, sin)
     assert rel_err(out, ref.permute(0, 2, 1, 3).reshape(B * S, H * hd).numpy()) < 1e-6
     back = O.rope(out, B, S, H, hd, theta, inverse=True)   # inverse = transpose rotation
