@@ -51,7 +51,23 @@ def parse():
                          "instead of launching eagerly (the roofline region is always eager)")
     ap.add_argument("--no-timing", action="store_true",
                     help="skip the per-kernel HIP events (roofline becomes null)")
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB three times with a plain "
+                         "device copy kernel: the reference reading for scaling HBM byte counters")
     return ap.parse_args()
+
+
+def traffic_bytes(config_id):
+    """HBM bytes per launch of the linear-GEMM family, from the two committed
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, scaled by a plain-copy
+    calibration) summarised under profiles/; counters cannot be read from
+    inside this process, so the figure is the profiled one, or None."""
+    path = os.path.join(ROOT, "profiles", f"gemm_linear_{config_id}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get("traffic_bytes_per_launch")
 
 
 def cpu_baseline(rc, seed, steps, threads):
@@ -180,7 +196,7 @@ def main():
         result["roofline"] = {
             "kernel": "gemm_kernel (linear fwd + dX, LoRA epilogue)", "bound": "mfma",
             "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-            "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": None,
+            "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic_bytes(args.config),
             "launches": n, "avg_launch_us": round(1000.0 * t_ms / max(n, 1), 2),
             "timed_steps": tsteps, "ms_per_step_with_events": round(ms_timed, 4)}
         br = {}
@@ -198,6 +214,15 @@ def main():
         result["breakdown"] = br
     else:
         result["roofline"] = None
+    if args.calibrate_copy_mb:
+        n = args.calibrate_copy_mb * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = n * 4
+        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(rc, args.seed, args.cpu_steps, args.cpu_threads)
     else:

@@ -52,6 +52,10 @@ struct GemmEpilogue {
   int r = 0;
   int64_t qsn = 0, qsj = 0;
   float lscale = 0.f;
+  // Call site: 0 = a layer's linear GEMM, 1 = the LM head.  Selects a
+  // separately named (otherwise identical) kernel instantiation so kernel
+  // traces and counter profiles attribute the two apart.
+  int site = 0;
 };
 
 // Device scratch handed to launchers (split-K partials, rank-r temporaries).

@@ -572,8 +572,10 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     rmsnorm_fwd(s, m->h_final, pd<float>(m, m->nfw), M, d, c.norm_eps, gemma, m->hf, m->frstd);
   // LM head: logits = hf · Eᵀ, E [V, d] is the [N, K] operand.
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
-  gemm(s, m->hf, d, E.data, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, GemmEpilogue(),
-       m->ws, t.events());
+  GemmEpilogue head;
+  head.site = 1;
+  gemm(s, m->hf, d, E.data, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, head, m->ws,
+       t.events());
 }
 
 void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs, int S,
@@ -603,8 +605,10 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   {
     // dhf = dlogits · E, E [V, d] is the [K, N] operand.
     Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
-    gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, GemmEpilogue(),
-         m->ws, t.events());
+    GemmEpilogue head;
+    head.site = 1;
+    gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
+         t.events());
   }
   if (gpt2)
     layernorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->fmean, m->frstd, M, d, m->dh, false);

@@ -76,7 +76,7 @@ __device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep, float ac
   return v;
 }
 
-template <int BM, int BN, int BK, bool B_NK, bool B_F16>
+template <int BM, int BN, int BK, bool B_NK, bool B_F16, int SITE>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   constexpr int NWM = BM / 64, NWN = BN / 64;  // 64×64 sub-tiles
   constexpr int KW = 4 / (NWM * NWN);          // waves sharing a sub-tile (K split)
@@ -346,6 +346,18 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int spli
   C[(int64_t)m * ldc + n] = epilogue_value(ep, s, m, n, C, ldc);
 }
 
+template <int BM, int BN, int BK, int SITE>
+void launch_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
+  const dim3 block(256);
+  if (b_nk) {
+    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, false, SITE>), grid, block, 0, s, p);
+  } else {
+    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, false, SITE>), grid, block, 0, s, p);
+  }
+}
+
 template <int BM, int BN, int BK>
 void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
@@ -353,13 +365,8 @@ void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   dim3 grid(p.tiles_per_xcd * 8, splits), block(256);
-  if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, true>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, false>), grid, block, 0, s, p);
-  } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, true>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, false>), grid, block, 0, s, p);
-  }
+  if (p.ep.site == 1) launch_variant<BM, BN, BK, 1>(s, p, grid, b_nk, b_f16);
+  else launch_variant<BM, BN, BK, 0>(s, p, grid, b_nk, b_f16);
   MFT_LAUNCH_CHECK();
 }
 
