@@ -91,6 +91,11 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y,
 void rank_outer(hipStream_t s, const float* P, const float* X, int64_t ldx,
                 int M, int C, int r, float scale, float* out, int64_t osj,
                 int64_t osc, bool accumulate, Scratch ws);
+// Two rank_outer products with the same M, r, scale in one launch.
+void rank_outer_pair(hipStream_t s, int M, int r, float scale, bool accumulate,
+                     const float* P0, const float* X0, int64_t ldx0, int C0, float* out0, int64_t osj0,
+                     int64_t osc0, const float* P1, const float* X1, int64_t ldx1, int C1, float* out1,
+                     int64_t osj1, int64_t osc1);
 
 void lora_linear_fwd(hipStream_t s, const float* x, int64_t M, int64_t K,
                      const void* W, bool w_f16, int64_t N, const float* bias,

@@ -486,8 +486,9 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
   if (lora) {
     Timed tr(m, CLS_RANK, 2.0 * M * r * (l.K + l.N));
     tr.begin();
-    rank_outer(m->stream, U, x, l.K, (int)M, l.K, r, lscale(m), m->P[l.A].grad, l.K, 1, true, rest);
-    rank_outer(m->stream, xa, dy, l.N, (int)M, l.N, r, lscale(m), m->P[l.B].grad, 1, r, true, rest);
+    // dA += s·Uᵀ·x and dB += s·dyᵀ·xa in one launch
+    rank_outer_pair(m->stream, (int)M, r, lscale(m), true, U, x, l.K, l.K, m->P[l.A].grad, l.K, 1, xa, dy,
+                    l.N, l.N, m->P[l.B].grad, 1, r);
     tr.end();
   }
 }

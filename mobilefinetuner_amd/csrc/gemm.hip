@@ -60,17 +60,12 @@ __device__ __forceinline__ floatx4 widen4(uint2 u) {
                  half_bits_to_float(u.y & 0xffff), half_bits_to_float(u.y >> 16)};
 }
 
+// Bias, residual and β·C; the rank-r term is accumulated on the matrix
+// cores before the epilogue.
 __device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep, float acc, int m, int n,
                                                 const float* C, int64_t ldc) {
   float v = acc;
   if (ep.bias) v += ep.bias[n];
-  if (ep.P) {
-    float s = 0.f;
-    const float* pr = ep.P + (int64_t)m * ep.r;
-    const float* qn = ep.Q + (int64_t)n * ep.qsn;
-    for (int j = 0; j < ep.r; ++j) s = fmaf(pr[j], qn[j * ep.qsj], s);
-    v = fmaf(ep.lscale, s, v);
-  }
   if (ep.resid) v += ep.resid[(int64_t)m * ldc + n];
   if (ep.beta != 0.f) v = fmaf(ep.beta, C[(int64_t)m * ldc + n], v);
   return v;
@@ -278,6 +273,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     if (kt + 1 < nk) step(I1{}, kt + 1);
   }
 
+  // Rank-r LoRA term on the matrix cores: C += lscale·P[M,r]·Qᵀ is one more
+  // K panel of depth r (padded to even), staged in the free LDS ring and
+  // multiplied by the waves of K-split slot 0 (split 0 only, so split-K adds
+  // it once).  Lane (li, lh) supplies P[row li][2t+lh] and Q[col li][2t+lh].
+  if (p.ep.P != nullptr && split == 0) {
+    const int r = p.ep.r, rp = (r + 1) & ~1, pr = rp + 1;  // odd pitch: conflict-free column reads
+    float* Ps = smem;
+    float* Qs = smem + BM * pr;
+    for (int i = tid; i < BM * rp; i += 256) {
+      const int row = i / rp, j = i % rp, m = m0 + row;
+      Ps[row * pr + j] = (m < p.M && j < r) ? p.ep.P[(int64_t)m * r + j] : 0.f;
+    }
+    for (int i = tid; i < BN * rp; i += 256) {
+      const int col = i / rp, j = i % rp, n = n0 + col;
+      Qs[col * pr + j] = (n < p.N && j < r) ? p.ep.lscale * p.ep.Q[(int64_t)n * p.ep.qsn + (int64_t)j * p.ep.qsj] : 0.f;
+    }
+    __syncthreads();
+    if (kw == 0) {
+      for (int t = 0; t < rp / 2; ++t) {
+        const int k = 2 * t + lh;
+        float fp[2], fq[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) fp[a] = Ps[(wm + a * 32 + li) * pr + k];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + b * 32 + li) * pr + k];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(fp[a], fq[b], acc[a][b], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
   const bool split_out = p.partial != nullptr;
   // K-split: every wave parks its partial sub-tile in LDS (the ring is free
   // after the final barrier), then all 256 threads sum the KW partials of
@@ -364,7 +394,7 @@ void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits
   p.tiles_n = (int)cdiv(p.N, BN);
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
-  dim3 grid(p.tiles_per_xcd * 8, splits), block(256);
+  const dim3 grid(p.tiles_per_xcd * 8, splits);
   if (p.ep.site == 1) launch_variant<BM, BN, BK, 1>(s, p, grid, b_nk, b_f16);
   else launch_variant<BM, BN, BK, 0>(s, p, grid, b_nk, b_f16);
   MFT_LAUNCH_CHECK();

@@ -71,8 +71,13 @@ void lora_linear_bwd(hipStream_t s, const float* dy, const float* x,
     gemm(s, dy, N, W, N, /*b_nk=*/true, w_f16, dx, K, (int)M, (int)K, (int)N, ep, rest, ev);
   }
   if (lora) {
-    if (dA) rank_outer(s, U, x, K, (int)M, (int)K, r, scale, dA, /*osj=*/K, /*osc=*/1, accumulate, rest);
-    if (dB) rank_outer(s, xa, dy, N, (int)M, (int)N, r, scale, dB, /*osj=*/1, /*osc=*/r, accumulate, rest);
+    // dA(j,k) = s·Σ_m U[m,j]·x[m,k] → dA[j*K + k];  dB(n,j) = s·Σ_m xa[m,j]·dy[m,n] → dB[n*r + j]
+    if (dA && dB)
+      rank_outer_pair(s, (int)M, r, scale, accumulate, U, x, K, (int)K, dA, K, 1, xa, dy, N, (int)N, dB, 1, r);
+    else if (dA)
+      rank_outer(s, U, x, K, (int)M, (int)K, r, scale, dA, /*osj=*/K, /*osc=*/1, accumulate, rest);
+    else if (dB)
+      rank_outer(s, xa, dy, N, (int)M, (int)N, r, scale, dB, /*osj=*/1, /*osc=*/r, accumulate, rest);
   }
 }
 

@@ -6,10 +6,10 @@
 // Both are HBM/latency-bound passes over X (2–16 MB at the benchmark
 // shapes).  rank_proj gives each wave two rows and has every lane stream
 // 128-bit chunks of K, so a wave keeps ~20 independent 16-byte loads in
-// flight; the r×K (or K×r) factor is re-read from L1/L2.  rank_outer splits M
-// into slices (≥ ~256 workgroups), keeps r partial sums per column in
-// registers, reduces the four waves of a workgroup in LDS and finishes the
-// slices in a fixed order (deterministic, no atomics).
+// flight; the r×K (or K×r) factor is re-read from L1/L2.  rank_outer runs on
+// the matrix cores, one launch for both gradients of a layer, with M split
+// over the waves of a workgroup and summed in wave order (deterministic, no
+// atomics, no second pass).
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -122,66 +122,86 @@ __global__ __launch_bounds__(256) void rank_proj_scalar_kernel(const float* X, i
   }
 }
 
-// Partial Σ_m P[m,j] X[m,c] over one row slice: 64 columns per workgroup
-// (one per lane), the 4 waves interleave rows.  part[slice][j][c].
-template <int R>
-__global__ __launch_bounds__(256) void rank_outer_kernel(const float* __restrict__ P,
-                                                          const float* __restrict__ X,
-                                                          int64_t ldx, int M, int C,
-                                                          int rows_per_slice, float scale,
-                                                          float* part, float* out, int64_t osj,
-                                                          int64_t osc, int direct,
-                                                          int accumulate) {
-  __shared__ float red[3][R][64];
+// out(j,c) (+)= scale·Σ_m P[m,j]·X[m,c] on the matrix cores
+// (v_mfma_f32_16x16x4_f32): D[c][j] += A[c][m]·B[m][j] with A = Xᵀ, B = P,
+// so lane (i, g) feeds X[m+g][c0+i] and P[m+g][16·jt+i] and ends holding
+// D[c0+4g+v][16·jt+i].  A workgroup owns 16 columns c of one product; its 8
+// waves take consecutive eighths of M (loads of 8 MFMA steps issued ahead of
+// the MFMAs) and are summed through LDS in wave order.  Two independent
+// products (dA and dB of one LoRA layer) share one launch.
+struct OuterJob {
+  const float* P;
+  const float* X;
+  int64_t ldx;
+  int C, blocks;
+  float* out;
+  int64_t osj, osc;
+};
+struct OuterArgs {
+  OuterJob job[2];
+  int M, r, accumulate;
+  float scale;
+};
+
+template <int JT>
+__global__ __launch_bounds__(512) void rank_outer_mfma(OuterArgs a) {
+  __shared__ floatx4 red[7][JT][64];
+  const bool second = (int)blockIdx.x >= a.job[0].blocks;
+  const OuterJob jb = second ? a.job[1] : a.job[0];
+  const int blk = second ? (int)blockIdx.x - a.job[0].blocks : (int)blockIdx.x;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
-  const int slice = blockIdx.y;
-  const int mb = slice * rows_per_slice, me = min(M, mb + rows_per_slice);
-  float acc[R];
+  const int i = lane & 15, g = lane >> 4;
+  const int c0 = blk * 16;
+  const int ci = min(c0 + i, jb.C - 1);
+  const bool cok = c0 + i < jb.C;
+  const int per = ((a.M + 8 * 32 - 1) / (8 * 32)) * 32;  // rows per wave, multiple of 32
+  const int mb = w * per, me = min(a.M, mb + per);
+  floatx4 acc[JT];
 #pragma unroll
-  for (int j = 0; j < R; ++j) acc[j] = 0.f;
-  if (c < C) {
-#pragma unroll 4
-    for (int m = mb + w; m < me; m += 4) {
-      const float xv = X[(int64_t)m * ldx + c];
-      const floatx4* pr = reinterpret_cast<const floatx4*>(P + (int64_t)m * R);
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int m = mb; m < me; m += 32) {
+    float xv[8], pv[JT][8];
 #pragma unroll
-      for (int jq = 0; jq < R / 4; ++jq) {
-        const floatx4 p4 = pr[jq];
+    for (int t = 0; t < 8; ++t) {
+      const int mr = m + 4 * t + g;
+      const bool ok = mr < me;
+      const int mc = ok ? mr : mb;
+      const float x = jb.X[(int64_t)mc * jb.ldx + ci];
+      xv[t] = (ok && cok) ? x : 0.f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[4 * jq + u] = fmaf(p4[u], xv, acc[4 * jq + u]);
+      for (int jt = 0; jt < JT; ++jt) {
+        const int jj = 16 * jt + i;
+        const float pp = jb.P[(int64_t)mc * a.r + min(jj, a.r - 1)];
+        pv[jt][t] = (ok && jj < a.r) ? pp : 0.f;
       }
     }
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t], pv[jt][t], acc[jt], 0, 0, 0);
   }
   if (w > 0) {
 #pragma unroll
-    for (int j = 0; j < R; ++j) red[w - 1][j][lane] = acc[j];
+    for (int jt = 0; jt < JT; ++jt) red[w - 1][jt][lane] = acc[jt];
   }
   __syncthreads();
-  if (w == 0 && c < C) {
+  if (w != 0) return;
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-      const float v = ((acc[j] + red[0][j][lane]) + red[1][j][lane]) + red[2][j][lane];
-      if (direct) {
-        float* o = out + (int64_t)j * osj + (int64_t)c * osc;
-        *o = accumulate ? fmaf(scale, v, *o) : scale * v;
-      } else {
-        part[((int64_t)slice * R + j) * C + c] = v;
-      }
+  for (int jt = 0; jt < JT; ++jt) {
+    floatx4 v = acc[jt];
+#pragma unroll
+    for (int q = 0; q < 7; ++q) v += red[q][jt][lane];
+    const int j = 16 * jt + i;
+    if (j >= a.r) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = c0 + 4 * g + e;
+      if (c >= jb.C) continue;
+      float* o = jb.out + (int64_t)j * jb.osj + (int64_t)c * jb.osc;
+      *o = a.accumulate ? fmaf(a.scale, v[e], *o) : a.scale * v[e];
     }
   }
-}
-
-__global__ void rank_outer_finish(const float* __restrict__ part, int slices, int C, int r,
-                                  float scale, float* out, int64_t osj, int64_t osc,
-                                  int accumulate) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)C * r) return;
-  const int j = (int)(idx / C), c = (int)(idx % C);
-  float s = 0.f;
-  for (int z = 0; z < slices; ++z) s += part[((int64_t)z * r + j) * C + c];
-  float* o = out + (int64_t)j * osj + (int64_t)c * osc;
-  *o = accumulate ? fmaf(scale, s, *o) : scale * s;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -194,26 +214,13 @@ void proj_vec(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y
   else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
 }
 
-template <int R>
-void outer_launch(hipStream_t s, const float* P, const float* X, int64_t ldx, int M, int C,
-                  float scale, float* out, int64_t osj, int64_t osc, bool accumulate, Scratch ws) {
-  const int64_t cblocks = cdiv(C, 64);
-  int64_t slices = std::max<int64_t>(1, std::min<int64_t>(cdiv(256, cblocks), cdiv(M, 16)));
-  while (slices > 1 && (size_t)slices * R * C * sizeof(float) > ws.bytes) slices /= 2;
-  if (!ws.ptr) slices = 1;
-  const int rows = (int)cdiv(M, slices);
-  slices = cdiv(M, rows);
-  const int direct = slices == 1;
-  dim3 grid((unsigned)cblocks, (unsigned)slices), block(256);
-  hipLaunchKernelGGL((rank_outer_kernel<R>), grid, block, 0, s, P, X, ldx, M, C, rows, scale, ws.ptr,
-                     out, osj, osc, direct, accumulate ? 1 : 0);
+void outer_launch(hipStream_t s, OuterArgs& a) {
+  a.job[0].blocks = (int)cdiv(a.job[0].C, 16);
+  a.job[1].blocks = a.job[1].out ? (int)cdiv(a.job[1].C, 16) : 0;
+  const dim3 grid((unsigned)(a.job[0].blocks + a.job[1].blocks)), block(512);
+  if (a.r <= 16) hipLaunchKernelGGL(rank_outer_mfma<1>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(rank_outer_mfma<2>, grid, block, 0, s, a);
   MFT_LAUNCH_CHECK();
-  if (!direct) {
-    hipLaunchKernelGGL(rank_outer_finish, dim3((unsigned)cdiv((int64_t)C * R, 256)), dim3(256), 0, s,
-                       (const float*)ws.ptr, (int)slices, C, R, scale, out, osj, osc,
-                       accumulate ? 1 : 0);
-    MFT_LAUNCH_CHECK();
-  }
 }
 
 }  // namespace
@@ -239,15 +246,38 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64
   MFT_LAUNCH_CHECK();
 }
 
+namespace {
+OuterJob make_job(const float* P, const float* X, int64_t ldx, int C, float* out, int64_t osj,
+                  int64_t osc) {
+  MFT_CHECK_ARG(P && X && out && C > 0, "rank_outer: null tensor or empty");
+  OuterJob j{};
+  j.P = P; j.X = X; j.ldx = ldx; j.C = C; j.out = out; j.osj = osj; j.osc = osc;
+  return j;
+}
+
+}  // namespace
+
 void rank_outer(hipStream_t s, const float* P, const float* X, int64_t ldx, int M, int C, int r,
-                float scale, float* out, int64_t osj, int64_t osc, bool accumulate, Scratch ws) {
-  MFT_CHECK_ARG(r == 4 || r == 8 || r == 16 || r == 32, "rank must be 4, 8, 16 or 32");
-  MFT_CHECK_ARG(M > 0 && C > 0, "empty");
-  MFT_CHECK_ARG(aligned16(P), "P must be 16-byte aligned");
-  if (r == 4) outer_launch<4>(s, P, X, ldx, M, C, scale, out, osj, osc, accumulate, ws);
-  else if (r == 8) outer_launch<8>(s, P, X, ldx, M, C, scale, out, osj, osc, accumulate, ws);
-  else if (r == 16) outer_launch<16>(s, P, X, ldx, M, C, scale, out, osj, osc, accumulate, ws);
-  else outer_launch<32>(s, P, X, ldx, M, C, scale, out, osj, osc, accumulate, ws);
+                float scale, float* out, int64_t osj, int64_t osc, bool accumulate, Scratch) {
+  MFT_CHECK_ARG(r >= 1 && r <= 32, "rank must be in [1,32]");
+  MFT_CHECK_ARG(M > 0, "empty");
+  OuterArgs a{};
+  a.job[0] = make_job(P, X, ldx, C, out, osj, osc);
+  a.M = M; a.r = r; a.accumulate = accumulate ? 1 : 0; a.scale = scale;
+  outer_launch(s, a);
+}
+
+void rank_outer_pair(hipStream_t s, int M, int r, float scale, bool accumulate,
+                     const float* P0, const float* X0, int64_t ldx0, int C0, float* out0, int64_t osj0,
+                     int64_t osc0, const float* P1, const float* X1, int64_t ldx1, int C1, float* out1,
+                     int64_t osj1, int64_t osc1) {
+  MFT_CHECK_ARG(r >= 1 && r <= 32, "rank must be in [1,32]");
+  MFT_CHECK_ARG(M > 0, "empty");
+  OuterArgs a{};
+  a.job[0] = make_job(P0, X0, ldx0, C0, out0, osj0, osc0);
+  a.job[1] = make_job(P1, X1, ldx1, C1, out1, osj1, osc1);
+  a.M = M; a.r = r; a.accumulate = accumulate ? 1 : 0; a.scale = scale;
+  outer_launch(s, a);
 }
 
 }  // namespace mft
