@@ -55,19 +55,42 @@ __device__ __forceinline__ bool visible(const AttnP& p, int i, int j, const floa
   return true;
 }
 
-// Stage rows [r0, r0+rows) of a token-major [.., S, H, HD] tensor (head h)
-// into LDS with pitch HD+4.  Rows past S are zero.
-template <int HD, int NT>
-__device__ __forceinline__ void stage_rows(float* lds, const float* src, int64_t rs, int b, int S,
-                                           int h, int r0, int rows, int tid) {
+// Stage rows [r0, r0+ROWS) of two token-major [.., S, H, HD] tensors (head
+// h) into LDS with pitch HD+4; rows past S are zero.  Branch-free: row
+// indices are clamped into the tensor and the values selected to zero, and
+// each thread issues a batch of CH loads per tensor before any LDS store, so
+// a block's loads are in flight together instead of one latency per element.
+template <int HD, int NT, int ROWS>
+__device__ __forceinline__ void stage_pair(float* lds1, const float* src1, int64_t rs1, float* lds2,
+                                           const float* src2, int64_t rs2, int b, int S, int h1, int h2,
+                                           int r0, int tid) {
   constexpr int P = HD + 4;
-  const int total = rows * (HD / 4);
-  for (int f = tid; f < total; f += NT) {
-    const int r = f / (HD / 4), c4 = f % (HD / 4);
-    const int gr = r0 + r;
-    floatx4 val = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (gr < S) val = *reinterpret_cast<const floatx4*>(src + ((int64_t)b * S + gr) * rs + (int64_t)h * HD + 4 * c4);
-    *reinterpret_cast<floatx4*>(lds + r * P + 4 * c4) = val;
+  constexpr int TOTAL = ROWS * (HD / 4);
+  static_assert(TOTAL % NT == 0, "staging shape");
+  constexpr int ITEMS = TOTAL / NT;
+  constexpr int CH = ITEMS < 512 / HD ? ITEMS : 512 / HD;
+  static_assert(ITEMS % CH == 0, "staging batch");
+#pragma unroll
+  for (int base = 0; base < ITEMS; base += CH) {
+    floatx4 v1[CH], v2[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int f = tid + NT * (base + c);
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      const int gr = min(r0 + r, S - 1);
+      const int64_t row = (int64_t)b * S + gr;
+      v1[c] = *reinterpret_cast<const floatx4*>(src1 + row * rs1 + (int64_t)h1 * HD + 4 * c4);
+      v2[c] = *reinterpret_cast<const floatx4*>(src2 + row * rs2 + (int64_t)h2 * HD + 4 * c4);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int f = tid + NT * (base + c);
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      const bool ok = r0 + r < S;
+      const floatx4 z = floatx4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<floatx4*>(lds1 + r * P + 4 * c4) = ok ? v1[c] : z;
+      *reinterpret_cast<floatx4*>(lds2 + r * P + 4 * c4) = ok ? v2[c] : z;
+    }
   }
 }
 
@@ -111,8 +134,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
-    stage_rows<HD, NT>(Ks, p.k, p.k_rs, b, p.S, kh, j0, BKV, tid);
-    stage_rows<HD, NT>(Vs, p.v, p.v_rs, b, p.S, kh, j0, BKV, tid);
+    stage_pair<HD, NT, BKV>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, j0, tid);
     if (kpb)
       for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S ? kpb[j0 + j] : 0.f;
     __syncthreads();
@@ -255,8 +277,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   const int kj = kbase + li;  // this lane's key (as S column)
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
 
-  stage_rows<HD, NT>(Ks, p.k, p.k_rs, b, p.S, kh, k0, BKEYS, tid);
-  stage_rows<HD, NT>(Vs, p.v, p.v_rs, b, p.S, kh, k0, BKEYS, tid);
+  stage_pair<HD, NT, BKEYS>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, k0, tid);
   if (kpb)
     for (int j = tid; j < BKEYS; j += NT) Kp[j] = k0 + j < p.S ? kpb[k0 + j] : 0.f;
 
@@ -270,8 +291,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   {
     for (int qb0 = (qstart / BQ) * BQ; qb0 <= qend; qb0 += BQ) {
       __syncthreads();
-      stage_rows<HD, NT>(Qs, p.q, p.q_rs, b, p.S, h, qb0, BQ, tid);
-      stage_rows<HD, NT>(Gs, p.dout, p.do_rs, b, p.S, h, qb0, BQ, tid);
+      stage_pair<HD, NT, BQ>(Qs, p.q, p.q_rs, Gs, p.dout, p.do_rs, b, p.S, h, h, qb0, tid);
       for (int e = tid; e < BQ; e += NT) {
         const int gi = qb0 + e;
         const int64_t l = ((int64_t)b * p.Hq + h) * p.S + gi;
@@ -417,8 +437,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
-    stage_rows<HD, NT>(Ks, p.k, p.k_rs, b, p.S, kh, j0, BKV, tid);
-    stage_rows<HD, NT>(Vs, p.v, p.v_rs, b, p.S, kh, j0, BKV, tid);
+    stage_pair<HD, NT, BKV>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, j0, tid);
     if (kpb)
       for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S ? kpb[j0 + j] : 0.f;
     __syncthreads();

@@ -365,6 +365,227 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     }
 }
 
+// 64×64 workgroup tile for the layer GEMMs: each of the four waves owns a
+// 32×32 quadrant as 2×2 tiles of v_mfma_f32_16x16x4_f32 (four independent
+// accumulation chains, 16 accumulator VGPRs), so no wave shares output
+// elements and the tile needs no LDS reduction at the end.  Lane (i, g) of a
+// 16×16×4 MFMA supplies A[row i][k g] and B[k g][col i] and holds D[row
+// 4g+v][col i]; over four consecutive MFMAs lane group g takes k = 4g..4g+3
+// of a 16-wide k block (the same order for A and B), so every A fragment and
+// every [N,K] B fragment is one 128-bit LDS read.  Panels of BK are staged
+// through two register sets and a two-stage LDS ring exactly like
+// gemm_kernel; the small register and LDS footprint allows four resident
+// workgroups per CU.
+template <int BK, bool B_NK, bool B_F16, int SITE>
+__global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
+  constexpr int BM = 64, BN = 64;
+  constexpr int PA = BK + 4;
+  constexpr int PB = B_NK ? BK + 4 : BN + 4;
+  constexpr int A_ITEMS = BM * BK / 4 / 256;
+  constexpr int B_ITEMS = BN * BK / 4 / 256;
+  constexpr int A_STAGE = BM * PA;
+  constexpr int B_STAGE = B_NK ? BN * PB : BK * PB;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  static_assert(BK % 16 == 0 && A_ITEMS >= 1 && B_ITEMS >= 1, "tile config");
+  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+
+  const int wg = blockIdx.x;
+  const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
+  if (tile >= p.tiles_m * p.tiles_n) return;
+  const int tm_idx = tile % p.tiles_m;
+  const int tn_idx = tile / p.tiles_m;
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int split = blockIdx.y;
+  const int kbeg = split * p.k_chunk;
+  const int kend = min(p.K, kbeg + p.k_chunk);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+  const int li = lane & 15, lg = lane >> 4;
+
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  floatx4 ra_set[2][A_ITEMS], rb_set[2][B_ITEMS];
+  auto load_panel = [&](auto sc, int k0) {
+    constexpr int S = decltype(sc)::value;
+    floatx4(&ra)[A_ITEMS] = ra_set[S];
+    floatx4(&rb)[B_ITEMS] = rb_set[S];
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      const int gm = min(m0 + row, p.M - 1), gk = k0 + kq;
+      floatx4 v = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
+      ra[it] = v;
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      floatx4 v;
+      if constexpr (B_NK) {
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        const int gn = min(n0 + row, p.N - 1), gk = k0 + kq;
+        const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
+        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
+      } else {
+        const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+        const int gk = k0 + k, gn = n0 + nq;
+        const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
+        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
+        const bool ok = gk < kend;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = ok ? v[e] : 0.f;
+      }
+      rb[it] = v;
+    }
+  };
+  auto store_panel = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    const floatx4(&ra)[A_ITEMS] = ra_set[S];
+    const floatx4(&rb)[B_ITEMS] = rb_set[S];
+    float* As = smem + S * STAGE;
+    float* Bs = As + A_STAGE;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = ra[it];
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      if constexpr (B_NK) {
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = rb[it];
+      } else {
+        const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = rb[it];
+      }
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  auto compute = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    const float* as = smem + S * STAGE;
+    const float* bs = as + A_STAGE;
+#pragma unroll
+    for (int kb = 0; kb < BK; kb += 16) {
+      floatx4 fa[2], fb[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) fa[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int col = wn + 16 * b + li;
+        if constexpr (B_NK) {
+          fb[b] = *reinterpret_cast<const floatx4*>(bs + col * PB + kb + 4 * lg);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) fb[b][t] = bs[(kb + 4 * lg + t) * PB + col];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a][t], fb[b][t], acc[a][b], 0, 0, 0);
+    }
+  };
+  constexpr int N_DSR = (BK / 16) * (2 + (B_NK ? 2 : 8));
+  constexpr int N_MFMA = (BK / 16) * 16;
+  constexpr int N_VMEM = A_ITEMS + B_ITEMS;
+  static_assert(N_MFMA >= 2 * N_VMEM, "schedule");
+  auto step = [&](auto sc, int kt) {
+    constexpr int S = decltype(sc)::value;
+    using SN = std::integral_constant<int, 1 - S>;
+    load_panel(sc, kbeg + (kt + 2) * BK);
+    compute(sc);
+    store_panel(SN{});
+    __builtin_amdgcn_sched_group_barrier(0x100, N_DSR, 0);
+#pragma unroll
+    for (int i = 0; i < N_VMEM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < N_VMEM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA - 2 * N_VMEM, 0);
+    __syncthreads();
+  };
+  if (nk > 0) load_panel(I0{}, kbeg);
+  if (nk > 1) load_panel(I1{}, kbeg + BK);
+  if (nk > 0) store_panel(I0{});
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(I0{}, kt);
+    if (kt + 1 < nk) step(I1{}, kt + 1);
+  }
+
+  // Rank-r LoRA term: one more K panel of depth r (padded to a multiple of
+  // 4) from the free LDS ring; split 0 only.
+  if (p.ep.P != nullptr && split == 0) {
+    const int r = p.ep.r, rp = (r + 3) & ~3, pr = rp + 1;
+    float* Ps = smem;
+    float* Qs = smem + BM * pr;
+    for (int i = tid; i < BM * rp; i += 256) {
+      const int row = i / rp, j = i % rp, m = m0 + row;
+      Ps[row * pr + j] = (m < p.M && j < r) ? p.ep.P[(int64_t)m * r + j] : 0.f;
+    }
+    for (int i = tid; i < BN * rp; i += 256) {
+      const int col = i / rp, j = i % rp, n = n0 + col;
+      Qs[col * pr + j] = (n < p.N && j < r) ? p.ep.lscale * p.ep.Q[(int64_t)n * p.ep.qsn + (int64_t)j * p.ep.qsj] : 0.f;
+    }
+    __syncthreads();
+    for (int t = 0; t < rp / 4; ++t) {
+      float fp[2], fq[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + 16 * b + li) * pr + 4 * t + lg];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fp[a], fq[b], acc[a][b], 0, 0, 0);
+    }
+  }
+
+  const bool split_out = p.partial != nullptr;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int n = n0 + wn + 16 * b + li;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm + 16 * a + 4 * lg + v;
+        if (m >= p.M) continue;
+        if (split_out)
+          p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][v];
+        else
+          p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, acc[a][b][v], m, n, p.C, p.ldc);
+      }
+    }
+}
+
 __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M, int N,
                                      float* C, int64_t ldc, GemmEpilogue ep) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -388,6 +609,30 @@ void launch_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bo
   }
 }
 
+template <int BK, int SITE>
+void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
+  const dim3 block(256);
+  if (b_nk) {
+    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BK, true, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_q_kernel<BK, true, false, SITE>), grid, block, 0, s, p);
+  } else {
+    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BK, false, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_q_kernel<BK, false, false, SITE>), grid, block, 0, s, p);
+  }
+}
+
+template <int BK>
+void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
+  p.tiles_m = (int)cdiv(p.M, 64);
+  p.tiles_n = (int)cdiv(p.N, 64);
+  const int tiles = p.tiles_m * p.tiles_n;
+  p.tiles_per_xcd = (int)cdiv(tiles, 8);
+  const dim3 grid(p.tiles_per_xcd * 8, splits);
+  if (p.ep.site == 1) launch_q_variant<BK, 1>(s, p, grid, b_nk, b_f16);
+  else launch_q_variant<BK, 0>(s, p, grid, b_nk, b_f16);
+  MFT_LAUNCH_CHECK();
+}
+
 template <int BM, int BN, int BK>
 void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
@@ -400,11 +645,13 @@ void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits
   MFT_LAUNCH_CHECK();
 }
 
+// bm = 64, bn = 64 → gemm_kernel 64×64 (K split over the waves);
+// bm = 64, bn = 0 → gemm_q_kernel (64×64, wave quadrants).
 struct Plan {
   int bm, bn, splits;
 };
 
-int plan_bk(int bm, int bn) { return (bm == 64 && bn == 64) ? 64 : 32; }
+int plan_bk(int bm, int bn) { return (bm == 64 && (bn == 64 || bn == 1)) ? 64 : 32; }
 
 // Tile shape and split-K, from sweeps of the benchmark shapes on MI355X:
 // 64×64 tiles (two resident workgroups per CU), with split-K doubled while
@@ -418,7 +665,7 @@ Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
   while (tiles * sp < 512 && K / (2 * sp) >= 512 && sp < 8 &&
          (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
     sp *= 2;
-  return {64, 64, sp};
+  return {64, 0, sp};
 }
 
 }  // namespace
@@ -460,12 +707,14 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
 
   Plan pl = plan_gemm(M, N, K, ws.ptr ? ws.bytes : 0);
   // Tuning hook: MFT_GEMM_PLAN="bm,bn,splits" forces the launch shape
-  // (bm×bn ∈ {128×128, 64×128, 64×64}); same arithmetic, other tiling.
+  // (bm×bn ∈ {128×128, 64×128, 64×64}, or "64,0,s" for the quadrant kernel);
+  // same arithmetic, other tiling.
   static const char* forced = getenv("MFT_GEMM_PLAN");
   if (forced) {
     int bm = 0, bn = 0, sp = 0;
     if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
-        ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
+        ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
+         (bm == 64 && (bn == 0 || bn == 1))) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
@@ -478,7 +727,9 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   if (ev && ev->start) MFT_HIP(hipEventRecord(ev->start, s));
   if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 128) launch_tile<64, 128, 32>(s, p, b_nk, b_f16, splits);
-  else launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bn == 64) launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bn == 1) launch_q<64>(s, p, b_nk, b_f16, splits);
+  else launch_q<32>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
 
   if (splits > 1) {
