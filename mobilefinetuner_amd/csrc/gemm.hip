@@ -137,10 +137,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       const int flat = tid + 256 * it;
       const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
       const int gm = min(m0 + row, p.M - 1), gk = k0 + kq;
-      floatx4 v = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
-      ra[it] = v;
+      ra[it] = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
@@ -152,42 +149,52 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
         if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
         const int gk = k0 + k, gn = n0 + nq;
         const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
         if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
-        const bool ok = gk < kend;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = ok ? v[e] : 0.f;
       }
       rb[it] = v;
     }
   };
-  auto store_panel = [&](auto sc) {
+  // The K-tail mask (elements at k ≥ kend read as zero) is applied here,
+  // at the LDS store, not at the load: a select on the loaded value would
+  // make the wave wait for its global loads right after issuing them.
+  auto store_panel = [&](auto sc, int k0) {
     constexpr int S = decltype(sc)::value;
-    const floatx4(&ra)[A_ITEMS] = ra_set[S];
-    const floatx4(&rb)[B_ITEMS] = rb_set[S];
+    floatx4(&ra)[A_ITEMS] = ra_set[S];
+    floatx4(&rb)[B_ITEMS] = rb_set[S];
     float* As = smem + S * STAGE;
     float* Bs = As + A_STAGE;
+    const bool tail = k0 + BK > kend;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = ra[it];
+      floatx4 v = ra[it];
+      if (tail) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (k0 + kq + e < kend) ? v[e] : 0.f;
+      }
+      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = v;
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
       const int flat = tid + 256 * it;
+      floatx4 v = rb[it];
       if constexpr (B_NK) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = rb[it];
+        if (tail) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (k0 + kq + e < kend) ? v[e] : 0.f;
+        }
+        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = v;
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
-        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = rb[it];
+        if (tail && k0 + k >= kend) v = floatx4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = v;
       }
     }
   };
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     using SN = std::integral_constant<int, 1 - S>;
     load_panel(sc, kbeg + (kt + 2) * BK);
     compute(sc);
-    store_panel(SN{});
+    store_panel(SN{}, kbeg + (kt + 1) * BK);
     __builtin_amdgcn_sched_group_barrier(0x100, N_DSR, 0);
 #pragma unroll
     for (int i = 0; i < N_VMEM; ++i) {
@@ -266,11 +273,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   };
   if (nk > 0) load_panel(I0{}, kbeg);
   if (nk > 1) load_panel(I1{}, kbeg + BK);
-  if (nk > 0) store_panel(I0{});
+  if (nk > 0) store_panel(I0{}, kbeg);
   __syncthreads();
+  // Both steps run unconditionally (no control flow inside the loop body,
+  // so the staged registers need no copies at a merge point): when nk is odd
+  // the last step multiplies a panel past kend, which the tail mask zeroed.
   for (int kt = 0; kt < nk; kt += 2) {
     step(I0{}, kt);
-    if (kt + 1 < nk) step(I1{}, kt + 1);
+    step(I1{}, kt + 1);
   }
 
   // Rank-r LoRA term on the matrix cores: C += lscale·P[M,r]·Qᵀ is one more
@@ -421,10 +431,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
       const int flat = tid + 256 * it;
       const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
       const int gm = min(m0 + row, p.M - 1), gk = k0 + kq;
-      floatx4 v = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
-      ra[it] = v;
+      ra[it] = *reinterpret_cast<const floatx4*>(p.A + (int64_t)gm * p.lda + (gk < kend ? gk : 0));
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
@@ -436,42 +443,52 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
         const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
         if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (gk + e < kend) ? v[e] : 0.f;
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
         const int gk = k0 + k, gn = n0 + nq;
         const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
         if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
-        const bool ok = gk < kend;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = ok ? v[e] : 0.f;
       }
       rb[it] = v;
     }
   };
-  auto store_panel = [&](auto sc) {
+  // The K-tail mask (elements at k ≥ kend read as zero) is applied here,
+  // at the LDS store, not at the load: a select on the loaded value would
+  // make the wave wait for its global loads right after issuing them.
+  auto store_panel = [&](auto sc, int k0) {
     constexpr int S = decltype(sc)::value;
-    const floatx4(&ra)[A_ITEMS] = ra_set[S];
-    const floatx4(&rb)[B_ITEMS] = rb_set[S];
+    floatx4(&ra)[A_ITEMS] = ra_set[S];
+    floatx4(&rb)[B_ITEMS] = rb_set[S];
     float* As = smem + S * STAGE;
     float* Bs = As + A_STAGE;
+    const bool tail = k0 + BK > kend;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = ra[it];
+      floatx4 v = ra[it];
+      if (tail) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (k0 + kq + e < kend) ? v[e] : 0.f;
+      }
+      *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = v;
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
       const int flat = tid + 256 * it;
+      floatx4 v = rb[it];
       if constexpr (B_NK) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = rb[it];
+        if (tail) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (k0 + kq + e < kend) ? v[e] : 0.f;
+        }
+        *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = v;
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
-        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = rb[it];
+        if (tail && k0 + k >= kend) v = floatx4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = v;
       }
     }
   };
@@ -514,7 +531,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     using SN = std::integral_constant<int, 1 - S>;
     load_panel(sc, kbeg + (kt + 2) * BK);
     compute(sc);
-    store_panel(SN{});
+    store_panel(SN{}, kbeg + (kt + 1) * BK);
     __builtin_amdgcn_sched_group_barrier(0x100, N_DSR, 0);
 #pragma unroll
     for (int i = 0; i < N_VMEM; ++i) {
@@ -531,11 +548,14 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
   };
   if (nk > 0) load_panel(I0{}, kbeg);
   if (nk > 1) load_panel(I1{}, kbeg + BK);
-  if (nk > 0) store_panel(I0{});
+  if (nk > 0) store_panel(I0{}, kbeg);
   __syncthreads();
+  // Both steps run unconditionally (no control flow inside the loop body,
+  // so the staged registers need no copies at a merge point): when nk is odd
+  // the last step multiplies a panel past kend, which the tail mask zeroed.
   for (int kt = 0; kt < nk; kt += 2) {
     step(I0{}, kt);
-    if (kt + 1 < nk) step(I1{}, kt + 1);
+    step(I1{}, kt + 1);
   }
 
   // Rank-r LoRA term: one more K panel of depth r (padded to a multiple of
