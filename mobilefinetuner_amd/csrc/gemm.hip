@@ -546,16 +546,113 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA - 2 * N_VMEM, 0);
     __syncthreads();
   };
-  if (nk > 0) load_panel(I0{}, kbeg);
-  if (nk > 1) load_panel(I1{}, kbeg + BK);
-  if (nk > 0) store_panel(I0{}, kbeg);
-  __syncthreads();
-  // Both steps run unconditionally (no control flow inside the loop body,
-  // so the staged registers need no copies at a merge point): when nk is odd
-  // the last step multiplies a panel past kend, which the tail mask zeroed.
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(I0{}, kt);
-    step(I1{}, kt + 1);
+  if ((kend - kbeg) % BK == 0) {
+    // Whole panels only (the common case): every thread's global addresses
+    // are fixed per tile up to the panel offset, so they are formed once
+    // here and a panel adds one uniform offset (clamped to the last panel,
+    // so the prefetches past the end stay in bounds; those panels are
+    // stored as zeros).  No per-element masks in the loop.
+    const float* a_ptr[A_ITEMS];
+    const char* b_ptr[B_ITEMS];
+    constexpr int BES = B_F16 ? 2 : 4;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      a_ptr[it] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + kq;
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      const int flat = tid + 256 * it;
+      if constexpr (B_NK) {
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)min(n0 + row, p.N - 1) * p.ldb + kq) * BES;
+      } else {
+        const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+        const int gn = n0 + nq < p.N ? n0 + nq : 0;
+        b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)k * p.ldb + gn) * BES;
+      }
+    }
+    auto load_fast = [&](auto sc, int k0) {
+      constexpr int S = decltype(sc)::value;
+      const int kc = min(k0, kend - BK);
+#pragma unroll
+      for (int it = 0; it < A_ITEMS; ++it) ra_set[S][it] = *reinterpret_cast<const floatx4*>(a_ptr[it] + kc);
+      const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
+#pragma unroll
+      for (int it = 0; it < B_ITEMS; ++it) {
+        if constexpr (B_F16) rb_set[S][it] = widen4(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
+        else rb_set[S][it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
+      }
+    };
+    auto store_fast = [&](auto sc, int k0) {
+      constexpr int S = decltype(sc)::value;
+      float* As = smem + S * STAGE;
+      float* Bs = As + A_STAGE;
+      // A panel past kend (only multiplied when nk is odd) is stored as
+      // zeros; the scale keeps this a multiply, not a per-element select.
+      const float keep = k0 >= kend ? 0.f : 1.f;
+#pragma unroll
+      for (int it = 0; it < A_ITEMS; ++it) {
+        const int flat = tid + 256 * it;
+        const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+        *reinterpret_cast<floatx4*>(&As[row * PA + kq]) = ra_set[S][it] * keep;
+      }
+#pragma unroll
+      for (int it = 0; it < B_ITEMS; ++it) {
+        const int flat = tid + 256 * it;
+        const floatx4 v = rb_set[S][it];
+        if constexpr (B_NK) {
+          const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+          *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = v;
+        } else {
+          const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+          *reinterpret_cast<floatx4*>(&Bs[k * PB + nq]) = v;
+        }
+      }
+    };
+    auto step_fast = [&](auto sc, int kt) {
+      using SN = std::integral_constant<int, 1 - decltype(sc)::value>;
+      load_fast(sc, kbeg + (kt + 2) * BK);
+      compute(sc);
+      store_fast(SN{}, kbeg + (kt + 1) * BK);
+      __builtin_amdgcn_sched_group_barrier(0x100, N_DSR, 0);
+#pragma unroll
+      for (int i = 0; i < N_VMEM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < N_VMEM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA - 2 * N_VMEM, 0);
+      __syncthreads();
+    };
+    if (nk > 0) {
+      load_fast(I0{}, kbeg);
+      load_fast(I1{}, kbeg + BK);
+      store_fast(I0{}, kbeg);
+      __syncthreads();
+      for (int kt = 0; kt < nk; kt += 2) {
+        step_fast(I0{}, kt);
+        step_fast(I1{}, kt + 1);
+      }
+    }
+  } else {
+    if (nk > 0) load_panel(I0{}, kbeg);
+    if (nk > 1) load_panel(I1{}, kbeg + BK);
+    if (nk > 0) store_panel(I0{}, kbeg);
+    __syncthreads();
+    // Both steps run unconditionally (no control flow inside the loop body,
+    // so the staged registers need no copies at a merge point): when nk is
+    // odd the last step multiplies a panel past kend, which the tail mask
+    // zeroed.
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(I0{}, kt);
+      step(I1{}, kt + 1);
+    }
   }
 
   // Rank-r LoRA term: one more K panel of depth r (padded to a multiple of

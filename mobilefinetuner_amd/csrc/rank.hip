@@ -3,10 +3,10 @@
 //   rank_proj:  out[M,r] = X[M,K] · Y          (xa = x·Aᵀ, U = dy·B)
 //   rank_outer: out(j,c) (+)= s · Σ_m P[m,j] X[m,c]   (dA = s·Uᵀx, dB = s·dyᵀxa)
 //
-// Both are HBM/latency-bound passes over X (2–16 MB at the benchmark
-// shapes).  rank_proj gives each wave two rows and has every lane stream
-// 128-bit chunks of K, so a wave keeps ~20 independent 16-byte loads in
-// flight; the r×K (or K×r) factor is re-read from L1/L2.  rank_outer runs on
+// Both are HBM/latency-bound passes over X (2–28 MB at the benchmark
+// shapes).  rank_proj spreads each row's K over a whole workgroup (128-bit
+// chunks, the r×K or K×r factor re-read from L1/L2) and reduces by
+// recursive halving; rank_outer runs on
 // the matrix cores, one launch for both gradients of a layer, with M split
 // over the waves of a workgroup and summed in wave order (deterministic, no
 // atomics, no second pass).
@@ -17,38 +17,61 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 namespace mft {
 namespace {
 
-constexpr int RW = 2;  // rows per wave in rank_proj
+// Reduce NV per-lane partial sums over a wave64 by recursive halving: at
+// offset o each lane keeps one half of its values and adds the partner's
+// copy of that half, so a wave needs NV-1 + log2(64/NV) shuffles instead of
+// 6·NV.  Afterwards lane l holds the wave total of value l / (64/NV).
+template <int NV>
+__device__ __forceinline__ float wave_reduce_spread(float (&v)[NV], int lane) {
+  static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "NV must be a power of two <= 64");
+  int o = 32;
+#pragma unroll
+  for (int half = NV / 2; half >= 1; half /= 2, o /= 2) {
+    const bool up = (lane & o) != 0;
+#pragma unroll
+    for (int q = 0; q < half; ++q) {
+      const float send = up ? v[q] : v[q + half];
+      const float keep = up ? v[q + half] : v[q];
+      v[q] = keep + __shfl_xor(send, o, 64);
+    }
+  }
+  float t = v[0];
+#pragma unroll
+  for (; o >= 1; o /= 2) t += __shfl_xor(t, o, 64);
+  return t;
+}
 
-// Y_RK: Y stored [R][K] (row j contiguous in k)  — xa = x·Aᵀ with A [r,K]
-// Y_KR: Y stored [K][R] (row k contiguous in j)  — U = dy·B with B [N,r]
-template <int R, bool Y_RK>
-__global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restrict__ X,
-                                                             int64_t ldx,
-                                                             const float* __restrict__ Y,
-                                                             int M, int K,
+// out[m, j] = Σ_k X[m,k]·Y(k,j) for RB rows per 256-thread workgroup; every
+// thread takes 128-bit chunks of K for all RB rows (so X is streamed once,
+// ~256 workgroups at M = 512–1024), the RB·R partial sums are reduced
+// within each wave by recursive halving and across the four waves in LDS.
+// Y_RK: Y stored [R][K] (xa = x·Aᵀ with A [r,K]); otherwise [K][R]
+// (U = dy·B with B [N,r]).
+template <int R, int RB, bool Y_RK>
+__global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restrict__ X, int64_t ldx,
+                                                             const float* __restrict__ Y, int M, int K,
                                                              float* __restrict__ out) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int m0 = (blockIdx.x * 4 + wave) * RW;
-  if (m0 >= M) return;
-  float acc[RW][R];
+  constexpr int NV = RB * R;
+  __shared__ float red[4][NV];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.x * RB;
+  float acc[NV];
 #pragma unroll
-  for (int i = 0; i < RW; ++i)
+  for (int q = 0; q < NV; ++q) acc[q] = 0.f;
+  for (int k = tid * 4; k < K; k += 1024) {
+    floatx4 xv[RB];
 #pragma unroll
-    for (int j = 0; j < R; ++j) acc[i][j] = 0.f;
-  const bool two = m0 + 1 < M;
-#pragma unroll 2
-  for (int k = lane * 4; k < K; k += 256) {
-    floatx4 xv[RW];
-    xv[0] = *reinterpret_cast<const floatx4*>(X + (int64_t)m0 * ldx + k);
-    xv[1] = two ? *reinterpret_cast<const floatx4*>(X + (int64_t)(m0 + 1) * ldx + k)
-                : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < RB; ++i) {
+      const int m = min(m0 + i, M - 1);
+      xv[i] = *reinterpret_cast<const floatx4*>(X + (int64_t)m * ldx + k);
+    }
     if constexpr (Y_RK) {
 #pragma unroll
       for (int j = 0; j < R; ++j) {
         const floatx4 y = *reinterpret_cast<const floatx4*>(Y + (int64_t)j * K + k);
 #pragma unroll
-        for (int i = 0; i < RW; ++i)
-          acc[i][j] += xv[i][0] * y[0] + xv[i][1] * y[1] + xv[i][2] * y[2] + xv[i][3] * y[3];
+        for (int i = 0; i < RB; ++i)
+          acc[i * R + j] += xv[i][0] * y[0] + xv[i][1] * y[1] + xv[i][2] * y[2] + xv[i][3] * y[3];
       }
     } else {
       const float* yk = Y + (int64_t)k * R;
@@ -58,31 +81,20 @@ __global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restr
         for (int jq = 0; jq < R / 4; ++jq) {
           const floatx4 y = *reinterpret_cast<const floatx4*>(yk + e * R + 4 * jq);
 #pragma unroll
-          for (int i = 0; i < RW; ++i)
+          for (int i = 0; i < RB; ++i)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[i][4 * jq + u] = fmaf(xv[i][e], y[u], acc[i][4 * jq + u]);
+            for (int u = 0; u < 4; ++u) acc[i * R + 4 * jq + u] = fmaf(xv[i][e], y[u], acc[i * R + 4 * jq + u]);
         }
     }
   }
-#pragma unroll
-  for (int i = 0; i < RW; ++i)
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      float v = acc[i][j];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      acc[i][j] = v;
-    }
-  if (lane < R) {
-#pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      if (m0 + i >= M) break;
-      float v = 0.f;
-#pragma unroll
-      for (int j = 0; j < R; ++j)
-        if (j == lane) v = acc[i][j];
-      out[(int64_t)(m0 + i) * R + lane] = v;
-    }
+  const float t = wave_reduce_spread<NV>(acc, lane);
+  constexpr int SPREAD = 64 / NV;
+  if ((lane % SPREAD) == 0) red[wave][lane / SPREAD] = t;
+  __syncthreads();
+  if (tid < NV) {
+    const int i = tid / R, j = tid % R;
+    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (m0 + i < M) out[(int64_t)(m0 + i) * R + j] = v;
   }
 }
 
@@ -206,12 +218,26 @@ __global__ __launch_bounds__(512) void rank_outer_mfma(OuterArgs a) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-template <int R>
+template <int R, int RB>
 void proj_vec(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y_rk, int M, int K,
               float* out) {
-  dim3 grid((unsigned)cdiv(M, 4 * RW)), block(256);
-  if (y_rk) hipLaunchKernelGGL((rank_proj_vec_kernel<R, true>), grid, block, 0, s, X, ldx, Y, M, K, out);
-  else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
+  const dim3 grid((unsigned)cdiv(M, RB)), block(256);
+  if (y_rk) hipLaunchKernelGGL((rank_proj_vec_kernel<R, RB, true>), grid, block, 0, s, X, ldx, Y, M, K, out);
+  else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, RB, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
+}
+
+// Rows per workgroup: about 256 workgroups, at most 64 partial sums per lane.
+template <int R>
+void proj_vec_rows(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y_rk, int M, int K,
+                   float* out) {
+  const int rb = M >= 1024 ? 4 : M >= 512 ? 2 : 1;
+  if constexpr (4 * R <= 64) {
+    if (rb == 4) return proj_vec<R, 4>(s, X, ldx, Y, y_rk, M, K, out);
+  }
+  if constexpr (2 * R <= 64) {
+    if (rb >= 2) return proj_vec<R, 2>(s, X, ldx, Y, y_rk, M, K, out);
+  }
+  proj_vec<R, 1>(s, X, ldx, Y, y_rk, M, K, out);
 }
 
 void outer_launch(hipStream_t s, OuterArgs& a) {
@@ -231,12 +257,13 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64
   MFT_CHECK_ARG(M > 0 && K > 0, "empty");
   const bool y_rk = ysk == 1 && ysj == K;
   const bool y_kr = ysj == 1 && ysk == r;
-  const bool vec = (r == 4 || r == 8 || r == 16) && (y_rk || y_kr) && K % 4 == 0 && ldx % 4 == 0 &&
+  const bool vec = (r == 4 || r == 8 || r == 16 || r == 32) && (y_rk || y_kr) && K % 4 == 0 && ldx % 4 == 0 &&
                    aligned16(X) && aligned16(Y);
   if (vec) {
-    if (r == 4) proj_vec<4>(s, X, ldx, Y, y_rk, M, K, out);
-    else if (r == 8) proj_vec<8>(s, X, ldx, Y, y_rk, M, K, out);
-    else proj_vec<16>(s, X, ldx, Y, y_rk, M, K, out);
+    if (r == 4) proj_vec_rows<4>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 8) proj_vec_rows<8>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 16) proj_vec_rows<16>(s, X, ldx, Y, y_rk, M, K, out);
+    else proj_vec_rows<32>(s, X, ldx, Y, y_rk, M, K, out);
   } else {
     dim3 grid((unsigned)cdiv(M, 4)), block(256);
     if (r <= 8)       hipLaunchKernelGGL(rank_proj_scalar_kernel<8>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
