@@ -386,9 +386,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 // through two register sets and a two-stage LDS ring exactly like
 // gemm_kernel; the small register and LDS footprint allows four resident
 // workgroups per CU.
-template <int BK, bool B_NK, bool B_F16, int SITE>
+template <int BM, int BK, bool B_NK, bool B_F16, int SITE>
 __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
-  constexpr int BM = 64, BN = 64;
+  constexpr int BN = 64;
+  constexpr int WA = BM / 32;  // 16-row MFMA tiles per wave (waves are 2 × 2)
   constexpr int PA = BK + 4;
   constexpr int PB = B_NK ? BK + 4 : BN + 4;
   constexpr int A_ITEMS = BM * BK / 4 / 256;
@@ -412,12 +413,12 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+  const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * 32;
   const int li = lane & 15, lg = lane >> 4;
 
-  floatx4 acc[2][2];
+  floatx4 acc[WA][2];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < WA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
@@ -500,9 +501,9 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     const float* bs = as + A_STAGE;
 #pragma unroll
     for (int kb = 0; kb < BK; kb += 16) {
-      floatx4 fa[2], fb[2];
+      floatx4 fa[WA], fb[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) fa[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
+      for (int a = 0; a < WA; ++a) fa[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int col = wn + 16 * b + li;
@@ -516,14 +517,14 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < WA; ++a)
 #pragma unroll
           for (int b = 0; b < 2; ++b)
             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a][t], fb[b][t], acc[a][b], 0, 0, 0);
     }
   };
-  constexpr int N_DSR = (BK / 16) * (2 + (B_NK ? 2 : 8));
-  constexpr int N_MFMA = (BK / 16) * 16;
+  constexpr int N_DSR = (BK / 16) * (WA + (B_NK ? 2 : 8));
+  constexpr int N_MFMA = (BK / 16) * 8 * WA;
   constexpr int N_VMEM = A_ITEMS + B_ITEMS;
   static_assert(N_MFMA >= 2 * N_VMEM, "schedule");
   auto step = [&](auto sc, int kt) {
@@ -671,13 +672,13 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     }
     __syncthreads();
     for (int t = 0; t < rp / 4; ++t) {
-      float fp[2], fq[2];
+      float fp[WA], fq[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
+      for (int a = 0; a < WA; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
 #pragma unroll
       for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + 16 * b + li) * pr + 4 * t + lg];
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < WA; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fp[a], fq[b], acc[a][b], 0, 0, 0);
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 
   const bool split_out = p.partial != nullptr;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < WA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int n = n0 + wn + 16 * b + li;
@@ -703,15 +704,30 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     }
 }
 
-__global__ void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M, int N,
-                                     float* C, int64_t ldc, GemmEpilogue ep) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Sum of the split-K partials in split order plus the epilogue.  Rows are
+// blockIdx.y; each thread takes four consecutive columns (128-bit partial
+// loads when N is a multiple of 4).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int splits,
+                                                            int M, int N, float* C, int64_t ldc,
+                                                            GemmEpilogue ep) {
+  const int n0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n0 >= N) return;
   const int64_t total = (int64_t)M * N;
-  if (idx >= total) return;
-  const int m = (int)(idx / N), n = (int)(idx % N);
-  float s = 0.f;
-  for (int z = 0; z < splits; ++z) s += partial[(int64_t)z * total + idx];
-  C[(int64_t)m * ldc + n] = epilogue_value(ep, s, m, n, C, ldc);
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const float* src = partial + (int64_t)m * N + n0;
+    if ((N & 3) == 0) {
+      floatx4 s = *reinterpret_cast<const floatx4*>(src);
+      for (int z = 1; z < splits; ++z) s += *reinterpret_cast<const floatx4*>(src + (int64_t)z * total);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) C[(int64_t)m * ldc + n0 + e] = epilogue_value(ep, s[e], m, n0 + e, C, ldc);
+    } else {
+      for (int e = 0; e < 4 && n0 + e < N; ++e) {
+        float s = 0.f;
+        for (int z = 0; z < splits; ++z) s += src[(int64_t)z * total + e];
+        C[(int64_t)m * ldc + n0 + e] = epilogue_value(ep, s, m, n0 + e, C, ldc);
+      }
+    }
+  }
 }
 
 template <int BM, int BN, int BK, int SITE>
@@ -726,27 +742,27 @@ void launch_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bo
   }
 }
 
-template <int BK, int SITE>
+template <int BM, int BK, int SITE>
 void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BK, true, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_q_kernel<BK, true, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BM, BK, true, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_q_kernel<BM, BK, true, false, SITE>), grid, block, 0, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BK, false, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_q_kernel<BK, false, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BM, BK, false, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_q_kernel<BM, BK, false, false, SITE>), grid, block, 0, s, p);
   }
 }
 
-template <int BK>
+template <int BM, int BK>
 void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
-  p.tiles_m = (int)cdiv(p.M, 64);
+  p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, 64);
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   const dim3 grid(p.tiles_per_xcd * 8, splits);
-  if (p.ep.site == 1) launch_q_variant<BK, 1>(s, p, grid, b_nk, b_f16);
-  else launch_q_variant<BK, 0>(s, p, grid, b_nk, b_f16);
+  if (p.ep.site == 1) launch_q_variant<BM, BK, 1>(s, p, grid, b_nk, b_f16);
+  else launch_q_variant<BM, BK, 0>(s, p, grid, b_nk, b_f16);
   MFT_LAUNCH_CHECK();
 }
 
@@ -770,14 +786,17 @@ struct Plan {
 
 int plan_bk(int bm, int bn) { return (bm == 64 && (bn == 64 || bn == 1)) ? 64 : 32; }
 
-// Tile shape and split-K, from sweeps of the benchmark shapes on MI355X:
-// 64×64 tiles (two resident workgroups per CU), with split-K doubled while
-// the grid has fewer than 512 workgroups (two per CU) and every split keeps
-// at least 512 of K; very large grids (the LM head over the vocabulary) use
-// 128×128 tiles, which halve the operand traffic per FLOP.
+// Tile shape and split-K, from sweeps of the benchmark shapes on MI355X
+// (M = 512 tokens): grids of ≥ 512 64×64 tiles run unsplit; smaller grids
+// with K < 2048 switch to 32×64 tiles (twice the workgroups, no partials);
+// deeper K keeps 64×64 tiles and doubles split-K while the grid has fewer
+// than 512 workgroups and every split keeps at least 512 of K.  Very large
+// grids (the LM head over the vocabulary) use the 128×128 kernel.
 Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
   if (cdiv(M, 128) * cdiv(N, 128) >= 1024) return {128, 128, 1};
   const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
+  if (tiles >= 512) return {64, 0, 1};
+  if (K < 2048) return {32, 0, 1};
   int sp = 1;
   while (tiles * sp < 512 && K / (2 * sp) >= 512 && sp < 8 &&
          (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
@@ -831,7 +850,7 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
     int bm = 0, bn = 0, sp = 0;
     if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
-         (bm == 64 && (bn == 0 || bn == 1))) &&
+         ((bm == 64 && (bn == 0 || bn == 1)) || (bm == 32 && bn == 0))) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
@@ -845,13 +864,13 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 128) launch_tile<64, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 64) launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
-  else if (pl.bn == 1) launch_q<64>(s, p, b_nk, b_f16, splits);
-  else launch_q<32>(s, p, b_nk, b_f16, splits);
+  else if (pl.bn == 1) launch_q<64, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bm == 32) launch_q<32, 32>(s, p, b_nk, b_f16, splits);
+  else launch_q<64, 32>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
 
   if (splits > 1) {
-    const int64_t total = (int64_t)M * N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256), 0, s,
                        (const float*)ws.ptr, splits, M, N, C, ldc, ep);
     MFT_LAUNCH_CHECK();
   }
