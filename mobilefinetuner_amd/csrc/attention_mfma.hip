@@ -24,6 +24,8 @@
 //   dQ kernel — per wave 16 queries; Sᵀ, dPᵀ transposed as in the forward so
 //     dS feeds dQ += dS·K from registers.
 // P is recomputed from the saved lse in both backward kernels.
+#include <cstdlib>
+
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -110,9 +112,12 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y, b = blockIdx.z;
+  // 1-D grid, heaviest causal query blocks (the last ones) first.
+  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int nqb = (p.S + 16 * NW - 1) / (16 * NW);
   const int kh = h / (p.Hq / p.Hkv);
-  const int q0 = blockIdx.x * 16 * NW;
+  const int q0 = (nqb - 1 - (int)blockIdx.x / (p.Hq * p.B)) * 16 * NW;
   const int qbase = q0 + 16 * w;
   const int qi = qbase + li;  // this lane's query
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
@@ -269,10 +274,12 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   // One workgroup per (key block, QUERY head): a GQA group's query heads
   // run in parallel and their dK/dV contributions are summed afterwards by
   // attn_group_sum_kernel in head order.
-  const int h = blockIdx.y, b = blockIdx.z;
+  // 1-D grid, heaviest causal key blocks (the first ones) first.
+  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
   const int grp = p.Hq / p.Hkv;
   const int kh = h / grp;
-  const int k0 = blockIdx.x * BKEYS;
+  const int k0 = ((int)blockIdx.x / (p.Hq * p.B)) * BKEYS;
   const int kbase = k0 + 16 * w;
   const int kj = kbase + li;  // this lane's key (as S column)
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
@@ -407,9 +414,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int nqb = (p.S + 16 * NW - 1) / (16 * NW);
   const int kh = h / (p.Hq / p.Hkv);
-  const int q0 = blockIdx.x * 16 * NW;
+  const int q0 = (nqb - 1 - (int)blockIdx.x / (p.Hq * p.B)) * 16 * NW;
   const int qbase = q0 + 16 * w;
   const int qi = qbase + li;
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
@@ -508,7 +517,7 @@ void fwd_launch(hipStream_t s, AttnP& p) {
   const size_t lds = sizeof(float) * std::max<size_t>(2 * BKV * P + BKV, 16 * NW * P);
   auto kern = attn_fwd_mfma<HD, NW, BKV>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
 }
@@ -520,7 +529,7 @@ void dkdv_launch(hipStream_t s, AttnP& p) {
   const size_t lds = sizeof(float) * (2 * 16 * NW * P + 2 * BQ * P + 2 * BQ + 16 * NW);
   auto kern = attn_bwd_dkdv_mfma<HD, NW, BQ>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
 }
@@ -532,19 +541,23 @@ void dq_launch(hipStream_t s, AttnP& p) {
   const size_t lds = sizeof(float) * (2 * BKV * P + BKV);
   auto kern = attn_bwd_dq_mfma<HD, NW, BKV>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)cdiv(p.S, 16 * NW), p.Hq, p.B);
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
 }
 
-// Waves per workgroup (16 queries or keys each): the widest that still gives
-// at least two workgroups per CU over the (S-blocks × Hq × B) grid.
+// Waves per workgroup (16 queries or keys each): four (two at head_dim 256,
+// for LDS) — the waves of a workgroup share every staged K/V (or Q/dO)
+// block, and with the heavy-first 1-D grid this measured fastest at
+// S = 128–1024 on MI355X.
 int pick_nw(const AttnArgs& a) {
-  for (int nw : {4, 2}) {
-    if (a.hd == 256 && nw == 4) continue;  // LDS budget at head_dim 256
-    if (cdiv(a.S, 16 * nw) * a.Hq * a.B >= 512) return nw;
+  // Tuning hook: MFT_ATTN_NW = 1, 2 or 4 waves per workgroup (4 not at hd 256).
+  static const char* forced = getenv("MFT_ATTN_NW");
+  if (forced) {
+    const int nw = atoi(forced);
+    if (nw == 1 || nw == 2 || (nw == 4 && a.hd != 256)) return nw;
   }
-  return 1;
+  return a.hd == 256 ? 2 : 4;
 }
 
 template <int HD>

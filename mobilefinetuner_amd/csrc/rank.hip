@@ -42,9 +42,9 @@ __device__ __forceinline__ float wave_reduce_spread(float (&v)[NV], int lane) {
 }
 
 // out[m, j] = Σ_k X[m,k]·Y(k,j) for RB rows per 256-thread workgroup; every
-// thread takes 128-bit chunks of K for all RB rows (so X is streamed once,
-// ~256 workgroups at M = 512–1024), the RB·R partial sums are reduced
-// within each wave by recursive halving and across the four waves in LDS.
+// thread takes 128-bit chunks of K for all RB rows (so X is streamed once),
+// the RB·R partial sums are reduced within each wave by recursive halving
+// and across the four waves in LDS.
 // Y_RK: Y stored [R][K] (xa = x·Aᵀ with A [r,K]); otherwise [K][R]
 // (U = dy·B with B [N,r]).
 template <int R, int RB, bool Y_RK>
@@ -226,20 +226,6 @@ void proj_vec(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y
   else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, RB, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
 }
 
-// Rows per workgroup: about 256 workgroups, at most 64 partial sums per lane.
-template <int R>
-void proj_vec_rows(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y_rk, int M, int K,
-                   float* out) {
-  const int rb = M >= 1024 ? 4 : M >= 512 ? 2 : 1;
-  if constexpr (4 * R <= 64) {
-    if (rb == 4) return proj_vec<R, 4>(s, X, ldx, Y, y_rk, M, K, out);
-  }
-  if constexpr (2 * R <= 64) {
-    if (rb >= 2) return proj_vec<R, 2>(s, X, ldx, Y, y_rk, M, K, out);
-  }
-  proj_vec<R, 1>(s, X, ldx, Y, y_rk, M, K, out);
-}
-
 void outer_launch(hipStream_t s, OuterArgs& a) {
   a.job[0].blocks = (int)cdiv(a.job[0].C, 16);
   a.job[1].blocks = a.job[1].out ? (int)cdiv(a.job[1].C, 16) : 0;
@@ -260,10 +246,11 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64
   const bool vec = (r == 4 || r == 8 || r == 16 || r == 32) && (y_rk || y_kr) && K % 4 == 0 && ldx % 4 == 0 &&
                    aligned16(X) && aligned16(Y);
   if (vec) {
-    if (r == 4) proj_vec_rows<4>(s, X, ldx, Y, y_rk, M, K, out);
-    else if (r == 8) proj_vec_rows<8>(s, X, ldx, Y, y_rk, M, K, out);
-    else if (r == 16) proj_vec_rows<16>(s, X, ldx, Y, y_rk, M, K, out);
-    else proj_vec_rows<32>(s, X, ldx, Y, y_rk, M, K, out);
+    // one row per workgroup (measured fastest at M = 512–1024 for r = 8)
+    if (r == 4) proj_vec<4, 1>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 8) proj_vec<8, 1>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 16) proj_vec<16, 1>(s, X, ldx, Y, y_rk, M, K, out);
+    else proj_vec<32, 1>(s, X, ldx, Y, y_rk, M, K, out);
   } else {
     dim3 grid((unsigned)cdiv(M, 4)), block(256);
     if (r <= 8)       hipLaunchKernelGGL(rank_proj_scalar_kernel<8>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
