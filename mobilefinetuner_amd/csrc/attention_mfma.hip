@@ -49,24 +49,50 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bool visible(const AttnP& p, int i, int j, const float* kp) {
-  if (j >= p.S || i >= p.S) return false;
-  if (p.causal && j > i) return false;
-  if (p.window > 0 && i - j >= p.window) return false;
-  if (kp && !(kp[j] > 0.5f)) return false;
-  return true;
-}
 
 // Stage rows [r0, r0+ROWS) of two token-major [.., S, H, HD] tensors (head
-// h) into LDS with pitch HD+4; rows past S are zero.  Branch-free: row
-// indices are clamped into the tensor and the values selected to zero, and
-// each thread issues a batch of CH loads per tensor before any LDS store, so
-// a block's loads are in flight together instead of one latency per element.
-template <int HD, int NT, int ROWS>
-__device__ __forceinline__ void stage_pair(float* lds1, const float* src1, int64_t rs1, float* lds2,
+// h1 / h2) into LDS; rows past S are zero.  Each tensor is stored row-major
+// (dst[r][d], pitch HD+4: conflict-free 128-bit row reads), transposed
+// (dst[d][r], pitch ROWS+4: one 128-bit read returns four consecutive rows
+// of one column, the operand order of a product that reduces over rows), or
+// both.  Row-major-only items give a wave whole rows; a tensor with a
+// transposed copy gives 16 consecutive lanes 16 consecutive rows of one
+// 4-column group, so the wave's scalar transposed stores land in 64 distinct
+// banks and its 128-bit row stores in distinct bank groups.  Branch-free:
+// row indices are clamped into the tensor and the values selected to zero,
+// and each thread issues a batch of CH loads per tensor before any LDS store.
+struct StageDst {
+  float* row;  // [ROWS][HD+4] or unused
+  float* trn;  // [HD][ROWS+4] or unused
+};
+
+template <int HD, int ROWS, bool T>
+__device__ __forceinline__ void stage_item(int f, int& r, int& c4) {
+  if constexpr (T) {
+    r = ((f >> 4) / (HD / 4)) * 16 + (f & 15);
+    c4 = (f >> 4) % (HD / 4);
+  } else {
+    r = f / (HD / 4);
+    c4 = f % (HD / 4);
+  }
+}
+
+template <int HD, int ROWS, bool R, bool T>
+__device__ __forceinline__ void stage_store(const StageDst& d, int r, int c4, bool ok, const floatx4& v) {
+  const floatx4 x = ok ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (R) *reinterpret_cast<floatx4*>(d.row + r * (HD + 4) + 4 * c4) = x;
+  if constexpr (T) {
+    constexpr int PT = ROWS + 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d.trn[(4 * c4 + e) * PT + r] = x[e];
+  }
+}
+
+template <int HD, int NT, int ROWS, bool R1, bool T1, bool R2, bool T2>
+__device__ __forceinline__ void stage_pair(StageDst d1, const float* src1, int64_t rs1, StageDst d2,
                                            const float* src2, int64_t rs2, int b, int S, int h1, int h2,
                                            int r0, int tid) {
-  constexpr int P = HD + 4;
+  static_assert(!(T1 || T2) || ROWS % 16 == 0, "transposed staging takes 16-row groups");
   constexpr int TOTAL = ROWS * (HD / 4);
   static_assert(TOTAL % NT == 0, "staging shape");
   constexpr int ITEMS = TOTAL / NT;
@@ -78,23 +104,30 @@ __device__ __forceinline__ void stage_pair(float* lds1, const float* src1, int64
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int f = tid + NT * (base + c);
-      const int r = f / (HD / 4), c4 = f % (HD / 4);
-      const int gr = min(r0 + r, S - 1);
-      const int64_t row = (int64_t)b * S + gr;
-      v1[c] = *reinterpret_cast<const floatx4*>(src1 + row * rs1 + (int64_t)h1 * HD + 4 * c4);
-      v2[c] = *reinterpret_cast<const floatx4*>(src2 + row * rs2 + (int64_t)h2 * HD + 4 * c4);
+      int r, c4;
+      stage_item<HD, ROWS, T1>(f, r, c4);
+      const int64_t row1 = (int64_t)b * S + min(r0 + r, S - 1);
+      v1[c] = *reinterpret_cast<const floatx4*>(src1 + row1 * rs1 + (int64_t)h1 * HD + 4 * c4);
+      stage_item<HD, ROWS, T2>(f, r, c4);
+      const int64_t row2 = (int64_t)b * S + min(r0 + r, S - 1);
+      v2[c] = *reinterpret_cast<const floatx4*>(src2 + row2 * rs2 + (int64_t)h2 * HD + 4 * c4);
     }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int f = tid + NT * (base + c);
-      const int r = f / (HD / 4), c4 = f % (HD / 4);
-      const bool ok = r0 + r < S;
-      const floatx4 z = floatx4{0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<floatx4*>(lds1 + r * P + 4 * c4) = ok ? v1[c] : z;
-      *reinterpret_cast<floatx4*>(lds2 + r * P + 4 * c4) = ok ? v2[c] : z;
+      int r, c4;
+      stage_item<HD, ROWS, T1>(f, r, c4);
+      stage_store<HD, ROWS, R1, T1>(d1, r, c4, r0 + r < S, v1[c]);
+      stage_item<HD, ROWS, T2>(f, r, c4);
+      stage_store<HD, ROWS, R2, T2>(d2, r, c4, r0 + r < S, v2[c]);
     }
   }
 }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ------------------------------------------------------------------------------
 // Forward
@@ -102,15 +135,17 @@ __device__ __forceinline__ void stage_pair(float* lds1, const float* src1, int64
 template <int HD, int NW, int BKV>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
-  constexpr int P = HD + 4;
+  constexpr int P = HD + 4;     // K row pitch
+  constexpr int PV = BKV + 4;   // Vᵀ pitch
   constexpr int NC = HD / 16;   // 16-wide slices of head_dim
   constexpr int KT = BKV / 16;  // key tiles per block
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* Ks = smem;            // [BKV][P]
-  float* Vs = Ks + BKV * P;    // [BKV][P]
-  float* Kp = Vs + BKV * P;    // [BKV] key-padding flags
+  float* Vt = Ks + BKV * P;    // [HD][PV]  (V transposed)
+  float* Kp = Vt + HD * PV;    // [BKV] key-padding flags
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
   // 1-D grid, heaviest causal query blocks (the last ones) first.
   const int hb = blockIdx.x % (p.Hq * p.B);
@@ -122,16 +157,22 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   const int qi = qbase + li;  // this lane's query
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
 
+  // Q carries scale·log2(e), so scores come out in base-2 units and the
+  // softmax exponentials are single v_exp_f32.
+  const float qscale = p.scale * kLog2e;
   floatx4 qreg[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
     qreg[c] = qi < p.S ? *reinterpret_cast<const floatx4*>(p.q + ((int64_t)b * p.S + qi) * p.q_rs +
-                                                          (int64_t)h * HD + 16 * c + 4 * lg)
+                                                          (int64_t)h * HD + 16 * c + 4 * lg) * qscale
                        : floatx4{0.f, 0.f, 0.f, 0.f};
   floatx4 oacc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   float mrow = -INFINITY, lrow = 0.f;
+  // keys visible to this lane's query: [jlo, jhi]
+  const int jhi = qi < p.S ? (p.causal ? qi : p.S - 1) : -1;
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
 
   const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
   const int jmax = p.causal ? qlast_wg : p.S - 1;
@@ -139,13 +180,13 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
-    stage_pair<HD, NT, BKV>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, j0, tid);
-    if (kpb)
-      for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S ? kpb[j0 + j] : 0.f;
+    stage_pair<HD, NT, BKV, true, false, false, true>({Ks, nullptr}, p.k, p.k_rs, {nullptr, Vt}, p.v, p.v_rs, b, p.S,
+                                                      kh, kh, j0, tid);
+    for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S && (!kpb || kpb[j0 + j] > 0.5f) ? 1.f : 0.f;
     __syncthreads();
     if (qbase > p.S - 1) continue;
-    // skip tiles this wave cannot see
-    floatx4 sacc[KT];
+    // Tiles this wave cannot see are skipped (wave-uniform); a block every
+    // key of which is visible to all 16 queries skips the per-element mask.
     bool tile_live[KT];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
@@ -153,8 +194,14 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
       bool live = jt0 < p.S && !(p.causal && jt0 > wave_qlast);
       if (p.window > 0 && wave_qlast - (jt0 + 15) >= p.window + 15) live = false;
       tile_live[kt] = live;
+    }
+    const bool full = !kpb && j0 + BKV <= p.S && qbase + 15 < p.S && (!p.causal || j0 + BKV - 1 <= qbase) &&
+                      (p.window <= 0 || qbase + 15 - j0 < p.window);
+    floatx4 sacc[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
       sacc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (!live) continue;
+      if (!tile_live[kt]) continue;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const floatx4 kv = *reinterpret_cast<const floatx4*>(&Ks[(16 * kt + li) * P + 16 * c + 4 * lg]);
@@ -162,51 +209,56 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
         for (int t = 0; t < 4; ++t) sacc[kt] = mfma4(kv[t], qreg[c][t], sacc[kt]);
       }
     }
-    // lane holds S[q = qi][key = j0 + 16kt + 4lg + v]
+    // lane holds S[q = qi][key = j0 + 16kt + 4lg + v] (base-2 units)
+    if (!full) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const floatx4 kp4 = *reinterpret_cast<const floatx4*>(&Kp[16 * kt + 4 * lg]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int j = j0 + 16 * kt + 4 * lg + v;
+          const bool ok = (j >= jlo) & (j <= jhi) & (kp4[v] > 0.5f);
+          sacc[kt][v] = ok ? sacc[kt][v] : -INFINITY;
+        }
+      }
+    }
     float mloc = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int j = j0 + 16 * kt + 4 * lg + v;
-        const bool ok = tile_live[kt] && visible(p, qi, j, kpb ? Kp - j0 : nullptr);
-        const float sv = ok ? sacc[kt][v] * p.scale : -INFINITY;
-        sacc[kt][v] = sv;
-        mloc = fmaxf(mloc, sv);
-      }
+      for (int v = 0; v < 4; ++v) mloc = fmaxf(mloc, sacc[kt][v]);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     const float mnew = fmaxf(mrow, mloc);
-    float corr = 1.f, lsum = 0.f;
-    if (mnew > -INFINITY) {
-      corr = __expf(mrow - mnew);
+    // With nothing visible yet every score is -inf: referencing 0 keeps the
+    // exponentials at exactly 0 instead of NaN.
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float corr = fast_exp2(mrow - mref);
+    float lsum = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float e = sacc[kt][v] > -INFINITY ? __expf(sacc[kt][v] - mnew) : 0.f;
-          sacc[kt][v] = e;
-          lsum += e;
-        }
-    } else {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) sacc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int v = 0; v < 4; ++v) {
+        const float e = fast_exp2(sacc[kt][v] - mref);
+        sacc[kt][v] = e;
+        lsum += e;
+      }
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     lrow = lrow * corr + lsum;
     mrow = mnew;
 #pragma unroll
     for (int c = 0; c < NC; ++c) oacc[c] *= corr;
-    // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]
+    // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]; lane (i, g) reads Vᵀ[16c+i][16kt+4g .. +3]
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       if (!tile_live[kt]) continue;
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 va = *reinterpret_cast<const floatx4*>(&Vt[(16 * c + li) * PV + 16 * kt + 4 * lg]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          oacc[c] = mfma4(Vs[(16 * kt + 4 * lg + t) * P + 16 * c + li], sacc[kt][t], oacc[c]);
+        for (int t = 0; t < 4; ++t) oacc[c] = mfma4(va[t], sacc[kt][t], oacc[c]);
+      }
     }
   }
   // lane holds Oᵀ[d = 16c + 4lg + v][q = qi]; transpose through LDS for
@@ -218,8 +270,10 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int v = 0; v < 4; ++v) Os[(16 * w + li) * P + 16 * c + 4 * lg + v] = oacc[c][v] * inv;
+  // lse in natural-log units: (m₂ + log₂ l)·ln 2
   if (lg == 0 && qi < p.S)
-    p.lse_out[((int64_t)b * p.Hq + h) * p.S + qi] = lrow > 0.f ? mrow + __logf(lrow) : -INFINITY;
+    p.lse_out[((int64_t)b * p.Hq + h) * p.S + qi] =
+        lrow > 0.f ? (mrow + __builtin_amdgcn_logf(lrow)) * kLn2 : -INFINITY;
   __syncthreads();
   for (int f = tid; f < 16 * NW * (HD / 4); f += NT) {
     const int r = f / (HD / 4), c4 = f % (HD / 4);
@@ -251,25 +305,33 @@ __global__ __launch_bounds__(256) void attn_delta_mfma_kernel(AttnP p) {
 }
 
 // ------------------------------------------------------------------------------
-// dK, dV: workgroup = 16·NW keys of one KV head; wave = 16 keys.
+// dK, dV: workgroup = 16·NW keys of one query head; wave = 16 keys.
 // ------------------------------------------------------------------------------
 template <int HD, int NW, int BQ>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
+  constexpr int PQ = BQ + 4;
   constexpr int NC = HD / 16;
   constexpr int QT = BQ / 16;
   constexpr int BKEYS = 16 * NW;
+  // head_dim ≤ 128: each wave keeps its 16 keys' K/V rows in registers and
+  // Q / dO also get a transposed LDS copy, so every MFMA operand is one
+  // 128-bit read.  head_dim 256 (register and LDS budget): K/V rows stay in
+  // LDS and the dV/dK operands are read by column.
+  constexpr bool WIDE = HD > 128;
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  float* Ks = smem;               // [BKEYS][P]
-  float* Vs = Ks + BKEYS * P;     // [BKEYS][P]
-  float* Qs = Vs + BKEYS * P;     // [BQ][P]
-  float* Gs = Qs + BQ * P;        // [BQ][P]  dO
-  float* Ls = Gs + BQ * P;        // [BQ] lse
-  float* Es = Ls + BQ;            // [BQ] delta
-  float* Kp = Es + BQ;            // [BKEYS]
+  float* Qs = smem;                              // [BQ][P]
+  float* Gs = Qs + BQ * P;                       // [BQ][P]  dO
+  float* Qt = Gs + BQ * P;                       // [HD][PQ] (not WIDE)
+  float* Gt = Qt + (WIDE ? 0 : HD * PQ);         // [HD][PQ] (not WIDE)
+  float* Ks = Gt + (WIDE ? 0 : HD * PQ);         // [BKEYS][P] (WIDE)
+  float* Vs = Ks + (WIDE ? BKEYS * P : 0);       // [BKEYS][P] (WIDE)
+  float* Ls = Vs + (WIDE ? BKEYS * P : 0);       // [BQ] lse·log2(e)
+  float* Es = Ls + BQ;                           // [BQ] delta
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
   // One workgroup per (key block, QUERY head): a GQA group's query heads
   // run in parallel and their dK/dV contributions are summed afterwards by
@@ -283,10 +345,28 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   const int kbase = k0 + 16 * w;
   const int kj = kbase + li;  // this lane's key (as S column)
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  // queries that see this lane's key: [qlo, qhi]
+  const bool kvalid = kj < p.S && (!kpb || kpb[min(kj, p.S - 1)] > 0.5f);
+  const int qlo = p.causal ? kj : 0;
+  const int qhi = !kvalid ? -1 : p.window > 0 ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
 
-  stage_pair<HD, NT, BKEYS>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, k0, tid);
-  if (kpb)
-    for (int j = tid; j < BKEYS; j += NT) Kp[j] = k0 + j < p.S ? kpb[k0 + j] : 0.f;
+  // Scores in base-2 units: the K operand (registers) carries scale·log2(e);
+  // the LDS copy of the WIDE form is scaled at use.
+  const float qk2 = p.scale * kLog2e;
+  const float sc = WIDE ? qk2 : 1.f;
+  floatx4 kreg[WIDE ? 1 : NC], vreg[WIDE ? 1 : NC];
+  if constexpr (WIDE) {
+    stage_pair<HD, NT, BKEYS, true, false, true, false>({Ks, nullptr}, p.k, p.k_rs, {Vs, nullptr}, p.v,
+                                                        p.v_rs, b, p.S, kh, kh, k0, tid);
+  } else {
+    const int64_t row = (int64_t)b * p.S + min(kj, p.S - 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t off = (int64_t)kh * HD + 16 * c + 4 * lg;
+      kreg[c] = *reinterpret_cast<const floatx4*>(p.k + row * p.k_rs + off) * qk2;
+      vreg[c] = *reinterpret_cast<const floatx4*>(p.v + row * p.v_rs + off);
+    }
+  }
 
   floatx4 dkacc[NC], dvacc[NC];
 #pragma unroll
@@ -295,61 +375,83 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   const int klast = min(k0 + BKEYS - 1, p.S - 1);
   const int qstart = p.causal ? k0 : 0;
   const int qend = p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1;
-  {
-    for (int qb0 = (qstart / BQ) * BQ; qb0 <= qend; qb0 += BQ) {
-      __syncthreads();
-      stage_pair<HD, NT, BQ>(Qs, p.q, p.q_rs, Gs, p.dout, p.do_rs, b, p.S, h, h, qb0, tid);
-      for (int e = tid; e < BQ; e += NT) {
-        const int gi = qb0 + e;
-        const int64_t l = ((int64_t)b * p.Hq + h) * p.S + gi;
-        Ls[e] = gi < p.S ? p.lse[l] : -INFINITY;
-        Es[e] = gi < p.S ? p.delta[l] : 0.f;
+  for (int qb0 = (qstart / BQ) * BQ; qb0 <= qend; qb0 += BQ) {
+    __syncthreads();
+    if constexpr (WIDE)
+      stage_pair<HD, NT, BQ, true, false, true, false>({Qs, nullptr}, p.q, p.q_rs, {Gs, nullptr}, p.dout,
+                                                       p.do_rs, b, p.S, h, h, qb0, tid);
+    else
+      stage_pair<HD, NT, BQ, true, true, true, true>({Qs, Qt}, p.q, p.q_rs, {Gs, Gt}, p.dout, p.do_rs, b,
+                                                     p.S, h, h, qb0, tid);
+    for (int e = tid; e < BQ; e += NT) {
+      const int gi = qb0 + e;
+      const int64_t l = ((int64_t)b * p.Hq + h) * p.S + gi;
+      Ls[e] = gi < p.S ? p.lse[l] * kLog2e : 0.f;
+      Es[e] = gi < p.S ? p.delta[l] : 0.f;
+    }
+    __syncthreads();
+    if (kbase > p.S - 1) continue;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int qt0 = qb0 + 16 * qt;
+      if (qt0 > p.S - 1) continue;
+      if (p.causal && qt0 + 15 < kbase) continue;
+      if (p.window > 0 && qt0 - (kbase + 15) >= p.window) continue;
+      // every query of the tile sees every key of the wave
+      const bool full = !kpb && qt0 + 15 < p.S && kbase + 15 < p.S && (!p.causal || qt0 >= kbase + 15) &&
+                        (p.window <= 0 || qt0 + 15 - kbase < p.window);
+      // S[q][key] and dP[q][key]: D[row q = 4lg+v][col key = li]
+      floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 qa = *reinterpret_cast<const floatx4*>(&Qs[(16 * qt + li) * P + 16 * c + 4 * lg]);
+        const floatx4 ga = *reinterpret_cast<const floatx4*>(&Gs[(16 * qt + li) * P + 16 * c + 4 * lg]);
+        floatx4 kb, vb;
+        if constexpr (WIDE) {
+          kb = *reinterpret_cast<const floatx4*>(&Ks[(16 * w + li) * P + 16 * c + 4 * lg]);
+          vb = *reinterpret_cast<const floatx4*>(&Vs[(16 * w + li) * P + 16 * c + 4 * lg]);
+        } else {
+          kb = kreg[c];
+          vb = vreg[c];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          s4 = mfma4(qa[t], kb[t], s4);
+          dp4 = mfma4(ga[t], vb[t], dp4);
+        }
       }
-      __syncthreads();
-      if (kbase > p.S - 1) continue;
+      // P = 2^(S₂ − lse₂); dS/scale = P∘(dP − delta) (scale applied at the end)
+      const floatx4 l4 = *reinterpret_cast<const floatx4*>(&Ls[16 * qt + 4 * lg]);
+      const floatx4 e4 = *reinterpret_cast<const floatx4*>(&Es[16 * qt + 4 * lg]);
+      floatx4 pv, ds;
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int qt0 = qb0 + 16 * qt;
-        if (qt0 > p.S - 1) continue;
-        if (p.causal && qt0 + 15 < kbase) continue;
-        if (p.window > 0 && qt0 - (kbase + 15) >= p.window) continue;
-        // S[q][key] and dP[q][key]: D[row q = 4lg+v][col key = li]
-        floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int v = 0; v < 4; ++v) {
+        const int gi = qt0 + 4 * lg + v;
+        // the mask selects the exponent, so a hidden entry is exactly 0
+        const bool ok = full | ((gi >= qlo) & (gi <= qhi));
+        const float pp = fast_exp2(ok ? fmaf(s4[v], sc, -l4[v]) : -INFINITY);
+        pv[v] = pp;
+        ds[v] = pp * (dp4[v] - e4[v]);
+      }
+      // dV[key][d] += Σ_q P[q][key] dO[q][d];  dK[key][d] += Σ_q dS[q][key] Q[q][d]
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const floatx4 qa = *reinterpret_cast<const floatx4*>(&Qs[(16 * qt + li) * P + 16 * c + 4 * lg]);
-          const floatx4 ga = *reinterpret_cast<const floatx4*>(&Gs[(16 * qt + li) * P + 16 * c + 4 * lg]);
-          const floatx4 kb = *reinterpret_cast<const floatx4*>(&Ks[(16 * w + li) * P + 16 * c + 4 * lg]);
-          const floatx4 vb = *reinterpret_cast<const floatx4*>(&Vs[(16 * w + li) * P + 16 * c + 4 * lg]);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            s4 = mfma4(qa[t], kb[t], s4);
-            dp4 = mfma4(ga[t], vb[t], dp4);
-          }
-        }
-        floatx4 pv, ds;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int qr = 16 * qt + 4 * lg + v;
-          const int gi = qb0 + qr;
-          const float lse = Ls[qr];
-          float pp = 0.f, d = 0.f;
-          if (lse > -INFINITY && visible(p, gi, kj, kpb ? Kp - k0 : nullptr)) {
-            pp = __expf(s4[v] * p.scale - lse);
-            d = pp * (dp4[v] - Es[qr]) * p.scale;
-          }
-          pv[v] = pp;
-          ds[v] = d;
-        }
-        // dV[key][d] += Σ_q P[q][key] dO[q][d];  dK[key][d] += Σ_q dS[q][key] Q[q][d]
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c) {
+        if constexpr (WIDE) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int qr = 16 * qt + 4 * lg + t;
             dvacc[c] = mfma4(pv[t], Gs[qr * P + 16 * c + li], dvacc[c]);
             dkacc[c] = mfma4(ds[t], Qs[qr * P + 16 * c + li], dkacc[c]);
           }
+        } else {
+          const floatx4 gt = *reinterpret_cast<const floatx4*>(&Gt[(16 * c + li) * PQ + 16 * qt + 4 * lg]);
+          const floatx4 qtv = *reinterpret_cast<const floatx4*>(&Qt[(16 * c + li) * PQ + 16 * qt + 4 * lg]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            dvacc[c] = mfma4(pv[t], gt[t], dvacc[c]);
+            dkacc[c] = mfma4(ds[t], qtv[t], dkacc[c]);
+          }
+        }
       }
     }
   }
@@ -365,7 +467,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
     float* dvr = direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      dkr[16 * c + li] = dkacc[c][v];
+      dkr[16 * c + li] = dkacc[c][v] * p.scale;
       dvr[16 * c + li] = dvacc[c][v];
     }
   }
@@ -405,14 +507,20 @@ template <int HD, int NW, int BKV>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
+  constexpr int PK = BKV + 4;
   constexpr int NC = HD / 16;
   constexpr int KT = BKV / 16;
+  // head_dim ≤ 128 also keeps a transposed copy of K for the dQ operand
+  // (one 128-bit read instead of four column reads); 256 reads by column.
+  constexpr bool WIDE = HD > 128;
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  float* Ks = smem;            // [BKV][P]
-  float* Vs = Ks + BKV * P;    // [BKV][P]
-  float* Kp = Vs + BKV * P;    // [BKV]
+  float* Ks = smem;                          // [BKV][P]
+  float* Vs = Ks + BKV * P;                  // [BKV][P]
+  float* Kt = Vs + BKV * P;                  // [HD][PK] (not WIDE)
+  float* Kp = Kt + (WIDE ? 0 : HD * PK);     // [BKV] visible-key flags
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
   const int hb = blockIdx.x % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
@@ -423,34 +531,45 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   const int qi = qbase + li;
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
 
+  // Q carries scale·log2(e): scores in base-2 units against lse·log2(e).
+  const float qscale = p.scale * kLog2e;
   floatx4 qreg[NC], greg[NC], dqacc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int64_t off = (int64_t)h * HD + 16 * c + 4 * lg;
     const bool ok = qi < p.S;
-    qreg[c] = ok ? *reinterpret_cast<const floatx4*>(p.q + ((int64_t)b * p.S + qi) * p.q_rs + off)
+    qreg[c] = ok ? *reinterpret_cast<const floatx4*>(p.q + ((int64_t)b * p.S + qi) * p.q_rs + off) * qscale
                  : floatx4{0.f, 0.f, 0.f, 0.f};
     greg[c] = ok ? *reinterpret_cast<const floatx4*>(p.dout + ((int64_t)b * p.S + qi) * p.do_rs + off)
                  : floatx4{0.f, 0.f, 0.f, 0.f};
     dqacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  float lse = -INFINITY, dlt = 0.f;
+  float lse2 = 0.f, dlt = 0.f;
   if (qi < p.S) {
     const int64_t l = ((int64_t)b * p.Hq + h) * p.S + qi;
-    lse = p.lse[l];
+    lse2 = p.lse[l] * kLog2e;
     dlt = p.delta[l];
   }
+  // keys visible to this lane's query: [jlo, jhi]
+  const int jhi = qi < p.S ? (p.causal ? qi : p.S - 1) : -1;
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
   const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
   const int jmax = p.causal ? qlast_wg : p.S - 1;
   const int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
   const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
-    stage_pair<HD, NT, BKV>(Ks, p.k, p.k_rs, Vs, p.v, p.v_rs, b, p.S, kh, kh, j0, tid);
-    if (kpb)
-      for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S ? kpb[j0 + j] : 0.f;
+    if constexpr (WIDE)
+      stage_pair<HD, NT, BKV, true, false, true, false>({Ks, nullptr}, p.k, p.k_rs, {Vs, nullptr}, p.v,
+                                                        p.v_rs, b, p.S, kh, kh, j0, tid);
+    else
+      stage_pair<HD, NT, BKV, true, true, true, false>({Ks, Kt}, p.k, p.k_rs, {Vs, nullptr}, p.v, p.v_rs, b,
+                                                       p.S, kh, kh, j0, tid);
+    for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S && (!kpb || kpb[j0 + j] > 0.5f) ? 1.f : 0.f;
     __syncthreads();
     if (qbase > p.S - 1) continue;
+    const bool full = !kpb && j0 + BKV <= p.S && qbase + 15 < p.S && (!p.causal || j0 + BKV - 1 <= qbase) &&
+                      (p.window <= 0 || qbase + 15 - j0 < p.window);
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int jt0 = j0 + 16 * kt;
@@ -468,23 +587,30 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
           dp4 = mfma4(va[t], greg[c][t], dp4);
         }
       }
+      // dS/scale = P∘(dP − delta), P = 2^(S₂ − lse₂) (scale applied at the end)
+      const floatx4 kp4 = *reinterpret_cast<const floatx4*>(&Kp[16 * kt + 4 * lg]);
       floatx4 ds;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int j = jt0 + 4 * lg + v;
-        float d = 0.f;
-        if (lse > -INFINITY && visible(p, qi, j, kpb ? Kp - j0 : nullptr)) {
-          const float pp = __expf(s4[v] * p.scale - lse);
-          d = pp * (dp4[v] - dlt) * p.scale;
-        }
-        ds[v] = d;
+        // the mask selects the exponent, so a hidden entry is exactly 0
+        const bool ok = full | ((j >= jlo) & (j <= jhi) & (kp4[v] > 0.5f));
+        const float pp = fast_exp2(ok ? s4[v] - lse2 : -INFINITY);
+        ds[v] = pp * (dp4[v] - dlt);
       }
       // dQ[q][d] += Σ_key dS[q][key] K[key][d]: A = dS (row q = li, k = key 4lg+t)
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c) {
+        if constexpr (WIDE) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          dqacc[c] = mfma4(ds[t], Ks[(16 * kt + 4 * lg + t) * P + 16 * c + li], dqacc[c]);
+          for (int t = 0; t < 4; ++t)
+            dqacc[c] = mfma4(ds[t], Ks[(16 * kt + 4 * lg + t) * P + 16 * c + li], dqacc[c]);
+        } else {
+          const floatx4 kb = *reinterpret_cast<const floatx4*>(&Kt[(16 * c + li) * PK + 16 * kt + 4 * lg]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], kb[t], dqacc[c]);
+        }
+      }
     }
   }
   // lane holds dQ[q = qbase + 4lg + v][d = 16c + li]
@@ -494,7 +620,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
     if (gq >= p.S) continue;
     float* r = p.dq + ((int64_t)b * p.S + gq) * p.dq_rs + (int64_t)h * HD;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) r[16 * c + li] = dqacc[c][v];
+    for (int c = 0; c < NC; ++c) r[16 * c + li] = dqacc[c][v] * p.scale;
   }
 }
 
@@ -514,7 +640,7 @@ template <int HD, int NW>
 void fwd_launch(hipStream_t s, AttnP& p) {
   constexpr int BKV = Cfg<HD>::FBKV;
   constexpr int P = HD + 4;
-  const size_t lds = sizeof(float) * std::max<size_t>(2 * BKV * P + BKV, 16 * NW * P);
+  const size_t lds = sizeof(float) * std::max<size_t>(BKV * P + HD * (BKV + 4) + BKV, 16 * NW * P);
   auto kern = attn_fwd_mfma<HD, NW, BKV>;
   set_lds(kern, lds);
   dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
@@ -526,7 +652,8 @@ template <int HD, int NW>
 void dkdv_launch(hipStream_t s, AttnP& p) {
   constexpr int P = HD + 4;
   constexpr int BQ = Cfg<HD>::BQ;
-  const size_t lds = sizeof(float) * (2 * 16 * NW * P + 2 * BQ * P + 2 * BQ + 16 * NW);
+  const size_t lds = sizeof(float) * (HD > 128 ? 2 * 16 * NW * P + 2 * BQ * P + 2 * BQ
+                                                : 2 * BQ * P + 2 * HD * (BQ + 4) + 2 * BQ);
   auto kern = attn_bwd_dkdv_mfma<HD, NW, BQ>;
   set_lds(kern, lds);
   dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
@@ -538,7 +665,7 @@ template <int HD, int NW>
 void dq_launch(hipStream_t s, AttnP& p) {
   constexpr int P = HD + 4;
   constexpr int BKV = Cfg<HD>::DQBKV;
-  const size_t lds = sizeof(float) * (2 * BKV * P + BKV);
+  const size_t lds = sizeof(float) * (2 * BKV * P + (HD > 128 ? 0 : HD * (BKV + 4)) + BKV);
   auto kern = attn_bwd_dq_mfma<HD, NW, BKV>;
   set_lds(kern, lds);
   dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
