@@ -43,6 +43,15 @@ struct AttnP {
   float scale;
   int causal, window;
   const float* kpad;
+  // key-split forward: chunks of ck keys per workgroup, partial O (relative
+  // to the chunk's running max) and (max, sum) pairs per chunk
+  int nch, ck;
+  float* opart;   // [B, Hq, nch, S, HD]
+  float2* mlpart; // [B, Hq, nch, S]
+  // split backward: dK/dV over query chunks of cq queries (nqc of them),
+  // dQ over key chunks of ckq keys (nkc); partial rows [chunk][B·S][Hq][HD]
+  int nqc, cq, nkc, ckq;
+  float* pdq;
 };
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
@@ -124,15 +133,40 @@ __device__ __forceinline__ void stage_pair(StageDst d1, const float* src1, int64
   }
 }
 
+// Most key chunks one forward query block is split into.
+constexpr int kMaxChunks = 8;
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x combined with the value held by lane l^16 (l^32): the gfx950 permlane
+// swaps exchange rows between two registers in the VALU (no LDS round trip);
+// with both operands = x, the two results hold this lane's and the partner
+// lane's value, in an order that depends on the lane — so only commutative
+// combinations are taken, and every lane of a pair gets the same bits.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ------------------------------------------------------------------------------
 // Forward
 // ------------------------------------------------------------------------------
-template <int HD, int NW, int BKV>
+template <int HD, int NW, int BKV, bool SPLIT>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;     // K row pitch
@@ -147,15 +181,29 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
-  // 1-D grid, heaviest causal query blocks (the last ones) first.
+  // 1-D grid, heaviest causal query blocks (the last ones) first; with a
+  // key split, item t = blockIdx / (Hq·B) is (query block, key chunk)
+  // = (nqb-1 - t % nqb, t / nqb).
   const int hb = blockIdx.x % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int nqb = (p.S + 16 * NW - 1) / (16 * NW);
   const int kh = h / (p.Hq / p.Hkv);
-  const int q0 = (nqb - 1 - (int)blockIdx.x / (p.Hq * p.B)) * 16 * NW;
+  const int item = (int)blockIdx.x / (p.Hq * p.B);
+  const int q0 = (nqb - 1 - (SPLIT ? item % nqb : item)) * 16 * NW;
+  const int chunk = SPLIT ? item / nqb : 0;
   const int qbase = q0 + 16 * w;
   const int qi = qbase + li;  // this lane's query
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+
+  const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
+  int jmax = p.causal ? qlast_wg : p.S - 1;
+  int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
+  if constexpr (SPLIT) {
+    // this workgroup's chunk of the block's key range; empty chunks exit
+    jmin = max(jmin, chunk * p.ck);
+    jmax = min(jmax, chunk * p.ck + p.ck - 1);
+    if (jmin > jmax) return;
+  }
 
   // Q carries scale·log2(e), so scores come out in base-2 units and the
   // softmax exponentials are single v_exp_f32.
@@ -174,10 +222,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
   const int jhi = qi < p.S ? (p.causal ? qi : p.S - 1) : -1;
   const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
 
-  const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
-  const int jmax = p.causal ? qlast_wg : p.S - 1;
-  const int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
-  const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
     stage_pair<HD, NT, BKV, true, false, false, true>({Ks, nullptr}, p.k, p.k_rs, {nullptr, Vt}, p.v, p.v_rs, b, p.S,
@@ -185,23 +229,16 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
     for (int j = tid; j < BKV; j += NT) Kp[j] = j0 + j < p.S && (!kpb || kpb[j0 + j] > 0.5f) ? 1.f : 0.f;
     __syncthreads();
     if (qbase > p.S - 1) continue;
-    // Tiles this wave cannot see are skipped (wave-uniform); a block every
-    // key of which is visible to all 16 queries skips the per-element mask.
-    bool tile_live[KT];
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      const int jt0 = j0 + 16 * kt;
-      bool live = jt0 < p.S && !(p.causal && jt0 > wave_qlast);
-      if (p.window > 0 && wave_qlast - (jt0 + 15) >= p.window + 15) live = false;
-      tile_live[kt] = live;
-    }
+    // Every tile of the block is computed (straight-line code the scheduler
+    // can interleave); tiles the wave cannot see are masked like any hidden
+    // key.  A block every key of which is visible to all 16 queries skips
+    // the per-element mask.
     const bool full = !kpb && j0 + BKV <= p.S && qbase + 15 < p.S && (!p.causal || j0 + BKV - 1 <= qbase) &&
                       (p.window <= 0 || qbase + 15 - j0 < p.window);
     floatx4 sacc[KT];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       sacc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (!tile_live[kt]) continue;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const floatx4 kv = *reinterpret_cast<const floatx4*>(&Ks[(16 * kt + li) * P + 16 * c + 4 * lg]);
@@ -227,8 +264,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) mloc = fmaxf(mloc, sacc[kt][v]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    mloc = max_xor32(max_xor16(mloc));
     const float mnew = fmaxf(mrow, mloc);
     // With nothing visible yet every score is -inf: referencing 0 keeps the
     // exponentials at exactly 0 instead of NaN.
@@ -243,8 +279,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
         sacc[kt][v] = e;
         lsum += e;
       }
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum = add_xor32(add_xor16(lsum));
     lrow = lrow * corr + lsum;
     mrow = mnew;
 #pragma unroll
@@ -252,7 +287,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
     // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]; lane (i, g) reads Vᵀ[16c+i][16kt+4g .. +3]
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      if (!tile_live[kt]) continue;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const floatx4 va = *reinterpret_cast<const floatx4*>(&Vt[(16 * c + li) * PV + 16 * kt + 4 * lg]);
@@ -262,26 +296,82 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma(AttnP p) {
     }
   }
   // lane holds Oᵀ[d = 16c + 4lg + v][q = qi]; transpose through LDS for
-  // coalesced row stores.
+  // coalesced row stores.  A key chunk stores O unnormalised with its
+  // (max, sum) pair for attn_combine_kernel.
   __syncthreads();
   float* Os = smem;  // [16*NW][P]
-  const float inv = lrow > 0.f ? 1.f / lrow : 0.f;
+  const float inv = SPLIT ? 1.f : lrow > 0.f ? 1.f / lrow : 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int v = 0; v < 4; ++v) Os[(16 * w + li) * P + 16 * c + 4 * lg + v] = oacc[c][v] * inv;
-  // lse in natural-log units: (m₂ + log₂ l)·ln 2
-  if (lg == 0 && qi < p.S)
-    p.lse_out[((int64_t)b * p.Hq + h) * p.S + qi] =
-        lrow > 0.f ? (mrow + __builtin_amdgcn_logf(lrow)) * kLn2 : -INFINITY;
+  const int64_t prow = (((int64_t)b * p.Hq + h) * p.nch + chunk) * p.S;  // partial rows of this chunk
+  if (lg == 0 && qi < p.S) {
+    if constexpr (SPLIT)
+      p.mlpart[prow + qi] = make_float2(mrow, lrow);
+    else  // lse in natural-log units: (m₂ + log₂ l)·ln 2
+      p.lse_out[((int64_t)b * p.Hq + h) * p.S + qi] =
+          lrow > 0.f ? (mrow + __builtin_amdgcn_logf(lrow)) * kLn2 : -INFINITY;
+  }
   __syncthreads();
   for (int f = tid; f < 16 * NW * (HD / 4); f += NT) {
     const int r = f / (HD / 4), c4 = f % (HD / 4);
     const int gq = q0 + r;
-    if (gq < p.S)
-      *reinterpret_cast<floatx4*>(p.out + ((int64_t)b * p.S + gq) * p.out_rs + (int64_t)h * HD + 4 * c4) =
-          *reinterpret_cast<const floatx4*>(&Os[r * P + 4 * c4]);
+    if (gq >= p.S) continue;
+    float* dst = SPLIT ? p.opart + (prow + gq) * HD + 4 * c4
+                       : p.out + ((int64_t)b * p.S + gq) * p.out_rs + (int64_t)h * HD + 4 * c4;
+    *reinterpret_cast<floatx4*>(dst) = *reinterpret_cast<const floatx4*>(&Os[r * P + 4 * c4]);
   }
+}
+
+// Merges the key chunks of the split forward: for each query row,
+// M = max_c m_c, L = Σ_c l_c·2^(m_c−M), O = Σ_c O_c·2^(m_c−M) / L and
+// lse = (M + log₂ L)·ln 2, over the chunks its query block was given
+// (same range test as the forward), in chunk order.  Thread = 4 columns of
+// one (b, h, q) row.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnP p, int qblock) {
+  const int64_t total = (int64_t)p.B * p.Hq * p.S * (HD / 4);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c4 = (int)(i % (HD / 4));
+  const int64_t row = i / (HD / 4);  // (b·Hq + h)·S + q
+  const int q = (int)(row % p.S);
+  const int64_t bh = row / p.S;
+  const int h = (int)(bh % p.Hq), b = (int)(bh / p.Hq);
+  const int q0 = (q / qblock) * qblock;
+  const int qlast = min(q0 + qblock - 1, p.S - 1);
+  const int jmax = p.causal ? qlast : p.S - 1;
+  const int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
+  const int c0 = jmin / p.ck, c1 = jmax / p.ck;
+  const int64_t base = bh * p.nch * p.S + q;  // + c·S
+  // all loads of the row issued together (chunks past c1 read as empty)
+  float2 ml[kMaxChunks];
+  floatx4 op[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const bool ok = c0 + i <= c1;
+    const int64_t r = base + (int64_t)min(c0 + i, c1) * p.S;
+    const float2 m2 = p.mlpart[r];
+    const floatx4 o4 = *reinterpret_cast<const floatx4*>(p.opart + r * HD + 4 * c4);
+    ml[i] = ok ? m2 : make_float2(-INFINITY, 0.f);
+    op[i] = ok ? o4 : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) M = fmaxf(M, ml[i].x);
+  const float Mref = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  floatx4 o = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const float wgt = fast_exp2(ml[i].x - Mref);  // 0 for a chunk with nothing visible
+    L += ml[i].y * wgt;
+    o += op[i] * wgt;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  *reinterpret_cast<floatx4*>(p.out + ((int64_t)b * p.S + q) * p.out_rs + (int64_t)h * HD + 4 * c4) = o * inv;
+  if (c4 == 0) p.lse_out[row] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
 }
 
 // delta[b,h,i] = Σ_d dO[i,d]·O[i,d]; one wave per row.
@@ -307,7 +397,7 @@ __global__ __launch_bounds__(256) void attn_delta_mfma_kernel(AttnP p) {
 // ------------------------------------------------------------------------------
 // dK, dV: workgroup = 16·NW keys of one query head; wave = 16 keys.
 // ------------------------------------------------------------------------------
-template <int HD, int NW, int BQ>
+template <int HD, int NW, int BQ, bool SPLIT>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
@@ -333,15 +423,21 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
-  // One workgroup per (key block, QUERY head): a GQA group's query heads
-  // run in parallel and their dK/dV contributions are summed afterwards by
-  // attn_group_sum_kernel in head order.
-  // 1-D grid, heaviest causal key blocks (the first ones) first.
+  // One workgroup per (key block, QUERY head[, query chunk]): a GQA
+  // group's query heads (and a split's query chunks) run in parallel and
+  // their dK/dV contributions are summed afterwards by attn_partial_sum_kernel
+  // in (chunk, head) order.
+  // 1-D grid, heaviest causal key blocks (the first ones) first; with a
+  // query split, item t = blockIdx / (Hq·B) is (key block, query chunk)
+  // = (t % nkb, t / nkb).
   const int hb = blockIdx.x % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int grp = p.Hq / p.Hkv;
   const int kh = h / grp;
-  const int k0 = ((int)blockIdx.x / (p.Hq * p.B)) * BKEYS;
+  const int nkb = (p.S + BKEYS - 1) / BKEYS;
+  const int item = (int)blockIdx.x / (p.Hq * p.B);
+  const int k0 = (SPLIT ? item % nkb : item) * BKEYS;
+  const int qc = SPLIT ? item / nkb : 0;
   const int kbase = k0 + 16 * w;
   const int kj = kbase + li;  // this lane's key (as S column)
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
@@ -373,8 +469,15 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   for (int c = 0; c < NC; ++c) dkacc[c] = dvacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int klast = min(k0 + BKEYS - 1, p.S - 1);
-  const int qstart = p.causal ? k0 : 0;
-  const int qend = p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1;
+  int qstart = p.causal ? k0 : 0;
+  int qend = p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1;
+  if constexpr (SPLIT) {
+    // this workgroup's chunk of the block's query range; empty chunks exit
+    // (whole workgroup, before any barrier)
+    qstart = max(qstart, qc * p.cq);
+    qend = min(qend, qc * p.cq + p.cq - 1);
+    if (qstart > qend) return;
+  }
   for (int qb0 = (qstart / BQ) * BQ; qb0 <= qend; qb0 += BQ) {
     __syncthreads();
     if constexpr (WIDE)
@@ -394,10 +497,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const int qt0 = qb0 + 16 * qt;
-      if (qt0 > p.S - 1) continue;
-      if (p.causal && qt0 + 15 < kbase) continue;
-      if (p.window > 0 && qt0 - (kbase + 15) >= p.window) continue;
-      // every query of the tile sees every key of the wave
+      // Tiles without a visible pair are computed and masked (straight-line
+      // loop body); every query of a full tile sees every key of the wave.
       const bool full = !kpb && qt0 + 15 < p.S && kbase + 15 < p.S && (!p.causal || qt0 >= kbase + 15) &&
                         (p.window <= 0 || qt0 + 15 - kbase < p.window);
       // S[q][key] and dP[q][key]: D[row q = 4lg+v][col key = li]
@@ -456,15 +557,17 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
     }
   }
   // lane holds [key = kbase + 4lg + v][d = 16c + li]; a group of one query
-  // head writes dK/dV directly, larger groups write per-head partials.
-  const bool direct = grp == 1;
+  // head without a query split writes dK/dV directly, otherwise each
+  // (chunk, head) writes a partial row.
+  const bool direct = grp == 1 && !SPLIT;
+  const int64_t prow0 = (int64_t)qc * p.B * p.S;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int gk = kbase + 4 * lg + v;
     if (gk >= p.S) continue;
     const int64_t tok = (int64_t)b * p.S + gk;
-    float* dkr = direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + (tok * p.Hq + h) * HD;
-    float* dvr = direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD;
+    float* dkr = direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + ((prow0 + tok) * p.Hq + h) * HD;
+    float* dvr = direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + ((prow0 + tok) * p.Hq + h) * HD;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       dkr[16 * c + li] = dkacc[c][v] * p.scale;
@@ -473,37 +576,67 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   }
 }
 
-// dK/dV[b,s,kh,:] = Σ_{j<grp} partial[b,s,kh·grp+j,:], in j order.
+// dK/dV[b,s,kh,:] = Σ_{c} Σ_{j<grp} partial[c][b,s,kh·grp+j,:], in (c, j)
+// order over the query chunks c the key's block was given (same range test
+// as the dK/dV kernel; c = 0 only without a split).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_group_sum_kernel(AttnP p) {
+__global__ __launch_bounds__(256) void attn_partial_sum_kernel(AttnP p, int bkeys) {
   const int grp = p.Hq / p.Hkv;
-  const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
+  const int64_t BS = (int64_t)p.B * p.S;
+  const int64_t total = BS * p.Hkv * (HD / 4);
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int c4 = (int)(i % (HD / 4));
     const int64_t r = i / (HD / 4);
     const int kh = (int)(r % p.Hkv);
     const int64_t tok = r / p.Hkv;
+    int c0 = 0, c1 = 0;
+    if (p.nqc > 1) {
+      const int k0 = ((int)(tok % p.S) / bkeys) * bkeys;
+      const int klast = min(k0 + bkeys - 1, p.S - 1);
+      const int qstart = p.causal ? k0 : 0;
+      const int qend = p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1;
+      c0 = qstart / p.cq;
+      c1 = qend / p.cq;
+    }
     floatx4 sk = floatx4{0.f, 0.f, 0.f, 0.f}, sv = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < grp; ++j) {
-      const int64_t off = (tok * p.Hq + kh * grp + j) * HD + 4 * c4;
-      sk += *reinterpret_cast<const floatx4*>(p.pdk + off);
-      sv += *reinterpret_cast<const floatx4*>(p.pdv + off);
-    }
-    float* dk = p.dk + tok * p.dk_rs + (int64_t)kh * HD + 4 * c4;
-    float* dv = p.dv + tok * p.dv_rs + (int64_t)kh * HD + 4 * c4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      dk[e] = sk[e];
-      dv[e] = sv[e];
-    }
+    for (int c = c0; c <= c1; ++c)
+      for (int j = 0; j < grp; ++j) {
+        const int64_t off = (((int64_t)c * BS + tok) * p.Hq + kh * grp + j) * HD + 4 * c4;
+        sk += *reinterpret_cast<const floatx4*>(p.pdk + off);
+        sv += *reinterpret_cast<const floatx4*>(p.pdv + off);
+      }
+    *reinterpret_cast<floatx4*>(p.dk + tok * p.dk_rs + (int64_t)kh * HD + 4 * c4) = sk;
+    *reinterpret_cast<floatx4*>(p.dv + tok * p.dv_rs + (int64_t)kh * HD + 4 * c4) = sv;
   }
+}
+
+// dQ[b,s,h,:] = scale · Σ_c partial[c][b,s,h,:] over the key chunks c the
+// query's block was given (same range test as the dQ kernel), in c order.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_dq_sum_kernel(AttnP p, int qblock) {
+  const int64_t BS = (int64_t)p.B * p.S;
+  const int64_t total = BS * p.Hq * (HD / 4);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c4 = (int)(i % (HD / 4));
+  const int64_t r = i / (HD / 4);  // tok·Hq + h
+  const int h = (int)(r % p.Hq);
+  const int64_t tok = r / p.Hq;
+  const int q0 = ((int)(tok % p.S) / qblock) * qblock;
+  const int qlast = min(q0 + qblock - 1, p.S - 1);
+  const int jmax = p.causal ? qlast : p.S - 1;
+  const int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
+  floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int c = jmin / p.ckq; c <= jmax / p.ckq; ++c)
+    s += *reinterpret_cast<const floatx4*>(p.pdq + (((int64_t)c * BS + tok) * p.Hq + h) * HD + 4 * c4);
+  *reinterpret_cast<floatx4*>(p.dq + tok * p.dq_rs + (int64_t)h * HD + 4 * c4) = s * p.scale;
 }
 
 // ------------------------------------------------------------------------------
 // dQ: workgroup = 16·NW queries of one head; wave = 16 queries.
 // ------------------------------------------------------------------------------
-template <int HD, int NW, int BKV>
+template <int HD, int NW, int BKV, bool SPLIT>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
@@ -522,14 +655,28 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
+  // 1-D grid, heaviest causal query blocks first; with a key split, item
+  // t = blockIdx / (Hq·B) is (query block, key chunk) = (nqb-1 - t % nqb, t / nqb).
   const int hb = blockIdx.x % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int nqb = (p.S + 16 * NW - 1) / (16 * NW);
   const int kh = h / (p.Hq / p.Hkv);
-  const int q0 = (nqb - 1 - (int)blockIdx.x / (p.Hq * p.B)) * 16 * NW;
+  const int item = (int)blockIdx.x / (p.Hq * p.B);
+  const int q0 = (nqb - 1 - (SPLIT ? item % nqb : item)) * 16 * NW;
+  const int kc = SPLIT ? item / nqb : 0;
   const int qbase = q0 + 16 * w;
   const int qi = qbase + li;
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+
+  const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
+  int jmax = p.causal ? qlast_wg : p.S - 1;
+  int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
+  if constexpr (SPLIT) {
+    // this workgroup's chunk of the block's key range; empty chunks exit
+    jmin = max(jmin, kc * p.ckq);
+    jmax = min(jmax, kc * p.ckq + p.ckq - 1);
+    if (jmin > jmax) return;
+  }
 
   // Q carries scale·log2(e): scores in base-2 units against lse·log2(e).
   const float qscale = p.scale * kLog2e;
@@ -553,10 +700,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   // keys visible to this lane's query: [jlo, jhi]
   const int jhi = qi < p.S ? (p.causal ? qi : p.S - 1) : -1;
   const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
-  const int qlast_wg = min(q0 + 16 * NW - 1, p.S - 1);
-  const int jmax = p.causal ? qlast_wg : p.S - 1;
-  const int jmin = p.window > 0 ? max(0, q0 - p.window + 1) : 0;
-  const int wave_qlast = min(qbase + 15, p.S - 1);
   for (int j0 = (jmin / BKV) * BKV; j0 <= jmax; j0 += BKV) {
     __syncthreads();
     if constexpr (WIDE)
@@ -573,8 +716,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int jt0 = j0 + 16 * kt;
-      if (jt0 >= p.S || (p.causal && jt0 > wave_qlast)) continue;
-      if (p.window > 0 && wave_qlast - (jt0 + 15) >= p.window + 15) continue;
+      // tiles without a visible pair are computed and masked (straight-line
+      // loop body)
       // Sᵀ and dPᵀ: D[row key = 4lg+v][col q = li]
       floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -613,14 +756,18 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
       }
     }
   }
-  // lane holds dQ[q = qbase + 4lg + v][d = 16c + li]
+  // lane holds dQ[q = qbase + 4lg + v][d = 16c + li]; a key chunk writes an
+  // unscaled partial row for attn_dq_sum_kernel
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int gq = qbase + 4 * lg + v;
     if (gq >= p.S) continue;
-    float* r = p.dq + ((int64_t)b * p.S + gq) * p.dq_rs + (int64_t)h * HD;
+    const int64_t tok = (int64_t)b * p.S + gq;
+    float* r = SPLIT ? p.pdq + (((int64_t)kc * p.B * p.S + tok) * p.Hq + h) * HD
+                     : p.dq + tok * p.dq_rs + (int64_t)h * HD;
+    const float sc = SPLIT ? 1.f : p.scale;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) r[16 * c + li] = dqacc[c][v] * p.scale;
+    for (int c = 0; c < NC; ++c) r[16 * c + li] = dqacc[c][v] * sc;
   }
 }
 
@@ -641,11 +788,17 @@ void fwd_launch(hipStream_t s, AttnP& p) {
   constexpr int BKV = Cfg<HD>::FBKV;
   constexpr int P = HD + 4;
   const size_t lds = sizeof(float) * std::max<size_t>(BKV * P + HD * (BKV + 4) + BKV, 16 * NW * P);
-  auto kern = attn_fwd_mfma<HD, NW, BKV>;
+  const bool split = p.nch > 1;
+  auto kern = split ? attn_fwd_mfma<HD, NW, BKV, true> : attn_fwd_mfma<HD, NW, BKV, false>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.nch * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
+  if (split) {
+    const int64_t total = (int64_t)p.B * p.Hq * p.S * (HD / 4);
+    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, 16 * NW);
+    MFT_LAUNCH_CHECK();
+  }
 }
 
 template <int HD, int NW>
@@ -654,9 +807,9 @@ void dkdv_launch(hipStream_t s, AttnP& p) {
   constexpr int BQ = Cfg<HD>::BQ;
   const size_t lds = sizeof(float) * (HD > 128 ? 2 * 16 * NW * P + 2 * BQ * P + 2 * BQ
                                                 : 2 * BQ * P + 2 * HD * (BQ + 4) + 2 * BQ);
-  auto kern = attn_bwd_dkdv_mfma<HD, NW, BQ>;
+  auto kern = p.nqc > 1 ? attn_bwd_dkdv_mfma<HD, NW, BQ, true> : attn_bwd_dkdv_mfma<HD, NW, BQ, false>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.nqc * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
 }
@@ -666,11 +819,16 @@ void dq_launch(hipStream_t s, AttnP& p) {
   constexpr int P = HD + 4;
   constexpr int BKV = Cfg<HD>::DQBKV;
   const size_t lds = sizeof(float) * (2 * BKV * P + (HD > 128 ? 0 : HD * (BKV + 4)) + BKV);
-  auto kern = attn_bwd_dq_mfma<HD, NW, BKV>;
+  auto kern = p.nkc > 1 ? attn_bwd_dq_mfma<HD, NW, BKV, true> : attn_bwd_dq_mfma<HD, NW, BKV, false>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.Hq * p.B));
+  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.nkc * p.Hq * p.B));
   hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
   MFT_LAUNCH_CHECK();
+  if (p.nkc > 1) {
+    const int64_t total = (int64_t)p.B * p.S * p.Hq * (HD / 4);
+    hipLaunchKernelGGL(attn_dq_sum_kernel<HD>, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, 16 * NW);
+    MFT_LAUNCH_CHECK();
+  }
 }
 
 // Waves per workgroup (16 queries or keys each): four (two at head_dim 256,
@@ -687,15 +845,74 @@ int pick_nw(const AttnArgs& a) {
   return a.hd == 256 ? 2 : 4;
 }
 
+// Splits of the inner loop.  A launch with fewer than ~2 waves per SIMD
+// (2048 waves on 256 CUs) leaves most matrix cores idle and each wave's
+// softmax unhidden, so the inner range (keys of a query block, or queries of
+// a key block) is cut into chunks of `per` loop blocks (≥ 2), one workgroup
+// per non-empty (block, chunk), aiming at ~4096 waves (twice that in chunks
+// for a causal mask, which empties about half of them), at most max_chunks
+// chunks.  Returns blocks per chunk, 0 for no split.  Tuning hook: the
+// environment variable `hook` forces blocks per chunk (0 = no split).
+int chunk_blocks(const AttnArgs& a, int64_t waves, int nblk, int max_chunks, const char* hook) {
+  int per = 0;
+  if (const char* forced = getenv(hook)) {
+    per = atoi(forced);
+  } else if (waves < 2048 && nblk >= 4) {
+    const int64_t want = std::min<int64_t>(cdiv(4096, waves) * (a.causal ? 2 : 1), max_chunks);
+    per = std::max(2, (int)cdiv(nblk, want));
+  }
+  if (per <= 0 || per >= nblk) return 0;
+  return std::max(per, (int)cdiv(nblk, max_chunks));
+}
+
+int64_t launch_waves(const AttnArgs& a, int nw) { return cdiv(a.S, 16 * nw) * nw * (int64_t)a.Hq * a.B; }
+
+struct FwdPlan {
+  int nw, nch, ck;
+};
+
+int fwd_bkv(int hd) { return hd == 64 ? Cfg<64>::FBKV : hd == 128 ? Cfg<128>::FBKV : Cfg<256>::FBKV; }
+
+FwdPlan fwd_plan(const AttnArgs& a) {
+  const int nw = pick_nw(a);
+  const int bkv = fwd_bkv(a.hd);
+  const int nkb = (int)cdiv(a.S, bkv);
+  const int per = chunk_blocks(a, launch_waves(a, nw), nkb, kMaxChunks, "MFT_ATTN_KBPC");
+  if (per == 0) return {nw, 1, a.S};
+  return {nw, (int)cdiv(nkb, per), per * bkv};
+}
+
+// Backward splits (dK/dV over query chunks, dQ over key chunks), at most
+// kMaxBwdChunks each: every chunk costs a partial row per (token, head).
+constexpr int kMaxBwdChunks = 4;
+
+struct BwdPlan {
+  int nw, nqc, cq, nkc, ckq;
+};
+
+BwdPlan bwd_plan(const AttnArgs& a) {
+  const int nw = pick_nw(a);
+  const int bq = a.hd == 64 ? Cfg<64>::BQ : a.hd == 128 ? Cfg<128>::BQ : Cfg<256>::BQ;
+  const int bkv = a.hd == 64 ? Cfg<64>::DQBKV : a.hd == 128 ? Cfg<128>::DQBKV : Cfg<256>::DQBKV;
+  const int64_t waves = launch_waves(a, nw);
+  const int nqb = (int)cdiv(a.S, bq), nkb = (int)cdiv(a.S, bkv);
+  const int pq = chunk_blocks(a, waves, nqb, kMaxBwdChunks, "MFT_ATTN_BWD_BPC");
+  const int pk = chunk_blocks(a, waves, nkb, kMaxBwdChunks, "MFT_ATTN_BWD_BPC");
+  BwdPlan pl{nw, 1, a.S, 1, a.S};
+  if (pq) { pl.nqc = (int)cdiv(nqb, pq); pl.cq = pq * bq; }
+  if (pk) { pl.nkc = (int)cdiv(nkb, pk); pl.ckq = pk * bkv; }
+  return pl;
+}
+
 template <int HD>
 void bwd_launch(hipStream_t s, AttnP& p, int nw) {
   if (nw == 4) { dkdv_launch<HD, 4>(s, p); dq_launch<HD, 4>(s, p); }
   else if (nw == 2) { dkdv_launch<HD, 2>(s, p); dq_launch<HD, 2>(s, p); }
   else { dkdv_launch<HD, 1>(s, p); dq_launch<HD, 1>(s, p); }
-  if (p.Hq != p.Hkv) {
+  if (p.Hq != p.Hkv || p.nqc > 1) {
     const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
-    hipLaunchKernelGGL(attn_group_sum_kernel<HD>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
-                       dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_partial_sum_kernel<HD>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
+                       dim3(256), 0, s, p, 16 * nw);
     MFT_LAUNCH_CHECK();
   }
 }
@@ -715,19 +932,43 @@ AttnP make(const AttnArgs& a) {
   p.causal = a.causal;
   p.window = a.window;
   p.kpad = a.kpad;
+  p.nch = p.nqc = p.nkc = 1;  // unsplit unless a plan says otherwise
+  p.ck = p.cq = p.ckq = a.S;
   return p;
 }
 
 }  // namespace
 
-void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* lse) {
+size_t attn_fwd_scratch_floats(const AttnArgs& a) {
+  const FwdPlan pl = fwd_plan(a);
+  if (pl.nch == 1) return 0;
+  return (size_t)a.B * a.Hq * pl.nch * a.S * (size_t)(a.hd + 2);
+}
+
+size_t attn_scratch_bound_floats(int64_t tokens, int Hq, int hd) {
+  const size_t rows = (size_t)tokens * Hq;
+  const size_t fwd = (size_t)kMaxChunks * rows * (size_t)(hd + 2);
+  const size_t bwd = (rows + 3) / 4 * 4 + 3 * (size_t)kMaxBwdChunks * rows * (size_t)hd;
+  return std::max(fwd, bwd);
+}
+
+void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* lse, Scratch ws) {
   AttnP p = make(a);
   MFT_CHECK_ARG(o && lse, "null output");
   MFT_CHECK_ARG(o_rs % 4 == 0 && ((uintptr_t)o & 15) == 0, "o must be 16-byte aligned rows");
   p.out = o;
   p.out_rs = o_rs;
   p.lse_out = lse;
-  switch (pick_nw(a)) {
+  const FwdPlan pl = fwd_plan(a);
+  p.nch = pl.nch;
+  p.ck = pl.ck;
+  if (pl.nch > 1) {
+    MFT_CHECK_ARG(ws.ptr && ws.bytes >= attn_fwd_scratch_floats(a) * sizeof(float),
+                  "attention forward scratch too small");
+    p.opart = ws.ptr;
+    p.mlpart = reinterpret_cast<float2*>(ws.ptr + (size_t)a.B * a.Hq * pl.nch * a.S * a.hd);
+  }
+  switch (pl.nw) {
     case 4: a.hd == 64 ? fwd_launch<64, 4>(s, p) : fwd_launch<128, 4>(s, p); break;
     case 2:
       a.hd == 64 ? fwd_launch<64, 2>(s, p) : a.hd == 128 ? fwd_launch<128, 2>(s, p) : fwd_launch<256, 2>(s, p);
@@ -753,32 +994,39 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
   p.dk = dk; p.dk_rs = dk_rs;
   p.dv = dv; p.dv_rs = dv_rs;
   const int64_t rows = (int64_t)a.B * a.S * a.Hq;
+  const BwdPlan pl = bwd_plan(a);
+  p.nqc = pl.nqc; p.cq = pl.cq;
+  p.nkc = pl.nkc; p.ckq = pl.ckq;
   p.delta_out = ws.ptr;
   p.delta = ws.ptr;
-  if (a.Hq != a.Hkv) {
-    // partial rows padded to a 16-byte boundary after delta
-    float* part = ws.ptr + (rows + 3) / 4 * 4;
+  // partial rows after delta (padded to a 16-byte boundary): dK, dV per
+  // (query chunk, query head), then dQ per key chunk
+  float* part = ws.ptr + (rows + 3) / 4 * 4;
+  if (a.Hq != a.Hkv || pl.nqc > 1) {
     p.pdk = part;
-    p.pdv = part + rows * a.hd;
+    p.pdv = part + pl.nqc * rows * a.hd;
+    part += 2 * pl.nqc * rows * a.hd;
   }
+  if (pl.nkc > 1) p.pdq = part;
   switch (a.hd) {
     case 64: hipLaunchKernelGGL(attn_delta_mfma_kernel<64>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
     case 128: hipLaunchKernelGGL(attn_delta_mfma_kernel<128>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
     default: hipLaunchKernelGGL(attn_delta_mfma_kernel<256>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p); break;
   }
   MFT_LAUNCH_CHECK();
-  const int nw = pick_nw(a);
   switch (a.hd) {
-    case 64: bwd_launch<64>(s, p, nw); break;
-    case 128: bwd_launch<128>(s, p, nw); break;
-    default: bwd_launch<256>(s, p, nw); break;
+    case 64: bwd_launch<64>(s, p, pl.nw); break;
+    case 128: bwd_launch<128>(s, p, pl.nw); break;
+    default: bwd_launch<256>(s, p, pl.nw); break;
   }
 }
 
 size_t attn_bwd_scratch_floats(const AttnArgs& a) {
+  const BwdPlan pl = bwd_plan(a);
   const size_t rows = (size_t)a.B * a.S * a.Hq;
   size_t n = (rows + 3) / 4 * 4;
-  if (a.Hq != a.Hkv) n += 2 * rows * (size_t)a.hd;
+  if (a.Hq != a.Hkv || pl.nqc > 1) n += 2 * (size_t)pl.nqc * rows * (size_t)a.hd;
+  if (pl.nkc > 1) n += (size_t)pl.nkc * rows * (size_t)a.hd;
   return n;
 }
 

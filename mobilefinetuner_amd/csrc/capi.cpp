@@ -190,7 +190,9 @@ int mft_attn_fwd(mft_handle h, const float* q, int64_t q_rs, const float* k,
   return guarded([&] {
     require_handle(h);
     mft::AttnArgs a{q, k, v, q_rs, k_rs, v_rs, B, Hq, Hkv, S, hd, scale, causal, window, kpad};
-    mft::attn_fwd(h->stream, a, o, o_rs, lse);
+    const size_t ws = mft::attn_fwd_scratch_floats(a) * sizeof(float);
+    mft::Scratch s{ws ? reinterpret_cast<float*>(scratch(h, ws)) : nullptr, ws};
+    mft::attn_fwd(h->stream, a, o, o_rs, lse, s);
   });
 }
 

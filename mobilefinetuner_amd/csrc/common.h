@@ -119,8 +119,14 @@ struct AttnArgs {
   int causal, window;
   const float* kpad;
 };
+// ws: scratch of attn_fwd_scratch_floats(a) floats (0 when the launch is not
+// split over keys).
 void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs,
-              float* lse);
+              float* lse, Scratch ws);
+size_t attn_fwd_scratch_floats(const AttnArgs& a);
+// Upper bound of attn_fwd / attn_bwd scratch over every shape with
+// B·S ≤ tokens.
+size_t attn_scratch_bound_floats(int64_t tokens, int Hq, int hd);
 void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs,
               const float* dout, int64_t do_rs, const float* lse, float* dq,
               int64_t dq_rs, float* dk, int64_t dk_rs, float* dv,

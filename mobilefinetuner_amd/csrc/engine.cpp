@@ -342,7 +342,9 @@ void alloc_acts(mft_model_s* m) {
     m->dup = b.f(M * ff);
     m->row_nll = b.f(M);
     const int64_t wide = std::max<int64_t>({d, ff, H * hd, 3 * d});
-    const int64_t wsf = M * std::max<int64_t>(r, 1) + 16 * std::max<int64_t>(r, 1) * wide + 8 * M * wide;
+    const int64_t wsf = std::max<int64_t>(
+        M * std::max<int64_t>(r, 1) + 16 * std::max<int64_t>(r, 1) * wide + 8 * M * wide,
+        (int64_t)attn_scratch_bound_floats(M, (int)H, (int)hd));
     m->ws.ptr = b.f(wsf);
     m->ws.bytes = (size_t)wsf * sizeof(float);
   };
@@ -505,7 +507,7 @@ void attention_fwd(mft_model_s* m, Acts& a, int li, const float* mask, int nseq,
   const double work = 2.0 * 2.0 * nseq * c.n_head * (double)S * S * c.head_dim * 0.5;
   Timed t(m, CLS_ATTN, work);
   t.begin();
-  attn_fwd(m->stream, g, a.att, (int64_t)c.n_head * c.head_dim, a.lse);
+  attn_fwd(m->stream, g, a.att, (int64_t)c.n_head * c.head_dim, a.lse, m->ws);
   t.end();
 }
 

@@ -157,6 +157,7 @@ def test_attention_fwd_bwd(B, Hq, Hkv, S, hd, window, pad):
     if pad:
         kpad = np.ones((B, S), np.float32)
         kpad[-1, S - S // 4:] = 0
+        kpad[0, :3] = 0  # leading padded keys: queries 0-2 of sequence 0 see nothing
     o_ref, lse_ref = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, True, window, kpad)
     o, lse = ops.attn_fwd(g(q), g(k), g(v), B, Hq, Hkv, S, hd, scale, True, window,
                           g(kpad) if pad else None)
@@ -171,6 +172,58 @@ def test_attention_fwd_bwd(B, Hq, Hkv, S, hd, window, pad):
     assert rel_err(h(dq), dq_ref) < TOL
     assert rel_err(h(dk), dk_ref) < TOL
     assert rel_err(h(dv), dv_ref) < TOL
+
+
+SPLIT_CASES = [
+    (1, 14, 2, 1024, 64, 0, False),   # Qwen2.5-0.5B shape: the default plan splits it
+    (2, 4, 1, 300, 256, 128, True),   # hd=256, sliding window, padding, ragged
+    (1, 4, 2, 333, 128, 0, True),     # hd=128, ragged S, padding
+]
+_SPLIT_REF = {}
+
+
+def _split_case(i):
+    """Inputs and oracle outputs of SPLIT_CASES[i], computed once per session."""
+    if i not in _SPLIT_REF:
+        B, Hq, Hkv, S, hd, window, pad = SPLIT_CASES[i]
+        rng = np.random.default_rng(100 + i)
+        q, k, v, dout = (rng.standard_normal((B * S, n * hd)).astype(np.float32)
+                         for n in (Hq, Hkv, Hkv, Hq))
+        kpad = None
+        if pad:
+            kpad = np.ones((B, S), np.float32)
+            kpad[-1, S - S // 4:] = 0
+            kpad[0, :3] = 0  # leading padded keys: early queries see nothing
+        scale = hd ** -0.5
+        o, lse = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, True, window, kpad)
+        grads = O.attn_bwd(q, k, v, o, dout, lse, B, Hq, Hkv, S, hd, scale, True, window, kpad)
+        _SPLIT_REF[i] = (q, k, v, dout, kpad, o, lse, grads)
+    return _SPLIT_REF[i]
+
+
+@pytest.mark.parametrize("per", ["0", "1", "2", "3"])
+def test_attention_split(monkeypatch, per):
+    """Forward split into key chunks and backward split into query (dK/dV) and
+    key (dQ) chunks of `per` loop blocks, merged by the combine / partial-sum
+    kernels, against the oracle; 0 = unsplit.  Results must not depend on the
+    chunking beyond fp32 rounding."""
+    monkeypatch.setenv("MFT_ATTN_KBPC", per)
+    monkeypatch.setenv("MFT_ATTN_BWD_BPC", per)
+    for i, (B, Hq, Hkv, S, hd, window, pad) in enumerate(SPLIT_CASES):
+        print(f"attention split per={per} B={B} Hq={Hq} S={S} hd={hd} win={window}", flush=True)
+        q, k, v, dout, kpad, o_ref, lse_ref, (dq_ref, dk_ref, dv_ref) = _split_case(i)
+        kp = g(kpad) if pad else None
+        scale = hd ** -0.5
+        o, lse = ops.attn_fwd(g(q), g(k), g(v), B, Hq, Hkv, S, hd, scale, True, window, kp)
+        assert rel_err(h(o), o_ref) < TOL
+        fin = np.isfinite(lse_ref)
+        assert np.array_equal(np.isfinite(h(lse)), fin)
+        assert rel_err(h(lse)[fin], lse_ref[fin]) < TOL
+        dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, True,
+                                  window, kp)
+        assert rel_err(h(dq), dq_ref) < TOL
+        assert rel_err(h(dk), dk_ref) < TOL
+        assert rel_err(h(dv), dv_ref) < TOL
 
 
 def test_attention_strided_qkv_view():
