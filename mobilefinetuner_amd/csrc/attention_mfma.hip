@@ -599,13 +599,27 @@ __global__ __launch_bounds__(256) void attn_partial_sum_kernel(AttnP p, int bkey
       c0 = qstart / p.cq;
       c1 = qend / p.cq;
     }
+    // loads in batches of 4 partial rows (rows past the last read as zero
+    // and are not added), summed in (c, j) order
     floatx4 sk = floatx4{0.f, 0.f, 0.f, 0.f}, sv = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int c = c0; c <= c1; ++c)
-      for (int j = 0; j < grp; ++j) {
+    const int n = (c1 - c0 + 1) * grp;
+    for (int t0 = 0; t0 < n; t0 += 4) {
+      floatx4 bk[4], bv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = min(t0 + u, n - 1);
+        const int c = c0 + t / grp, j = t % grp;
         const int64_t off = (((int64_t)c * BS + tok) * p.Hq + kh * grp + j) * HD + 4 * c4;
-        sk += *reinterpret_cast<const floatx4*>(p.pdk + off);
-        sv += *reinterpret_cast<const floatx4*>(p.pdv + off);
+        bk[u] = *reinterpret_cast<const floatx4*>(p.pdk + off);
+        bv[u] = *reinterpret_cast<const floatx4*>(p.pdv + off);
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (t0 + u < n) {
+          sk += bk[u];
+          sv += bv[u];
+        }
+    }
     *reinterpret_cast<floatx4*>(p.dk + tok * p.dk_rs + (int64_t)kh * HD + 4 * c4) = sk;
     *reinterpret_cast<floatx4*>(p.dv + tok * p.dv_rs + (int64_t)kh * HD + 4 * c4) = sv;
   }
