@@ -41,6 +41,15 @@ void set_last_error(const std::string& msg);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// IEEE fp16 bits → fp32 (exact), one value and four packed in a uint2.
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ float __attribute__((ext_vector_type(4))) widen4(uint2 u) {
+  return {half_bits_to_float(u.x & 0xffff), half_bits_to_float(u.x >> 16), half_bits_to_float(u.y & 0xffff),
+          half_bits_to_float(u.y >> 16)};
+}
+
 // ---- launchers shared by the C-ABI and the step engine ----------------------
 struct GemmEpilogue {
   const float* bias = nullptr;   // [N]
@@ -96,6 +105,44 @@ void rank_outer_pair(hipStream_t s, int M, int r, float scale, bool accumulate,
                      const float* P0, const float* X0, int64_t ldx0, int C0, float* out0, int64_t osj0,
                      int64_t osc0, const float* P1, const float* X1, int64_t ldx1, int C1, float* out1,
                      int64_t osj1, int64_t osc1);
+
+// ---- batched LoRA work of the step engine (job tables in device memory) ----
+// W_eff = W + scale·Aᵀ·Bᵀ for one LoRA linear: W [K,N] fp32 or fp16 (f16 = 1),
+// A [r,K], B [N,r], out [K,N] fp32.  N must be a multiple of 4.
+struct MergeJob {
+  const void* W;
+  const float* A;
+  const float* B;
+  float* out;
+  int K, N, f16;
+  int tile0;  // first tile of this job (tiles of 16 rows × 256 columns)
+};
+size_t merge_tiles(int K, int N);
+// jobs: device array of njobs MergeJobs with increasing tile0; r ∈ {4, 8, 16, 32}.
+void lora_merge(hipStream_t s, const MergeJob* jobs, int njobs, int total_tiles, int r, float scale);
+
+// One rank-r product of a batched launch.
+//   kind 0 (projection): out[M,r] = X[M,K]·Y, Y = A [r,K] (y_rk) or B [K,r];
+//   kind 1 (outer):      out(j,c) (+)= scale·Σ_m P[m,j]·X[m,c], c < C.
+// Projection jobs come first in a table and take cdiv(M, 16) workgroups
+// each; outer jobs take `blocks` = rank_outer_blocks(C) workgroups (a
+// multiple of 8) from `block0`, counted after the projections.
+struct RankJob {
+  int kind;
+  int K;  // projection: K; outer: C
+  int y_rk;
+  int accumulate;
+  int blocks, block0;
+  const float* X;
+  int64_t ldx;
+  const float* Y;  // projection: Y; outer: P [M, r]
+  float* out;
+  int64_t osj, osc;
+  float scale;
+};
+int rank_outer_blocks(int C);
+// Runs jobs[0, njobs) (the first nproj are projections) over M rows.
+void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r);
 
 void lora_linear_fwd(hipStream_t s, const float* x, int64_t M, int64_t K,
                      const void* W, bool w_f16, int64_t N, const float* bias,

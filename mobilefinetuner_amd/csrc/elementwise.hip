@@ -14,10 +14,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
-  return (float)__builtin_bit_cast(_Float16, h);
-}
-
 // Round-to-nearest-even fp32 → fp16 via the hardware conversion
 // (v_cvt_f16_f32 rounds to nearest even under the default rounding mode).
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {

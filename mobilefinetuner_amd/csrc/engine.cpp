@@ -46,11 +46,17 @@ struct Param {
 struct Linear {
   int W = -1, b = -1, A = -1, B = -1;
   int K = 0, N = 0;
+  float* weff = nullptr;  // merged weight W + s·Aᵀ·Bᵀ [K, N] fp32 (LoRA linears)
 };
+
+// Backward groups of LoRA linears whose dY are ready together (GPT-2:
+// c_fc2 | c_fc | c_proj | c_attn; Qwen2/Gemma3: down | gate, up | o | q, k, v).
+enum { LG_MLP_OUT = 0, LG_MLP_IN, LG_ATTN_OUT, LG_ATTN_IN, LG_MAX };
 
 struct Layer {
   int n1w = -1, n1b = -1, n2w = -1, n2b = -1, qn = -1, kn = -1, pan = -1, pfn = -1;
   Linear lin[T_MAX];
+  int dy_batch[LG_MAX] = {-1, -1, -1, -1};  // index into mft_model_s::batches
 };
 
 struct Acts {
@@ -58,6 +64,7 @@ struct Acts {
   float *q, *k, *v, *qraw, *kraw, *qrs, *krs;
   int64_t qs, ks, vs;
   float* xa[T_MAX];
+  float* U[T_MAX];  // dY·B of each LoRA linear (kept for dA at the end of the backward)
   float *att, *lse, *o, *ors, *hmid, *n2, *mean2, *rstd2;
   float *gate, *up, *act, *mo, *mrs;
 };
@@ -110,6 +117,24 @@ struct mft_model_s {
   float *dtq = nullptr, *dtk = nullptr;
   float* row_nll = nullptr;
   Scratch ws;
+  // Merged LoRA weights and batched rank-r work.  With `merged`, every LoRA
+  // linear multiplies by W_eff = W + s·Aᵀ·Bᵀ (rebuilt by one launch at the
+  // start of each forward), and the gradients dA = s·Uᵀ·x, dB = s·dYᵀ·xa
+  // (U = dY·B, xa = x·Aᵀ) come from table-driven launches: all xa at the
+  // start of the backward, U and dB per group of linears whose dY are ready,
+  // all dA at the end.
+  bool merged = false;
+  void* weff_mem = nullptr;
+  void* tables = nullptr;  // device: MergeJob[n_merge], then RankJob[]
+  const MergeJob* d_merge = nullptr;
+  int n_merge = 0, merge_tiles_total = 0;
+  struct Batch {
+    const RankJob* jobs;
+    int njobs, nproj, outer_blocks;
+    double work_per_row;  // flops per token (timing)
+  };
+  std::vector<Batch> batches;
+  int xa_batch = -1, da_batch = -1;
   // device scalars: [0..63] per-micro loss sums (double), counts (int64)
   double* d_loss = nullptr;
   int64_t* d_cnt = nullptr;
@@ -306,7 +331,10 @@ void alloc_acts(mft_model_s* m) {
       }
       const Layer& L = m->L[l];
       for (int t = 0; t < T_MAX; ++t)
-        if (L.lin[t].A >= 0) a.xa[t] = b.f(M * r);
+        if (L.lin[t].A >= 0) {
+          a.xa[t] = b.f(M * r);
+          a.U[t] = b.f(M * r);
+        }
       a.att = b.f(M * H * hd);
       a.lse = b.f(M * H);
       a.o = b.f(M * d);
@@ -377,6 +405,133 @@ void alloc_acts(mft_model_s* m) {
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
 }
 
+// ---- merged LoRA: W_eff arena and job tables --------------------------------------
+// x and dY of LoRA linear t of layer li as the backward pass sees them.
+void lora_io(mft_model_s* m, int li, int t, const float** x, const float** dy) {
+  const Acts& a = m->A[li];
+  const bool gemma = m->c.arch == MFT_ARCH_GEMMA3;
+  if (m->c.arch == MFT_ARCH_GPT2) {
+    const float* xs[4] = {a.n1, a.att, a.n2, a.act};
+    const float* ds[4] = {m->dqkv, m->dh, m->dgate, m->dh};
+    *x = xs[t];
+    *dy = ds[t];
+    return;
+  }
+  const float* xs[T_MAX] = {a.n1, a.n1, a.n1, a.att, a.n2, a.n2, a.act};
+  const float* ds[T_MAX] = {gemma ? m->dtq : m->dq, gemma ? m->dtk : m->dk, m->dv, gemma ? m->dtmp : m->dh,
+                            m->dgate, m->dup, gemma ? m->dtmp : m->dh};
+  *x = xs[t];
+  *dy = ds[t];
+}
+
+float lscale(const mft_model_s* m);
+
+// Builds W_eff buffers and the device job tables once the activation arena
+// exists (the tables hold activation and gradient pointers).  Leaves
+// `merged` false when a shape does not fit the batched kernels (then every
+// LoRA linear keeps its rank-r epilogue path).
+void build_lora_tables(mft_model_s* m) {
+  const mft_model_cfg& c = m->c;
+  const int r = c.lora_r;
+  if (r != 4 && r != 8 && r != 16 && r != 32) return;
+  const bool gpt2 = c.arch == MFT_ARCH_GPT2;
+  const int nt = gpt2 ? 4 : T_MAX;
+  size_t weff_floats = 0;
+  for (auto& L : m->L)
+    for (int t = 0; t < nt; ++t) {
+      const Linear& l = L.lin[t];
+      if (l.A < 0) continue;
+      if (l.N % 4 || l.K % 4) return;
+      weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
+    }
+  if (weff_floats == 0) return;
+  if (hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
+    throw Error(MFT_ENOMEM, "merged LoRA weights (" + std::to_string(weff_floats * 4) + " bytes)");
+  const float s = lscale(m);
+  std::vector<MergeJob> mj;
+  std::vector<RankJob> rj;
+  struct Pending {
+    size_t off;
+    int njobs, nproj, outer_blocks;
+    double work;
+  };
+  std::vector<Pending> pend;
+  auto proj_job = [&](const float* X, int K, const float* Y, bool y_rk, float* out) {
+    RankJob j{};
+    j.kind = 0; j.K = K; j.y_rk = y_rk ? 1 : 0; j.X = X; j.ldx = K; j.Y = Y; j.out = out; j.scale = 1.f;
+    return j;
+  };
+  auto outer_job = [&](const float* P, const float* X, int C, float* out, int64_t osj, int64_t osc) {
+    RankJob j{};
+    j.kind = 1; j.K = C; j.accumulate = 1; j.blocks = rank_outer_blocks(C); j.X = X; j.ldx = C; j.Y = P;
+    j.out = out; j.osj = osj; j.osc = osc; j.scale = s;
+    return j;
+  };
+  // Appends one batch (projections first, then outer products) and returns
+  // its index.
+  auto add_batch = [&](std::vector<RankJob> proj, std::vector<RankJob> outer) {
+    if (proj.empty() && outer.empty()) return -1;
+    Pending p{rj.size(), (int)(proj.size() + outer.size()), (int)proj.size(), 0, 0.0};
+    for (auto& j : proj) {
+      p.work += 2.0 * j.K * r;
+      rj.push_back(j);
+    }
+    for (auto& j : outer) {
+      j.block0 = p.outer_blocks;
+      p.outer_blocks += j.blocks;
+      p.work += 2.0 * j.K * r;
+      rj.push_back(j);
+    }
+    pend.push_back(p);
+    return (int)pend.size() - 1;
+  };
+  std::vector<RankJob> xa_jobs, da_jobs;
+  size_t woff = 0;
+  int tiles = 0;
+  static const int kGroupGpt2[4] = {LG_ATTN_IN, LG_ATTN_OUT, LG_MLP_IN, LG_MLP_OUT};
+  static const int kGroupHf[T_MAX] = {LG_ATTN_IN, LG_ATTN_IN, LG_ATTN_IN, LG_ATTN_OUT,
+                                      LG_MLP_IN, LG_MLP_IN, LG_MLP_OUT};
+  for (int li = 0; li < c.n_layer; ++li) {
+    Layer& L = m->L[li];
+    Acts& a = m->A[li];
+    std::vector<RankJob> gp[LG_MAX], go[LG_MAX];
+    for (int t = 0; t < nt; ++t) {
+      Linear& l = L.lin[t];
+      if (l.A < 0) continue;
+      l.weff = static_cast<float*>(m->weff_mem) + woff;
+      woff += ((size_t)l.K * l.N + 63) / 64 * 64;
+      MergeJob g{};
+      g.W = m->P[l.W].data; g.A = static_cast<const float*>(m->P[l.A].data);
+      g.B = static_cast<const float*>(m->P[l.B].data); g.out = l.weff; g.K = l.K; g.N = l.N;
+      g.f16 = m->P[l.W].f16 ? 1 : 0; g.tile0 = tiles;
+      tiles += (int)merge_tiles(l.K, l.N);
+      mj.push_back(g);
+      const float *x, *dy;
+      lora_io(m, li, t, &x, &dy);
+      // xa = x·Aᵀ; U = dY·B; dB += s·dYᵀ·xa (out(j,n) = dB[n][j]); dA += s·Uᵀ·x
+      xa_jobs.push_back(proj_job(x, l.K, static_cast<const float*>(m->P[l.A].data), true, a.xa[t]));
+      const int grp = gpt2 ? kGroupGpt2[t] : kGroupHf[t];
+      gp[grp].push_back(proj_job(dy, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
+      go[grp].push_back(outer_job(a.xa[t], dy, l.N, m->P[l.B].grad, 1, r));
+      da_jobs.push_back(outer_job(a.U[t], x, l.K, m->P[l.A].grad, l.K, 1));
+    }
+    for (int gi = 0; gi < LG_MAX; ++gi) L.dy_batch[gi] = add_batch(gp[gi], go[gi]);
+  }
+  m->xa_batch = add_batch(xa_jobs, {});
+  m->da_batch = add_batch({}, da_jobs);
+  const size_t mbytes = (mj.size() * sizeof(MergeJob) + 255) & ~size_t(255);
+  const size_t bytes = mbytes + rj.size() * sizeof(RankJob);
+  if (hipMalloc(&m->tables, bytes) != hipSuccess) throw Error(MFT_ENOMEM, "LoRA job tables");
+  MFT_HIP(hipMemcpy(m->tables, mj.data(), mj.size() * sizeof(MergeJob), hipMemcpyHostToDevice));
+  const RankJob* d_rank = reinterpret_cast<const RankJob*>(static_cast<char*>(m->tables) + mbytes);
+  MFT_HIP(hipMemcpy(const_cast<RankJob*>(d_rank), rj.data(), rj.size() * sizeof(RankJob), hipMemcpyHostToDevice));
+  m->d_merge = static_cast<const MergeJob*>(m->tables);
+  m->n_merge = (int)mj.size();
+  m->merge_tiles_total = tiles;
+  for (auto& p : pend) m->batches.push_back({d_rank + p.off, p.njobs, p.nproj, p.outer_blocks, p.work});
+  m->merged = true;
+}
+
 // ---- timing helpers -------------------------------------------------------------
 hipEvent_t next_event(mft_model_s* m) {
   if (m->capturing) {  // events owned by the captured graph
@@ -443,6 +598,11 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   GemmEpilogue ep;
   ep.bias = l.b >= 0 ? static_cast<const float*>(m->P[l.b].data) : nullptr;
   ep.resid = resid;
+  if (lora && m->merged) {  // y = x·W_eff (+ bias, residual)
+    Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
+    gemm(m->stream, x, l.K, l.weff, l.N, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+    return;
+  }
   if (lora) {
     Timed tr(m, CLS_RANK, 4.0 * M * l.K * r);
     tr.begin();
@@ -463,6 +623,14 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
              int64_t M, float* dx) {
   const Param& W = m->P[l.W];
   const bool lora = l.A >= 0;
+  if (lora && m->merged) {  // dX = dY·W_effᵀ; dA/dB come from the batched launches
+    if (dx) {
+      Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
+      gemm(m->stream, dy, l.N, l.weff, l.N, true, false, dx, l.K, (int)M, l.K, l.N, GemmEpilogue(), m->ws,
+           t.events());
+    }
+    return;
+  }
   const int r = lora ? m->c.lora_r : 0;
   float* U = m->ws.ptr;
   Scratch rest = m->ws.offset((size_t)(M * (r > 0 ? r : 1)));
@@ -495,6 +663,29 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
   }
 }
 
+// One table-driven launch of batched rank-r work (see build_lora_tables).
+void run_batch(mft_model_s* m, int idx, int64_t M) {
+  if (!m->merged || idx < 0) return;
+  const mft_model_s::Batch& b = m->batches[idx];
+  Timed t(m, CLS_RANK, b.work_per_row * M);
+  t.begin();
+  rank_batch(m->stream, b.jobs, b.njobs, b.nproj, b.outer_blocks, (int)M, m->c.lora_r);
+  t.end();
+}
+
+// W_eff = W + s·Aᵀ·Bᵀ for every LoRA linear (one launch).
+void merge_lora(mft_model_s* m) {
+  if (!m->merged) return;
+  double work = 0.0;
+  for (auto& L : m->L)
+    for (auto& l : L.lin)
+      if (l.weff) work += 2.0 * l.K * l.N * m->c.lora_r;
+  Timed t(m, CLS_RANK, work);
+  t.begin();
+  lora_merge(m->stream, m->d_merge, m->n_merge, m->merge_tiles_total, m->c.lora_r, lscale(m));
+  t.end();
+}
+
 template <typename T>
 const T* pd(const mft_model_s* m, int i) {
   return i < 0 ? nullptr : static_cast<const T*>(m->P[i].data);
@@ -518,6 +709,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
+  merge_lora(m);  // A, B (or W) may have changed since the last forward
   embed(s, ids, M, S, E.data, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
         gemma ? std::sqrt((float)d) : 1.f, m->A[0].x);
   for (int li = 0; li < c.n_layer; ++li) {
@@ -605,6 +797,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
+  run_batch(m, m->xa_batch, M);  // xa = x·Aᵀ of every LoRA linear
   {
     // dhf = dlogits · E, E [V, d] is the [K, N] operand.
     Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
@@ -627,14 +820,18 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       rmsnorm_bwd(s, m->dh, a.mo, pd<float>(m, L.pfn), a.mrs, M, d, true, m->dtmp, false);
       dmo = m->dtmp;
     }
+    // U = dY·B and dB += s·dYᵀ·xa of each LoRA group as soon as its dY exist
+    run_batch(m, L.dy_batch[LG_MLP_OUT], M);
     if (gpt2) {
       lin_bwd(m, L.lin[G_FC2], dmo, a.act, a.xa[G_FC2], M, m->dact);
       glu_bwd(s, m->dact, a.gate, nullptr, nf, 0, m->dgate, nullptr);
+      run_batch(m, L.dy_batch[LG_MLP_IN], M);
       lin_bwd(m, L.lin[G_FC], m->dgate, a.n2, a.xa[G_FC], M, m->dn);
       layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, m->dh, true);
     } else {
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
       glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, m->dgate, m->dup);
+      run_batch(m, L.dy_batch[LG_MLP_IN], M);
       lin_bwd(m, L.lin[T_GATE], m->dgate, a.n2, a.xa[T_GATE], M, m->dn);
       lin_bwd(m, L.lin[T_UP], m->dup, a.n2, a.xa[T_UP], M, m->dtmp);
       add_inplace(s, m->dn, m->dtmp, M * d);
@@ -646,6 +843,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       rmsnorm_bwd(s, m->dh, a.o, pd<float>(m, L.pan), a.ors, M, d, true, m->dtmp, false);
       dox = m->dtmp;
     }
+    run_batch(m, L.dy_batch[LG_ATTN_OUT], M);
     lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};
@@ -659,6 +857,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
                  3 * d, m->dqkv + 2 * d, 3 * d, m->ws);
         t.end();
       }
+      run_batch(m, L.dy_batch[LG_ATTN_IN], M);
       lin_bwd(m, L.lin[G_ATTN], m->dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
       if (need_dx)
         layernorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.mean1, a.rstd1, M, d, m->dh, true);
@@ -682,6 +881,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       dqx = m->dtq;
       dkx = m->dtk;
     }
+    run_batch(m, L.dy_batch[LG_ATTN_IN], M);
     lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, need_dx ? m->dn : nullptr);
     lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, need_dx ? m->dtmp : nullptr);
     if (need_dx) add_inplace(s, m->dn, m->dtmp, M * d);
@@ -691,6 +891,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       rmsnorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.rstd1, M, d, gemma, m->dh, true);
     }
   }
+  run_batch(m, m->da_batch, M);  // dA += s·Uᵀ·x of every LoRA linear
 }
 
 // Hyper-parameters reach the device as kernel arguments of a one-block
@@ -817,6 +1018,7 @@ int mft_model_create(mft_model* out, const mft_model_cfg* cfg, int64_t max_token
       build_params(m);
       alloc_params(m);
       alloc_acts(m);
+      build_lora_tables(m);
     } catch (...) {
       mft_model_destroy(m);
       throw;
@@ -835,7 +1037,8 @@ int mft_model_destroy(mft_model m) {
     if (m->ev_in) (void)hipEventDestroy(m->ev_in);
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
-    void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss};
+    void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss,
+                    m->weff_mem, m->tables};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     delete m;

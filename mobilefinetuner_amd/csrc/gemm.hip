@@ -51,15 +51,6 @@ struct GemmParams {
   GemmEpilogue ep;
 };
 
-__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
-  return (float)__builtin_bit_cast(_Float16, h);
-}
-
-__device__ __forceinline__ floatx4 widen4(uint2 u) {
-  return floatx4{half_bits_to_float(u.x & 0xffff), half_bits_to_float(u.x >> 16),
-                 half_bits_to_float(u.y & 0xffff), half_bits_to_float(u.y >> 16)};
-}
-
 // Bias, residual and β·C; the rank-r term is accumulated on the matrix
 // cores before the epilogue.
 __device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep, float acc, int m, int n,

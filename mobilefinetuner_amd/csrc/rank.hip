@@ -137,15 +137,18 @@ __global__ __launch_bounds__(256) void rank_proj_scalar_kernel(const float* X, i
 // out(j,c) (+)= scale·Σ_m P[m,j]·X[m,c] on the matrix cores
 // (v_mfma_f32_16x16x4_f32): D[c][j] += A[c][m]·B[m][j] with A = Xᵀ, B = P,
 // so lane (i, g) feeds X[m+g][c0+i] and P[m+g][16·jt+i] and ends holding
-// D[c0+4g+v][16·jt+i].  A workgroup owns 16 columns c of one product; its 8
-// waves take consecutive eighths of M (loads of 8 MFMA steps issued ahead of
-// the MFMAs) and are summed through LDS in wave order.  Two independent
-// products (dA and dB of one LoRA layer) share one launch.
+// D[c0+4g+v][16·jt+i].  A workgroup owns 16 columns c of one product; its
+// 16 waves take consecutive sixteenths of M in chunks of 32 rows, each
+// chunk's loads issued while the previous chunk is multiplied, and are
+// summed through LDS in wave order (deterministic, no atomics).  Column
+// blocks are dealt to the eight XCDs in contiguous runs, so the workgroups
+// sharing a 128-byte line of X share one L2.  Two independent products (dA
+// and dB of one LoRA layer) share one launch.
 struct OuterJob {
   const float* P;
   const float* X;
   int64_t ldx;
-  int C, blocks;
+  int C, blocks;  // blocks: launched for this job (a multiple of 8)
   float* out;
   int64_t osj, osc;
 };
@@ -155,43 +158,71 @@ struct OuterArgs {
   float scale;
 };
 
+constexpr int kOuterWaves = 16;
+
 template <int JT>
-__global__ __launch_bounds__(512) void rank_outer_mfma(OuterArgs a) {
-  __shared__ floatx4 red[7][JT][64];
+struct OuterChunk {
+  float x[8], p[JT][8];
+};
+
+template <int JT>
+__device__ __forceinline__ void outer_load(OuterChunk<JT>& ch, const OuterJob& jb, int r, int m, int me, int mb,
+                                           int ci, bool cok, int i, int g) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int mr = m + 4 * t + g;
+    const bool ok = mr < me;
+    const int mc = ok ? mr : mb;
+    const float x = jb.X[(int64_t)mc * jb.ldx + ci];
+    ch.x[t] = (ok && cok) ? x : 0.f;
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      const int jj = 16 * jt + i;
+      const float pp = jb.P[(int64_t)mc * r + min(jj, r - 1)];
+      ch.p[jt][t] = (ok && jj < r) ? pp : 0.f;
+    }
+  }
+}
+
+template <int JT>
+__device__ __forceinline__ void outer_mfma(floatx4 (&acc)[JT], const OuterChunk<JT>& ch) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+      acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ch.x[t], ch.p[jt][t], acc[jt], 0, 0, 0);
+}
+
+template <int JT>
+__global__ __launch_bounds__(64 * kOuterWaves) void rank_outer_mfma(OuterArgs a) {
+  __shared__ floatx4 red[kOuterWaves - 1][JT][64];
   const bool second = (int)blockIdx.x >= a.job[0].blocks;
   const OuterJob jb = second ? a.job[1] : a.job[0];
-  const int blk = second ? (int)blockIdx.x - a.job[0].blocks : (int)blockIdx.x;
+  const int raw = second ? (int)blockIdx.x - a.job[0].blocks : (int)blockIdx.x;
+  const int blk = (raw % 8) * (jb.blocks / 8) + raw / 8;  // contiguous column runs per XCD
+  const int c0 = blk * 16;
+  if (c0 >= jb.C) return;  // whole workgroup, before any barrier
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int c0 = blk * 16;
   const int ci = min(c0 + i, jb.C - 1);
   const bool cok = c0 + i < jb.C;
-  const int per = ((a.M + 8 * 32 - 1) / (8 * 32)) * 32;  // rows per wave, multiple of 32
-  const int mb = w * per, me = min(a.M, mb + per);
+  // rows per wave, a multiple of 32
+  const int per = ((a.M + kOuterWaves * 32 - 1) / (kOuterWaves * 32)) * 32;
+  const int mb = min(a.M, w * per), me = min(a.M, mb + per);
   floatx4 acc[JT];
 #pragma unroll
   for (int jt = 0; jt < JT; ++jt) acc[jt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int m = mb; m < me; m += 32) {
-    float xv[8], pv[JT][8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int mr = m + 4 * t + g;
-      const bool ok = mr < me;
-      const int mc = ok ? mr : mb;
-      const float x = jb.X[(int64_t)mc * jb.ldx + ci];
-      xv[t] = (ok && cok) ? x : 0.f;
-#pragma unroll
-      for (int jt = 0; jt < JT; ++jt) {
-        const int jj = 16 * jt + i;
-        const float pp = jb.P[(int64_t)mc * a.r + min(jj, a.r - 1)];
-        pv[jt][t] = (ok && jj < a.r) ? pp : 0.f;
-      }
+  if (mb < me) {
+    OuterChunk<JT> c0v, c1v;
+    outer_load(c0v, jb, a.r, mb, me, mb, ci, cok, i, g);
+    for (int m = mb; m < me; m += 64) {
+      // chunks past me load clamped rows and are multiplied as zeros
+      outer_load(c1v, jb, a.r, m + 32, me, mb, ci, cok, i, g);
+      outer_mfma(acc, c0v);
+      if (m + 32 >= me) break;
+      outer_load(c0v, jb, a.r, m + 64, me, mb, ci, cok, i, g);
+      outer_mfma(acc, c1v);
     }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int jt = 0; jt < JT; ++jt)
-        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t], pv[jt][t], acc[jt], 0, 0, 0);
   }
   if (w > 0) {
 #pragma unroll
@@ -203,7 +234,7 @@ __global__ __launch_bounds__(512) void rank_outer_mfma(OuterArgs a) {
   for (int jt = 0; jt < JT; ++jt) {
     floatx4 v = acc[jt];
 #pragma unroll
-    for (int q = 0; q < 7; ++q) v += red[q][jt][lane];
+    for (int q = 0; q < kOuterWaves - 1; ++q) v += red[q][jt][lane];
     const int j = 16 * jt + i;
     if (j >= a.r) continue;
 #pragma unroll
@@ -214,6 +245,228 @@ __global__ __launch_bounds__(512) void rank_outer_mfma(OuterArgs a) {
       *o = a.accumulate ? fmaf(a.scale, v[e], *o) : a.scale * v[e];
     }
   }
+}
+
+// ---- batched LoRA work ---------------------------------------------------------
+// W_eff[k][n] = W[k][n] + scale·Σ_j A[j][k]·B[n][j].  A workgroup owns 16
+// rows × 256 columns of one job; a thread takes 4 rows × 4 columns (the
+// A values of its rows are wave-uniform, its B rows are 4·R contiguous
+// floats).  HBM-bound: reads W once, writes W_eff once.
+template <int R>
+__global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restrict__ jobs, int njobs, float scale) {
+  const int t = blockIdx.x;
+  int lo = 0, hi = njobs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (jobs[mid].tile0 <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const MergeJob jb = jobs[lo];
+  const int tiles_n = (jb.N + 255) / 256;
+  const int tt = t - jb.tile0;
+  const int k0 = (tt / tiles_n) * 16 + 4 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = (tt % tiles_n) * 256 + 4 * (threadIdx.x & 63);
+  if (n >= jb.N) return;
+  float bv[4][R];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int j4 = 0; j4 < R / 4; ++j4) {
+      const floatx4 b4 = *reinterpret_cast<const floatx4*>(jb.B + (int64_t)(n + e) * R + 4 * j4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bv[e][4 * j4 + u] = b4[u];
+    }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k = k0 + q;
+    if (k >= jb.K) break;
+    floatx4 w;
+    if (jb.f16) w = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
+    else w = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
+    float a[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) a[j] = jb.A[(int64_t)j * jb.K + k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < R; ++j) d = fmaf(a[j], bv[e][j], d);
+      w[e] = fmaf(scale, d, w[e]);
+    }
+    *reinterpret_cast<floatx4*>(jb.out + (int64_t)k * jb.N + n) = w;
+  }
+}
+
+// Batched rank-r products: each 1024-thread workgroup runs one job's share.
+//
+// Projection role (out[M,r] = X·Y): 16 rows per workgroup on the matrix
+// cores, K split over the 16 waves in 16-wide blocks (four blocks' loads
+// issued before their MFMAs), wave partials summed in LDS in wave order.
+// Lane (i, g) feeds A = X[m0+i][k0+4g+t] (one 128-bit load per four MFMAs)
+// and B = Y(k0+4g+t, 16·jt+i); it ends holding D[m0+4g+v][16·jt+i].  Y is
+// read once per 16 rows.
+//
+// Outer role (out(j,c) (+)= s·Σ_m P[m,j]·X[m,c]): 16·kBatchCT columns per
+// workgroup (a wave's loads of one row cover whole 128-byte lines), M split
+// over the 16 waves in 32-row chunks with the next chunk's loads in flight,
+// LDS reduction in wave order, column runs per XCD.
+constexpr int kBatchCT = 2;
+
+template <int R>
+__device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floatx4* lds) {
+  constexpr int JT = (R + 15) / 16;
+  floatx4 (*red)[JT][64] = reinterpret_cast<floatx4 (*)[JT][64]>(lds);  // [kOuterWaves-1]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int m0 = b * 16;
+  const int xrow = min(m0 + i, M - 1);
+  const int K = jb.K;
+  const int nkb = (K + 15) / 16;
+  const int per = (nkb + kOuterWaves - 1) / kOuterWaves;
+  const int kb0 = min(nkb, w * per), kb1 = min(nkb, kb0 + per);
+  floatx4 acc[JT];
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = kb0; kb < kb1; kb += 4) {
+    floatx4 xa[4], yb[4][JT];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = 16 * (kb + u) + 4 * g;
+      const bool ok = kb + u < kb1 && k < K;
+      const int kc = ok ? k : 0;  // K is a multiple of 4: k..k+3 stay inside a row
+      const floatx4 xv = *reinterpret_cast<const floatx4*>(jb.X + (int64_t)xrow * jb.ldx + kc);
+      xa[u] = ok ? xv : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const int j = min(16 * jt + i, R - 1);
+        floatx4 y;
+        if (jb.y_rk) {
+          y = *reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + kc);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) y[t] = jb.Y[(int64_t)(kc + t) * R + j];
+        }
+        yb[u][jt] = (ok && 16 * jt + i < R) ? y : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt)
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[u][t], yb[u][jt][t], acc[jt], 0, 0, 0);
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) red[w - 1][jt][lane] = acc[jt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) {
+    floatx4 v = acc[jt];
+#pragma unroll
+    for (int q = 0; q < kOuterWaves - 1; ++q) v += red[q][jt][lane];
+    const int j = 16 * jt + i;
+    if (j >= R) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + 4 * g + e;
+      if (m < M) jb.out[(int64_t)m * R + j] = v[e];
+    }
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, floatx4* lds) {
+  constexpr int JT = (R + 15) / 16;
+  constexpr int CT = kBatchCT;
+  floatx4 (*red)[CT][JT][64] = reinterpret_cast<floatx4 (*)[CT][JT][64]>(lds);  // [kOuterWaves-1]
+  const int blk = (raw % 8) * (jb.blocks / 8) + raw / 8;
+  const int c0 = blk * 16 * CT;
+  if (c0 >= jb.K) return;  // whole workgroup, before any barrier
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int per = ((M + kOuterWaves * 32 - 1) / (kOuterWaves * 32)) * 32;
+  const int mb = min(M, w * per), me = min(M, mb + per);
+  floatx4 acc[CT][JT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (mb < me) {
+    OuterChunk<JT> c0v[CT], c1v[CT];
+    OuterJob o[CT];
+    int ci[CT];
+    bool cok[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      o[ct] = OuterJob{};
+      o[ct].P = jb.Y; o[ct].X = jb.X; o[ct].ldx = jb.ldx; o[ct].C = jb.K;
+      ci[ct] = min(c0 + 16 * ct + i, jb.K - 1);
+      cok[ct] = c0 + 16 * ct + i < jb.K;
+      outer_load(c0v[ct], o[ct], R, mb, me, mb, ci[ct], cok[ct], i, g);
+    }
+    for (int m = mb; m < me; m += 64) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) outer_load(c1v[ct], o[ct], R, m + 32, me, mb, ci[ct], cok[ct], i, g);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) outer_mfma(acc[ct], c0v[ct]);
+      if (m + 32 >= me) break;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) outer_load(c0v[ct], o[ct], R, m + 64, me, mb, ci[ct], cok[ct], i, g);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) outer_mfma(acc[ct], c1v[ct]);
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) red[w - 1][ct][jt][lane] = acc[ct][jt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      floatx4 v = acc[ct][jt];
+#pragma unroll
+      for (int q = 0; q < kOuterWaves - 1; ++q) v += red[q][ct][jt][lane];
+      const int j = 16 * jt + i;
+      if (j >= R) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = c0 + 16 * ct + 4 * g + e;
+        if (c >= jb.K) continue;
+        float* out = jb.out + (int64_t)j * jb.osj + (int64_t)c * jb.osc;
+        *out = jb.accumulate ? fmaf(jb.scale, v[e], *out) : jb.scale * v[e];
+      }
+    }
+}
+
+template <int R>
+__global__ __launch_bounds__(64 * kOuterWaves) void rank_batch_kernel(const RankJob* __restrict__ jobs, int njobs,
+                                                                     int nproj, int M) {
+  constexpr int JT = (R + 15) / 16;
+  __shared__ floatx4 lds[(kOuterWaves - 1) * kBatchCT * JT * 64];
+  const int pb = (M + 15) / 16;
+  int b = blockIdx.x;
+  if (b < nproj * pb) {
+    const int ji = b / pb;
+    batch_proj<R>(jobs[ji], b - ji * pb, M, lds);
+    return;
+  }
+  b -= nproj * pb;
+  int lo = nproj, hi = njobs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (jobs[mid].block0 <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  batch_outer<R>(jobs[lo], b - jobs[lo].block0, M, lds);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -227,15 +480,47 @@ void proj_vec(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y
 }
 
 void outer_launch(hipStream_t s, OuterArgs& a) {
-  a.job[0].blocks = (int)cdiv(a.job[0].C, 16);
-  a.job[1].blocks = a.job[1].out ? (int)cdiv(a.job[1].C, 16) : 0;
-  const dim3 grid((unsigned)(a.job[0].blocks + a.job[1].blocks)), block(512);
+  // column blocks of 16, padded to a multiple of 8 (one run per XCD)
+  a.job[0].blocks = (int)cdiv(cdiv(a.job[0].C, 16), 8) * 8;
+  a.job[1].blocks = a.job[1].out ? (int)cdiv(cdiv(a.job[1].C, 16), 8) * 8 : 0;
+  const dim3 grid((unsigned)(a.job[0].blocks + a.job[1].blocks)), block(64 * kOuterWaves);
   if (a.r <= 16) hipLaunchKernelGGL(rank_outer_mfma<1>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(rank_outer_mfma<2>, grid, block, 0, s, a);
   MFT_LAUNCH_CHECK();
 }
 
 }  // namespace
+
+size_t merge_tiles(int K, int N) { return (size_t)cdiv(K, 16) * (size_t)cdiv(N, 256); }
+
+void lora_merge(hipStream_t s, const MergeJob* jobs, int njobs, int total_tiles, int r, float scale) {
+  MFT_CHECK_ARG(jobs && njobs > 0 && total_tiles > 0, "empty merge");
+  const dim3 grid((unsigned)total_tiles), block(256);
+  switch (r) {
+    case 4: hipLaunchKernelGGL(lora_merge_kernel<4>, grid, block, 0, s, jobs, njobs, scale); break;
+    case 8: hipLaunchKernelGGL(lora_merge_kernel<8>, grid, block, 0, s, jobs, njobs, scale); break;
+    case 16: hipLaunchKernelGGL(lora_merge_kernel<16>, grid, block, 0, s, jobs, njobs, scale); break;
+    case 32: hipLaunchKernelGGL(lora_merge_kernel<32>, grid, block, 0, s, jobs, njobs, scale); break;
+    default: MFT_CHECK_ARG(false, "merged LoRA takes r in {4, 8, 16, 32}");
+  }
+  MFT_LAUNCH_CHECK();
+}
+
+int rank_outer_blocks(int C) { return (int)cdiv(cdiv(C, 16 * kBatchCT), 8) * 8; }
+
+void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r) {
+  MFT_CHECK_ARG(jobs && njobs > 0 && M > 0, "empty rank batch");
+  const int64_t blocks = (int64_t)nproj * cdiv(M, 16) + outer_blocks;
+  const dim3 grid((unsigned)blocks), block(64 * kOuterWaves);
+  switch (r) {
+    case 4: hipLaunchKernelGGL(rank_batch_kernel<4>, grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 8: hipLaunchKernelGGL(rank_batch_kernel<8>, grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 16: hipLaunchKernelGGL(rank_batch_kernel<16>, grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 32: hipLaunchKernelGGL(rank_batch_kernel<32>, grid, block, 0, s, jobs, njobs, nproj, M); break;
+    default: MFT_CHECK_ARG(false, "batched rank-r work takes r in {4, 8, 16, 32}");
+  }
+  MFT_LAUNCH_CHECK();
+}
 
 void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64_t ysk,
                int64_t ysj, int M, int K, int r, float* out) {
@@ -246,7 +531,7 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64
   const bool vec = (r == 4 || r == 8 || r == 16 || r == 32) && (y_rk || y_kr) && K % 4 == 0 && ldx % 4 == 0 &&
                    aligned16(X) && aligned16(Y);
   if (vec) {
-    // one row per workgroup (measured fastest at M = 512–1024 for r = 8)
+    // one row per workgroup
     if (r == 4) proj_vec<4, 1>(s, X, ldx, Y, y_rk, M, K, out);
     else if (r == 8) proj_vec<8, 1>(s, X, ldx, Y, y_rk, M, K, out);
     else if (r == 16) proj_vec<16, 1>(s, X, ldx, Y, y_rk, M, K, out);
