@@ -775,7 +775,7 @@ struct Plan {
   int bm, bn, splits;
 };
 
-int plan_bk(int bm, int bn) { return (bm == 64 && (bn == 64 || bn == 1)) ? 64 : 32; }
+int plan_bk(int bm, int bn) { return ((bm == 64 || bm == 128) && (bn == 64 || bn == 1)) ? 64 : 32; }
 
 // Tile shape and split-K, from sweeps of the benchmark shapes on MI355X
 // (M = 512 tokens): grids of ≥ 512 64×64 tiles run unsplit; smaller grids
@@ -841,7 +841,7 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
     int bm = 0, bn = 0, sp = 0;
     if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
-         ((bm == 64 && (bn == 0 || bn == 1)) || (bm == 32 && bn == 0))) &&
+         (((bm == 64 || bm == 128) && (bn == 0 || bn == 1)) || (bm == 32 && bn == 0))) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
@@ -852,7 +852,9 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   if (splits > 1) p.partial = ws.ptr;
 
   if (ev && ev->start) MFT_HIP(hipEventRecord(ev->start, s));
-  if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
+  if (pl.bm == 128 && pl.bn == 0) launch_q<128, 32>(s, p, b_nk, b_f16, splits);
+  else if (pl.bm == 128 && pl.bn == 1) launch_q<128, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 128) launch_tile<64, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 64) launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 1) launch_q<64, 64>(s, p, b_nk, b_f16, splits);
