@@ -41,6 +41,18 @@ void set_last_error(const std::string& msg);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// GELU, tanh approximation (GPT-2's gelu_new), and its derivative.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;  // sqrt(2/pi)
+  return 0.5f * x * (1.f + tanhf(c * fmaf(0.044715f * x, x * x, x)));
+}
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * fmaf(0.044715f * x, x * x, x));
+  const float du = c * fmaf(3.f * 0.044715f, x * x, 1.f);
+  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * du;
+}
+
 // IEEE fp16 bits → fp32 (exact), one value and four packed in a uint2.
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -61,6 +73,12 @@ struct GemmEpilogue {
   int r = 0;
   int64_t qsn = 0, qsj = 0;
   float lscale = 0.f;
+  // GELU (tanh form) fused into the output, for GPT-2's MLP:
+  //   gelu_out:     C keeps the pre-activation v, gelu_out[m·ldc + n] = gelu(v);
+  //   gelu_grad_of: C = v · gelu'(gelu_grad_of[m·ldc + n]), i.e. the gradient
+  //                 of the activation's input from that of its output.
+  float* gelu_out = nullptr;
+  const float* gelu_grad_of = nullptr;
   // Call site: 0 = a layer's linear GEMM, 1 = the LM head.  Selects a
   // separately named (otherwise identical) kernel instantiation so kernel
   // traces and counter profiles attribute the two apart.

@@ -118,16 +118,6 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
 }
 
 // ---- activations ---------------------------------------------------------------
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float c = 0.7978845608028654f;
-  return 0.5f * x * (1.f + tanhf(c * fmaf(0.044715f * x, x * x, x)));
-}
-__device__ __forceinline__ float gelu_tanh_grad(float x) {
-  const float c = 0.7978845608028654f;
-  const float t = tanhf(c * fmaf(0.044715f * x, x * x, x));
-  const float du = c * fmaf(3.f * 0.044715f, x * x, 1.f);
-  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * du;
-}
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 __device__ __forceinline__ float silu_grad(float x) {
   const float s = 1.f / (1.f + expf(-x));

@@ -590,14 +590,17 @@ void collect_timing(mft_model_s* m) {
 // ---- building blocks ---------------------------------------------------------------
 float lscale(const mft_model_s* m) { return m->c.lora_alpha / (float)m->c.lora_r; }
 
+// y = x·W (+ LoRA) + bias (+ resid); with gelu_out, y keeps the
+// pre-activation and gelu_out receives GELU(y) (GPT-2 c_fc).
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
-             const float* resid) {
+             const float* resid, float* gelu_out = nullptr) {
   const Param& W = m->P[l.W];
   const bool lora = l.A >= 0;
   const int r = lora ? m->c.lora_r : 0;
   GemmEpilogue ep;
   ep.bias = l.b >= 0 ? static_cast<const float*>(m->P[l.b].data) : nullptr;
   ep.resid = resid;
+  ep.gelu_out = gelu_out;
   if (lora && m->merged) {  // y = x·W_eff (+ bias, residual)
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
     gemm(m->stream, x, l.K, l.weff, l.N, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
@@ -619,15 +622,18 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
 }
 
+// dx = dy·Wᵀ (+ LoRA); with gelu_grad_of = the pre-activation that fed a
+// GELU into this layer, dx is the gradient of that pre-activation instead.
 void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, const float* xa,
-             int64_t M, float* dx) {
+             int64_t M, float* dx, const float* gelu_grad_of = nullptr) {
   const Param& W = m->P[l.W];
   const bool lora = l.A >= 0;
   if (lora && m->merged) {  // dX = dY·W_effᵀ; dA/dB come from the batched launches
     if (dx) {
+      GemmEpilogue ep;
+      ep.gelu_grad_of = gelu_grad_of;
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
-      gemm(m->stream, dy, l.N, l.weff, l.N, true, false, dx, l.K, (int)M, l.K, l.N, GemmEpilogue(), m->ws,
-           t.events());
+      gemm(m->stream, dy, l.N, l.weff, l.N, true, false, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
     }
     return;
   }
@@ -642,6 +648,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
   }
   if (dx) {
     GemmEpilogue ep;
+    ep.gelu_grad_of = gelu_grad_of;
     if (lora) {
       ep.P = U;
       ep.Q = static_cast<const float*>(m->P[l.A].data);
@@ -722,8 +729,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       attention_fwd(m, a, li, mask, nseq, S);
       lin_fwd(m, L.lin[G_PROJ], a.att, M, a.hmid, a.xa[G_PROJ], a.x);  // residual fused
       layernorm_fwd(s, a.hmid, pd<float>(m, L.n2w), pd<float>(m, L.n2b), M, d, c.norm_eps, a.n2, a.mean2, a.rstd2);
-      lin_fwd(m, L.lin[G_FC], a.n2, M, a.gate, a.xa[G_FC], nullptr);
-      glu_fwd(s, a.gate, nullptr, M * c.d_ff, 0, a.act);
+      lin_fwd(m, L.lin[G_FC], a.n2, M, a.gate, a.xa[G_FC], nullptr, a.act);  // GELU fused
       lin_fwd(m, L.lin[G_FC2], a.act, M, hout, a.xa[G_FC2], a.hmid);  // residual fused
       continue;
     }
@@ -823,8 +829,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     // U = dY·B and dB += s·dYᵀ·xa of each LoRA group as soon as its dY exist
     run_batch(m, L.dy_batch[LG_MLP_OUT], M);
     if (gpt2) {
-      lin_bwd(m, L.lin[G_FC2], dmo, a.act, a.xa[G_FC2], M, m->dact);
-      glu_bwd(s, m->dact, a.gate, nullptr, nf, 0, m->dgate, nullptr);
+      lin_bwd(m, L.lin[G_FC2], dmo, a.act, a.xa[G_FC2], M, m->dgate, a.gate);  // GELU' fused
       run_batch(m, L.dy_batch[LG_MLP_IN], M);
       lin_bwd(m, L.lin[G_FC], m->dgate, a.n2, a.xa[G_FC], M, m->dn);
       layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, m->dh, true);

@@ -62,6 +62,17 @@ __device__ __forceinline__ float epilogue_value(const GemmEpilogue& ep, float ac
   return v;
 }
 
+// Final value of C[m][n] (epilogue_value, then the fused GELU variants) and
+// its store; with gelu_out also stores the activation.
+__device__ __forceinline__ void epilogue_store(const GemmEpilogue& ep, float acc, int m, int n, float* C,
+                                               int64_t ldc) {
+  const int64_t at = (int64_t)m * ldc + n;
+  float v = epilogue_value(ep, acc, m, n, C, ldc);
+  if (ep.gelu_grad_of) v *= gelu_tanh_grad(ep.gelu_grad_of[at]);
+  C[at] = v;
+  if (ep.gelu_out) ep.gelu_out[at] = gelu_tanh(v);
+}
+
 template <int BM, int BN, int BK, bool B_NK, bool B_F16, int SITE>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   constexpr int NWM = BM / 64, NWN = BN / 64;  // 64×64 sub-tiles
@@ -340,7 +351,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         if (split_out)
           p.partial[((int64_t)split * p.M + m) * p.N + n] = v;
         else
-          p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, v, m, n, p.C, p.ldc);
+          epilogue_store(p.ep, v, m, n, p.C, p.ldc);
       }
     }
     return;
@@ -361,7 +372,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         if (split_out)
           p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][e];
         else
-          p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, acc[a][b][e], m, n, p.C, p.ldc);
+          epilogue_store(p.ep, acc[a][b][e], m, n, p.C, p.ldc);
       }
     }
 }
@@ -690,7 +701,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
         if (split_out)
           p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][v];
         else
-          p.C[(int64_t)m * p.ldc + n] = epilogue_value(p.ep, acc[a][b][v], m, n, p.C, p.ldc);
+          epilogue_store(p.ep, acc[a][b][v], m, n, p.C, p.ldc);
       }
     }
 }
@@ -710,12 +721,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
       floatx4 s = *reinterpret_cast<const floatx4*>(src);
       for (int z = 1; z < splits; ++z) s += *reinterpret_cast<const floatx4*>(src + (int64_t)z * total);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) C[(int64_t)m * ldc + n0 + e] = epilogue_value(ep, s[e], m, n0 + e, C, ldc);
+      for (int e = 0; e < 4; ++e) epilogue_store(ep, s[e], m, n0 + e, C, ldc);
     } else {
       for (int e = 0; e < 4 && n0 + e < N; ++e) {
         float s = 0.f;
         for (int z = 0; z < splits; ++z) s += src[(int64_t)z * total + e];
-        C[(int64_t)m * ldc + n0 + e] = epilogue_value(ep, s, m, n0 + e, C, ldc);
+        epilogue_store(ep, s, m, n0 + e, C, ldc);
       }
     }
   }
