@@ -706,6 +706,204 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     }
 }
 
+// Pipelined form of gemm_q_kernel for whole 32-deep panels and no rank-r
+// panel.  Panel p lives in LDS stage p % 3 of a three-stage ring, and is
+// stored one step earlier than in gemm_q_kernel, so during step k every wave
+// can already read the first 16-wide fragments of panel k+1 (made visible by
+// the barrier ending step k-1): a step's MFMAs start on fragments that are
+// in registers, and the second half's LDS reads are hidden behind the first
+// half's MFMAs.  Global loads run four panels ahead through two register
+// sets (panel p in set p % 2, stored two steps after it is loaded).  One
+// barrier per step orders both the stores of panel k+2 before their reads
+// in step k+1 and the reads of stage k % 3 before it is rewritten in step
+// k+1.  Panels past the end load the last panel (in bounds) and are stored
+// as zeros on the A side.
+template <int BM, bool B_NK, bool B_F16, int SITE>
+__global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
+  constexpr int BK = 32, BN = 64;
+  constexpr int WA = BM / 32;
+  constexpr int PA = BK + 4;
+  constexpr int PB = B_NK ? BK + 4 : BN + 4;
+  constexpr int A_ITEMS = BM * BK / 4 / 256;
+  constexpr int B_ITEMS = BN * BK / 4 / 256;
+  constexpr int A_STAGE = BM * PA;
+  constexpr int B_STAGE = B_NK ? BN * PB : BK * PB;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  constexpr int BES = B_F16 ? 2 : 4;
+  static_assert(A_ITEMS >= 1 && B_ITEMS >= 1, "tile config");
+  __shared__ __attribute__((aligned(16))) float smem[3 * STAGE];
+
+  const int wg = blockIdx.x;
+  const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
+  if (tile >= p.tiles_m * p.tiles_n) return;
+  const int tm_idx = tile % p.tiles_m;
+  const int tn_idx = tile / p.tiles_m;
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int split = blockIdx.y;
+  const int kbeg = split * p.k_chunk;
+  const int kend = min(p.K, kbeg + p.k_chunk);
+  const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * 32;
+  const int li = lane & 15, lg = lane >> 4;
+
+  floatx4 acc[WA][2];
+#pragma unroll
+  for (int a = 0; a < WA; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // per-thread global addresses, fixed up to the panel offset
+  const float* a_ptr[A_ITEMS];
+  const char* b_ptr[B_ITEMS];
+  int a_lds[A_ITEMS], b_lds[B_ITEMS];  // LDS offsets (floats) within a stage
+#pragma unroll
+  for (int it = 0; it < A_ITEMS; ++it) {
+    const int flat = tid + 256 * it;
+    const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+    a_ptr[it] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + kq;
+    a_lds[it] = row * PA + kq;
+  }
+#pragma unroll
+  for (int it = 0; it < B_ITEMS; ++it) {
+    const int flat = tid + 256 * it;
+    if constexpr (B_NK) {
+      const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
+      b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)min(n0 + row, p.N - 1) * p.ldb + kq) * BES;
+      b_lds[it] = A_STAGE + row * PB + kq;
+    } else {
+      const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
+      const int gn = n0 + nq < p.N ? n0 + nq : 0;
+      b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)k * p.ldb + gn) * BES;
+      b_lds[it] = A_STAGE + k * PB + nq;
+    }
+  }
+
+  floatx4 rs[2][A_ITEMS + B_ITEMS];  // register staging sets
+  auto gload = [&](auto sc, int panel) {
+    constexpr int S = decltype(sc)::value;
+    const int kc = min(kbeg + panel * BK, kend - BK);
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) rs[S][it] = *reinterpret_cast<const floatx4*>(a_ptr[it] + kc);
+    const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) {
+      if constexpr (B_F16) rs[S][A_ITEMS + it] = widen4(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
+      else rs[S][A_ITEMS + it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
+    }
+  };
+  auto lstore = [&](auto sc, int stage, int panel) {
+    constexpr int S = decltype(sc)::value;
+    float* st = smem + stage * STAGE;
+    const float keep = panel < nk ? 1.f : 0.f;  // past-end panels multiply as zeros
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + a_lds[it]) = rs[S][it] * keep;
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + b_lds[it]) = rs[S][A_ITEMS + it];
+  };
+  struct Frags {
+    floatx4 a[WA], b[2];
+  };
+  auto read_frags = [&](Frags& f, int stage, int kb) {
+    const float* as = smem + stage * STAGE;
+    const float* bs = as + A_STAGE;
+#pragma unroll
+    for (int a = 0; a < WA; ++a)
+      f.a[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int col = wn + 16 * b + li;
+      if constexpr (B_NK) {
+        f.b[b] = *reinterpret_cast<const floatx4*>(bs + col * PB + kb + 4 * lg);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) f.b[b][t] = bs[(kb + 4 * lg + t) * PB + col];
+      }
+    }
+  };
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int a = 0; a < WA; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[a][t], f.b[b][t], acc[a][b], 0, 0, 0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  Frags pf, f1;
+  int s_cur = 0, s_nxt = 1, s_st = 2;  // stages of panels k, k+1, k+2 (wave-uniform)
+  // LDS read instructions per read_frags (the column reads of a [K,N] B pair
+  // up into ds_read2_b32) and the schedule of one step: f1's reads, pf's 16
+  // MFMAs, the next panel's reads, then f1's 16 MFMAs with the LDS stores and
+  // global loads interleaved.
+  constexpr int N_RD = WA + (B_NK ? 2 : 4);
+  constexpr int N_ST = A_ITEMS + B_ITEMS;
+  constexpr int N_MF = 4 * WA * 2;  // MFMAs per 16-wide k block
+  static_assert(N_MF >= 2 * N_ST, "schedule");
+  auto step = [&](auto sc, int kt) {
+    read_frags(f1, s_cur, 16);     // second half of panel k
+    mfmas(pf);                     // first half of panel k (fragments read last step)
+    read_frags(pf, s_nxt, 0);      // first half of panel k+1 (visible since the last barrier)
+    lstore(sc, s_st, kt + 2);      // panel k+2, loaded two steps ago
+    gload(sc, kt + 4);             // panel k+4 into the same register set
+    mfmas(f1);
+    __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, N_MF, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
+#pragma unroll
+    for (int i = 0; i < N_ST; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < N_ST; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, N_MF - 2 * N_ST, 0);
+    __syncthreads();
+    const int t = s_cur;
+    s_cur = s_nxt;
+    s_nxt = s_st;
+    s_st = t;
+  };
+  gload(I0{}, 0);
+  gload(I1{}, 1);
+  lstore(I0{}, 0, 0);
+  lstore(I1{}, 1, 1);
+  gload(I0{}, 2);
+  gload(I1{}, 3);
+  __syncthreads();
+  read_frags(pf, 0, 0);
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(I0{}, kt);
+    step(I1{}, kt + 1);  // when nk is odd this multiplies the zero panel nk
+  }
+
+  const bool split_out = p.partial != nullptr;
+#pragma unroll
+  for (int a = 0; a < WA; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int n = n0 + wn + 16 * b + li;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm + 16 * a + 4 * lg + v;
+        if (m >= p.M) continue;
+        if (split_out)
+          p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][v];
+        else
+          epilogue_store(p.ep, acc[a][b][v], m, n, p.C, p.ldc);
+      }
+    }
+}
+
 // Sum of the split-K partials in split order plus the epilogue.  Rows are
 // blockIdx.y; each thread takes four consecutive columns (128-bit partial
 // loads when N is a multiple of 4).
@@ -756,6 +954,18 @@ void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, 
   }
 }
 
+template <int BM, int SITE>
+void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
+  const dim3 block(256);
+  if (b_nk) {
+    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, true, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_p_kernel<BM, true, false, SITE>), grid, block, 0, s, p);
+  } else {
+    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, false, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_p_kernel<BM, false, false, SITE>), grid, block, 0, s, p);
+  }
+}
+
 template <int BM, int BK>
 void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
@@ -763,6 +973,26 @@ void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   const dim3 grid(p.tiles_per_xcd * 8, splits);
+  // The pipelined kernel takes whole 32-deep panels in every split and no
+  // rank-r panel; it is used for [N,K] B operands (the dX products), where
+  // cold-cache sweeps of the layer shapes measured it 0–20% faster, while
+  // for [K,N] B (column-read fragments) it measured 0–4% slower.  Tuning
+  // hook: MFT_GEMM_PIPE=0 keeps gemm_q_kernel, 2 uses the pipelined kernel
+  // for both layouts.
+  static const int pipe_mode = [] {
+    const char* e = getenv("MFT_GEMM_PIPE");
+    return e ? atoi(e) : 1;
+  }();
+  const bool pipe_ok = pipe_mode == 2 || (pipe_mode == 1 && b_nk);
+  if constexpr (BK == 32 && BM <= 64) {
+    const bool whole = p.k_chunk % 32 == 0 && p.K % 32 == 0;
+    if (pipe_ok && whole && p.ep.P == nullptr) {
+      if (p.ep.site == 1) launch_p_variant<BM, 1>(s, p, grid, b_nk, b_f16);
+      else launch_p_variant<BM, 0>(s, p, grid, b_nk, b_f16);
+      MFT_LAUNCH_CHECK();
+      return;
+    }
+  }
   if (p.ep.site == 1) launch_q_variant<BM, BK, 1>(s, p, grid, b_nk, b_f16);
   else launch_q_variant<BM, BK, 0>(s, p, grid, b_nk, b_f16);
   MFT_LAUNCH_CHECK();

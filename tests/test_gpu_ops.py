@@ -115,6 +115,34 @@ def test_lora_linear_fp16_weight(M, K, N):
     assert rel_err(h(dB), dB_ref) < TOL
 
 
+PIPE_SHAPES = [
+    (512, 1024, 4096, False),  # 64x64 tiles, 32 whole panels
+    (512, 1024, 1024, False),  # 32x64 tiles
+    (200, 96, 300, False),     # three panels (odd count), ragged M and N
+    (512, 4096, 1024, False),  # split-K: whole panels in every split
+    (128, 1152, 1024, True),   # fp16 W widened in the pipelined tile load
+]
+
+
+@pytest.mark.parametrize("M,K,N,f16", PIPE_SHAPES)
+def test_plain_linear_pipelined(M, K, N, f16):
+    """Linears without a rank-r panel whose K splits into whole 32-deep panels:
+    dX (W as the [N,K] operand of dY·Wᵀ) runs the three-stage pipelined GEMM,
+    the forward (W as [K,N]) the two-stage one; both against the oracle,
+    including an odd panel count, split-K and fp16 W."""
+    print(f"pipelined gemm M={M} K={K} N={N} f16={f16}", flush=True)
+    x, dy, b = rn(M, K), rn(M, N), rn(N)
+    W = rn(K, N, std=0.03)
+    Wd = W.astype(np.float16) if f16 else W
+    Wf = Wd.astype(np.float32)
+    y_ref, _ = O.lora_linear_fwd(x, Wf, b, None, None, 1.0)
+    y, _ = ops.lora_linear_fwd(g(x), g(Wd), g(b), None, None, 1.0)
+    assert rel_err(h(y), y_ref) < TOL
+    dx_ref, _, _ = O.lora_linear_bwd(dy, x, Wf, None, None, None, 1.0)
+    dx, _, _ = ops.lora_linear_bwd(g(dy), g(x), g(Wd), None, None, None, 1.0)
+    assert rel_err(h(dx), dx_ref) < TOL
+
+
 def test_lm_head_shapes_odd_vocab():
     """LM-head-shaped product with an odd output width (V = 5003); the
     reduction over an odd V (dH = dlogits·E) runs inside the engine on a
