@@ -280,7 +280,7 @@ int mft_layernorm_bwd(mft_handle h, const float* dy, const float* x,
                       int64_t M, int64_t C, float* dx, int accumulate) {
   return guarded([&] {
     require_handle(h);
-    mft::layernorm_bwd(h->stream, dy, x, g, mean, rstd, M, C, dx, accumulate != 0);
+    mft::layernorm_bwd(h->stream, dy, x, g, mean, rstd, M, C, dx, accumulate != 0 ? dx : nullptr);
   });
 }
 int mft_rmsnorm_fwd(mft_handle h, const float* x, const float* w, int64_t M,
@@ -296,7 +296,7 @@ int mft_rmsnorm_bwd(mft_handle h, const float* dy, const float* x,
                     int unit_offset, float* dx, int accumulate) {
   return guarded([&] {
     require_handle(h);
-    mft::rmsnorm_bwd(h->stream, dy, x, w, rstd, M, C, unit_offset != 0, dx, accumulate != 0);
+    mft::rmsnorm_bwd(h->stream, dy, x, w, rstd, M, C, unit_offset != 0, dx, accumulate != 0 ? dx : nullptr);
   });
 }
 int mft_glu_fwd(mft_handle h, const float* gate, const float* up, int64_t n,

@@ -227,26 +227,29 @@ void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,
 void layernorm_fwd(hipStream_t s, const float* x, const float* g,
                    const float* b, int64_t M, int64_t C, float eps, float* y,
                    float* mean, float* rstd);
+// dx = LayerNorm backward of dy (+ resid[M,C] when resid is not null; resid
+// may alias dx for in-place accumulation).
 void layernorm_bwd(hipStream_t s, const float* dy, const float* x,
                    const float* g, const float* mean, const float* rstd,
-                   int64_t M, int64_t C, float* dx, bool accumulate);
+                   int64_t M, int64_t C, float* dx, const float* resid);
 void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
                  int64_t C, float eps, bool unit_offset, float* y,
                  float* rstd);
+// dx = RMSNorm backward of dy (+ resid, as layernorm_bwd).
 void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
                  const float* w, const float* rstd, int64_t M, int64_t C,
-                 bool unit_offset, float* dx, bool accumulate);
+                 bool unit_offset, float* dx, const float* resid);
 // Row-loop fallbacks of the four norm launchers (elementwise.hip).
 void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g, const float* b,
                            int64_t M, int64_t C, float eps, float* y, float* mean, float* rstd);
 void layernorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x, const float* g,
                            const float* mean, const float* rstd, int64_t M, int64_t C,
-                           float* dx, bool accumulate);
+                           float* dx, const float* resid);
 void rmsnorm_fwd_rowloop(hipStream_t s, const float* x, const float* w, int64_t M, int64_t C,
                          float eps, bool unit_offset, float* y, float* rstd);
 void rmsnorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x, const float* w,
                          const float* rstd, int64_t M, int64_t C, bool unit_offset, float* dx,
-                         bool accumulate);
+                         const float* resid);
 void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
              int act, float* out);
 void glu_bwd(hipStream_t s, const float* dout, const float* gate,

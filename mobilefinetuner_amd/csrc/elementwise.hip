@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ g, const float* __restrict__ mean,
     const float* __restrict__ rstd, int64_t M, int C, float* dx,
-    int accumulate) {
+    const float* resid) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(
   for (int j = lane; j < C; j += 64) {
     const float xh = (xr[j] - mu) * rs;
     const float r = rs * (dyr[j] * g[j] - s1 - xh * s2);
-    dxr[j] = accumulate ? dxr[j] + r : r;
+    dxr[j] = resid ? resid[row * C + j] + r : r;
   }
 }
 
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ rstd, int64_t M,
-    int C, int unit_offset, float* dx, int accumulate) {
+    int C, int unit_offset, float* dx, const float* resid) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
   for (int j = lane; j < C; j += 64) {
     const float wj = unit_offset ? 1.f + w[j] : w[j];
     const float r = rs * (dyr[j] * wj - xr[j] * rs * s);
-    dxr[j] = accumulate ? dxr[j] + r : r;
+    dxr[j] = resid ? resid[row * C + j] + r : r;
   }
 }
 
@@ -406,10 +406,10 @@ void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g,
 }
 void layernorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x,
                            const float* g, const float* mean, const float* rstd,
-                           int64_t M, int64_t C, float* dx, bool accumulate) {
+                           int64_t M, int64_t C, float* dx, const float* resid) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(layernorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
-                     dy, x, g, mean, rstd, M, (int)C, dx, accumulate ? 1 : 0);
+                     dy, x, g, mean, rstd, M, (int)C, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 void rmsnorm_fwd_rowloop(hipStream_t s, const float* x, const float* w, int64_t M,
@@ -421,10 +421,10 @@ void rmsnorm_fwd_rowloop(hipStream_t s, const float* x, const float* w, int64_t 
 }
 void rmsnorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x,
                          const float* w, const float* rstd, int64_t M, int64_t C,
-                         bool unit_offset, float* dx, bool accumulate) {
+                         bool unit_offset, float* dx, const float* resid) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s,
-                     dy, x, w, rstd, M, (int)C, unit_offset ? 1 : 0, dx, accumulate ? 1 : 0);
+                     dy, x, w, rstd, M, (int)C, unit_offset ? 1 : 0, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,

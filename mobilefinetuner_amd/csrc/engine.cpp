@@ -49,14 +49,10 @@ struct Linear {
   float* weff = nullptr;  // merged weight W + s·Aᵀ·Bᵀ [K, N] fp32 (LoRA linears)
 };
 
-// Backward groups of LoRA linears whose dY are ready together (GPT-2:
-// c_fc2 | c_fc | c_proj | c_attn; Qwen2/Gemma3: down | gate, up | o | q, k, v).
-enum { LG_MLP_OUT = 0, LG_MLP_IN, LG_ATTN_OUT, LG_ATTN_IN, LG_MAX };
 
 struct Layer {
   int n1w = -1, n1b = -1, n2w = -1, n2b = -1, qn = -1, kn = -1, pan = -1, pfn = -1;
   Linear lin[T_MAX];
-  int dy_batch[LG_MAX] = {-1, -1, -1, -1};  // index into mft_model_s::batches
 };
 
 struct Acts {
@@ -64,7 +60,8 @@ struct Acts {
   float *q, *k, *v, *qraw, *kraw, *qrs, *krs;
   int64_t qs, ks, vs;
   float* xa[T_MAX];
-  float* U[T_MAX];  // dY·B of each LoRA linear (kept for dA at the end of the backward)
+  float* U[T_MAX];   // dY·B of each LoRA linear (kept for dA at the end of the backward)
+  float* DY[T_MAX];  // dY of each LoRA linear, kept until the end of the backward
   float *att, *lse, *o, *ors, *hmid, *n2, *mean2, *rstd2;
   float *gate, *up, *act, *mo, *mrs;
 };
@@ -111,7 +108,9 @@ struct mft_model_s {
   float *h_final = nullptr, *hf = nullptr, *fmean = nullptr, *frstd = nullptr;
   float* logits = nullptr;
   int64_t ldv = 0;  // logits row stride: vocab rounded up to 4 (zeroed padding)
-  float *dh = nullptr, *dtmp = nullptr, *dn = nullptr, *datt = nullptr;
+  // dh, dh2: residual-stream gradients entering a layer's MLP and attention
+  // blocks (alternating, so norm backward passes run out of place)
+  float *dh = nullptr, *dh2 = nullptr, *dtmp = nullptr, *dn = nullptr, *datt = nullptr;
   float *dq = nullptr, *dk = nullptr, *dv = nullptr, *dqkv = nullptr;
   float *dact = nullptr, *dgate = nullptr, *dup = nullptr;
   float *dtq = nullptr, *dtk = nullptr;
@@ -119,10 +118,10 @@ struct mft_model_s {
   Scratch ws;
   // Merged LoRA weights and batched rank-r work.  With `merged`, every LoRA
   // linear multiplies by W_eff = W + s·Aᵀ·Bᵀ (rebuilt by one launch at the
-  // start of each forward), and the gradients dA = s·Uᵀ·x, dB = s·dYᵀ·xa
-  // (U = dY·B, xa = x·Aᵀ) come from table-driven launches: all xa at the
-  // start of the backward, U and dB per group of linears whose dY are ready,
-  // all dA at the end.
+  // start of each forward), its dY is written to a buffer of its own and kept,
+  // and the gradients dA = s·Uᵀ·x, dB = s·dYᵀ·xa (U = dY·B, xa = x·Aᵀ) come
+  // from three table-driven launches: all xa at the start of the backward,
+  // all U and dB after the last layer, then all dA.
   bool merged = false;
   void* weff_mem = nullptr;
   void* tables = nullptr;  // device: MergeJob[n_merge], then RankJob[]
@@ -134,7 +133,7 @@ struct mft_model_s {
     double work_per_row;  // flops per token (timing)
   };
   std::vector<Batch> batches;
-  int xa_batch = -1, da_batch = -1;
+  int xa_batch = -1, udb_batch = -1, da_batch = -1;
   // device scalars: [0..63] per-micro loss sums (double), counts (int64)
   double* d_loss = nullptr;
   int64_t* d_cnt = nullptr;
@@ -296,6 +295,21 @@ float attn_scale(const mft_model_cfg& c) {
   return c.attn_scale > 0.f ? c.attn_scale : 1.f / std::sqrt((float)c.head_dim);
 }
 
+// The merged-weight LoRA path (W_eff GEMMs + batched rank-r launches) takes
+// r ∈ {4, 8, 16, 32} and LoRA linears with K and N multiples of 4.
+bool lora_mergeable(const mft_model_s* m) {
+  const int r = m->c.lora_r;
+  if (r != 4 && r != 8 && r != 16 && r != 32) return false;
+  bool any = false;
+  for (const auto& L : m->L)
+    for (const auto& l : L.lin) {
+      if (l.A < 0) continue;
+      if (l.N % 4 || l.K % 4) return false;
+      any = true;
+    }
+  return any;
+}
+
 void alloc_acts(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
   const int64_t M = m->max_tokens;
@@ -330,10 +344,12 @@ void alloc_acts(mft_model_s* m) {
         }
       }
       const Layer& L = m->L[l];
+      const bool keep_dy = lora_mergeable(m);
       for (int t = 0; t < T_MAX; ++t)
         if (L.lin[t].A >= 0) {
           a.xa[t] = b.f(M * r);
           a.U[t] = b.f(M * r);
+          if (keep_dy) a.DY[t] = b.f(M * L.lin[t].N);
         }
       a.att = b.f(M * H * hd);
       a.lse = b.f(M * H);
@@ -356,6 +372,7 @@ void alloc_acts(mft_model_s* m) {
     m->ldv = (c.vocab + 3) / 4 * 4;
     m->logits = b.f(M * m->ldv);
     m->dh = b.f(M * d);
+    m->dh2 = b.f(M * d);
     m->dtmp = b.f(M * d);
     m->dn = b.f(M * d);
     m->datt = b.f(M * H * hd);
@@ -406,22 +423,15 @@ void alloc_acts(mft_model_s* m) {
 }
 
 // ---- merged LoRA: W_eff arena and job tables --------------------------------------
-// x and dY of LoRA linear t of layer li as the backward pass sees them.
-void lora_io(mft_model_s* m, int li, int t, const float** x, const float** dy) {
+// Input x of LoRA linear t of layer li (its dY lives in A[li].DY[t]).
+const float* lora_x(mft_model_s* m, int li, int t) {
   const Acts& a = m->A[li];
-  const bool gemma = m->c.arch == MFT_ARCH_GEMMA3;
   if (m->c.arch == MFT_ARCH_GPT2) {
     const float* xs[4] = {a.n1, a.att, a.n2, a.act};
-    const float* ds[4] = {m->dqkv, m->dh, m->dgate, m->dh};
-    *x = xs[t];
-    *dy = ds[t];
-    return;
+    return xs[t];
   }
   const float* xs[T_MAX] = {a.n1, a.n1, a.n1, a.att, a.n2, a.n2, a.act};
-  const float* ds[T_MAX] = {gemma ? m->dtq : m->dq, gemma ? m->dtk : m->dk, m->dv, gemma ? m->dtmp : m->dh,
-                            m->dgate, m->dup, gemma ? m->dtmp : m->dh};
-  *x = xs[t];
-  *dy = ds[t];
+  return xs[t];
 }
 
 float lscale(const mft_model_s* m);
@@ -433,18 +443,15 @@ float lscale(const mft_model_s* m);
 void build_lora_tables(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
   const int r = c.lora_r;
-  if (r != 4 && r != 8 && r != 16 && r != 32) return;
+  if (!lora_mergeable(m)) return;
   const bool gpt2 = c.arch == MFT_ARCH_GPT2;
   const int nt = gpt2 ? 4 : T_MAX;
   size_t weff_floats = 0;
   for (auto& L : m->L)
     for (int t = 0; t < nt; ++t) {
       const Linear& l = L.lin[t];
-      if (l.A < 0) continue;
-      if (l.N % 4 || l.K % 4) return;
-      weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
+      if (l.A >= 0) weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
     }
-  if (weff_floats == 0) return;
   if (hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
     throw Error(MFT_ENOMEM, "merged LoRA weights (" + std::to_string(weff_floats * 4) + " bytes)");
   const float s = lscale(m);
@@ -485,16 +492,12 @@ void build_lora_tables(mft_model_s* m) {
     pend.push_back(p);
     return (int)pend.size() - 1;
   };
-  std::vector<RankJob> xa_jobs, da_jobs;
+  std::vector<RankJob> xa_jobs, u_jobs, db_jobs, da_jobs;
   size_t woff = 0;
   int tiles = 0;
-  static const int kGroupGpt2[4] = {LG_ATTN_IN, LG_ATTN_OUT, LG_MLP_IN, LG_MLP_OUT};
-  static const int kGroupHf[T_MAX] = {LG_ATTN_IN, LG_ATTN_IN, LG_ATTN_IN, LG_ATTN_OUT,
-                                      LG_MLP_IN, LG_MLP_IN, LG_MLP_OUT};
   for (int li = 0; li < c.n_layer; ++li) {
     Layer& L = m->L[li];
     Acts& a = m->A[li];
-    std::vector<RankJob> gp[LG_MAX], go[LG_MAX];
     for (int t = 0; t < nt; ++t) {
       Linear& l = L.lin[t];
       if (l.A < 0) continue;
@@ -506,18 +509,17 @@ void build_lora_tables(mft_model_s* m) {
       g.f16 = m->P[l.W].f16 ? 1 : 0; g.tile0 = tiles;
       tiles += (int)merge_tiles(l.K, l.N);
       mj.push_back(g);
-      const float *x, *dy;
-      lora_io(m, li, t, &x, &dy);
+      const float* x = lora_x(m, li, t);
+      const float* dy = a.DY[t];
       // xa = x·Aᵀ; U = dY·B; dB += s·dYᵀ·xa (out(j,n) = dB[n][j]); dA += s·Uᵀ·x
       xa_jobs.push_back(proj_job(x, l.K, static_cast<const float*>(m->P[l.A].data), true, a.xa[t]));
-      const int grp = gpt2 ? kGroupGpt2[t] : kGroupHf[t];
-      gp[grp].push_back(proj_job(dy, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
-      go[grp].push_back(outer_job(a.xa[t], dy, l.N, m->P[l.B].grad, 1, r));
+      u_jobs.push_back(proj_job(dy, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
+      db_jobs.push_back(outer_job(a.xa[t], dy, l.N, m->P[l.B].grad, 1, r));
       da_jobs.push_back(outer_job(a.U[t], x, l.K, m->P[l.A].grad, l.K, 1));
     }
-    for (int gi = 0; gi < LG_MAX; ++gi) L.dy_batch[gi] = add_batch(gp[gi], go[gi]);
   }
   m->xa_batch = add_batch(xa_jobs, {});
+  m->udb_batch = add_batch(u_jobs, db_jobs);
   m->da_batch = add_batch({}, da_jobs);
   const size_t mbytes = (mj.size() * sizeof(MergeJob) + 255) & ~size_t(255);
   const size_t bytes = mbytes + rj.size() * sizeof(RankJob);
@@ -803,6 +805,16 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
+  // Where dY of linear t of layer li goes: its own kept buffer for a LoRA
+  // linear on the merged path, else the shared temporary `fb`.
+  auto dyb = [&](int li, int t, float* fb) -> float* {
+    return m->merged && m->L[li].lin[t].A >= 0 ? m->A[li].DY[t] : fb;
+  };
+  // Residual-stream gradient entering layer li's MLP block (GPT-2 / Qwen2: the
+  // dY of c_fc2 / down_proj) and its attention block (dY of c_proj / o_proj).
+  // Norm backward passes write them out of place: dres_out = dres_in + ∂norm.
+  auto res_in = [&](int li) { return gemma ? m->dh : dyb(li, gpt2 ? G_FC2 : T_DOWN, m->dh); };
+  auto res_mid = [&](int li) { return gemma ? m->dh2 : dyb(li, gpt2 ? G_PROJ : T_O, m->dh2); };
   run_batch(m, m->xa_batch, M);  // xa = x·Aᵀ of every LoRA linear
   {
     // dhf = dlogits · E, E [V, d] is the [K, N] operand.
@@ -812,91 +824,100 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
          t.events());
   }
+  const int top = c.n_layer - 1;
   if (gpt2)
-    layernorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->fmean, m->frstd, M, d, m->dh, false);
+    layernorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->fmean, m->frstd, M, d, res_in(top), nullptr);
   else
-    rmsnorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->frstd, M, d, gemma, m->dh, false);
+    rmsnorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->frstd, M, d, gemma, res_in(top), nullptr);
   const int64_t nf = M * c.d_ff;
-  for (int li = c.n_layer - 1; li >= 0; --li) {
+  for (int li = top; li >= 0; --li) {
     const Layer& L = m->L[li];
     Acts& a = m->A[li];
+    float* rin = res_in(li);
+    float* rmid = res_mid(li);
+    const bool need_dx = li > 0;
     // ---- MLP block ----
-    const float* dmo = m->dh;
-    if (gemma) {
-      rmsnorm_bwd(s, m->dh, a.mo, pd<float>(m, L.pfn), a.mrs, M, d, true, m->dtmp, false);
-      dmo = m->dtmp;
-    }
-    // U = dY·B and dB += s·dYᵀ·xa of each LoRA group as soon as its dY exist
-    run_batch(m, L.dy_batch[LG_MLP_OUT], M);
     if (gpt2) {
-      lin_bwd(m, L.lin[G_FC2], dmo, a.act, a.xa[G_FC2], M, m->dgate, a.gate);  // GELU' fused
-      run_batch(m, L.dy_batch[LG_MLP_IN], M);
-      lin_bwd(m, L.lin[G_FC], m->dgate, a.n2, a.xa[G_FC], M, m->dn);
-      layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, m->dh, true);
+      float* dgate = dyb(li, G_FC, m->dgate);
+      lin_bwd(m, L.lin[G_FC2], rin, a.act, a.xa[G_FC2], M, dgate, a.gate);  // GELU' fused
+      lin_bwd(m, L.lin[G_FC], dgate, a.n2, a.xa[G_FC], M, m->dn);
+      layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, rmid, rin);
     } else {
+      const float* dmo = rin;
+      if (gemma) {
+        float* t = dyb(li, T_DOWN, m->dtmp);
+        rmsnorm_bwd(s, rin, a.mo, pd<float>(m, L.pfn), a.mrs, M, d, true, t, nullptr);
+        dmo = t;
+      }
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
-      glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, m->dgate, m->dup);
-      run_batch(m, L.dy_batch[LG_MLP_IN], M);
-      lin_bwd(m, L.lin[T_GATE], m->dgate, a.n2, a.xa[T_GATE], M, m->dn);
-      lin_bwd(m, L.lin[T_UP], m->dup, a.n2, a.xa[T_UP], M, m->dtmp);
+      float* dgate = dyb(li, T_GATE, m->dgate);
+      float* dup = dyb(li, T_UP, m->dup);
+      glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, dgate, dup);
+      lin_bwd(m, L.lin[T_GATE], dgate, a.n2, a.xa[T_GATE], M, m->dn);
+      lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dtmp);
       add_inplace(s, m->dn, m->dtmp, M * d);
-      rmsnorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.rstd2, M, d, gemma, m->dh, true);
+      rmsnorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.rstd2, M, d, gemma, rmid, rin);
     }
     // ---- attention block ----
-    const float* dox = m->dh;
+    const float* dox = rmid;
     if (gemma) {
-      rmsnorm_bwd(s, m->dh, a.o, pd<float>(m, L.pan), a.ors, M, d, true, m->dtmp, false);
-      dox = m->dtmp;
+      float* t = dyb(li, T_O, m->dtmp);
+      rmsnorm_bwd(s, rmid, a.o, pd<float>(m, L.pan), a.ors, M, d, true, t, nullptr);
+      dox = t;
     }
-    run_batch(m, L.dy_batch[LG_ATTN_OUT], M);
     lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};
-    const bool need_dx = li > 0;
     const double awork = 2.0 * 5.0 * nseq * H * (double)S * S * hd * 0.5;
+    float* rnext = need_dx ? res_in(li - 1) : nullptr;
     if (gpt2) {
+      float* dqkv = dyb(li, G_ATTN, m->dqkv);
       {
         Timed t(m, CLS_ATTN, awork);
         t.begin();
-        attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dqkv, 3 * d, m->dqkv + d,
-                 3 * d, m->dqkv + 2 * d, 3 * d, m->ws);
+        attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, dqkv, 3 * d, dqkv + d, 3 * d,
+                 dqkv + 2 * d, 3 * d, m->ws);
         t.end();
       }
-      run_batch(m, L.dy_batch[LG_ATTN_IN], M);
-      lin_bwd(m, L.lin[G_ATTN], m->dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
-      if (need_dx)
-        layernorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.mean1, a.rstd1, M, d, m->dh, true);
+      lin_bwd(m, L.lin[G_ATTN], dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
+      if (need_dx) layernorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.mean1, a.rstd1, M, d, rnext, rmid);
       continue;
     }
+    // q/k dY: after RoPE's inverse (Qwen2) or after the q/k norms' backward (Gemma3)
+    float* dq = gemma ? m->dq : dyb(li, T_Q, m->dq);
+    float* dk = gemma ? m->dk : dyb(li, T_K, m->dk);
+    float* dv = dyb(li, T_V, m->dv);
     {
       Timed t(m, CLS_ATTN, awork);
       t.begin();
-      attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, m->dq, (int64_t)H * hd, m->dk,
-               (int64_t)Hk * hd, m->dv, (int64_t)Hk * hd, m->ws);
+      attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, dq, (int64_t)H * hd, dk,
+               (int64_t)Hk * hd, dv, (int64_t)Hk * hd, m->ws);
       t.end();
     }
     const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
-    rope(s, m->dq, (int64_t)H * hd, nseq, S, H, hd, th, true);
-    rope(s, m->dk, (int64_t)Hk * hd, nseq, S, Hk, hd, th, true);
-    const float* dqx = m->dq;
-    const float* dkx = m->dk;
+    rope(s, dq, (int64_t)H * hd, nseq, S, H, hd, th, true);
+    rope(s, dk, (int64_t)Hk * hd, nseq, S, Hk, hd, th, true);
+    const float* dqx = dq;
+    const float* dkx = dk;
     if (gemma) {
-      rmsnorm_bwd(s, m->dq, a.qraw, pd<float>(m, L.qn), a.qrs, M * H, hd, true, m->dtq, false);
-      rmsnorm_bwd(s, m->dk, a.kraw, pd<float>(m, L.kn), a.krs, M * Hk, hd, true, m->dtk, false);
-      dqx = m->dtq;
-      dkx = m->dtk;
+      float* tq = dyb(li, T_Q, m->dtq);
+      float* tk = dyb(li, T_K, m->dtk);
+      rmsnorm_bwd(s, dq, a.qraw, pd<float>(m, L.qn), a.qrs, M * H, hd, true, tq, nullptr);
+      rmsnorm_bwd(s, dk, a.kraw, pd<float>(m, L.kn), a.krs, M * Hk, hd, true, tk, nullptr);
+      dqx = tq;
+      dkx = tk;
     }
-    run_batch(m, L.dy_batch[LG_ATTN_IN], M);
     lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, need_dx ? m->dn : nullptr);
     lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, need_dx ? m->dtmp : nullptr);
     if (need_dx) add_inplace(s, m->dn, m->dtmp, M * d);
-    lin_bwd(m, L.lin[T_V], m->dv, a.n1, a.xa[T_V], M, need_dx ? m->dtmp : nullptr);
+    lin_bwd(m, L.lin[T_V], dv, a.n1, a.xa[T_V], M, need_dx ? m->dtmp : nullptr);
     if (need_dx) {
       add_inplace(s, m->dn, m->dtmp, M * d);
-      rmsnorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.rstd1, M, d, gemma, m->dh, true);
+      rmsnorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.rstd1, M, d, gemma, rnext, rmid);
     }
   }
-  run_batch(m, m->da_batch, M);  // dA += s·Uᵀ·x of every LoRA linear
+  run_batch(m, m->udb_batch, M);  // U = dY·B and dB += s·dYᵀ·xa of every LoRA linear
+  run_batch(m, m->da_batch, M);   // dA += s·Uᵀ·x of every LoRA linear
 }
 
 // Hyper-parameters reach the device as kernel arguments of a one-block

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void ln_bwd_vec(const float* __restrict__ dy,
                                                   const float* __restrict__ g,
                                                   const float* __restrict__ mean,
                                                   const float* __restrict__ rstd, int64_t M, int C,
-                                                  float* dx, int accumulate) {
+                                                  float* dx, const float* resid) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
@@ -111,8 +111,8 @@ __global__ __launch_bounds__(256) void ln_bwd_vec(const float* __restrict__ dy,
     floatx4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = rs * (gv[i][e] - s1 - xv[i][e] * s2);
-    if (accumulate) {
-      const floatx4 old = *o;
+    if (resid) {
+      const floatx4 old = reinterpret_cast<const floatx4*>(resid + row * C)[qi];
 #pragma unroll
       for (int e = 0; e < 4; ++e) r[e] += old[e];
     }
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy,
                                                    const float* __restrict__ w,
                                                    const float* __restrict__ rstd, int64_t M,
                                                    int C, int unit_offset, float* dx,
-                                                   int accumulate) {
+                                                   const float* resid) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
@@ -190,8 +190,8 @@ __global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy,
     floatx4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = rs * (gv[i][e] - xv[i][e] * s);
-    if (accumulate) {
-      const floatx4 old = *o;
+    if (resid) {
+      const floatx4 old = reinterpret_cast<const floatx4*>(resid + row * C)[qi];
 #pragma unroll
       for (int e = 0; e < 4; ++e) r[e] += old[e];
     }
@@ -232,13 +232,13 @@ void layernorm_fwd(hipStream_t s, const float* x, const float* g, const float* b
 
 void layernorm_bwd(hipStream_t s, const float* dy, const float* x, const float* g,
                    const float* mean, const float* rstd, int64_t M, int64_t C, float* dx,
-                   bool accumulate) {
+                   const float* resid) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
-  if (!vec_ok(C, {dy, x, g, dx}))
-    return layernorm_bwd_rowloop(s, dy, x, g, mean, rstd, M, C, dx, accumulate);
+  if (!vec_ok(C, {dy, x, g, dx, resid}))
+    return layernorm_bwd_rowloop(s, dy, x, g, mean, rstd, M, C, dx, resid);
   const int nv = (int)cdiv(C, 256);
   MFT_NV_DISPATCH(nv, ln_bwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, dy, x, g, mean, rstd, M,
-                  (int)C, dx, accumulate ? 1 : 0);
+                  (int)C, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 
@@ -253,13 +253,13 @@ void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M, int64
 }
 
 void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x, const float* w, const float* rstd,
-                 int64_t M, int64_t C, bool unit_offset, float* dx, bool accumulate) {
+                 int64_t M, int64_t C, bool unit_offset, float* dx, const float* resid) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
-  if (!vec_ok(C, {dy, x, w, dx}))
-    return rmsnorm_bwd_rowloop(s, dy, x, w, rstd, M, C, unit_offset, dx, accumulate);
+  if (!vec_ok(C, {dy, x, w, dx, resid}))
+    return rmsnorm_bwd_rowloop(s, dy, x, w, rstd, M, C, unit_offset, dx, resid);
   const int nv = (int)cdiv(C, 256);
   MFT_NV_DISPATCH(nv, rms_bwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, dy, x, w, rstd, M,
-                  (int)C, unit_offset ? 1 : 0, dx, accumulate ? 1 : 0);
+                  (int)C, unit_offset ? 1 : 0, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 
