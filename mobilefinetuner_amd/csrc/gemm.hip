@@ -1022,15 +1022,21 @@ int plan_bk(int bm, int bn) { return ((bm == 64 || bm == 128) && (bn == 64 || bn
 // (M = 512 tokens): grids of ≥ 512 64×64 tiles run unsplit; smaller grids
 // with K < 2048 switch to 32×64 tiles (twice the workgroups, no partials);
 // deeper K keeps 64×64 tiles and doubles split-K while the grid has fewer
-// than 512 workgroups and every split keeps at least 512 of K.  Very large
-// grids (the LM head over the vocabulary) use the 128×128 kernel.
+// than 512 workgroups and every split keeps at least 512 of K.  Reductions
+// over a vocabulary (K ≥ 16384: the LM head's dH = dlogits·E) keep
+// doubling up to 16 splits and 2048 workgroups — 1.2–1.45× faster than 2–4
+// splits at the Gemma-3 / Qwen2.5 / GPT-2 vocabularies.  Very large grids
+// (the LM head's forward over the vocabulary) use the 128×128 kernel.
 Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
   if (cdiv(M, 128) * cdiv(N, 128) >= 1024) return {128, 128, 1};
   const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
   if (tiles >= 512) return {64, 0, 1};
   if (K < 2048) return {32, 0, 1};
+  const bool vocab = K >= 16384;
+  const int64_t target = vocab ? 2048 : 512;
+  const int max_sp = vocab ? 16 : 8;
   int sp = 1;
-  while (tiles * sp < 512 && K / (2 * sp) >= 512 && sp < 8 &&
+  while (tiles * sp < target && K / (2 * sp) >= 512 && sp < max_sp &&
          (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
     sp *= 2;
   return {64, 0, sp};
