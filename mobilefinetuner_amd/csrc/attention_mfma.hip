@@ -398,7 +398,7 @@ __global__ __launch_bounds__(256) void attn_delta_mfma_kernel(AttnP p) {
 // dK, dV: workgroup = 16·NW keys of one query head; wave = 16 keys.
 // ------------------------------------------------------------------------------
 template <int HD, int NW, int BQ, bool SPLIT>
-__global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
+__device__ __forceinline__ void attn_bwd_dkdv_role(const AttnP& p, int bid, float* smem) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
   constexpr int PQ = BQ + 4;
@@ -410,7 +410,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   // 128-bit read.  head_dim 256 (register and LDS budget): K/V rows stay in
   // LDS and the dV/dK operands are read by column.
   constexpr bool WIDE = HD > 128;
-  extern __shared__ __attribute__((aligned(16))) float smem[];
   float* Qs = smem;                              // [BQ][P]
   float* Gs = Qs + BQ * P;                       // [BQ][P]  dO
   float* Qt = Gs + BQ * P;                       // [HD][PQ] (not WIDE)
@@ -428,14 +427,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkdv_mfma(AttnP p) {
   // their dK/dV contributions are summed afterwards by attn_partial_sum_kernel
   // in (chunk, head) order.
   // 1-D grid, heaviest causal key blocks (the first ones) first; with a
-  // query split, item t = blockIdx / (Hq·B) is (key block, query chunk)
+  // query split, item t = bid / (Hq·B) is (key block, query chunk)
   // = (t % nkb, t / nkb).
-  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int hb = bid % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int grp = p.Hq / p.Hkv;
   const int kh = h / grp;
   const int nkb = (p.S + BKEYS - 1) / BKEYS;
-  const int item = (int)blockIdx.x / (p.Hq * p.B);
+  const int item = (int)bid / (p.Hq * p.B);
   const int k0 = (SPLIT ? item % nkb : item) * BKEYS;
   const int qc = SPLIT ? item / nkb : 0;
   const int kbase = k0 + 16 * w;
@@ -651,7 +650,7 @@ __global__ __launch_bounds__(256) void attn_dq_sum_kernel(AttnP p, int qblock) {
 // dQ: workgroup = 16·NW queries of one head; wave = 16 queries.
 // ------------------------------------------------------------------------------
 template <int HD, int NW, int BKV, bool SPLIT>
-__global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
+__device__ __forceinline__ void attn_bwd_dq_role(const AttnP& p, int bid, float* smem) {
   constexpr int NT = 64 * NW;
   constexpr int P = HD + 4;
   constexpr int PK = BKV + 4;
@@ -660,7 +659,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   // head_dim ≤ 128 also keeps a transposed copy of K for the dQ operand
   // (one 128-bit read instead of four column reads); 256 reads by column.
   constexpr bool WIDE = HD > 128;
-  extern __shared__ __attribute__((aligned(16))) float smem[];
   float* Ks = smem;                          // [BKV][P]
   float* Vs = Ks + BKV * P;                  // [BKV][P]
   float* Kt = Vs + BKV * P;                  // [HD][PK] (not WIDE)
@@ -670,12 +668,12 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int li = lane & 15, lg = lane >> 4;
   // 1-D grid, heaviest causal query blocks first; with a key split, item
-  // t = blockIdx / (Hq·B) is (query block, key chunk) = (nqb-1 - t % nqb, t / nqb).
-  const int hb = blockIdx.x % (p.Hq * p.B);
+  // t = bid / (Hq·B) is (query block, key chunk) = (nqb-1 - t % nqb, t / nqb).
+  const int hb = bid % (p.Hq * p.B);
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int nqb = (p.S + 16 * NW - 1) / (16 * NW);
   const int kh = h / (p.Hq / p.Hkv);
-  const int item = (int)blockIdx.x / (p.Hq * p.B);
+  const int item = (int)bid / (p.Hq * p.B);
   const int q0 = (nqb - 1 - (SPLIT ? item % nqb : item)) * 16 * NW;
   const int kc = SPLIT ? item / nqb : 0;
   const int qbase = q0 + 16 * w;
@@ -785,6 +783,19 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_mfma(AttnP p) {
   }
 }
 
+// The backward's two main products in one launch: blocks [0, n_dkdv) run the
+// dK/dV role (one per key block, query head and query chunk), the rest the
+// dQ role (one per query block, head and key chunk).  The roles are
+// independent given delta, so they fill the GPU together instead of as two
+// half-empty launches at short sequence lengths.
+template <int HD, int NW, int BQ, int BKV, bool SQ, bool SK>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_mfma(AttnP p, int n_dkdv) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int bid = (int)blockIdx.x;
+  if (bid < n_dkdv) attn_bwd_dkdv_role<HD, NW, BQ, SQ>(p, bid, smem);
+  else attn_bwd_dq_role<HD, NW, BKV, SK>(p, bid - n_dkdv, smem);
+}
+
 template <typename K>
 void set_lds(K kernel, size_t bytes) {
   MFT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -815,29 +826,31 @@ void fwd_launch(hipStream_t s, AttnP& p) {
   }
 }
 
-template <int HD, int NW>
-void dkdv_launch(hipStream_t s, AttnP& p) {
+template <int HD, int NW, bool SQ, bool SK>
+void bwd_main_launch(hipStream_t s, AttnP& p) {
   constexpr int P = HD + 4;
   constexpr int BQ = Cfg<HD>::BQ;
-  const size_t lds = sizeof(float) * (HD > 128 ? 2 * 16 * NW * P + 2 * BQ * P + 2 * BQ
-                                                : 2 * BQ * P + 2 * HD * (BQ + 4) + 2 * BQ);
-  auto kern = p.nqc > 1 ? attn_bwd_dkdv_mfma<HD, NW, BQ, true> : attn_bwd_dkdv_mfma<HD, NW, BQ, false>;
+  constexpr int BKV = Cfg<HD>::DQBKV;
+  const size_t lds_kv = sizeof(float) * (HD > 128 ? 2 * 16 * NW * P + 2 * BQ * P + 2 * BQ
+                                                   : 2 * BQ * P + 2 * HD * (BQ + 4) + 2 * BQ);
+  const size_t lds_q = sizeof(float) * (2 * BKV * P + (HD > 128 ? 0 : HD * (BKV + 4)) + BKV);
+  const size_t lds = std::max(lds_kv, lds_q);
+  auto kern = attn_bwd_mfma<HD, NW, BQ, BKV, SQ, SK>;
   set_lds(kern, lds);
-  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.nqc * p.Hq * p.B));
-  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  const int64_t blocks = cdiv(p.S, 16 * NW) * (int64_t)p.Hq * p.B;
+  const int n_dkdv = (int)(blocks * p.nqc);
+  dim3 grid((unsigned)(n_dkdv + blocks * p.nkc));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p, n_dkdv);
   MFT_LAUNCH_CHECK();
 }
 
 template <int HD, int NW>
-void dq_launch(hipStream_t s, AttnP& p) {
-  constexpr int P = HD + 4;
-  constexpr int BKV = Cfg<HD>::DQBKV;
-  const size_t lds = sizeof(float) * (2 * BKV * P + (HD > 128 ? 0 : HD * (BKV + 4)) + BKV);
-  auto kern = p.nkc > 1 ? attn_bwd_dq_mfma<HD, NW, BKV, true> : attn_bwd_dq_mfma<HD, NW, BKV, false>;
-  set_lds(kern, lds);
-  dim3 grid((unsigned)(cdiv(p.S, 16 * NW) * p.nkc * p.Hq * p.B));
-  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
-  MFT_LAUNCH_CHECK();
+void bwd_main(hipStream_t s, AttnP& p) {
+  const bool sq = p.nqc > 1, sk = p.nkc > 1;
+  if (sq && sk) bwd_main_launch<HD, NW, true, true>(s, p);
+  else if (sq) bwd_main_launch<HD, NW, true, false>(s, p);
+  else if (sk) bwd_main_launch<HD, NW, false, true>(s, p);
+  else bwd_main_launch<HD, NW, false, false>(s, p);
   if (p.nkc > 1) {
     const int64_t total = (int64_t)p.B * p.S * p.Hq * (HD / 4);
     hipLaunchKernelGGL(attn_dq_sum_kernel<HD>, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, 16 * NW);
@@ -920,9 +933,9 @@ BwdPlan bwd_plan(const AttnArgs& a) {
 
 template <int HD>
 void bwd_launch(hipStream_t s, AttnP& p, int nw) {
-  if (nw == 4) { dkdv_launch<HD, 4>(s, p); dq_launch<HD, 4>(s, p); }
-  else if (nw == 2) { dkdv_launch<HD, 2>(s, p); dq_launch<HD, 2>(s, p); }
-  else { dkdv_launch<HD, 1>(s, p); dq_launch<HD, 1>(s, p); }
+  if (nw == 4) bwd_main<HD, 4>(s, p);
+  else if (nw == 2) bwd_main<HD, 2>(s, p);
+  else bwd_main<HD, 1>(s, p);
   if (p.Hq != p.Hkv || p.nqc > 1) {
     const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
     hipLaunchKernelGGL(attn_partial_sum_kernel<HD>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
