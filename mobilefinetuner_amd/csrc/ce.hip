@@ -2,14 +2,18 @@
 // backward in one pass structure:
 //   1. count the valid targets (label != ignore_index, shifted by one),
 //   2. one workgroup per logits row: online max/sum-exp over V in registers
-//      (each thread keeps its own running max and rescaled sum, merged by a
-//      wave64 shuffle tree and an LDS step), NLL = lse − x[label], then a
-//      second sweep writes dlogits = (exp(x − lse) − onehot)·upstream/n in
-//      place (the row is re-read from L2/MALL, not HBM, at these row sizes),
+//      (base 2 on x·log2e; each thread keeps its own running max and
+//      rescaled sum over 128-bit loads, merged by a wave64 shuffle tree and
+//      an LDS step), NLL = lse − x[label], then a second sweep writes
+//      dlogits = (exp(x − lse) − onehot)·upstream/n in place (the row is
+//      re-read from L2/MALL, not HBM, at these row sizes),
 //   3. a single-workgroup fixed-order reduction of the per-row NLLs into the
 //      fp64 loss sum (deterministic).
 // Algorithmic HBM traffic: read logits once + write dlogits once
 // (8·rows·V bytes).
+#include <algorithm>
+#include <cfloat>
+
 #include "common.h"
 
 namespace mft {
@@ -38,51 +42,84 @@ __global__ __launch_bounds__(256) void ce_count_kernel(const int32_t* __restrict
   }
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Running (max, Σ 2^(t − max)) pairs over base-2 scaled logits t = x·log2e.
+// The max starts at −FLT_MAX (not −inf) so that merging two empty pairs
+// gives 0·2^0 = 0 rather than NaN.
 __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
-  if (m2 > m) {
-    s = s * __expf(m - m2) + s2;
-    m = m2;
-  } else if (m2 > -INFINITY) {
-    s += s2 * __expf(m2 - m);
-  }
+  const float mm = fmaxf(m, m2);
+  s = s * __builtin_amdgcn_exp2f(m - mm) + s2 * __builtin_amdgcn_exp2f(m2 - mm);
+  m = mm;
 }
 
+// One workgroup per logits row.  The row is walked as an aligned float4 body
+// (rows start at any 4-byte offset when V is odd) plus a scalar head and
+// tail; each thread keeps U float4 loads in flight per step and folds each
+// group of 4·U values into its running pair with one rescale.  The gradient
+// sweep re-reads the row (from L2 / MALL) and writes dlogits in place.
 template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S,
     int64_t V, int64_t ld, int ignore_index, float upstream, int64_t norm_count,
     const int64_t* __restrict__ cnt, float* dlogits, float* __restrict__ row_nll) {
-  constexpr int NW = BLOCK / 64;
+  constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
   const int64_t row = blockIdx.x;
   const int s = (int)(row % S);
   const int label = (s + 1 < S) ? labels[row + 1] : ignore_index;
   const float* x = logits + row * ld;
   float* dx = dlogits ? dlogits + row * ld : nullptr;
+  const int tid = threadIdx.x;
   if (label == ignore_index || label < 0 || (int64_t)label >= V) {
     if (dx)
-      for (int64_t j = threadIdx.x; j < V; j += BLOCK) dx[j] = 0.f;
-    if (threadIdx.x == 0) row_nll[row] = 0.f;
+      for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
+    if (tid == 0) row_nll[row] = 0.f;
     return;
   }
-  float m = -INFINITY, sum = 0.f;
-  for (int64_t j = threadIdx.x; j < V; j += BLOCK) {
-    const float v = x[j];
-    if (v > m) {
-      sum = sum * __expf(m - v) + 1.f;
-      m = v;
-    } else {
-      sum += __expf(v - m);
+  const float xl = x[label];  // read before any thread writes (dx may alias x)
+  const int64_t head = std::min<int64_t>((4 - (((uintptr_t)x >> 2) & 3)) & 3, V);
+  const int64_t n4 = (V - head) / 4;
+  const int64_t tail0 = head + 4 * n4;
+  const floatx4* x4 = reinterpret_cast<const floatx4*>(x + head);
+
+  float m = -FLT_MAX, sum = 0.f;
+  for (int64_t j = tid; j < head; j += BLOCK) merge_ms(m, sum, x[j] * kLog2e, 1.f);
+  for (int64_t b = tid; b < n4; b += (int64_t)BLOCK * U) {
+    floatx4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = b + (int64_t)u * BLOCK;
+      v[u] = q < n4 ? x4[q] : floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
+    float mx = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[u][e] *= kLog2e;
+        mx = fmaxf(mx, v[u][e]);
+      }
+    float acc = sum * __builtin_amdgcn_exp2f(m - mx);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc += __builtin_amdgcn_exp2f(v[u][e] - mx);
+    sum = acc;
+    m = mx;
   }
+  for (int64_t j = tail0 + tid; j < V; j += BLOCK) merge_ms(m, sum, x[j] * kLog2e, 1.f);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float m2 = __shfl_xor(m, off, 64);
     const float s2 = __shfl_xor(sum, off, 64);
     merge_ms(m, sum, m2, s2);
   }
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
+  const int w = tid >> 6;
+  if ((tid & 63) == 0) {
     sm[w] = m;
     ss[w] = sum;
   }
@@ -91,19 +128,41 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
   sum = ss[0];
 #pragma unroll
   for (int i = 1; i < NW; ++i) merge_ms(m, sum, sm[i], ss[i]);
-  const float lse = m + logf(sum);
-  const float xl = x[label];
-  if (threadIdx.x == 0) row_nll[row] = lse - xl;
-  if (dx) {
-    const int64_t n = norm_count > 0 ? norm_count : *cnt;
-    const float g = n > 0 ? upstream / (float)n : 0.f;
-    // dx may alias x: every element is read before it is written by the
-    // same thread, and the label logit was read above the barrier.
-    __syncthreads();
-    for (int64_t j = threadIdx.x; j < V; j += BLOCK) {
-      const float p = __expf(x[j] - lse);
-      dx[j] = (j == label ? p - 1.f : p) * g;
+  const float lse2 = m + __builtin_amdgcn_logf(sum);  // log2 Σ 2^t (sum ≥ 1)
+  if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
+  if (!dx) return;
+  const int64_t n = norm_count > 0 ? norm_count : *cnt;
+  const float g = n > 0 ? upstream / (float)n : 0.f;
+  // dlogits = (softmax − onehot(label))·g; every element is read before the
+  // same thread writes it.
+  for (int64_t j = tid; j < head; j += BLOCK) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(x[j], kLog2e, -lse2));
+    dx[j] = (j == label ? p - 1.f : p) * g;
+  }
+  floatx4* d4 = reinterpret_cast<floatx4*>(dx + head);
+  for (int64_t b = tid; b < n4; b += (int64_t)BLOCK * U) {
+    floatx4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = b + (int64_t)u * BLOCK;
+      if (q < n4) v[u] = x4[q];
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = b + (int64_t)u * BLOCK;
+      if (q >= n4) continue;
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(v[u][e], kLog2e, -lse2));
+        o[e] = (head + 4 * q + e == label ? p - 1.f : p) * g;
+      }
+      d4[q] = o;
+    }
+  }
+  for (int64_t j = tail0 + tid; j < V; j += BLOCK) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(x[j], kLog2e, -lse2));
+    dx[j] = (j == label ? p - 1.f : p) * g;
   }
 }
 
@@ -139,7 +198,7 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   hipLaunchKernelGGL(ce_count_kernel, dim3((unsigned)std::min<int64_t>(cdiv(rows, 256), 64)), dim3(256),
                      0, s, labels, B, S, ignore_index, count_scratch);
   MFT_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ce_row_kernel<512>, dim3((unsigned)rows), dim3(512), 0, s, logits, labels, B, S, V, ld,
+  hipLaunchKernelGGL(ce_row_kernel<1024>, dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V, ld,
                      ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,

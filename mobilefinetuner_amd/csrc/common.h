@@ -63,6 +63,30 @@ __device__ __forceinline__ float __attribute__((ext_vector_type(4))) widen4(uint
 }
 
 // ---- launchers shared by the C-ABI and the step engine ----------------------
+// A row norm applied to the finished rows of a GEMM output C[M,N] (N = the
+// normalised width, ldc = N):
+//   NORM_LN_FWD:  y = LayerNorm(C row)·w + b, mean and rstd stored;
+//   NORM_RMS_FWD: y = C row · rstd · (w + unit_offset), rstd stored;
+//   NORM_LN_BWD / NORM_RMS_BWD: C is the gradient of the norm's output for
+//     input rows x (with the stored mean / rstd); y = resid + ∂x (resid may
+//     be null or alias y).  skip_c: C itself is not needed afterwards.
+// With split-K the reduction, the epilogue and the norm run as one pass
+// (the row is finished in registers); otherwise the norm runs after the GEMM.
+enum { NORM_NONE = 0, NORM_LN_FWD, NORM_RMS_FWD, NORM_LN_BWD, NORM_RMS_BWD };
+struct RowNorm {
+  int kind = NORM_NONE;
+  const float* w = nullptr;
+  const float* b = nullptr;
+  float eps = 0.f;
+  int unit_offset = 0;
+  float* y = nullptr;
+  float* mean = nullptr;  // LN forward: written; LN backward: read
+  float* rstd = nullptr;  // forward: written; backward: read
+  const float* x = nullptr;
+  const float* resid = nullptr;
+  bool skip_c = false;
+};
+
 struct GemmEpilogue {
   const float* bias = nullptr;   // [N]
   const float* resid = nullptr;  // [M,N] row stride ldc; may alias C
@@ -83,6 +107,8 @@ struct GemmEpilogue {
   // separately named (otherwise identical) kernel instantiation so kernel
   // traces and counter profiles attribute the two apart.
   int site = 0;
+  // Host-side only: row norm of the finished output (never read by kernels).
+  const RowNorm* norm = nullptr;
 };
 
 // Device scratch handed to launchers (split-K partials, rank-r temporaries).
@@ -239,6 +265,13 @@ void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M,
 void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
                  const float* w, const float* rstd, int64_t M, int64_t C,
                  bool unit_offset, float* dx, const float* resid);
+// The norm of nm applied to finished rows c[M,C] (one of the four launchers).
+void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm& nm);
+// Split-K reduction (partials [splits][M][N], summed in split order) + the
+// GEMM epilogue + the row norm in one pass.  Returns false, launching
+// nothing, when the shape or alignment does not fit the fused kernel.
+bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, float* C, int64_t ldc,
+                 const GemmEpilogue& ep, const RowNorm& nm);
 // Row-loop fallbacks of the four norm launchers (elementwise.hip).
 void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g, const float* b,
                            int64_t M, int64_t C, float eps, float* y, float* mean, float* rstd);

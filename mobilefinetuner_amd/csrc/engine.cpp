@@ -595,7 +595,7 @@ float lscale(const mft_model_s* m) { return m->c.lora_alpha / (float)m->c.lora_r
 // y = x·W (+ LoRA) + bias (+ resid); with gelu_out, y keeps the
 // pre-activation and gelu_out receives GELU(y) (GPT-2 c_fc).
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
-             const float* resid, float* gelu_out = nullptr) {
+             const float* resid, float* gelu_out = nullptr, const RowNorm* norm = nullptr) {
   const Param& W = m->P[l.W];
   const bool lora = l.A >= 0;
   const int r = lora ? m->c.lora_r : 0;
@@ -603,6 +603,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   ep.bias = l.b >= 0 ? static_cast<const float*>(m->P[l.b].data) : nullptr;
   ep.resid = resid;
   ep.gelu_out = gelu_out;
+  ep.norm = norm;
   if (lora && m->merged) {  // y = x·W_eff (+ bias, residual)
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
     gemm(m->stream, x, l.K, l.weff, l.N, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
@@ -624,16 +625,20 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
 }
 
-// dx = dy·Wᵀ (+ LoRA); with gelu_grad_of = the pre-activation that fed a
-// GELU into this layer, dx is the gradient of that pre-activation instead.
+// dx = dy·Wᵀ (+ LoRA) (+ beta·dx); with gelu_grad_of = the pre-activation
+// that fed a GELU into this layer, dx is the gradient of that pre-activation
+// instead; norm: the backward of the norm that produced x, applied to dx.
 void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, const float* xa,
-             int64_t M, float* dx, const float* gelu_grad_of = nullptr) {
+             int64_t M, float* dx, const float* gelu_grad_of = nullptr, const RowNorm* norm = nullptr,
+             float beta = 0.f) {
   const Param& W = m->P[l.W];
   const bool lora = l.A >= 0;
   if (lora && m->merged) {  // dX = dY·W_effᵀ; dA/dB come from the batched launches
     if (dx) {
       GemmEpilogue ep;
       ep.gelu_grad_of = gelu_grad_of;
+      ep.norm = norm;
+      ep.beta = beta;
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
       gemm(m->stream, dy, l.N, l.weff, l.N, true, false, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
     }
@@ -651,6 +656,8 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
   if (dx) {
     GemmEpilogue ep;
     ep.gelu_grad_of = gelu_grad_of;
+    ep.norm = norm;
+    ep.beta = beta;
     if (lora) {
       ep.P = U;
       ep.Q = static_cast<const float*>(m->P[l.A].data);
@@ -721,21 +728,49 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   merge_lora(m);  // A, B (or W) may have changed since the last forward
   embed(s, ids, M, S, E.data, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
         gemma ? std::sqrt((float)d) : 1.f, m->A[0].x);
+  // Input norm of layer li (li == n_layer: the final norm).  GPT-2 and Qwen2
+  // run it inside the GEMM that produced its input (the previous layer's
+  // residual-fused down projection); Gemma3's post-norms sit in between.
+  auto norm1 = [&](int li) {
+    const bool fin = li == c.n_layer;
+    RowNorm nm;
+    nm.kind = gpt2 ? NORM_LN_FWD : NORM_RMS_FWD;
+    nm.w = pd<float>(m, fin ? m->nfw : m->L[li].n1w);
+    nm.b = gpt2 ? pd<float>(m, fin ? m->nfb : m->L[li].n1b) : nullptr;
+    nm.eps = c.norm_eps;
+    nm.unit_offset = gemma ? 1 : 0;
+    nm.y = fin ? m->hf : m->A[li].n1;
+    nm.mean = gpt2 ? (fin ? m->fmean : m->A[li].mean1) : nullptr;
+    nm.rstd = fin ? m->frstd : m->A[li].rstd1;
+    return nm;
+  };
+  auto norm2 = [&](int li) {  // the pre-MLP norm of layer li
+    RowNorm nm;
+    Acts& a = m->A[li];
+    nm.kind = gpt2 ? NORM_LN_FWD : NORM_RMS_FWD;
+    nm.w = pd<float>(m, m->L[li].n2w);
+    nm.b = gpt2 ? pd<float>(m, m->L[li].n2b) : nullptr;
+    nm.eps = c.norm_eps;
+    nm.unit_offset = gemma ? 1 : 0;
+    nm.y = a.n2;
+    nm.mean = gpt2 ? a.mean2 : nullptr;
+    nm.rstd = a.rstd2;
+    return nm;
+  };
   for (int li = 0; li < c.n_layer; ++li) {
     const Layer& L = m->L[li];
     Acts& a = m->A[li];
     float* hout = li + 1 < c.n_layer ? m->A[li + 1].x : m->h_final;
+    if (li == 0 || gemma) row_norm(s, a.x, M, d, norm1(li));
+    const RowNorm n2 = norm2(li), nx = norm1(li + 1);
     if (gpt2) {
-      layernorm_fwd(s, a.x, pd<float>(m, L.n1w), pd<float>(m, L.n1b), M, d, c.norm_eps, a.n1, a.mean1, a.rstd1);
       lin_fwd(m, L.lin[G_ATTN], a.n1, M, a.q, a.xa[G_ATTN], nullptr);
       attention_fwd(m, a, li, mask, nseq, S);
-      lin_fwd(m, L.lin[G_PROJ], a.att, M, a.hmid, a.xa[G_PROJ], a.x);  // residual fused
-      layernorm_fwd(s, a.hmid, pd<float>(m, L.n2w), pd<float>(m, L.n2b), M, d, c.norm_eps, a.n2, a.mean2, a.rstd2);
-      lin_fwd(m, L.lin[G_FC], a.n2, M, a.gate, a.xa[G_FC], nullptr, a.act);  // GELU fused
-      lin_fwd(m, L.lin[G_FC2], a.act, M, hout, a.xa[G_FC2], a.hmid);  // residual fused
+      lin_fwd(m, L.lin[G_PROJ], a.att, M, a.hmid, a.xa[G_PROJ], a.x, nullptr, &n2);  // residual + LN fused
+      lin_fwd(m, L.lin[G_FC], a.n2, M, a.gate, a.xa[G_FC], nullptr, a.act);         // GELU fused
+      lin_fwd(m, L.lin[G_FC2], a.act, M, hout, a.xa[G_FC2], a.hmid, nullptr, &nx);   // residual + LN fused
       continue;
     }
-    rmsnorm_fwd(s, a.x, pd<float>(m, L.n1w), M, d, c.norm_eps, gemma, a.n1, a.rstd1);
     if (gemma) {
       lin_fwd(m, L.lin[T_Q], a.n1, M, a.qraw, a.xa[T_Q], nullptr);
       lin_fwd(m, L.lin[T_K], a.n1, M, a.kraw, a.xa[T_K], nullptr);
@@ -754,10 +789,10 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr);
       rmsnorm_fwd(s, a.o, pd<float>(m, L.pan), M, d, c.norm_eps, true, m->dtmp, a.ors);
       add_out(s, a.hmid, a.x, m->dtmp, M * d);
+      rmsnorm_fwd(s, a.hmid, pd<float>(m, L.n2w), M, d, c.norm_eps, gemma, a.n2, a.rstd2);
     } else {
-      lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x);
+      lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x, nullptr, &n2);  // residual + norm fused
     }
-    rmsnorm_fwd(s, a.hmid, pd<float>(m, L.n2w), M, d, c.norm_eps, gemma, a.n2, a.rstd2);
     lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
     lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
     glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
@@ -766,13 +801,10 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       rmsnorm_fwd(s, a.mo, pd<float>(m, L.pfn), M, d, c.norm_eps, true, m->dtmp, a.mrs);
       add_out(s, hout, a.hmid, m->dtmp, M * d);
     } else {
-      lin_fwd(m, L.lin[T_DOWN], a.act, M, hout, a.xa[T_DOWN], a.hmid);
+      lin_fwd(m, L.lin[T_DOWN], a.act, M, hout, a.xa[T_DOWN], a.hmid, nullptr, &nx);  // residual + norm fused
     }
   }
-  if (gpt2)
-    layernorm_fwd(s, m->h_final, pd<float>(m, m->nfw), pd<float>(m, m->nfb), M, d, c.norm_eps, m->hf, m->fmean, m->frstd);
-  else
-    rmsnorm_fwd(s, m->h_final, pd<float>(m, m->nfw), M, d, c.norm_eps, gemma, m->hf, m->frstd);
+  if (gemma) row_norm(s, m->h_final, M, d, norm1(c.n_layer));
   // LM head: logits = hf · Eᵀ, E [V, d] is the [N, K] operand.
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
   GemmEpilogue head;
@@ -816,19 +848,33 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   auto res_in = [&](int li) { return gemma ? m->dh : dyb(li, gpt2 ? G_FC2 : T_DOWN, m->dh); };
   auto res_mid = [&](int li) { return gemma ? m->dh2 : dyb(li, gpt2 ? G_PROJ : T_O, m->dh2); };
   run_batch(m, m->xa_batch, M);  // xa = x·Aᵀ of every LoRA linear
+  const int top = c.n_layer - 1;
+  // Backward of a norm (ln: LayerNorm, else RMSNorm) over input rows x, run
+  // in the epilogue of the GEMM producing its output gradient: y = resid + ∂x.
+  auto norm_bwd = [&](const float* x, int w, float* mean, float* rstd, float* y, const float* resid) {
+    RowNorm nm;
+    nm.kind = gpt2 ? NORM_LN_BWD : NORM_RMS_BWD;
+    nm.x = x;
+    nm.w = pd<float>(m, w);
+    nm.mean = mean;
+    nm.rstd = rstd;
+    nm.unit_offset = gemma ? 1 : 0;
+    nm.y = y;
+    nm.resid = resid;
+    nm.skip_c = true;
+    return nm;
+  };
   {
-    // dhf = dlogits · E, E [V, d] is the [K, N] operand.
+    // dhf = dlogits · E, E [V, d] is the [K, N] operand; the final norm's
+    // backward runs in its epilogue.
     Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
+    const RowNorm nf = norm_bwd(m->h_final, m->nfw, gpt2 ? m->fmean : nullptr, m->frstd, res_in(top), nullptr);
     GemmEpilogue head;
     head.site = 1;
+    head.norm = &nf;
     gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
          t.events());
   }
-  const int top = c.n_layer - 1;
-  if (gpt2)
-    layernorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->fmean, m->frstd, M, d, res_in(top), nullptr);
-  else
-    rmsnorm_bwd(s, m->dn, m->h_final, pd<float>(m, m->nfw), m->frstd, M, d, gemma, res_in(top), nullptr);
   const int64_t nf = M * c.d_ff;
   for (int li = top; li >= 0; --li) {
     const Layer& L = m->L[li];
@@ -836,12 +882,14 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     float* rin = res_in(li);
     float* rmid = res_mid(li);
     const bool need_dx = li > 0;
+    const RowNorm nb2 = norm_bwd(a.hmid, L.n2w, gpt2 ? a.mean2 : nullptr, a.rstd2, rmid, rin);
+    float* rnext = need_dx ? res_in(li - 1) : nullptr;
+    const RowNorm nb1 = norm_bwd(a.x, L.n1w, gpt2 ? a.mean1 : nullptr, a.rstd1, rnext, rmid);
     // ---- MLP block ----
     if (gpt2) {
       float* dgate = dyb(li, G_FC, m->dgate);
       lin_bwd(m, L.lin[G_FC2], rin, a.act, a.xa[G_FC2], M, dgate, a.gate);  // GELU' fused
-      lin_bwd(m, L.lin[G_FC], dgate, a.n2, a.xa[G_FC], M, m->dn);
-      layernorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.mean2, a.rstd2, M, d, rmid, rin);
+      lin_bwd(m, L.lin[G_FC], dgate, a.n2, a.xa[G_FC], M, m->dn, nullptr, &nb2);  // LN backward fused
     } else {
       const float* dmo = rin;
       if (gemma) {
@@ -854,9 +902,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       float* dup = dyb(li, T_UP, m->dup);
       glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, dgate, dup);
       lin_bwd(m, L.lin[T_GATE], dgate, a.n2, a.xa[T_GATE], M, m->dn);
-      lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dtmp);
-      add_inplace(s, m->dn, m->dtmp, M * d);
-      rmsnorm_bwd(s, m->dn, a.hmid, pd<float>(m, L.n2w), a.rstd2, M, d, gemma, rmid, rin);
+      lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dn, nullptr, &nb2, 1.f);  // dn += ...; norm fused
     }
     // ---- attention block ----
     const float* dox = rmid;
@@ -869,7 +915,6 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};
     const double awork = 2.0 * 5.0 * nseq * H * (double)S * S * hd * 0.5;
-    float* rnext = need_dx ? res_in(li - 1) : nullptr;
     if (gpt2) {
       float* dqkv = dyb(li, G_ATTN, m->dqkv);
       {
@@ -879,8 +924,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
                  dqkv + 2 * d, 3 * d, m->ws);
         t.end();
       }
-      lin_bwd(m, L.lin[G_ATTN], dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr);
-      if (need_dx) layernorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.mean1, a.rstd1, M, d, rnext, rmid);
+      lin_bwd(m, L.lin[G_ATTN], dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr, nullptr,
+              need_dx ? &nb1 : nullptr);  // LN backward fused
       continue;
     }
     // q/k dY: after RoPE's inverse (Qwen2) or after the q/k norms' backward (Gemma3)
@@ -907,14 +952,12 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       dqx = tq;
       dkx = tk;
     }
-    lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, need_dx ? m->dn : nullptr);
-    lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, need_dx ? m->dtmp : nullptr);
-    if (need_dx) add_inplace(s, m->dn, m->dtmp, M * d);
-    lin_bwd(m, L.lin[T_V], dv, a.n1, a.xa[T_V], M, need_dx ? m->dtmp : nullptr);
-    if (need_dx) {
-      add_inplace(s, m->dn, m->dtmp, M * d);
-      rmsnorm_bwd(s, m->dn, a.x, pd<float>(m, L.n1w), a.rstd1, M, d, gemma, rnext, rmid);
-    }
+    // dn = dq·Wqᵀ + dk·Wkᵀ + dv·Wvᵀ accumulated in the GEMM epilogues, the
+    // input norm's backward fused into the last one.
+    float* dn = need_dx ? m->dn : nullptr;
+    lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, dn);
+    lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, dn, nullptr, nullptr, 1.f);
+    lin_bwd(m, L.lin[T_V], dv, a.n1, a.xa[T_V], M, dn, nullptr, need_dx ? &nb1 : nullptr, 1.f);
   }
   run_batch(m, m->udb_batch, M);  // U = dY·B and dB += s·dYᵀ·xa of every LoRA linear
   run_batch(m, m->da_batch, M);   // dA += s·Uᵀ·x of every LoRA linear

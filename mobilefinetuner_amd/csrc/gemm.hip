@@ -1109,10 +1109,15 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   else launch_q<64, 32>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
 
-  if (splits > 1) {
+  const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
+  MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
+  if (splits > 1 && !(nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm))) {
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256), 0, s,
                        (const float*)ws.ptr, splits, M, N, C, ldc, ep);
     MFT_LAUNCH_CHECK();
+    if (nm) row_norm(s, C, M, N, *nm);
+  } else if (splits == 1 && nm) {
+    row_norm(s, C, M, N, *nm);
   }
 }
 

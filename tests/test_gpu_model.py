@@ -31,6 +31,9 @@ SMALL = {
     "gpt2-all-targets": (gpt2(2, 128, 2, vocab=517, max_pos=64, name="gpt2-t4", lora_mask=0b1111),
                          3, 40, 1),
     "qwen2": (qwen2(2, 256, 4, 2, 64, 384, vocab=997, name="qwen-t"), 2, 64, 2),
+    # d_ff = 1024: the down projection and the gate/up dX products take the
+    # split-K path, so the RMSNorms run inside the split-K reduction.
+    "qwen2-wide": (qwen2(2, 256, 4, 2, 64, 1024, vocab=613, name="qwen-w"), 2, 64, 1),
     "gemma3": (gemma3(6, 128, 2, 1, 256, 256, vocab=1009, name="gemma-t", sliding_window=24,
                       query_pre_attn_scalar=256), 2, 40, 1),
     "gemma3-fp16w": (gemma3(2, 128, 2, 1, 256, 320, vocab=611, name="gemma-t16", w_fp16=1,
