@@ -395,7 +395,7 @@ inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 8192) {
 }  // namespace
 
 // Row-loop versions for shapes the vectorised kernels (norms.hip) do not
-// take: C not a multiple of 4, unaligned rows, or C > 2048.
+// take: C not a multiple of 4, unaligned rows, or C > 4096.
 void layernorm_fwd_rowloop(hipStream_t s, const float* x, const float* g,
                            const float* b, int64_t M, int64_t C, float eps, float* y,
                            float* mean, float* rstd) {

@@ -1092,6 +1092,18 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
+  const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
+  // A row norm after the GEMM costs nothing extra in a split-K reduction and
+  // a launch of its own otherwise: an unsplit plan with K >= 1024 becomes
+  // 32-row tiles split in two (GPT-2 medium's attention c_proj: 53.3k vs
+  // 52.9k tokens/s on MI355X).  Tuning hook: MFT_GEMM_NORM_PLAN="bm,0,splits".
+  if (nm && !forced && pl.splits == 1 && K >= 1024 && N % 4 == 0 && N <= 4096 && ldc == N) {
+    static const char* nplan = getenv("MFT_GEMM_NORM_PLAN");
+    int bm = 32, bn = 0, sp = 2;
+    if (nplan && !(sscanf(nplan, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 && (bm == 32 || bm == 64) && bn == 0))
+      bm = 32, bn = 0, sp = 2;
+    if ((size_t)sp * M * N * sizeof(float) <= ws.bytes) pl = {bm, bn, sp};
+  }
   const int bk = plan_bk(pl.bm, pl.bn);
   int splits = pl.splits;
   p.k_chunk = (int)(cdiv(cdiv(K, splits), bk) * bk);
@@ -1109,7 +1121,6 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   else launch_q<64, 32>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
 
-  const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
   MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
   if (splits > 1 && !(nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm))) {
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256), 0, s,

@@ -1,12 +1,18 @@
 // norms.hip — LayerNorm / RMSNorm forward and backward with the row held in
-// registers: one wave64 per row, each lane loads NV 128-bit chunks up front
-// (all loads in flight at once), reduces with shuffles and writes once.
-// HBM traffic is the algorithmic minimum (fwd: read x, write y; bwd: read
-// dy and x, write/accumulate dx).  Rows wider than 2048, C % 4 != 0 or
-// unaligned rows go to the row-loop kernels in elementwise.hip.
+// registers.  A row is owned by a group of RW waves (RW = 4 for rows wider
+// than 512 floats, so a 1024-wide row is one 128-bit chunk per thread of a
+// 256-thread workgroup; 2 or 1 for narrow rows such as per-head q/k norms);
+// every thread loads its NV chunks up front (all loads in flight at once),
+// sums reduce with wave shuffles plus one LDS step across the group, and the
+// row is written once.  HBM traffic is the algorithmic minimum (fwd: read
+// x, write y; bwd: read dy and x, write/accumulate dx).  Rows wider than
+// 4096, C % 4 != 0 or unaligned rows go to the row-loop kernels in
+// elementwise.hip.
+//
 // The same row code also finishes split-K GEMM outputs (splitk_norm_vec):
-// the norm whose input is a linear layer's output then runs inside that
-// GEMM's reduction pass.
+// the norm whose input is a linear layer's output runs inside that GEMM's
+// reduction pass, with every split's partial load issued before the first
+// is used.
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -20,40 +26,85 @@ __device__ __forceinline__ float wsum(float v) {
   return v;
 }
 
-template <int NV>
-__device__ __forceinline__ void load_row(const float* __restrict__ base, int C4, int lane,
-                                         floatx4 (&v)[NV]) {
+// Thread placement: row group `grp` of the workgroup (4 / RW groups), lane
+// `gl` ∈ [0, 64·RW) within it; chunk q = gl + 64·RW·i for i < NV.
+template <int RW>
+struct Place {
+  int wave, grp, gl;
+  __device__ __forceinline__ Place() {
+    wave = (int)threadIdx.x >> 6;
+    grp = wave / RW;
+    gl = (wave % RW) * 64 + ((int)threadIdx.x & 63);
+  }
+};
+
+// Σ over the row group of one or two per-thread values.  red: LDS slots
+// [2][4] owned by this call site (distinct sites use distinct slots, so
+// no barrier is needed before a slot is reused within the kernel).
+template <int RW>
+__device__ __forceinline__ void row_sum2(float& a, float& b, float (*red)[4], int wave) {
+  a = wsum(a);
+  b = wsum(b);
+  if constexpr (RW > 1) {
+    if ((threadIdx.x & 63) == 0) {
+      red[0][wave] = a;
+      red[1][wave] = b;
+    }
+    __syncthreads();
+    const int g0 = wave & ~(RW - 1);
+    a = red[0][g0];
+    b = red[1][g0];
+#pragma unroll
+    for (int i = 1; i < RW; ++i) {
+      a += red[0][g0 + i];
+      b += red[1][g0 + i];
+    }
+  }
+}
+template <int RW>
+__device__ __forceinline__ float row_sum(float a, float (*red)[4], int wave) {
+  float b = 0.f;
+  row_sum2<RW>(a, b, red, wave);
+  return a;
+}
+
+template <int NV, int RW>
+__device__ __forceinline__ void load_row(const float* __restrict__ base, int C4, int gl, floatx4 (&v)[NV]) {
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int q = lane + 64 * i;
+    const int q = gl + 64 * RW * i;
     v[i] = q < C4 ? reinterpret_cast<const floatx4*>(base)[q] : floatx4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-// ---- the four norms on a row held in registers (lane owns chunks lane+64i) --
-template <int NV>
-__device__ __forceinline__ void ln_fwd_row(const floatx4 (&v)[NV], int C, int lane, const float* __restrict__ g,
+// ---- the four norms on a row held in registers ---------------------------
+// `valid` is false for a row group past the last row (it still takes part
+// in the group's barriers, reading a clamped row, and stores nothing).
+template <int NV, int RW>
+__device__ __forceinline__ void ln_fwd_row(const floatx4 (&v)[NV], int C, const Place<RW>& pl, bool valid,
+                                           float (*red)[4], const float* __restrict__ g,
                                            const float* __restrict__ b, float eps, float* __restrict__ yrow,
                                            float* mean, float* rstd) {
   const int C4 = C / 4;
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
-  const float mu = wsum(s) / (float)C;
+  const float mu = row_sum<RW>(s, red, pl.wave) / (float)C;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    if (lane + 64 * i >= C4) continue;
+    if (pl.gl + 64 * RW * i >= C4) continue;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float d = v[i][e] - mu;
       q = fmaf(d, d, q);
     }
   }
-  const float rs = rsqrtf(wsum(q) / (float)C + eps);
+  const float rs = rsqrtf(row_sum<RW>(q, red + 2, pl.wave) / (float)C + eps);
+  if (!valid) return;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     const floatx4 gv = reinterpret_cast<const floatx4*>(g)[qi];
     const floatx4 bv = reinterpret_cast<const floatx4*>(b)[qi];
@@ -62,24 +113,22 @@ __device__ __forceinline__ void ln_fwd_row(const floatx4 (&v)[NV], int C, int la
     for (int e = 0; e < 4; ++e) o[e] = fmaf((v[i][e] - mu) * rs, gv[e], bv[e]);
     reinterpret_cast<floatx4*>(yrow)[qi] = o;
   }
-  if (lane == 0) {
+  if (pl.gl == 0) {
     if (mean) *mean = mu;
     if (rstd) *rstd = rs;
   }
 }
 
-// gv: dy row (overwritten); xrow: the norm's input row.
-template <int NV>
-__device__ __forceinline__ void ln_bwd_row(floatx4 (&gv)[NV], const float* __restrict__ xrow, int C, int lane,
-                                           const float* __restrict__ g, float mu, float rs, float* dxrow,
-                                           const float* residrow) {
+// gv: dy row (overwritten); xv: the norm's input row (overwritten).
+template <int NV, int RW>
+__device__ __forceinline__ void ln_bwd_row(floatx4 (&gv)[NV], floatx4 (&xv)[NV], int C, const Place<RW>& pl,
+                                           bool valid, float (*red)[4], const float* __restrict__ g, float mu,
+                                           float rs, float* dxrow, const float* residrow) {
   const int C4 = C / 4;
-  floatx4 xv[NV];
-  load_row<NV>(xrow, C4, lane, xv);
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     const floatx4 gg = reinterpret_cast<const floatx4*>(g)[qi];
 #pragma unroll
@@ -90,11 +139,13 @@ __device__ __forceinline__ void ln_bwd_row(floatx4 (&gv)[NV], const float* __res
       s2 = fmaf(gv[i][e], xv[i][e], s2);
     }
   }
-  s1 = wsum(s1) / (float)C;
-  s2 = wsum(s2) / (float)C;
+  row_sum2<RW>(s1, s2, red, pl.wave);
+  s1 /= (float)C;
+  s2 /= (float)C;
+  if (!valid) return;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     floatx4 r;
 #pragma unroll
@@ -108,20 +159,22 @@ __device__ __forceinline__ void ln_bwd_row(floatx4 (&gv)[NV], const float* __res
   }
 }
 
-template <int NV>
-__device__ __forceinline__ void rms_fwd_row(const floatx4 (&v)[NV], int C, int lane, const float* __restrict__ w,
-                                            float eps, int unit_offset, float* __restrict__ yrow, float* rstd) {
+template <int NV, int RW>
+__device__ __forceinline__ void rms_fwd_row(const floatx4 (&v)[NV], int C, const Place<RW>& pl, bool valid,
+                                            float (*red)[4], const float* __restrict__ w, float eps,
+                                            int unit_offset, float* __restrict__ yrow, float* rstd) {
   const int C4 = C / 4;
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i)
 #pragma unroll
     for (int e = 0; e < 4; ++e) s = fmaf(v[i][e], v[i][e], s);
-  const float rs = rsqrtf(wsum(s) / (float)C + eps);
+  const float rs = rsqrtf(row_sum<RW>(s, red, pl.wave) / (float)C + eps);
+  if (!valid) return;
   const float off = unit_offset ? 1.f : 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     const floatx4 wv = reinterpret_cast<const floatx4*>(w)[qi];
     floatx4 o;
@@ -129,21 +182,19 @@ __device__ __forceinline__ void rms_fwd_row(const floatx4 (&v)[NV], int C, int l
     for (int e = 0; e < 4; ++e) o[e] = v[i][e] * rs * (off + wv[e]);
     reinterpret_cast<floatx4*>(yrow)[qi] = o;
   }
-  if (lane == 0 && rstd) *rstd = rs;
+  if (pl.gl == 0 && rstd) *rstd = rs;
 }
 
-template <int NV>
-__device__ __forceinline__ void rms_bwd_row(floatx4 (&gv)[NV], const float* __restrict__ xrow, int C, int lane,
-                                            const float* __restrict__ w, float rs, int unit_offset, float* dxrow,
-                                            const float* residrow) {
+template <int NV, int RW>
+__device__ __forceinline__ void rms_bwd_row(floatx4 (&gv)[NV], floatx4 (&xv)[NV], int C, const Place<RW>& pl,
+                                            bool valid, float (*red)[4], const float* __restrict__ w, float rs,
+                                            int unit_offset, float* dxrow, const float* residrow) {
   const int C4 = C / 4;
-  floatx4 xv[NV];
-  load_row<NV>(xrow, C4, lane, xv);
   const float off = unit_offset ? 1.f : 0.f;
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     const floatx4 wv = reinterpret_cast<const floatx4*>(w)[qi];
 #pragma unroll
@@ -153,10 +204,11 @@ __device__ __forceinline__ void rms_bwd_row(floatx4 (&gv)[NV], const float* __re
       s = fmaf(gv[i][e], xv[i][e], s);
     }
   }
-  s = wsum(s) / (float)C;
+  s = row_sum<RW>(s, red, pl.wave) / (float)C;
+  if (!valid) return;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     floatx4 r;
 #pragma unroll
@@ -170,97 +222,113 @@ __device__ __forceinline__ void rms_bwd_row(floatx4 (&gv)[NV], const float* __re
   }
 }
 
-// ---- standalone launches: one wave per row, four rows per workgroup ----------
-template <int NV>
-__global__ __launch_bounds__(256) void ln_fwd_vec(const float* __restrict__ x,
-                                                  const float* __restrict__ g,
-                                                  const float* __restrict__ b, int64_t M, int C,
-                                                  float eps, float* __restrict__ y,
-                                                  float* __restrict__ mean,
+// ---- standalone launches: 4 / RW rows per 256-thread workgroup -------------
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void ln_fwd_vec(const float* __restrict__ x, const float* __restrict__ g,
+                                                  const float* __restrict__ b, int64_t M, int C, float eps,
+                                                  float* __restrict__ y, float* __restrict__ mean,
                                                   float* __restrict__ rstd) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+  __shared__ float red[4][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
   floatx4 v[NV];
-  load_row<NV>(x + row * C, C / 4, lane, v);
-  ln_fwd_row<NV>(v, C, lane, g, b, eps, y + row * C, mean ? mean + row : nullptr, rstd ? rstd + row : nullptr);
+  load_row<NV, RW>(x + r * C, C / 4, pl.gl, v);
+  ln_fwd_row<NV, RW>(v, C, pl, valid, red, g, b, eps, y + r * C, mean ? mean + r : nullptr,
+                     rstd ? rstd + r : nullptr);
 }
 
-template <int NV>
-__global__ __launch_bounds__(256) void ln_bwd_vec(const float* __restrict__ dy,
-                                                  const float* __restrict__ x,
-                                                  const float* __restrict__ g,
-                                                  const float* __restrict__ mean,
-                                                  const float* __restrict__ rstd, int64_t M, int C,
-                                                  float* dx, const float* resid) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  floatx4 gv[NV];
-  load_row<NV>(dy + row * C, C / 4, lane, gv);
-  ln_bwd_row<NV>(gv, x + row * C, C, lane, g, mean[row], rstd[row], dx + row * C,
-                 resid ? resid + row * C : nullptr);
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void ln_bwd_vec(const float* __restrict__ dy, const float* __restrict__ x,
+                                                  const float* __restrict__ g, const float* __restrict__ mean,
+                                                  const float* __restrict__ rstd, int64_t M, int C, float* dx,
+                                                  const float* resid) {
+  __shared__ float red[2][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
+  floatx4 gv[NV], xv[NV];
+  load_row<NV, RW>(dy + r * C, C / 4, pl.gl, gv);
+  load_row<NV, RW>(x + r * C, C / 4, pl.gl, xv);
+  ln_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, g, mean[r], rstd[r], dx + r * C, resid ? resid + r * C : nullptr);
 }
 
-template <int NV>
-__global__ __launch_bounds__(256) void rms_fwd_vec(const float* __restrict__ x,
-                                                   const float* __restrict__ w, int64_t M, int C,
-                                                   float eps, int unit_offset,
-                                                   float* __restrict__ y,
-                                                   float* __restrict__ rstd) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void rms_fwd_vec(const float* __restrict__ x, const float* __restrict__ w,
+                                                   int64_t M, int C, float eps, int unit_offset,
+                                                   float* __restrict__ y, float* __restrict__ rstd) {
+  __shared__ float red[2][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
   floatx4 v[NV];
-  load_row<NV>(x + row * C, C / 4, lane, v);
-  rms_fwd_row<NV>(v, C, lane, w, eps, unit_offset, y + row * C, rstd ? rstd + row : nullptr);
+  load_row<NV, RW>(x + r * C, C / 4, pl.gl, v);
+  rms_fwd_row<NV, RW>(v, C, pl, valid, red, w, eps, unit_offset, y + r * C, rstd ? rstd + r : nullptr);
 }
 
-template <int NV>
-__global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy,
-                                                   const float* __restrict__ x,
-                                                   const float* __restrict__ w,
-                                                   const float* __restrict__ rstd, int64_t M,
-                                                   int C, int unit_offset, float* dx,
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy, const float* __restrict__ x,
+                                                   const float* __restrict__ w, const float* __restrict__ rstd,
+                                                   int64_t M, int C, int unit_offset, float* dx,
                                                    const float* resid) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  floatx4 gv[NV];
-  load_row<NV>(dy + row * C, C / 4, lane, gv);
-  rms_bwd_row<NV>(gv, x + row * C, C, lane, w, rstd[row], unit_offset, dx + row * C,
-                  resid ? resid + row * C : nullptr);
+  __shared__ float red[2][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
+  floatx4 gv[NV], xv[NV];
+  load_row<NV, RW>(dy + r * C, C / 4, pl.gl, gv);
+  load_row<NV, RW>(x + r * C, C / 4, pl.gl, xv);
+  rms_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, w, rstd[r], unit_offset, dx + r * C,
+                      resid ? resid + r * C : nullptr);
 }
 
-// ---- split-K reduction + GEMM epilogue + norm ---------------------------------
-// Each wave finishes one row of C: the partials are summed in split order and
-// the epilogue (bias, residual, beta·C, GELU') applied exactly as the plain
-// reduction does, C is stored (unless skip_c) and the row goes straight into
-// the norm, so the norm's input is never re-read from memory and the norm
-// costs no launch of its own.
-template <int NV, int KIND>
+// ---- split-K reduction + GEMM epilogue + norm ------------------------------
+// Each row group finishes one row of C: the partials are summed in split
+// order and the epilogue (bias, residual, beta·C, GELU') applied exactly as
+// the plain reduction does, C is stored (unless skip_c) and the row goes
+// straight into the norm, so the norm's input is never re-read and the norm
+// costs no launch of its own.  Partial loads are issued four splits at a
+// time before any is added, and the norm's other row operands (residual,
+// the input rows of a backward) are loaded first, so a row's loads overlap.
+template <int NV, int RW, int KIND>
 __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__ partial, int splits, int64_t M,
                                                        int C, float* Cout, GemmEpilogue ep, RowNorm nm) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+  __shared__ float red[4][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
   const int C4 = C / 4;
   const int64_t plane = M * C;
+  constexpr bool BWD = KIND == NORM_LN_BWD || KIND == NORM_RMS_BWD;
+  floatx4 xv[NV], rv[NV];
+  if constexpr (BWD) load_row<NV, RW>(nm.x + r * C, C4, pl.gl, xv);
+  if (ep.resid) load_row<NV, RW>(ep.resid + r * C, C4, pl.gl, rv);
   floatx4 v[NV];
-  load_row<NV>(partial + row * C, C4, lane, v);
-  for (int z = 1; z < splits; ++z) {
-    floatx4 t[NV];
-    load_row<NV>(partial + z * plane + row * C, C4, lane, t);
+  load_row<NV, RW>(partial + r * C, C4, pl.gl, v);
+  for (int z0 = 1; z0 < splits; z0 += 4) {
+    floatx4 t[4][NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] += t[i];
+    for (int j = 0; j < 4; ++j)
+      if (z0 + j < splits) load_row<NV, RW>(partial + (z0 + j) * plane + r * C, C4, pl.gl, t[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (z0 + j < splits) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] += t[j][i];
+      }
   }
-  const int64_t r4 = row * C4;
+  const int64_t r4 = r * C4;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int qi = lane + 64 * i;
+    const int qi = pl.gl + 64 * RW * i;
     if (qi >= C4) continue;
     if (ep.bias) v[i] += reinterpret_cast<const floatx4*>(ep.bias)[qi];
-    if (ep.resid) v[i] += reinterpret_cast<const floatx4*>(ep.resid)[r4 + qi];
+    if (ep.resid) v[i] += rv[i];
     if (ep.beta != 0.f) {
       const floatx4 old = reinterpret_cast<const floatx4*>(Cout)[r4 + qi];
 #pragma unroll
@@ -271,6 +339,7 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[i][e] *= gelu_tanh_grad(pre[e]);
     }
+    if (!valid) continue;
     if (!nm.skip_c) reinterpret_cast<floatx4*>(Cout)[r4 + qi] = v[i];
     if (ep.gelu_out) {
       floatx4 a;
@@ -280,37 +349,63 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
     }
   }
   if constexpr (KIND == NORM_LN_FWD) {
-    ln_fwd_row<NV>(v, C, lane, nm.w, nm.b, nm.eps, nm.y + row * C, nm.mean ? nm.mean + row : nullptr,
-                   nm.rstd ? nm.rstd + row : nullptr);
+    ln_fwd_row<NV, RW>(v, C, pl, valid, red, nm.w, nm.b, nm.eps, nm.y + r * C, nm.mean ? nm.mean + r : nullptr,
+                       nm.rstd ? nm.rstd + r : nullptr);
   } else if constexpr (KIND == NORM_RMS_FWD) {
-    rms_fwd_row<NV>(v, C, lane, nm.w, nm.eps, nm.unit_offset, nm.y + row * C, nm.rstd ? nm.rstd + row : nullptr);
+    rms_fwd_row<NV, RW>(v, C, pl, valid, red, nm.w, nm.eps, nm.unit_offset, nm.y + r * C,
+                        nm.rstd ? nm.rstd + r : nullptr);
   } else if constexpr (KIND == NORM_LN_BWD) {
-    ln_bwd_row<NV>(v, nm.x + row * C, C, lane, nm.w, nm.mean[row], nm.rstd[row], nm.y + row * C,
-                   nm.resid ? nm.resid + row * C : nullptr);
+    ln_bwd_row<NV, RW>(v, xv, C, pl, valid, red, nm.w, nm.mean[r], nm.rstd[r], nm.y + r * C,
+                       nm.resid ? nm.resid + r * C : nullptr);
   } else {
-    rms_bwd_row<NV>(v, nm.x + row * C, C, lane, nm.w, nm.rstd[row], nm.unit_offset, nm.y + row * C,
-                    nm.resid ? nm.resid + row * C : nullptr);
+    rms_bwd_row<NV, RW>(v, xv, C, pl, valid, red, nm.w, nm.rstd[r], nm.unit_offset, nm.y + r * C,
+                        nm.resid ? nm.resid + r * C : nullptr);
   }
 }
 
 bool vec_ok(int64_t C, std::initializer_list<const void*> ptrs) {
-  if (C % 4 != 0 || C > 2048) return false;
+  if (C % 4 != 0 || C > 4096) return false;
   for (const void* p : ptrs)
     if (p && ((uintptr_t)p & 15)) return false;
   return true;
 }
 
-#define MFT_NV_DISPATCH(NVVAL, KERNEL, ...)                                              \
-  switch (NVVAL) {                                                                       \
-    case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                           \
-    case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;                           \
-    case 3: hipLaunchKernelGGL(KERNEL<3>, __VA_ARGS__); break;                           \
-    case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                           \
-    case 5: hipLaunchKernelGGL(KERNEL<5>, __VA_ARGS__); break;                           \
-    case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;                           \
-    case 7: hipLaunchKernelGGL(KERNEL<7>, __VA_ARGS__); break;                           \
-    default: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;                          \
-  }
+// Row-group shape for width C: RW waves per row, NV chunks per thread.
+struct RowShape {
+  int rw, nv;
+};
+RowShape row_shape(int64_t C) {
+  const int64_t c4 = C / 4;
+  const int rw = c4 > 128 ? 4 : (c4 > 64 ? 2 : 1);
+  return {rw, (int)cdiv(c4, 64 * rw)};
+}
+dim3 row_grid(int64_t M, const RowShape& sh) { return dim3((unsigned)cdiv(M, 4 / sh.rw)); }
+
+// Instantiated shapes: RW = 1 or 2 with NV = 1 (C ≤ 512), RW = 4 with
+// NV = 1..4 (C ≤ 4096).
+#define MFT_ROW_DISPATCH(SH, KERNEL, ...)                                    \
+  do {                                                                       \
+    if ((SH).rw == 1) hipLaunchKernelGGL((KERNEL<1, 1>), __VA_ARGS__);        \
+    else if ((SH).rw == 2) hipLaunchKernelGGL((KERNEL<1, 2>), __VA_ARGS__);   \
+    else if ((SH).nv == 1) hipLaunchKernelGGL((KERNEL<1, 4>), __VA_ARGS__);   \
+    else if ((SH).nv == 2) hipLaunchKernelGGL((KERNEL<2, 4>), __VA_ARGS__);   \
+    else if ((SH).nv == 3) hipLaunchKernelGGL((KERNEL<3, 4>), __VA_ARGS__);   \
+    else hipLaunchKernelGGL((KERNEL<4, 4>), __VA_ARGS__);                     \
+  } while (0)
+
+template <int KIND>
+void splitk_norm_launch(hipStream_t s, const RowShape& sh, const float* partial, int splits, int M, int N, float* C,
+                        const GemmEpilogue& ep, const RowNorm& nm) {
+  const dim3 grid = row_grid(M, sh), block(256);
+  const int64_t m = M;
+  if (sh.rw == 1) hipLaunchKernelGGL((splitk_norm_vec<1, 1, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.rw == 2) hipLaunchKernelGGL((splitk_norm_vec<1, 2, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 1) hipLaunchKernelGGL((splitk_norm_vec<1, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 2) hipLaunchKernelGGL((splitk_norm_vec<2, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 3) hipLaunchKernelGGL((splitk_norm_vec<3, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else hipLaunchKernelGGL((splitk_norm_vec<4, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  MFT_LAUNCH_CHECK();
+}
 
 }  // namespace
 
@@ -318,9 +413,8 @@ void layernorm_fwd(hipStream_t s, const float* x, const float* g, const float* b
                    int64_t C, float eps, float* y, float* mean, float* rstd) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   if (!vec_ok(C, {x, g, b, y})) return layernorm_fwd_rowloop(s, x, g, b, M, C, eps, y, mean, rstd);
-  const int nv = (int)cdiv(C, 256);
-  MFT_NV_DISPATCH(nv, ln_fwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, x, g, b, M, (int)C, eps,
-                  y, mean, rstd);
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, ln_fwd_vec, row_grid(M, sh), dim3(256), 0, s, x, g, b, M, (int)C, eps, y, mean, rstd);
   MFT_LAUNCH_CHECK();
 }
 
@@ -330,9 +424,8 @@ void layernorm_bwd(hipStream_t s, const float* dy, const float* x, const float* 
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   if (!vec_ok(C, {dy, x, g, dx, resid}))
     return layernorm_bwd_rowloop(s, dy, x, g, mean, rstd, M, C, dx, resid);
-  const int nv = (int)cdiv(C, 256);
-  MFT_NV_DISPATCH(nv, ln_bwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, dy, x, g, mean, rstd, M,
-                  (int)C, dx, resid);
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, ln_bwd_vec, row_grid(M, sh), dim3(256), 0, s, dy, x, g, mean, rstd, M, (int)C, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 
@@ -340,9 +433,9 @@ void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M, int64
                  bool unit_offset, float* y, float* rstd) {
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   if (!vec_ok(C, {x, w, y})) return rmsnorm_fwd_rowloop(s, x, w, M, C, eps, unit_offset, y, rstd);
-  const int nv = (int)cdiv(C, 256);
-  MFT_NV_DISPATCH(nv, rms_fwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, x, w, M, (int)C, eps,
-                  unit_offset ? 1 : 0, y, rstd);
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, rms_fwd_vec, row_grid(M, sh), dim3(256), 0, s, x, w, M, (int)C, eps, unit_offset ? 1 : 0,
+                   y, rstd);
   MFT_LAUNCH_CHECK();
 }
 
@@ -351,9 +444,9 @@ void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x, const float* w,
   MFT_CHECK_ARG(M > 0 && C > 0, "empty");
   if (!vec_ok(C, {dy, x, w, dx, resid}))
     return rmsnorm_bwd_rowloop(s, dy, x, w, rstd, M, C, unit_offset, dx, resid);
-  const int nv = (int)cdiv(C, 256);
-  MFT_NV_DISPATCH(nv, rms_bwd_vec, dim3((unsigned)cdiv(M, 4)), dim3(256), 0, s, dy, x, w, rstd, M,
-                  (int)C, unit_offset ? 1 : 0, dx, resid);
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, rms_bwd_vec, row_grid(M, sh), dim3(256), 0, s, dy, x, w, rstd, M, (int)C,
+                   unit_offset ? 1 : 0, dx, resid);
   MFT_LAUNCH_CHECK();
 }
 
@@ -367,34 +460,17 @@ void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm
   }
 }
 
-template <int KIND>
-void splitk_norm_launch(hipStream_t s, int nv, const float* partial, int splits, int M, int N, float* C,
-                        const GemmEpilogue& ep, const RowNorm& nm) {
-  const dim3 grid((unsigned)cdiv(M, 4)), block(256);
-  switch (nv) {
-    case 1: hipLaunchKernelGGL((splitk_norm_vec<1, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 2: hipLaunchKernelGGL((splitk_norm_vec<2, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 3: hipLaunchKernelGGL((splitk_norm_vec<3, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 4: hipLaunchKernelGGL((splitk_norm_vec<4, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 5: hipLaunchKernelGGL((splitk_norm_vec<5, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 6: hipLaunchKernelGGL((splitk_norm_vec<6, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    case 7: hipLaunchKernelGGL((splitk_norm_vec<7, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-    default: hipLaunchKernelGGL((splitk_norm_vec<8, KIND>), grid, block, 0, s, partial, splits, M, N, C, ep, nm); break;
-  }
-  MFT_LAUNCH_CHECK();
-}
-
 bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, float* C, int64_t ldc,
                  const GemmEpilogue& ep, const RowNorm& nm) {
   if (ldc != N || splits < 1 || M <= 0) return false;
   if (!vec_ok(N, {partial, C, ep.bias, ep.resid, ep.gelu_out, ep.gelu_grad_of, nm.w, nm.b, nm.y, nm.x, nm.resid}))
     return false;
-  const int nv = (int)cdiv(N, 256);
+  const RowShape sh = row_shape(N);
   switch (nm.kind) {
-    case NORM_LN_FWD: splitk_norm_launch<NORM_LN_FWD>(s, nv, partial, splits, M, N, C, ep, nm); return true;
-    case NORM_RMS_FWD: splitk_norm_launch<NORM_RMS_FWD>(s, nv, partial, splits, M, N, C, ep, nm); return true;
-    case NORM_LN_BWD: splitk_norm_launch<NORM_LN_BWD>(s, nv, partial, splits, M, N, C, ep, nm); return true;
-    case NORM_RMS_BWD: splitk_norm_launch<NORM_RMS_BWD>(s, nv, partial, splits, M, N, C, ep, nm); return true;
+    case NORM_LN_FWD: splitk_norm_launch<NORM_LN_FWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
+    case NORM_RMS_FWD: splitk_norm_launch<NORM_RMS_FWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
+    case NORM_LN_BWD: splitk_norm_launch<NORM_LN_BWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
+    case NORM_RMS_BWD: splitk_norm_launch<NORM_RMS_BWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
     default: return false;
   }
 }

@@ -341,8 +341,9 @@ def test_adam_sumsq_clip():
 
 
 # ------------------------------------------------------------------ support ops
-def test_layernorm():
-    x, gm, b, dy = rn(300, 1024, std=2), rn(1024), rn(1024), rn(300, 1024)
+@pytest.mark.parametrize("C", [1024, 3072])
+def test_layernorm(C):
+    x, gm, b, dy = rn(300, C, std=2), rn(C), rn(C), rn(300, C)
     y_ref, mu, rs = O.layernorm_fwd(x, gm, b, 1e-5)
     y, tmu, trs = ops.layernorm_fwd(g(x), g(gm), g(b), 1e-5)
     assert rel_err(h(y), y_ref) < TOL
@@ -350,9 +351,12 @@ def test_layernorm():
                    O.layernorm_bwd(dy, x, gm, mu, rs)) < TOL
 
 
-@pytest.mark.parametrize("C,unit", [(896, 0), (640, 1), (256, 1)])
+# Row groups of 4 waves (896, 640, 4000: one to four chunks per thread), 2
+# waves (384, with an odd row count so the last workgroup holds a row past
+# the end) and 1 wave (256).
+@pytest.mark.parametrize("C,unit", [(896, 0), (640, 1), (256, 1), (384, 0), (4000, 1)])
 def test_rmsnorm(C, unit):
-    x, w, dy = rn(500, C, std=2), rn(C, std=0.3), rn(500, C)
+    x, w, dy = rn(501, C, std=2), rn(C, std=0.3), rn(501, C)
     y_ref, rs = O.rmsnorm_fwd(x, w, 1e-6, unit)
     y, trs = ops.rmsnorm_fwd(g(x), g(w), 1e-6, unit)
     assert rel_err(h(y), y_ref) < TOL
