@@ -384,7 +384,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 // 16×16×4 MFMA supplies A[row i][k g] and B[k g][col i] and holds D[row
 // 4g+v][col i]; over four consecutive MFMAs lane group g takes k = 4g..4g+3
 // of a 16-wide k block (the same order for A and B), so every A fragment and
-// every [N,K] B fragment is one 128-bit LDS read.  Panels of BK are staged
+// every [N,K] B fragment is one 128-bit LDS read; with B as [K,N] the
+// wave's two column tiles interleave (tile b holds columns 2i + b), so one
+// 64-bit read gives a lane its B values of both tiles.  Panels of BK are staged
 // through two register sets and a two-stage LDS ring exactly like
 // gemm_kernel; the small register and LDS footprint allows four resident
 // workgroups per CU.
@@ -506,14 +508,17 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
       floatx4 fa[WA], fb[2];
 #pragma unroll
       for (int a = 0; a < WA; ++a) fa[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
+      if constexpr (B_NK) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int col = wn + 16 * b + li;
-        if constexpr (B_NK) {
-          fb[b] = *reinterpret_cast<const floatx4*>(bs + col * PB + kb + 4 * lg);
-        } else {
+        for (int b = 0; b < 2; ++b) fb[b] = *reinterpret_cast<const floatx4*>(bs + (wn + 16 * b + li) * PB + kb + 4 * lg);
+      } else {
+        // [K,N] B: the two 16-column tiles interleave (tile b takes columns
+        // wn + 2i + b), so one 64-bit read per k feeds both MFMAs.
 #pragma unroll
-          for (int t = 0; t < 4; ++t) fb[b][t] = bs[(kb + 4 * lg + t) * PB + col];
+        for (int t = 0; t < 4; ++t) {
+          const float2 v = *reinterpret_cast<const float2*>(bs + (kb + 4 * lg + t) * PB + wn + 2 * li);
+          fb[0][t] = v.x;
+          fb[1][t] = v.y;
         }
       }
 #pragma unroll
@@ -525,7 +530,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a][t], fb[b][t], acc[a][b], 0, 0, 0);
     }
   };
-  constexpr int N_DSR = (BK / 16) * (WA + (B_NK ? 2 : 8));
+  constexpr int N_DSR = (BK / 16) * (WA + (B_NK ? 2 : 4));
   constexpr int N_MFMA = (BK / 16) * 8 * WA;
   constexpr int N_VMEM = A_ITEMS + B_ITEMS;
   static_assert(N_MFMA >= 2 * N_VMEM, "schedule");
@@ -678,7 +683,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 #pragma unroll
       for (int a = 0; a < WA; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + 16 * b + li) * pr + 4 * t + lg];
+      for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + (B_NK ? 16 * b + li : 2 * li + b)) * pr + 4 * t + lg];
 #pragma unroll
       for (int a = 0; a < WA; ++a)
 #pragma unroll
@@ -692,7 +697,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
   for (int a = 0; a < WA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int n = n0 + wn + 16 * b + li;
+      const int n = n0 + wn + (B_NK ? 16 * b + li : 2 * li + b);
       if (n >= p.N) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
