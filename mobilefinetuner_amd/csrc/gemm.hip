@@ -395,7 +395,9 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
   constexpr int BN = 64;
   constexpr int WA = BM / 32;  // 16-row MFMA tiles per wave (waves are 2 × 2)
   constexpr int PA = BK + 4;
-  constexpr int PB = B_NK ? BK + 4 : BN + 4;
+  // [K,N] B: 4·PB ≡ 32 (mod 64) puts lane groups g and g+1 of a 64-bit
+  // fragment read in disjoint LDS bank halves.
+  constexpr int PB = B_NK ? BK + 4 : BN + 8;
   constexpr int A_ITEMS = BM * BK / 4 / 256;
   constexpr int B_ITEMS = BN * BK / 4 / 256;
   constexpr int A_STAGE = BM * PA;
