@@ -730,7 +730,7 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   constexpr int BK = 32, BN = 64;
   constexpr int WA = BM / 32;
   constexpr int PA = BK + 4;
-  constexpr int PB = B_NK ? BK + 4 : BN + 4;
+  constexpr int PB = B_NK ? BK + 4 : BN + 8;  // as in gemm_q_kernel
   constexpr int A_ITEMS = BM * BK / 4 / 256;
   constexpr int B_ITEMS = BN * BK / 4 / 256;
   constexpr int A_STAGE = BM * PA;
@@ -819,14 +819,15 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
 #pragma unroll
     for (int a = 0; a < WA; ++a)
       f.a[a] = *reinterpret_cast<const floatx4*>(as + (wm + 16 * a + li) * PA + kb + 4 * lg);
+    if constexpr (B_NK) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int col = wn + 16 * b + li;
-      if constexpr (B_NK) {
-        f.b[b] = *reinterpret_cast<const floatx4*>(bs + col * PB + kb + 4 * lg);
-      } else {
+      for (int b = 0; b < 2; ++b) f.b[b] = *reinterpret_cast<const floatx4*>(bs + (wn + 16 * b + li) * PB + kb + 4 * lg);
+    } else {  // interleaved column tiles, one 64-bit read per k (as in gemm_q_kernel)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) f.b[b][t] = bs[(kb + 4 * lg + t) * PB + col];
+      for (int t = 0; t < 4; ++t) {
+        const float2 v = *reinterpret_cast<const float2*>(bs + (kb + 4 * lg + t) * PB + wn + 2 * li);
+        f.b[0][t] = v.x;
+        f.b[1][t] = v.y;
       }
     }
   };
@@ -844,8 +845,7 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
 
   Frags pf, f1;
   int s_cur = 0, s_nxt = 1, s_st = 2;  // stages of panels k, k+1, k+2 (wave-uniform)
-  // LDS read instructions per read_frags (the column reads of a [K,N] B pair
-  // up into ds_read2_b32) and the schedule of one step: f1's reads, pf's 16
+  // LDS read instructions per read_frags and the schedule of one step: f1's reads, pf's 16
   // MFMAs, the next panel's reads, then f1's 16 MFMAs with the LDS stores and
   // global loads interleaved.
   constexpr int N_RD = WA + (B_NK ? 2 : 4);
@@ -897,7 +897,7 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   for (int a = 0; a < WA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int n = n0 + wn + 16 * b + li;
+      const int n = n0 + wn + (B_NK ? 16 * b + li : 2 * li + b);
       if (n >= p.N) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
