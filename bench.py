@@ -194,7 +194,7 @@ def main():
         t_ms, work, n = cls(CLS_LINEAR)
         ach = work / (t_ms / 1000.0) / 1e12 if t_ms > 0 else 0.0
         result["roofline"] = {
-            "kernel": "gemm_q_kernel (linear fwd + dX, merged LoRA weights)", "bound": "mfma",
+            "kernel": "gemm_q_kernel + gemm_p_kernel (linear fwd + dX, merged LoRA weights)", "bound": "mfma",
             "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
             "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic_bytes(args.config),
             "launches": n, "avg_launch_us": round(1000.0 * t_ms / max(n, 1), 2),
