@@ -122,7 +122,9 @@ def test_model_step_vs_hf(case):
     B, S = 2, 12
     om = O.OracleModel(mc)
     vals = init_values(om, seed=3)
-    ids = RNG.integers(0, mc.vocab, (B, S)).astype(np.int32)
+    # ids from a per-case generator: the result must not depend on test order
+    rng = np.random.default_rng(sorted(CASES).index(case) + 11)
+    ids = rng.integers(0, mc.vocab, (B, S)).astype(np.int32)
     labels = ids.copy()
     labels[1, 4] = -100
     mask = np.ones((B, S), np.float32)
@@ -147,11 +149,18 @@ def test_model_step_vs_hf(case):
     if tot > clip:
         for p in params:
             p.grad *= clip / (tot + 1e-6)
+    grads = {id(p): p.grad.detach().clone() for p in params}
     opt = torch.optim.Adam(params, lr=lr, betas=(0.9, 0.999), eps=1e-8)
     opt.step()
     for name, w in wraps.items():
-        assert rel_err(om.get(name + ".lora_A"), w.A.detach().numpy()) < 2e-5, name
-        assert rel_err(om.get(name + ".lora_B"), w.B.detach().numpy()) < 2e-5, name
+        for t, p in (("lora_A", w.A), ("lora_B", w.B)):
+            # Adam's first step is ~lr*sign(g); an element whose fp64 gradient
+            # is below the fp32 gradient's rounding noise (1e-6 of the tensor's
+            # largest) has no defined sign in fp32, so it is left out.
+            g = grads[id(p)].numpy()
+            ok = np.abs(g) > 1e-6 * np.abs(g).max()
+            assert ok.mean() > 0.99, (name, t)
+            assert rel_err(om.get(name + "." + t)[ok], p.detach().numpy()[ok]) < 2e-5, (name, t)
         assert np.abs(om.get(name + ".lora_A", grad=True)).max() == 0  # zero_grad
 
 
