@@ -713,22 +713,30 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     }
 }
 
-// Pipelined form of gemm_q_kernel for whole 32-deep panels and no rank-r
-// panel.  Panel p lives in LDS stage p % 3 of a three-stage ring, and is
-// stored one step earlier than in gemm_q_kernel, so during step k every wave
-// can already read the first 16-wide fragments of panel k+1 (made visible by
-// the barrier ending step k-1): a step's MFMAs start on fragments that are
-// in registers, and the second half's LDS reads are hidden behind the first
-// half's MFMAs.  Global loads run four panels ahead through two register
-// sets (panel p in set p % 2, stored two steps after it is loaded).  One
-// barrier per step orders both the stores of panel k+2 before their reads
-// in step k+1 and the reads of stage k % 3 before it is rewritten in step
-// k+1.  Panels past the end load the last panel (in bounds) and are stored
-// as zeros on the A side.
-template <int BM, bool B_NK, bool B_F16, int SITE>
+// Pipelined GEMM for whole BK-deep panels (BK = 32 or 64) and no rank-r
+// panel.  Workgroup tile BM×64 (BM = 32, 64 or 128), four waves as 2×2, each
+// owning (BM/2)×32 outputs as 16×16 v_mfma_f32_16x16x4_f32 tiles.  Panel
+// entry j lives in LDS stage j % 3 of a three-stage ring and is stored two
+// steps before it is multiplied, so during step j every wave already holds
+// the fragments of the first 16-wide k block of entry j+1 (read after the
+// barrier that ended step j-1): within a step, the fragments of k block q+1
+// are read while block q is multiplied, and a step's MFMAs never wait on an
+// LDS read issued in the same step.  Global loads run four entries ahead
+// through two register sets (entry j in set j % 2, stored two steps after it
+// was loaded), interleaved with the MFMAs of the step's last k block
+// together with the LDS stores.  One barrier per step orders both the
+// stores of entry j+2 before their reads and the reads of stage j % 3
+// before it is rewritten.
+//
+// The loop runs two steps per iteration (the register sets alternate), so
+// an odd panel count is padded at the front with a virtual entry of zeros
+// stored by the prologue; loads past the last panel re-read the last panel
+// (in bounds) and are never multiplied.  No per-step masks or selects.
+template <int BM, int BK, bool B_NK, bool B_F16, int SITE>
 __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
-  constexpr int BK = 32, BN = 64;
+  constexpr int BN = 64;
   constexpr int WA = BM / 32;
+  constexpr int Q = BK / 16;  // 16-wide k blocks per panel
   constexpr int PA = BK + 4;
   constexpr int PB = B_NK ? BK + 4 : BN + 8;  // as in gemm_q_kernel
   constexpr int A_ITEMS = BM * BK / 4 / 256;
@@ -737,7 +745,7 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   constexpr int B_STAGE = B_NK ? BN * PB : BK * PB;
   constexpr int STAGE = A_STAGE + B_STAGE;
   constexpr int BES = B_F16 ? 2 : 4;
-  static_assert(A_ITEMS >= 1 && B_ITEMS >= 1, "tile config");
+  static_assert(A_ITEMS >= 1 && B_ITEMS >= 1 && (Q == 2 || Q == 4), "tile config");
   __shared__ __attribute__((aligned(16))) float smem[3 * STAGE];
 
   const int wg = blockIdx.x;
@@ -750,6 +758,8 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
+  const int odd = nk & 1;             // entry 0 is a zero panel when nk is odd
+  const int T = nk + odd;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -789,9 +799,10 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   }
 
   floatx4 rs[2][A_ITEMS + B_ITEMS];  // register staging sets
-  auto gload = [&](auto sc, int panel) {
+  // Entry j holds panel j - odd, clamped into [0, nk-1].
+  auto gload = [&](auto sc, int j) {
     constexpr int S = decltype(sc)::value;
-    const int kc = min(kbeg + panel * BK, kend - BK);
+    const int kc = kbeg + min(max(j - odd, 0), nk - 1) * BK;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) rs[S][it] = *reinterpret_cast<const floatx4*>(a_ptr[it] + kc);
     const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
@@ -801,12 +812,11 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
       else rs[S][A_ITEMS + it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
     }
   };
-  auto lstore = [&](auto sc, int stage, int panel) {
+  auto lstore = [&](auto sc, int stage) {
     constexpr int S = decltype(sc)::value;
     float* st = smem + stage * STAGE;
-    const float keep = panel < nk ? 1.f : 0.f;  // past-end panels multiply as zeros
 #pragma unroll
-    for (int it = 0; it < A_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + a_lds[it]) = rs[S][it] * keep;
+    for (int it = 0; it < A_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + a_lds[it]) = rs[S][it];
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + b_lds[it]) = rs[S][A_ITEMS + it];
   };
@@ -843,36 +853,48 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
-  Frags pf, f1;
-  int s_cur = 0, s_nxt = 1, s_st = 2;  // stages of panels k, k+1, k+2 (wave-uniform)
-  // LDS read instructions per read_frags and the schedule of one step: f1's reads, pf's 16
-  // MFMAs, the next panel's reads, then f1's 16 MFMAs with the LDS stores and
-  // global loads interleaved.
-  constexpr int N_RD = WA + (B_NK ? 2 : 4);
+  // Schedule of one step, per k block q: the next block's fragment reads,
+  // then the block's MFMAs; in the last block the LDS stores and global loads
+  // alternate with the MFMAs.
+  constexpr int N_RD = WA + (B_NK ? 2 : 4);  // LDS read instructions per read_frags
   constexpr int N_ST = A_ITEMS + B_ITEMS;
-  constexpr int N_MF = 4 * WA * 2;  // MFMAs per 16-wide k block
-  static_assert(N_MF >= 2 * N_ST, "schedule");
-  auto step = [&](auto sc, int kt) {
-    read_frags(f1, s_cur, 16);     // second half of panel k
-    mfmas(pf);                     // first half of panel k (fragments read last step)
-    read_frags(pf, s_nxt, 0);      // first half of panel k+1 (visible since the last barrier)
-    lstore(sc, s_st, kt + 2);      // panel k+2, loaded two steps ago
-    gload(sc, kt + 4);             // panel k+4 into the same register set
-    mfmas(f1);
-    __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, N_MF, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
+  constexpr int N_MF = 4 * WA * 2;           // MFMAs per 16-wide k block
+  Frags F[2];
+  int s_cur = 0, s_nxt = 1, s_st = 2;  // stages of entries j, j+1, j+2 (wave-uniform)
+  auto step = [&](auto sc, int j) {
 #pragma unroll
-    for (int i = 0; i < N_ST; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    for (int q = 0; q < Q; ++q) {
+      if (q + 1 < Q) read_frags(F[(q + 1) & 1], s_cur, 16 * (q + 1));
+      else read_frags(F[(q + 1) & 1], s_nxt, 0);  // entry j+1, visible since the last barrier
+      if (q == Q - 1) {
+        lstore(sc, s_st);  // entry j+2, loaded two steps ago
+        gload(sc, j + 4);  // into the same register set
+      }
+      mfmas(F[q & 1]);
     }
 #pragma unroll
-    for (int i = 0; i < N_ST; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    for (int q = 0; q < Q; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
+      if (q == Q - 1 && N_MF >= 2 * N_ST) {
+#pragma unroll
+        for (int i = 0; i < N_ST; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < N_ST; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, N_MF - 2 * N_ST, 0);
+      } else if (q == Q - 1) {
+        __builtin_amdgcn_sched_group_barrier(0x200, N_ST, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, N_ST, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, N_MF, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, N_MF, 0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, N_MF - 2 * N_ST, 0);
     __syncthreads();
     const int t = s_cur;
     s_cur = s_nxt;
@@ -881,15 +903,19 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   };
   gload(I0{}, 0);
   gload(I1{}, 1);
-  lstore(I0{}, 0, 0);
-  lstore(I1{}, 1, 1);
+  if (odd) {  // the virtual entry 0: a stage of zeros (no garbage NaN·0 either)
+    for (int i = tid; i < STAGE / 4; i += 256) reinterpret_cast<floatx4*>(smem)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    lstore(I0{}, 0);
+  }
+  lstore(I1{}, 1);
   gload(I0{}, 2);
   gload(I1{}, 3);
   __syncthreads();
-  read_frags(pf, 0, 0);
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(I0{}, kt);
-    step(I1{}, kt + 1);  // when nk is odd this multiplies the zero panel nk
+  read_frags(F[0], 0, 0);
+  for (int j = 0; j < T; j += 2) {
+    step(I0{}, j);
+    step(I1{}, j + 1);
   }
 
   const bool split_out = p.partial != nullptr;
@@ -961,15 +987,15 @@ void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, 
   }
 }
 
-template <int BM, int SITE>
+template <int BM, int BK, int SITE>
 void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, true, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_p_kernel<BM, true, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, BK, true, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_p_kernel<BM, BK, true, false, SITE>), grid, block, 0, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, false, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_p_kernel<BM, false, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, BK, false, true, SITE>), grid, block, 0, s, p);
+    else       hipLaunchKernelGGL((gemm_p_kernel<BM, BK, false, false, SITE>), grid, block, 0, s, p);
   }
 }
 
@@ -980,25 +1006,19 @@ void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   const dim3 grid(p.tiles_per_xcd * 8, splits);
-  // The pipelined kernel takes whole 32-deep panels in every split and no
-  // rank-r panel; it is used for [N,K] B operands (the dX products), where
-  // cold-cache sweeps of the layer shapes measured it 0–20% faster, while
-  // for [K,N] B (column-read fragments) it measured 0–4% slower.  Tuning
-  // hook: MFT_GEMM_PIPE=0 keeps gemm_q_kernel, 2 uses the pipelined kernel
-  // for both layouts.
+  // The pipelined kernel takes whole BK-deep panels in every split and no
+  // rank-r panel; gemm_q_kernel covers K tails and the rank-r panel.  Tuning
+  // hook: MFT_GEMM_PIPE=0 keeps gemm_q_kernel everywhere.
   static const int pipe_mode = [] {
     const char* e = getenv("MFT_GEMM_PIPE");
     return e ? atoi(e) : 1;
   }();
-  const bool pipe_ok = pipe_mode == 2 || (pipe_mode == 1 && b_nk);
-  if constexpr (BK == 32 && BM <= 64) {
-    const bool whole = p.k_chunk % 32 == 0 && p.K % 32 == 0;
-    if (pipe_ok && whole && p.ep.P == nullptr) {
-      if (p.ep.site == 1) launch_p_variant<BM, 1>(s, p, grid, b_nk, b_f16);
-      else launch_p_variant<BM, 0>(s, p, grid, b_nk, b_f16);
-      MFT_LAUNCH_CHECK();
-      return;
-    }
+  const bool whole = p.k_chunk % BK == 0 && p.K % BK == 0;
+  if (pipe_mode != 0 && whole && p.ep.P == nullptr) {
+    if (p.ep.site == 1) launch_p_variant<BM, BK, 1>(s, p, grid, b_nk, b_f16);
+    else launch_p_variant<BM, BK, 0>(s, p, grid, b_nk, b_f16);
+    MFT_LAUNCH_CHECK();
+    return;
   }
   if (p.ep.site == 1) launch_q_variant<BM, BK, 1>(s, p, grid, b_nk, b_f16);
   else launch_q_variant<BM, BK, 0>(s, p, grid, b_nk, b_f16);
@@ -1023,30 +1043,54 @@ struct Plan {
   int bm, bn, splits;
 };
 
-int plan_bk(int bm, int bn) { return ((bm == 64 || bm == 128) && (bn == 64 || bn == 1)) ? 64 : 32; }
+int plan_bk(int bm, int bn) { return ((bm == 64 || bm == 128) && bn == 64) || bn == 1 ? 64 : 32; }
 
-// Tile shape and split-K, from sweeps of the benchmark shapes on MI355X
-// (M = 512 tokens): grids of ≥ 512 64×64 tiles run unsplit; smaller grids
-// with K < 2048 switch to 32×64 tiles (twice the workgroups, no partials);
-// deeper K keeps 64×64 tiles and doubles split-K while the grid has fewer
-// than 512 workgroups and every split keeps at least 512 of K.  Reductions
-// over a vocabulary (K ≥ 16384: the LM head's dH = dlogits·E) keep
-// doubling up to 16 splits and 2048 workgroups — 1.2–1.45× faster than 2–4
-// splits at the Gemma-3 / Qwen2.5 / GPT-2 vocabularies.  Very large grids
-// (the LM head's forward over the vocabulary) use the 128×128 kernel.
+// Tile shape and split-K.  Very large grids (the LM head's forward over the
+// vocabulary) use the 128×128 kernel.  Reductions over a vocabulary
+// (K ≥ 16384: the LM head's dH = dlogits·E) double split-K up to 16 splits
+// and 2048 workgroups — 1.2–1.45× faster than 2–4 splits at the Gemma-3 /
+// Qwen2.5 / GPT-2 vocabularies.  Every other GEMM takes the cheapest of
+// 64- or 32-row tiles with 1, 2, 4 or 8 splits under a wave-quantisation
+// cost model: a launch runs in ceil(workgroups / capacity) rounds, capacity
+// = 256 CUs × resident workgroups per CU (2 for 64-row tiles, 3 for 32-row
+// tiles, from their LDS and VGPR use), a round costs the per-CU matrix work
+// of those workgroups (32-row tiles at 0.8 of the 64-row rate), and a split
+// adds 8 µs plus 2 µs per MB of partials written and read back.  Fitted to
+// cold-cache sweeps of the 41 layer shapes of the five benchmark
+// configurations on MI355X, it lands within 0.8% of the best measured plan
+// in total (a 576-workgroup plan, one full round plus an eighth of a
+// second, was the costliest miss of the previous rule).
 Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
   if (cdiv(M, 128) * cdiv(N, 128) >= 1024) return {128, 128, 1};
-  const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
-  if (tiles >= 512) return {64, 0, 1};
-  if (K < 2048) return {32, 0, 1};
-  const bool vocab = K >= 16384;
-  const int64_t target = vocab ? 2048 : 512;
-  const int max_sp = vocab ? 16 : 8;
-  int sp = 1;
-  while (tiles * sp < target && K / (2 * sp) >= 512 && sp < max_sp &&
-         (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
-    sp *= 2;
-  return {64, 0, sp};
+  if (K >= 16384) {
+    const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
+    int sp = 1;
+    while (tiles * sp < 2048 && K / (2 * sp) >= 512 && sp < 16 &&
+           (size_t)(2 * sp) * M * N * sizeof(float) <= ws_bytes)
+      sp *= 2;
+    return {64, 0, sp};
+  }
+  Plan best{32, 0, 1};
+  double best_t = 1e30;
+  for (int bm : {64, 32}) {
+    const int occ = bm == 64 ? 2 : 3;
+    const double eff = bm == 64 ? 1.0 : 0.8;
+    const int64_t tiles = cdiv(M, bm) * cdiv(N, 64);
+    for (int sp : {1, 2, 4, 8}) {
+      const int64_t kc = cdiv(cdiv(K, sp), 32) * 32;
+      if (cdiv(K, kc) != sp) continue;
+      if (sp > 1 && (kc < 256 || (size_t)sp * M * N * sizeof(float) > ws_bytes)) continue;
+      const int64_t rounds = cdiv(tiles * sp, 256 * occ);
+      // µs: 2·(rows·64·k) FLOPs per workgroup at 80% of a CU's 157.3/256 TFLOP/s
+      double t = (double)rounds * occ * bm * 64 * kc / eff * 2.0 / (157.3e12 / 256) * 1e6 * 1.25;
+      if (sp > 1) t += 8.0 + 2.0 * sp * (double)M * N * 4 / 1e6;
+      if (t < best_t) {
+        best_t = t;
+        best = {bm, 0, sp};
+      }
+    }
+  }
+  return best;
 }
 
 }  // namespace
@@ -1095,7 +1139,7 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
     int bm = 0, bn = 0, sp = 0;
     if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
-         (((bm == 64 || bm == 128) && (bn == 0 || bn == 1)) || (bm == 32 && bn == 0))) &&
+         ((bm == 32 || bm == 64 || bm == 128) && (bn == 0 || bn == 1))) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
@@ -1123,7 +1167,8 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   else if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 128) launch_tile<64, 128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bn == 64) launch_tile<64, 64, 64>(s, p, b_nk, b_f16, splits);
-  else if (pl.bn == 1) launch_q<64, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bm == 64 && pl.bn == 1) launch_q<64, 64>(s, p, b_nk, b_f16, splits);
+  else if (pl.bm == 32 && pl.bn == 1) launch_q<32, 64>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 32) launch_q<32, 32>(s, p, b_nk, b_f16, splits);
   else launch_q<64, 32>(s, p, b_nk, b_f16, splits);
   if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
