@@ -78,6 +78,25 @@ int mft_model_fwd_bwd(mft_model m, const int32_t* ids, const float* mask,
 int mft_model_forward(mft_model m, const int32_t* ids, const float* mask,
                       const int32_t* labels, int n_micro, int seqs_per_micro,
                       int S, float* logits);
+/* Split points of the step for an operator-level host API whose autograd
+ * tape runs model.forward → lm_cross_entropy → mul(loss, 1/accum) →
+ * backward() one call at a time (gpt2_small_lora_finetune/src/main.cpp:
+ * 471-487).  mft_model_forward_train runs the forward of nseq sequences of
+ * length S and keeps every activation; mft_model_logits gives the device
+ * logits buffer [nseq*S rows, row pitch ld ≥ vocab].  mft_model_ce adds the
+ * summed NLL and the valid-target count of that forward's logits to the
+ * DEVICE scalars loss_sum / n_valid (labels: device int32 [nseq*S], HF shift,
+ * ignore_index); with backward != 0 it also overwrites the logits with
+ * dlogits = upstream·(softmax − onehot)/norm (norm = norm_count if > 0, else
+ * the valid count), after which mft_model_backward accumulates the LoRA
+ * gradients.  Asynchronous. */
+int mft_model_forward_train(mft_model m, const int32_t* ids, const float* mask,
+                            int nseq, int S);
+int mft_model_logits(mft_model m, float** logits, int64_t* ld);
+int mft_model_ce(mft_model m, const int32_t* labels, int nseq, int S,
+                 int ignore_index, float upstream, int64_t norm_count,
+                 int backward, double* loss_sum, int64_t* n_valid);
+int mft_model_backward(mft_model m, const float* mask, int nseq, int S);
 /* Global grad-norm clip + Adam on the LoRA parameters + zero_grad, entirely
  * on the device (no host round trip). */
 int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps,

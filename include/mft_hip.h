@@ -152,6 +152,17 @@ int mft_sumsq(mft_handle h, const float* g, int64_t n, double* out);
 int mft_clip_scale(mft_handle h, const double* sumsq, float max_norm,
                    float* scale_out, float* norm_out);
 
+/* ---- autograd support ---------------------------------------------------------
+ * y = a·x (y may alias x): ops::mul(TensorPtr, float) and the loss scaling of
+ * gpt2_small_lora_finetune/src/main.cpp:481-485 applied to a device tensor.
+ * mft_axpy: y += a·x, gradient accumulation into a leaf's grad across
+ * backward() calls (gpt2_small_lora_finetune/src/main.cpp:471-487).
+ * mft_fill: p[i] = v, the device side of Tensor::zero_grad()
+ * (gpt2_small_lora_finetune/src/main.cpp:503-505). */
+int mft_scale(mft_handle h, const float* x, int64_t n, float a, float* y);
+int mft_axpy(mft_handle h, float a, const float* x, float* y, int64_t n);
+int mft_fill(mft_handle h, float* p, int64_t n, float v);
+
 /* ---- a10: support ops of the three graphs -------------------------------------
  * LayerNorm (GPT-2, γ/β frozen): saves mean/rstd [M]. */
 int mft_layernorm_fwd(mft_handle h, const float* x, const float* g,

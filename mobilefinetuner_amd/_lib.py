@@ -72,6 +72,9 @@ _SIGS = {
     "mft_glu_bwd": (_I, [_P, _P, _P, _P, _L, _I, _P, _P]),
     "mft_rope": (_I, [_P, _P, _L, _I, _I, _I, _I, _D, _I]),
     "mft_embed": (_I, [_P, _P, _L, _I, _P, _I, _P, _L, _F, _P]),
+    "mft_scale": (_I, [_P, _P, _L, _F, _P]),
+    "mft_axpy": (_I, [_P, _F, _P, _P, _L]),
+    "mft_fill": (_I, [_P, _P, _L, _F]),
     # engine
     "mft_model_create": (_I, [C.POINTER(_P), C.POINTER(ModelCfg), _L, _P]),
     "mft_model_destroy": (_I, [_P]),
@@ -82,6 +85,10 @@ _SIGS = {
     "mft_model_init_params": (_I, [_P, C.c_uint64, _F, _F, _F]),
     "mft_model_fwd_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _F]),
     "mft_model_forward": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "mft_model_forward_train": (_I, [_P, _P, _P, _I, _I]),
+    "mft_model_logits": (_I, [_P, C.POINTER(_P), C.POINTER(_L)]),
+    "mft_model_ce": (_I, [_P, _P, _I, _I, _I, _F, _L, _I, _P, _P]),
+    "mft_model_backward": (_I, [_P, _P, _I, _I]),
     "mft_model_opt_step": (_I, [_P, _F, _F, _F, _F, _F, _F]),
     "mft_model_train_step": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _F, _F, _F, _F, _F, _F, _I]),
     "mft_model_read_stats": (_I, [_P, C.POINTER(_F), C.POINTER(_L), C.POINTER(_F)]),

@@ -267,6 +267,30 @@ int mft_clip_scale(mft_handle h, const double* sumsq, float max_norm,
   });
 }
 
+int mft_scale(mft_handle h, const float* x, int64_t n, float a, float* y) {
+  return guarded([&] {
+    require_handle(h);
+    if (n < 0 || (n > 0 && (!x || !y))) throw mft::Error(MFT_EINVAL, "mft_scale: bad arguments");
+    mft::scale(h->stream, x, n, a, y);
+  });
+}
+
+int mft_axpy(mft_handle h, float a, const float* x, float* y, int64_t n) {
+  return guarded([&] {
+    require_handle(h);
+    if (n < 0 || (n > 0 && (!x || !y))) throw mft::Error(MFT_EINVAL, "mft_axpy: bad arguments");
+    mft::axpy(h->stream, a, x, y, n);
+  });
+}
+
+int mft_fill(mft_handle h, float* p, int64_t n, float v) {
+  return guarded([&] {
+    require_handle(h);
+    if (n < 0 || (n > 0 && !p)) throw mft::Error(MFT_EINVAL, "mft_fill: bad arguments");
+    mft::fill_const(h->stream, p, n, v);
+  });
+}
+
 int mft_layernorm_fwd(mft_handle h, const float* x, const float* g,
                       const float* b, int64_t M, int64_t C, float eps,
                       float* y, float* mean, float* rstd) {

@@ -298,6 +298,8 @@ void fill_normal(hipStream_t s, float* p, int64_t n, uint64_t seed, float std,
 void fill_normal_f16(hipStream_t s, uint16_t* p, int64_t n, uint64_t seed,
                      float std);
 void fill_const(hipStream_t s, float* p, int64_t n, float v);
+void scale(hipStream_t s, const float* x, int64_t n, float a, float* y);
+void axpy(hipStream_t s, float a, const float* x, float* y, int64_t n);
 void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,
                       int32_t hi);
 

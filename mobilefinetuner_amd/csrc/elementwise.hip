@@ -390,6 +390,16 @@ __global__ void fill_const_kernel(float* p, int64_t n, float v) {
        i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
 }
+__global__ void scale_kernel(const float* x, int64_t n, float a, float* y) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = a * x[i];
+}
+__global__ void axpy_kernel(float a, const float* x, float* y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = fmaf(a, x[i], y[i]);
+}
 __global__ void fill_uniform_int_kernel(int32_t* p, int64_t n, uint64_t seed,
                                         int32_t hi) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -550,6 +560,16 @@ void fill_normal_f16(hipStream_t s, uint16_t* p, int64_t n, uint64_t seed,
 void fill_const(hipStream_t s, float* p, int64_t n, float v) {
   if (n <= 0) return;
   hipLaunchKernelGGL(fill_const_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
+  MFT_LAUNCH_CHECK();
+}
+void scale(hipStream_t s, const float* x, int64_t n, float a, float* y) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n, a, y);
+  MFT_LAUNCH_CHECK();
+}
+void axpy(hipStream_t s, float a, const float* x, float* y, int64_t n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(axpy_kernel, dim3(grid_for(n)), dim3(256), 0, s, a, x, y, n);
   MFT_LAUNCH_CHECK();
 }
 void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,

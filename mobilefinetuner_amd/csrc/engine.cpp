@@ -144,6 +144,10 @@ struct mft_model_s {
   int* d_t = nullptr;       // Adam step count (advanced on the device)
   int n_micro_pending = 0;
   int adam_t = 0;
+  // operator-level split points: shape of the forward whose activations are
+  // kept (0 = none) and whether its logits buffer now holds dlogits
+  int api_nseq = 0, api_S = 0;
+  bool api_dlogits = false;
   // captured train-step graph
   hipStream_t cap_stream = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
@@ -1181,6 +1185,51 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask, const 
                                sizeof(float) * m->c.vocab, (size_t)nseq * S, hipMemcpyDeviceToDevice,
                                m->stream));
     if (labels) cross_entropy(m, labels, n_micro, seqs_per_micro, S, 1.f, false);
+  });
+}
+
+int mft_model_forward_train(mft_model m, const int32_t* ids, const float* mask, int nseq, int S) {
+  return guarded([&] {
+    if (!m || !ids) throw Error(MFT_EINVAL, "null argument");
+    if (nseq <= 0 || S <= 0) throw Error(MFT_EINVAL, "empty batch");
+    if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
+    if (m->c.arch == MFT_ARCH_GPT2 && S > m->c.max_pos) throw Error(MFT_EINVAL, "seq_len exceeds n_positions");
+    forward(m, ids, mask, nseq, S);
+    m->api_nseq = nseq;
+    m->api_S = S;
+    m->api_dlogits = false;
+  });
+}
+
+int mft_model_logits(mft_model m, float** logits, int64_t* ld) {
+  return guarded([&] {
+    if (!m || !logits || !ld) throw Error(MFT_EINVAL, "null argument");
+    *logits = m->logits;
+    *ld = m->ldv;
+  });
+}
+
+int mft_model_ce(mft_model m, const int32_t* labels, int nseq, int S, int ignore_index, float upstream,
+                 int64_t norm_count, int backward, double* loss_sum, int64_t* n_valid) {
+  return guarded([&] {
+    if (!m || !labels) throw Error(MFT_EINVAL, "null argument");
+    if (nseq != m->api_nseq || S != m->api_S || nseq <= 0)
+      throw Error(MFT_EINVAL, "mft_model_ce: no forward of this shape is pending");
+    if (m->api_dlogits) throw Error(MFT_EINVAL, "mft_model_ce: the logits were already turned into dlogits");
+    ce_fwd_bwd(m->stream, m->logits, labels, nseq, S, m->c.vocab, m->ldv, ignore_index, upstream, norm_count,
+               loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt);
+    if (backward) m->api_dlogits = true;
+  });
+}
+
+int mft_model_backward(mft_model m, const float* mask, int nseq, int S) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    if (nseq != m->api_nseq || S != m->api_S || nseq <= 0 || !m->api_dlogits)
+      throw Error(MFT_EINVAL, "mft_model_backward: needs mft_model_forward_train and mft_model_ce(backward) first");
+    backward(m, mask, nseq, S);
+    m->api_nseq = m->api_S = 0;
+    m->api_dlogits = false;
   });
 }
 

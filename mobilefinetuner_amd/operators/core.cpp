@@ -1,0 +1,655 @@
+// core.cpp — Tensor, autograd tape, operators, LM loss, Adam and memory hooks
+// of the finetune_ops host library, on libmft_hip's C-ABI.
+//
+// Host code only: every computation is a libmft_hip kernel launch on the
+// library's stream; this file moves pointers, shapes and gradients.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "finetune_ops/core/autograd_engine.h"
+#include "finetune_ops/core/lm_loss.h"
+#include "finetune_ops/core/memory_manager.h"
+#include "finetune_ops/core/ops.h"
+#include "finetune_ops/optim/adam.h"
+#include "internal.h"
+
+namespace ops {
+
+namespace detail {
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void mft_check(int rc, const char* what) {
+  if (rc != 0) throw std::runtime_error(std::string(what) + ": " + mft_last_error());
+}
+
+mft_handle handle() {
+  // One handle on the default stream: host copies (hipMemcpy) order with it.
+  static mft_handle h = [] {
+    mft_handle out = nullptr;
+    mft_check(mft_create(&out, nullptr), "mft_create");
+    return out;
+  }();
+  return h;
+}
+
+float read_scalar(const TensorPtr& t) {
+  if (!t || t->numel() != 1) throw std::runtime_error("expected a one-element tensor");
+  if (t->dtype() != kFloat32) throw std::runtime_error("expected a float32 tensor");
+  return t->data<float>()[0];
+}
+
+}  // namespace detail
+
+using detail::hip_check;
+using detail::mft_check;
+
+size_t dtype_size(DType t) {
+  switch (t) {
+    case kFloat32: return 4;
+    case kInt32: return 4;
+    case kFloat16: return 2;
+  }
+  throw std::runtime_error("unknown dtype");
+}
+
+// ---------------------------------------------------------------- Tensor --
+
+void Tensor::init_shape(std::vector<int64_t> shape, DType dtype, Device device) {
+  int64_t n = 1;
+  for (int64_t d : shape) {
+    if (d < 0) throw std::invalid_argument("Tensor: negative dimension");
+    n *= d;
+  }
+  shape_ = std::move(shape);
+  numel_ = n;
+  dtype_ = dtype;
+  device_ = device;
+  pitch_ = shape_.empty() ? 1 : shape_.back();
+}
+
+Tensor::Tensor(std::vector<int64_t> shape, DType dtype, Device device) {
+  init_shape(std::move(shape), dtype, device);
+  const size_t bytes = (size_t)numel_ * dtype_size(dtype_);
+  if (bytes) {
+    hip_check(hipMalloc(&dev_, bytes), "hipMalloc");
+    owns_ = true;
+    hip_check(hipMemset(dev_, 0, bytes), "hipMemset");
+  }
+}
+
+Tensor::Tensor(std::vector<int64_t> shape, const void* data, DType dtype, Device device) {
+  init_shape(std::move(shape), dtype, device);
+  const size_t bytes = (size_t)numel_ * dtype_size(dtype_);
+  if (bytes) {
+    if (!data) throw std::invalid_argument("Tensor: null data");
+    hip_check(hipMalloc(&dev_, bytes), "hipMalloc");
+    owns_ = true;
+    hip_check(hipMemcpy(dev_, data, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  }
+}
+
+TensorPtr Tensor::view(std::vector<int64_t> shape, DType dtype, void* device_ptr, int64_t pitch,
+                       std::shared_ptr<void> owner) {
+  TensorPtr t(new Tensor());
+  t->init_shape(std::move(shape), dtype, kGPU);
+  if (!t->shape_.empty() && pitch < t->shape_.back()) throw std::invalid_argument("Tensor::view: pitch < row length");
+  if (!t->shape_.empty()) t->pitch_ = pitch;
+  t->dev_ = device_ptr;
+  t->owns_ = false;
+  t->owner_ = std::move(owner);
+  return t;
+}
+
+Tensor::~Tensor() {
+  if (owns_ && dev_) (void)hipFree(dev_);
+}
+
+void Tensor::sync_host(bool will_write) const {
+  const size_t esz = dtype_size(dtype_);
+  if (host_.size() != (size_t)numel_ * esz) {
+    host_.assign((size_t)numel_ * esz, 0);
+    host_state_ = 0;
+  }
+  if (host_state_ == 0 && numel_ > 0) {
+    const int64_t row = shape_.empty() ? 1 : shape_.back();
+    const int64_t rows = row ? numel_ / row : 0;
+    if (pitch_ == row)
+      hip_check(hipMemcpy(host_.data(), dev_, host_.size(), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    else
+      hip_check(hipMemcpy2D(host_.data(), row * esz, dev_, pitch_ * esz, row * esz, rows, hipMemcpyDeviceToHost),
+                "hipMemcpy2D D2H");
+    host_state_ = 1;
+  }
+  if (will_write) host_state_ = 2;
+}
+
+void Tensor::upload_if_dirty() const {
+  if (host_state_ != 2) return;
+  const size_t esz = dtype_size(dtype_);
+  const int64_t row = shape_.empty() ? 1 : shape_.back();
+  const int64_t rows = row ? numel_ / row : 0;
+  if (pitch_ == row)
+    hip_check(hipMemcpy(dev_, host_.data(), host_.size(), hipMemcpyHostToDevice), "hipMemcpy H2D");
+  else
+    hip_check(hipMemcpy2D(dev_, pitch_ * esz, host_.data(), row * esz, row * esz, rows, hipMemcpyHostToDevice),
+              "hipMemcpy2D H2D");
+  host_state_ = 1;
+}
+
+void* Tensor::device_data() {
+  upload_if_dirty();
+  return dev_;
+}
+
+const void* Tensor::device_data() const {
+  upload_if_dirty();
+  return dev_;
+}
+
+void Tensor::mark_device_written() { host_state_ = 0; }
+
+void Tensor::zero_grad() {
+  if (!grad_) return;
+  if (grad_->dtype() != kFloat32) throw std::runtime_error("zero_grad: float32 gradients only");
+  if (!grad_->contiguous()) throw std::runtime_error("zero_grad: strided gradient");
+  mft_check(mft_fill(detail::handle(), static_cast<float*>(grad_->device_data()), grad_->numel(), 0.f), "mft_fill");
+  grad_->mark_device_written();
+}
+
+void Tensor::backward() {
+  if (numel_ != 1) throw std::runtime_error("backward(): the tensor must have one element (pass a gradient otherwise)");
+  const float one = 1.f;
+  backward(std::make_shared<Tensor>(std::vector<int64_t>{1}, &one, kFloat32, kCPU));
+}
+
+void Tensor::backward(const TensorPtr& grad_output) {
+  autograd::Engine::instance().backward(shared_from_this(), grad_output);
+}
+
+TensorPtr zeros(const std::vector<int64_t>& shape, DType dtype) { return std::make_shared<Tensor>(shape, dtype, kGPU); }
+
+TensorPtr from_host(const std::vector<int64_t>& shape, const void* data, DType dtype) {
+  return std::make_shared<Tensor>(shape, data, dtype, kGPU);
+}
+
+// -------------------------------------------------------------- autograd --
+
+namespace autograd {
+
+Engine& Engine::instance() {
+  static Engine e;
+  return e;
+}
+
+void Engine::record(const TensorPtr& out, std::shared_ptr<Node> fn) {
+  if (!enabled_) return;
+  bool needs = false;
+  for (const auto& in : fn->inputs) needs = needs || (in && (in->requires_grad() || in->grad_fn()));
+  if (!needs) return;
+  out->set_grad_fn(std::move(fn));
+  out->set_requires_grad(true);
+  if (recorded_.size() >= 4096) {  // forget outputs that no longer exist
+    std::vector<std::weak_ptr<Tensor>> live;
+    for (auto& w : recorded_)
+      if (!w.expired()) live.push_back(w);
+    recorded_.swap(live);
+  }
+  recorded_.push_back(out);
+}
+
+void Engine::clear_graph() {
+  for (auto& w : recorded_)
+    if (auto t = w.lock()) t->set_grad_fn(nullptr);
+  recorded_.clear();
+}
+
+void accumulate_grad(const TensorPtr& t, const TensorPtr& g) {
+  if (g->numel() != t->numel()) throw std::runtime_error("gradient size mismatch");
+  if (!t->grad()) {
+    auto z = std::make_shared<Tensor>(t->shape(), kFloat32, kGPU);
+    t->set_grad(z);
+  }
+  const TensorPtr& dst = t->grad();
+  if (!dst->contiguous() || !g->contiguous()) throw std::runtime_error("accumulate_grad: strided tensors");
+  mft_check(mft_axpy(detail::handle(), 1.f, static_cast<const float*>(g->device_data()),
+                     static_cast<float*>(dst->device_data()), g->numel()),
+            "mft_axpy");
+  dst->mark_device_written();
+}
+
+void Engine::backward(const TensorPtr& root, const TensorPtr& grad_output) {
+  if (!root->grad_fn()) {
+    if (root->requires_grad()) accumulate_grad(root, grad_output);
+    return;
+  }
+  // Reverse topological order of the nodes reachable from the root.
+  std::vector<Node*> order;
+  std::unordered_set<Node*> seen;
+  std::function<void(Node*)> visit = [&](Node* n) {
+    if (!seen.insert(n).second) return;
+    for (const auto& in : n->inputs)
+      if (in && in->grad_fn()) visit(in->grad_fn().get());
+    order.push_back(n);
+  };
+  visit(root->grad_fn().get());
+  std::unordered_map<Node*, TensorPtr> pending;
+  pending[root->grad_fn().get()] = grad_output;
+  if (root->retains_grad()) accumulate_grad(root, grad_output);
+  for (auto it = order.rbegin(); it != order.rend(); ++it) {
+    Node* n = *it;
+    auto pit = pending.find(n);
+    if (pit == pending.end()) continue;
+    TensorPtr g = pit->second;
+    pending.erase(pit);
+    std::vector<TensorPtr> gin = n->apply(g);
+    for (size_t i = 0; i < n->inputs.size() && i < gin.size(); ++i) {
+      const TensorPtr& in = n->inputs[i];
+      const TensorPtr& gi = gin[i];
+      if (!in || !gi) continue;
+      if (in->grad_fn()) {
+        Node* p = in->grad_fn().get();
+        auto q = pending.find(p);
+        if (q == pending.end()) {
+          pending[p] = gi;
+        } else {  // sum of the gradients reaching one output
+          auto sum = std::make_shared<Tensor>(gi->shape(), kFloat32, kGPU);
+          mft_check(mft_axpy(detail::handle(), 1.f, static_cast<const float*>(q->second->device_data()),
+                             static_cast<float*>(sum->device_data()), sum->numel()), "mft_axpy");
+          mft_check(mft_axpy(detail::handle(), 1.f, static_cast<const float*>(gi->device_data()),
+                             static_cast<float*>(sum->device_data()), sum->numel()), "mft_axpy");
+          q->second = sum;
+        }
+        if (in->retains_grad()) accumulate_grad(in, gi);
+      } else if (in->requires_grad()) {
+        accumulate_grad(in, gi);
+      }
+    }
+  }
+}
+
+}  // namespace autograd
+
+// ------------------------------------------------------------- operators --
+
+namespace {
+
+using autograd::Node;
+
+const float* fptr(const TensorPtr& t) { return t ? static_cast<const float*>(t->device_data()) : nullptr; }
+
+void require_f32(const TensorPtr& t, const char* what) {
+  if (!t) throw std::invalid_argument(std::string(what) + ": null tensor");
+  if (t->dtype() != kFloat32) throw std::invalid_argument(std::string(what) + ": float32 tensor required");
+  if (!t->contiguous()) throw std::invalid_argument(std::string(what) + ": contiguous tensor required");
+}
+
+TensorPtr new_f32(const std::vector<int64_t>& shape) { return std::make_shared<Tensor>(shape, kFloat32, kGPU); }
+
+struct MulNode : Node {
+  float s;
+  const char* name() const override { return "MulBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    auto out = new_f32(g->shape());
+    mft_check(mft_scale(detail::handle(), fptr(g), g->numel(), s, static_cast<float*>(out->device_data())), "mft_scale");
+    return {out};
+  }
+};
+
+struct AddNode : Node {
+  const char* name() const override { return "AddBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override { return {g, g}; }
+};
+
+struct ReshapeNode : Node {
+  std::vector<int64_t> in_shape;
+  const char* name() const override { return "ReshapeBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    return {Tensor::view(in_shape, kFloat32, g->device_data(), in_shape.empty() ? 1 : in_shape.back(), g)};
+  }
+};
+
+int64_t rows_of(const TensorPtr& x) { return x->shape().empty() ? 1 : x->numel() / x->shape().back(); }
+
+struct LinearNode : Node {
+  // inputs: x, A, B  (W, b frozen, saved below)
+  TensorPtr W, xa;
+  int w_dtype = MFT_F32;
+  float scale = 0.f;
+  int64_t M = 0, K = 0, N = 0;
+  int r = 0;
+  const char* name() const override { return "LoRALinearBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    require_f32(g, "linear backward");
+    const TensorPtr& x = inputs[0];
+    const TensorPtr A = inputs.size() > 1 ? inputs[1] : nullptr;
+    const TensorPtr B = inputs.size() > 2 ? inputs[2] : nullptr;
+    const bool need_dx = x->requires_grad() || x->grad_fn();
+    TensorPtr dx = need_dx ? new_f32(x->shape()) : nullptr;
+    TensorPtr dA = A ? new_f32(A->shape()) : nullptr;
+    TensorPtr dB = B ? new_f32(B->shape()) : nullptr;
+    mft_check(mft_lora_linear_bwd(detail::handle(), fptr(g), fptr(x), W->device_data(), w_dtype, fptr(A), fptr(B),
+                                  fptr(xa), M, K, N, r, scale, dx ? static_cast<float*>(dx->device_data()) : nullptr,
+                                  dA ? static_cast<float*>(dA->device_data()) : nullptr,
+                                  dB ? static_cast<float*>(dB->device_data()) : nullptr, 0, 0),
+              "mft_lora_linear_bwd");
+    return {dx, dA, dB};
+  }
+};
+
+struct AttnNode : Node {
+  // inputs: q, k, v
+  TensorPtr o, lse, kmask;
+  int B = 0, S = 0, Hq = 0, Hkv = 0, hd = 0, window = 0;
+  float scale = 0.f;
+  const char* name() const override { return "CausalAttentionBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    require_f32(g, "attention backward");
+    auto dq = new_f32(inputs[0]->shape()), dk = new_f32(inputs[1]->shape()), dv = new_f32(inputs[2]->shape());
+    mft_check(mft_attn_bwd(detail::handle(), fptr(inputs[0]), (int64_t)Hq * hd, fptr(inputs[1]), (int64_t)Hkv * hd,
+                           fptr(inputs[2]), (int64_t)Hkv * hd, fptr(o), (int64_t)Hq * hd, fptr(g), (int64_t)Hq * hd,
+                           fptr(lse), B, Hq, Hkv, S, hd, scale, 1, window, fptr(kmask),
+                           static_cast<float*>(dq->device_data()), (int64_t)Hq * hd,
+                           static_cast<float*>(dk->device_data()), (int64_t)Hkv * hd,
+                           static_cast<float*>(dv->device_data()), (int64_t)Hkv * hd),
+              "mft_attn_bwd");
+    return {dq, dk, dv};
+  }
+};
+
+}  // namespace
+
+TensorPtr mul(const TensorPtr& a, float s) {
+  require_f32(a, "mul");
+  auto out = new_f32(a->shape());
+  mft_check(mft_scale(detail::handle(), fptr(a), a->numel(), s, static_cast<float*>(out->device_data())), "mft_scale");
+  auto n = std::make_shared<MulNode>();
+  n->s = s;
+  n->inputs = {a};
+  autograd::Engine::instance().record(out, n);
+  return out;
+}
+
+TensorPtr add(const TensorPtr& a, const TensorPtr& b) {
+  require_f32(a, "add");
+  require_f32(b, "add");
+  if (a->shape() != b->shape()) throw std::invalid_argument("add: shape mismatch");
+  auto out = new_f32(a->shape());
+  float* o = static_cast<float*>(out->device_data());
+  mft_check(mft_axpy(detail::handle(), 1.f, fptr(a), o, a->numel()), "mft_axpy");
+  mft_check(mft_axpy(detail::handle(), 1.f, fptr(b), o, b->numel()), "mft_axpy");
+  auto n = std::make_shared<AddNode>();
+  n->inputs = {a, b};
+  autograd::Engine::instance().record(out, n);
+  return out;
+}
+
+TensorPtr lora_linear(const TensorPtr& x, const TensorPtr& W, const TensorPtr& b, const TensorPtr& A,
+                      const TensorPtr& B, float scale) {
+  require_f32(x, "linear input");
+  if (!W || W->dim() != 2 || !W->contiguous()) throw std::invalid_argument("linear: W must be a contiguous [in, out] matrix");
+  if (W->dtype() != kFloat32 && W->dtype() != kFloat16) throw std::invalid_argument("linear: W must be float32 or float16");
+  if (W->requires_grad()) throw std::invalid_argument("linear: W is frozen on this path (no dW); call set_requires_grad(false)");
+  if (b && b->requires_grad()) throw std::invalid_argument("linear: the bias is frozen on this path");
+  const int64_t K = W->shape()[0], N = W->shape()[1];
+  if (x->shape().empty() || x->shape().back() != K) throw std::invalid_argument("linear: x's last dimension must equal W's rows");
+  if ((A == nullptr) != (B == nullptr)) throw std::invalid_argument("lora_linear: A and B must both be given");
+  int r = 0;
+  if (A) {
+    require_f32(A, "lora A");
+    require_f32(B, "lora B");
+    r = (int)A->shape()[0];
+    if (A->dim() != 2 || A->shape()[1] != K || B->dim() != 2 || B->shape()[0] != N || B->shape()[1] != r)
+      throw std::invalid_argument("lora_linear: A must be [r, in] and B [out, r]");
+  }
+  if (b) {
+    require_f32(b, "bias");
+    if (b->numel() != N) throw std::invalid_argument("linear: bias must have out elements");
+  }
+  const int64_t M = rows_of(x);
+  std::vector<int64_t> oshape = x->shape();
+  oshape.back() = N;
+  auto y = new_f32(oshape);
+  TensorPtr xa = r ? new_f32({M, r}) : nullptr;
+  const int wdt = W->dtype() == kFloat16 ? MFT_F16 : MFT_F32;
+  mft_check(mft_lora_linear_fwd(detail::handle(), fptr(x), M, K, W->device_data(), wdt, N, fptr(b), fptr(A), fptr(B), r,
+                                scale, static_cast<float*>(y->device_data()),
+                                xa ? static_cast<float*>(xa->device_data()) : nullptr, nullptr),
+            "mft_lora_linear_fwd");
+  auto n = std::make_shared<LinearNode>();
+  n->W = W;
+  n->xa = xa;
+  n->w_dtype = wdt;
+  n->scale = scale;
+  n->M = M;
+  n->K = K;
+  n->N = N;
+  n->r = r;
+  n->inputs = {x};
+  if (A) {
+    n->inputs.push_back(A);
+    n->inputs.push_back(B);
+  }
+  autograd::Engine::instance().record(y, n);
+  return y;
+}
+
+TensorPtr linear(const TensorPtr& x, const TensorPtr& W, const TensorPtr& b) {
+  return lora_linear(x, W, b, nullptr, nullptr, 0.f);
+}
+
+TensorPtr causal_attention(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, float scale, int window,
+                           const TensorPtr& key_mask) {
+  require_f32(q, "attention q");
+  require_f32(k, "attention k");
+  require_f32(v, "attention v");
+  if (q->dim() != 4 || k->dim() != 4 || v->dim() != 4 || k->shape() != v->shape())
+    throw std::invalid_argument("causal_attention: q [B,S,Hq,hd], k/v [B,S,Hkv,hd]");
+  const int B = (int)q->shape()[0], S = (int)q->shape()[1], Hq = (int)q->shape()[2], hd = (int)q->shape()[3];
+  const int Hkv = (int)k->shape()[2];
+  if (k->shape()[0] != B || k->shape()[1] != S || k->shape()[3] != hd || Hkv <= 0 || Hq % Hkv != 0)
+    throw std::invalid_argument("causal_attention: q/k/v shapes disagree");
+  if (key_mask) {
+    require_f32(key_mask, "attention key mask");
+    if (key_mask->numel() != (int64_t)B * S) throw std::invalid_argument("causal_attention: key mask must be [B, S]");
+  }
+  auto o = new_f32(q->shape());
+  auto lse = new_f32({B, Hq, S});
+  mft_check(mft_attn_fwd(detail::handle(), fptr(q), (int64_t)Hq * hd, fptr(k), (int64_t)Hkv * hd, fptr(v),
+                         (int64_t)Hkv * hd, B, Hq, Hkv, S, hd, scale, 1, window, fptr(key_mask),
+                         static_cast<float*>(o->device_data()), (int64_t)Hq * hd, static_cast<float*>(lse->device_data())),
+            "mft_attn_fwd");
+  auto n = std::make_shared<AttnNode>();
+  n->o = o;
+  n->lse = lse;
+  n->kmask = key_mask;
+  n->B = B;
+  n->S = S;
+  n->Hq = Hq;
+  n->Hkv = Hkv;
+  n->hd = hd;
+  n->window = window;
+  n->scale = scale;
+  n->inputs = {q, k, v};
+  autograd::Engine::instance().record(o, n);
+  return o;
+}
+
+TensorPtr reshape(const TensorPtr& x, const std::vector<int64_t>& shape) {
+  if (!x->contiguous()) throw std::invalid_argument("reshape: contiguous tensor required");
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  if (n != x->numel()) throw std::invalid_argument("reshape: element count differs");
+  auto out = Tensor::view(shape, x->dtype(), x->device_data(), shape.empty() ? 1 : shape.back(), x);
+  auto node = std::make_shared<ReshapeNode>();
+  node->in_shape = x->shape();
+  node->inputs = {x};
+  autograd::Engine::instance().record(out, node);
+  return out;
+}
+
+TensorPtr flatten(const TensorPtr& x, int start_dim, int end_dim) {
+  const int nd = (int)x->dim();
+  if (start_dim < 0) start_dim += nd;
+  if (end_dim < 0) end_dim += nd;
+  if (start_dim < 0 || end_dim >= nd || start_dim > end_dim) throw std::invalid_argument("flatten: bad dimensions");
+  std::vector<int64_t> s;
+  for (int i = 0; i < start_dim; ++i) s.push_back(x->shape()[i]);
+  int64_t m = 1;
+  for (int i = start_dim; i <= end_dim; ++i) m *= x->shape()[i];
+  s.push_back(m);
+  for (int i = end_dim + 1; i < nd; ++i) s.push_back(x->shape()[i]);
+  return reshape(x, s);
+}
+
+// ----------------------------------------------------------------- loss --
+
+namespace {
+
+struct CeNode : Node {
+  // inputs: logits
+  TensorPtr labels;
+  int ignore_index = -100;
+  bool sum = false;
+  int B = 0, S = 0;
+  const char* name() const override { return "LmCrossEntropyBackward"; }
+  std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    const float up = detail::read_scalar(g);
+    const TensorPtr& logits = inputs[0];
+    const int64_t V = logits->shape().back();
+    auto dl = new_f32(logits->shape());
+    auto scratch = new_f32({(int64_t)B * S});
+    mft_check(mft_ce_fwd_bwd(detail::handle(), fptr(logits), static_cast<const int32_t*>(labels->device_data()), B, S, V,
+                             ignore_index, up, sum ? 1 : 0, nullptr, nullptr, static_cast<float*>(dl->device_data()),
+                             static_cast<float*>(scratch->device_data())),
+              "mft_ce_fwd_bwd");
+    return {dl};
+  }
+};
+
+}  // namespace
+
+namespace detail {
+
+TensorPtr make_loss(double loss_sum, int64_t n_valid, bool sum) {
+  const float v = sum ? (float)loss_sum : (n_valid > 0 ? (float)(loss_sum / (double)n_valid) : 0.f);
+  return std::make_shared<Tensor>(std::vector<int64_t>{1}, &v, kFloat32, kCPU);
+}
+
+bool parse_reduction(const std::string& r) {
+  if (r == "mean") return false;
+  if (r == "sum") return true;
+  throw std::invalid_argument("lm_cross_entropy: reduction must be \"mean\" or \"sum\"");
+}
+
+}  // namespace detail
+
+TensorPtr lm_cross_entropy(const TensorPtr& logits, const TensorPtr& labels, int ignore_index,
+                           const std::string& reduction) {
+  const bool sum = detail::parse_reduction(reduction);
+  if (!logits || logits->dtype() != kFloat32 || logits->dim() != 3)
+    throw std::invalid_argument("lm_cross_entropy: logits must be float32 [B, S, V]");
+  if (!labels || labels->dtype() != kInt32 || labels->numel() != logits->shape()[0] * logits->shape()[1])
+    throw std::invalid_argument("lm_cross_entropy: labels must be int32 [B, S]");
+  // Logits produced by an engine-backed model go through the model's own
+  // loss (its logits buffer turns into dlogits in place).
+  if (auto hook = detail::model_loss_hook(logits)) return hook(labels, ignore_index, sum);
+  if (!logits->contiguous()) throw std::invalid_argument("lm_cross_entropy: contiguous logits required");
+  const int B = (int)logits->shape()[0], S = (int)logits->shape()[1];
+  const int64_t V = logits->shape()[2];
+  auto stats = std::make_shared<Tensor>(std::vector<int64_t>{4}, kFloat32, kGPU);  // double sum + int64 count
+  auto scratch = new_f32({(int64_t)B * S});
+  char* st = static_cast<char*>(stats->device_data());
+  mft_check(mft_ce_fwd_bwd(detail::handle(), fptr(logits), static_cast<const int32_t*>(labels->device_data()), B, S, V,
+                           ignore_index, 1.f, 0, reinterpret_cast<double*>(st), reinterpret_cast<int64_t*>(st + 8),
+                           nullptr, static_cast<float*>(scratch->device_data())),
+            "mft_ce_fwd_bwd");
+  double ls = 0;
+  int64_t nv = 0;
+  hip_check(hipMemcpy(&ls, st, 8, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  hip_check(hipMemcpy(&nv, st + 8, 8, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  auto loss = detail::make_loss(ls, nv, sum);
+  auto n = std::make_shared<CeNode>();
+  n->labels = labels;
+  n->ignore_index = ignore_index;
+  n->sum = sum;
+  n->B = B;
+  n->S = S;
+  n->inputs = {logits};
+  autograd::Engine::instance().record(loss, n);
+  return loss;
+}
+
+float perplexity_from_loss(float loss) { return std::exp(loss); }
+
+// ------------------------------------------------------------------ Adam --
+
+struct Adam::State {
+  TensorPtr m, v;
+};
+
+Adam::Adam(const AdamConfig& cfg) : cfg_(cfg) {}
+Adam::~Adam() = default;
+
+void Adam::step(const std::vector<TensorPtr>& params, const std::vector<TensorPtr>& grads) {
+  if (params.size() != grads.size()) throw std::invalid_argument("Adam::step: params and grads differ in length");
+  ++t_;
+  for (size_t i = 0; i < params.size(); ++i) {
+    const TensorPtr& p = params[i];
+    const TensorPtr& g = grads[i];
+    if (!p || !g) continue;
+    require_f32(p, "Adam parameter");
+    require_f32(g, "Adam gradient");
+    if (g->numel() != p->numel()) throw std::invalid_argument("Adam::step: gradient size differs from its parameter");
+    auto& st = state_[p.get()];
+    if (!st) {
+      st = std::make_unique<State>();
+      st->m = new_f32(p->shape());
+      st->v = new_f32(p->shape());
+    }
+    mft_check(mft_adam_step(detail::handle(), static_cast<float*>(p->device_data()), static_cast<float*>(g->device_data()),
+                            static_cast<float*>(st->m->device_data()), static_cast<float*>(st->v->device_data()),
+                            p->numel(), cfg_.learning_rate, cfg_.beta1, cfg_.beta2, cfg_.epsilon, cfg_.weight_decay, t_,
+                            nullptr, 0),
+              "mft_adam_step");
+    p->mark_device_written();
+  }
+}
+
+// ---------------------------------------------------------------- memory --
+
+MemoryManager& MemoryManager::instance() {
+  static MemoryManager m;
+  return m;
+}
+
+void MemoryManager::force_cleanup() { hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+void MemoryManager::clear_unused_memory() { force_cleanup(); }
+void MemoryManager::cleanup_dead_references() {}
+
+void MemoryManager::print_memory_stats() const {
+  size_t free_b = 0, total_b = 0;
+  hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+  std::printf("[MemoryManager] device: %.1f MiB used of %.1f MiB\n", (total_b - free_b) / 1048576.0,
+              total_b / 1048576.0);
+}
+
+size_t MemoryMonitor::get_system_memory_usage() {
+  std::ifstream f("/proc/self/statm");
+  size_t pages = 0, resident = 0;
+  if (f >> pages >> resident) return resident * 4096;
+  return 0;
+}
+
+}  // namespace ops

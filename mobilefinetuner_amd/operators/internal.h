@@ -1,0 +1,28 @@
+// internal.h — shared helpers of the finetune_ops host library (not installed).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <functional>
+#include <memory>
+#include <string>
+
+#include "finetune_ops/core/tensor.h"
+#include "mft_hip.h"
+
+namespace ops {
+namespace detail {
+
+void hip_check(hipError_t e, const char* what);
+void mft_check(int rc, const char* what);
+mft_handle handle();
+float read_scalar(const TensorPtr& t);
+TensorPtr make_loss(double loss_sum, int64_t n_valid, bool sum);
+bool parse_reduction(const std::string& r);
+
+// Loss over logits that an engine-backed model produced (nullptr when the
+// tensor is not such a logits view).
+using ModelLoss = std::function<TensorPtr(const TensorPtr& labels, int ignore_index, bool sum)>;
+ModelLoss model_loss_hook(const TensorPtr& logits);
+
+}  // namespace detail
+}  // namespace ops

@@ -1,0 +1,24 @@
+"""Parity of the finetune_ops C++ API (Tensor / autograd / models / Adam on
+the GPU) against the CPU oracle, through the driver-style program
+tests/cpp/test_operators.cpp (built by __graft_entry__.build())."""
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "tests", "cpp", "bin", "test_operators")
+
+
+@pytest.mark.gpu
+def test_cpp_operator_api_matches_oracle():
+    assert os.path.exists(EXE), "tests/cpp/bin/test_operators missing: run __graft_entry__.build()"
+    print("running", EXE, flush=True)
+    r = subprocess.run([EXE], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-6000:])
+    print(r.stderr[-2000:])
+    fails = [ln for ln in r.stdout.splitlines() if ln.startswith("FAIL")]
+    assert r.returncode == 0 and not fails, "\n".join(fails) or r.stderr[-2000:]
+    # every family and the op chain actually ran
+    for tag in ("ops chain dA", "gpt2 step1", "qwen2 step1", "gemma3 step1", "gemma3-fp16w step1"):
+        assert any(tag in ln for ln in r.stdout.splitlines()), tag
