@@ -297,166 +297,170 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
   }
 }
 
-// Batched rank-r products: each 1024-thread workgroup runs one job's share.
+// Batched rank-r products: each 256-thread workgroup runs one job's share.
+// Both roles are HBM-bound streams over X (every byte read once); they run on
+// the vector units with full-width loads rather than on the matrix cores
+// (r = 8 would fill half a 16-wide MFMA tile and the K split it needs left
+// 1024-thread workgroups with a few KB of loads each).
 //
-// Projection role (out[M,r] = X·Y): 16 rows per workgroup on the matrix
-// cores, K split over the 16 waves in 16-wide blocks (four blocks' loads
-// issued before their MFMAs), wave partials summed in LDS in wave order.
-// Lane (i, g) feeds A = X[m0+i][k0+4g+t] (one 128-bit load per four MFMAs)
-// and B = Y(k0+4g+t, 16·jt+i); it ends holding D[m0+4g+v][16·jt+i].  Y is
-// read once per 16 rows.
+// Projection role (out[M,r] = X·Y, Y(k,j) = Y[j·K+k] or Y[k·r+j]): a wave
+// owns RW consecutive rows (RW·r = 32 or 64 values) and strides K with one
+// 128-bit load per row per lane (a wave reads 1 KB of a row per step); Y's
+// four k rows of the step are the same for every wave of the GPU and come
+// from the caches.  The RW·r per-lane partial sums are combined across the
+// wave by a halving butterfly (each xor-shuffle step hands half of the
+// remaining values to the partner lane), after which value v sits in lanes
+// with lane >> (6 − log2(RW·r)) == v.
 //
-// Outer role (out(j,c) (+)= s·Σ_m P[m,j]·X[m,c]): 16·kBatchCT columns per
-// workgroup (a wave's loads of one row cover whole 128-byte lines), M split
-// over the 16 waves in 32-row chunks with the next chunk's loads in flight,
-// LDS reduction in wave order, column runs per XCD.
-constexpr int kBatchCT = 2;
+// Outer role (out(j,c) (+)= s·Σ_m P[m,j]·X[m,c]): 256 columns per workgroup
+// (four per lane, so a wave reads 1 KB of a row), the rows split over the
+// four waves; P's row is uniform across the wave.  Wave partials are added
+// through LDS in wave order (deterministic), column runs per XCD.
+constexpr int kBatchThreads = 256;
+constexpr int kBatchCols = 256;
 
 template <int R>
-__device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floatx4* lds) {
-  constexpr int JT = (R + 15) / 16;
-  floatx4 (*red)[JT][64] = reinterpret_cast<floatx4 (*)[JT][64]>(lds);  // [kOuterWaves-1]
+constexpr int batch_rows_per_wave() { return R <= 16 ? 4 : 2; }
+
+template <int R>
+__device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M) {
+  constexpr int RW = batch_rows_per_wave<R>();
+  constexpr int V = RW * R;  // 16 .. 64 partial sums per lane
+  static_assert(V >= 2 && V <= 64 && (V & (V - 1)) == 0, "butterfly size");
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int i = lane & 15, g = lane >> 4;
-  const int m0 = b * 16;
-  const int xrow = min(m0 + i, M - 1);
+  const int m0 = (b * 4 + w) * RW;
+  if (m0 >= M) return;  // no barriers in this role
   const int K = jb.K;
-  const int nkb = (K + 15) / 16;
-  const int per = (nkb + kOuterWaves - 1) / kOuterWaves;
-  const int kb0 = min(nkb, w * per), kb1 = min(nkb, kb0 + per);
-  floatx4 acc[JT];
+  const float* xr[RW];
 #pragma unroll
-  for (int jt = 0; jt < JT; ++jt) acc[jt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = kb0; kb < kb1; kb += 4) {
-    floatx4 xa[4], yb[4][JT];
+  for (int q = 0; q < RW; ++q) xr[q] = jb.X + (int64_t)min(m0 + q, M - 1) * jb.ldx;
+  float acc[RW][R];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = 16 * (kb + u) + 4 * g;
-      const bool ok = kb + u < kb1 && k < K;
-      const int kc = ok ? k : 0;  // K is a multiple of 4: k..k+3 stay inside a row
-      const floatx4 xv = *reinterpret_cast<const floatx4*>(jb.X + (int64_t)xrow * jb.ldx + kc);
-      xa[u] = ok ? xv : floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < RW; ++q)
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) {
-        const int j = min(16 * jt + i, R - 1);
-        floatx4 y;
-        if (jb.y_rk) {
-          y = *reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + kc);
-        } else {
+    for (int j = 0; j < R; ++j) acc[q][j] = 0.f;
+  // K is a multiple of 4 (checked on the host), so a 4-vector never crosses a row.
+#pragma unroll 2
+  for (int k = 4 * lane; k < K; k += 256) {
+    floatx4 xv[RW];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] = jb.Y[(int64_t)(kc + t) * R + j];
-        }
-        yb[u][jt] = (ok && 16 * jt + i < R) ? y : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < RW; ++q) xv[q] = *reinterpret_cast<const floatx4*>(xr[q] + k);
+    if (jb.y_rk) {  // Y [r, K]
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        const floatx4 y = *reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + k);
+#pragma unroll
+        for (int q = 0; q < RW; ++q)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[q][j] = fmaf(xv[q][t], y[t], acc[q][j]);
       }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
+    } else {  // Y [K, r]: rows k..k+3 are 4·r consecutive floats
+      const floatx4* yp = reinterpret_cast<const floatx4*>(jb.Y + (int64_t)k * R);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int jt = 0; jt < JT; ++jt)
-          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[u][t], yb[u][jt][t], acc[jt], 0, 0, 0);
-  }
-  if (w > 0) {
+        for (int jq = 0; jq < R / 4; ++jq) {
+          const floatx4 y = yp[t * (R / 4) + jq];
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt) red[w - 1][jt][lane] = acc[jt];
-  }
-  __syncthreads();
-  if (w != 0) return;
+          for (int q = 0; q < RW; ++q)
 #pragma unroll
-  for (int jt = 0; jt < JT; ++jt) {
-    floatx4 v = acc[jt];
-#pragma unroll
-    for (int q = 0; q < kOuterWaves - 1; ++q) v += red[q][jt][lane];
-    const int j = 16 * jt + i;
-    if (j >= R) continue;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 4 * g + e;
-      if (m < M) jb.out[(int64_t)m * R + j] = v[e];
+            for (int e = 0; e < 4; ++e) acc[q][4 * jq + e] = fmaf(xv[q][t], y[e], acc[q][4 * jq + e]);
+        }
     }
+  }
+  float v[V];
+#pragma unroll
+  for (int q = 0; q < RW; ++q)
+#pragma unroll
+    for (int j = 0; j < R; ++j) v[q * R + j] = acc[q][j];
+  int n = V;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    if (n > 1) {
+      const bool upper = (lane & d) != 0;
+#pragma unroll
+      for (int i = 0; i < V / 2; ++i) {
+        if (i < n / 2) {
+          const float send = upper ? v[i] : v[i + n / 2];
+          const float keep = upper ? v[i + n / 2] : v[i];
+          v[i] = keep + __shfl_xor(send, d, 64);
+        }
+      }
+      n /= 2;
+    } else {
+      v[0] += __shfl_xor(v[0], d, 64);
+    }
+  }
+  constexpr int SH = V == 64 ? 0 : V == 32 ? 1 : V == 16 ? 2 : V == 8 ? 3 : V == 4 ? 4 : 5;
+  const int vi = lane >> SH;
+  if ((lane & ((1 << SH) - 1)) == 0) {
+    const int q = vi / R, j = vi % R, m = m0 + q;
+    if (m < M) jb.out[(int64_t)m * R + j] = v[0];
   }
 }
 
 template <int R>
-__device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, floatx4* lds) {
-  constexpr int JT = (R + 15) / 16;
-  constexpr int CT = kBatchCT;
-  floatx4 (*red)[CT][JT][64] = reinterpret_cast<floatx4 (*)[CT][JT][64]>(lds);  // [kOuterWaves-1]
+__device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, float* lds) {
   const int blk = (raw % 8) * (jb.blocks / 8) + raw / 8;
-  const int c0 = blk * 16 * CT;
+  const int c0 = blk * kBatchCols;
   if (c0 >= jb.K) return;  // whole workgroup, before any barrier
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int i = lane & 15, g = lane >> 4;
-  const int per = ((M + kOuterWaves * 32 - 1) / (kOuterWaves * 32)) * 32;
-  const int mb = min(M, w * per), me = min(M, mb + per);
-  floatx4 acc[CT][JT];
+  const int c = c0 + 4 * lane;
+  const bool cok = c < jb.K;  // C is a multiple of 4 (checked on the host)
+  const int per = (M + 3) / 4;
+  const int mb = w * per, me = min(M, mb + per);
+  float acc[R][4];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
+  for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  if (mb < me) {
-    OuterChunk<JT> c0v[CT], c1v[CT];
-    OuterJob o[CT];
-    int ci[CT];
-    bool cok[CT];
+    for (int e = 0; e < 4; ++e) acc[j][e] = 0.f;
+  const float* xp = jb.X + (cok ? c : 0);
+#pragma unroll 4
+  for (int m = mb; m < me; ++m) {
+    const floatx4 x = *reinterpret_cast<const floatx4*>(xp + (int64_t)m * jb.ldx);
+    const floatx4* pp = reinterpret_cast<const floatx4*>(jb.Y + (int64_t)m * R);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      o[ct] = OuterJob{};
-      o[ct].P = jb.Y; o[ct].X = jb.X; o[ct].ldx = jb.ldx; o[ct].C = jb.K;
-      ci[ct] = min(c0 + 16 * ct + i, jb.K - 1);
-      cok[ct] = c0 + 16 * ct + i < jb.K;
-      outer_load(c0v[ct], o[ct], R, mb, me, mb, ci[ct], cok[ct], i, g);
-    }
-    for (int m = mb; m < me; m += 64) {
+    for (int jq = 0; jq < R / 4; ++jq) {
+      const floatx4 pv = pp[jq];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) outer_load(c1v[ct], o[ct], R, m + 32, me, mb, ci[ct], cok[ct], i, g);
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) outer_mfma(acc[ct], c0v[ct]);
-      if (m + 32 >= me) break;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) outer_load(c0v[ct], o[ct], R, m + 64, me, mb, ci[ct], cok[ct], i, g);
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) outer_mfma(acc[ct], c1v[ct]);
+        for (int t = 0; t < 4; ++t) acc[4 * jq + e][t] = fmaf(pv[e], x[t], acc[4 * jq + e][t]);
     }
   }
-  if (w > 0) {
+  // wave-ordered sum through LDS: lds[j][256 columns]
+  for (int q = 0; q < 4; ++q) {
+    if (w == q) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
+      for (int j = 0; j < R; ++j)
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) red[w - 1][ct][jt][lane] = acc[ct][jt];
+        for (int e = 0; e < 4; ++e) {
+          float& d = lds[j * kBatchCols + 4 * lane + e];
+          d = q == 0 ? acc[j][e] : d + acc[j][e];
+        }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (w != 0) return;
+  if (w != 0 || !cok) return;
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
+  for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt) {
-      floatx4 v = acc[ct][jt];
-#pragma unroll
-      for (int q = 0; q < kOuterWaves - 1; ++q) v += red[q][ct][jt][lane];
-      const int j = 16 * jt + i;
-      if (j >= R) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = c0 + 16 * ct + 4 * g + e;
-        if (c >= jb.K) continue;
-        float* out = jb.out + (int64_t)j * jb.osj + (int64_t)c * jb.osc;
-        *out = jb.accumulate ? fmaf(jb.scale, v[e], *out) : jb.scale * v[e];
-      }
+    for (int e = 0; e < 4; ++e) {
+      float* out = jb.out + (int64_t)j * jb.osj + (int64_t)(c + e) * jb.osc;
+      const float v = lds[j * kBatchCols + 4 * lane + e];
+      *out = jb.accumulate ? fmaf(jb.scale, v, *out) : jb.scale * v;
     }
 }
 
 template <int R>
-__global__ __launch_bounds__(64 * kOuterWaves) void rank_batch_kernel(const RankJob* __restrict__ jobs, int njobs,
-                                                                     int nproj, int M) {
-  constexpr int JT = (R + 15) / 16;
-  __shared__ floatx4 lds[(kOuterWaves - 1) * kBatchCT * JT * 64];
-  const int pb = (M + 15) / 16;
+__global__ __launch_bounds__(kBatchThreads) void rank_batch_kernel(const RankJob* __restrict__ jobs, int njobs,
+                                                                   int nproj, int M) {
+  __shared__ float lds[R * kBatchCols];
+  const int pb = (M + 4 * batch_rows_per_wave<R>() - 1) / (4 * batch_rows_per_wave<R>());
   int b = blockIdx.x;
   if (b < nproj * pb) {
     const int ji = b / pb;
-    batch_proj<R>(jobs[ji], b - ji * pb, M, lds);
+    batch_proj<R>(jobs[ji], b - ji * pb, M);
     return;
   }
   b -= nproj * pb;
@@ -506,12 +510,13 @@ void lora_merge(hipStream_t s, const MergeJob* jobs, int njobs, int total_tiles,
   MFT_LAUNCH_CHECK();
 }
 
-int rank_outer_blocks(int C) { return (int)cdiv(cdiv(C, 16 * kBatchCT), 8) * 8; }
+int rank_outer_blocks(int C) { return (int)cdiv(cdiv(C, kBatchCols), 8) * 8; }
 
 void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r) {
   MFT_CHECK_ARG(jobs && njobs > 0 && M > 0, "empty rank batch");
-  const int64_t blocks = (int64_t)nproj * cdiv(M, 16) + outer_blocks;
-  const dim3 grid((unsigned)blocks), block(64 * kOuterWaves);
+  const int rows_per_wg = 4 * (r <= 16 ? 4 : 2);
+  const int64_t blocks = (int64_t)nproj * cdiv(M, rows_per_wg) + outer_blocks;
+  const dim3 grid((unsigned)blocks), block(kBatchThreads);
   switch (r) {
     case 4: hipLaunchKernelGGL(rank_batch_kernel<4>, grid, block, 0, s, jobs, njobs, nproj, M); break;
     case 8: hipLaunchKernelGGL(rank_batch_kernel<8>, grid, block, 0, s, jobs, njobs, nproj, M); break;
