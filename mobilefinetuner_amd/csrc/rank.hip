@@ -276,13 +276,21 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
 #pragma unroll
       for (int u = 0; u < 4; ++u) bv[e][4 * j4 + u] = b4[u];
     }
+  // All four rows' W loads are issued before any is used (rows past K re-read
+  // row K-1 and are not stored), so each thread has four loads in flight.
+  floatx4 w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k = min(k0 + q, jb.K - 1);
+    if (jb.f16)
+      w[q] = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
+    else
+      w[q] = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
+  }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int k = k0 + q;
     if (k >= jb.K) break;
-    floatx4 w;
-    if (jb.f16) w = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
-    else w = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
     float a[R];
 #pragma unroll
     for (int j = 0; j < R; ++j) a[j] = jb.A[(int64_t)j * jb.K + k];
@@ -291,9 +299,9 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
       float d = 0.f;
 #pragma unroll
       for (int j = 0; j < R; ++j) d = fmaf(a[j], bv[e][j], d);
-      w[e] = fmaf(scale, d, w[e]);
+      w[q][e] = fmaf(scale, d, w[q][e]);
     }
-    *reinterpret_cast<floatx4*>(jb.out + (int64_t)k * jb.N + n) = w;
+    *reinterpret_cast<floatx4*>(jb.out + (int64_t)k * jb.N + n) = w[q];
   }
 }
 
