@@ -157,9 +157,10 @@ struct MergeJob {
   const void* W;
   const float* A;
   const float* B;
-  float* out;
+  float* out;  // [K, N] rows ldo apart (ldo > N: a column block of a fused W_eff)
   int K, N, f16;
   int tile0;  // first tile of this job (tiles of 16 rows × 256 columns)
+  int ldo;
 };
 size_t merge_tiles(int K, int N);
 // jobs: device array of njobs MergeJobs with increasing tile0; r ∈ {4, 8, 16, 32}.
@@ -266,6 +267,12 @@ void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x,
                  const float* w, const float* rstd, int64_t M, int64_t C,
                  bool unit_offset, float* dx, const float* resid);
 // The norm of nm applied to finished rows c[M,C] (one of the four launchers).
+// RMSNorm over rows grouped seg per token (row r at (r/seg)·ld + (r%seg)·C):
+// per-head norms reading or writing head rows of a fused q|k|v buffer.
+void rmsnorm_fwd_seg(hipStream_t s, const float* x, int64_t x_ld, const float* w, int64_t M, int64_t C, int seg,
+                     float eps, bool unit_offset, float* y, int64_t y_ld, float* rstd);
+void rmsnorm_bwd_seg(hipStream_t s, const float* dy, int64_t dy_ld, const float* x, int64_t x_ld, const float* w,
+                     const float* rstd, int64_t M, int64_t C, int seg, bool unit_offset, float* dx, int64_t dx_ld);
 void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm& nm);
 // Split-K reduction (partials [splits][M][N], summed in split order) + the
 // GEMM epilogue + the row norm in one pass.  Returns false, launching

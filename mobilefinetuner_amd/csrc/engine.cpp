@@ -46,7 +46,8 @@ struct Param {
 struct Linear {
   int W = -1, b = -1, A = -1, B = -1;
   int K = 0, N = 0;
-  float* weff = nullptr;  // merged weight W + s·Aᵀ·Bᵀ [K, N] fp32 (LoRA linears)
+  float* weff = nullptr;  // merged weight W + s·Aᵀ·Bᵀ [K, N] fp32 (LoRA linears), rows weff_ld apart
+  int weff_ld = 0;
 };
 
 
@@ -62,6 +63,8 @@ struct Acts {
   float* xa[T_MAX];
   float* U[T_MAX];   // dY·B of each LoRA linear (kept for dA at the end of the backward)
   float* DY[T_MAX];  // dY of each LoRA linear, kept until the end of the backward
+  int64_t dy_ld[T_MAX];  // row pitch of DY[t] (N, or the fused q|k|v width)
+  float *qkv, *dyqkv;    // fused q|k|v projection output and its gradient (fuse_qkv)
   float *att, *lse, *o, *ors, *hmid, *n2, *mean2, *rstd2;
   float *gate, *up, *act, *mo, *mrs;
 };
@@ -144,6 +147,10 @@ struct mft_model_s {
   int* d_t = nullptr;       // Adam step count (advanced on the device)
   int n_micro_pending = 0;
   int adam_t = 0;
+  // Qwen2 / Gemma3 with LoRA on q, k and v (merged path): one GEMM for
+  // q|k|v forward and one for its dX, over a W_eff block [d, nqkv]
+  bool fuse_qkv = false;
+  int nqkv = 0;
   // operator-level split points: shape of the forward whose activations are
   // kept (0 = none) and whether its logits buffer now holds dlogits
   int api_nseq = 0, api_S = 0;
@@ -237,8 +244,12 @@ void build_params(mft_model_s* m) {
     L.n1w = add_param(m, pfx + ".input_layernorm.weight", d, 0, false, false, norm_init);
     const int outs[7] = {H * hd, Hk * hd, Hk * hd, d, c.d_ff, c.d_ff, d};
     const int ins[7] = {d, d, d, H * hd, d, d, c.d_ff};
-    for (int t = 0; t < 4; ++t)
-      add_linear(m, L.lin[t], pfx, kHfLin[t], ins[t], outs[t], qwen && t < 3, (c.lora_mask >> t) & 1);
+    for (int t = 0; t < 4; ++t) add_linear(m, L.lin[t], pfx, kHfLin[t], ins[t], outs[t], false, (c.lora_mask >> t) & 1);
+    // Qwen2's q/k/v biases are placed back to back in the frozen arena, so a
+    // fused q|k|v GEMM can take them as one bias vector.
+    if (qwen)
+      for (int t = 0; t < 3; ++t)
+        L.lin[t].b = add_param(m, pfx + "." + kHfLin[t] + ".bias", outs[t], 0, false, false, INIT_NORMAL);
     if (!qwen) {
       L.qn = add_param(m, pfx + ".self_attn.q_norm.weight", hd, 0, false, false, INIT_ZERO);
       L.kn = add_param(m, pfx + ".self_attn.k_norm.weight", hd, 0, false, false, INIT_ZERO);
@@ -314,8 +325,28 @@ bool lora_mergeable(const mft_model_s* m) {
   return any;
 }
 
+// q, k and v fuse into one projection when all three are merged LoRA
+// linears and (Qwen2) their biases sit back to back.
+bool qkv_fusable(const mft_model_s* m) {
+  if (m->c.arch == MFT_ARCH_GPT2 || !lora_mergeable(m)) return false;
+  for (const auto& L : m->L) {
+    for (int t = 0; t < 3; ++t)
+      if (L.lin[t].A < 0) return false;
+    if (L.lin[0].b >= 0) {
+      const char* b0 = static_cast<const char*>(m->P[L.lin[0].b].data);
+      if (L.lin[1].b < 0 || L.lin[2].b < 0 ||
+          static_cast<const char*>(m->P[L.lin[1].b].data) != b0 + 4 * (size_t)L.lin[0].N ||
+          static_cast<const char*>(m->P[L.lin[2].b].data) != b0 + 4 * (size_t)(L.lin[0].N + L.lin[1].N))
+        return false;
+    }
+  }
+  return true;
+}
+
 void alloc_acts(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
+  m->fuse_qkv = qkv_fusable(m);
+  m->nqkv = c.n_head * c.head_dim + 2 * c.n_kv_head * c.head_dim;
   const int64_t M = m->max_tokens;
   const int64_t d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim, ff = c.d_ff, r = c.lora_r;
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
@@ -334,6 +365,27 @@ void alloc_acts(mft_model_s* m) {
         a.k = a.q + d;
         a.v = a.q + 2 * d;
         a.qs = a.ks = a.vs = 3 * d;
+      } else if (m->fuse_qkv) {
+        // one [M, nqkv] projection output: q|k|v (Qwen2), qraw|kraw|v (Gemma3)
+        const int64_t nq = H * hd, nk = Hk * hd, nt = m->nqkv;
+        a.qkv = b.f(M * nt);
+        a.dyqkv = b.f(M * nt);
+        if (gemma) {
+          a.qraw = a.qkv;
+          a.kraw = a.qkv + nq;
+          a.q = b.f(M * nq);
+          a.k = b.f(M * nk);
+          a.qs = nq;
+          a.ks = nk;
+          a.qrs = b.f(M * H);
+          a.krs = b.f(M * Hk);
+        } else {
+          a.q = a.qkv;
+          a.k = a.qkv + nq;
+          a.qs = a.ks = nt;
+        }
+        a.v = a.qkv + nq + nk;
+        a.vs = nt;
       } else {
         a.q = b.f(M * H * hd);
         a.k = b.f(M * Hk * hd);
@@ -353,7 +405,13 @@ void alloc_acts(mft_model_s* m) {
         if (L.lin[t].A >= 0) {
           a.xa[t] = b.f(M * r);
           a.U[t] = b.f(M * r);
-          if (keep_dy) a.DY[t] = b.f(M * L.lin[t].N);
+          if (m->fuse_qkv && t < 3) {  // views of the fused gradient
+            a.DY[t] = a.dyqkv + (t == 0 ? 0 : H * hd + (t - 1) * Hk * hd);
+            a.dy_ld[t] = m->nqkv;
+          } else if (keep_dy) {
+            a.DY[t] = b.f(M * L.lin[t].N);
+            a.dy_ld[t] = L.lin[t].N;
+          }
         }
       a.att = b.f(M * H * hd);
       a.lse = b.f(M * H);
@@ -454,7 +512,12 @@ void build_lora_tables(mft_model_s* m) {
   for (auto& L : m->L)
     for (int t = 0; t < nt; ++t) {
       const Linear& l = L.lin[t];
-      if (l.A >= 0) weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
+      if (l.A < 0) continue;
+      if (m->fuse_qkv && t < 3) {
+        if (t == 0) weff_floats += ((size_t)l.K * m->nqkv + 63) / 64 * 64;  // one [d, nqkv] block
+        continue;
+      }
+      weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
     }
   if (hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
     throw Error(MFT_ENOMEM, "merged LoRA weights (" + std::to_string(weff_floats * 4) + " bytes)");
@@ -467,14 +530,14 @@ void build_lora_tables(mft_model_s* m) {
     double work;
   };
   std::vector<Pending> pend;
-  auto proj_job = [&](const float* X, int K, const float* Y, bool y_rk, float* out) {
+  auto proj_job = [&](const float* X, int64_t ldx, int K, const float* Y, bool y_rk, float* out) {
     RankJob j{};
-    j.kind = 0; j.K = K; j.y_rk = y_rk ? 1 : 0; j.X = X; j.ldx = K; j.Y = Y; j.out = out; j.scale = 1.f;
+    j.kind = 0; j.K = K; j.y_rk = y_rk ? 1 : 0; j.X = X; j.ldx = ldx; j.Y = Y; j.out = out; j.scale = 1.f;
     return j;
   };
-  auto outer_job = [&](const float* P, const float* X, int C, float* out, int64_t osj, int64_t osc) {
+  auto outer_job = [&](const float* P, const float* X, int64_t ldx, int C, float* out, int64_t osj, int64_t osc) {
     RankJob j{};
-    j.kind = 1; j.K = C; j.accumulate = 1; j.blocks = rank_outer_blocks(C); j.X = X; j.ldx = C; j.Y = P;
+    j.kind = 1; j.K = C; j.accumulate = 1; j.blocks = rank_outer_blocks(C); j.X = X; j.ldx = ldx; j.Y = P;
     j.out = out; j.osj = osj; j.osc = osc; j.scale = s;
     return j;
   };
@@ -505,21 +568,34 @@ void build_lora_tables(mft_model_s* m) {
     for (int t = 0; t < nt; ++t) {
       Linear& l = L.lin[t];
       if (l.A < 0) continue;
-      l.weff = static_cast<float*>(m->weff_mem) + woff;
-      woff += ((size_t)l.K * l.N + 63) / 64 * 64;
+      if (m->fuse_qkv && t < 3) {  // column block t of the layer's [d, nqkv] W_eff
+        if (t == 0) {
+          l.weff = static_cast<float*>(m->weff_mem) + woff;
+          woff += ((size_t)l.K * m->nqkv + 63) / 64 * 64;
+        } else {
+          l.weff = L.lin[t - 1].weff + L.lin[t - 1].N;
+        }
+        l.weff_ld = m->nqkv;
+      } else {
+        l.weff = static_cast<float*>(m->weff_mem) + woff;
+        woff += ((size_t)l.K * l.N + 63) / 64 * 64;
+        l.weff_ld = l.N;
+      }
       MergeJob g{};
       g.W = m->P[l.W].data; g.A = static_cast<const float*>(m->P[l.A].data);
       g.B = static_cast<const float*>(m->P[l.B].data); g.out = l.weff; g.K = l.K; g.N = l.N;
+      g.ldo = l.weff_ld;
       g.f16 = m->P[l.W].f16 ? 1 : 0; g.tile0 = tiles;
       tiles += (int)merge_tiles(l.K, l.N);
       mj.push_back(g);
       const float* x = lora_x(m, li, t);
       const float* dy = a.DY[t];
       // xa = x·Aᵀ; U = dY·B; dB += s·dYᵀ·xa (out(j,n) = dB[n][j]); dA += s·Uᵀ·x
-      xa_jobs.push_back(proj_job(x, l.K, static_cast<const float*>(m->P[l.A].data), true, a.xa[t]));
-      u_jobs.push_back(proj_job(dy, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
-      db_jobs.push_back(outer_job(a.xa[t], dy, l.N, m->P[l.B].grad, 1, r));
-      da_jobs.push_back(outer_job(a.U[t], x, l.K, m->P[l.A].grad, l.K, 1));
+      const int64_t dld = a.dy_ld[t];
+      xa_jobs.push_back(proj_job(x, l.K, l.K, static_cast<const float*>(m->P[l.A].data), true, a.xa[t]));
+      u_jobs.push_back(proj_job(dy, dld, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
+      db_jobs.push_back(outer_job(a.xa[t], dy, dld, l.N, m->P[l.B].grad, 1, r));
+      da_jobs.push_back(outer_job(a.U[t], x, l.K, l.K, m->P[l.A].grad, l.K, 1));
     }
   }
   m->xa_batch = add_batch(xa_jobs, {});
@@ -610,7 +686,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   ep.norm = norm;
   if (lora && m->merged) {  // y = x·W_eff (+ bias, residual)
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
-    gemm(m->stream, x, l.K, l.weff, l.N, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+    gemm(m->stream, x, l.K, l.weff, l.weff_ld, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
     return;
   }
   if (lora) {
@@ -644,7 +720,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
       ep.norm = norm;
       ep.beta = beta;
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
-      gemm(m->stream, dy, l.N, l.weff, l.N, true, false, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
+      gemm(m->stream, dy, l.N, l.weff, l.weff_ld, true, false, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
     }
     return;
   }
@@ -775,16 +851,28 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       lin_fwd(m, L.lin[G_FC2], a.act, M, hout, a.xa[G_FC2], a.hmid, nullptr, &nx);   // residual + LN fused
       continue;
     }
-    if (gemma) {
-      lin_fwd(m, L.lin[T_Q], a.n1, M, a.qraw, a.xa[T_Q], nullptr);
-      lin_fwd(m, L.lin[T_K], a.n1, M, a.kraw, a.xa[T_K], nullptr);
-      rmsnorm_fwd(s, a.qraw, pd<float>(m, L.qn), M * H, hd, c.norm_eps, true, a.q, a.qrs);
-      rmsnorm_fwd(s, a.kraw, pd<float>(m, L.kn), M * Hk, hd, c.norm_eps, true, a.k, a.krs);
+    if (m->fuse_qkv) {  // q|k|v = n1·W_eff[d, nqkv] (+ the back-to-back biases) in one GEMM
+      const int nt = m->nqkv;
+      GemmEpilogue ep;
+      ep.bias = pd<float>(m, L.lin[T_Q].b);
+      Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
+      gemm(s, a.n1, d, L.lin[T_Q].weff, nt, false, false, a.qkv, nt, (int)M, nt, d, ep, m->ws, t.events());
+      if (gemma) {
+        rmsnorm_fwd_seg(s, a.qraw, nt, pd<float>(m, L.qn), M * H, hd, H, c.norm_eps, true, a.q, H * hd, a.qrs);
+        rmsnorm_fwd_seg(s, a.kraw, nt, pd<float>(m, L.kn), M * Hk, hd, Hk, c.norm_eps, true, a.k, Hk * hd, a.krs);
+      }
     } else {
-      lin_fwd(m, L.lin[T_Q], a.n1, M, a.q, a.xa[T_Q], nullptr);
-      lin_fwd(m, L.lin[T_K], a.n1, M, a.k, a.xa[T_K], nullptr);
+      if (gemma) {
+        lin_fwd(m, L.lin[T_Q], a.n1, M, a.qraw, a.xa[T_Q], nullptr);
+        lin_fwd(m, L.lin[T_K], a.n1, M, a.kraw, a.xa[T_K], nullptr);
+        rmsnorm_fwd(s, a.qraw, pd<float>(m, L.qn), M * H, hd, c.norm_eps, true, a.q, a.qrs);
+        rmsnorm_fwd(s, a.kraw, pd<float>(m, L.kn), M * Hk, hd, c.norm_eps, true, a.k, a.krs);
+      } else {
+        lin_fwd(m, L.lin[T_Q], a.n1, M, a.q, a.xa[T_Q], nullptr);
+        lin_fwd(m, L.lin[T_K], a.n1, M, a.k, a.xa[T_K], nullptr);
+      }
+      lin_fwd(m, L.lin[T_V], a.n1, M, a.v, a.xa[T_V], nullptr);
     }
-    lin_fwd(m, L.lin[T_V], a.n1, M, a.v, a.xa[T_V], nullptr);
     const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
     rope(s, a.q, a.qs, nseq, S, H, hd, th, false);
     rope(s, a.k, a.ks, nseq, S, Hk, hd, th, false);
@@ -930,6 +1018,37 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       }
       lin_bwd(m, L.lin[G_ATTN], dqkv, a.n1, a.xa[G_ATTN], M, need_dx ? m->dn : nullptr, nullptr,
               need_dx ? &nb1 : nullptr);  // LN backward fused
+      continue;
+    }
+    if (m->fuse_qkv) {
+      // dq|dk|dv land in the fused [M, nqkv] gradient (Gemma3: dq, dk first
+      // through RoPE's inverse and the q/k norms' backward), then one GEMM
+      // gives dn = dqkv·W_eff[d, nqkv]ᵀ with the input norm's backward fused.
+      const int64_t nt = m->nqkv;
+      float* dq = gemma ? m->dq : a.DY[T_Q];
+      float* dk = gemma ? m->dk : a.DY[T_K];
+      const int64_t qld = gemma ? (int64_t)H * hd : nt, kld = gemma ? (int64_t)Hk * hd : nt;
+      {
+        Timed t(m, CLS_ATTN, awork);
+        t.begin();
+        attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, dq, qld, dk, kld, a.DY[T_V], nt,
+                 m->ws);
+        t.end();
+      }
+      const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
+      rope(s, dq, qld, nseq, S, H, hd, th, true);
+      rope(s, dk, kld, nseq, S, Hk, hd, th, true);
+      if (gemma) {
+        rmsnorm_bwd_seg(s, dq, qld, a.qraw, nt, pd<float>(m, L.qn), a.qrs, M * H, hd, H, true, a.DY[T_Q], nt);
+        rmsnorm_bwd_seg(s, dk, kld, a.kraw, nt, pd<float>(m, L.kn), a.krs, M * Hk, hd, Hk, true, a.DY[T_K], nt);
+      }
+      if (need_dx) {
+        GemmEpilogue ep;
+        ep.norm = &nb1;
+        Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
+        gemm(s, a.dyqkv, nt, L.lin[T_Q].weff, nt, true, false, m->dn, d, (int)M, d, (int)nt, ep, m->ws,
+             t.events());
+      }
       continue;
     }
     // q/k dY: after RoPE's inverse (Qwen2) or after the q/k norms' backward (Gemma3)

@@ -255,35 +255,45 @@ __global__ __launch_bounds__(256) void ln_bwd_vec(const float* __restrict__ dy, 
   ln_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, g, mean[r], rstd[r], dx + r * C, resid ? resid + r * C : nullptr);
 }
 
+// Row r of a segmented operand starts at (r / seg)·ld + (r % seg)·C: seg
+// rows of C per token, tokens ld apart (seg = 1, ld = C: plain rows).  Lets a
+// per-head norm read or write head rows inside a fused q|k|v buffer.
+__device__ __forceinline__ int64_t seg_off(int64_t r, int seg, int64_t ld, int C) {
+  return (r / seg) * ld + (r % seg) * C;
+}
+
 template <int NV, int RW>
 __global__ __launch_bounds__(256) void rms_fwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                                                    int64_t M, int C, float eps, int unit_offset,
-                                                   float* __restrict__ y, float* __restrict__ rstd) {
+                                                   float* __restrict__ y, float* __restrict__ rstd, int seg,
+                                                   int64_t x_ld, int64_t y_ld) {
   __shared__ float red[2][4];
   const Place<RW> pl;
   const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
   const bool valid = row < M;
   const int64_t r = valid ? row : M - 1;
   floatx4 v[NV];
-  load_row<NV, RW>(x + r * C, C / 4, pl.gl, v);
-  rms_fwd_row<NV, RW>(v, C, pl, valid, red, w, eps, unit_offset, y + r * C, rstd ? rstd + r : nullptr);
+  load_row<NV, RW>(x + seg_off(r, seg, x_ld, C), C / 4, pl.gl, v);
+  rms_fwd_row<NV, RW>(v, C, pl, valid, red, w, eps, unit_offset, y + seg_off(r, seg, y_ld, C),
+                      rstd ? rstd + r : nullptr);
 }
 
 template <int NV, int RW>
 __global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy, const float* __restrict__ x,
                                                    const float* __restrict__ w, const float* __restrict__ rstd,
                                                    int64_t M, int C, int unit_offset, float* dx,
-                                                   const float* resid) {
+                                                   const float* resid, int seg, int64_t dy_ld, int64_t x_ld,
+                                                   int64_t dx_ld) {
   __shared__ float red[2][4];
   const Place<RW> pl;
   const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
   const bool valid = row < M;
   const int64_t r = valid ? row : M - 1;
   floatx4 gv[NV], xv[NV];
-  load_row<NV, RW>(dy + r * C, C / 4, pl.gl, gv);
-  load_row<NV, RW>(x + r * C, C / 4, pl.gl, xv);
-  rms_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, w, rstd[r], unit_offset, dx + r * C,
-                      resid ? resid + r * C : nullptr);
+  load_row<NV, RW>(dy + seg_off(r, seg, dy_ld, C), C / 4, pl.gl, gv);
+  load_row<NV, RW>(x + seg_off(r, seg, x_ld, C), C / 4, pl.gl, xv);
+  const int64_t o = seg_off(r, seg, dx_ld, C);
+  rms_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, w, rstd[r], unit_offset, dx + o, resid ? resid + o : nullptr);
 }
 
 // ---- split-K reduction + GEMM epilogue + norm ------------------------------
@@ -435,7 +445,18 @@ void rmsnorm_fwd(hipStream_t s, const float* x, const float* w, int64_t M, int64
   if (!vec_ok(C, {x, w, y})) return rmsnorm_fwd_rowloop(s, x, w, M, C, eps, unit_offset, y, rstd);
   const RowShape sh = row_shape(C);
   MFT_ROW_DISPATCH(sh, rms_fwd_vec, row_grid(M, sh), dim3(256), 0, s, x, w, M, (int)C, eps, unit_offset ? 1 : 0,
-                   y, rstd);
+                   y, rstd, 1, C, C);
+  MFT_LAUNCH_CHECK();
+}
+
+void rmsnorm_fwd_seg(hipStream_t s, const float* x, int64_t x_ld, const float* w, int64_t M, int64_t C, int seg,
+                     float eps, bool unit_offset, float* y, int64_t y_ld, float* rstd) {
+  MFT_CHECK_ARG(M > 0 && C > 0 && seg > 0 && M % seg == 0, "segmented norm: bad shape");
+  MFT_CHECK_ARG(vec_ok(C, {x, w, y}) && x_ld % 4 == 0 && y_ld % 4 == 0 && x_ld >= seg * C && y_ld >= seg * C,
+                "segmented norm: 16-byte aligned rows required");
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, rms_fwd_vec, row_grid(M, sh), dim3(256), 0, s, x, w, M, (int)C, eps, unit_offset ? 1 : 0,
+                   y, rstd, seg, x_ld, y_ld);
   MFT_LAUNCH_CHECK();
 }
 
@@ -446,7 +467,19 @@ void rmsnorm_bwd(hipStream_t s, const float* dy, const float* x, const float* w,
     return rmsnorm_bwd_rowloop(s, dy, x, w, rstd, M, C, unit_offset, dx, resid);
   const RowShape sh = row_shape(C);
   MFT_ROW_DISPATCH(sh, rms_bwd_vec, row_grid(M, sh), dim3(256), 0, s, dy, x, w, rstd, M, (int)C,
-                   unit_offset ? 1 : 0, dx, resid);
+                   unit_offset ? 1 : 0, dx, resid, 1, C, C, C);
+  MFT_LAUNCH_CHECK();
+}
+
+void rmsnorm_bwd_seg(hipStream_t s, const float* dy, int64_t dy_ld, const float* x, int64_t x_ld, const float* w,
+                     const float* rstd, int64_t M, int64_t C, int seg, bool unit_offset, float* dx, int64_t dx_ld) {
+  MFT_CHECK_ARG(M > 0 && C > 0 && seg > 0 && M % seg == 0, "segmented norm: bad shape");
+  MFT_CHECK_ARG(vec_ok(C, {dy, x, w, dx}) && dy_ld % 4 == 0 && x_ld % 4 == 0 && dx_ld % 4 == 0 &&
+                    dy_ld >= seg * C && x_ld >= seg * C && dx_ld >= seg * C,
+                "segmented norm: 16-byte aligned rows required");
+  const RowShape sh = row_shape(C);
+  MFT_ROW_DISPATCH(sh, rms_bwd_vec, row_grid(M, sh), dim3(256), 0, s, dy, x, w, rstd, M, (int)C,
+                   unit_offset ? 1 : 0, dx, nullptr, seg, dy_ld, x_ld, dx_ld);
   MFT_LAUNCH_CHECK();
 }
 

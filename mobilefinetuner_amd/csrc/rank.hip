@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
       for (int j = 0; j < R; ++j) d = fmaf(a[j], bv[e][j], d);
       w[q][e] = fmaf(scale, d, w[q][e]);
     }
-    *reinterpret_cast<floatx4*>(jb.out + (int64_t)k * jb.N + n) = w[q];
+    *reinterpret_cast<floatx4*>(jb.out + (int64_t)k * jb.ldo + n) = w[q];
   }
 }
 

@@ -38,6 +38,12 @@ SMALL = {
                       query_pre_attn_scalar=256), 2, 40, 1),
     "gemma3-fp16w": (gemma3(2, 128, 2, 1, 256, 320, vocab=611, name="gemma-t16", w_fp16=1,
                             sliding_window=512, query_pre_attn_scalar=256), 2, 32, 2),
+    # LoRA on q and v only: q, k and v stay separate GEMMs (the fused q|k|v
+    # projection needs adapters on all three); Qwen2 with biases, Gemma3 with
+    # the per-head q/k norms on unfused buffers.
+    "qwen2-qv": (qwen2(2, 256, 4, 2, 64, 384, vocab=601, name="qwen-qv", lora_mask=0b0101), 2, 48, 1),
+    "gemma3-qv": (gemma3(2, 128, 2, 1, 256, 256, vocab=509, name="gemma-qv", sliding_window=24,
+                         query_pre_attn_scalar=256, lora_mask=0b0000101), 2, 32, 1),
 }
 
 
