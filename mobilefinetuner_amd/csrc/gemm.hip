@@ -30,6 +30,8 @@
 #include <cstdlib>
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -963,15 +965,29 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// Launch of the GEMM kernel proper.  With timing events set, the dispatch
+// itself records them (hipExtLaunchKernel: the timestamps bracket the
+// kernel's execution), so timing adds no event packets to the stream and the
+// measured span matches a kernel trace's duration.
+thread_local const KernelEvents* t_gemm_events = nullptr;
+
+template <typename Kern>
+void launch_gemm_kernel(Kern kernel, dim3 grid, dim3 block, hipStream_t s, const GemmParams& p) {
+  if (t_gemm_events)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, t_gemm_events->start, t_gemm_events->stop, 0, p);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, p);
+}
+
 template <int BM, int BN, int BK, int SITE>
 void launch_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, true, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_kernel<BM, BN, BK, true, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_kernel<BM, BN, BK, true, false, SITE>, grid, block, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, false, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_kernel<BM, BN, BK, false, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_kernel<BM, BN, BK, false, false, SITE>, grid, block, s, p);
   }
 }
 
@@ -979,11 +995,11 @@ template <int BM, int BK, int SITE>
 void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BM, BK, true, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_q_kernel<BM, BK, true, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_q_kernel<BM, BK, true, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_q_kernel<BM, BK, true, false, SITE>, grid, block, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_q_kernel<BM, BK, false, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_q_kernel<BM, BK, false, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_q_kernel<BM, BK, false, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_q_kernel<BM, BK, false, false, SITE>, grid, block, s, p);
   }
 }
 
@@ -991,11 +1007,11 @@ template <int BM, int BK, int SITE>
 void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, BK, true, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_p_kernel<BM, BK, true, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, true, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, true, false, SITE>, grid, block, s, p);
   } else {
-    if (b_f16) hipLaunchKernelGGL((gemm_p_kernel<BM, BK, false, true, SITE>), grid, block, 0, s, p);
-    else       hipLaunchKernelGGL((gemm_p_kernel<BM, BK, false, false, SITE>), grid, block, 0, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, false, true, SITE>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, false, false, SITE>, grid, block, s, p);
   }
 }
 
@@ -1161,7 +1177,13 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   splits = (int)cdiv(K, p.k_chunk);
   if (splits > 1) p.partial = ws.ptr;
 
-  if (ev && ev->start) MFT_HIP(hipEventRecord(ev->start, s));
+  // Timing: events recorded by the dispatch itself, except under stream
+  // capture, where they are separate event records around the launch.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (ev) MFT_HIP(hipStreamIsCapturing(s, &cap));
+  const bool dispatch_events = ev && ev->start && ev->stop && cap == hipStreamCaptureStatusNone;
+  if (ev && ev->start && !dispatch_events) MFT_HIP(hipEventRecord(ev->start, s));
+  t_gemm_events = dispatch_events ? ev : nullptr;
   if (pl.bm == 128 && pl.bn == 0) launch_q<128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 128 && pl.bn == 1) launch_q<128, 64>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
@@ -1171,7 +1193,8 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   else if (pl.bm == 32 && pl.bn == 1) launch_q<32, 64>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 32) launch_q<32, 32>(s, p, b_nk, b_f16, splits);
   else launch_q<64, 32>(s, p, b_nk, b_f16, splits);
-  if (ev && ev->stop) MFT_HIP(hipEventRecord(ev->stop, s));
+  t_gemm_events = nullptr;
+  if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
 
   MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
   if (splits > 1 && !(nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm))) {
