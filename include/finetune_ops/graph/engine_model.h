@@ -61,13 +61,17 @@ class EngineModel {
   std::vector<std::string> parameter_names();
   TensorPtr get_parameter(const std::string& name);
   bool has_lora() const { return lora_r_ > 0 && lora_mask_ != 0; }
+  // Attaches (or re-attaches) LoRA with rank r, alpha and a target bit mask
+  // (GPT-2: bit0 c_attn, bit1 attn c_proj, bit2 mlp c_fc, bit3 mlp c_proj;
+  // Qwen2 / Gemma3: bits 0..6 q, k, v, o, gate, up, down); frozen weights
+  // carry over, and mask 0 or r 0 removes the adapters.
+  void set_lora(int rank, float alpha, int target_mask) { attach_lora(rank, alpha, target_mask); }
+  const EngineModelConfig& engine_config() const { return ecfg_; }
   int lora_rank() const { return lora_r_; }
   float lora_alpha() const { return lora_alpha_; }
   int lora_mask() const { return lora_mask_; }
 
  protected:
-  // Attaches (or re-attaches) LoRA with rank r, alpha and a target bit mask;
-  // frozen weights carry over.  mask 0 / r 0 removes the adapters.
   void attach_lora(int r, float alpha, int mask);
   virtual std::string normalise_name(const std::string& name) const { return name; }
   void ensure_engine();

@@ -41,7 +41,6 @@ class GemmaModel : public EngineModel {
  public:
   explicit GemmaModel(const GemmaTextConfig& cfg);
   const GemmaTextConfig& config() const { return cfg_; }
-  void set_lora(int rank, float alpha, int target_mask) { attach_lora(rank, alpha, target_mask); }
   void set_debug_retain_grads(bool) {}
 
  protected:

@@ -11,7 +11,9 @@
 // the "transformer." prefix (which is also accepted): wte, wpe,
 // h.{i}.ln_1.weight, h.{i}.attn.c_attn.weight / .bias / .lora_A / .lora_B,
 // h.{i}.attn.c_proj.*, h.{i}.ln_2.*, h.{i}.mlp.c_fc.*, h.{i}.mlp.c_proj.*,
-// ln_f.weight / .bias.
+// ln_f.weight / .bias.  The reference's internal names (wte.weight,
+// blocks.{i}.attn.qkv.weight, blocks.{i}.attn.proj.*, blocks.{i}.mlp.fc_in.*,
+// blocks.{i}.mlp.fc_out.*, main_full.cpp:122-151) are accepted as aliases.
 #pragma once
 #include <memory>
 #include <string>
@@ -59,9 +61,6 @@ class GPT2Model : public EngineModel {
   void init_lora_modules() {}  // adapters attach in LoraInjector::inject
   GPT2Block& get_block(int i);
   const GPT2Config& config() const { return cfg_; }
-  // LoRA attach / detach by target bits (bit0 c_attn, bit1 attn c_proj,
-  // bit2 mlp c_fc, bit3 mlp c_proj).
-  void set_lora(int rank, float alpha, int target_mask) { attach_lora(rank, alpha, target_mask); }
   void clear_lora_bits(int bits);
 
  protected:

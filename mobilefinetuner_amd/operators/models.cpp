@@ -530,6 +530,21 @@ std::string GPT2Model::normalise_name(const std::string& raw) const {
   if (n == "lm_head.weight" || ends_with(n, ".attn.bias") || ends_with(n, ".attn.masked_bias")) return "";
   if (n == "wte.weight") return "wte";
   if (n == "wpe.weight") return "wpe";
+  // The reference's internal names, blocks.{i}.attn.qkv.weight and so on
+  // (gpt2_small_lora_finetune/src/main_full.cpp:122-151).
+  if (strip(n, "blocks.")) {
+    n = "h." + n;
+    static const char* const kRef[4][2] = {
+        {".attn.qkv.", ".attn.c_attn."}, {".attn.proj.", ".attn.c_proj."},
+        {".mlp.fc_in.", ".mlp.c_fc."}, {".mlp.fc_out.", ".mlp.c_proj."}};
+    for (const auto& r : kRef) {
+      const size_t pos = n.find(r[0]);
+      if (pos != std::string::npos) {
+        n.replace(pos, std::string(r[0]).size(), r[1]);
+        break;
+      }
+    }
+  }
   return n;
 }
 

@@ -1,5 +1,7 @@
 // test_operators.cpp — parity of the finetune_ops C++ API (GPU) against the
-// CPU oracle, driven the way the reference drivers drive their operators:
+// CPU oracle, plus checkpoint round trips (frozen weights through
+// SafeTensorsReader + the key mappers, adapters through LoraSaver) into a
+// fresh model whose logits must equal the trained model's, driven the way the reference drivers drive their operators:
 //   logits = model.forward(ids, mask); loss = lm_cross_entropy(logits, labels,
 //   -100, "mean"); mul(loss, 1/accum)->backward();  then the host-side clip
 //   over p->grad()->data<float>(), optimizer.step(trainable, grads) and
@@ -9,9 +11,13 @@
 //
 // Exit status = number of failed checks.  Tolerances:
 // loss and gradients ≤ 1e-4 relative L2, parameters after Adam ≤ 1e-5.
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
+#include <functional>
 #include <memory>
 #include <random>
 #include <string>
@@ -24,7 +30,9 @@
 #include "finetune_ops/graph/gemma_model.h"
 #include "finetune_ops/graph/gpt2_model.h"
 #include "finetune_ops/graph/lora_injector.h"
+#include "finetune_ops/graph/lora_saver.h"
 #include "finetune_ops/graph/qwen_model.h"
+#include "finetune_ops/graph/safetensors_loader.h"
 #include "finetune_ops/optim/adam.h"
 #include "oracle.h"
 
@@ -219,6 +227,73 @@ static void driver_loop(const std::string& tag, EngineModel& model, orc_model* o
   }
 }
 
+
+static std::vector<float> host_copy(const TensorPtr& t) {
+  const float* p = static_cast<const Tensor&>(*t).data<float>();
+  return std::vector<float>(p, p + t->numel());
+}
+
+// Writes `trained`'s frozen weights as an HF checkpoint (nn.Linear weights
+// back in [out, in] when `hf_linear`), saves its adapters with `save`, then
+// loads both into `fresh` the way the drivers do (main.cpp:207-219,
+// 244-262) and compares logits and adapters.
+static void checkpoint_roundtrip(const std::string& tag, EngineModel& trained, EngineModel& fresh, bool hf_linear,
+                                 const std::unordered_map<std::string, std::string>& mapping,
+                                 const std::function<void(const std::string&)>& save, int B, int S) {
+  const std::string dir = "/tmp/mft_ckpt_" + tag + "_" + std::to_string(getpid());
+  std::vector<std::vector<float>> keep;
+  keep.reserve(mapping.size());
+  std::vector<SafeTensorsEntry> entries;
+  for (const auto& kv : mapping) {
+    TensorPtr t = trained.get_parameter(kv.first);
+    std::vector<float> v = host_copy(t);
+    std::vector<int64_t> shape = t->shape();
+    if (hf_linear && shape.size() == 2 && kv.first.find("embed") == std::string::npos) {
+      std::vector<float> tr(v.size());
+      for (int64_t r = 0; r < shape[0]; ++r)
+        for (int64_t c = 0; c < shape[1]; ++c) tr[c * shape[0] + r] = v[r * shape[1] + c];
+      v.swap(tr);
+      std::swap(shape[0], shape[1]);
+    }
+    keep.push_back(std::move(v));
+    entries.push_back({kv.second, "F32", shape, keep.back().data(), keep.back().size() * 4});
+  }
+  write_safetensors(dir + "/model.safetensors", entries);
+  save(dir + "/adapter_model.safetensors");
+
+  SafeTensorsReader reader(dir + "/model.safetensors");
+  reader.parse_header();
+  SafeTensorsLoadOptions opts;
+  opts.transpose_linear = hf_linear;
+  opts.verbose = false;
+  for (auto& kv : reader.load_tensors_mapped(mapping, opts)) fresh.assign_weight(kv.first, kv.second);
+  LoraState st = LoraSaver::load_safetensors(dir + "/adapter_model.safetensors");
+  check(tag + " checkpoint adapters compatible", st.compatible_with(fresh) ? 0.0 : 1.0, 0.0);
+  check(tag + " checkpoint rank/alpha", std::fabs(st.rank - trained.lora_rank()) + std::fabs(st.alpha - trained.lora_alpha()),
+        0.0);
+  check(tag + " checkpoint adapter_config.json written",
+        std::filesystem::exists(dir + "/adapter_config.json") ? 0.0 : 1.0, 0.0);
+  LoraSaver::attach_from_state(fresh, st);
+
+  double worst = 0;
+  for (const auto& name : trained.parameter_names()) {
+    const auto a = host_copy(trained.get_parameter(name)), b = host_copy(fresh.get_parameter(name));
+    worst = std::max(worst, rel_l2(b.data(), a.data(), (int64_t)a.size()));
+  }
+  check(tag + " checkpoint every parameter restored", worst, 0.0);
+
+  std::mt19937 rng(5);
+  std::vector<int32_t> ids(B * S);
+  for (auto& x : ids) x = (int32_t)(rng() % 50);
+  auto ids_t = std::make_shared<Tensor>(std::vector<int64_t>{B, S}, ids.data(), kInt32, kCPU);
+  autograd::Engine::instance().set_enabled(false);
+  const auto la = host_copy(trained.forward(ids_t, nullptr));
+  const auto lb = host_copy(fresh.forward(ids_t, nullptr));
+  autograd::Engine::instance().set_enabled(true);
+  check(tag + " checkpoint logits equal", rel_l2(lb.data(), la.data(), (int64_t)la.size()), 0.0);
+  std::filesystem::remove_all(dir);
+}
+
 static void test_gpt2() {
   GPT2Config cfg;
   cfg.vocab_size = 101;
@@ -254,6 +329,9 @@ static void test_gpt2() {
   init_both(model, om, 11);
   driver_loop("gpt2", model, om, 2, 16, 101, 2, 2, false, 0.05f, 1e-3f);
   orc_model_destroy(om);
+  GPT2Model fresh(cfg);
+  checkpoint_roundtrip("gpt2", model, fresh, false, GPT2KeyMapper::generate_gpt2_mapping(cfg.n_layer),
+                       [&](const std::string& p) { LoraSaver::save_safetensors(p, model, spec); }, 2, 16);
 }
 
 static void test_qwen() {
@@ -291,6 +369,9 @@ static void test_qwen() {
   init_both(model, om, 12);
   driver_loop("qwen2", model, om, 2, 12, 97, 2, 1, true, 1.0f, 1e-3f);
   orc_model_destroy(om);
+  QwenModel fresh(cfg);
+  checkpoint_roundtrip("qwen2", model, fresh, true, QwenKeyMapper::generate_qwen_mapping(cfg.num_hidden_layers),
+                       [&](const std::string& p) { LoraSaver::save_safetensors(p, model); }, 2, 12);
 }
 
 static void test_gemma(bool fp16) {
