@@ -159,7 +159,7 @@ struct MergeJob {
   const float* B;
   float* out;  // [K, N] rows ldo apart (ldo > N: a column block of a fused W_eff)
   int K, N, f16;
-  int tile0;  // first tile of this job (tiles of 16 rows × 256 columns)
+  int tile0;  // first tile of this job (tiles of merge_tiles' size: 32 rows × 256 columns)
   int ldo;
 };
 size_t merge_tiles(int K, int N);

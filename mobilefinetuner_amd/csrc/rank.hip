@@ -248,10 +248,12 @@ __global__ __launch_bounds__(64 * kOuterWaves) void rank_outer_mfma(OuterArgs a)
 }
 
 // ---- batched LoRA work ---------------------------------------------------------
-// W_eff[k][n] = W[k][n] + scale·Σ_j A[j][k]·B[n][j].  A workgroup owns 16
-// rows × 256 columns of one job; a thread takes 4 rows × 4 columns (the
-// A values of its rows are wave-uniform, its B rows are 4·R contiguous
-// floats).  HBM-bound: reads W once, writes W_eff once.
+// W_eff[k][n] = W[k][n] + scale·Σ_j A[j][k]·B[n][j].  A workgroup owns
+// kMergeRows·4 rows × 256 columns of one job; a thread takes kMergeRows rows ×
+// 4 columns (the A values of its rows are wave-uniform, its B rows are 4·R
+// contiguous floats, reused over all its rows).  HBM-bound: reads W once,
+// writes W_eff once.
+constexpr int kMergeRows = 8;
 template <int R>
 __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restrict__ jobs, int njobs, float scale) {
   const int t = blockIdx.x;
@@ -264,9 +266,20 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
   const MergeJob jb = jobs[lo];
   const int tiles_n = (jb.N + 255) / 256;
   const int tt = t - jb.tile0;
-  const int k0 = (tt / tiles_n) * 16 + 4 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int k0 = (tt / tiles_n) * (4 * kMergeRows) + kMergeRows * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = (tt % tiles_n) * 256 + 4 * (threadIdx.x & 63);
   if (n >= jb.N) return;
+  // All rows' W loads are issued before any is used (rows past K re-read
+  // row K-1 and are not stored), so each thread has kMergeRows loads in flight.
+  floatx4 w[kMergeRows];
+#pragma unroll
+  for (int q = 0; q < kMergeRows; ++q) {
+    const int k = min(k0 + q, jb.K - 1);
+    if (jb.f16)
+      w[q] = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
+    else
+      w[q] = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
+  }
   float bv[4][R];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -276,19 +289,8 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
 #pragma unroll
       for (int u = 0; u < 4; ++u) bv[e][4 * j4 + u] = b4[u];
     }
-  // All four rows' W loads are issued before any is used (rows past K re-read
-  // row K-1 and are not stored), so each thread has four loads in flight.
-  floatx4 w[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int k = min(k0 + q, jb.K - 1);
-    if (jb.f16)
-      w[q] = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
-    else
-      w[q] = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < kMergeRows; ++q) {
     const int k = k0 + q;
     if (k >= jb.K) break;
     float a[R];
@@ -503,7 +505,7 @@ void outer_launch(hipStream_t s, OuterArgs& a) {
 
 }  // namespace
 
-size_t merge_tiles(int K, int N) { return (size_t)cdiv(K, 16) * (size_t)cdiv(N, 256); }
+size_t merge_tiles(int K, int N) { return (size_t)cdiv(K, 4 * kMergeRows) * (size_t)cdiv(N, 256); }
 
 void lora_merge(hipStream_t s, const MergeJob* jobs, int njobs, int total_tiles, int r, float scale) {
   MFT_CHECK_ARG(jobs && njobs > 0 && total_tiles > 0, "empty merge");
