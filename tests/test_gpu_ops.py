@@ -340,6 +340,18 @@ def test_adam_sumsq_clip():
     assert np.abs(h(tg)).max() == 0
 
 
+def test_adam_weight_decay():
+    n = 4099
+    p, gr = rn(n), rn(n, std=0.1)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    tp, tg, tm, tv = g(p), g(gr), g(m), g(v)
+    for t in (1, 2, 3):
+        ops.adam_step(tp, tg, tm, tv, 1e-2, 0.9, 0.999, 1e-8, 0.05, t)
+        O.adam_step(p, gr, m, v, 1e-2, 0.9, 0.999, 1e-8, 0.05, t)
+    assert rel_err(h(tp), p) < 1e-6
+    assert rel_err(h(tv), v) < 1e-6
+
+
 # ------------------------------------------------------------------ support ops
 @pytest.mark.parametrize("C", [1024, 3072])
 def test_layernorm(C):

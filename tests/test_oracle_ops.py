@@ -218,6 +218,32 @@ def test_adam_matches_torch_adam():
     assert rel_err(p, tp.detach().numpy()) < 1e-6
 
 
+@pytest.mark.parametrize("wd", [0.01, 0.1])
+def test_adam_weight_decay_matches_torch_adamw(wd):
+    """Weight decay is decoupled: the reference's PyTorch mirrors train with
+    torch.optim.AdamW (pytorch_alignment/gpt2_lora_finetune.py:313)."""
+    n = 1000
+    p = rn(n)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    tp = torch.nn.Parameter(torch.tensor(p, dtype=torch.float32))
+    opt = torch.optim.AdamW([tp], lr=1e-2, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+    for t in range(1, 6):
+        g = rn(n)
+        O.adam_step(p, g, m, v, 1e-2, 0.9, 0.999, 1e-8, wd, t)
+        tp.grad = torch.tensor(g, dtype=torch.float32)
+        opt.step()
+    assert rel_err(p, tp.detach().numpy()) < 1e-6
+    # a coupled (L2-in-gradient) decay would differ far beyond that
+    p2 = rn(n)
+    p2c = p2.copy()
+    g = rn(n)
+    O.adam_step(p2, g, np.zeros(n, np.float32), np.zeros(n, np.float32), 1e-2, 0.9, 0.999, 1e-8, wd, 1)
+    gc = g + wd * p2c
+    coupled = p2c - 1e-2 * gc / (np.abs(gc) + 1e-8)
+    assert rel_err(p2, coupled) > 1e-4
+
+
 def test_adam_first_step_closed_form():
     p = rn(100)
     p0 = p.copy()
