@@ -120,7 +120,8 @@ def step_flops(rc: RunConfig) -> dict:
     lin = sum(4.0 * M * K * N for K, N in shapes) * m.n_layer
     lora = sum(6.0 * M * r * (shapes[i][0] + shapes[i][1]) for i in lora_t) * m.n_layer
     head = 4.0 * M * d * V
-    attn = 6.0 * rc.batch * H * rc.seq * rc.seq * hd * m.n_layer * 0.5
+    # causal: fwd 2 + bwd 4 products of 2·S²·hd each, half of them masked → 6·B·H·S²·hd per layer
+    attn = 6.0 * rc.batch * H * rc.seq * rc.seq * hd * m.n_layer
     per_micro = {"linear": lin, "lora": lora, "lm_head": head, "attention": attn}
     return {k: v * rc.accum for k, v in per_micro.items()}
 
