@@ -115,7 +115,10 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask,
                          int use_graph);
 /* Synchronises, returns the mean over micro-batches of the micro-batch mean
  * loss since the last call (the driver's accum_loss / accum), the number of
- * valid targets and the last pre-clip grad norm; resets the loss statistics. */
+ * valid targets and the last pre-clip grad norm; resets the loss statistics.
+ * Returns MFT_EINVAL (after filling the outputs) when a token id or a label
+ * (other than ignore_index) outside [0, vocab) reached a step since the last
+ * call: such ids embed as zero rows, such labels count as ignored. */
 int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid,
                          float* grad_norm);
 
@@ -123,9 +126,13 @@ int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid,
  * When enabled, HIP events are recorded on the model's stream around every
  * launch of a kernel class; mft_model_timing returns the summed duration
  * (ms), algorithmic FLOPs or bytes, and launch count since the last reset.
- * class 0 = linear GEMMs (LoRA and frozen projections, fwd + dX),
- * 1 = LM-head GEMMs, 2 = attention kernels (fwd + bwd), 3 = cross-entropy,
- * 4 = rank-r LoRA kernels. */
+ * class 0 = linear GEMMs (LoRA and frozen projections, fwd + dX; a GEMM's
+ * time includes its split-K reduction, where the plan splits K),
+ * 1 = LM-head GEMMs (likewise), 2 = attention kernels (fwd + bwd; work =
+ * 2·B·H·S²·hd forward and 4·B·H·S²·hd backward, causal), 3 = cross-entropy
+ * (work in HBM bytes: read logits, write dlogits), 4 = rank-r LoRA kernels
+ * (work in HBM bytes: the W_eff merge and the rank-r projections and outer
+ * products). */
 int mft_model_set_timing(mft_model m, int enable);
 int mft_model_timing(mft_model m, int cls, double* ms, double* work,
                      int64_t* launches);

@@ -117,7 +117,9 @@ int mft_attn_bwd(mft_handle h, const float* q, int64_t q_rs, const float* k,
  * (gpt2_small_lora_finetune/src/main.cpp:475; closed form restated at
  * gemma_3_270m_lora_finetune/src/main.cpp:100-133): row (b,s), s < S-1,
  * predicts labels[b,s+1]; NLL = logsumexp(row) − row[label]; mean over
- * targets != ignore_index.  logits [B*S, V] fp32, labels [B,S] int32.
+ * valid targets (label != ignore_index and 0 <= label < V; any other label
+ * counts as ignored in both the loss and its normaliser).  logits [B*S, V]
+ * fp32, labels [B,S] int32.
  * dlogits (nullable; may equal logits for in-place) = (softmax − onehot) ·
  * upstream / n, where n = norm_count if > 0, else the number of valid
  * targets counted on the device.  Ignored and last-position rows get 0.
@@ -192,10 +194,12 @@ int mft_glu_bwd(mft_handle h, const float* dout, const float* gate,
  * (the backward). */
 int mft_rope(mft_handle h, float* x, int64_t rs, int B, int S, int H, int hd,
              double theta, int inverse);
-/* h[m] = wte[ids[m]]·scale (+ wpe[m % S]); wte fp32 or fp16 (w_dtype). */
+/* h[m] = wte[ids[m]]·scale (+ wpe[m % S]); wte [vocab, C] fp32 or fp16
+ * (w_dtype).  An id outside [0, vocab) reads nothing: its row of h is zeros
+ * and *bad_ids (device int32, nullable) is set to 1. */
 int mft_embed(mft_handle h, const int32_t* ids, int64_t M, int S,
-              const void* wte, int w_dtype, const float* wpe, int64_t C,
-              float scale, float* out);
+              const void* wte, int64_t vocab, int w_dtype, const float* wpe,
+              int64_t C, float scale, float* out, int32_t* bad_ids);
 
 #ifdef __cplusplus
 }

@@ -71,7 +71,7 @@ _SIGS = {
     "mft_glu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mft_glu_bwd": (_I, [_P, _P, _P, _P, _L, _I, _P, _P]),
     "mft_rope": (_I, [_P, _P, _L, _I, _I, _I, _I, _D, _I]),
-    "mft_embed": (_I, [_P, _P, _L, _I, _P, _I, _P, _L, _F, _P]),
+    "mft_embed": (_I, [_P, _P, _L, _I, _P, _L, _I, _P, _L, _F, _P, _P]),
     "mft_scale": (_I, [_P, _P, _L, _F, _P]),
     "mft_axpy": (_I, [_P, _F, _P, _P, _L]),
     "mft_fill": (_I, [_P, _P, _L, _F]),

@@ -348,12 +348,13 @@ int mft_rope(mft_handle h, float* x, int64_t rs, int B, int S, int H, int hd,
   });
 }
 int mft_embed(mft_handle h, const int32_t* ids, int64_t M, int S,
-              const void* wte, int w_dtype, const float* wpe, int64_t C,
-              float scale, float* out) {
+              const void* wte, int64_t vocab, int w_dtype, const float* wpe,
+              int64_t C, float scale, float* out, int32_t* bad_ids) {
   return guarded([&] {
     require_handle(h);
     if (w_dtype != MFT_F32 && w_dtype != MFT_F16) throw mft::Error(MFT_EINVAL, "bad w_dtype");
-    mft::embed(h->stream, ids, M, S, wte, w_dtype == MFT_F16, wpe, C, scale, out);
+    if (vocab <= 0) throw mft::Error(MFT_EINVAL, "mft_embed: vocab must be positive");
+    mft::embed(h->stream, ids, M, S, wte, vocab, w_dtype == MFT_F16, wpe, C, scale, out, bad_ids);
   });
 }
 

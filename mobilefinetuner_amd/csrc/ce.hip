@@ -21,17 +21,26 @@ namespace {
 
 __global__ void zero_i64_kernel(int64_t* p) { *p = 0; }
 
+// Counts the valid shifted targets: label != ignore_index and inside
+// [0, V) — the same test ce_row_kernel applies, so an out-of-range label is
+// excluded from both the loss and its normaliser (and flagged in *bad).
 __global__ __launch_bounds__(256) void ce_count_kernel(const int32_t* __restrict__ labels,
-                                                       int B, int S, int ignore_index,
-                                                       int64_t* cnt) {
+                                                       int B, int S, int64_t V, int ignore_index,
+                                                       int64_t* cnt, int* bad) {
   __shared__ int red[4];
   int c = 0;
+  bool out_of_range = false;
   const int64_t total = (int64_t)B * S;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int s = (int)(i % S);
-    if (s + 1 < S && labels[i + 1] != ignore_index) c++;
+    if (s + 1 >= S) continue;
+    const int lab = labels[i + 1];
+    if (lab == ignore_index) continue;
+    if (lab >= 0 && (int64_t)lab < V) c++;
+    else out_of_range = true;
   }
+  if (out_of_range && bad) atomicOr(bad, 1);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
@@ -187,7 +196,7 @@ __global__ __launch_bounds__(256) void ce_sum_kernel(const float* __restrict__ r
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
-                float* dlogits, float* row_nll, int64_t* count_scratch) {
+                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label) {
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
@@ -196,7 +205,7 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(1), 0, s, count_scratch);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_count_kernel, dim3((unsigned)std::min<int64_t>(cdiv(rows, 256), 64)), dim3(256),
-                     0, s, labels, B, S, ignore_index, count_scratch);
+                     0, s, labels, B, S, V, ignore_index, count_scratch, bad_label);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_row_kernel<1024>, dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V, ld,
                      ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);

@@ -1,5 +1,6 @@
 // common.h — shared plumbing for the gfx950 kernel library.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -125,11 +126,28 @@ struct Scratch {
   }
 };
 
-// Optional events recorded immediately around the main GEMM kernel (not the
-// split-K reduction), for live per-kernel timing.
+// Optional events for live per-kernel timing of a GEMM: start/stop bracket
+// the main GEMM kernel; tail_start/tail_stop bracket the split-K reduction
+// (with its fused epilogue and row norm) when the plan splits K, and the
+// GEMM then sets tail_used.  The GEMM's time is (start→stop) plus
+// (tail_start→tail_stop) when tail_used.
 struct KernelEvents {
   hipEvent_t start = nullptr, stop = nullptr;
+  hipEvent_t tail_start = nullptr, tail_stop = nullptr;
+  mutable bool tail_used = false;
 };
+// Set by gemm() around the launch of its split-K reduction: the reduction
+// launchers (splitk_reduce in gemm.hip, splitk_norm_vec in norms.hip) pass
+// these events to the dispatch (hipExtLaunchKernel) when non-null.
+extern thread_local hipEvent_t t_tail_start, t_tail_stop;
+#define MFT_LAUNCH_TAIL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                                   \
+  do {                                                                                             \
+    if (::mft::t_tail_start)                                                                       \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ::mft::t_tail_start,               \
+                            ::mft::t_tail_stop, 0, __VA_ARGS__);                                   \
+    else                                                                                           \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                         \
+  } while (0)
 
 // C[M,N] = A[M,K] · op(B) (+ epilogue).  b_nk=false: B is [K,N] (ldb = row
 // stride); b_nk=true: B is [N,K].  b_f16: B holds IEEE fp16 values.
@@ -228,10 +246,12 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs,
 size_t attn_bwd_scratch_floats(const AttnArgs& a);
 
 // logits rows have stride ld (>= V); dlogits (may alias logits) uses the same.
+// A target is valid iff label != ignore_index and 0 <= label < V; other
+// labels count as ignored, and set *bad_label (device int, nullable) to 1.
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
-                float* dlogits, float* row_nll, int64_t* count_scratch);
+                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label = nullptr);
 
 void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n);
 void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n);
@@ -296,9 +316,10 @@ void glu_bwd(hipStream_t s, const float* dout, const float* gate,
              const float* up, int64_t n, int act, float* dgate, float* dup);
 void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
           double theta, bool inverse);
+// Ids outside [0, V) give zero rows and set *bad (device int, nullable).
 void embed(hipStream_t s, const int32_t* ids, int64_t M, int S,
-           const void* wte, bool w_f16, const float* wpe, int64_t C,
-           float scale, float* out);
+           const void* wte, int64_t V, bool w_f16, const float* wpe, int64_t C,
+           float scale, float* out, int* bad);
 void add_inplace(hipStream_t s, float* a, const float* b, int64_t n);
 void fill_normal(hipStream_t s, float* p, int64_t n, uint64_t seed, float std,
                  float mean);

@@ -174,14 +174,21 @@ __global__ void rope_kernel(float* x, int64_t rs, int B, int S, int H, int hd,
 }
 
 // ---- embedding ------------------------------------------------------------------
+// A token id outside [0, V) reads nothing: its row is written as zeros and
+// *bad (when given) is set to 1, for the host to report.
 template <bool F16>
 __global__ void embed_kernel(const int32_t* __restrict__ ids, int64_t M, int S,
-                             const void* __restrict__ wte, const float* __restrict__ wpe,
-                             int C, float scale, float* __restrict__ out) {
+                             const void* __restrict__ wte, int64_t V, const float* __restrict__ wpe,
+                             int C, float scale, float* __restrict__ out, int* bad) {
   const int64_t row = blockIdx.x;
   if (row >= M) return;
   const int64_t id = ids[row];
   const int s = (int)(row % S);
+  if (id < 0 || id >= V) {
+    for (int j = threadIdx.x; j < C; j += blockDim.x) out[row * C + j] = 0.f;
+    if (bad && threadIdx.x == 0) atomicOr(bad, 1);
+    return;
+  }
   for (int j = threadIdx.x; j < C; j += blockDim.x) {
     float e;
     if constexpr (F16)
@@ -474,13 +481,15 @@ void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
   MFT_LAUNCH_CHECK();
 }
 void embed(hipStream_t s, const int32_t* ids, int64_t M, int S,
-           const void* wte, bool w_f16, const float* wpe, int64_t C,
-           float scale, float* out) {
-  MFT_CHECK_ARG(M > 0 && C > 0 && S > 0, "empty");
+           const void* wte, int64_t V, bool w_f16, const float* wpe, int64_t C,
+           float scale, float* out, int* bad) {
+  MFT_CHECK_ARG(M > 0 && C > 0 && S > 0 && V > 0, "empty");
   if (w_f16)
-    hipLaunchKernelGGL(embed_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, wpe, (int)C, scale, out);
+    hipLaunchKernelGGL(embed_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, V, wpe, (int)C, scale,
+                       out, bad);
   else
-    hipLaunchKernelGGL(embed_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, wpe, (int)C, scale, out);
+    hipLaunchKernelGGL(embed_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, ids, M, S, wte, V, wpe, (int)C, scale,
+                       out, bad);
   MFT_LAUNCH_CHECK();
 }
 void add_inplace(hipStream_t s, float* a, const float* b, int64_t n) {

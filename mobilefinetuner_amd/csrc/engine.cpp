@@ -86,6 +86,7 @@ struct TimedLaunch {
   int cls;
   double work;
   hipEvent_t a, b;
+  hipEvent_t c = nullptr, d = nullptr;  // a second interval (a GEMM's split-K reduction), or null
 };
 
 }  // namespace
@@ -133,7 +134,7 @@ struct mft_model_s {
   struct Batch {
     const RankJob* jobs;
     int njobs, nproj, outer_blocks;
-    double work_per_row;  // flops per token (timing)
+    double work_per_row;  // HBM bytes per token row (timing)
   };
   std::vector<Batch> batches;
   int xa_batch = -1, udb_batch = -1, da_batch = -1;
@@ -145,6 +146,10 @@ struct mft_model_s {
   float* d_clip = nullptr;  // [0] scale, [1] norm
   float* d_hp = nullptr;    // {lr, b1, b2, eps, wd, max_norm}
   int* d_t = nullptr;       // Adam step count (advanced on the device)
+  // input error bits set by kernels: 1 = a token id outside [0, vocab)
+  // (its embedding row is zeros), 2 = a label outside [0, vocab) that is not
+  // ignore_index (counted as ignored); reported by mft_model_read_stats
+  int* d_err = nullptr;
   int n_micro_pending = 0;
   int adam_t = 0;
   // Qwen2 / Gemma3 with LoRA on q, k and v (merged path): one GEMM for
@@ -479,6 +484,7 @@ void alloc_acts(mft_model_s* m) {
   m->d_clip = reinterpret_cast<float*>(static_cast<char*>(sc) + 1536);
   m->d_hp = reinterpret_cast<float*>(static_cast<char*>(sc) + 1792);
   m->d_t = reinterpret_cast<int*>(static_cast<char*>(sc) + 2048);
+  m->d_err = reinterpret_cast<int*>(static_cast<char*>(sc) + 2304);
   MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
@@ -546,14 +552,16 @@ void build_lora_tables(mft_model_s* m) {
   auto add_batch = [&](std::vector<RankJob> proj, std::vector<RankJob> outer) {
     if (proj.empty() && outer.empty()) return -1;
     Pending p{rj.size(), (int)(proj.size() + outer.size()), (int)proj.size(), 0, 0.0};
+    // timing work in HBM bytes per token row: a projection reads a K-wide
+    // row and writes r values; an outer product reads a C-wide row and r values
     for (auto& j : proj) {
-      p.work += 2.0 * j.K * r;
+      p.work += 4.0 * (j.K + r);
       rj.push_back(j);
     }
     for (auto& j : outer) {
       j.block0 = p.outer_blocks;
       p.outer_blocks += j.blocks;
-      p.work += 2.0 * j.K * r;
+      p.work += 4.0 * (j.K + r);
       rj.push_back(j);
     }
     pend.push_back(p);
@@ -641,7 +649,13 @@ struct Timed {
       ev.stop = next_event(m);
     }
   }
-  const KernelEvents* events() const { return m->timing ? &ev : nullptr; }
+  // Events for a GEMM launch: the main kernel and its split-K reduction.
+  const KernelEvents* events() {
+    if (!m->timing) return nullptr;
+    ev.tail_start = next_event(m);
+    ev.tail_stop = next_event(m);
+    return &ev;
+  }
   void begin() {
     if (m->timing) MFT_HIP(hipEventRecord(ev.start, m->stream));
   }
@@ -650,8 +664,13 @@ struct Timed {
   }
   ~Timed() {
     if (!m->timing) return;
-    if (m->capturing) m->graph_timed.push_back({cls, work, ev.start, ev.stop});
-    else m->launches.push_back({cls, work, ev.start, ev.stop});
+    TimedLaunch t{cls, work, ev.start, ev.stop};
+    if (ev.tail_used) {
+      t.c = ev.tail_start;
+      t.d = ev.tail_stop;
+    }
+    if (m->capturing) m->graph_timed.push_back(t);
+    else m->launches.push_back(t);
   }
 };
 
@@ -659,9 +678,10 @@ void collect_timing(mft_model_s* m) {
   if (m->launches.empty()) return;
   MFT_HIP(hipStreamSynchronize(m->stream));
   for (auto& t : m->launches) {
-    float ms = 0.f;
+    float ms = 0.f, ms2 = 0.f;
     MFT_HIP(hipEventElapsedTime(&ms, t.a, t.b));
-    m->t_ms[t.cls] += ms;
+    if (t.c) MFT_HIP(hipEventElapsedTime(&ms2, t.c, t.d));
+    m->t_ms[t.cls] += ms + ms2;
     m->t_work[t.cls] += t.work;
     m->t_n[t.cls] += 1;
   }
@@ -690,7 +710,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     return;
   }
   if (lora) {
-    Timed tr(m, CLS_RANK, 4.0 * M * l.K * r);
+    Timed tr(m, CLS_RANK, 4.0 * M * (l.K + r));  // bytes: read x, write xa
     tr.begin();
     rank_proj(m->stream, x, l.K, static_cast<const float*>(m->P[l.A].data), 1, l.K, (int)M, l.K, r, xa);
     tr.end();
@@ -728,7 +748,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
   float* U = m->ws.ptr;
   Scratch rest = m->ws.offset((size_t)(M * (r > 0 ? r : 1)));
   if (lora) {
-    Timed tr(m, CLS_RANK, 2.0 * M * l.N * r);
+    Timed tr(m, CLS_RANK, 4.0 * M * (l.N + r));  // bytes: read dy, write U
     tr.begin();
     rank_proj(m->stream, dy, l.N, static_cast<const float*>(m->P[l.B].data), r, 1, (int)M, l.N, r, U);
     tr.end();
@@ -750,7 +770,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
     gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
   }
   if (lora) {
-    Timed tr(m, CLS_RANK, 2.0 * M * r * (l.K + l.N));
+    Timed tr(m, CLS_RANK, 4.0 * M * (l.K + l.N + 2 * r));  // bytes: read x, dy, U, xa
     tr.begin();
     // dA += s·Uᵀ·x and dB += s·dyᵀ·xa in one launch
     rank_outer_pair(m->stream, (int)M, r, lscale(m), true, U, x, l.K, l.K, m->P[l.A].grad, l.K, 1, xa, dy,
@@ -772,10 +792,10 @@ void run_batch(mft_model_s* m, int idx, int64_t M) {
 // W_eff = W + s·Aᵀ·Bᵀ for every LoRA linear (one launch).
 void merge_lora(mft_model_s* m) {
   if (!m->merged) return;
-  double work = 0.0;
+  double work = 0.0;  // HBM bytes: read W (fp32 or fp16), write W_eff
   for (auto& L : m->L)
     for (auto& l : L.lin)
-      if (l.weff) work += 2.0 * l.K * l.N * m->c.lora_r;
+      if (l.weff) work += (double)l.K * l.N * ((m->P[l.W].f16 ? 2 : 4) + 4);
   Timed t(m, CLS_RANK, work);
   t.begin();
   lora_merge(m->stream, m->d_merge, m->n_merge, m->merge_tiles_total, m->c.lora_r, lscale(m));
@@ -806,8 +826,8 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
   merge_lora(m);  // A, B (or W) may have changed since the last forward
-  embed(s, ids, M, S, E.data, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
-        gemma ? std::sqrt((float)d) : 1.f, m->A[0].x);
+  embed(s, ids, M, S, E.data, c.vocab, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
+        gemma ? std::sqrt((float)d) : 1.f, m->A[0].x, m->d_err);
   // Input norm of layer li (li == n_layer: the final norm).  GPT-2 and Qwen2
   // run it inside the GEMM that produced its input (the previous layer's
   // residual-fused down projection); Gemma3's post-norms sit in between.
@@ -916,7 +936,7 @@ void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs,
     t.begin();
     ce_fwd_bwd(m->stream, lg, labels + row0, seqs, S, c.vocab, m->ldv, -100, upstream, 0,
                m->d_loss + m->n_micro_pending, m->d_cnt + m->n_micro_pending, backward ? lg : nullptr,
-               m->row_nll + row0, m->d_tmpcnt);
+               m->row_nll + row0, m->d_tmpcnt, m->d_err + 1);
     t.end();
     m->n_micro_pending++;
   }
@@ -1006,7 +1026,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};
-    const double awork = 2.0 * 5.0 * nseq * H * (double)S * S * hd * 0.5;
+    // algorithmic: dV, dP, dQ, dK (the recomputed scores are not counted), causal half
+    const double awork = 2.0 * 4.0 * nseq * H * (double)S * S * hd * 0.5;
     if (gpt2) {
       float* dqkv = dyb(li, G_ATTN, m->dqkv);
       {
@@ -1336,7 +1357,7 @@ int mft_model_ce(mft_model m, const int32_t* labels, int nseq, int S, int ignore
       throw Error(MFT_EINVAL, "mft_model_ce: no forward of this shape is pending");
     if (m->api_dlogits) throw Error(MFT_EINVAL, "mft_model_ce: the logits were already turned into dlogits");
     ce_fwd_bwd(m->stream, m->logits, labels, nseq, S, m->c.vocab, m->ldv, ignore_index, upstream, norm_count,
-               loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt);
+               loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt, m->d_err + 1);
     if (backward) m->api_dlogits = true;
   });
 }
@@ -1398,9 +1419,10 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, con
       // The graph re-records the same events on every replay: read them now.
       MFT_HIP(hipStreamSynchronize(m->cap_stream));
       for (auto& t : m->graph_timed) {
-        float ms = 0.f;
+        float ms = 0.f, ms2 = 0.f;
         MFT_HIP(hipEventElapsedTime(&ms, t.a, t.b));
-        m->t_ms[t.cls] += ms;
+        if (t.c) MFT_HIP(hipEventElapsedTime(&ms2, t.c, t.d));
+        m->t_ms[t.cls] += ms + ms2;
         m->t_work[t.cls] += t.work;
         m->t_n[t.cls] += 1;
       }
@@ -1421,6 +1443,8 @@ int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid, float*
       MFT_HIP(hipMemcpy(cn, m->d_cnt, sizeof(int64_t) * n, hipMemcpyDeviceToHost));
     }
     MFT_HIP(hipMemcpy(cl, m->d_clip, sizeof(cl), hipMemcpyDeviceToHost));
+    int err[2] = {0, 0};
+    MFT_HIP(hipMemcpy(err, m->d_err, sizeof(err), hipMemcpyDeviceToHost));
     double acc = 0.0;
     int64_t tot = 0;
     for (int i = 0; i < n; ++i) {
@@ -1432,6 +1456,14 @@ int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid, float*
     if (grad_norm) *grad_norm = cl[1];
     MFT_HIP(hipMemset(m->d_loss, 0, 1024));
     m->n_micro_pending = 0;
+    if (err[0] || err[1]) {
+      MFT_HIP(hipMemset(m->d_err, 0, sizeof(err)));
+      throw Error(MFT_EINVAL, std::string("mft_model_read_stats: since the last call ") +
+                                  (err[0] ? "a token id was outside [0, vocab) (its embedding row was zeroed)" : "") +
+                                  (err[0] && err[1] ? "; " : "") +
+                                  (err[1] ? "a label outside [0, vocab) other than ignore_index was treated as ignored"
+                                          : ""));
+    }
   });
 }
 

@@ -970,6 +970,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // kernel's execution), so timing adds no event packets to the stream and the
 // measured span matches a kernel trace's duration.
 thread_local const KernelEvents* t_gemm_events = nullptr;
+}  // namespace
+thread_local hipEvent_t t_tail_start = nullptr, t_tail_stop = nullptr;
+namespace {
 
 template <typename Kern>
 void launch_gemm_kernel(Kern kernel, dim3 grid, dim3 block, hipStream_t s, const GemmParams& p) {
@@ -1197,12 +1200,32 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
 
   MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
-  if (splits > 1 && !(nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm))) {
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256), 0, s,
-                       (const float*)ws.ptr, splits, M, N, C, ldc, ep);
+  if (splits > 1) {
+    // The split-K reduction (with the epilogue and, when fused, the row
+    // norm) belongs to the GEMM's time: bracket it with the tail events.
+    const bool tail = ev && ev->tail_start && ev->tail_stop;
+    if (tail) {
+      ev->tail_used = true;
+      if (dispatch_events) {
+        t_tail_start = ev->tail_start;
+        t_tail_stop = ev->tail_stop;
+      } else {
+        MFT_HIP(hipEventRecord(ev->tail_start, s));
+      }
+    }
+    struct TailReset {
+      ~TailReset() { t_tail_start = t_tail_stop = nullptr; }
+    } tail_reset;
+    const bool fused = nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm);
+    if (!fused) {
+      MFT_LAUNCH_TAIL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256),
+                      0, s, (const float*)ws.ptr, splits, M, N, C, ldc, ep);
+    }
+    t_tail_start = t_tail_stop = nullptr;
+    if (tail && !dispatch_events) MFT_HIP(hipEventRecord(ev->tail_stop, s));
     MFT_LAUNCH_CHECK();
-    if (nm) row_norm(s, C, M, N, *nm);
-  } else if (splits == 1 && nm) {
+    if (!fused && nm) row_norm(s, C, M, N, *nm);
+  } else if (nm) {
     row_norm(s, C, M, N, *nm);
   }
 }

@@ -408,12 +408,12 @@ void splitk_norm_launch(hipStream_t s, const RowShape& sh, const float* partial,
                         const GemmEpilogue& ep, const RowNorm& nm) {
   const dim3 grid = row_grid(M, sh), block(256);
   const int64_t m = M;
-  if (sh.rw == 1) hipLaunchKernelGGL((splitk_norm_vec<1, 1, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
-  else if (sh.rw == 2) hipLaunchKernelGGL((splitk_norm_vec<1, 2, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
-  else if (sh.nv == 1) hipLaunchKernelGGL((splitk_norm_vec<1, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
-  else if (sh.nv == 2) hipLaunchKernelGGL((splitk_norm_vec<2, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
-  else if (sh.nv == 3) hipLaunchKernelGGL((splitk_norm_vec<3, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
-  else hipLaunchKernelGGL((splitk_norm_vec<4, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  if (sh.rw == 1) MFT_LAUNCH_TAIL((splitk_norm_vec<1, 1, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.rw == 2) MFT_LAUNCH_TAIL((splitk_norm_vec<1, 2, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 1) MFT_LAUNCH_TAIL((splitk_norm_vec<1, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 2) MFT_LAUNCH_TAIL((splitk_norm_vec<2, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else if (sh.nv == 3) MFT_LAUNCH_TAIL((splitk_norm_vec<3, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
+  else MFT_LAUNCH_TAIL((splitk_norm_vec<4, 4, KIND>), grid, block, 0, s, partial, splits, m, N, C, ep, nm);
   MFT_LAUNCH_CHECK();
 }
 

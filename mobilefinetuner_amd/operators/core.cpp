@@ -547,6 +547,23 @@ TensorPtr make_loss(double loss_sum, int64_t n_valid, bool sum) {
   return std::make_shared<Tensor>(std::vector<int64_t>{1}, &v, kFloat32, kCPU);
 }
 
+void check_ids(const TensorPtr& ids, int64_t vocab, const char* what) {
+  const int32_t* p = static_cast<const Tensor&>(*ids).data<int32_t>();
+  for (int64_t i = 0; i < ids->numel(); ++i)
+    if (p[i] < 0 || (int64_t)p[i] >= vocab)
+      throw std::invalid_argument(std::string(what) + ": token id " + std::to_string(p[i]) + " at position " +
+                                  std::to_string(i) + " is outside [0, " + std::to_string(vocab) + ")");
+}
+
+void check_labels(const TensorPtr& labels, int64_t vocab, int ignore_index, const char* what) {
+  const int32_t* p = static_cast<const Tensor&>(*labels).data<int32_t>();
+  for (int64_t i = 0; i < labels->numel(); ++i)
+    if (p[i] != ignore_index && (p[i] < 0 || (int64_t)p[i] >= vocab))
+      throw std::invalid_argument(std::string(what) + ": label " + std::to_string(p[i]) + " at position " +
+                                  std::to_string(i) + " is outside [0, " + std::to_string(vocab) +
+                                  ") and is not ignore_index");
+}
+
 bool parse_reduction(const std::string& r) {
   if (r == "mean") return false;
   if (r == "sum") return true;
@@ -562,6 +579,7 @@ TensorPtr lm_cross_entropy(const TensorPtr& logits, const TensorPtr& labels, int
     throw std::invalid_argument("lm_cross_entropy: logits must be float32 [B, S, V]");
   if (!labels || labels->dtype() != kInt32 || labels->numel() != logits->shape()[0] * logits->shape()[1])
     throw std::invalid_argument("lm_cross_entropy: labels must be int32 [B, S]");
+  detail::check_labels(labels, logits->shape()[2], ignore_index, "lm_cross_entropy");
   // Logits produced by an engine-backed model go through the model's own
   // loss (its logits buffer turns into dlogits in place).
   if (auto hook = detail::model_loss_hook(logits)) return hook(labels, ignore_index, sum);
@@ -595,7 +613,11 @@ float perplexity_from_loss(float loss) { return std::exp(loss); }
 
 // ------------------------------------------------------------------ Adam --
 
+// Moment state of one parameter.  Keyed by the parameter's address, so the
+// entry also remembers which tensor it belongs to: a parameter created after
+// another was freed can reuse its address, and then gets fresh state.
 struct Adam::State {
+  std::weak_ptr<Tensor> owner;
   TensorPtr m, v;
 };
 
@@ -613,8 +635,9 @@ void Adam::step(const std::vector<TensorPtr>& params, const std::vector<TensorPt
     require_f32(g, "Adam gradient");
     if (g->numel() != p->numel()) throw std::invalid_argument("Adam::step: gradient size differs from its parameter");
     auto& st = state_[p.get()];
-    if (!st) {
+    if (!st || st->owner.lock() != p || st->m->numel() != p->numel()) {
       st = std::make_unique<State>();
+      st->owner = p;
       st->m = new_f32(p->shape());
       st->v = new_f32(p->shape());
     }

@@ -24,5 +24,12 @@ bool parse_reduction(const std::string& r);
 using ModelLoss = std::function<TensorPtr(const TensorPtr& labels, int ignore_index, bool sum)>;
 ModelLoss model_loss_hook(const TensorPtr& logits);
 
+// Host-side range checks of int32 index tensors (read through the host
+// mirror; ids and labels come from the host): every token id in [0, vocab),
+// every label in [0, vocab) or equal to ignore_index.  Throws
+// std::invalid_argument naming the first offender.
+void check_ids(const TensorPtr& ids, int64_t vocab, const char* what);
+void check_labels(const TensorPtr& labels, int64_t vocab, int ignore_index, const char* what);
+
 }  // namespace detail
 }  // namespace ops

@@ -314,6 +314,7 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
   const int B = (int)ids->shape()[0], S = (int)ids->shape()[1];
   if (mask && (mask->dtype() != kFloat32 || mask->numel() != (int64_t)B * S))
     throw std::invalid_argument("forward: attention_mask must be float32 [B, S]");
+  detail::check_ids(ids, ecfg_.vocab, "forward");
   // Parameters edited through host views are copied back before the forward.
   for (auto& v : views_)
     if (v) (void)v->device_data();

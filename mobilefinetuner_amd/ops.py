@@ -233,13 +233,15 @@ def rope_(x, B, S, H, hd, theta, inverse=False, rs=None):
     return x
 
 
-def embed(ids, S, wte, wpe, scale, out=None):
+def embed(ids, S, wte, wpe, scale, out=None, bad=None):
+    """h = wte[ids]·scale (+ wpe[pos]).  An id outside [0, vocab) gives a zero
+    row and sets bad[0] = 1 (bad: optional int32 device tensor)."""
     M = ids.numel()
-    Cc = wte.shape[1]
+    V, Cc = wte.shape
     if out is None:
         out = torch.empty(M, Cc, device=ids.device, dtype=torch.float32)
-    call("mft_embed", handle(), _p(ids, torch.int32), M, S, _p(wte, _W), _wdtype(wte),
-         _p(wpe), Cc, scale, _p(out))
+    call("mft_embed", handle(), _p(ids, torch.int32), M, S, _p(wte, _W), V, _wdtype(wte),
+         _p(wpe), Cc, scale, _p(out), _p(bad, torch.int32))
     return out
 
 

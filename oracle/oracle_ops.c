@@ -267,53 +267,65 @@ static int visible(int causal, int window, const float* kpad, int b, int S,
   return 1;
 }
 
+/* Scores of query row i of head h against every key, scaled, with invisible
+ * keys at -inf; returns the row max. */
+static double attn_scores(const float* qi, const float* k, int64_t k_rs, int b, int kh, int S,
+                          int hd, float scale, int causal, int window, const float* kpad,
+                          int i, double* sc) {
+  double mx = -INFINITY;
+  for (int j = 0; j < S; ++j) {
+    if (!visible(causal, window, kpad, b, S, i, j)) { sc[j] = -INFINITY; continue; }
+    const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
+    double s = 0.0;
+    for (int d = 0; d < hd; ++d) s += (double)qi[d] * kj[d];
+    sc[j] = s * scale;
+    if (sc[j] > mx) mx = sc[j];
+  }
+  return mx;
+}
+
 void orc_attn_fwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
                   const float* v, int64_t v_rs, int B, int Hq, int Hkv, int S,
                   int hd, float scale, int causal, int window,
                   const float* kpad, float* o, int64_t o_rs, float* lse) {
   const int grp = Hq / Hkv;
-#pragma omp parallel for collapse(2) schedule(dynamic)
-  for (int b = 0; b < B; ++b)
-    for (int h = 0; h < Hq; ++h) {
-      const int kh = h / grp;
-      double* sc = (double*)malloc(sizeof(double) * (size_t)S);
-      double* acc = (double*)malloc(sizeof(double) * (size_t)hd);
-      for (int i = 0; i < S; ++i) {
-        const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
-        double mx = -INFINITY;
-        for (int j = 0; j < S; ++j) {
-          if (!visible(causal, window, kpad, b, S, i, j)) { sc[j] = -INFINITY; continue; }
-          const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
-          double s = 0.0;
-          for (int d = 0; d < hd; ++d) s += (double)qi[d] * kj[d];
-          sc[j] = s * scale;
-          if (sc[j] > mx) mx = sc[j];
+  /* every query row is independent: parallel over (b, h, i) */
+#pragma omp parallel
+  {
+    double* sc = (double*)malloc(sizeof(double) * (size_t)S);
+    double* acc = (double*)malloc(sizeof(double) * (size_t)hd);
+#pragma omp for collapse(3) schedule(dynamic, 16)
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < Hq; ++h)
+        for (int i = 0; i < S; ++i) {
+          const int kh = h / grp;
+          const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
+          const double mx = attn_scores(qi, k, k_rs, b, kh, S, hd, scale, causal, window, kpad, i, sc);
+          float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
+          const int64_t li = ((int64_t)b * Hq + h) * S + i;
+          if (mx == -INFINITY) {
+            for (int d = 0; d < hd; ++d) oi[d] = 0.0f;
+            if (lse) lse[li] = -INFINITY;
+            continue;
+          }
+          double sum = 0.0;
+          for (int j = 0; j < S; ++j) {
+            sc[j] = sc[j] == -INFINITY ? 0.0 : exp(sc[j] - mx);
+            sum += sc[j];
+          }
+          for (int d = 0; d < hd; ++d) acc[d] = 0.0;
+          for (int j = 0; j < S; ++j) {
+            if (sc[j] == 0.0) continue;
+            const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
+            const double p = sc[j] / sum;
+            for (int d = 0; d < hd; ++d) acc[d] += p * vj[d];
+          }
+          for (int d = 0; d < hd; ++d) oi[d] = (float)acc[d];
+          if (lse) lse[li] = (float)(mx + log(sum));
         }
-        float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
-        int64_t li = ((int64_t)b * Hq + h) * S + i;
-        if (mx == -INFINITY) {
-          for (int d = 0; d < hd; ++d) oi[d] = 0.0f;
-          if (lse) lse[li] = -INFINITY;
-          continue;
-        }
-        double sum = 0.0;
-        for (int j = 0; j < S; ++j) {
-          sc[j] = sc[j] == -INFINITY ? 0.0 : exp(sc[j] - mx);
-          sum += sc[j];
-        }
-        for (int d = 0; d < hd; ++d) acc[d] = 0.0;
-        for (int j = 0; j < S; ++j) {
-          if (sc[j] == 0.0) continue;
-          const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
-          double p = sc[j] / sum;
-          for (int d = 0; d < hd; ++d) acc[d] += p * vj[d];
-        }
-        for (int d = 0; d < hd; ++d) oi[d] = (float)acc[d];
-        if (lse) lse[li] = (float)(mx + log(sum));
-      }
-      free(sc);
-      free(acc);
-    }
+    free(sc);
+    free(acc);
+  }
 }
 
 void orc_attn_bwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
@@ -324,73 +336,94 @@ void orc_attn_bwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
                   int64_t dk_rs, float* dv, int64_t dv_rs) {
   (void)lse;
   const int grp = Hq / Hkv;
-  /* dk/dv accumulate over the group: do it per (b, kv-head) to stay race-free */
-#pragma omp parallel for collapse(2) schedule(dynamic)
-  for (int b = 0; b < B; ++b)
-    for (int kh = 0; kh < Hkv; ++kh) {
-      double* dK = (double*)calloc((size_t)S * hd, sizeof(double));
-      double* dV = (double*)calloc((size_t)S * hd, sizeof(double));
-      double* P = (double*)malloc(sizeof(double) * (size_t)S);
-      double* dP = (double*)malloc(sizeof(double) * (size_t)S);
-      for (int h = kh * grp; h < (kh + 1) * grp; ++h) {
-        for (int i = 0; i < S; ++i) {
-          const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
-          const float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
-          const float* gi = dout + ((int64_t)b * S + i) * do_rs + (int64_t)h * hd;
-          float* dqi = dq + ((int64_t)b * S + i) * dq_rs + (int64_t)h * hd;
-          double mx = -INFINITY;
-          for (int j = 0; j < S; ++j) {
-            if (!visible(causal, window, kpad, b, S, i, j)) { P[j] = -INFINITY; continue; }
-            const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
-            double s = 0.0;
-            for (int d = 0; d < hd; ++d) s += (double)qi[d] * kj[d];
-            P[j] = s * scale;
-            if (P[j] > mx) mx = P[j];
-          }
-          if (mx == -INFINITY) {
-            for (int d = 0; d < hd; ++d) dqi[d] = 0.0f;
-            continue;
-          }
-          double sum = 0.0;
-          for (int j = 0; j < S; ++j) {
-            P[j] = P[j] == -INFINITY ? 0.0 : exp(P[j] - mx);
-            sum += P[j];
-          }
-          double Di = 0.0; /* rowsum(dO∘O) */
-          for (int d = 0; d < hd; ++d) Di += (double)gi[d] * oi[d];
-          for (int j = 0; j < S; ++j) {
-            P[j] /= sum;
-            if (P[j] == 0.0) { dP[j] = 0.0; continue; }
-            const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
-            double s = 0.0;
-            for (int d = 0; d < hd; ++d) s += (double)gi[d] * vj[d];
-            dP[j] = s;
-          }
-          double* dqa = (double*)calloc((size_t)hd, sizeof(double));
-          for (int j = 0; j < S; ++j) {
-            if (P[j] == 0.0) continue;
-            double ds = P[j] * (dP[j] - Di) * scale;
-            const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
-            for (int d = 0; d < hd; ++d) {
-              dqa[d] += ds * kj[d];
-              dK[(int64_t)j * hd + d] += ds * qi[d];
-              dV[(int64_t)j * hd + d] += P[j] * gi[d];
-            }
-          }
-          for (int d = 0; d < hd; ++d) dqi[d] = (float)dqa[d];
-          free(dqa);
+  /* Work units (b, h, chunk of query rows): dQ rows are written directly;
+   * each unit keeps its own fp64 dK/dV partial [S, hd], summed afterwards
+   * over the chunks and the heads of each GQA group in a fixed order (the
+   * result does not depend on the thread count). */
+  const int QC = 64;
+  const int nch = (S + QC - 1) / QC;
+  const int64_t units = (int64_t)B * Hq * nch;
+  const size_t part = (size_t)S * hd;
+  double* dKp = (double*)calloc((size_t)units * part, sizeof(double));
+  double* dVp = (double*)calloc((size_t)units * part, sizeof(double));
+#pragma omp parallel
+  {
+    double* P = (double*)malloc(sizeof(double) * (size_t)S);
+    double* dP = (double*)malloc(sizeof(double) * (size_t)S);
+    double* dqa = (double*)malloc(sizeof(double) * (size_t)hd);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t u = 0; u < units; ++u) {
+      const int b = (int)(u / ((int64_t)Hq * nch));
+      const int h = (int)((u / nch) % Hq);
+      const int c = (int)(u % nch);
+      const int kh = h / grp;
+      double* dK = dKp + (size_t)u * part;
+      double* dV = dVp + (size_t)u * part;
+      const int i1 = (c + 1) * QC < S ? (c + 1) * QC : S;
+      for (int i = c * QC; i < i1; ++i) {
+        const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
+        const float* oi = o + ((int64_t)b * S + i) * o_rs + (int64_t)h * hd;
+        const float* gi = dout + ((int64_t)b * S + i) * do_rs + (int64_t)h * hd;
+        float* dqi = dq + ((int64_t)b * S + i) * dq_rs + (int64_t)h * hd;
+        const double mx = attn_scores(qi, k, k_rs, b, kh, S, hd, scale, causal, window, kpad, i, P);
+        if (mx == -INFINITY) {
+          for (int d = 0; d < hd; ++d) dqi[d] = 0.0f;
+          continue;
         }
+        double sum = 0.0;
+        for (int j = 0; j < S; ++j) {
+          P[j] = P[j] == -INFINITY ? 0.0 : exp(P[j] - mx);
+          sum += P[j];
+        }
+        double Di = 0.0; /* rowsum(dO∘O) */
+        for (int d = 0; d < hd; ++d) Di += (double)gi[d] * oi[d];
+        for (int j = 0; j < S; ++j) {
+          P[j] /= sum;
+          if (P[j] == 0.0) { dP[j] = 0.0; continue; }
+          const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
+          double s2 = 0.0;
+          for (int d = 0; d < hd; ++d) s2 += (double)gi[d] * vj[d];
+          dP[j] = s2;
+        }
+        for (int d = 0; d < hd; ++d) dqa[d] = 0.0;
+        for (int j = 0; j < S; ++j) {
+          if (P[j] == 0.0) continue;
+          const double ds = P[j] * (dP[j] - Di) * scale;
+          const float* kj = k + ((int64_t)b * S + j) * k_rs + (int64_t)kh * hd;
+          for (int d = 0; d < hd; ++d) {
+            dqa[d] += ds * kj[d];
+            dK[(int64_t)j * hd + d] += ds * qi[d];
+            dV[(int64_t)j * hd + d] += P[j] * gi[d];
+          }
+        }
+        for (int d = 0; d < hd; ++d) dqi[d] = (float)dqa[d];
       }
+    }
+    free(P);
+    free(dP);
+    free(dqa);
+  }
+  /* dK/dV of KV head kh: Σ over its query heads, then over their chunks */
+#pragma omp parallel for collapse(3) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int kh = 0; kh < Hkv; ++kh)
       for (int j = 0; j < S; ++j) {
         float* dkj = dk + ((int64_t)b * S + j) * dk_rs + (int64_t)kh * hd;
         float* dvj = dv + ((int64_t)b * S + j) * dv_rs + (int64_t)kh * hd;
         for (int d = 0; d < hd; ++d) {
-          dkj[d] = (float)dK[(int64_t)j * hd + d];
-          dvj[d] = (float)dV[(int64_t)j * hd + d];
+          double sk = 0.0, sv = 0.0;
+          for (int h = kh * grp; h < (kh + 1) * grp; ++h)
+            for (int c = 0; c < nch; ++c) {
+              const size_t off = ((size_t)((int64_t)b * Hq + h) * nch + c) * part + (size_t)j * hd + d;
+              sk += dKp[off];
+              sv += dVp[off];
+            }
+          dkj[d] = (float)sk;
+          dvj[d] = (float)sv;
         }
       }
-      free(dK); free(dV); free(P); free(dP);
-    }
+  free(dKp);
+  free(dVp);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -405,10 +438,16 @@ int64_t orc_ce_fwd_bwd(const float* logits, const int32_t* labels, int B,
                        int S, int64_t V, int ignore_index, float upstream,
                        int64_t norm_count, double* loss_sum, float* dlogits,
                        float* row_nll) {
+  /* A target counts iff label != ignore_index and 0 <= label < V.  The
+   * reference indexes row[label] unchecked (main.cpp:126), so an out-of-range
+   * label has no defined result there; here it is ignored in both the sum and
+   * the normaliser. */
   int64_t nvalid = 0;
   for (int b = 0; b < B; ++b)
-    for (int s = 0; s + 1 < S; ++s)
-      if (labels[(int64_t)b * S + s + 1] != ignore_index) nvalid++;
+    for (int s = 0; s + 1 < S; ++s) {
+      const int lab = labels[(int64_t)b * S + s + 1];
+      if (lab != ignore_index && lab >= 0 && lab < V) nvalid++;
+    }
   const int64_t denom = norm_count > 0 ? norm_count : nvalid;
   const double g = denom > 0 ? (double)upstream / (double)denom : 0.0;
   double total = 0.0;

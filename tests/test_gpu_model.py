@@ -8,13 +8,15 @@ weights), parameters after clip + Adam within 1e-5.
 Micro-batches: the engine runs all micro-batches of a step as one fused pass
 with per-micro-batch CE normalisation; the oracle runs them one after another
 like the reference driver (gpt2_small_lora_finetune/src/main.cpp:471-487)."""
+import dataclasses
+
 import numpy as np
 import pytest
 
 import oracle as O
 from conftest import rel_err
 from helpers import param_values
-from mobilefinetuner_amd.configs import CONFIGS, gemma3, gpt2, qwen2
+from mobilefinetuner_amd.configs import CONFIG_ORDER, CONFIGS, gemma3, gpt2, qwen2
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
@@ -154,32 +156,115 @@ def test_fp16_weights_against_fp32_reference():
     eng.close()
 
 
-def test_full_size_gpt2_small_step():
-    """BASELINE config 1 at full size (GPT-2 small, batch 4 × 128, LoRA r=8
-    on c_attn + c_proj): one fwd+bwd+clip+Adam step against the oracle
-    (BLAS-backed GEMMs, fp64-accumulated attention and CE)."""
-    rc = CONFIGS["gpt2s"]
+@pytest.mark.parametrize("cid", CONFIG_ORDER)
+def test_full_size_step(cid):
+    """Every BASELINE config at full size: one fwd+bwd+clip+Adam optimizer
+    step (all micro-batches of it) against the oracle (BLAS-backed GEMMs,
+    fp64-accumulated attention and CE), on the parameters the bench uses
+    (device init: W, biases, embeddings N(0, 0.02), LoRA A N(0, 1/r), B
+    N(0, 0.02); Gemma-3 1B's W and E stored as fp16), copied to the oracle.
+    Loss, every LoRA gradient and the grad norm within 1e-4; parameters after
+    clip + Adam within 1e-6 of a host replay.  For the fp16-W config the
+    oracle is fed the same fp16 values (exact widening), so the fp32 bar
+    applies; test_full_size_fp16_weights_against_fp32 covers the 2e-3 bar."""
+    rc = CONFIGS[cid]
     mc = rc.model
-    print("full-size gpt2-small step", flush=True)
+    B, S, acc = rc.batch, rc.seq, rc.accum
+    print(f"full-size step {cid}: B={B} S={S} accum={acc}", flush=True)
     O.lib().orc_set_blas(1)
     try:
+        eng = Model(mc, rc.tokens_per_step)
+        eng.init_params(1234 + CONFIG_ORDER.index(cid), 0.02, 1.0 / mc.lora_r, 0.02)
         om = O.OracleModel(mc)
-        eng = Model(mc, rc.batch * rc.seq)
-        rng = np.random.default_rng(1234)
-        vals = param_values(om.params, seed=1234)
-        for n, v in vals.items():
-            om.set_param(n, v)
-            eng.set_param(n, v)
-        ids = rng.integers(0, mc.vocab, (1, rc.batch, rc.seq)).astype(np.int32)
-        lo, le, grads, no, ne = run_step(om, eng, ids, ids.copy(), None, rc.batch, rc.seq, 1,
-                                         lr=2e-4)
+        for p in om.params:
+            om.set_param(p["name"], eng.get(p["name"]))
+        rng = np.random.default_rng(77)
+        ids = rng.integers(0, mc.vocab, (acc, B, S)).astype(np.int32)
+        lo, le, grads, no, ne = run_step(om, eng, ids, ids.copy(), None, B, S, acc, lr=2e-4,
+                                         replay=AdamReplay())
+        print(f"  loss gpu={le:.6f} oracle={lo:.6f} norm gpu={ne:.6f} oracle={no:.6f}", flush=True)
         assert abs(le - lo) < TOL * abs(lo)
-        worst = max(rel_err(ge, go) for ge, go in grads.values())
-        assert worst < TOL, worst
+        errs = {n: rel_err(ge, go) for n, (ge, go) in grads.items()}
+        worst = max(errs, key=errs.get)
+        print(f"  worst LoRA grad {worst}: {errs[worst]:.2e} over {len(errs)} tensors", flush=True)
+        assert errs[worst] < TOL, (worst, errs[worst])
         assert abs(ne - no) < TOL * no
         eng.close()
     finally:
         O.lib().orc_set_blas(0)
+
+
+def test_full_size_fp16_weights_against_fp32():
+    """Gemma-3 1B at full size with fp16-stored frozen W and E (config 5)
+    against the oracle on the UNROUNDED fp32 weights.  The loss and the whole
+    LoRA gradient (all tensors as one vector) are held to the fp16-W bar of
+    2e-3.  Single tensors can differ from the fp32 model by more than that
+    (a rank-8 gradient deep in the network sums many rounded-weight
+    products); each is held instead to the difference the fp16 rounding
+    itself makes: the oracle fed the same fp16 values against the fp32
+    oracle, plus the 1e-4 parity bar."""
+    rc = CONFIGS["gemma1b"]
+    mc16 = rc.model
+    mc32 = dataclasses.replace(mc16, w_fp16=0, name="gemma3-1b-fp32")
+    B, S, acc = rc.batch, rc.seq, rc.accum
+    print(f"full-size gemma1b fp16 W vs fp32 reference: B={B} S={S} accum={acc}", flush=True)
+    O.lib().orc_set_blas(1)
+    try:
+        eng = Model(mc16, rc.tokens_per_step)
+        om32 = O.OracleModel(mc32)
+        om16 = O.OracleModel(mc16)
+        rng = np.random.default_rng(5)
+        for p in om32.params:
+            n = p["name"]
+            if n.endswith("lora_A"):
+                v = rng.standard_normal(p["shape"], dtype=np.float32) / mc16.lora_r
+            elif "norm" in n:
+                v = np.zeros(p["shape"], np.float32)
+            else:
+                v = rng.standard_normal(p["shape"], dtype=np.float32) * 0.02
+            om32.set_param(n, v)
+            v16 = v.astype(np.float16).view(np.uint16) if eng.by_name[n]["f16"] else v
+            om16.set_param(n, v16)
+            eng.set_param(n, v16)
+        ids = rng.integers(0, mc16.vocab, (acc, B, S)).astype(np.int32)
+        for i in range(acc):
+            om16.fwd_bwd(ids[i], None, ids[i], B, S, 1.0 / acc)
+        lo, le, grads, no, ne = run_step(om32, eng, ids, ids.copy(), None, B, S, acc, lr=2e-4)
+        names = list(grads)
+        g16 = {n: om16.get(n, grad=True) for n in names}
+        allg = lambda d: np.concatenate([d[n].ravel() for n in names])  # noqa: E731
+        whole = rel_err(allg({n: grads[n][0] for n in names}), allg({n: grads[n][1] for n in names}))
+        e_gpu = {n: rel_err(grads[n][0], grads[n][1]) for n in names}
+        e_ref = {n: rel_err(g16[n], grads[n][1]) for n in names}
+        worst = max(names, key=lambda n: e_gpu[n] - e_ref[n])
+        print(f"  loss gpu={le:.6f} fp32 oracle={lo:.6f}; whole-gradient rel err {whole:.2e}; "
+              f"largest per-tensor excess over fp16 rounding: {worst} gpu {e_gpu[worst]:.2e} "
+              f"vs oracle-fp16 {e_ref[worst]:.2e}", flush=True)
+        assert abs(le - lo) < TOL_F16W * abs(lo)
+        assert whole < TOL_F16W, whole
+        for n in names:
+            assert e_gpu[n] <= e_ref[n] + TOL, (n, e_gpu[n], e_ref[n])
+        eng.close()
+    finally:
+        O.lib().orc_set_blas(0)
+
+
+def test_out_of_range_token_id_is_reported():
+    """A token id outside [0, vocab) embeds as a zero row (nothing is read out
+    of bounds) and the step's statistics report it as an error."""
+    mc, B, S, _ = SMALL["gpt2"]
+    eng = Model(mc, B * S)
+    eng.init_params(3)
+    ids = np.random.default_rng(1).integers(0, mc.vocab, (B * S,)).astype(np.int32)
+    bad = ids.copy()
+    bad[5] = mc.vocab + 17
+    dev = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+    eng.train_step(dev(bad), dev(ids), S=S, graph=False)
+    with pytest.raises(RuntimeError, match="token id"):
+        eng.read_stats()
+    eng.train_step(dev(ids), dev(ids), S=S, graph=False)
+    eng.read_stats()  # the flag was cleared by the report
+    eng.close()
 
 
 def test_graph_replay_equals_eager_steps():

@@ -50,7 +50,7 @@ LIN_SHAPES = [
     (512, 768, 2304, 8, True),   # GPT-2 small c_attn
     (512, 768, 768, 8, True),    # GPT-2 small attn c_proj (split-K path)
     (64, 3072, 768, 4, False),   # few tiles, deep K (split-K)
-    (256, 1024, 4096, 16, True), # 128x128 tile path
+    (256, 1024, 4096, 16, True), # rank 16, 64 tiles of 64x64 (the 128x128 kernel needs >= 1024 tiles)
     (33, 20, 50, 0, True),       # plain frozen linear (no LoRA)
 ]
 
@@ -113,6 +113,33 @@ def test_lora_linear_fp16_weight(M, K, N):
     assert rel_err(h(dx), dx_ref) < TOL
     assert rel_err(h(dA), dA_ref) < TOL
     assert rel_err(h(dB), dB_ref) < TOL
+
+
+def test_lm_head_fp16_vocab_gemms():
+    """Gemma-3 1B's LM head with the tied embedding E [V, d] stored as fp16
+    (config 5): logits = h·Eᵀ runs the 128×128 kernel with an [N, K] fp16
+    operand widened in the tile load (8192 tiles at M = 512, V = 262144), and
+    dH = dlogits·E reduces over the whole vocabulary (K = 262144, split 16
+    ways).  Both against the oracle (BLAS-backed GEMMs) on the same fp16
+    values, at the fp32 bar."""
+    M, d, V = 512, 1152, 262144
+    print(f"lm head fp16 M={M} d={d} V={V}", flush=True)
+    E16 = rn(V, d, std=0.02).astype(np.float16)
+    Ef = E16.astype(np.float32)
+    hf = rn(M, d)
+    dlg = rn(M, V, std=1e-4)
+    O.lib().orc_set_blas(1)
+    try:
+        logits_ref = O.lora_linear_bwd(hf, None, Ef, None, None, None, 1.0)[0]
+        dh_ref = O.lora_linear_fwd(dlg, Ef, None, None, None, 1.0)[0]
+    finally:
+        O.lib().orc_set_blas(0)
+    gE = g(E16)
+    logits = ops.lora_linear_bwd(g(hf), None, gE, None, None, None, 1.0)[0]
+    assert rel_err(h(logits), logits_ref) < TOL
+    del logits
+    dh = ops.lora_linear_fwd(g(dlg), gE, None, None, None, 1.0)[0]
+    assert rel_err(h(dh), dh_ref) < TOL
 
 
 PIPE_SHAPES = [
@@ -284,6 +311,23 @@ def test_cross_entropy(B, S, V):
     assert rel_err(h(dl), dl_ref) < TOL
 
 
+def test_cross_entropy_out_of_range_labels_count_as_ignored():
+    """A label outside [0, V) other than ignore_index is excluded from both the
+    loss and the normaliser (the count kernel and the row kernel apply the same
+    test), exactly as the oracle does."""
+    B, S, V = 2, 9, 3001
+    logits = rn(B * S, V, std=2.0)
+    labels = RNG.integers(0, V, (B, S)).astype(np.int32)
+    labels[0, 2], labels[0, 5], labels[1, 4], labels[1, 7] = V, -5, V + 1000, -100
+    ls_ref, n_ref, dl_ref, nll_ref = O.ce_fwd_bwd(logits, labels, B, S, -100, 1.0)
+    assert n_ref == B * (S - 1) - 4
+    ls, n, dl, nll = ops.ce_fwd_bwd(g(logits), g(labels), B, S, -100, 1.0)
+    assert int(h(n)[0]) == n_ref
+    assert abs(float(h(ls)[0]) - ls_ref) < TOL * abs(ls_ref)
+    assert rel_err(h(dl), dl_ref) < TOL
+    assert np.abs(h(dl).reshape(B, S, V)[0, 1]).max() == 0.0  # row predicting label V
+
+
 def test_cross_entropy_all_ignored_row_zero_grad():
     B, S, V = 1, 5, 1000
     logits = rn(B * S, V)
@@ -416,6 +460,28 @@ def test_embed():
     out16 = ops.embed(g(ids), S, g(w16), None, math.sqrt(640))
     ref16 = O.embed(ids, S, None, None, math.sqrt(640), wte_f16=w16.view(np.uint16))
     assert np.array_equal(h(out16), ref16)
+
+
+def test_embed_out_of_range_ids_give_zero_rows_and_flag():
+    """Ids outside [0, vocab) read nothing: their rows are zeros and the
+    device flag is set; the other rows are exact."""
+    V, C, S = 1000, 64, 8
+    wte = rn(V, C)
+    ids = RNG.integers(0, V, (2, S)).astype(np.int32)
+    bad_rows = [(0, 1), (0, 6), (1, 3)]
+    ids[0, 1], ids[0, 6], ids[1, 3] = -100, V, V + 12345
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = h(ops.embed(g(ids), S, g(wte), None, 1.0, bad=bad)).reshape(2, S, C)
+    assert int(h(bad)[0]) == 1
+    for b in range(2):
+        for s in range(S):
+            if (b, s) in bad_rows:
+                assert np.all(out[b, s] == 0.0)
+            else:
+                assert np.array_equal(out[b, s], wte[ids[b, s]])
+    ok = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.embed(g(np.clip(ids, 0, V - 1)), S, g(wte), None, 1.0, bad=ok)
+    assert int(h(ok)[0]) == 0
 
 
 def test_outputs_float32_whatever_the_default_dtype():

@@ -185,6 +185,25 @@ def test_ce_closed_forms():
 
 
 # ---------------------------------------------------------------- fp16
+def test_ce_out_of_range_label_equals_ignored():
+    """A label outside [0, V) (other than ignore_index) contributes nothing and
+    is not counted: identical to the same label set to ignore_index (the
+    reference indexes such a label unchecked, so this is the defined rule)."""
+    rng = np.random.default_rng(3)
+    B, S, V = 2, 7, 50
+    lg = rng.standard_normal((B * S, V)).astype(np.float32)
+    lab = rng.integers(0, V, (B, S)).astype(np.int32)
+    bad = lab.copy()
+    bad[0, 2], bad[1, 5] = V, -7
+    ign = lab.copy()
+    ign[0, 2], ign[1, 5] = -100, -100
+    a = O.ce_fwd_bwd(lg, bad, B, S, -100, 1.0)
+    b = O.ce_fwd_bwd(lg, ign, B, S, -100, 1.0)
+    # the loss sum is an OpenMP reduction (order varies run to run): fp64-close
+    assert abs(a[0] - b[0]) <= 1e-12 * abs(b[0]) and a[1] == b[1] == B * (S - 1) - 2
+    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
+
+
 def test_f16_exhaustive_widening():
     bits = np.arange(65536, dtype=np.uint16)
     out = O.f16_to_f32(bits)
