@@ -130,6 +130,21 @@ int mft_ce_fwd_bwd(mft_handle h, const float* logits, const int32_t* labels,
                    int64_t norm_count, double* loss_sum, int64_t* n_valid,
                    float* dlogits, float* row_nll);
 
+/* The same computation as mft_ce_fwd_bwd, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Its scratch (the
+ * valid-target counter and, when row_nll is NULL, the per-row NLLs) is a
+ * fixed device array of 256 KiB + 256 B inside the library, held by each
+ * device until the process ends; the call allocates nothing.  B*S must not
+ * exceed 65536 rows (MFT_EINVAL otherwise, nothing launched).  Every call on
+ * one device shares that array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+int mft_ce_fwd_bwd_noalloc(mft_handle h, const float* logits,
+                           const int32_t* labels, int B, int S, int64_t V,
+                           int ignore_index, float upstream,
+                           int64_t norm_count, double* loss_sum,
+                           int64_t* n_valid, float* dlogits, float* row_nll);
+
 /* ---- a7: fp16 → fp32 widening ------------------------------------------------
  * The FP16 shard store's require() path (ParameterSharder, opt_ops/sharding;
  * --shard_fp16_disk, README.md:311,318).  Exact for every bit pattern. */

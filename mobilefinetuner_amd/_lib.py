@@ -59,6 +59,7 @@ _SIGS = {
     "mft_attn_bwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, _I, _I, _I, _I, _I, _F,
                           _I, _I, _P, _P, _L, _P, _L, _P, _L]),
     "mft_ce_fwd_bwd": (_I, [_P, _P, _P, _I, _I, _L, _I, _F, _L, _P, _P, _P, _P]),
+    "mft_ce_fwd_bwd_noalloc": (_I, [_P, _P, _P, _I, _I, _L, _I, _F, _L, _P, _P, _P, _P]),
     "mft_dequant_f16": (_I, [_P, _P, _P, _L]),
     "mft_quant_f16": (_I, [_P, _P, _P, _L]),
     "mft_adam_step": (_I, [_P, _P, _P, _P, _P, _L, _F, _F, _F, _F, _F, _I, _P, _I]),
