@@ -796,6 +796,442 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_mfma(AttnP p, int n_dkdv) {
   else attn_bwd_dq_role<HD, NW, BKV, SK>(p, bid - n_dkdv, smem);
 }
 
+// ------------------------------------------------------------------------------
+// Short sequences: a workgroup per 16-row tile, its inner loop split over
+// the waves.
+// ------------------------------------------------------------------------------
+// At S ≤ 256 the blocked kernels above leave each workgroup one or two
+// blocks of serial work on one wave per SIMD, so every block pays its load
+// latency in full.  Here a workgroup owns one 16-query tile (forward, dQ)
+// or one 16-key tile (dK/dV) of one head; its NW waves take the tile's
+// visible inner tiles (16 keys, or 16 queries) round-robin, each reading its
+// operands straight from global memory (L2) into MFMA operand registers,
+// and the waves' partial results are merged through LDS in wave order
+// (deterministic).  Operand layouts per lane (i = lane % 16, g = lane / 16):
+// a 128-bit read Rows[i][16c + 4g .. +3] for an operand indexed (row i,
+// reduction d), four 32-bit reads Rows[4g + t][16c + i] for an operand
+// indexed (reduction row, column d).  The backward forms delta =
+// rowsum(dO∘O) from O and dO rows it loads anyway (no separate pass).
+
+// Forward: Sᵀ = K·Qᵀ (lane: query i, keys 4g+v of the tile), online softmax
+// per query, O += P·V with P from registers (A operand) and V as four
+// column reads; O partial [query 4g+v][d 16c+i] and (max, sum) per query to
+// LDS, merged over the waves.
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_fwd_short(AttnP p) {
+  constexpr int NC = HD / 16;
+  constexpr int PO = HD + 4;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Os = smem;              // [NW][16][PO]
+  float* Ms = Os + NW * 16 * PO;  // [NW][16]
+  float* Ls = Ms + NW * 16;       // [NW][16]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int nqt = (p.S + 15) / 16;
+  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int qt = nqt - 1 - (int)blockIdx.x / (p.Hq * p.B);  // heaviest (last) tiles first
+  const int q0 = 16 * qt;
+  const int kh = h / (p.Hq / p.Hkv);
+  const int qi = q0 + li;
+  const bool qok = qi < p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const int64_t tok0 = (int64_t)b * p.S;
+  const int qlast = min(q0 + 15, p.S - 1);
+  const int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
+  const int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  const int jhi = qok ? (p.causal ? qi : p.S - 1) : -1;  // keys visible to query qi
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
+
+  const float qscale = p.scale * kLog2e;  // scores in base-2 units
+  floatx4 qreg[NC], oacc[NC];
+  {
+    const float* qr = p.q + (tok0 + min(qi, p.S - 1)) * p.q_rs + (int64_t)h * HD + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(qr + 16 * c);
+      qreg[c] = qok ? x * qscale : floatx4{0.f, 0.f, 0.f, 0.f};
+      oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  float mrow = -INFINITY, lrow = 0.f;
+  const float* kbase = p.k + (int64_t)kh * HD;
+  const float* vbase = p.v + (int64_t)kh * HD;
+  auto load = [&](int kt, floatx4 (&kr)[NC], float (&vr)[NC][4]) {
+    const float* krow = kbase + (tok0 + min(16 * kt + li, p.S - 1)) * p.k_rs + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kr[c] = *reinterpret_cast<const floatx4*>(krow + 16 * c);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float* vrow = vbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.v_rs + li;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) vr[c][t] = vrow[16 * c];
+    }
+  };
+  floatx4 kc[NC];
+  float vc[NC][4];
+  int kt = kt_lo + w;
+  if (kt <= kt_hi) load(kt, kc, vc);
+  for (; kt <= kt_hi; kt += NW) {
+    floatx4 kn[NC];
+    float vn[NC][4];
+    const bool more = kt + NW <= kt_hi;
+    if (more) load(kt + NW, kn, vn);
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s = mfma4(kc[c][t], qreg[c][t], s);
+    // lane holds S[query qi][key j0 + v]
+    const int j0 = 16 * kt + 4 * lg;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = j0 + v;
+      bool ok = (j >= jlo) & (j <= jhi) & (j < p.S);
+      if (kpb) ok = ok & (kpb[min(j, p.S - 1)] > 0.5f);
+      s[v] = ok ? s[v] : -INFINITY;
+    }
+    float mloc = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mloc = max_xor32(max_xor16(mloc));
+    const float mnew = fmaxf(mrow, mloc);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;  // nothing visible yet: exact zeros, no NaN
+    const float corr = fast_exp2(mrow - mref);
+    floatx4 pr;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) pr[v] = fast_exp2(s[v] - mref);
+    const float lsum = add_xor32(add_xor16((pr[0] + pr[1]) + (pr[2] + pr[3])));
+    lrow = lrow * corr + lsum;
+    mrow = mnew;
+    // O rows are queries 4g+v: their rescale factors live in lanes 4g+v
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float cv = __shfl(corr, 4 * lg + v, 64);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) oacc[c][v] *= cv;
+    }
+    // O[q][d] += Σ_key P[q][key]·V[key][d]
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) oacc[c] = mfma4(pr[t], vc[c][t], oacc[c]);
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        kc[c] = kn[c];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) vc[c][t] = vn[c][t];
+      }
+    }
+  }
+  if (lg == 0) {
+    Ms[w * 16 + li] = mrow;
+    Ls[w * 16 + li] = lrow;
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Os[(w * 16 + 4 * lg + v) * PO + 16 * c + li] = oacc[c][v];
+  __syncthreads();
+  // merge in wave order: M = max_w m_w, L = Σ_w l_w·2^(m_w − M), O = Σ_w O_w·2^(m_w − M) / L
+  for (int f = tid; f < 16 * (HD / 4); f += 64 * NW) {
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    const int gq = q0 + r;
+    if (gq >= p.S) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) M = fmaxf(M, Ms[u * 16 + r]);
+    const float Mref = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    floatx4 o = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float wgt = fast_exp2(Ms[u * 16 + r] - Mref);
+      L += Ls[u * 16 + r] * wgt;
+      o += *reinterpret_cast<const floatx4*>(&Os[(u * 16 + r) * PO + 4 * c4]) * wgt;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *reinterpret_cast<floatx4*>(p.out + (tok0 + gq) * p.out_rs + (int64_t)h * HD + 4 * c4) = o * inv;
+    if (c4 == 0) p.lse_out[((int64_t)b * p.Hq + h) * p.S + gq] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
+  }
+}
+
+// dK/dV role: workgroup = one 16-key tile of one QUERY head; waves take the
+// query tiles that see it round-robin.  K, V of the tile stay in registers
+// (B operands of S = Q·Kᵀ and dP = dO·Vᵀ); per query tile a wave reads Q,
+// dO, O rows (A operands, and delta) and Q, dO by column (B operands of
+// dK += dSᵀ·Q, dV += Pᵀ·dO).  The partials [key 4g+v][d 16c+i] are summed
+// over the waves through LDS; GQA groups > 1 write per-query-head partials.
+template <int HD, int NW>
+__device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, float* smem) {
+  constexpr int NC = HD / 16;
+  constexpr int PO = HD + 4;
+  float* Dk = smem;               // [NW][16][PO]
+  float* Dv = Dk + NW * 16 * PO;  // [NW][16][PO]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int hb = bid % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int grp = p.Hq / p.Hkv;
+  const int kh = h / grp;
+  const int kt = bid / (p.Hq * p.B);  // heaviest (first) key tiles first
+  const int k0 = 16 * kt;
+  const int kj = k0 + li;  // this lane's key (S column)
+  const int64_t tok0 = (int64_t)b * p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const bool kvalid = kj < p.S && (!kpb || kpb[min(kj, p.S - 1)] > 0.5f);
+  const int klast = min(k0 + 15, p.S - 1);
+  const int qt_lo = (p.causal ? k0 : 0) / 16;
+  const int qt_hi = (p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1) / 16;
+
+  const float qk2 = p.scale * kLog2e;
+  floatx4 kreg[NC], vreg[NC], dkacc[NC], dvacc[NC];
+  {
+    const int64_t row = tok0 + min(kj, p.S - 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t off = (int64_t)kh * HD + 16 * c + 4 * lg;
+      kreg[c] = *reinterpret_cast<const floatx4*>(p.k + row * p.k_rs + off) * qk2;
+      vreg[c] = *reinterpret_cast<const floatx4*>(p.v + row * p.v_rs + off);
+      dkacc[c] = dvacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  const int64_t lrow0 = ((int64_t)b * p.Hq + h) * p.S;
+  // one query tile's operands: Q, dO, O rows (128-bit), Q and dO columns,
+  // lse of query q0 + i
+  struct QTile {
+    floatx4 qa[NC], ga[NC], oa[NC];
+    float qb[NC][4], gb[NC][4];
+    float lse;
+  };
+  auto load = [&](int qt, QTile& T) {
+    const int q0 = 16 * qt;
+    const int64_t row = tok0 + min(q0 + li, p.S - 1);
+    const int64_t off = (int64_t)h * HD + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      T.qa[c] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off + 16 * c);
+      T.ga[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
+      T.oa[c] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t r2 = tok0 + min(q0 + 4 * lg + t, p.S - 1);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        T.qb[c][t] = p.q[r2 * p.q_rs + (int64_t)h * HD + 16 * c + li];
+        T.gb[c][t] = p.dout[r2 * p.do_rs + (int64_t)h * HD + 16 * c + li];
+      }
+    }
+    T.lse = p.lse[lrow0 + min(q0 + li, p.S - 1)];
+  };
+  auto compute = [&](int qt, const QTile& T) {
+    const int q0 = 16 * qt;
+    const float l2 = T.lse * kLog2e;  // query q0 + li
+    float dl = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dl = fmaf(T.ga[c][e], T.oa[c][e], dl);
+    dl = add_xor32(add_xor16(dl));  // delta of query q0 + li
+    floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s4 = mfma4(T.qa[c][t], kreg[c][t], s4);
+        dp4 = mfma4(T.ga[c][t], vreg[c][t], dp4);
+      }
+    // S[q0 + 4g + v][key kj]: P = 2^(S₂ − lse₂), dS/scale = P∘(dP − delta)
+    floatx4 pv, ds;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int qv = q0 + 4 * lg + v;
+      const float l2v = __shfl(l2, 4 * lg + v, 64);
+      const float dlv = __shfl(dl, 4 * lg + v, 64);
+      const bool ok = kvalid & (qv < p.S) & (!p.causal | (qv >= kj)) & ((p.window <= 0) | (qv - kj < p.window));
+      pv[v] = fast_exp2(ok ? s4[v] - l2v : -INFINITY);
+      ds[v] = pv[v] * (dp4[v] - dlv);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        dvacc[c] = mfma4(pv[t], T.gb[c][t], dvacc[c]);
+        dkacc[c] = mfma4(ds[t], T.qb[c][t], dkacc[c]);
+      }
+  };
+  // One tile of operands in registers at a time: holding the next tile's
+  // loads in flight as well (two tiles of registers) halves the waves per
+  // SIMD and measured slower at GPT-2's shapes.
+  for (int qt = qt_lo + w; qt <= qt_hi; qt += NW) {
+    QTile cur;
+    load(qt, cur);
+    compute(qt, cur);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      Dk[(w * 16 + 4 * lg + v) * PO + 16 * c + li] = dkacc[c][v];
+      Dv[(w * 16 + 4 * lg + v) * PO + 16 * c + li] = dvacc[c][v];
+    }
+  __syncthreads();
+  const bool direct = grp == 1;
+  for (int f = tid; f < 16 * (HD / 4); f += 64 * NW) {
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    const int gk = k0 + r;
+    if (gk >= p.S) continue;
+    floatx4 sk = floatx4{0.f, 0.f, 0.f, 0.f}, sv = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      sk += *reinterpret_cast<const floatx4*>(&Dk[(u * 16 + r) * PO + 4 * c4]);
+      sv += *reinterpret_cast<const floatx4*>(&Dv[(u * 16 + r) * PO + 4 * c4]);
+    }
+    const int64_t tok = tok0 + gk;
+    float* dkr = direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + (tok * p.Hq + h) * HD;
+    float* dvr = direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD;
+    *reinterpret_cast<floatx4*>(dkr + 4 * c4) = sk * p.scale;
+    *reinterpret_cast<floatx4*>(dvr + 4 * c4) = sv;
+  }
+}
+
+// dQ role: workgroup = one 16-query tile of one head; waves take its visible
+// key tiles round-robin.  Q, dO of the tile stay in registers (B operands of
+// Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ, so a lane owns one query's softmax row); per
+// key tile a wave reads K, V rows (A operands) and K by column (B operand of
+// dQ += dS·K).  The partials [query 4g+v][d 16c+i] are summed over the
+// waves through LDS.
+template <int HD, int NW>
+__device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float* smem) {
+  constexpr int NC = HD / 16;
+  constexpr int PO = HD + 4;
+  float* Dq = smem;  // [NW][16][PO]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int nqt = (p.S + 15) / 16;
+  const int hb = bid % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int qt = nqt - 1 - bid / (p.Hq * p.B);  // heaviest (last) query tiles first
+  const int q0 = 16 * qt;
+  const int kh = h / (p.Hq / p.Hkv);
+  const int qi = q0 + li;
+  const bool qok = qi < p.S;
+  const int64_t tok0 = (int64_t)b * p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const int qlast = min(q0 + 15, p.S - 1);
+  const int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
+  const int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  const int jhi = qok ? (p.causal ? qi : p.S - 1) : -1;
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
+
+  const float qk2 = p.scale * kLog2e;
+  const float* kbase = p.k + (int64_t)kh * HD;
+  const float* vbase = p.v + (int64_t)kh * HD;
+  floatx4 qreg[NC], greg[NC], dqacc[NC], orow[NC];
+  {
+    const int64_t row = tok0 + min(qi, p.S - 1);
+    const int64_t off = (int64_t)h * HD + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qreg[c] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off + 16 * c);
+      greg[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
+      orow[c] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
+      dqacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  const float lse_q = p.lse[((int64_t)b * p.Hq + h) * p.S + min(qi, p.S - 1)];
+  float dl = 0.f, l2 = 0.f;  // delta and lse·log2(e) of query qi (formed below)
+  // one key tile's operands: K, V rows (128-bit) and K columns
+  struct KTile {
+    floatx4 ka[NC], va[NC];
+    float kb[NC][4];
+  };
+  auto load = [&](int kt, KTile& T) {
+    const int64_t row = tok0 + min(16 * kt + li, p.S - 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      T.ka[c] = *reinterpret_cast<const floatx4*>(kbase + row * p.k_rs + 16 * c + 4 * lg);
+      T.va[c] = *reinterpret_cast<const floatx4*>(vbase + row * p.v_rs + 16 * c + 4 * lg);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float* kr = kbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.k_rs + li;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) T.kb[c][t] = kr[16 * c];
+    }
+  };
+  auto compute = [&](int kt, const KTile& T) {
+    floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s4 = mfma4(T.ka[c][t], qreg[c][t], s4);
+        dp4 = mfma4(T.va[c][t], greg[c][t], dp4);
+      }
+    // Sᵀ[key 16kt + 4g + v][query qi]
+    floatx4 ds;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = 16 * kt + 4 * lg + v;
+      bool ok = (j >= jlo) & (j <= jhi) & (j < p.S);
+      if (kpb) ok = ok & (kpb[min(j, p.S - 1)] > 0.5f);
+      const float pp = fast_exp2(ok ? s4[v] - l2 : -INFINITY);
+      ds[v] = pp * (dp4[v] - dl);
+    }
+    // dQ[q][d] += Σ_key dS[q][key]·K[key][d]
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], T.kb[c][t], dqacc[c]);
+  };
+  // the first key tile's loads go out with the query rows' (before delta is
+  // formed); each later tile's after the previous one is multiplied (one
+  // tile of registers, as in the dK/dV role)
+  KTile cur;
+  int kt = kt_lo + w;
+  if (kt <= kt_hi) load(kt, cur);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    qreg[c] *= qk2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dl = fmaf(greg[c][e], orow[c][e], dl);
+  }
+  dl = add_xor32(add_xor16(dl));
+  l2 = lse_q * kLog2e;
+  for (; kt <= kt_hi; kt += NW) {
+    compute(kt, cur);
+    if (kt + NW <= kt_hi) load(kt + NW, cur);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Dq[(w * 16 + 4 * lg + v) * PO + 16 * c + li] = dqacc[c][v];
+  __syncthreads();
+  for (int f = tid; f < 16 * (HD / 4); f += 64 * NW) {
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    const int gq = q0 + r;
+    if (gq >= p.S) continue;
+    floatx4 sq = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) sq += *reinterpret_cast<const floatx4*>(&Dq[(u * 16 + r) * PO + 4 * c4]);
+    *reinterpret_cast<floatx4*>(p.dq + (tok0 + gq) * p.dq_rs + (int64_t)h * HD + 4 * c4) = sq * p.scale;
+  }
+}
+
+// Both short-sequence backward roles in one launch: blocks [0, n_dkdv) are
+// dK/dV tiles, the rest dQ tiles.
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_short(AttnP p, int n_dkdv) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int bid = (int)blockIdx.x;
+  if (bid < n_dkdv) attn_bwd_short_dkdv<HD, NW>(p, bid, smem);
+  else attn_bwd_short_dq<HD, NW>(p, bid - n_dkdv, smem);
+}
+
 template <typename K>
 void set_lds(K kernel, size_t bytes) {
   MFT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -944,6 +1380,44 @@ void bwd_launch(hipStream_t s, AttnP& p, int nw) {
   }
 }
 
+// The short-sequence kernels serve S ≤ 256 at head_dim 64 and 128.  Tuning
+// hook: MFT_ATTN_SHORT=0 keeps the blocked kernels, =1 takes the short ones
+// at any S (head_dim ≤ 128).
+constexpr int kShortWaves = 4;
+bool use_short(const AttnArgs& a) {
+  if (a.hd > 128) return false;
+  if (const char* forced = getenv("MFT_ATTN_SHORT")) return atoi(forced) != 0;
+  return a.S <= 256;
+}
+
+template <int HD>
+void fwd_short_launch(hipStream_t s, AttnP& p) {
+  constexpr int NW = kShortWaves;
+  const size_t lds = sizeof(float) * (NW * 16 * (HD + 4) + 2 * NW * 16);
+  auto kern = attn_fwd_short<HD, NW>;
+  set_lds(kern, lds);
+  const dim3 grid((unsigned)(cdiv(p.S, 16) * p.Hq * p.B));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  MFT_LAUNCH_CHECK();
+}
+
+template <int HD>
+void bwd_short_launch(hipStream_t s, AttnP& p) {
+  constexpr int NW = kShortWaves;
+  const size_t lds = sizeof(float) * 2 * NW * 16 * (HD + 4);
+  auto kern = attn_bwd_short<HD, NW>;
+  set_lds(kern, lds);
+  const int tiles = (int)(cdiv(p.S, 16) * p.Hq * p.B);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * tiles)), dim3(64 * NW), lds, s, p, tiles);
+  MFT_LAUNCH_CHECK();
+  if (p.Hq != p.Hkv) {
+    const int64_t total = (int64_t)p.B * p.S * p.Hkv * (HD / 4);
+    hipLaunchKernelGGL(attn_partial_sum_kernel<HD>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
+                       dim3(256), 0, s, p, 16);
+    MFT_LAUNCH_CHECK();
+  }
+}
+
 AttnP make(const AttnArgs& a) {
   MFT_CHECK_ARG(a.B > 0 && a.S > 0 && a.Hq > 0 && a.Hkv > 0, "empty attention");
   MFT_CHECK_ARG(a.Hq % a.Hkv == 0, "Hq must be a multiple of Hkv");
@@ -967,6 +1441,7 @@ AttnP make(const AttnArgs& a) {
 }  // namespace
 
 size_t attn_fwd_scratch_floats(const AttnArgs& a) {
+  if (use_short(a)) return 0;
   const FwdPlan pl = fwd_plan(a);
   if (pl.nch == 1) return 0;
   return (size_t)a.B * a.Hq * pl.nch * a.S * (size_t)(a.hd + 2);
@@ -986,6 +1461,10 @@ void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* l
   p.out = o;
   p.out_rs = o_rs;
   p.lse_out = lse;
+  if (use_short(a)) {
+    a.hd == 64 ? fwd_short_launch<64>(s, p) : fwd_short_launch<128>(s, p);
+    return;
+  }
   const FwdPlan pl = fwd_plan(a);
   p.nch = pl.nch;
   p.ck = pl.ck;
@@ -1021,6 +1500,17 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
   p.dk = dk; p.dk_rs = dk_rs;
   p.dv = dv; p.dv_rs = dv_rs;
   const int64_t rows = (int64_t)a.B * a.S * a.Hq;
+  // the short kernels read O and write dQ/dK/dV as 128-bit rows
+  auto rows16 = [](const float* t, int64_t rs) { return rs % 4 == 0 && ((uintptr_t)t & 15) == 0; };
+  const bool short_ok = rows16(o, o_rs) && rows16(dq, dq_rs) && rows16(dk, dk_rs) && rows16(dv, dv_rs);
+  if (short_ok && use_short(a)) {  // delta formed in-kernel; GQA partials after the delta rows
+    if (a.Hq != a.Hkv) {
+      p.pdk = ws.ptr + (rows + 3) / 4 * 4;
+      p.pdv = p.pdk + rows * a.hd;
+    }
+    a.hd == 64 ? bwd_short_launch<64>(s, p) : bwd_short_launch<128>(s, p);
+    return;
+  }
   const BwdPlan pl = bwd_plan(a);
   p.nqc = pl.nqc; p.cq = pl.cq;
   p.nkc = pl.nkc; p.ckq = pl.ckq;
@@ -1051,7 +1541,7 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
 size_t attn_bwd_scratch_floats(const AttnArgs& a) {
   const BwdPlan pl = bwd_plan(a);
   const size_t rows = (size_t)a.B * a.S * a.Hq;
-  size_t n = (rows + 3) / 4 * 4;
+  size_t n = (rows + 3) / 4 * 4;  // covers the short kernels' need too
   if (a.Hq != a.Hkv || pl.nqc > 1) n += 2 * (size_t)pl.nqc * rows * (size_t)a.hd;
   if (pl.nkc > 1) n += (size_t)pl.nkc * rows * (size_t)a.hd;
   return n;

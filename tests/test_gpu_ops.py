@@ -196,6 +196,7 @@ ATTN = [
     (2, 4, 1, 96, 256, 0, False),     # Gemma hd=256, GQA 4:1
     (1, 4, 1, 200, 256, 64, False),   # Gemma sliding window
     (1, 4, 2, 77, 128, 0, True),      # hd=128, ragged S
+    (2, 4, 2, 200, 64, 48, True),     # short-sequence kernels: sliding window, padding, GQA
     # grids large enough for the 4- and 2-wave workgroup variants
     (8, 16, 4, 256, 64, 0, False),    # 4 waves / workgroup, GQA 4:1
     (4, 8, 2, 500, 128, 0, True),     # 2 waves / workgroup, ragged S, padding mask
@@ -273,6 +274,39 @@ def test_attention_split(monkeypatch, per):
         assert rel_err(h(o), o_ref) < TOL
         fin = np.isfinite(lse_ref)
         assert np.array_equal(np.isfinite(h(lse)), fin)
+        assert rel_err(h(lse)[fin], lse_ref[fin]) < TOL
+        dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, True,
+                                  window, kp)
+        assert rel_err(h(dq), dq_ref) < TOL
+        assert rel_err(h(dk), dk_ref) < TOL
+        assert rel_err(h(dv), dv_ref) < TOL
+
+
+@pytest.mark.parametrize("mode", ["0", "1"])
+def test_attention_short_and_blocked_kernels(monkeypatch, mode):
+    """Each kernel family on the other's shapes: the short-sequence kernels
+    (one workgroup per 16-row tile, waves splitting the inner loop) forced
+    at S = 1024 and 333, the blocked kernels forced at GPT-2's S = 128."""
+    monkeypatch.setenv("MFT_ATTN_SHORT", mode)
+    cases = [(4, 12, 12, 128, 64, 0, False, None)] if mode == "0" else [
+        (None,) * 7 + (0,), (None,) * 7 + (2,)]
+    for case in cases:
+        if case[-1] is not None:
+            B, Hq, Hkv, S, hd, window, pad = SPLIT_CASES[case[-1]]
+            q, k, v, dout, kpad, o_ref, lse_ref, (dq_ref, dk_ref, dv_ref) = _split_case(case[-1])
+        else:
+            B, Hq, Hkv, S, hd, window, pad = case[:7]
+            q, k, v, dout = rn(B * S, Hq * hd), rn(B * S, Hkv * hd), rn(B * S, Hkv * hd), rn(B * S, Hq * hd)
+            kpad = None
+            o_ref, lse_ref = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, hd ** -0.5, True, window, kpad)
+            dq_ref, dk_ref, dv_ref = O.attn_bwd(q, k, v, o_ref, dout, lse_ref, B, Hq, Hkv, S, hd,
+                                                hd ** -0.5, True, window, kpad)
+        print(f"attention MFT_ATTN_SHORT={mode} B={B} Hq={Hq} Hkv={Hkv} S={S} hd={hd}", flush=True)
+        kp = g(kpad) if kpad is not None else None
+        scale = hd ** -0.5
+        o, lse = ops.attn_fwd(g(q), g(k), g(v), B, Hq, Hkv, S, hd, scale, True, window, kp)
+        assert rel_err(h(o), o_ref) < TOL
+        fin = np.isfinite(lse_ref)
         assert rel_err(h(lse)[fin], lse_ref[fin]) < TOL
         dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, True,
                                   window, kp)
