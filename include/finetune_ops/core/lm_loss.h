@@ -8,6 +8,7 @@
 // skipped, NLL = logsumexp(row) − row[label] summed in double; "mean"
 // divides by the number of valid targets, "sum" does not.
 #pragma once
+#include <cmath>
 #include <string>
 
 #include "finetune_ops/core/tensor.h"

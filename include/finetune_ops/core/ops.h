@@ -39,4 +39,20 @@ TensorPtr causal_attention(const TensorPtr& q, const TensorPtr& k, const TensorP
 TensorPtr reshape(const TensorPtr& x, const std::vector<int64_t>& shape);
 TensorPtr flatten(const TensorPtr& x, int start_dim, int end_dim);
 
+// Layout and analysis ops the Gemma driver applies to dumped gradients in
+// its alignment mode (gemma_3_270m_lora_finetune/src/main.cpp:626-651).
+// They return new contiguous float32 tensors computed on the GPU and record
+// no autograd node (the driver uses them on gradients, after backward()).
+// permute: out dimension i is x's dimension dims[i] (negative dims count
+// from the end).
+TensorPtr permute(const TensorPtr& x, const std::vector<int64_t>& dims);
+// Swaps two dimensions (e.g. transpose(t, -2, -1)).
+TensorPtr transpose(const TensorPtr& x, int64_t dim0, int64_t dim1);
+// [B, Hkv, S, D] → [B, Hkv·n_rep, S, D]: head h of the result is head
+// h / n_rep of x (HF repeat_kv).
+TensorPtr repeat_kv_heads(const TensorPtr& x, int n_rep);
+// Batched matrix product over the last two dimensions: a [..., M, K],
+// b [..., K, N] with equal leading dimensions (or b 2-D, shared) → [..., M, N].
+TensorPtr matmul(const TensorPtr& a, const TensorPtr& b);
+
 }  // namespace ops

@@ -74,12 +74,15 @@ class EngineModel {
  protected:
   void attach_lora(int r, float alpha, int mask);
   virtual std::string normalise_name(const std::string& name) const { return name; }
+  // Called at the end of every forward (debug dumps).
+  virtual void after_forward() {}
   void ensure_engine();
 
   EngineModelConfig ecfg_;
   int lora_r_ = 0, lora_mask_ = 0;
   float lora_alpha_ = 0.f;
   int64_t max_tokens_ = 4096;
+  int last_S_ = 0;  // sequence length of the last forward
   std::shared_ptr<EngineState> st_;
   std::vector<TensorPtr> views_, grad_views_;  // parameter / gradient views, created on demand
   std::map<std::string, TensorPtr> pending_;  // assigned before the engine exists

@@ -2,19 +2,20 @@
 //
 // Replaces the reference's GemmaTextConfig / GemmaModel / GemmaLoraSpec /
 // GemmaLoraInjector (absent), driven as GemmaTextConfig::from_pretrained(dir),
-// GemmaModel(cfg), assign_weight, GemmaLoraSpec::full_attn_mlp() /
-// attention_only() / attention_light() with target_modules, then
-// GemmaLoraInjector().inject(model, spec) (gemma_3_270m_lora_finetune/src/
-// main.cpp:326-379; target names from pytorch_alignment/
-// gemma_lora_finetune.py:144-151).  RMSNorm with (1 + w), √d embedding
+// GemmaModel(cfg), assign_weight, get_block(i), the alignment-dump hooks
+// (gemma_3_270m_lora_finetune/src/main.cpp:326-416,455-666); the LoRA spec
+// and injector are in graph/gemma_lora_injector.h.  RMSNorm with (1 + w), √d embedding
 // scale, q/k RMSNorm, GeGLU MLP, grouped KV heads, local (sliding-window,
 // rope_local_base_freq) and global layers.  Names are HF's without the
 // "model." / "language_model.model." prefixes (both accepted).
 #pragma once
+#include <memory>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "finetune_ops/graph/engine_model.h"
+#include "finetune_ops/nn/lora_linear.h"
 
 namespace ops {
 
@@ -37,36 +38,53 @@ struct GemmaTextConfig {
   static GemmaTextConfig from_pretrained(const std::string& model_dir);
 };
 
+// LoRA linears of one decoder layer, as handles on the model's own
+// parameters (frozen W and the adapter views): blk.q_proj_lora->debug_params()
+// and friends (gemma_3_270m_lora_finetune/src/main.cpp:382-416,535-537).
+// A handle without an adapter has no debug params.
+struct GemmaBlock {
+  std::shared_ptr<LoRALinear> q_proj_lora, k_proj_lora, v_proj_lora, o_proj_lora;
+  std::shared_ptr<LoRALinear> gate_proj_lora, up_proj_lora, down_proj_lora;
+};
+
 class GemmaModel : public EngineModel {
  public:
   explicit GemmaModel(const GemmaTextConfig& cfg);
   const GemmaTextConfig& config() const { return cfg_; }
+  // Gradients of intermediate activations are not kept by the fused engine;
+  // the switch is accepted for source compatibility.
   void set_debug_retain_grads(bool) {}
+  // Handles on layer i's LoRA linears (rebuilt when the adapters change).
+  GemmaBlock& get_block(int i);
+
+  // Alignment dumps (gemma_3_270m_lora_finetune/src/main.cpp:455-666).
+  // enable_debug_dump: after every later forward, the activations the engine
+  // keeps for `layers` (all when empty) are written to `dir` as float32 .npy
+  // files named <activation>_l<layer>.npy (hidden_states_emb.npy for the
+  // scaled embedding), shaped [B, S, C] without a leading batch of one.
+  void enable_debug_dump(const std::string& dir, const std::vector<int>& layers);
+  // The same activations of the last forward as tensors (views valid until
+  // the next forward), keyed as the dumps are named without ".npy".  The
+  // fused engine keeps no gradients of intermediates and never forms the
+  // [S, S] attention scores or probabilities, so those keys are absent and
+  // the tensors carry no grad().
+  std::unordered_map<std::string, TensorPtr> debug_tensors();
+  // Writes layer i's norm weights (input_layernorm, post_attention_layernorm,
+  // pre_feedforward_layernorm, post_feedforward_layernorm, q_norm, k_norm) to
+  // dir as float32 .npy files named layer<i>_<norm>.npy.
+  void dump_layer_norm_weights(int layer, const std::string& dir);
 
  protected:
   std::string normalise_name(const std::string& name) const override;
 
  private:
   GemmaTextConfig cfg_;
-};
-
-struct GemmaLoraSpec {
-  int rank = 8;
-  float alpha = 32.0f;
-  float dropout = 0.0f;
-  std::vector<std::string> target_modules;  // q_proj k_proj v_proj o_proj gate_proj up_proj down_proj
-  static GemmaLoraSpec full_attn_mlp();
-  static GemmaLoraSpec attention_only();
-  static GemmaLoraSpec attention_light();  // q_proj, v_proj
-};
-
-class GemmaLoraInjector {
- public:
-  void inject(GemmaModel& model, const GemmaLoraSpec& spec);
-  void print_info() const;
-
- private:
-  GemmaLoraSpec last_;
+  std::vector<GemmaBlock> blocks_;
+  const void* blocks_engine_ = nullptr;  // engine the handles were built on
+  std::string dump_dir_;
+  std::vector<int> dump_layers_;
+  bool dump_ = false;
+  void after_forward() override;
 };
 
 }  // namespace ops

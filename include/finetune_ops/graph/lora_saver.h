@@ -23,7 +23,7 @@
 
 #include "finetune_ops/core/tensor.h"
 #include "finetune_ops/graph/engine_model.h"
-#include "finetune_ops/graph/gemma_model.h"
+#include "finetune_ops/graph/gemma_lora_injector.h"
 #include "finetune_ops/graph/lora_injector.h"
 
 namespace ops {

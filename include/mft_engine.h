@@ -122,6 +122,21 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask,
 int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid,
                          float* grad_norm);
 
+/* Saved forward activation of the last forward, for debugging dumps (the
+ * Gemma driver's alignment mode, gemma_3_270m_lora_finetune/src/main.cpp:
+ * 455-666): device pointer to `rows` token rows of `cols` floats, rows `ld`
+ * apart; valid until the next forward or backward.  layer -1: "embed" (the
+ * scaled embedding, layer 0's input), "final_norm".  Per layer: "x" (layer
+ * input), "norm1", "q", "k", "v" (as attention reads them: after Gemma's
+ * q/k norms and RoPE), "attn" (attention output), "mid" (residual stream
+ * after the attention block), "norm2", "gate" (GPT-2: c_fc pre-activation),
+ * "up" (Qwen2/Gemma3), "act" (MLP activation), "out" (layer output); Gemma3
+ * also "q_proj", "k_proj" (before the q/k norms), "o_proj", "down_proj"
+ * (before the post-norms).  MFT_EINVAL for a name the model does not keep. */
+int mft_model_activation(mft_model m, int layer, const char* name,
+                         const float** ptr, int64_t* rows, int64_t* cols,
+                         int64_t* ld);
+
 /* ---- measurement ----------------------------------------------------------
  * When enabled, HIP events are recorded on the model's stream around every
  * launch of a kernel class; mft_model_timing returns the summed duration

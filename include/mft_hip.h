@@ -180,6 +180,19 @@ int mft_scale(mft_handle h, const float* x, int64_t n, float a, float* y);
 int mft_axpy(mft_handle h, float a, const float* x, float* y, int64_t n);
 int mft_fill(mft_handle h, float* p, int64_t n, float v);
 
+/* ---- layout ops of the operators API (not on the training path) ----------------
+ * The free functions matmul / transpose / permute / repeat_kv_heads the Gemma
+ * driver applies to dumped gradients in its alignment mode
+ * (gemma_3_270m_lora_finetune/src/main.cpp:626-651).
+ * mft_strided_copy: dst (contiguous in `shape`, ndim ≤ 8) = src read at
+ * Σ_d coord_d·src_strides[d] (elements; a stride of 0 repeats that dimension).
+ * mft_batched_matmul: C[b] = A[b]·B[b], row-major A [M,K], B [K,N], C [M,N]
+ * packed per batch entry (fp32 FMA, not the MFMA training kernels). */
+int mft_strided_copy(mft_handle h, const float* src, float* dst, int ndim,
+                     const int64_t* shape, const int64_t* src_strides);
+int mft_batched_matmul(mft_handle h, const float* A, const float* B, float* C,
+                       int batch, int M, int K, int N);
+
 /* ---- a10: support ops of the three graphs -------------------------------------
  * LayerNorm (GPT-2, γ/β frozen): saves mean/rstd [M]. */
 int mft_layernorm_fwd(mft_handle h, const float* x, const float* g,

@@ -72,6 +72,8 @@ _SIGS = {
     "mft_glu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mft_glu_bwd": (_I, [_P, _P, _P, _P, _L, _I, _P, _P]),
     "mft_rope": (_I, [_P, _P, _L, _I, _I, _I, _I, _D, _I]),
+    "mft_strided_copy": (_I, [_P, _P, _P, _I, _P, _P]),
+    "mft_batched_matmul": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "mft_embed": (_I, [_P, _P, _L, _I, _P, _L, _I, _P, _L, _F, _P, _P]),
     "mft_scale": (_I, [_P, _P, _L, _F, _P]),
     "mft_axpy": (_I, [_P, _F, _P, _P, _L]),
@@ -93,6 +95,7 @@ _SIGS = {
     "mft_model_opt_step": (_I, [_P, _F, _F, _F, _F, _F, _F]),
     "mft_model_train_step": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _F, _F, _F, _F, _F, _F, _I]),
     "mft_model_read_stats": (_I, [_P, C.POINTER(_F), C.POINTER(_L), C.POINTER(_F)]),
+    "mft_model_activation": (_I, [_P, _I, C.c_char_p, C.POINTER(_P), C.POINTER(_L), C.POINTER(_L), C.POINTER(_L)]),
     "mft_model_set_timing": (_I, [_P, _I]),
     "mft_model_timing": (_I, [_P, _I, C.POINTER(_D), C.POINTER(_D), C.POINTER(_L)]),
     "mft_model_reset_timing": (_I, [_P]),

@@ -291,6 +291,24 @@ int mft_fill(mft_handle h, float* p, int64_t n, float v) {
   });
 }
 
+int mft_strided_copy(mft_handle h, const float* src, float* dst, int ndim,
+                     const int64_t* shape, const int64_t* src_strides) {
+  return guarded([&] {
+    require_handle(h);
+    if (!src || !dst || !shape || !src_strides) throw mft::Error(MFT_EINVAL, "mft_strided_copy: null argument");
+    mft::strided_copy(h->stream, src, dst, ndim, shape, src_strides);
+  });
+}
+
+int mft_batched_matmul(mft_handle h, const float* A, const float* B, float* C,
+                       int batch, int M, int K, int N) {
+  return guarded([&] {
+    require_handle(h);
+    if (!A || !B || !C) throw mft::Error(MFT_EINVAL, "mft_batched_matmul: null argument");
+    mft::batched_matmul(h->stream, A, B, C, batch, M, K, N);
+  });
+}
+
 int mft_layernorm_fwd(mft_handle h, const float* x, const float* g,
                       const float* b, int64_t M, int64_t C, float eps,
                       float* y, float* mean, float* rstd) {

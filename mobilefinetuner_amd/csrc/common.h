@@ -330,5 +330,10 @@ void scale(hipStream_t s, const float* x, int64_t n, float a, float* y);
 void axpy(hipStream_t s, float a, const float* x, float* y, int64_t n);
 void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,
                       int32_t hi);
+// Layout ops of the operators API (off the hot path).
+constexpr int kMaxCopyDims = 8;
+void strided_copy(hipStream_t s, const float* src, float* dst, int ndim, const int64_t* shape,
+                  const int64_t* stride);
+void batched_matmul(hipStream_t s, const float* A, const float* B, float* C, int batch, int M, int K, int N);
 
 }  // namespace mft

@@ -418,6 +418,52 @@ __global__ void fill_uniform_int_kernel(int32_t* p, int64_t n, uint64_t seed,
 // kernels are grid-stride loops, so any grid is correct): one item per
 // thread keeps the most loads in flight; a capped grid that loops measured
 // 20% below the copy rate on the HBM-bound kernels.
+// ---- layout ops of the operators API (off the training hot path) ---------------
+// dst (contiguous, row-major in `shape`) = src read at Σ_d coord_d·stride_d
+// (strides in elements; 0 repeats a dimension).  Covers permute, transpose,
+// repeat_kv_heads and contiguous copies of views.
+struct StridedShape {
+  int ndim;
+  int64_t shape[kMaxCopyDims];
+  int64_t stride[kMaxCopyDims];
+};
+__global__ void strided_copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n,
+                                    StridedShape sh) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rem = i, off = 0;
+    for (int d = sh.ndim - 1; d >= 0; --d) {
+      const int64_t c = rem % sh.shape[d];
+      rem /= sh.shape[d];
+      off += c * sh.stride[d];
+    }
+    dst[i] = src[off];
+  }
+}
+
+// C[b] = A[b]·B[b] for row-major A [M,K], B [K,N], C [M,N] per batch entry
+// (batch strides M·K, K·N, M·N): 16×16 output tiles through LDS, fp32 FMA
+// (debug and analysis products; the training GEMMs use the MFMA kernels).
+__global__ __launch_bounds__(256) void batched_matmul_kernel(const float* __restrict__ A,
+                                                             const float* __restrict__ B, float* __restrict__ C,
+                                                             int M, int K, int N) {
+  __shared__ float As[16][17], Bs[16][17];
+  const int b = blockIdx.z;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
+  const float* a = A + (int64_t)b * M * K;
+  const float* bb = B + (int64_t)b * K * N;
+  float acc = 0.f;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    As[ty][tx] = row < M && k0 + tx < K ? a[(int64_t)row * K + k0 + tx] : 0.f;
+    Bs[ty][tx] = k0 + ty < K && col < N ? bb[(int64_t)(k0 + ty) * N + col] : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc = fmaf(As[ty][k], Bs[k][tx], acc);
+    __syncthreads();
+  }
+  if (row < M && col < N) C[(int64_t)b * M * N + (int64_t)row * N + col] = acc;
+}
+
 inline unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 1 << 20) {
   int64_t g = cdiv(n, per_block);
   if (g < 1) g = 1;
@@ -585,6 +631,29 @@ void fill_uniform_int(hipStream_t s, int32_t* p, int64_t n, uint64_t seed,
                       int32_t hi) {
   if (n <= 0) return;
   hipLaunchKernelGGL(fill_uniform_int_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, seed, hi);
+  MFT_LAUNCH_CHECK();
+}
+
+void strided_copy(hipStream_t s, const float* src, float* dst, int ndim, const int64_t* shape,
+                  const int64_t* stride) {
+  MFT_CHECK_ARG(ndim >= 1 && ndim <= kMaxCopyDims, "1 to 8 dimensions");
+  StridedShape sh{};
+  sh.ndim = ndim;
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) {
+    MFT_CHECK_ARG(shape[d] >= 0 && stride[d] >= 0, "negative shape or stride");
+    sh.shape[d] = shape[d];
+    sh.stride[d] = stride[d];
+    n *= shape[d];
+  }
+  if (n == 0) return;
+  hipLaunchKernelGGL(strided_copy_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n, sh);
+  MFT_LAUNCH_CHECK();
+}
+void batched_matmul(hipStream_t s, const float* A, const float* B, float* C, int batch, int M, int K, int N) {
+  MFT_CHECK_ARG(batch > 0 && M > 0 && K > 0 && N > 0, "empty matmul");
+  const dim3 grid((unsigned)cdiv(N, 16), (unsigned)cdiv(M, 16), (unsigned)batch);
+  hipLaunchKernelGGL(batched_matmul_kernel, grid, dim3(256), 0, s, A, B, C, M, K, N);
   MFT_LAUNCH_CHECK();
 }
 

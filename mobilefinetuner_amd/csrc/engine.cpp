@@ -160,6 +160,7 @@ struct mft_model_s {
   // kept (0 = none) and whether its logits buffer now holds dlogits
   int api_nseq = 0, api_S = 0;
   bool api_dlogits = false;
+  int64_t last_rows = 0;  // token rows of the last forward (activation accessor)
   // captured train-step graph
   hipStream_t cap_stream = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
@@ -825,6 +826,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
+  m->last_rows = M;
   merge_lora(m);  // A, B (or W) may have changed since the last forward
   embed(s, ids, M, S, E.data, c.vocab, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
         gemma ? std::sqrt((float)d) : 1.f, m->A[0].x, m->d_err);
@@ -1464,6 +1466,53 @@ int mft_model_read_stats(mft_model m, float* mean_loss, int64_t* n_valid, float*
                                   (err[1] ? "a label outside [0, vocab) other than ignore_index was treated as ignored"
                                           : ""));
     }
+  });
+}
+
+int mft_model_activation(mft_model m, int layer, const char* name, const float** ptr, int64_t* rows,
+                         int64_t* cols, int64_t* ld) {
+  return guarded([&] {
+    if (!m || !name || !ptr) throw Error(MFT_EINVAL, "null argument");
+    if (m->last_rows == 0) throw Error(MFT_EINVAL, "mft_model_activation: no forward has run");
+    const mft_model_cfg& c = m->c;
+    const std::string n = name;
+    const int64_t d = c.d, hq = (int64_t)c.n_head * c.head_dim, hk = (int64_t)c.n_kv_head * c.head_dim;
+    const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
+    const float* p = nullptr;
+    int64_t w = 0, pitch = 0;
+    auto set = [&](const float* q, int64_t width, int64_t l) {
+      p = q;
+      w = width;
+      pitch = l;
+    };
+    if (layer < 0) {
+      if (n == "embed") set(m->A[0].x, d, d);
+      else if (n == "final_norm") set(m->hf, d, d);
+    } else {
+      if (layer >= c.n_layer) throw Error(MFT_EINVAL, "mft_model_activation: layer out of range");
+      const Acts& a = m->A[layer];
+      if (n == "x") set(a.x, d, d);
+      else if (n == "norm1") set(a.n1, d, d);
+      else if (n == "q") set(a.q, hq, a.qs);
+      else if (n == "k") set(a.k, hk, a.ks);
+      else if (n == "v") set(a.v, hk, a.vs);
+      else if (n == "q_proj" && gemma) set(a.qraw, hq, m->fuse_qkv ? m->nqkv : hq);
+      else if (n == "k_proj" && gemma) set(a.kraw, hk, m->fuse_qkv ? m->nqkv : hk);
+      else if (n == "attn") set(a.att, hq, hq);
+      else if (n == "o_proj" && gemma) set(a.o, d, d);
+      else if (n == "mid") set(a.hmid, d, d);
+      else if (n == "norm2") set(a.n2, d, d);
+      else if (n == "gate") set(a.gate, c.d_ff, c.d_ff);
+      else if (n == "up" && !gpt2) set(a.up, c.d_ff, c.d_ff);
+      else if (n == "act") set(a.act, c.d_ff, c.d_ff);
+      else if (n == "down_proj" && gemma) set(a.mo, d, d);
+      else if (n == "out") set(layer + 1 < c.n_layer ? m->A[layer + 1].x : m->h_final, d, d);
+    }
+    if (!p) throw Error(MFT_EINVAL, "mft_model_activation: this model keeps no activation '" + n + "'");
+    *ptr = p;
+    if (rows) *rows = m->last_rows;
+    if (cols) *cols = w;
+    if (ld) *ld = pitch;
   });
 }
 

@@ -12,6 +12,8 @@
 #include <functional>
 #include <stdexcept>
 #include <string>
+#include <sys/stat.h>
+
 #include <unordered_map>
 #include <unordered_set>
 
@@ -513,6 +515,111 @@ TensorPtr flatten(const TensorPtr& x, int start_dim, int end_dim) {
   return reshape(x, s);
 }
 
+// ------------------------------------------------------- layout / analysis --
+
+namespace {
+
+// Contiguous float32 input for the layout ops (views with a row pitch are
+// gathered first).
+TensorPtr dense_f32(const TensorPtr& x, const char* what) {
+  if (!x || x->dtype() != kFloat32) throw std::invalid_argument(std::string(what) + ": float32 tensor required");
+  if (x->contiguous()) return x;
+  const int64_t rows = x->numel() / (x->shape().empty() ? 1 : x->shape().back());
+  const int64_t shape[2] = {rows, x->shape().back()};
+  const int64_t stride[2] = {x->pitch(), 1};
+  auto out = new_f32(x->shape());
+  mft_check(mft_strided_copy(detail::handle(), fptr(x), static_cast<float*>(out->device_data()), 2, shape, stride),
+            "mft_strided_copy");
+  return out;
+}
+
+int64_t norm_dim(int64_t d, int64_t nd, const char* what) {
+  if (d < 0) d += nd;
+  if (d < 0 || d >= nd) throw std::invalid_argument(std::string(what) + ": dimension out of range");
+  return d;
+}
+
+std::vector<int64_t> contiguous_strides(const std::vector<int64_t>& shape) {
+  std::vector<int64_t> st(shape.size(), 1);
+  for (int64_t i = (int64_t)shape.size() - 2; i >= 0; --i) st[i] = st[i + 1] * shape[i + 1];
+  return st;
+}
+
+TensorPtr gather(const TensorPtr& src, const std::vector<int64_t>& out_shape, const std::vector<int64_t>& strides,
+                 const char* what) {
+  if (out_shape.size() > 8) throw std::invalid_argument(std::string(what) + ": at most 8 dimensions");
+  auto out = new_f32(out_shape);
+  if (out->numel() == 0) return out;
+  mft_check(mft_strided_copy(detail::handle(), fptr(src), static_cast<float*>(out->device_data()),
+                             (int)out_shape.size(), out_shape.data(), strides.data()),
+            "mft_strided_copy");
+  return out;
+}
+
+}  // namespace
+
+TensorPtr permute(const TensorPtr& x0, const std::vector<int64_t>& dims) {
+  auto x = dense_f32(x0, "permute");
+  const int64_t nd = x->dim();
+  if ((int64_t)dims.size() != nd) throw std::invalid_argument("permute: one entry per dimension required");
+  const auto in_st = contiguous_strides(x->shape());
+  std::vector<int64_t> shape(nd), st(nd);
+  std::vector<bool> seen(nd, false);
+  for (int64_t i = 0; i < nd; ++i) {
+    const int64_t d = norm_dim(dims[i], nd, "permute");
+    if (seen[d]) throw std::invalid_argument("permute: repeated dimension");
+    seen[d] = true;
+    shape[i] = x->shape()[d];
+    st[i] = in_st[d];
+  }
+  return gather(x, shape, st, "permute");
+}
+
+TensorPtr transpose(const TensorPtr& x, int64_t dim0, int64_t dim1) {
+  const int64_t nd = x ? x->dim() : 0;
+  std::vector<int64_t> dims(nd);
+  for (int64_t i = 0; i < nd; ++i) dims[i] = i;
+  std::swap(dims[norm_dim(dim0, nd, "transpose")], dims[norm_dim(dim1, nd, "transpose")]);
+  return permute(x, dims);
+}
+
+TensorPtr repeat_kv_heads(const TensorPtr& x0, int n_rep) {
+  auto x = dense_f32(x0, "repeat_kv_heads");
+  if (x->dim() != 4 || n_rep < 1) throw std::invalid_argument("repeat_kv_heads: [B, H, S, D] and n_rep >= 1 required");
+  const auto& s = x->shape();
+  const auto in_st = contiguous_strides(s);
+  // result viewed as [B, H, n_rep, S, D] with a zero stride on the repeat
+  auto out = gather(x, {s[0], s[1], n_rep, s[2], s[3]}, {in_st[0], in_st[1], 0, in_st[2], in_st[3]},
+                    "repeat_kv_heads");
+  return reshape(out, {s[0], s[1] * n_rep, s[2], s[3]});
+}
+
+TensorPtr matmul(const TensorPtr& a0, const TensorPtr& b0) {
+  auto a = dense_f32(a0, "matmul");
+  auto b = dense_f32(b0, "matmul");
+  if (a->dim() < 2 || b->dim() < 2) throw std::invalid_argument("matmul: operands need at least 2 dimensions");
+  const int64_t M = a->shape()[a->dim() - 2], K = a->shape()[a->dim() - 1];
+  const int64_t K2 = b->shape()[b->dim() - 2], N = b->shape()[b->dim() - 1];
+  if (K != K2) throw std::invalid_argument("matmul: inner dimensions differ");
+  const int64_t batch = a->numel() / std::max<int64_t>(1, M * K);
+  const int64_t bbatch = b->numel() / std::max<int64_t>(1, K * N);
+  if (bbatch != batch && !(b->dim() == 2))
+    throw std::invalid_argument("matmul: leading dimensions of a and b must match (or b be 2-D)");
+  std::vector<int64_t> shape(a->shape().begin(), a->shape().end() - 2);
+  shape.push_back(M);
+  shape.push_back(N);
+  auto out = new_f32(shape);
+  if (out->numel() == 0) return out;
+  TensorPtr bb = b;
+  if (b->dim() == 2 && batch > 1) {  // one shared right operand, repeated per batch entry
+    bb = gather(b, {batch, K, N}, {0, N, 1}, "matmul");
+  }
+  mft_check(mft_batched_matmul(detail::handle(), fptr(a), fptr(bb), static_cast<float*>(out->device_data()),
+                               (int)batch, (int)M, (int)K, (int)N),
+            "mft_batched_matmul");
+  return out;
+}
+
 // ----------------------------------------------------------------- loss --
 
 namespace {
@@ -562,6 +669,40 @@ void check_labels(const TensorPtr& labels, int64_t vocab, int ignore_index, cons
       throw std::invalid_argument(std::string(what) + ": label " + std::to_string(p[i]) + " at position " +
                                   std::to_string(i) + " is outside [0, " + std::to_string(vocab) +
                                   ") and is not ignore_index");
+}
+
+void make_parent_dirs(const std::string& path) {
+  const size_t slash = path.find_last_of('/');
+  if (slash == std::string::npos || slash == 0) return;
+  const std::string dir = path.substr(0, slash);
+  for (size_t i = 1; i <= dir.size(); ++i)
+    if (i == dir.size() || dir[i] == '/') (void)::mkdir(dir.substr(0, i).c_str(), 0755);
+}
+
+void write_npy(const std::string& path, const void* data, const std::vector<int64_t>& shape, bool int32) {
+  make_parent_dirs(path);
+  std::string dict = std::string("{'descr': '") + (int32 ? "<i4" : "<f4") + "', 'fortran_order': False, 'shape': (";
+  int64_t n = 1;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    dict += std::to_string(shape[i]) + (shape.size() == 1 || i + 1 < shape.size() ? "," : "");
+    if (i + 1 < shape.size()) dict += " ";
+    n *= shape[i];
+  }
+  dict += "), }";
+  // magic (6) + version (2) + header length (2) + header, padded with spaces
+  // and a newline to a multiple of 64 bytes
+  const size_t total = 10 + dict.size() + 1;
+  dict += std::string((64 - total % 64) % 64, ' ') + "\n";
+  std::ofstream f(path, std::ios::binary);
+  if (!f) throw std::runtime_error("write_npy: cannot open " + path);
+  const char magic[8] = {'\x93', 'N', 'U', 'M', 'P', 'Y', 1, 0};
+  f.write(magic, 8);
+  const uint16_t hl = (uint16_t)dict.size();
+  const char hb[2] = {(char)(hl & 0xff), (char)(hl >> 8)};
+  f.write(hb, 2);
+  f.write(dict.data(), (std::streamsize)dict.size());
+  f.write(static_cast<const char*>(data), (std::streamsize)(n * 4));
+  if (!f) throw std::runtime_error("write_npy: write failed for " + path);
 }
 
 bool parse_reduction(const std::string& r) {

@@ -29,6 +29,11 @@ ModelLoss model_loss_hook(const TensorPtr& logits);
 // every label in [0, vocab) or equal to ignore_index.  Throws
 // std::invalid_argument naming the first offender.
 void check_ids(const TensorPtr& ids, int64_t vocab, const char* what);
+// Creates the parent directories of a file path (mkdir -p).
+void make_parent_dirs(const std::string& path);
+// Writes a row-major array as a NumPy .npy file (format 1.0, little
+// endian): descr "<f4" or "<i4"; creates the parent directory.
+void write_npy(const std::string& path, const void* data, const std::vector<int64_t>& shape, bool int32);
 void check_labels(const TensorPtr& labels, int64_t vocab, int ignore_index, const char* what);
 
 }  // namespace detail

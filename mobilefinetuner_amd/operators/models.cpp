@@ -3,6 +3,7 @@
 // that joins lm_cross_entropy on a model's logits to the engine's backward.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <fstream>
@@ -12,7 +13,7 @@
 #include <unordered_map>
 
 #include "finetune_ops/core/autograd_engine.h"
-#include "finetune_ops/graph/gemma_model.h"
+#include "finetune_ops/graph/gemma_lora_injector.h"
 #include "finetune_ops/graph/gpt2_model.h"
 #include "finetune_ops/graph/lora_injector.h"
 #include "finetune_ops/graph/qwen_model.h"
@@ -82,6 +83,7 @@ void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int 
 struct ModelLossNode : autograd::Node {
   std::shared_ptr<EngineState> st;
   LogitsCtx ctx;
+  std::weak_ptr<Tensor> logits;
   TensorPtr labels;
   int ignore = -100;
   bool sum = false;
@@ -93,6 +95,19 @@ struct ModelLossNode : autograd::Node {
     double ls;
     int64_t nv;
     model_ce(st.get(), ctx, labels, ignore, up, sum, true, &ls, &nv);
+    // logits->retain_grad(): the gradient the CE just wrote over the logits
+    // buffer is copied out before the backward consumes it
+    if (auto lg = logits.lock())
+      if (lg->retains_grad()) {
+        float* dl = nullptr;
+        int64_t ld = 0;
+        mft_check(mft_model_logits(st->m, &dl, &ld), "mft_model_logits");
+        const int64_t V = lg->shape().back(), rows = lg->numel() / V;
+        auto g = std::make_shared<Tensor>(lg->shape(), kFloat32, kGPU);
+        hip_check(hipMemcpy2D(g->device_data(), V * 4, dl, ld * 4, V * 4, rows, hipMemcpyDeviceToDevice),
+                  "hipMemcpy2D");
+        autograd::accumulate_grad(lg, g);
+      }
     mft_check(mft_model_backward(st->m, ctx.mask ? static_cast<const float*>(ctx.mask->device_data()) : nullptr, ctx.B,
                                  ctx.S),
               "mft_model_backward");
@@ -128,6 +143,7 @@ ModelLoss model_loss_hook(const TensorPtr& logits) {
       n->labels = labels;
       n->ignore = ignore;
       n->sum = sum;
+      n->logits = logits;
       for (size_t i = 0; i < st->recs.size(); ++i)
         if (st->recs[i].trainable)
           if (auto v = st->views[i].lock()) n->inputs.push_back(v);
@@ -322,6 +338,7 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
                                     mask ? static_cast<const float*>(mask->device_data()) : nullptr, B, S),
             "mft_model_forward_train");
   st_->generation++;
+  last_S_ = S;
   float* lg = nullptr;
   int64_t ld = 0;
   mft_check(mft_model_logits(st_->m, &lg, &ld), "mft_model_logits");
@@ -338,6 +355,7 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
   for (auto it = reg.begin(); it != reg.end();)  // drop entries of earlier forwards
     it = it->second.st.lock() == st_ || it->second.st.expired() ? reg.erase(it) : std::next(it);
   reg[logits.get()] = ctx;
+  after_forward();
   return logits;
 }
 
@@ -636,6 +654,93 @@ std::string GemmaModel::normalise_name(const std::string& raw) const {
   if (!strip(n, "language_model.model.")) strip(n, "model.");
   if (n == "lm_head.weight") return "";
   return n;
+}
+
+GemmaBlock& GemmaModel::get_block(int i) {
+  if (i < 0 || i >= cfg_.num_hidden_layers) throw std::out_of_range("get_block: layer index");
+  ensure_engine();
+  if (blocks_engine_ != st_.get() || blocks_.empty()) {
+    blocks_.assign(cfg_.num_hidden_layers, GemmaBlock{});
+    for (int l = 0; l < cfg_.num_hidden_layers; ++l) {
+      GemmaBlock& b = blocks_[l];
+      std::shared_ptr<LoRALinear>* slots[7] = {&b.q_proj_lora,    &b.k_proj_lora,  &b.v_proj_lora,
+                                               &b.o_proj_lora,    &b.gate_proj_lora, &b.up_proj_lora,
+                                               &b.down_proj_lora};
+      for (int t = 0; t < 7; ++t) {
+        const std::string mod = std::string("layers.") + std::to_string(l) +
+                                (t < 4 ? ".self_attn." : ".mlp.") + kGemmaTargets[t];
+        auto lin = std::make_shared<LoRALinear>(get_parameter(mod + ".weight"), nullptr);
+        lin->set_name(mod);
+        if (has_lora() && ((lora_mask() >> t) & 1))
+          lin->attach_lora(get_parameter(mod + ".lora_A"), get_parameter(mod + ".lora_B"), lora_alpha());
+        *slots[t] = lin;
+      }
+    }
+    blocks_engine_ = st_.get();
+  }
+  return blocks_[i];
+}
+
+namespace {
+// (dump name, engine activation name) pairs of a Gemma layer.
+const char* const kGemmaDumps[][2] = {
+    {"hidden_before_attn", "x"},     {"hidden_after_attn_norm", "norm1"}, {"q_proj_out", "q_proj"},
+    {"k_proj_out", "k_proj"},        {"v_proj_out", "v"},                 {"q_rotary_out", "q"},
+    {"k_rotary_out", "k"},           {"attn_context", "attn"},           {"attn_out_raw", "o_proj"},
+    {"hidden_after_attn", "mid"},    {"hidden_before_mlp_norm", "mid"},  {"hidden_after_mlp_norm", "norm2"},
+    {"gate_proj_out", "gate"},       {"up_proj_out", "up"},              {"mlp_prod", "act"},
+    {"down_proj_out", "down_proj"},  {"hidden_after_mlp", "out"}};
+}  // namespace
+
+std::unordered_map<std::string, TensorPtr> GemmaModel::debug_tensors() {
+  std::unordered_map<std::string, TensorPtr> out;
+  if (!st_) return out;
+  const float* p = nullptr;
+  int64_t rows = 0, cols = 0, ld = 0;
+  auto add = [&](const std::string& key, int layer, const char* act) {
+    if (mft_model_activation(st_->m, layer, act, &p, &rows, &cols, &ld) != 0) return;
+    const int64_t S = last_S_ > 0 ? last_S_ : rows;
+    out[key] = Tensor::view({rows / S, S, cols}, kFloat32, const_cast<float*>(p), ld, st_);
+  };
+  add("hidden_states_emb", -1, "embed");
+  for (int l = 0; l < cfg_.num_hidden_layers; ++l) {
+    if (!dump_layers_.empty() && std::find(dump_layers_.begin(), dump_layers_.end(), l) == dump_layers_.end())
+      continue;
+    for (const auto& d : kGemmaDumps) add(std::string(d[0]) + "_l" + std::to_string(l), l, d[1]);
+  }
+  return out;
+}
+
+void GemmaModel::enable_debug_dump(const std::string& dir, const std::vector<int>& layers) {
+  dump_dir_ = dir;
+  dump_layers_ = layers;
+  dump_ = true;
+}
+
+void GemmaModel::after_forward() {
+  if (!dump_) return;
+  for (auto& kv : debug_tensors()) {
+    const TensorPtr& t = kv.second;
+    std::vector<int64_t> shp = t->shape();
+    if (!shp.empty() && shp[0] == 1) shp.erase(shp.begin());
+    detail::write_npy(dump_dir_ + "/" + kv.first + ".npy", t->data<float>(), shp, false);
+  }
+}
+
+void GemmaModel::dump_layer_norm_weights(int layer, const std::string& dir) {
+  if (layer < 0 || layer >= cfg_.num_hidden_layers) throw std::out_of_range("dump_layer_norm_weights: layer index");
+  static const char* const kNorms[6] = {"input_layernorm",           "post_attention_layernorm",
+                                        "pre_feedforward_layernorm", "post_feedforward_layernorm",
+                                        "self_attn.q_norm",          "self_attn.k_norm"};
+  for (const char* n : kNorms) {
+    const std::string name = "layers." + std::to_string(layer) + "." + n + ".weight";
+    auto t = get_parameter(name);
+    std::string file = n;
+    const size_t dot = file.find('.');
+    if (dot != std::string::npos) file = file.substr(dot + 1);
+    detail::write_npy(dir + "/layer" + std::to_string(layer) + "_" + file + ".npy", t->data<float>(), t->shape(),
+                      false);
+  }
 }
 
 GemmaLoraSpec GemmaLoraSpec::full_attn_mlp() {

@@ -13,7 +13,9 @@
 // loss and gradients ≤ 1e-4 relative L2, parameters after Adam ≤ 1e-5.
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
+#include <fstream>
 #include <cstdio>
 #include <cstring>
 #include <filesystem>
@@ -27,13 +29,14 @@
 #include "finetune_ops/core/lm_loss.h"
 #include "finetune_ops/core/memory_manager.h"
 #include "finetune_ops/core/ops.h"
-#include "finetune_ops/graph/gemma_model.h"
+#include "finetune_ops/graph/gemma_lora_injector.h"
 #include "finetune_ops/graph/gpt2_model.h"
 #include "finetune_ops/graph/lora_injector.h"
 #include "finetune_ops/graph/lora_saver.h"
 #include "finetune_ops/graph/qwen_model.h"
 #include "finetune_ops/graph/safetensors_loader.h"
 #include "finetune_ops/optim/adam.h"
+#include "finetune_ops/optim/gemma_trainer.h"
 #include "oracle.h"
 
 using namespace ops;
@@ -422,6 +425,257 @@ static void test_gemma(bool fp16) {
   orc_model_destroy(om);
 }
 
+// A tiny Gemma-3 config shared by the trainer and debug-API tests.
+static GemmaTextConfig tiny_gemma() {
+  GemmaTextConfig cfg;
+  cfg.vocab_size = 89;
+  cfg.hidden_size = 64;
+  cfg.intermediate_size = 96;
+  cfg.num_hidden_layers = 3;
+  cfg.num_attention_heads = 4;
+  cfg.num_key_value_heads = 1;
+  cfg.head_dim = 64;
+  cfg.max_position_embeddings = 64;
+  cfg.sliding_window = 5;
+  cfg.sliding_window_pattern = 3;
+  cfg.rms_norm_eps = 1e-6f;
+  cfg.rope_theta = 1e6;
+  cfg.rope_local_base_freq = 1e4;
+  cfg.query_pre_attn_scalar = 16.f;
+  return cfg;
+}
+
+static orc_model* tiny_gemma_oracle(int lora_mask) {
+  orc_model_cfg oc{};
+  oc.arch = ORC_GEMMA3;
+  oc.n_layer = 3;
+  oc.d = 64;
+  oc.n_head = 4;
+  oc.n_kv_head = 1;
+  oc.head_dim = 64;
+  oc.d_ff = 96;
+  oc.max_pos = 64;
+  oc.vocab = 89;
+  oc.lora_r = 8;
+  oc.lora_alpha = 32.f;
+  oc.lora_mask = lora_mask;
+  oc.norm_eps = 1e-6f;
+  oc.rope_theta = 1e6;
+  oc.rope_local_theta = 1e4;
+  oc.sliding_pattern = 3;
+  oc.sliding_window = 5;
+  oc.attn_scale = 1.f / std::sqrt(16.f);
+  return orc_model_create(&oc);
+}
+
+// A dataset with the reference data layer's interface over a fixed pool of
+// seeded sequences (the trainer binds any such type).
+struct SyntheticLM {
+  struct Batch {
+    TensorPtr input_ids, attention_mask, labels;
+  };
+  int S = 12, V = 89;
+  std::vector<std::vector<int32_t>> seqs;
+  size_t cursor = 0;
+  SyntheticLM(int n, uint64_t seed) {
+    std::mt19937_64 rng(seed);
+    for (int i = 0; i < n; ++i) {
+      std::vector<int32_t> s(S);
+      for (auto& t : s) t = (int32_t)(rng() % V);
+      seqs.push_back(s);
+    }
+  }
+  size_t num_sequences() const { return seqs.size(); }
+  void reset_cursor() { cursor = 0; }
+  // the sequences of the next batch, as the trainer will see them
+  std::vector<int32_t> take(int bs, bool loop) {
+    std::vector<int32_t> ids;
+    for (int b = 0; b < bs; ++b) {
+      if (cursor >= seqs.size()) {
+        if (!loop) return {};
+        cursor = 0;
+      }
+      ids.insert(ids.end(), seqs[cursor].begin(), seqs[cursor].end());
+      ++cursor;
+    }
+    return ids;
+  }
+  Batch next_batch(int bs, bool loop) {
+    auto ids = take(bs, loop);
+    if (ids.empty()) return {};
+    std::vector<float> mask(ids.size(), 1.f);
+    Batch b;
+    b.input_ids = std::make_shared<Tensor>(std::vector<int64_t>{bs, S}, ids.data(), kInt32, kCPU);
+    b.attention_mask = std::make_shared<Tensor>(std::vector<int64_t>{bs, S}, mask.data(), kFloat32, kCPU);
+    b.labels = std::make_shared<Tensor>(std::vector<int64_t>{bs, S}, ids.data(), kInt32, kCPU);
+    return b;
+  }
+};
+
+// GemmaLoRATrainer against the oracle driven through the same schedule:
+// 10 sequences, micro-batch 2, grad_accum 2, one epoch → 3 steps, warmup
+// int(3·0.34) = 1, linear decay, clip 0.5, AdamW with weight decay 0.01.
+static void test_gemma_trainer() {
+  const GemmaTextConfig cfg = tiny_gemma();
+  GemmaModel model(cfg);
+  GemmaLoraInjector injector;
+  injector.inject(model, GemmaLoraSpec::full_attn_mlp());
+  orc_model* om = tiny_gemma_oracle(0x7f);
+  init_both(model, om, 21);
+  SyntheticLM train(10, 5), eval(4, 6);
+  GemmaTrainerConfig tc;
+  tc.learning_rate = 1e-3f;
+  tc.num_epochs = 1;
+  tc.micro_batch_size = 2;
+  tc.grad_accum_steps = 2;
+  tc.warmup_ratio = 0.34f;
+  tc.max_grad_norm = 0.5f;
+  tc.weight_decay = 0.01f;
+  tc.eval_steps = 3;
+  tc.eval_batches = 2;
+  tc.output_dir = "/tmp/mft_trainer_test";
+  GemmaLoRATrainer trainer(model, injector, train, eval, tc);
+  check("gemma trainer total steps", std::abs(trainer.total_steps() - 3), 0);
+  check("gemma trainer warmup steps", std::abs(trainer.warmup_steps() - 1), 0);
+  const float want_lr[3] = {1e-3f, 5e-4f, 0.f};  // warmup 1/1, then decay over 2 steps
+  for (int s = 1; s <= 3; ++s) check("gemma trainer lr step" + std::to_string(s), std::abs(trainer.lr_at(s) - want_lr[s - 1]), 1e-9);
+  trainer.train();
+  const auto& hist = trainer.history();
+  check("gemma trainer ran 3 steps", std::abs((int)hist.size() - 3), 0);
+  // oracle replay
+  SyntheticLM replay(10, 5);
+  std::vector<float> mask(2 * 12, 1.f);
+  for (int step = 1; step <= 3 && step <= (int)hist.size(); ++step) {
+    double loss = 0;
+    for (int a = 0; a < 2; ++a) {
+      auto ids = replay.take(2, true);
+      loss += orc_model_fwd_bwd(om, ids.data(), mask.data(), ids.data(), 2, 12, 0.5f);
+    }
+    // the oracle returns the norm after clipping (clip_and_get_grad_norm's
+    // value); the trainer logs the norm before it
+    const float norm = orc_model_opt_step(om, trainer.lr_at(step), 0.9f, 0.999f, 1e-8f, 0.01f, 0.5f);
+    const float clipped = std::min(hist[step - 1].grad_norm, 0.5f);
+    check("gemma trainer step" + std::to_string(step) + " loss", std::abs(hist[step - 1].loss - loss / 2) / (loss / 2), 1e-4);
+    check("gemma trainer step" + std::to_string(step) + " clipped grad norm", std::abs(clipped - norm) / norm, 1e-4);
+  }
+  // parameters after the three AdamW steps
+  std::vector<float> got, want;
+  for (auto& name : model.parameter_names()) {
+    if (name.find(".lora_") == std::string::npos) continue;
+    auto t = model.get_parameter(name);
+    const float* g = static_cast<const Tensor&>(*t).data<float>();
+    const float* o = static_cast<const float*>(orc_model_param_data(om, oracle_index(om, name)));
+    got.insert(got.end(), g, g + t->numel());
+    want.insert(want.end(), o, o + t->numel());
+  }
+  check("gemma trainer LoRA params after 3 steps", rel_l2(got.data(), want.data(), (int64_t)got.size()), 1e-5);
+  trainer.save_lora(tc.output_dir + "/gemma_lora.safetensors");
+  std::ifstream saved(tc.output_dir + "/gemma_lora.safetensors", std::ios::binary);
+  check("gemma trainer adapter written", saved.good() ? 0.0 : 1.0, 0);
+  orc_model_destroy(om);
+}
+
+// The Gemma driver's alignment-mode API: block handles and debug_params,
+// dumps, dlogits through retain_grad, and the layout ops it applies.
+static void test_gemma_debug_api() {
+  const GemmaTextConfig cfg = tiny_gemma();
+  GemmaModel model(cfg);
+  GemmaLoraInjector injector;
+  injector.inject(model, GemmaLoraSpec::attention_only());
+  orc_model* om = tiny_gemma_oracle(0x0f);
+  init_both(model, om, 22);
+  auto& blk = model.get_block(1);
+  auto dp = blk.q_proj_lora->debug_params();
+  check("gemma debug_params names", dp.size() == 2 && dp[0].first == "layers_1_self_attn_q_proj_lora_A_weight" &&
+                                            dp[1].first == "layers_1_self_attn_q_proj_lora_B_weight" ? 0.0 : 1.0, 0);
+  check("gemma no adapter on gate_proj", blk.gate_proj_lora->debug_params().empty() ? 0.0 : 1.0, 0);
+  // a host write through the handle reaches the model (the align mode's LoRA-A load)
+  auto A = dp[0].second;
+  float* a = A->data<float>();
+  for (int64_t i = 0; i < A->numel(); ++i) a[i] = 0.01f * (float)((i % 7) - 3);
+  const float* back = static_cast<const Tensor&>(*model.get_parameter("layers.1.self_attn.q_proj.lora_A")).data<float>();
+  check("gemma debug_params write-through", std::abs(back[5] - 0.01f * 2.f), 0);
+  const std::string dir = "/tmp/mft_align_dump";
+  model.enable_debug_dump(dir, {0, 2});
+  model.dump_layer_norm_weights(0, dir);
+  std::vector<int32_t> ids(12);
+  for (int i = 0; i < 12; ++i) ids[i] = (i * 37 + 5) % 89;
+  auto tids = std::make_shared<Tensor>(std::vector<int64_t>{1, 12}, ids.data(), kInt32, kCPU);
+  auto logits = model.forward(tids, nullptr);
+  logits->set_requires_grad(true);
+  logits->retain_grad();
+  std::vector<float> lg(static_cast<const Tensor&>(*logits).data<float>(),
+                        static_cast<const Tensor&>(*logits).data<float>() + 12 * 89);
+  auto loss = lm_cross_entropy(logits, tids, -100, "mean");
+  loss->backward();
+  std::vector<float> dl_ref(12 * 89), nll(12);
+  double ls = 0;
+  orc_ce_fwd_bwd(lg.data(), ids.data(), 1, 12, 89, -100, 1.f, 0, &ls, dl_ref.data(), nll.data());
+  check("gemma retain_grad dlogits", logits->grad() ? rel_l2(logits->grad()->data<float>(), dl_ref.data(), 12 * 89) : 1.0, 1e-5);
+  auto dbg = model.debug_tensors();
+  check("gemma debug tensors present",
+        dbg.count("q_rotary_out_l0") && dbg.count("attn_context_l2") && dbg.count("hidden_states_emb") &&
+                !dbg.count("attn_scores_l0") && !dbg.count("q_rotary_out_l1") ? 0.0 : 1.0, 0);
+  for (const char* f : {"/hidden_states_emb.npy", "/q_rotary_out_l0.npy", "/mlp_prod_l2.npy", "/layer0_q_norm.npy"}) {
+    std::ifstream in(dir + f, std::ios::binary);
+    char magic[6] = {0};
+    in.read(magic, 6);
+    check(std::string("gemma dump ") + f, in.good() && magic[1] == 'N' && magic[5] == 'Y' ? 0.0 : 1.0, 0);
+  }
+  // hidden_states_emb = E[ids]·sqrt(d), against the frozen table
+  {
+    auto emb = dbg["hidden_states_emb"];
+    const float* e = static_cast<const Tensor&>(*emb).data<float>();
+    const float* E = static_cast<const Tensor&>(*model.get_parameter("embed_tokens.weight")).data<float>();
+    std::vector<float> want(12 * 64);
+    for (int t = 0; t < 12; ++t)
+      for (int c = 0; c < 64; ++c) want[t * 64 + c] = E[ids[t] * 64 + c] * std::sqrt(64.f);
+    check("gemma hidden_states_emb", rel_l2(e, want.data(), 12 * 64), 1e-6);
+  }
+  // layout ops against host loops
+  std::vector<float> x(2 * 3 * 4 * 5);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i * 0.5f - 7.f;
+  auto tx = std::make_shared<Tensor>(std::vector<int64_t>{2, 3, 4, 5}, x.data(), kFloat32, kCPU);
+  auto tp = permute(tx, {0, 2, 1, 3});
+  auto tt = transpose(tx, -2, -1);
+  auto tr = repeat_kv_heads(tx, 2);
+  auto y = std::make_shared<Tensor>(std::vector<int64_t>{2, 3, 5, 6}, x.data(), kFloat32, kCPU);  // reuse values
+  std::vector<float> yv(2 * 3 * 5 * 6);
+  for (size_t i = 0; i < yv.size(); ++i) yv[i] = std::sin((float)i);
+  y = std::make_shared<Tensor>(std::vector<int64_t>{2, 3, 5, 6}, yv.data(), kFloat32, kCPU);
+  auto mm = matmul(tx, y);
+  double e_p = 0, e_t = 0, e_r = 0, e_m = 0;
+  const float* pp = tp->data<float>();
+  const float* pt = tt->data<float>();
+  const float* pr = tr->data<float>();
+  const float* pm = mm->data<float>();
+  for (int b = 0; b < 2; ++b)
+    for (int h = 0; h < 3; ++h)
+      for (int s2 = 0; s2 < 4; ++s2)
+        for (int d = 0; d < 5; ++d) {
+          const float v = x[((b * 3 + h) * 4 + s2) * 5 + d];
+          e_p += std::abs(pp[((b * 4 + s2) * 3 + h) * 5 + d] - v);
+          e_t += std::abs(pt[((b * 3 + h) * 5 + d) * 4 + s2] - v);
+          for (int r = 0; r < 2; ++r) e_r += std::abs(pr[((b * 6 + h * 2 + r) * 4 + s2) * 5 + d] - v);
+        }
+  for (int b = 0; b < 2; ++b)
+    for (int h = 0; h < 3; ++h)
+      for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 6; ++j) {
+          double acc = 0;
+          for (int k = 0; k < 5; ++k) acc += (double)x[((b * 3 + h) * 4 + i) * 5 + k] * yv[((b * 3 + h) * 5 + k) * 6 + j];
+          e_m += std::abs(pm[((b * 3 + h) * 4 + i) * 6 + j] - acc) / (1 + std::abs(acc));
+        }
+  check("layout permute", e_p, 0);
+  check("layout transpose", e_t, 0);
+  check("layout repeat_kv_heads", e_r, 0);
+  check("layout matmul", e_m, 1e-4);
+  check("layout shapes", tp->shape() == std::vector<int64_t>{2, 4, 3, 5} && tt->shape() == std::vector<int64_t>{2, 3, 5, 4} &&
+                             tr->shape() == std::vector<int64_t>{2, 6, 4, 5} && mm->shape() == std::vector<int64_t>{2, 3, 4, 6}
+                         ? 0.0 : 1.0, 0);
+  orc_model_destroy(om);
+}
+
 // lora_linear → causal_attention (q, k, v views of one projection output) →
 // lm_cross_entropy, backward to x, A, B; against the oracle's functions.
 static void test_ops_chain() {
@@ -510,6 +764,8 @@ int main() {
     test_qwen();
     test_gemma(false);
     test_gemma(true);
+    test_gemma_trainer();
+    test_gemma_debug_api();
     MemoryManager::instance().force_cleanup();
   } catch (const std::exception& e) {
     std::printf("FAIL exception: %s\n", e.what());
