@@ -66,6 +66,14 @@ class EngineModel {
   // Qwen2 / Gemma3: bits 0..6 q, k, v, o, gate, up, down); frozen weights
   // carry over, and mask 0 or r 0 removes the adapters.
   void set_lora(int rank, float alpha, int target_mask) { attach_lora(rank, alpha, target_mask); }
+  // Dropout probability on every LoRA linear's input in training forwards
+  // (forwards with autograd enabled) and the seed of its counter-based mask
+  // stream (each training forward draws fresh masks from seed and a forward
+  // counter); takes effect at the next set_lora.
+  static constexpr uint64_t kDefaultDropoutSeed = 0x5EED0000ull;
+  void set_lora_dropout(float p, uint64_t seed = kDefaultDropoutSeed);
+  float lora_dropout() const { return lora_dropout_; }
+  uint64_t lora_dropout_seed() const { return dropout_seed_; }
   const EngineModelConfig& engine_config() const { return ecfg_; }
   int lora_rank() const { return lora_r_; }
   float lora_alpha() const { return lora_alpha_; }
@@ -81,6 +89,8 @@ class EngineModel {
   EngineModelConfig ecfg_;
   int lora_r_ = 0, lora_mask_ = 0;
   float lora_alpha_ = 0.f;
+  float lora_dropout_ = 0.f;
+  uint64_t dropout_seed_ = kDefaultDropoutSeed;
   int64_t max_tokens_ = 4096;
   int last_S_ = 0;  // sequence length of the last forward
   std::shared_ptr<EngineState> st_;

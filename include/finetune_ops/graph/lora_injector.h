@@ -5,8 +5,9 @@
 // MlpFcIn, MlpFcOut}, applied by LoraInjector().inject(model, spec)
 // (gpt2_small_lora_finetune/src/main.cpp:264-276).  Adapters are A [r, in]
 // and B [out, r] (PEFT layout, README.md:282,296) with scale alpha / r;
-// dropout must be 0 on this path and split_qkv=false (the fused c_attn
-// carries one adapter, as PEFT does).
+// dropout is PEFT's lora_dropout on the adapter input in training forwards
+// (autograd enabled); split_qkv=false (the fused c_attn carries one adapter,
+// as PEFT does).
 #pragma once
 #include <vector>
 

@@ -5,6 +5,8 @@
 // assign_weight(name, t) with W transposed to [in, out] at load,
 // init_lora(r, alpha, dropout[, qv_only]), freeze_base(), get_lora_parameters()
 // (qwen_lora_finetune/src/wikitext_main.cpp:63-79, mmlu_main.cpp:125,145,217).
+// dropout is PEFT's lora_dropout on the adapter inputs in training forwards
+// (autograd enabled); the WikiText driver's default is 0.05 (:26).
 // Adapters on q/k/v/o (q/v only with qv_only).  RMSNorm, SwiGLU MLP, RoPE,
 // grouped KV heads, q/k/v biases.  Names are HF's without the "model."
 // prefix (also accepted): embed_tokens.weight,

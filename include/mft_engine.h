@@ -42,6 +42,13 @@ typedef struct {
   int sliding_window;  /* key window of local layers (0 = none) */
   float attn_scale;    /* 0 → 1/sqrt(head_dim) */
   int w_fp16;          /* frozen linear + embedding weights stored as fp16 */
+  /* PEFT's lora_dropout on every LoRA linear's input in training forwards
+   * (QwenModel::init_lora(r, alpha, dropout), qwen_lora_finetune/src/
+   * wikitext_main.cpp:26,77; LoraSpec.dropout).  Masks come from a counter
+   * hash of (dropout_seed, training-forward count, layer·8 + target,
+   * element) — the same stream the CPU oracle restates.  0 = off. */
+  float lora_dropout;
+  uint64_t dropout_seed;
 } mft_model_cfg;
 
 typedef struct mft_model_s* mft_model;
@@ -51,6 +58,11 @@ typedef struct mft_model_s* mft_model;
 int mft_model_create(mft_model* out, const mft_model_cfg* cfg,
                      int64_t max_tokens, void* stream);
 int mft_model_destroy(mft_model m);
+/* Training (default) or evaluation mode of the forwards that keep
+ * activations for a backward (mft_model_fwd_bwd, mft_model_forward_train,
+ * mft_model_train_step): only training forwards apply LoRA dropout, as
+ * PEFT's module.train() / eval() do.  mft_model_forward never does. */
+int mft_model_set_training(mft_model m, int training);
 int mft_model_num_params(mft_model m);
 /* Parameter i: name, shape, trainable flag, storage dtype, device pointers
  * (grad is NULL for frozen parameters). */

@@ -220,6 +220,26 @@ void lora_linear_bwd(hipStream_t s, const float* dy, const float* x,
                      const KernelEvents* ev = nullptr);
 // Scratch floats lora_linear_bwd needs for its rank-r temporaries.
 size_t lora_bwd_scratch_floats(int64_t M, int64_t K, int64_t N, int r);
+// LoRA dropout (lora.hip).  A DropStream covers n_fwd training forwards
+// launched as one (rows_per_fwd rows each) whose last one is step *step.
+struct DropStream {
+  float p;
+  uint64_t seed;
+  const int* step;
+  int n_fwd;
+  int64_t rows_per_fwd;
+};
+// keep threshold on the top 24 bits of the mask hash: floor(p·2^24)
+uint32_t dropout_threshold(float p);
+// *step += n (n training forwards start)
+void dropout_step(hipStream_t s, int* step, int n);
+// xd = x∘mask of stream `lid` (x rows ldx apart, xd dense [M,K])
+void dropout_apply(hipStream_t s, const float* x, int64_t ldx, int64_t M, int64_t K, const DropStream& d, int lid,
+                   float* xd);
+// dx += scale·(U·A)∘mask; gelu_grad_scale: x *= gelu'(pre) elementwise
+void dropout_dx(hipStream_t s, float* dx, int64_t M, int64_t K, const float* U, const float* A, int r, float scale,
+                const DropStream& d, int lid);
+void gelu_grad_scale(hipStream_t s, float* x, const float* pre, int64_t n);
 
 struct AttnArgs {
   const float *q, *k, *v;

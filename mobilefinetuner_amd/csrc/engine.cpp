@@ -48,6 +48,8 @@ struct Linear {
   int K = 0, N = 0;
   float* weff = nullptr;  // merged weight W + s·Aᵀ·Bᵀ [K, N] fp32 (LoRA linears), rows weff_ld apart
   int weff_ld = 0;
+  int lid = 0;            // LoRA dropout stream: layer·8 + target
+  float* xd = nullptr;    // LoRA input after dropout [M, K] (training forwards with dropout)
 };
 
 
@@ -150,6 +152,11 @@ struct mft_model_s {
   // (its embedding row is zeros), 2 = a label outside [0, vocab) that is not
   // ignore_index (counted as ignored); reported by mft_model_read_stats
   int* d_err = nullptr;
+  int* d_drop_step = nullptr;  // training forwards run (LoRA dropout stream)
+  bool training = true;        // training forwards apply LoRA dropout
+  bool fwd_dropout = false;    // the last forward applied it (its backward must too)
+  int drop_n_fwd = 1;          // micro-batch forwards the last forward launch covered
+  int64_t drop_rows = 0;       // rows per micro-batch forward
   int n_micro_pending = 0;
   int adam_t = 0;
   // Qwen2 / Gemma3 with LoRA on q, k and v (merged path): one GEMM for
@@ -172,7 +179,7 @@ struct mft_model_s {
     const void *ids, *mask, *labels;
     int n_micro, seqs, S;
     float upstream;
-    bool timing;
+    bool timing, training;
   } graph_key{};
   // timing
   bool timing = false;
@@ -271,6 +278,11 @@ void build_params(mft_model_s* m) {
   m->nfw = add_param(m, "norm.weight", d, 0, false, false, norm_init);
 }
 
+void assign_dropout_streams(mft_model_s* m) {
+  for (size_t li = 0; li < m->L.size(); ++li)
+    for (int t = 0; t < T_MAX; ++t) m->L[li].lin[t].lid = (int)li * 8 + t;
+}
+
 void alloc_params(mft_model_s* m) {
   size_t fb = 0;
   int64_t ln = 0;
@@ -321,6 +333,8 @@ float attn_scale(const mft_model_cfg& c) {
 bool lora_mergeable(const mft_model_s* m) {
   const int r = m->c.lora_r;
   if (r != 4 && r != 8 && r != 16 && r != 32) return false;
+  // dropout masks the LoRA branch's input only, which a merged W_eff cannot express
+  if (m->c.lora_dropout > 0.f) return false;
   bool any = false;
   for (const auto& L : m->L)
     for (const auto& l : L.lin) {
@@ -405,10 +419,11 @@ void alloc_acts(mft_model_s* m) {
           a.krs = b.f(M * Hk);
         }
       }
-      const Layer& L = m->L[l];
+      Layer& L = m->L[l];
       const bool keep_dy = lora_mergeable(m);
       for (int t = 0; t < T_MAX; ++t)
         if (L.lin[t].A >= 0) {
+          if (c.lora_dropout > 0.f) L.lin[t].xd = b.f(M * L.lin[t].K);
           a.xa[t] = b.f(M * r);
           a.U[t] = b.f(M * r);
           if (m->fuse_qkv && t < 3) {  // views of the fused gradient
@@ -486,6 +501,7 @@ void alloc_acts(mft_model_s* m) {
   m->d_hp = reinterpret_cast<float*>(static_cast<char*>(sc) + 1792);
   m->d_t = reinterpret_cast<int*>(static_cast<char*>(sc) + 2048);
   m->d_err = reinterpret_cast<int*>(static_cast<char*>(sc) + 2304);
+  m->d_drop_step = reinterpret_cast<int*>(static_cast<char*>(sc) + 2560);
   MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
@@ -693,6 +709,10 @@ void collect_timing(mft_model_s* m) {
 // ---- building blocks ---------------------------------------------------------------
 float lscale(const mft_model_s* m) { return m->c.lora_alpha / (float)m->c.lora_r; }
 
+DropStream drop_stream(const mft_model_s* m) {
+  return DropStream{m->c.lora_dropout, m->c.dropout_seed, m->d_drop_step, m->drop_n_fwd, m->drop_rows};
+}
+
 // y = x·W (+ LoRA) + bias (+ resid); with gelu_out, y keeps the
 // pre-activation and gelu_out receives GELU(y) (GPT-2 c_fc).
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
@@ -711,9 +731,15 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     return;
   }
   if (lora) {
+    // training forward with LoRA dropout: the branch reads xd = x∘mask
+    const float* xin = x;
+    if (m->fwd_dropout) {
+      dropout_apply(m->stream, x, l.K, M, l.K, drop_stream(m), l.lid, l.xd);
+      xin = l.xd;
+    }
     Timed tr(m, CLS_RANK, 4.0 * M * (l.K + r));  // bytes: read x, write xa
     tr.begin();
-    rank_proj(m->stream, x, l.K, static_cast<const float*>(m->P[l.A].data), 1, l.K, (int)M, l.K, r, xa);
+    rank_proj(m->stream, xin, l.K, static_cast<const float*>(m->P[l.A].data), 1, l.K, (int)M, l.K, r, xa);
     tr.end();
     ep.P = xa;
     ep.Q = static_cast<const float*>(m->P[l.B].data);
@@ -753,6 +779,27 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
     tr.begin();
     rank_proj(m->stream, dy, l.N, static_cast<const float*>(m->P[l.B].data), r, 1, (int)M, l.N, r, U);
     tr.end();
+  }
+  if (lora && m->fwd_dropout) {
+    // dX = dY·Wᵀ + s·(U·A)∘mask: the masked rank-r term is added after the
+    // GEMM, then the fused epilogue steps the plain path takes (GELU', the
+    // norm backward) run on the complete gradient; dA reads xd = x∘mask.
+    if (dx) {
+      GemmEpilogue ep;
+      ep.beta = beta;
+      Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
+      gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
+      dropout_dx(m->stream, dx, M, l.K, U, static_cast<const float*>(m->P[l.A].data), r, lscale(m),
+                 drop_stream(m), l.lid);
+      if (gelu_grad_of) gelu_grad_scale(m->stream, dx, gelu_grad_of, M * l.K);
+      if (norm && norm->kind != NORM_NONE) row_norm(m->stream, dx, M, l.K, *norm);
+    }
+    Timed tr(m, CLS_RANK, 4.0 * M * (l.K + l.N + 2 * r));
+    tr.begin();
+    rank_outer_pair(m->stream, (int)M, r, lscale(m), true, U, l.xd, l.K, l.K, m->P[l.A].grad, l.K, 1, xa, dy,
+                    l.N, l.N, m->P[l.B].grad, 1, r);
+    tr.end();
+    return;
   }
   if (dx) {
     GemmEpilogue ep;
@@ -819,8 +866,14 @@ void attention_fwd(mft_model_s* m, Acts& a, int li, const float* mask, int nseq,
   t.end();
 }
 
-void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S) {
+// n_fwd: the micro-batch forwards this launch stands for (nseq/n_fwd
+// sequences each); with LoRA dropout each draws its own masks.
+void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S, bool train, int n_fwd) {
   const mft_model_cfg& c = m->c;
+  m->fwd_dropout = train && c.lora_dropout > 0.f && c.lora_r > 0 && c.lora_mask != 0;
+  m->drop_n_fwd = n_fwd;
+  m->drop_rows = (int64_t)(nseq / n_fwd) * S;
+  if (m->fwd_dropout) dropout_step(m->stream, m->d_drop_step, n_fwd);  // these forwards' mask streams
   const int64_t M = (int64_t)nseq * S;
   const int d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim;
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
@@ -1140,7 +1193,7 @@ void drop_graph(mft_model_s* m) {
   m->graph_timed.clear();
 }
 
-void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S);
+void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S, bool train, int n_fwd);
 void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs, int S, float upstream,
                    bool backward);
 void backward(mft_model_s* m, const float* mask, int nseq, int S);
@@ -1160,7 +1213,7 @@ void capture_step(mft_model_s* m, const int32_t* ids, const float* mask, const i
     MFT_HIP(hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal));
     zero_stats(m, n_micro);
     m->n_micro_pending = 0;
-    forward(m, ids, mask, n_micro * seqs, S);
+    forward(m, ids, mask, n_micro * seqs, S, m->training, n_micro);
     cross_entropy(m, labels, n_micro, seqs, S, upstream, true);
     backward(m, mask, n_micro * seqs, S);
     opt_device(m);
@@ -1187,6 +1240,7 @@ void capture_step(mft_model_s* m, const int32_t* ids, const float* mask, const i
   m->graph_key.S = S;
   m->graph_key.upstream = upstream;
   m->graph_key.timing = m->timing;
+  m->graph_key.training = m->training;
 }
 
 template <typename F>
@@ -1214,6 +1268,7 @@ void check_cfg(const mft_model_cfg& c) {
   MFT_CHECK_ARG(c.lora_r == 0 || c.lora_r == 4 || c.lora_r == 8 || c.lora_r == 16 || c.lora_r == 32,
                 "lora_r must be 0, 4, 8, 16 or 32");
   MFT_CHECK_ARG(c.d % 4 == 0 && c.d_ff % 4 == 0 && c.head_dim % 4 == 0, "dims must be multiples of 4");
+  MFT_CHECK_ARG(c.lora_dropout >= 0.f && c.lora_dropout < 1.f, "lora_dropout must lie in [0, 1)");
 }
 
 }  // namespace
@@ -1231,6 +1286,7 @@ int mft_model_create(mft_model* out, const mft_model_cfg* cfg, int64_t max_token
       m->stream = reinterpret_cast<hipStream_t>(stream);
       m->max_tokens = max_tokens;
       build_params(m);
+      assign_dropout_streams(m);
       alloc_params(m);
       alloc_acts(m);
       build_lora_tables(m);
@@ -1261,6 +1317,13 @@ int mft_model_destroy(mft_model m) {
 }
 
 int mft_model_num_params(mft_model m) { return m ? (int)m->P.size() : 0; }
+
+int mft_model_set_training(mft_model m, int training) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    m->training = training != 0;
+  });
+}
 
 int mft_model_param_info(mft_model m, int i, const char** name, int* ndim, int64_t* dims, int* trainable,
                          int* is_f16, void** data, float** grad) {
@@ -1309,7 +1372,7 @@ int mft_model_fwd_bwd(mft_model m, const int32_t* ids, const float* mask, const 
     if (n_micro <= 0 || seqs_per_micro <= 0 || S <= 0) throw Error(MFT_EINVAL, "empty batch");
     if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
     if (m->c.arch == MFT_ARCH_GPT2 && S > m->c.max_pos) throw Error(MFT_EINVAL, "seq_len exceeds n_positions");
-    forward(m, ids, mask, nseq, S);
+    forward(m, ids, mask, nseq, S, m->training, n_micro);
     cross_entropy(m, labels, n_micro, seqs_per_micro, S, upstream, true);
     backward(m, mask, nseq, S);
   });
@@ -1321,7 +1384,7 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask, const 
     if (!m || !ids) throw Error(MFT_EINVAL, "null argument");
     const int nseq = n_micro * seqs_per_micro;
     if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
-    forward(m, ids, mask, nseq, S);
+    forward(m, ids, mask, nseq, S, false, 1);
     if (logits)
       MFT_HIP(hipMemcpy2DAsync(logits, sizeof(float) * m->c.vocab, m->logits, sizeof(float) * m->ldv,
                                sizeof(float) * m->c.vocab, (size_t)nseq * S, hipMemcpyDeviceToDevice,
@@ -1336,7 +1399,7 @@ int mft_model_forward_train(mft_model m, const int32_t* ids, const float* mask, 
     if (nseq <= 0 || S <= 0) throw Error(MFT_EINVAL, "empty batch");
     if ((int64_t)nseq * S > m->max_tokens) throw Error(MFT_EINVAL, "batch exceeds max_tokens");
     if (m->c.arch == MFT_ARCH_GPT2 && S > m->c.max_pos) throw Error(MFT_EINVAL, "seq_len exceeds n_positions");
-    forward(m, ids, mask, nseq, S);
+    forward(m, ids, mask, nseq, S, m->training, 1);
     m->api_nseq = nseq;
     m->api_S = S;
     m->api_dlogits = false;
@@ -1396,7 +1459,7 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, con
     if (!use_graph) {
       zero_stats(m, n_micro);
       m->n_micro_pending = 0;
-      forward(m, ids, mask, nseq, S);
+      forward(m, ids, mask, nseq, S, m->training, n_micro);
       cross_entropy(m, labels, n_micro, seqs_per_micro, S, upstream, true);
       backward(m, mask, nseq, S);
       upload_hparams(m, lr, b1, b2, eps, wd, clip);
@@ -1407,7 +1470,8 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, con
     const bool same = m->graph_exec && m->graph_key.ids == ids && m->graph_key.mask == mask &&
                       m->graph_key.labels == labels && m->graph_key.n_micro == n_micro &&
                       m->graph_key.seqs == seqs_per_micro && m->graph_key.S == S &&
-                      m->graph_key.upstream == upstream && m->graph_key.timing == m->timing;
+                      m->graph_key.upstream == upstream && m->graph_key.timing == m->timing &&
+                      m->graph_key.training == m->training;
     if (!same) capture_step(m, ids, mask, labels, n_micro, seqs_per_micro, S, upstream);
     upload_hparams(m, lr, b1, b2, eps, wd, clip);
     MFT_HIP(hipEventRecord(m->ev_in, m->stream));

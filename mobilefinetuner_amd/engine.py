@@ -127,6 +127,10 @@ class Model:
              _dev(mask, torch.float32, "mask"), _dev(labels, torch.int32, "labels"), n_micro,
              seqs_per_micro, S, upstream, lr, b1, b2, eps, wd, clip, int(graph))
 
+    def set_training(self, on: bool):
+        """Training forwards apply LoRA dropout; evaluation forwards do not."""
+        call("mft_model_set_training", self.h, int(on))
+
     def read_stats(self):
         loss = C.c_float()
         n = C.c_int64()

@@ -195,6 +195,8 @@ void EngineModel::ensure_engine() {
   c.sliding_window = ecfg_.sliding_window;
   c.attn_scale = ecfg_.attn_scale;
   c.w_fp16 = ecfg_.w_fp16 ? 1 : 0;
+  c.lora_dropout = has_lora() ? lora_dropout_ : 0.f;
+  c.dropout_seed = dropout_seed_;
   auto st = std::make_shared<EngineState>();
   mft_check(mft_model_create(&st->m, &c, max_tokens_, nullptr), "mft_model_create");
   const int n = mft_model_num_params(st->m);
@@ -242,6 +244,12 @@ void EngineModel::ensure_engine() {
     if (kv.first.find(".lora_") != std::string::npos && !st_->index.count(kv.first)) continue;
     assign_weight(kv.first, kv.second);
   }
+}
+
+void EngineModel::set_lora_dropout(float p, uint64_t seed) {
+  if (!(p >= 0.f && p < 1.f)) throw std::invalid_argument("LoRA dropout must lie in [0, 1)");
+  lora_dropout_ = p;
+  dropout_seed_ = seed;
 }
 
 void EngineModel::attach_lora(int r, float alpha, int mask) {
@@ -334,6 +342,9 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
   // Parameters edited through host views are copied back before the forward.
   for (auto& v : views_)
     if (v) (void)v->device_data();
+  // training forward (LoRA dropout) iff gradients are being recorded
+  mft_check(mft_model_set_training(st_->m, autograd::Engine::instance().is_enabled() ? 1 : 0),
+            "mft_model_set_training");
   mft_check(mft_model_forward_train(st_->m, static_cast<const int32_t*>(ids->device_data()),
                                     mask ? static_cast<const float*>(mask->device_data()) : nullptr, B, S),
             "mft_model_forward_train");
@@ -568,10 +579,10 @@ std::string GPT2Model::normalise_name(const std::string& raw) const {
 }
 
 void LoraInjector::inject(GPT2Model& model, const LoraSpec& spec) {
-  if (spec.dropout != 0.f) throw std::invalid_argument("LoraInjector: LoRA dropout must be 0 on this backend");
   if (spec.split_qkv) throw std::invalid_argument("LoraInjector: split_qkv is not supported (one adapter on c_attn)");
   int mask = 0;
   for (auto t : spec.targets) mask |= 1 << (int)t;
+  model.set_lora_dropout(spec.dropout);
   model.set_lora(spec.rank, spec.alpha, mask);
   last_ = spec;
   n_targets_ = model.config().n_layer * (int)spec.targets.size();
@@ -607,7 +618,7 @@ EngineModelConfig qwen_ecfg(const QwenConfig& c) {
 QwenModel::QwenModel(const QwenConfig& cfg) : EngineModel(qwen_ecfg(cfg)), cfg_(cfg) {}
 
 void QwenModel::init_lora(int rank, float alpha, float dropout, bool qv_only) {
-  if (dropout != 0.f) throw std::invalid_argument("init_lora: LoRA dropout must be 0 on this backend");
+  set_lora_dropout(dropout);
   attach_lora(rank, alpha, qv_only ? 0b0101 : 0b1111);
 }
 
@@ -760,7 +771,6 @@ GemmaLoraSpec GemmaLoraSpec::attention_light() {
 }
 
 void GemmaLoraInjector::inject(GemmaModel& model, const GemmaLoraSpec& spec) {
-  if (spec.dropout != 0.f) throw std::invalid_argument("GemmaLoraInjector: LoRA dropout must be 0 on this backend");
   int mask = 0;
   for (const auto& t : spec.target_modules) {
     int bit = -1;
@@ -769,6 +779,7 @@ void GemmaLoraInjector::inject(GemmaModel& model, const GemmaLoraSpec& spec) {
     if (bit < 0) throw std::invalid_argument("GemmaLoraInjector: unknown target module " + t);
     mask |= 1 << bit;
   }
+  model.set_lora_dropout(spec.dropout);
   model.set_lora(spec.rank, spec.alpha, mask);
   last_ = spec;
 }

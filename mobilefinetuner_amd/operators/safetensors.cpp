@@ -725,7 +725,7 @@ void LoraSaver::save_safetensors(const std::string& path, EngineModel& model, co
 }
 
 void LoraSaver::save_safetensors(const std::string& path, EngineModel& model) {
-  save_impl(path, model, model.lora_rank(), model.lora_alpha(), 0.f, false);
+  save_impl(path, model, model.lora_rank(), model.lora_alpha(), model.lora_dropout(), false);
 }
 
 LoraState LoraSaver::load_safetensors(const std::string& path) {
@@ -812,6 +812,7 @@ void LoraSaver::attach_from_state(EngineModel& model, const LoraState& state) {
     parse_lora_key(kv.first, k);
     mask |= 1 << k.bit;
   }
+  model.set_lora_dropout(state.dropout);
   model.set_lora(state.rank, state.alpha, mask);
   for (const auto& kv : state.tensors) {
     LoraKey k;

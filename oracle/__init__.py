@@ -31,12 +31,13 @@ class OrcCfg(C.Structure):
         ("head_dim", _I), ("d_ff", _I), ("max_pos", _I), ("vocab", _L), ("lora_r", _I),
         ("lora_alpha", _F), ("lora_mask", _I), ("norm_eps", _F), ("rope_theta", _D),
         ("rope_local_theta", _D), ("sliding_pattern", _I), ("sliding_window", _I),
-        ("attn_scale", _F), ("w_fp16", _I),
+        ("attn_scale", _F), ("w_fp16", _I), ("lora_dropout", _F), ("dropout_seed", C.c_uint64),
     ]
 
 
 _SIGS = {
     "orc_set_blas": (_I, [_I]),
+    "orc_dropout_mask": (None, [C.c_uint64, C.c_uint32, C.c_uint32, _L, _F, _P]),
     "orc_blas_backend": (C.c_char_p, []),
     "orc_set_threads": (None, [_I]),
     "orc_get_threads": (_I, []),
@@ -272,7 +273,8 @@ class OracleModel:
         c = OrcCfg(mcfg.arch, mcfg.n_layer, mcfg.d, mcfg.n_head, mcfg.n_kv_head, mcfg.head_dim,
                    mcfg.d_ff, mcfg.max_pos, mcfg.vocab, mcfg.lora_r, mcfg.lora_alpha,
                    mcfg.lora_mask, mcfg.norm_eps, mcfg.rope_theta, mcfg.rope_local_theta,
-                   mcfg.sliding_pattern, mcfg.sliding_window, mcfg.attn_scale, mcfg.w_fp16)
+                   mcfg.sliding_pattern, mcfg.sliding_window, mcfg.attn_scale, mcfg.w_fp16,
+                   mcfg.lora_dropout, mcfg.dropout_seed)
         self._c = c
         self.h = lib().orc_model_create(C.byref(c))
         self.params = []
@@ -326,3 +328,11 @@ class OracleModel:
 
     def opt_step(self, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0):
         return lib().orc_model_opt_step(self.h, lr, b1, b2, eps, wd, clip)
+
+
+def dropout_mask(seed, step, lid, shape, p):
+    """The LoRA dropout mask (1/(1-p) where kept, 0 elsewhere) of stream
+    `lid` in training forward `step` (oracle.h: orc_dropout_mask)."""
+    out = np.empty(shape, np.float32)
+    lib().orc_dropout_mask(seed, step, lid, out.size, p, ptr(out))
+    return out

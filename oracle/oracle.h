@@ -120,6 +120,18 @@ void orc_embed(const int32_t* ids, int64_t M, int S, const float* wte,
                const uint16_t* wte_f16, const float* wpe, int64_t C,
                float scale, float* h);
 
+/* ---- LoRA dropout mask ----------------------------------------------------
+ * PEFT's lora_dropout on the LoRA branch input: xd = x∘keep/(1−p).  keep of
+ * element idx (= row·K + column) of LoRA linear `lid` (= layer·8 + target)
+ * in the `step`-th training forward: the top 24 bits of
+ * mix64(mix64(seed ^ step<<20 ^ lid) + idx) are ≥ ⌊p·2^24⌋, where mix64 is
+ * the splitmix64 output function (Steele, Lea, Flood 2014; constants of
+ * Vigna's reference).  The reference's own RNG is not in the published tree;
+ * this counter-based form lets the backward regenerate the forward's mask.
+ * mask[i] = 1/(1−p) where kept, 0 elsewhere. */
+void orc_dropout_mask(uint64_t seed, uint32_t step, uint32_t lid, int64_t n,
+                      float p, float* mask);
+
 /* ---- model-level step (GPT-2 / Qwen2 / Gemma3 LoRA) --------------------- */
 enum { ORC_GPT2 = 0, ORC_QWEN2 = 1, ORC_GEMMA3 = 2 };
 typedef struct {
@@ -134,6 +146,8 @@ typedef struct {
   int sliding_window;  /* Gemma3 local layers: key window; 0 = none */
   float attn_scale;    /* 0 → 1/sqrt(head_dim) */
   int w_fp16;          /* frozen linear + embedding weights stored fp16 */
+  float lora_dropout;  /* LoRA input dropout in training forwards (0 = off) */
+  uint64_t dropout_seed;
 } orc_model_cfg;
 
 typedef struct orc_model orc_model;
@@ -147,7 +161,9 @@ int64_t    orc_model_param_info(const orc_model* m, int i, const char** name,
 void*      orc_model_param_data(orc_model* m, int i);
 float*     orc_model_param_grad(orc_model* m, int i);
 /* One micro-batch forward + CE + backward; grads accumulate.  Returns the
- * micro-batch mean loss.  upstream = 1/accum (loss scaling, main.cpp:480-485). */
+ * micro-batch mean loss.  upstream = 1/accum (loss scaling, main.cpp:480-485).
+ * A training forward: with lora_dropout > 0 it advances the dropout step and
+ * drops LoRA inputs (orc_dropout_mask); orc_model_forward never does. */
 float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
                         const int32_t* labels, int B, int S, float upstream);
 /* Forward only; writes logits [B*S, V] when logits != NULL; returns loss. */

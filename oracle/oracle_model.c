@@ -47,6 +47,7 @@ enum { G_ATTN = 0, G_PROJ, G_FC, G_FC2 };
 typedef struct {
   int W, b, A, B; /* param indices, -1 if absent */
   int K, N;
+  int lid;        /* dropout stream id: layer·8 + target */
 } olinear;
 
 typedef struct {
@@ -63,6 +64,8 @@ struct orc_model {
   int wte, wpe, nfw, nfb;
   olayer* L;
   int t; /* Adam step count */
+  uint32_t drop_step; /* training forwards run (LoRA dropout stream) */
+  int training;       /* the current forward drops LoRA inputs */
   /* activation cache for the current micro-batch */
   int B, S;
   float** act;
@@ -187,6 +190,8 @@ orc_model* orc_model_create(const orc_model_cfg* cfg) {
     m->nfw = add_param(m, "norm.weight", d, 0, 0, 0);
     m->nfb = -1;
   }
+  for (int li = 0; li < c->n_layer; ++li)
+    for (int t = 0; t < T_MAX; ++t) m->L[li].lin[t].lid = li * 8 + t;
   return m;
 }
 
@@ -246,26 +251,107 @@ static const float* wview(orc_model* m, int i, float** tmp) {
 
 static float lscale(const orc_model* m) { return m->c.lora_alpha / (float)m->c.lora_r; }
 
+static int dropout_active(const orc_model* m, const olinear* l) {
+  return l->A >= 0 && m->training && m->c.lora_dropout > 0.0f;
+}
+
+/* y = x·W + b + s·(xd·Aᵀ)·Bᵀ, xd = x (or x∘mask with LoRA dropout in a
+ * training forward: PEFT's lora_B(lora_A(dropout(x)))·s).  xa = xd·Aᵀ and
+ * xd are kept for the backward. */
 static void lin_fwd(orc_model* m, const olinear* l, const float* x, int64_t M,
-                    float* y, float** xa_out) {
+                    float* y, float** xa_out, float** xd_out) {
   float* tmp;
   const float* W = wview(m, l->W, &tmp);
+  const int r = m->c.lora_r;
   float* xa = NULL;
-  if (l->A >= 0) xa = F(m, M * m->c.lora_r);
-  orc_lora_linear_fwd(x, M, l->K, W, l->N, P(m, l->b), P(m, l->A), P(m, l->B),
-                      l->A >= 0 ? m->c.lora_r : 0, lscale(m), y, xa);
+  *xd_out = NULL;
+  if (l->A >= 0) xa = F(m, M * r);
+  if (!dropout_active(m, l)) {
+    orc_lora_linear_fwd(x, M, l->K, W, l->N, P(m, l->b), P(m, l->A), P(m, l->B),
+                        l->A >= 0 ? r : 0, lscale(m), y, xa);
+  } else {
+    const int64_t K = l->K, N = l->N;
+    float* xd = F(m, M * K);
+    orc_dropout_mask(m->c.dropout_seed, m->drop_step, (uint32_t)l->lid, M * K, m->c.lora_dropout, xd);
+    for (int64_t i = 0; i < M * K; ++i) xd[i] *= x[i];
+    orc_lora_linear_fwd(x, M, K, W, N, P(m, l->b), NULL, NULL, 0, 0.0f, y, NULL);
+    const float* A = P(m, l->A);
+    const float* Bm = P(m, l->B);
+    const float s = lscale(m);
+#pragma omp parallel for
+    for (int64_t i = 0; i < M; ++i) {
+      for (int j = 0; j < r; ++j) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; ++k) acc += (double)xd[i * K + k] * A[(int64_t)j * K + k];
+        xa[i * r + j] = (float)acc;
+      }
+      for (int64_t n = 0; n < N; ++n) {
+        double t = 0.0;
+        for (int j = 0; j < r; ++j) t += (double)xa[i * r + j] * Bm[n * r + j];
+        y[i * N + n] += (float)(s * t);
+      }
+    }
+    *xd_out = xd;
+  }
   free(tmp);
   *xa_out = xa;
 }
 
+/* dX = dY·Wᵀ + s·(dY·B·A)∘mask; dA += s·(dY·B)ᵀ·xd; dB += s·dYᵀ·xa (no
+ * mask: xd = x without dropout). */
 static void lin_bwd(orc_model* m, const olinear* l, const float* dy,
-                    const float* x, const float* xa, int64_t M, float* dx) {
+                    const float* x, const float* xa, const float* xd, int64_t M, float* dx) {
   float* tmp;
   const float* W = wview(m, l->W, &tmp);
   int r = l->A >= 0 ? m->c.lora_r : 0;
-  orc_lora_linear_bwd(dy, x, W, P(m, l->A), P(m, l->B), xa, M, l->K, l->N, r,
-                      lscale(m), dx, l->A >= 0 ? m->p[l->A].grad : NULL,
-                      l->B >= 0 ? m->p[l->B].grad : NULL, 1);
+  if (!xd) {
+    orc_lora_linear_bwd(dy, x, W, P(m, l->A), P(m, l->B), xa, M, l->K, l->N, r,
+                        lscale(m), dx, l->A >= 0 ? m->p[l->A].grad : NULL,
+                        l->B >= 0 ? m->p[l->B].grad : NULL, 1);
+  } else {
+    const int64_t K = l->K, N = l->N;
+    const float s = lscale(m);
+    const float* A = P(m, l->A);
+    const float* Bm = P(m, l->B);
+    float* dA = m->p[l->A].grad;
+    float* dB = m->p[l->B].grad;
+    if (dx) orc_lora_linear_bwd(dy, x, W, NULL, NULL, NULL, M, K, N, 0, 0.0f, dx, NULL, NULL, 1);
+    float* U = (float*)xmalloc(sizeof(float) * (size_t)(M * r));
+    float* mask = (float*)xmalloc(sizeof(float) * (size_t)(M * K));
+    orc_dropout_mask(m->c.dropout_seed, m->drop_step, (uint32_t)l->lid, M * K, m->c.lora_dropout, mask);
+#pragma omp parallel for
+    for (int64_t i = 0; i < M; ++i)
+      for (int j = 0; j < r; ++j) {
+        double acc = 0.0;
+        for (int64_t n = 0; n < N; ++n) acc += (double)dy[i * N + n] * Bm[n * r + j];
+        U[i * r + j] = (float)acc;
+      }
+    if (dx) {
+#pragma omp parallel for
+      for (int64_t i = 0; i < M; ++i)
+        for (int64_t k = 0; k < K; ++k) {
+          double t = 0.0;
+          for (int j = 0; j < r; ++j) t += (double)U[i * r + j] * A[(int64_t)j * K + k];
+          dx[i * K + k] += (float)(s * t * mask[i * K + k]);
+        }
+    }
+#pragma omp parallel for
+    for (int j = 0; j < r; ++j)
+      for (int64_t k = 0; k < K; ++k) {
+        double t = 0.0;
+        for (int64_t i = 0; i < M; ++i) t += (double)U[i * r + j] * xd[i * K + k];
+        dA[(int64_t)j * K + k] += (float)(s * t);
+      }
+#pragma omp parallel for
+    for (int64_t n = 0; n < N; ++n)
+      for (int j = 0; j < r; ++j) {
+        double t = 0.0;
+        for (int64_t i = 0; i < M; ++i) t += (double)dy[i * N + n] * xa[i * r + j];
+        dB[n * r + j] += (float)(s * t);
+      }
+    free(U);
+    free(mask);
+  }
   free(tmp);
 }
 
@@ -281,6 +367,7 @@ typedef struct {
   float *qrs, *krs;       /* Gemma: per (token,head) rstd */
   int64_t qs, ks, vs;     /* row strides of q/k/v */
   float *xa[T_MAX];
+  float *xd[T_MAX];       /* LoRA inputs after dropout (training forwards) */
   float *att, *lse;
   float *o, *ors;         /* Gemma: o_proj output before post-attn norm */
   float *hmid;
@@ -327,16 +414,16 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
       C->mean1 = F(m, M);
       orc_layernorm_fwd(h, P(m, L->n1w), P(m, L->n1b), M, d, c->norm_eps, C->n1, C->mean1, C->rstd1);
       float* qkv = F(m, M * 3 * d);
-      lin_fwd(m, &L->lin[G_ATTN], C->n1, M, qkv, &C->xa[G_ATTN]);
+      lin_fwd(m, &L->lin[G_ATTN], C->n1, M, qkv, &C->xa[G_ATTN], &C->xd[G_ATTN]);
       C->q = qkv; C->k = qkv + d; C->v = qkv + 2 * d;
       C->qs = C->ks = C->vs = 3 * d;
     } else {
       orc_rmsnorm_fwd(h, P(m, L->n1w), M, d, c->norm_eps, gemma, C->n1, C->rstd1);
       C->q = F(m, M * H * hd); C->k = F(m, M * Hk * hd); C->v = F(m, M * Hk * hd);
       C->qs = (int64_t)H * hd; C->ks = C->vs = (int64_t)Hk * hd;
-      lin_fwd(m, &L->lin[T_Q], C->n1, M, C->q, &C->xa[T_Q]);
-      lin_fwd(m, &L->lin[T_K], C->n1, M, C->k, &C->xa[T_K]);
-      lin_fwd(m, &L->lin[T_V], C->n1, M, C->v, &C->xa[T_V]);
+      lin_fwd(m, &L->lin[T_Q], C->n1, M, C->q, &C->xa[T_Q], &C->xd[T_Q]);
+      lin_fwd(m, &L->lin[T_K], C->n1, M, C->k, &C->xa[T_K], &C->xd[T_K]);
+      lin_fwd(m, &L->lin[T_V], C->n1, M, C->v, &C->xa[T_V], &C->xd[T_V]);
       if (gemma) { /* QK RMSNorm over head_dim, (1+w) form */
         C->qraw = F(m, M * H * hd); C->kraw = F(m, M * Hk * hd);
         memcpy(C->qraw, C->q, sizeof(float) * (size_t)(M * H * hd));
@@ -357,7 +444,7 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
     float* hmid = F(m, M * d);
     const olinear* lo = gpt2 ? &L->lin[G_PROJ] : &L->lin[T_O];
     C->o = F(m, M * d);
-    lin_fwd(m, lo, C->att, M, C->o, gpt2 ? &C->xa[G_PROJ] : &C->xa[T_O]);
+    lin_fwd(m, lo, C->att, M, C->o, gpt2 ? &C->xa[G_PROJ] : &C->xa[T_O], gpt2 ? &C->xd[G_PROJ] : &C->xd[T_O]);
     if (gemma) {
       C->ors = F(m, M);
       float* on = F(m, M * d);
@@ -381,15 +468,15 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
     float* hout = F(m, M * d);
     C->mo = F(m, M * d);
     if (gpt2) {
-      lin_fwd(m, &L->lin[G_FC], C->n2, M, C->gate, &C->xa[G_FC]);
+      lin_fwd(m, &L->lin[G_FC], C->n2, M, C->gate, &C->xa[G_FC], &C->xd[G_FC]);
       orc_glu_fwd(C->gate, NULL, nf, 0, C->act);
-      lin_fwd(m, &L->lin[G_FC2], C->act, M, C->mo, &C->xa[G_FC2]);
+      lin_fwd(m, &L->lin[G_FC2], C->act, M, C->mo, &C->xa[G_FC2], &C->xd[G_FC2]);
     } else {
       C->up = F(m, nf);
-      lin_fwd(m, &L->lin[T_GATE], C->n2, M, C->gate, &C->xa[T_GATE]);
-      lin_fwd(m, &L->lin[T_UP], C->n2, M, C->up, &C->xa[T_UP]);
+      lin_fwd(m, &L->lin[T_GATE], C->n2, M, C->gate, &C->xa[T_GATE], &C->xd[T_GATE]);
+      lin_fwd(m, &L->lin[T_UP], C->n2, M, C->up, &C->xa[T_UP], &C->xd[T_UP]);
       orc_glu_fwd(C->gate, C->up, nf, gemma ? 0 : 1, C->act);
-      lin_fwd(m, &L->lin[T_DOWN], C->act, M, C->mo, &C->xa[T_DOWN]);
+      lin_fwd(m, &L->lin[T_DOWN], C->act, M, C->mo, &C->xa[T_DOWN], &C->xd[T_DOWN]);
     }
     if (gemma) {
       C->mrs = F(m, M);
@@ -426,6 +513,7 @@ float orc_model_forward(orc_model* m, const int32_t* ids, const float* mask,
   lcache* cache = (lcache*)xmalloc(sizeof(lcache) * (size_t)m->c.n_layer);
   float *hf, *hl, *fm, *fr;
   float* lg = logits ? logits : (float*)xmalloc((size_t)(M * m->c.vocab) * 4);
+  m->training = 0;  /* evaluation: no dropout */
   forward_all(m, ids, mask, B, S, cache, &hf, &hl, &fm, &fr, lg);
   double ls = 0.0;
   int64_t n = orc_ce_fwd_bwd(lg, labels, B, S, m->c.vocab, -100, 1.0f, 0, &ls, NULL, NULL);
@@ -444,6 +532,9 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
   lcache* cache = (lcache*)xmalloc(sizeof(lcache) * (size_t)c->n_layer);
   float *hf, *hl, *fm, *fr;
   float* logits = (float*)xmalloc((size_t)(M * c->vocab) * 4);
+  /* a training forward: the LoRA dropout stream advances */
+  m->training = 1;
+  if (c->lora_dropout > 0.0f) m->drop_step++;
   forward_all(m, ids, mask, B, S, cache, &hf, &hl, &fm, &fr, logits);
   double ls = 0.0;
   int64_t n = orc_ce_fwd_bwd(logits, labels, B, S, c->vocab, -100, upstream, 0,
@@ -487,15 +578,15 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
       dmo = dtmp;
     }
     if (gpt2) {
-      lin_bwd(m, &L->lin[G_FC2], dmo, C->act, C->xa[G_FC2], M, dact);
+      lin_bwd(m, &L->lin[G_FC2], dmo, C->act, C->xa[G_FC2], C->xd[G_FC2], M, dact);
       orc_glu_bwd(dact, C->gate, NULL, nf, 0, dgate, NULL);
-      lin_bwd(m, &L->lin[G_FC], dgate, C->n2, C->xa[G_FC], M, dn);
+      lin_bwd(m, &L->lin[G_FC], dgate, C->n2, C->xa[G_FC], C->xd[G_FC], M, dn);
       orc_layernorm_bwd(dn, C->hmid, P(m, L->n2w), C->mean2, C->rstd2, M, d, dh, 1);
     } else {
-      lin_bwd(m, &L->lin[T_DOWN], dmo, C->act, C->xa[T_DOWN], M, dact);
+      lin_bwd(m, &L->lin[T_DOWN], dmo, C->act, C->xa[T_DOWN], C->xd[T_DOWN], M, dact);
       orc_glu_bwd(dact, C->gate, C->up, nf, gemma ? 0 : 1, dgate, dup);
-      lin_bwd(m, &L->lin[T_GATE], dgate, C->n2, C->xa[T_GATE], M, dn);
-      lin_bwd(m, &L->lin[T_UP], dup, C->n2, C->xa[T_UP], M, dtmp);
+      lin_bwd(m, &L->lin[T_GATE], dgate, C->n2, C->xa[T_GATE], C->xd[T_GATE], M, dn);
+      lin_bwd(m, &L->lin[T_UP], dup, C->n2, C->xa[T_UP], C->xd[T_UP], M, dtmp);
       add_into(dn, dtmp, M * d);
       orc_rmsnorm_bwd(dn, C->hmid, P(m, L->n2w), C->rstd2, M, d, gemma, dh, 1);
     }
@@ -506,14 +597,14 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
       dox = dtmp;
     }
     lin_bwd(m, gpt2 ? &L->lin[G_PROJ] : &L->lin[T_O], dox, C->att,
-            C->xa[gpt2 ? G_PROJ : T_O], M, datt);
+            C->xa[gpt2 ? G_PROJ : T_O], C->xd[gpt2 ? G_PROJ : T_O], M, datt);
     int win = layer_is_local(c, li) ? c->sliding_window : 0;
     const int need_dx = li > 0; /* nothing trainable below layer 0 */
     if (gpt2) {
       orc_attn_bwd(C->q, C->qs, C->k, C->ks, C->v, C->vs, C->att, (int64_t)H * hd,
                    datt, (int64_t)H * hd, C->lse, B, H, Hk, S, hd, attn_scale(c), 1,
                    win, mask, dqkv, 3 * d, dqkv + d, 3 * d, dqkv + 2 * d, 3 * d);
-      lin_bwd(m, &L->lin[G_ATTN], dqkv, C->n1, C->xa[G_ATTN], M, need_dx ? dn1 : NULL);
+      lin_bwd(m, &L->lin[G_ATTN], dqkv, C->n1, C->xa[G_ATTN], C->xd[G_ATTN], M, need_dx ? dn1 : NULL);
       if (need_dx)
         orc_layernorm_bwd(dn1, C->x, P(m, L->n1w), C->mean1, C->rstd1, M, d, dh, 1);
     } else {
@@ -532,10 +623,10 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
         memcpy(dq, t1, sizeof(float) * (size_t)(M * H * hd));
         memcpy(dk, t2, sizeof(float) * (size_t)(M * Hk * hd));
       }
-      lin_bwd(m, &L->lin[T_Q], dq, C->n1, C->xa[T_Q], M, need_dx ? dn1 : NULL);
-      lin_bwd(m, &L->lin[T_K], dk, C->n1, C->xa[T_K], M, need_dx ? dtmp : NULL);
+      lin_bwd(m, &L->lin[T_Q], dq, C->n1, C->xa[T_Q], C->xd[T_Q], M, need_dx ? dn1 : NULL);
+      lin_bwd(m, &L->lin[T_K], dk, C->n1, C->xa[T_K], C->xd[T_K], M, need_dx ? dtmp : NULL);
       if (need_dx) add_into(dn1, dtmp, M * d);
-      lin_bwd(m, &L->lin[T_V], dv, C->n1, C->xa[T_V], M, need_dx ? dtmp : NULL);
+      lin_bwd(m, &L->lin[T_V], dv, C->n1, C->xa[T_V], C->xd[T_V], M, need_dx ? dtmp : NULL);
       if (need_dx) {
         add_into(dn1, dtmp, M * d);
         orc_rmsnorm_bwd(dn1, C->x, P(m, L->n1w), C->rstd1, M, d, gemma, dh, 1);

@@ -701,3 +701,25 @@ void orc_embed(const int32_t* ids, int64_t M, int S, const float* wte,
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* LoRA dropout mask (see oracle.h).                                        */
+/* ------------------------------------------------------------------------ */
+static uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+void orc_dropout_mask(uint64_t seed, uint32_t step, uint32_t lid, int64_t n,
+                      float p, float* mask) {
+  const uint64_t key = mix64(seed ^ ((uint64_t)step << 20) ^ (uint64_t)lid);
+  const uint32_t thr = (uint32_t)((double)p * 16777216.0);
+  const float inv = 1.0f / (1.0f - p);
+#pragma omp parallel for
+  for (int64_t i = 0; i < n; ++i) {
+    const uint32_t u = (uint32_t)(mix64(key + (uint64_t)i) >> 40);
+    mask[i] = u >= thr ? inv : 0.0f;
+  }
+}

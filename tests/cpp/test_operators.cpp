@@ -377,6 +377,47 @@ static void test_qwen() {
                        [&](const std::string& p) { LoraSaver::save_safetensors(p, model); }, 2, 12);
 }
 
+// LoRA dropout p = 0.1 through QwenModel::init_lora: each micro-batch's
+// training forward draws the oracle's masks (same seed, same forward counter).
+static void test_qwen_dropout() {
+  QwenConfig cfg;
+  cfg.vocab_size = 89;
+  cfg.hidden_size = 128;
+  cfg.intermediate_size = 160;
+  cfg.num_hidden_layers = 2;
+  cfg.num_attention_heads = 2;
+  cfg.num_key_value_heads = 1;
+  cfg.max_position_embeddings = 64;
+  cfg.rms_norm_eps = 1e-6f;
+  cfg.rope_theta = 1e6;
+  QwenModel model(cfg);
+  model.init_lora(8, 16.f, 0.1f);
+  model.freeze_base();
+
+  orc_model_cfg oc{};
+  oc.arch = ORC_QWEN2;
+  oc.n_layer = 2;
+  oc.d = 128;
+  oc.n_head = 2;
+  oc.n_kv_head = 1;
+  oc.head_dim = 64;
+  oc.d_ff = 160;
+  oc.max_pos = 64;
+  oc.vocab = 89;
+  oc.lora_r = 8;
+  oc.lora_alpha = 16.f;
+  oc.lora_mask = 0b1111;
+  oc.norm_eps = 1e-6f;
+  oc.rope_theta = 1e6;
+  oc.rope_local_theta = 1e6;
+  oc.lora_dropout = 0.1f;
+  oc.dropout_seed = EngineModel::kDefaultDropoutSeed;
+  orc_model* om = orc_model_create(&oc);
+  init_both(model, om, 21);
+  driver_loop("qwen2-dropout", model, om, 2, 12, 89, 2, 2, false, 1.0f, 1e-3f);
+  orc_model_destroy(om);
+}
+
 static void test_gemma(bool fp16) {
   GemmaTextConfig cfg;
   cfg.vocab_size = 89;
@@ -762,6 +803,7 @@ int main() {
     test_ops_chain();
     test_gpt2();
     test_qwen();
+    test_qwen_dropout();
     test_gemma(false);
     test_gemma(true);
     test_gemma_trainer();

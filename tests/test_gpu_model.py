@@ -249,6 +249,73 @@ def test_full_size_fp16_weights_against_fp32():
         O.lib().orc_set_blas(0)
 
 
+@pytest.mark.parametrize("case", ["gpt2-all-targets", "qwen2", "qwen2-qv", "gemma3"])
+def test_lora_dropout_steps_match_oracle(case):
+    """LoRA dropout (p = 0.2) on the training forwards: the engine draws the
+    same counter-based masks as the oracle (one stream per micro-batch
+    forward, advancing every step), so losses and gradients agree to the
+    fp32 bar over three steps; an evaluation forward applies no dropout."""
+    mc, B, S, accum = SMALL[case]
+    mc = dataclasses.replace(mc, lora_dropout=0.2, dropout_seed=77)
+    print(f"dropout step {case} B={B} S={S} accum={accum}", flush=True)
+    O.lib().orc_set_blas(0)
+    om, eng, _ = build_pair(mc, accum * B * S)
+    rng = np.random.default_rng(9)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    for step in range(3):
+        ids = rng.integers(0, mc.vocab, (accum, B, S)).astype(np.int32)
+        labels = ids.copy()
+        lo, le, grads, no, ne = run_step(om, eng, ids, labels, None, B, S, accum)
+        assert abs(le - lo) < TOL * abs(lo), (step, le, lo)
+        for name, (ge, go) in grads.items():
+            assert rel_err(ge, go) < TOL, (step, name, rel_err(ge, go))
+        for p in om.params:
+            if p["trainable"]:
+                om.set_param(p["name"], eng.get(p["name"]))
+    # evaluation: no masks, and the stream does not advance
+    ids = rng.integers(0, mc.vocab, (B, S)).astype(np.int32)
+    eng.set_training(False)
+    eng.forward(dev(ids.reshape(-1)), labels=dev(ids.reshape(-1)), S=S)
+    loss_e = eng.read_stats()[0]
+    loss_o = om.forward(ids, None, ids, B, S)
+    loss_o = loss_o[0] if isinstance(loss_o, tuple) else loss_o
+    assert abs(loss_e - loss_o) < TOL * abs(loss_o), (loss_e, loss_o)
+    eng.set_training(True)
+    ids = rng.integers(0, mc.vocab, (accum, B, S)).astype(np.int32)
+    lo, le, grads, _, _ = run_step(om, eng, ids, ids.copy(), None, B, S, accum)
+    assert abs(le - lo) < TOL * abs(lo), (le, lo)
+    for name, (ge, go) in grads.items():
+        assert rel_err(ge, go) < TOL, (name, rel_err(ge, go))
+    eng.close()
+
+
+def test_lora_dropout_graph_replay_equals_eager():
+    """With LoRA dropout the captured step graph reads the mask counter from
+    device memory, so every replay draws the next step's masks exactly as
+    eager steps do."""
+    mc = dataclasses.replace(SMALL["qwen2"][0], lora_dropout=0.1, dropout_seed=5)
+    B, S, accum = 2, 64, 2
+    ids = torch.from_numpy(np.random.default_rng(13).integers(0, mc.vocab, (accum * B * S,)).astype(np.int32)).cuda()
+    models = []
+    for _ in range(2):
+        eng = Model(mc, accum * B * S)
+        for n, v in param_values(eng.params, seed=4).items():
+            eng.set_param(n, v)
+        models.append(eng)
+    for step in range(4):
+        out = []
+        for graph, eng in zip((False, True), models):
+            eng.train_step(ids, ids, n_micro=accum, S=S, lr=1e-3, clip=1.0, graph=graph)
+            out.append(eng.read_stats())
+        torch.zeros(1000, device="cuda").sum().item()
+        assert abs(out[0][0] - out[1][0]) <= 1e-6 * abs(out[0][0]), (step, out)
+    for p in models[0].params:
+        if p["trainable"]:
+            assert rel_err(models[1].get(p["name"]), models[0].get(p["name"])) < 1e-6, p["name"]
+    for eng in models:
+        eng.close()
+
+
 def test_out_of_range_token_id_is_reported():
     """A token id outside [0, vocab) embeds as a zero row (nothing is read out
     of bounds) and the step's statistics report it as an error."""

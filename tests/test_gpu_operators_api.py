@@ -20,7 +20,7 @@ def test_cpp_operator_api_matches_oracle():
     fails = [ln for ln in r.stdout.splitlines() if ln.startswith("FAIL")]
     assert r.returncode == 0 and not fails, "\n".join(fails) or r.stderr[-2000:]
     # every family and the op chain actually ran
-    for tag in ("ops chain dA", "gpt2 step1", "qwen2 step1", "gemma3 step1", "gemma3-fp16w step1",
+    for tag in ("ops chain dA", "gpt2 step1", "qwen2 step1", "qwen2-dropout step1", "gemma3 step1", "gemma3-fp16w step1",
                 "gpt2 checkpoint logits equal", "qwen2 checkpoint logits equal",
                 "gemma trainer step3 loss", "gemma trainer LoRA params after 3 steps",
                 "gemma retain_grad dlogits", "layout matmul"):

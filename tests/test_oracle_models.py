@@ -221,3 +221,81 @@ def test_blas_backed_oracle_equals_exact_loops():
         pytest.skip("no CBLAS available")
     assert abs(res[0][0] - res[1][0]) < 1e-5 * res[0][0]
     assert rel_err(res[1][1], res[0][1]) < 1e-4
+
+
+class LoraDropWrap(LoraWrap):
+    """PEFT's lora_B(lora_A(dropout(x)))·s with a given dropout mask
+    (1/(1-p) where kept) over the token rows of x."""
+
+    def __init__(self, base, A, B, s, mask):
+        super().__init__(base, A, B, s)
+        self.mask = torch.tensor(mask, dtype=torch.float64)
+
+    def forward(self, x):
+        xd = x * self.mask.reshape(x.shape)
+        return self.base(x) + self.s * (xd @ self.A.T) @ self.B.T
+
+
+def _lid(mc, name):
+    """The dropout stream id of a LoRA linear: layer·8 + target index."""
+    parts = name.split(".")
+    layer = int(parts[1])
+    tail = ".".join(parts[2:])
+    names = (["attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"] if mc.arch == 0 else
+             ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+              "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"])
+    return layer * 8 + names.index(tail)
+
+
+def test_dropout_mask_statistics_and_determinism():
+    """The mask holds exactly 0 or 1/(1-p), keeps a Binomial(n, 1-p) share of
+    elements (within 5 sigma), is a pure function of (seed, step, stream) and
+    differs between steps and streams; p = 0 keeps everything."""
+    n, p = 200_000, 0.1
+    m = O.dropout_mask(9, 1, 3, (n,), p)
+    keep = m > 0
+    assert np.all((m == 0) | (m == np.float32(1 / (1 - p))))
+    assert abs(keep.mean() - (1 - p)) < 5 * np.sqrt(p * (1 - p) / n)
+    assert np.array_equal(m, O.dropout_mask(9, 1, 3, (n,), p))
+    for other in (O.dropout_mask(9, 2, 3, (n,), p), O.dropout_mask(9, 1, 4, (n,), p),
+                  O.dropout_mask(10, 1, 3, (n,), p)):
+        agree = ((other > 0) == keep).mean()
+        assert agree < 1 - p * (1 - p)  # independent masks agree on p²+(1-p)² of elements
+    assert np.all(O.dropout_mask(9, 1, 3, (1000,), 0.0) == 1.0)
+
+
+@pytest.mark.parametrize("case", ["gpt2-mlp-lora", "qwen2"])
+def test_model_step_with_lora_dropout_vs_hf(case):
+    """LoRA dropout (training forward, p = 0.2): the oracle's loss and every
+    LoRA gradient against HF models whose LoRA branch reads x·mask, the mask
+    of each linear taken from the oracle's stream (step 1 of the run).  A
+    second oracle forward in evaluation mode applies no dropout."""
+    import dataclasses
+    mc = dataclasses.replace(CASES[case], lora_dropout=0.2, dropout_seed=77)
+    B, S = 2, 12
+    om = O.OracleModel(mc)
+    vals = init_values(om, seed=4)
+    ids = np.random.default_rng(31).integers(0, mc.vocab, (B, S)).astype(np.int32)
+    loss = om.fwd_bwd(ids, None, ids, B, S, 1.0)
+    model = hf_model(mc)
+    wraps = load_hf(model, dataclasses.replace(mc, lora_dropout=0.0), vals)
+    prefix = "transformer." if mc.arch == 0 else "model."
+    for name, w in list(wraps.items()):
+        K = w.A.shape[1]
+        mask = O.dropout_mask(77, 1, _lid(mc, name), (B * S, K), 0.2)
+        dw = LoraDropWrap(w.base, w.A.detach().numpy(), w.B.detach().numpy(), w.s, mask)
+        mod_path = prefix + name
+        parent = model.get_submodule(mod_path.rsplit(".", 1)[0])
+        setattr(parent, mod_path.rsplit(".", 1)[1], dw)
+        wraps[name] = dw
+    out = model(input_ids=torch.tensor(ids, dtype=torch.long), labels=torch.tensor(ids, dtype=torch.long))
+    assert abs(loss - out.loss.item()) < 2e-5 * abs(out.loss.item()), (loss, out.loss.item())
+    out.loss.backward()
+    for name, w in wraps.items():
+        assert rel_err(om.get(name + ".lora_A", grad=True), w.A.grad.numpy()) < 1e-4, name
+        assert rel_err(om.get(name + ".lora_B", grad=True), w.B.grad.numpy()) < 1e-4, name
+    # evaluation forward: no dropout, same loss as a model built without it
+    plain = O.OracleModel(dataclasses.replace(mc, lora_dropout=0.0))
+    for n, v in vals.items():
+        plain.set_param(n, v)
+    assert om.forward(ids, None, ids, B, S)[0] == plain.forward(ids, None, ids, B, S)[0]
