@@ -19,20 +19,19 @@
 namespace mft {
 namespace {
 
-__global__ void zero_i64_kernel(int64_t* p) { *p = 0; }
-
 // Counts the valid shifted targets: label != ignore_index and inside
 // [0, V) — the same test ce_row_kernel applies, so an out-of-range label is
 // excluded from both the loss and its normaliser (and flagged in *bad).
-__global__ __launch_bounds__(256) void ce_count_kernel(const int32_t* __restrict__ labels,
-                                                       int B, int S, int64_t V, int ignore_index,
-                                                       int64_t* cnt, int* bad) {
-  __shared__ int red[4];
+// One workgroup: the count is stored, not accumulated, so no clearing
+// launch precedes it.
+__global__ __launch_bounds__(1024) void ce_count_kernel(const int32_t* __restrict__ labels,
+                                                        int B, int S, int64_t V, int ignore_index,
+                                                        int64_t* cnt, int* bad) {
+  __shared__ int red[16];
   int c = 0;
   bool out_of_range = false;
   const int64_t total = (int64_t)B * S;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
     const int s = (int)(i % S);
     if (s + 1 >= S) continue;
     const int lab = labels[i + 1];
@@ -46,8 +45,9 @@ __global__ __launch_bounds__(256) void ce_count_kernel(const int32_t* __restrict
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int v = red[0] + red[1] + red[2] + red[3];
-    if (v) atomicAdd((unsigned long long*)cnt, (unsigned long long)v);
+    int64_t v = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) v += red[w];
+    *cnt = v;
   }
 }
 
@@ -200,12 +200,8 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
-  // A fill kernel rather than hipMemsetAsync keeps the sequence capturable
-  // in a HIP graph.
-  hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(1), 0, s, count_scratch);
-  MFT_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ce_count_kernel, dim3((unsigned)std::min<int64_t>(cdiv(rows, 256), 64)), dim3(256),
-                     0, s, labels, B, S, V, ignore_index, count_scratch, bad_label);
+  hipLaunchKernelGGL(ce_count_kernel, dim3(1), dim3(1024), 0, s, labels, B, S, V, ignore_index, count_scratch,
+                     bad_label);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_row_kernel<1024>, dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V, ld,
                      ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);

@@ -279,14 +279,14 @@ void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
                int64_t n, float lr, float b1, float b2, float eps, float wd,
                int t, const float* clip_scale, bool zero_grad);
 // Device-parameterised variants for captured step graphs:
-// hp = {lr, b1, b2, eps, wd, max_norm}; *tstep is the 1-based Adam step,
-// advanced by clip_scale_dev.
+// hp = {lr, b1, b2, eps, wd, max_norm}; *tstep is the 1-based Adam step.
+// set_hparams writes hp, advances *tstep and clears the Σg² accumulator *ss;
+// adam_step_dev clips by the norm in *ss (clip factor and clipped norm to
+// clip_out[0..1]) and applies Adam.
 void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n,
-                   const float* hp, const int* tstep, const float* clip_scale, bool zero_grad);
-void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,
-                    int* tstep);
+                   const float* hp, const int* tstep, const double* ss, float* clip_out, bool zero_grad);
 void set_hparams(hipStream_t s, float* hp, float lr, float b1, float b2, float eps, float wd,
-                 float max_norm);
+                 float max_norm, double* ss, int* tstep);
 void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n);
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out);
 void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,

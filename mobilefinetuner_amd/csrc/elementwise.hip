@@ -279,17 +279,29 @@ __global__ void adam_kernel(float* __restrict__ p, float* __restrict__ g,
 }
 
 // Same update with the hyper-parameters and the 1-based step count read
-// from device memory (hp = {lr, b1, b2, eps, wd}), so a captured step graph
-// can be replayed with a new learning rate and step.
+// from device memory (hp = {lr, b1, b2, eps, wd, max_norm}), so a captured
+// step graph can be replayed with a new learning rate and step.  The clip
+// factor comes from Σg² (ss) in every thread: max_norm/(norm + 1e-6) when
+// norm > max_norm > 0, else 1; thread 0 also stores it and the clipped norm
+// (out[0], out[1]).
 __global__ void adam_dev_kernel(float* __restrict__ p, float* __restrict__ g,
                                 float* __restrict__ m, float* __restrict__ v, int64_t n,
                                 const float* __restrict__ hp, const int* __restrict__ tstep,
-                                const float* __restrict__ clip_scale, int zero_grad) {
-  const float lr = hp[0], b1 = hp[1], b2 = hp[2], eps = hp[3], wd = hp[4];
+                                const double* __restrict__ ss, float* __restrict__ out, int zero_grad) {
+  const float lr = hp[0], b1 = hp[1], b2 = hp[2], eps = hp[3], wd = hp[4], max_norm = hp[5];
   const int t = *tstep;
   const double bc1 = 1.0 - pow((double)b1, (double)t);
   const double bc2 = 1.0 - pow((double)b2, (double)t);
-  const float cs = clip_scale ? *clip_scale : 1.f;
+  float nv = (float)sqrt(*ss);
+  float cs = 1.f;
+  if (max_norm > 0.f && nv > max_norm) {
+    cs = max_norm / (nv + 1e-6f);
+    nv = max_norm;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    out[0] = cs;
+    out[1] = nv;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const float gi = g[i] * cs;
@@ -306,28 +318,16 @@ __global__ void adam_dev_kernel(float* __restrict__ p, float* __restrict__ g,
   }
 }
 
-// hp = {lr, b1, b2, eps, wd, max_norm}, written by a kernel that takes the
-// values as arguments (no host staging buffer for the captured graph to read).
+// Start of a device-side optimizer step: hp = {lr, b1, b2, eps, wd,
+// max_norm} from the arguments (no host staging buffer for a captured graph
+// to read), the step counter advanced, the Σg² accumulator cleared.
 __global__ void set_hparams_kernel(float* hp, float lr, float b1, float b2, float eps, float wd,
-                                   float max_norm) {
+                                   float max_norm, double* ss, int* tstep) {
   if (threadIdx.x == 0) {
     hp[0] = lr; hp[1] = b1; hp[2] = b2; hp[3] = eps; hp[4] = wd; hp[5] = max_norm;
+    *ss = 0.0;
+    *tstep += 1;
   }
-}
-
-// Clip factor from Σg² with max_norm = hp[5]; advances the step counter.
-__global__ void clip_dev_kernel(const double* ss, const float* hp, float* scale, float* norm,
-                                int* tstep) {
-  const float max_norm = hp[5];
-  float nv = (float)sqrt(*ss);
-  float sc = 1.f;
-  if (max_norm > 0.f && nv > max_norm) {
-    sc = max_norm / (nv + 1e-6f);
-    nv = max_norm;
-  }
-  *scale = sc;
-  *norm = nv;
-  *tstep += 1;
 }
 
 __global__ void add_out_kernel(float* __restrict__ out, const float* __restrict__ a,
@@ -569,20 +569,15 @@ void adam_step(hipStream_t s, float* p, float* g, float* m, float* v,
   MFT_LAUNCH_CHECK();
 }
 void adam_step_dev(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n,
-                   const float* hp, const int* tstep, const float* clip_scale, bool zero_grad) {
+                   const float* hp, const int* tstep, const double* ss, float* clip_out, bool zero_grad) {
   if (n <= 0) return;
   hipLaunchKernelGGL(adam_dev_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, hp,
-                     tstep, clip_scale, zero_grad ? 1 : 0);
+                     tstep, ss, clip_out, zero_grad ? 1 : 0);
   MFT_LAUNCH_CHECK();
 }
 void set_hparams(hipStream_t s, float* hp, float lr, float b1, float b2, float eps, float wd,
-                 float max_norm) {
-  hipLaunchKernelGGL(set_hparams_kernel, dim3(1), dim3(64), 0, s, hp, lr, b1, b2, eps, wd, max_norm);
-  MFT_LAUNCH_CHECK();
-}
-void clip_scale_dev(hipStream_t s, const double* ss, const float* hp, float* scale, float* norm,
-                    int* tstep) {
-  hipLaunchKernelGGL(clip_dev_kernel, dim3(1), dim3(1), 0, s, ss, hp, scale, norm, tstep);
+                 float max_norm, double* ss, int* tstep) {
+  hipLaunchKernelGGL(set_hparams_kernel, dim3(1), dim3(64), 0, s, hp, lr, b1, b2, eps, wd, max_norm, ss, tstep);
   MFT_LAUNCH_CHECK();
 }
 void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n) {

@@ -1166,23 +1166,25 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
 // kernel launched ahead of the optimizer (or of the captured step graph), so
 // no host buffer is read by the device.
 void upload_hparams(mft_model_s* m, float lr, float b1, float b2, float eps, float wd, float clip) {
-  set_hparams(m->stream, m->d_hp, lr, b1, b2, eps, wd, clip);
+  set_hparams(m->stream, m->d_hp, lr, b1, b2, eps, wd, clip, m->d_sumsq, m->d_t);
 }
 
 // clip_and_get_grad_norm + Adam::step + zero_grad on the flat LoRA arrays;
-// reads d_hp / d_t only, so it can live inside a captured graph.
+// reads d_hp / d_t only, so it can live inside a captured graph.  Follows
+// upload_hparams, which advanced d_t and cleared d_sumsq.
 void opt_device(mft_model_s* m) {
   const hipStream_t s = m->stream;
-  fill_const(s, reinterpret_cast<float*>(m->d_sumsq), 2, 0.f);  // one double = two floats
   sumsq(s, m->lora_g, m->lora_n, m->d_sumsq);
-  clip_scale_dev(s, m->d_sumsq, m->d_hp, m->d_clip, m->d_clip + 1, m->d_t);
-  adam_step_dev(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, m->d_hp, m->d_t, m->d_clip, true);
+  adam_step_dev(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, m->d_hp, m->d_t, m->d_sumsq, m->d_clip,
+                true);
 }
 
 void zero_stats(mft_model_s* m, int n_micro) {
-  // per-micro loss sums (doubles) and counts (int64) are 8 bytes each
-  fill_const(m->stream, reinterpret_cast<float*>(m->d_loss), 2 * n_micro, 0.f);
-  fill_const(m->stream, reinterpret_cast<float*>(m->d_cnt), 2 * n_micro, 0.f);
+  // the 64 per-micro loss sums (doubles) and the 64 counts (int64) that
+  // follow them: one launch over both arrays
+  (void)n_micro;
+  static_assert(sizeof(double) == 8 && sizeof(int64_t) == 8, "stat slots");
+  fill_const(m->stream, reinterpret_cast<float*>(m->d_loss), (512 + 512) / 4, 0.f);
 }
 
 void drop_graph(mft_model_s* m) {

@@ -1164,15 +1164,33 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   }
   const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
   // A row norm after the GEMM costs nothing extra in a split-K reduction and
-  // a launch of its own otherwise: an unsplit plan with K >= 1024 becomes
+  // a launch of its own otherwise: an unsplit plan with K >= 512 becomes
   // 32-row tiles split in two (GPT-2 medium's attention c_proj: 53.3k vs
-  // 52.9k tokens/s on MI355X).  Tuning hook: MFT_GEMM_NORM_PLAN="bm,0,splits".
-  if (nm && !forced && pl.splits == 1 && K >= 1024 && N % 4 == 0 && N <= 4096 && ldc == N) {
+  // 52.9k tokens/s on MI355X; GPT-2 small's, K = 768: +1.1%).  Tuning hooks: MFT_GEMM_NORM_PLAN="bm,0,splits",
+  // MFT_GEMM_NORM_MINK (the K threshold).
+  static const int norm_min_k = [] {
+    const char* e = getenv("MFT_GEMM_NORM_MINK");
+    return e ? atoi(e) : 512;
+  }();
+  if (nm && !forced && pl.splits == 1 && K >= norm_min_k && N % 4 == 0 && N <= 4096 && ldc == N) {
     static const char* nplan = getenv("MFT_GEMM_NORM_PLAN");
     int bm = 32, bn = 0, sp = 2;
     if (nplan && !(sscanf(nplan, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 && (bm == 32 || bm == 64) && bn == 0))
       bm = 32, bn = 0, sp = 2;
     if ((size_t)sp * M * N * sizeof(float) <= ws.bytes) pl = {bm, bn, sp};
+  }
+  // Wave quantisation of the 128×128 plan: two such workgroups fit a CU, so
+  // the launch runs in rounds of 512 tiles.  When its last round would be
+  // under a quarter full (GPT-2's 50257-entry vocabulary at M = 512: 1572
+  // tiles, 36 of them in a fourth round), the trailing column tiles become
+  // an unsplit 32-row-tile launch instead, which spreads that work over the
+  // whole GPU for a fraction of a round.  Plain epilogues only (bias allowed).
+  int n_main = 0;
+  if (pl.bm == 128 && pl.bn == 128 && !forced && !nm && ep.P == nullptr && !ep.resid && ep.beta == 0.f &&
+      !ep.gelu_out && !ep.gelu_grad_of) {
+    const int64_t tm = cdiv(M, 128), tn = cdiv(N, 128), tiles = tm * tn;
+    const int64_t rem = tiles % 512;
+    if (tiles > 512 && rem > 0 && rem * 4 <= 512) n_main = (int)((tn - cdiv(rem, tm)) * 128);
   }
   const int bk = plan_bk(pl.bm, pl.bn);
   int splits = pl.splits;
@@ -1187,6 +1205,34 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   const bool dispatch_events = ev && ev->start && ev->stop && cap == hipStreamCaptureStatusNone;
   if (ev && ev->start && !dispatch_events) MFT_HIP(hipEventRecord(ev->start, s));
   t_gemm_events = dispatch_events ? ev : nullptr;
+  if (n_main > 0) {
+    GemmParams pm = p;
+    pm.N = n_main;
+    launch_tile<128, 128, 32>(s, pm, b_nk, b_f16, 1);
+    t_gemm_events = nullptr;
+    if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
+    // columns [n_main, N): the tail events time this launch
+    GemmParams pt = p;
+    const size_t esz = b_f16 ? 2 : 4;
+    pt.B = static_cast<const char*>(p.B) + (b_nk ? (size_t)n_main * p.ldb : (size_t)n_main) * esz;
+    pt.C = C + n_main;
+    pt.N = N - n_main;
+    if (pt.ep.bias) pt.ep.bias += n_main;
+    pt.k_chunk = (int)(cdiv(K, 32) * 32);
+    const bool tail = ev && ev->tail_start && ev->tail_stop;
+    KernelEvents tev;
+    if (tail) {
+      ev->tail_used = true;
+      tev.start = ev->tail_start;
+      tev.stop = ev->tail_stop;
+      if (!dispatch_events) MFT_HIP(hipEventRecord(ev->tail_start, s));
+    }
+    t_gemm_events = tail && dispatch_events ? &tev : nullptr;
+    launch_q<32, 32>(s, pt, b_nk, b_f16, 1);
+    t_gemm_events = nullptr;
+    if (tail && !dispatch_events) MFT_HIP(hipEventRecord(ev->tail_stop, s));
+    return;
+  }
   if (pl.bm == 128 && pl.bn == 0) launch_q<128, 32>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 128 && pl.bn == 1) launch_q<128, 64>(s, p, b_nk, b_f16, splits);
   else if (pl.bm == 128) launch_tile<128, 128, 32>(s, p, b_nk, b_f16, splits);
