@@ -62,6 +62,17 @@ __device__ __forceinline__ float __attribute__((ext_vector_type(4))) widen4(uint
   return {half_bits_to_float(u.x & 0xffff), half_bits_to_float(u.x >> 16), half_bits_to_float(u.y & 0xffff),
           half_bits_to_float(u.y >> 16)};
 }
+// fp16 operand staging in the GEMMs: the raw 64 bits ride in lanes 0–1 of a
+// float4 register set from the global load until the LDS store, which
+// widens them; widening at the load would make the wave wait for the load
+// right after issuing it and lose the prefetch distance.
+__device__ __forceinline__ float __attribute__((ext_vector_type(4))) stash_f16(uint2 u) {
+  return {__uint_as_float(u.x), __uint_as_float(u.y), 0.f, 0.f};
+}
+__device__ __forceinline__ float __attribute__((ext_vector_type(4))) unstash_f16(
+    float __attribute__((ext_vector_type(4))) v) {
+  return widen4(uint2{__float_as_uint(v[0]), __float_as_uint(v[1])});
+}
 
 // ---- launchers shared by the C-ABI and the step engine ----------------------
 // A row norm applied to the finished rows of a GEMM output C[M,N] (N = the

@@ -50,6 +50,11 @@ struct Linear {
   int weff_ld = 0;
   int lid = 0;            // LoRA dropout stream: layer·8 + target
   float* xd = nullptr;    // LoRA input after dropout [M, K] (training forwards with dropout)
+  // rank-r panel path: batched launch run before this linear's forward GEMM
+  // (every xa of its input group) and before its dX GEMM (every U of its
+  // gradient group); -1 when another linear of the group runs it
+  int xa_batch = -1, u_batch = -1;
+  float* u = nullptr;  // U = dY·B of this linear (panel path)
 };
 
 
@@ -129,6 +134,13 @@ struct mft_model_s {
   // from three table-driven launches: all xa at the start of the backward,
   // all U and dB after the last layer, then all dA.
   bool merged = false;
+  // Rank-r panel path (LoRA linears over fp16-stored W, which a fp32 W_eff
+  // would double): every LoRA linear multiplies the frozen W, widened in the
+  // GEMM's tile load, and adds s·xa·Bᵀ (forward) or s·U·A (dX) as one more
+  // MFMA K-panel of depth r.  xa and U come from one batched launch per
+  // input / gradient group of a layer (q|k|v, o, gate|up, down); dB and dA
+  // from two whole-model launches at the end of the backward.
+  bool panel = false;
   void* weff_mem = nullptr;
   void* tables = nullptr;  // device: MergeJob[n_merge], then RankJob[]
   const MergeJob* d_merge = nullptr;
@@ -139,7 +151,7 @@ struct mft_model_s {
     double work_per_row;  // HBM bytes per token row (timing)
   };
   std::vector<Batch> batches;
-  int xa_batch = -1, udb_batch = -1, da_batch = -1;
+  int xa_batch = -1, udb_batch = -1, da_batch = -1, db_batch = -1;
   // device scalars: [0..63] per-micro loss sums (double), counts (int64)
   double* d_loss = nullptr;
   int64_t* d_cnt = nullptr;
@@ -328,9 +340,9 @@ float attn_scale(const mft_model_cfg& c) {
   return c.attn_scale > 0.f ? c.attn_scale : 1.f / std::sqrt((float)c.head_dim);
 }
 
-// The merged-weight LoRA path (W_eff GEMMs + batched rank-r launches) takes
+// The batched rank-r kernels (merged-weight and rank-r panel paths) take
 // r ∈ {4, 8, 16, 32} and LoRA linears with K and N multiples of 4.
-bool lora_mergeable(const mft_model_s* m) {
+bool lora_batched(const mft_model_s* m) {
   const int r = m->c.lora_r;
   if (r != 4 && r != 8 && r != 16 && r != 32) return false;
   // dropout masks the LoRA branch's input only, which a merged W_eff cannot express
@@ -345,10 +357,27 @@ bool lora_mergeable(const mft_model_s* m) {
   return any;
 }
 
+// The merged-weight path serves fp32 W; LoRA linears over fp16-stored W take
+// the rank-r panel path, so W stays 2 bytes per element.  Tuning hook:
+// MFT_LORA_MERGE=0 puts fp32 models on the panel path too, =2 merges fp16 W
+// into an fp32 W_eff as well.
+bool lora_merge(const mft_model_s* m) {
+  static const int hook = [] {
+    const char* e = getenv("MFT_LORA_MERGE");
+    return e ? atoi(e) : 1;
+  }();
+  if (!hook || !lora_batched(m)) return false;
+  if (hook == 2) return true;
+  for (const auto& L : m->L)
+    for (const auto& l : L.lin)
+      if (l.A >= 0 && m->P[l.W].f16) return false;
+  return true;
+}
+
 // q, k and v fuse into one projection when all three are merged LoRA
 // linears and (Qwen2) their biases sit back to back.
 bool qkv_fusable(const mft_model_s* m) {
-  if (m->c.arch == MFT_ARCH_GPT2 || !lora_mergeable(m)) return false;
+  if (m->c.arch == MFT_ARCH_GPT2 || !lora_merge(m)) return false;
   for (const auto& L : m->L) {
     for (int t = 0; t < 3; ++t)
       if (L.lin[t].A < 0) return false;
@@ -420,7 +449,7 @@ void alloc_acts(mft_model_s* m) {
         }
       }
       Layer& L = m->L[l];
-      const bool keep_dy = lora_mergeable(m);
+      const bool keep_dy = lora_batched(m);
       for (int t = 0; t < T_MAX; ++t)
         if (L.lin[t].A >= 0) {
           if (c.lora_dropout > 0.f) L.lin[t].xd = b.f(M * L.lin[t].K);
@@ -528,10 +557,12 @@ float lscale(const mft_model_s* m);
 void build_lora_tables(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
   const int r = c.lora_r;
-  if (!lora_mergeable(m)) return;
+  if (!lora_batched(m)) return;
+  const bool panel = !lora_merge(m);
   const bool gpt2 = c.arch == MFT_ARCH_GPT2;
   const int nt = gpt2 ? 4 : T_MAX;
   size_t weff_floats = 0;
+  if (!panel)
   for (auto& L : m->L)
     for (int t = 0; t < nt; ++t) {
       const Linear& l = L.lin[t];
@@ -542,7 +573,7 @@ void build_lora_tables(mft_model_s* m) {
       }
       weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
     }
-  if (hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
+  if (!panel && hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
     throw Error(MFT_ENOMEM, "merged LoRA weights (" + std::to_string(weff_floats * 4) + " bytes)");
   const float s = lscale(m);
   std::vector<MergeJob> mj;
@@ -587,9 +618,35 @@ void build_lora_tables(mft_model_s* m) {
   std::vector<RankJob> xa_jobs, u_jobs, db_jobs, da_jobs;
   size_t woff = 0;
   int tiles = 0;
+  // input / gradient groups of the panel path: GPT-2's four linears each
+  // alone; q|k|v (input n1), o, gate|up (input n2), down
+  auto group = [&](int t) { return gpt2 ? t : (t < 3 ? 0 : t == T_O ? 1 : t < T_DOWN ? 2 : 3); };
   for (int li = 0; li < c.n_layer; ++li) {
     Layer& L = m->L[li];
     Acts& a = m->A[li];
+    if (panel) {
+      for (int g = 0; g < 4; ++g) {
+        std::vector<RankJob> gx, gu;
+        int first = -1;
+        for (int t = 0; t < nt; ++t) {
+          Linear& l = L.lin[t];
+          if (l.A < 0 || group(t) != g) continue;
+          if (first < 0) first = t;
+          const int64_t dld = a.dy_ld[t];
+          gx.push_back(proj_job(lora_x(m, li, t), l.K, l.K, static_cast<const float*>(m->P[l.A].data), true,
+                                a.xa[t]));
+          gu.push_back(proj_job(a.DY[t], dld, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
+          db_jobs.push_back(outer_job(a.xa[t], a.DY[t], dld, l.N, m->P[l.B].grad, 1, r));
+          da_jobs.push_back(outer_job(a.U[t], lora_x(m, li, t), l.K, l.K, m->P[l.A].grad, l.K, 1));
+        }
+        if (first < 0) continue;
+        for (int t = 0; t < nt; ++t)
+          if (L.lin[t].A >= 0) L.lin[t].u = a.U[t];
+        L.lin[first].xa_batch = add_batch(gx, {});
+        L.lin[first].u_batch = add_batch(gu, {});
+      }
+      continue;
+    }
     for (int t = 0; t < nt; ++t) {
       Linear& l = L.lin[t];
       if (l.A < 0) continue;
@@ -623,8 +680,12 @@ void build_lora_tables(mft_model_s* m) {
       da_jobs.push_back(outer_job(a.U[t], x, l.K, l.K, m->P[l.A].grad, l.K, 1));
     }
   }
-  m->xa_batch = add_batch(xa_jobs, {});
-  m->udb_batch = add_batch(u_jobs, db_jobs);
+  if (panel) {
+    m->db_batch = add_batch({}, db_jobs);
+  } else {
+    m->xa_batch = add_batch(xa_jobs, {});
+    m->udb_batch = add_batch(u_jobs, db_jobs);
+  }
   m->da_batch = add_batch({}, da_jobs);
   const size_t mbytes = (mj.size() * sizeof(MergeJob) + 255) & ~size_t(255);
   const size_t bytes = mbytes + rj.size() * sizeof(RankJob);
@@ -636,7 +697,8 @@ void build_lora_tables(mft_model_s* m) {
   m->n_merge = (int)mj.size();
   m->merge_tiles_total = tiles;
   for (auto& p : pend) m->batches.push_back({d_rank + p.off, p.njobs, p.nproj, p.outer_blocks, p.work});
-  m->merged = true;
+  m->merged = !panel;
+  m->panel = panel;
 }
 
 // ---- timing helpers -------------------------------------------------------------
@@ -713,6 +775,8 @@ DropStream drop_stream(const mft_model_s* m) {
   return DropStream{m->c.lora_dropout, m->c.dropout_seed, m->d_drop_step, m->drop_n_fwd, m->drop_rows};
 }
 
+void run_batch(mft_model_s* m, int idx, int64_t M);
+
 // y = x·W (+ LoRA) + bias (+ resid); with gelu_out, y keeps the
 // pre-activation and gelu_out receives GELU(y) (GPT-2 c_fc).
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
@@ -728,6 +792,18 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   if (lora && m->merged) {  // y = x·W_eff (+ bias, residual)
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
     gemm(m->stream, x, l.K, l.weff, l.weff_ld, false, false, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+    return;
+  }
+  if (lora && m->panel) {  // y = x·W + s·xa·Bᵀ, xa from the group's batched launch
+    run_batch(m, l.xa_batch, M);
+    ep.P = xa;
+    ep.Q = static_cast<const float*>(m->P[l.B].data);
+    ep.r = r;
+    ep.qsn = r;
+    ep.qsj = 1;
+    ep.lscale = lscale(m);
+    Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
+    gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
     return;
   }
   if (lora) {
@@ -772,6 +848,24 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
     return;
   }
   const int r = lora ? m->c.lora_r : 0;
+  if (lora && m->panel) {  // dX = dY·Wᵀ + s·U·A, U from the group's batched launch; dA, dB at the end
+    run_batch(m, l.u_batch, M);
+    if (dx) {
+      GemmEpilogue ep;
+      ep.gelu_grad_of = gelu_grad_of;
+      ep.norm = norm;
+      ep.beta = beta;
+      ep.P = l.u;
+      ep.Q = static_cast<const float*>(m->P[l.A].data);
+      ep.r = r;
+      ep.qsn = 1;
+      ep.qsj = l.K;
+      ep.lscale = lscale(m);
+      Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.K * r);
+      gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
+    }
+    return;
+  }
   float* U = m->ws.ptr;
   Scratch rest = m->ws.offset((size_t)(M * (r > 0 ? r : 1)));
   if (lora) {
@@ -829,7 +923,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
 
 // One table-driven launch of batched rank-r work (see build_lora_tables).
 void run_batch(mft_model_s* m, int idx, int64_t M) {
-  if (!m->merged || idx < 0) return;
+  if (idx < 0) return;
   const mft_model_s::Batch& b = m->batches[idx];
   Timed t(m, CLS_RANK, b.work_per_row * M);
   t.begin();
@@ -1007,7 +1101,7 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   // Where dY of linear t of layer li goes: its own kept buffer for a LoRA
   // linear on the merged path, else the shared temporary `fb`.
   auto dyb = [&](int li, int t, float* fb) -> float* {
-    return m->merged && m->L[li].lin[t].A >= 0 ? m->A[li].DY[t] : fb;
+    return (m->merged || m->panel) && m->L[li].lin[t].A >= 0 ? m->A[li].DY[t] : fb;
   };
   // Residual-stream gradient entering layer li's MLP block (GPT-2 / Qwen2: the
   // dY of c_fc2 / down_proj) and its attention block (dY of c_proj / o_proj).
@@ -1158,7 +1252,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, dn, nullptr, nullptr, 1.f);
     lin_bwd(m, L.lin[T_V], dv, a.n1, a.xa[T_V], M, dn, nullptr, need_dx ? &nb1 : nullptr, 1.f);
   }
-  run_batch(m, m->udb_batch, M);  // U = dY·B and dB += s·dYᵀ·xa of every LoRA linear
+  run_batch(m, m->udb_batch, M);  // merged: U = dY·B and dB += s·dYᵀ·xa of every LoRA linear
+  run_batch(m, m->db_batch, M);   // panel: dB += s·dYᵀ·xa of every LoRA linear
   run_batch(m, m->da_batch, M);   // dA += s·Uᵀ·x of every LoRA linear
 }
 

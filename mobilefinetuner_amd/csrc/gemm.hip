@@ -151,13 +151,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
         const int gn = min(n0 + row, p.N - 1), gk = k0 + kq;
         const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
-        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        if constexpr (B_F16) v = stash_f16(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
         const int gk = k0 + k, gn = n0 + nq;
         const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
-        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        if constexpr (B_F16) v = stash_f16(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
       }
       rb[it] = v;
@@ -188,6 +188,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     for (int it = 0; it < B_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       floatx4 v = rb[it];
+      if constexpr (B_F16) v = unstash_f16(v);
       if constexpr (B_NK) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
         if (tail) {
@@ -450,13 +451,13 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
         const int gn = min(n0 + row, p.N - 1), gk = k0 + kq;
         const int64_t off = (int64_t)gn * p.ldb + (gk < kend ? gk : 0);
-        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        if constexpr (B_F16) v = stash_f16(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
         const int gk = k0 + k, gn = n0 + nq;
         const int64_t off = (int64_t)(gk < kend ? gk : kend - 1) * p.ldb + (gn < p.N ? gn : 0);
-        if constexpr (B_F16) v = widen4(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
+        if constexpr (B_F16) v = stash_f16(*reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.B) + off));
         else v = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.B) + off);
       }
       rb[it] = v;
@@ -487,6 +488,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     for (int it = 0; it < B_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       floatx4 v = rb[it];
+      if constexpr (B_F16) v = unstash_f16(v);
       if constexpr (B_NK) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
         if (tail) {
@@ -593,7 +595,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
       const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
 #pragma unroll
       for (int it = 0; it < B_ITEMS; ++it) {
-        if constexpr (B_F16) rb_set[S][it] = widen4(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
+        if constexpr (B_F16) rb_set[S][it] = stash_f16(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
         else rb_set[S][it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
       }
     };
@@ -613,7 +615,8 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 #pragma unroll
       for (int it = 0; it < B_ITEMS; ++it) {
         const int flat = tid + 256 * it;
-        const floatx4 v = rb_set[S][it];
+        floatx4 v = rb_set[S][it];
+        if constexpr (B_F16) v = unstash_f16(v);
         if constexpr (B_NK) {
           const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
           *reinterpret_cast<floatx4*>(&Bs[row * PB + kq]) = v;
@@ -715,8 +718,8 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     }
 }
 
-// Pipelined GEMM for whole BK-deep panels (BK = 32 or 64) and no rank-r
-// panel.  Workgroup tile BM×64 (BM = 32, 64 or 128), four waves as 2×2, each
+// Pipelined GEMM for whole BK-deep panels (BK = 32 or 64), with an optional
+// rank-r LoRA panel after the last one.  Workgroup tile BM×64 (BM = 32, 64 or 128), four waves as 2×2, each
 // owning (BM/2)×32 outputs as 16×16 v_mfma_f32_16x16x4_f32 tiles.  Panel
 // entry j lives in LDS stage j % 3 of a three-stage ring and is stored two
 // steps before it is multiplied, so during step j every wave already holds
@@ -734,7 +737,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
 // an odd panel count is padded at the front with a virtual entry of zeros
 // stored by the prologue; loads past the last panel re-read the last panel
 // (in bounds) and are never multiplied.  No per-step masks or selects.
-template <int BM, int BK, bool B_NK, bool B_F16, int SITE>
+template <int BM, int BK, bool B_NK, bool B_F16, int SITE, bool RANK>
 __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   constexpr int BN = 64;
   constexpr int WA = BM / 32;
@@ -810,7 +813,7 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
     const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
-      if constexpr (B_F16) rs[S][A_ITEMS + it] = widen4(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
+      if constexpr (B_F16) rs[S][A_ITEMS + it] = stash_f16(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
       else rs[S][A_ITEMS + it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
     }
   };
@@ -820,7 +823,11 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + a_lds[it]) = rs[S][it];
 #pragma unroll
-    for (int it = 0; it < B_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + b_lds[it]) = rs[S][A_ITEMS + it];
+    for (int it = 0; it < B_ITEMS; ++it) {
+      floatx4 v = rs[S][A_ITEMS + it];
+      if constexpr (B_F16) v = unstash_f16(v);
+      *reinterpret_cast<floatx4*>(st + b_lds[it]) = v;
+    }
   };
   struct Frags {
     floatx4 a[WA], b[2];
@@ -920,6 +927,36 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
     step(I1{}, j + 1);
   }
 
+  // Rank-r LoRA term: one more K panel of depth r (padded to a multiple of
+  // 4), staged in the ring's LDS once the last step's barrier has passed;
+  // split 0 only.
+  if (RANK && split == 0) {
+    const int r = p.ep.r, rp = (r + 3) & ~3, pr = rp + 1;
+    float* Ps = smem;
+    float* Qs = smem + BM * pr;
+    for (int i = tid; i < BM * rp; i += 256) {
+      const int row = i / rp, j = i % rp, m = m0 + row;
+      Ps[row * pr + j] = (m < p.M && j < r) ? p.ep.P[(int64_t)m * r + j] : 0.f;
+    }
+    for (int i = tid; i < BN * rp; i += 256) {
+      const int col = i / rp, j = i % rp, n = n0 + col;
+      Qs[col * pr + j] = (n < p.N && j < r) ? p.ep.lscale * p.ep.Q[(int64_t)n * p.ep.qsn + (int64_t)j * p.ep.qsj] : 0.f;
+    }
+    __syncthreads();
+    for (int t = 0; t < rp / 4; ++t) {
+      float fp[WA], fq[2];
+#pragma unroll
+      for (int a = 0; a < WA; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) fq[b] = Qs[(wn + (B_NK ? 16 * b + li : 2 * li + b)) * pr + 4 * t + lg];
+#pragma unroll
+      for (int a = 0; a < WA; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fp[a], fq[b], acc[a][b], 0, 0, 0);
+    }
+  }
+
   const bool split_out = p.partial != nullptr;
 #pragma unroll
   for (int a = 0; a < WA; ++a)
@@ -1006,16 +1043,24 @@ void launch_q_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, 
   }
 }
 
-template <int BM, int BK, int SITE>
-void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
+template <int BM, int BK, int SITE, bool RANK>
+void launch_p_rank(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
   const dim3 block(256);
   if (b_nk) {
-    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, true, true, SITE>, grid, block, s, p);
-    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, true, false, SITE>, grid, block, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, true, true, SITE, RANK>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, true, false, SITE, RANK>, grid, block, s, p);
   } else {
-    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, false, true, SITE>, grid, block, s, p);
-    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, false, false, SITE>, grid, block, s, p);
+    if (b_f16) launch_gemm_kernel(gemm_p_kernel<BM, BK, false, true, SITE, RANK>, grid, block, s, p);
+    else       launch_gemm_kernel(gemm_p_kernel<BM, BK, false, false, SITE, RANK>, grid, block, s, p);
   }
+}
+
+// The rank-r panel is a template switch, so GEMMs without it keep the
+// register allocation of the plain kernel.
+template <int BM, int BK, int SITE>
+void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, bool b_f16) {
+  if (p.ep.P != nullptr) launch_p_rank<BM, BK, SITE, true>(s, p, grid, b_nk, b_f16);
+  else launch_p_rank<BM, BK, SITE, false>(s, p, grid, b_nk, b_f16);
 }
 
 template <int BM, int BK>
@@ -1025,15 +1070,15 @@ void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   const int tiles = p.tiles_m * p.tiles_n;
   p.tiles_per_xcd = (int)cdiv(tiles, 8);
   const dim3 grid(p.tiles_per_xcd * 8, splits);
-  // The pipelined kernel takes whole BK-deep panels in every split and no
-  // rank-r panel; gemm_q_kernel covers K tails and the rank-r panel.  Tuning
-  // hook: MFT_GEMM_PIPE=0 keeps gemm_q_kernel everywhere.
+  // The pipelined kernel takes whole BK-deep panels in every split (and
+  // the rank-r panel); gemm_q_kernel covers K tails.  Tuning hook:
+  // MFT_GEMM_PIPE=0 keeps gemm_q_kernel everywhere.
   static const int pipe_mode = [] {
     const char* e = getenv("MFT_GEMM_PIPE");
     return e ? atoi(e) : 1;
   }();
   const bool whole = p.k_chunk % BK == 0 && p.K % BK == 0;
-  if (pipe_mode != 0 && whole && p.ep.P == nullptr) {
+  if (pipe_mode != 0 && whole) {
     if (p.ep.site == 1) launch_p_variant<BM, BK, 1>(s, p, grid, b_nk, b_f16);
     else launch_p_variant<BM, BK, 0>(s, p, grid, b_nk, b_f16);
     MFT_LAUNCH_CHECK();

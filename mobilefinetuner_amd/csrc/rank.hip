@@ -332,14 +332,18 @@ constexpr int kBatchCols = 256;
 template <int R>
 constexpr int batch_rows_per_wave() { return R <= 16 ? 4 : 2; }
 
-template <int R>
-__device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M) {
+// KS = 1: each wave owns RW rows and the whole of K.  KS = 4: the four
+// waves share RW rows and take interleaved 256-wide slices of K (for batches
+// with few jobs, where one wave per RW rows leaves the GPU mostly idle), and
+// their sums are added in wave order through LDS.
+template <int R, int KS>
+__device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, float* lds) {
   constexpr int RW = batch_rows_per_wave<R>();
   constexpr int V = RW * R;  // 16 .. 64 partial sums per lane
   static_assert(V >= 2 && V <= 64 && (V & (V - 1)) == 0, "butterfly size");
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int m0 = (b * 4 + w) * RW;
-  if (m0 >= M) return;  // no barriers in this role
+  const int m0 = (KS == 1 ? b * 4 + w : b) * RW;
+  if (m0 >= M) return;  // the same m0 for every wave when KS > 1: no wave waits at the barrier
   const int K = jb.K;
   const float* xr[RW];
 #pragma unroll
@@ -351,7 +355,7 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M) {
     for (int j = 0; j < R; ++j) acc[q][j] = 0.f;
   // K is a multiple of 4 (checked on the host), so a 4-vector never crosses a row.
 #pragma unroll 2
-  for (int k = 4 * lane; k < K; k += 256) {
+  for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
     floatx4 xv[RW];
 #pragma unroll
     for (int q = 0; q < RW; ++q) xv[q] = *reinterpret_cast<const floatx4*>(xr[q] + k);
@@ -403,9 +407,21 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M) {
   }
   constexpr int SH = V == 64 ? 0 : V == 32 ? 1 : V == 16 ? 2 : V == 8 ? 3 : V == 4 ? 4 : 5;
   const int vi = lane >> SH;
-  if ((lane & ((1 << SH) - 1)) == 0) {
-    const int q = vi / R, j = vi % R, m = m0 + q;
-    if (m < M) jb.out[(int64_t)m * R + j] = v[0];
+  if constexpr (KS == 1) {
+    if ((lane & ((1 << SH) - 1)) == 0) {
+      const int q = vi / R, j = vi % R, m = m0 + q;
+      if (m < M) jb.out[(int64_t)m * R + j] = v[0];
+    }
+  } else {
+    if ((lane & ((1 << SH) - 1)) == 0) lds[w * V + vi] = v[0];
+    __syncthreads();
+    if (w == 0 && lane < V) {
+      float t = lds[lane];
+#pragma unroll
+      for (int u = 1; u < KS; ++u) t += lds[u * V + lane];
+      const int q = lane / R, j = lane % R, m = m0 + q;
+      if (m < M) jb.out[(int64_t)m * R + j] = t;
+    }
   }
 }
 
@@ -462,15 +478,16 @@ __device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, f
     }
 }
 
-template <int R>
+template <int R, int KS>
 __global__ __launch_bounds__(kBatchThreads) void rank_batch_kernel(const RankJob* __restrict__ jobs, int njobs,
                                                                    int nproj, int M) {
   __shared__ float lds[R * kBatchCols];
-  const int pb = (M + 4 * batch_rows_per_wave<R>() - 1) / (4 * batch_rows_per_wave<R>());
+  constexpr int ROWS = (KS == 1 ? 4 : 1) * batch_rows_per_wave<R>();  // rows per workgroup
+  const int pb = (M + ROWS - 1) / ROWS;
   int b = blockIdx.x;
   if (b < nproj * pb) {
     const int ji = b / pb;
-    batch_proj<R>(jobs[ji], b - ji * pb, M);
+    batch_proj<R, KS>(jobs[ji], b - ji * pb, M, lds);
     return;
   }
   b -= nproj * pb;
@@ -522,19 +539,30 @@ void lora_merge(hipStream_t s, const MergeJob* jobs, int njobs, int total_tiles,
 
 int rank_outer_blocks(int C) { return (int)cdiv(cdiv(C, kBatchCols), 8) * 8; }
 
-void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r) {
-  MFT_CHECK_ARG(jobs && njobs > 0 && M > 0, "empty rank batch");
-  const int rows_per_wg = 4 * (r <= 16 ? 4 : 2);
+template <int KS>
+void rank_batch_launch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r) {
+  const int rows_per_wg = (KS == 1 ? 4 : 1) * (r <= 16 ? 4 : 2);
   const int64_t blocks = (int64_t)nproj * cdiv(M, rows_per_wg) + outer_blocks;
   const dim3 grid((unsigned)blocks), block(kBatchThreads);
   switch (r) {
-    case 4: hipLaunchKernelGGL(rank_batch_kernel<4>, grid, block, 0, s, jobs, njobs, nproj, M); break;
-    case 8: hipLaunchKernelGGL(rank_batch_kernel<8>, grid, block, 0, s, jobs, njobs, nproj, M); break;
-    case 16: hipLaunchKernelGGL(rank_batch_kernel<16>, grid, block, 0, s, jobs, njobs, nproj, M); break;
-    case 32: hipLaunchKernelGGL(rank_batch_kernel<32>, grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 4: hipLaunchKernelGGL((rank_batch_kernel<4, KS>), grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 8: hipLaunchKernelGGL((rank_batch_kernel<8, KS>), grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 16: hipLaunchKernelGGL((rank_batch_kernel<16, KS>), grid, block, 0, s, jobs, njobs, nproj, M); break;
+    case 32: hipLaunchKernelGGL((rank_batch_kernel<32, KS>), grid, block, 0, s, jobs, njobs, nproj, M); break;
     default: MFT_CHECK_ARG(false, "batched rank-r work takes r in {4, 8, 16, 32}");
   }
   MFT_LAUNCH_CHECK();
+}
+
+void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r) {
+  MFT_CHECK_ARG(jobs && njobs > 0 && M > 0, "empty rank batch");
+  // Projection-only batches of under 256 workgroups (the per-layer groups
+  // of the rank-r panel path) split K over the four waves of a workgroup.
+  const int rows_per_wg = 4 * (r <= 16 ? 4 : 2);
+  if (outer_blocks == 0 && (int64_t)nproj * cdiv(M, rows_per_wg) < 256)
+    rank_batch_launch<4>(s, jobs, njobs, nproj, outer_blocks, M, r);
+  else
+    rank_batch_launch<1>(s, jobs, njobs, nproj, outer_blocks, M, r);
 }
 
 void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64_t ysk,
