@@ -60,6 +60,10 @@ def parse():
                     help="time one standalone operator instead of the training step: "
                          "dequant_f16 = fp16 → fp32 widening of --elements values (HBM-bound)")
     ap.add_argument("--elements", type=int, default=256 << 20)
+    ap.add_argument("--shard-budget-mb", type=float, default=0.0,
+                    help="stream the frozen linear weights and the token embedding from pinned host "
+                         "memory through an HBM pool of this size (the reference's --shard_budget_mb); "
+                         "0 keeps every weight resident")
     return ap.parse_args()
 
 
@@ -194,6 +198,9 @@ def main():
                                             Model)
     rc = CONFIGS[args.config]
     mc = rc.model
+    if args.shard_budget_mb > 0:
+        import dataclasses
+        mc = dataclasses.replace(mc, shard_budget=int(args.shard_budget_mb * (1 << 20)))
     torch.cuda.set_device(0)
     tokens = rc.tokens_per_step
     model = Model(mc, tokens)
@@ -250,7 +257,8 @@ def main():
                                f"targets_mask={mc.lora_mask:#x} fwd+bwd+clip+Adam",
                    "config_id": args.config, "batch": rc.batch, "seq_len": rc.seq,
                    "grad_accum": rc.accum, "tokens_per_step": tokens,
-                   "weights": "fp16-stored frozen W" if mc.w_fp16 else "fp32"},
+                   "weights": "fp16-stored frozen W" if mc.w_fp16 else "fp32",
+                   "shard_budget_mb": args.shard_budget_mb or None},
         "algorithmic_tflop_per_step": round(sum(fl.values()) / 1e12, 4),
         "achieved_tflops_step": round(sum(fl.values()) / (ms / 1000.0) / 1e12, 2),
         "last_loss_mean": loss,
@@ -284,6 +292,9 @@ def main():
         result["breakdown"] = br
     else:
         result["roofline"] = None
+    if mc.shard_budget > 0:
+        loads, hits, budget = model.shard_stats()
+        result["shard_store"] = {"budget_bytes": budget, "loads": loads, "hits": hits}
     if args.calibrate_copy_mb:
         n = args.calibrate_copy_mb * (1 << 20) // 4
         src = torch.ones(n, device="cuda")

@@ -49,9 +49,28 @@ typedef struct {
    * element) — the same stream the CPU oracle restates.  0 = off. */
   float lora_dropout;
   uint64_t dropout_seed;
+  /* Shard store (ParameterSharder's require() streaming, README.md:302-329):
+   * > 0 keeps the frozen linear weights and the token embedding in pinned
+   * host memory (fp16 when w_fp16, as --shard_fp16_disk) and streams them
+   * into an HBM pool of this many bytes on demand, least recently used
+   * evicted, the next tensor of the previous step's order prefetched on a
+   * copy stream while the current one is in use.  Must be at least the
+   * largest such tensor (scripts/benchmark/test_sharding_aggressive.sh:
+   * 58-65).  LoRA linears then take the rank-r panel path.  0 = all
+   * parameters resident in HBM. */
+  int64_t shard_budget;
 } mft_model_cfg;
 
 typedef struct mft_model_s* mft_model;
+
+/* Shard store statistics since creation: tensors copied host→HBM (loads),
+ * uses served by a resident copy (hits), and the pool size.  All zero when
+ * the model is not sharded. */
+int mft_model_shard_stats(mft_model m, int64_t* loads, int64_t* hits, int64_t* budget);
+/* Drops every HBM copy of a streamed tensor (after the host copies were
+ * written through mft_model_param_info's data pointers).  A no-op when the
+ * model is not sharded. */
+int mft_model_shard_reset(mft_model m);
 
 /* max_tokens: capacity in tokens of one fused fwd/bwd pass (activations are
  * sized for it).  stream: hipStream_t or NULL. */

@@ -29,7 +29,7 @@ class ModelCfg(C.Structure):
         ("lora_mask", C.c_int), ("norm_eps", C.c_float), ("rope_theta", C.c_double),
         ("rope_local_theta", C.c_double), ("sliding_pattern", C.c_int),
         ("sliding_window", C.c_int), ("attn_scale", C.c_float), ("w_fp16", C.c_int),
-        ("lora_dropout", C.c_float), ("dropout_seed", C.c_uint64),
+        ("lora_dropout", C.c_float), ("dropout_seed", C.c_uint64), ("shard_budget", C.c_int64),
     ]
 
 
@@ -99,6 +99,8 @@ _SIGS = {
     "mft_model_activation": (_I, [_P, _I, C.c_char_p, C.POINTER(_P), C.POINTER(_L), C.POINTER(_L), C.POINTER(_L)]),
     "mft_model_set_timing": (_I, [_P, _I]),
     "mft_model_set_training": (_I, [_P, _I]),
+    "mft_model_shard_stats": (_I, [_P, C.POINTER(_L), C.POINTER(_L), C.POINTER(_L)]),
+    "mft_model_shard_reset": (_I, [_P]),
     "mft_model_timing": (_I, [_P, _I, C.POINTER(_D), C.POINTER(_D), C.POINTER(_L)]),
     "mft_model_reset_timing": (_I, [_P]),
 }

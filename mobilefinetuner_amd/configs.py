@@ -42,6 +42,7 @@ class ModelConfig:
     w_fp16: int = 0
     lora_dropout: float = 0.0
     dropout_seed: int = 0
+    shard_budget: int = 0
 
     def to_ctypes(self):
         from ._lib import ModelCfg
@@ -49,7 +50,8 @@ class ModelConfig:
                         self.head_dim, self.d_ff, self.max_pos, self.vocab, self.lora_r,
                         self.lora_alpha, self.lora_mask, self.norm_eps, self.rope_theta,
                         self.rope_local_theta, self.sliding_pattern, self.sliding_window,
-                        self.attn_scale, self.w_fp16, self.lora_dropout, self.dropout_seed)
+                        self.attn_scale, self.w_fp16, self.lora_dropout, self.dropout_seed,
+                        self.shard_budget)
 
     def as_dict(self):
         return dataclasses.asdict(self)

@@ -130,14 +130,16 @@ int mft_free(void* ptr) {
 int mft_memcpy_h2d(mft_handle h, void* dst, const void* src, size_t bytes) {
   return guarded([&] {
     require_handle(h);
-    MFT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, h->stream));
+    // Default: the runtime reads the pointer kinds (a streamed model's
+    // frozen tensors live in pinned host memory)
+    MFT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, h->stream));
     MFT_HIP(hipStreamSynchronize(h->stream));
   });
 }
 int mft_memcpy_d2h(mft_handle h, void* dst, const void* src, size_t bytes) {
   return guarded([&] {
     require_handle(h);
-    MFT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream));
+    MFT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, h->stream));
     MFT_HIP(hipStreamSynchronize(h->stream));
   });
 }

@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -38,7 +39,9 @@ struct Param {
   int64_t numel = 0;
   bool trainable = false, f16 = false;
   InitKind init = INIT_NORMAL;
-  size_t offset = 0;  // bytes in the frozen arena, or floats in the LoRA arrays
+  bool streamable = false;  // a linear weight or the token embedding (shard store)
+  int shard = -1;           // its shard store entry when the model is sharded
+  size_t offset = 0;  // bytes in the frozen arena (or the host store), or floats in the LoRA arrays
   void* data = nullptr;
   float* grad = nullptr;
 };
@@ -101,8 +104,37 @@ struct TimedLaunch {
 
 using namespace mft;
 
+// Frozen weights streamed from pinned host memory into an HBM pool
+// (ParameterSharder's require(), README.md:302-329).  Every use takes the
+// tensor's pool copy (loading it first when absent: least recently used
+// entries are evicted until a first-fit block is free), makes the compute
+// stream wait for the copy, and records a use event after the launch, which
+// the copy stream waits on before it overwrites the block.  After each use
+// the tensor that followed it in the previous pass is prefetched.
+struct ShardStore {
+  int64_t budget = 0;
+  char* pool = nullptr;  // device, budget bytes
+  char* host = nullptr;  // pinned host memory holding every streamed tensor
+  hipStream_t copy = nullptr;
+  struct Entry {
+    int param = -1;
+    size_t bytes = 0;
+    int64_t off = -1;  // pool offset while resident
+    uint64_t last = 0;  // LRU clock of the last use or prefetch
+    bool held = false;  // in use by a launch being enqueued
+    bool used_valid = false, ready_valid = false;
+    hipEvent_t ready = nullptr, used = nullptr;
+  };
+  std::vector<Entry> ents;
+  std::map<int64_t, int64_t> free_blocks;  // pool offset → bytes
+  uint64_t clock = 0;
+  std::vector<int> seq, prev;  // entries in use order: this pass and the previous one
+  int64_t loads = 0, hits = 0;
+};
+
 struct mft_model_s {
   mft_model_cfg c{};
+  ShardStore sh;
   hipStream_t stream = nullptr;
   int64_t max_tokens = 0;
   std::vector<Param> P;
@@ -229,6 +261,7 @@ void add_linear(mft_model_s* m, Linear& l, const std::string& pfx, const char* n
   l.K = K;
   l.N = N;
   l.W = add_param(m, pfx + "." + nm + ".weight", K, N, false, m->c.w_fp16 != 0, INIT_NORMAL);
+  m->P[l.W].streamable = true;
   if (bias) l.b = add_param(m, pfx + "." + nm + ".bias", N, 0, false, false, INIT_NORMAL);
   if (lora && m->c.lora_r > 0) {
     l.A = add_param(m, pfx + "." + nm + ".lora_A", m->c.lora_r, K, true, false, INIT_LORA_A);
@@ -243,6 +276,7 @@ void build_params(mft_model_s* m) {
   m->L.resize(c.n_layer);
   if (c.arch == MFT_ARCH_GPT2) {
     m->wte = add_param(m, "wte", c.vocab, d, false, f16, INIT_NORMAL);
+    m->P[m->wte].streamable = true;
     m->wpe = add_param(m, "wpe", c.max_pos, d, false, false, INIT_NORMAL);
     for (int i = 0; i < c.n_layer; ++i) {
       Layer& L = m->L[i];
@@ -263,6 +297,7 @@ void build_params(mft_model_s* m) {
   const bool qwen = c.arch == MFT_ARCH_QWEN2;
   const InitKind norm_init = qwen ? INIT_ONE : INIT_ZERO;
   m->wte = add_param(m, "embed_tokens.weight", c.vocab, d, false, f16, INIT_NORMAL);
+  m->P[m->wte].streamable = true;
   for (int i = 0; i < c.n_layer; ++i) {
     Layer& L = m->L[i];
     const std::string pfx = "layers." + std::to_string(i);
@@ -295,16 +330,50 @@ void assign_dropout_streams(mft_model_s* m) {
     for (int t = 0; t < T_MAX; ++t) m->L[li].lin[t].lid = (int)li * 8 + t;
 }
 
+size_t shard_round(size_t b) { return (b + 255) & ~size_t(255); }
+
 void alloc_params(mft_model_s* m) {
-  size_t fb = 0;
+  size_t fb = 0, hb = 0, largest = 0;
   int64_t ln = 0;
-  for (auto& p : m->P) {
+  ShardStore& sh = m->sh;
+  const bool sharded = m->c.shard_budget > 0;
+  for (size_t i = 0; i < m->P.size(); ++i) {
+    Param& p = m->P[i];
+    const size_t bytes = (size_t)p.numel * (p.f16 ? 2 : 4);
     if (p.trainable) {
       p.offset = (size_t)ln;
       ln += (p.numel + 63) / 64 * 64;
+    } else if (sharded && p.streamable) {
+      p.offset = hb;
+      hb += shard_round(bytes);
+      largest = std::max(largest, shard_round(bytes));
+      p.shard = (int)sh.ents.size();
+      ShardStore::Entry e;
+      e.param = (int)i;
+      e.bytes = bytes;
+      sh.ents.push_back(e);
     } else {
       p.offset = fb;
-      fb += ((size_t)p.numel * (p.f16 ? 2 : 4) + 255) & ~size_t(255);
+      fb += shard_round(bytes);
+    }
+  }
+  if (sharded) {
+    const int64_t budget = m->c.shard_budget & ~int64_t(255);
+    if (budget < (int64_t)largest)
+      throw Error(MFT_EINVAL, "shard_budget (" + std::to_string(m->c.shard_budget) +
+                                  " bytes) is below the largest streamed tensor (" + std::to_string(largest) +
+                                  " bytes)");
+    sh.budget = budget;
+    if (hipHostMalloc(reinterpret_cast<void**>(&sh.host), hb ? hb : 256, hipHostMallocDefault) != hipSuccess)
+      throw Error(MFT_ENOMEM, "shard store host memory (" + std::to_string(hb) + " bytes)");
+    std::memset(sh.host, 0, hb ? hb : 256);
+    if (hipMalloc(reinterpret_cast<void**>(&sh.pool), (size_t)budget) != hipSuccess)
+      throw Error(MFT_ENOMEM, "shard store pool (" + std::to_string(budget) + " bytes)");
+    sh.free_blocks[0] = budget;
+    MFT_HIP(hipStreamCreateWithFlags(&sh.copy, hipStreamNonBlocking));
+    for (auto& e : sh.ents) {
+      MFT_HIP(hipEventCreateWithFlags(&e.ready, hipEventDisableTiming));
+      MFT_HIP(hipEventCreateWithFlags(&e.used, hipEventDisableTiming));
     }
   }
   m->frozen_bytes = fb;
@@ -327,10 +396,138 @@ void alloc_params(mft_model_s* m) {
     if (p.trainable) {
       p.data = m->lora_p + p.offset;
       p.grad = m->lora_g + p.offset;
+    } else if (p.shard >= 0) {
+      p.data = sh.host + p.offset;
     } else {
       p.data = static_cast<char*>(m->frozen) + p.offset;
     }
   }
+}
+
+// ---- shard store --------------------------------------------------------------
+int64_t shard_alloc(ShardStore& sh, size_t need) {
+  for (auto it = sh.free_blocks.begin(); it != sh.free_blocks.end(); ++it) {
+    if ((size_t)it->second >= need) {
+      const int64_t off = it->first, rest = it->second - (int64_t)need;
+      sh.free_blocks.erase(it);
+      if (rest > 0) sh.free_blocks[off + (int64_t)need] = rest;
+      return off;
+    }
+  }
+  return -1;
+}
+
+void shard_free(ShardStore& sh, int64_t off, int64_t bytes) {
+  auto it = sh.free_blocks.emplace(off, bytes).first;
+  auto nx = std::next(it);
+  if (nx != sh.free_blocks.end() && it->first + it->second == nx->first) {
+    it->second += nx->second;
+    sh.free_blocks.erase(nx);
+  }
+  if (it != sh.free_blocks.begin()) {
+    auto pv = std::prev(it);
+    if (pv->first + pv->second == it->first) {
+      pv->second += it->second;
+      sh.free_blocks.erase(it);
+    }
+  }
+}
+
+// Makes entry i resident: evicts the least recently used entries no launch
+// holds until a first-fit block is free, then copies the tensor on the copy
+// stream, behind the last uses of every evicted block.
+void shard_load(mft_model_s* m, int i) {
+  ShardStore& sh = m->sh;
+  const size_t need = shard_round(sh.ents[i].bytes);
+  int64_t off;
+  while ((off = shard_alloc(sh, need)) < 0) {
+    int v = -1;
+    for (int j = 0; j < (int)sh.ents.size(); ++j) {
+      const ShardStore::Entry& c = sh.ents[j];
+      if (j != i && c.off >= 0 && !c.held && (v < 0 || c.last < sh.ents[v].last)) v = j;
+    }
+    if (v < 0) throw Error(MFT_EINVAL, "shard budget too small for the tensors one launch uses");
+    ShardStore::Entry& ev = sh.ents[v];
+    if (ev.used_valid) MFT_HIP(hipStreamWaitEvent(sh.copy, ev.used, 0));
+    shard_free(sh, ev.off, (int64_t)shard_round(ev.bytes));
+    ev.off = -1;
+  }
+  ShardStore::Entry& e = sh.ents[i];
+  e.off = off;
+  MFT_HIP(hipMemcpyAsync(sh.pool + off, sh.host + m->P[e.param].offset, e.bytes, hipMemcpyHostToDevice, sh.copy));
+  MFT_HIP(hipEventRecord(e.ready, sh.copy));
+  e.ready_valid = true;
+  ++sh.loads;
+}
+
+// Device address of frozen parameter p for the next launch on the model's
+// stream (the shard store's pool copy when p is streamed); release() follows
+// the launch.
+struct WeightUse {
+  mft_model_s* m;
+  int p;
+  const void* ptr;
+  WeightUse(mft_model_s* mm, int pi) : m(mm), p(pi) {
+    const int i = m->P[p].shard;
+    if (i < 0) {
+      ptr = m->P[p].data;
+      return;
+    }
+    ShardStore& sh = m->sh;
+    ShardStore::Entry& e = sh.ents[i];
+    e.held = true;
+    e.last = ++sh.clock;
+    if (e.off < 0) shard_load(m, i);
+    else ++sh.hits;
+    if (e.ready_valid) MFT_HIP(hipStreamWaitEvent(m->stream, e.ready, 0));
+    sh.seq.push_back(i);
+    ptr = sh.pool + e.off;
+  }
+  ~WeightUse() {
+    const int i = m->P[p].shard;
+    if (i < 0) return;
+    ShardStore& sh = m->sh;
+    ShardStore::Entry& e = sh.ents[i];
+    e.held = false;
+    if (hipEventRecord(e.used, m->stream) != hipSuccess) return;
+    e.used_valid = true;
+    // prefetch the tensor that followed this use in the previous pass
+    const size_t pos = sh.seq.size();
+    if (pos < sh.prev.size()) {
+      ShardStore::Entry& n = sh.ents[sh.prev[pos]];
+      if (n.off < 0 && !n.held) {
+        n.last = ++sh.clock;
+        try {
+          shard_load(m, sh.prev[pos]);
+        } catch (...) {
+        }
+      }
+    }
+  }
+};
+
+// A new pass (forward, then its backward) starts a new use order.
+void shard_begin(mft_model_s* m) {
+  ShardStore& sh = m->sh;
+  if (!sh.copy || sh.seq.empty()) return;
+  sh.prev.swap(sh.seq);
+  sh.seq.clear();
+}
+
+// Drops every pool copy (host copies rewritten, or the pool reused as scratch).
+void shard_reset(mft_model_s* m) {
+  ShardStore& sh = m->sh;
+  if (!sh.copy) return;
+  MFT_HIP(hipStreamSynchronize(m->stream));
+  MFT_HIP(hipStreamSynchronize(sh.copy));
+  for (auto& e : sh.ents) {
+    e.off = -1;
+    e.held = e.used_valid = e.ready_valid = false;
+  }
+  sh.free_blocks.clear();
+  sh.free_blocks[0] = sh.budget;
+  sh.seq.clear();
+  sh.prev.clear();
 }
 
 bool layer_local(const mft_model_cfg& c, int i) {
@@ -367,6 +564,7 @@ bool lora_merge(const mft_model_s* m) {
     return e ? atoi(e) : 1;
   }();
   if (!hook || !lora_batched(m)) return false;
+  if (m->c.shard_budget > 0) return false;  // streamed W: no whole-model merge
   if (hook == 2) return true;
   for (const auto& L : m->L)
     for (const auto& l : L.lin)
@@ -782,6 +980,7 @@ void run_batch(mft_model_s* m, int idx, int64_t M);
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
              const float* resid, float* gelu_out = nullptr, const RowNorm* norm = nullptr) {
   const Param& W = m->P[l.W];
+  const WeightUse wu(m, l.W);
   const bool lora = l.A >= 0;
   const int r = lora ? m->c.lora_r : 0;
   GemmEpilogue ep;
@@ -803,7 +1002,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     ep.qsj = 1;
     ep.lscale = lscale(m);
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
-    gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+    gemm(m->stream, x, l.K, wu.ptr, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
     return;
   }
   if (lora) {
@@ -825,7 +1024,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     ep.lscale = lscale(m);
   }
   Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
-  gemm(m->stream, x, l.K, W.data, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+  gemm(m->stream, x, l.K, wu.ptr, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
 }
 
 // dx = dy·Wᵀ (+ LoRA) (+ beta·dx); with gelu_grad_of = the pre-activation
@@ -835,6 +1034,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
              int64_t M, float* dx, const float* gelu_grad_of = nullptr, const RowNorm* norm = nullptr,
              float beta = 0.f) {
   const Param& W = m->P[l.W];
+  const WeightUse wu(m, l.W);
   const bool lora = l.A >= 0;
   if (lora && m->merged) {  // dX = dY·W_effᵀ; dA/dB come from the batched launches
     if (dx) {
@@ -862,7 +1062,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
       ep.qsj = l.K;
       ep.lscale = lscale(m);
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.K * r);
-      gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
+      gemm(m->stream, dy, l.N, wu.ptr, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
     }
     return;
   }
@@ -882,7 +1082,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
       GemmEpilogue ep;
       ep.beta = beta;
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K);
-      gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
+      gemm(m->stream, dy, l.N, wu.ptr, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
       dropout_dx(m->stream, dx, M, l.K, U, static_cast<const float*>(m->P[l.A].data), r, lscale(m),
                  drop_stream(m), l.lid);
       if (gelu_grad_of) gelu_grad_scale(m->stream, dx, gelu_grad_of, M * l.K);
@@ -909,7 +1109,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
       ep.lscale = lscale(m);
     }
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.K * r);
-    gemm(m->stream, dy, l.N, W.data, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
+    gemm(m->stream, dy, l.N, wu.ptr, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, rest, t.events());
   }
   if (lora) {
     Timed tr(m, CLS_RANK, 4.0 * M * (l.K + l.N + 2 * r));  // bytes: read x, dy, U, xa
@@ -974,9 +1174,13 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   const hipStream_t s = m->stream;
   const Param& E = m->P[m->wte];
   m->last_rows = M;
+  shard_begin(m);
   merge_lora(m);  // A, B (or W) may have changed since the last forward
-  embed(s, ids, M, S, E.data, c.vocab, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
-        gemma ? std::sqrt((float)d) : 1.f, m->A[0].x, m->d_err);
+  {
+    const WeightUse we(m, m->wte);
+    embed(s, ids, M, S, we.ptr, c.vocab, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
+          gemma ? std::sqrt((float)d) : 1.f, m->A[0].x, m->d_err);
+  }
   // Input norm of layer li (li == n_layer: the final norm).  GPT-2 and Qwen2
   // run it inside the GEMM that produced its input (the previous layer's
   // residual-fused down projection); Gemma3's post-norms sit in between.
@@ -1067,10 +1271,11 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   }
   if (gemma) row_norm(s, m->h_final, M, d, norm1(c.n_layer));
   // LM head: logits = hf · Eᵀ, E [V, d] is the [N, K] operand.
+  const WeightUse wh(m, m->wte);
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
   GemmEpilogue head;
   head.site = 1;
-  gemm(s, m->hf, d, E.data, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, head, m->ws,
+  gemm(s, m->hf, d, wh.ptr, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, head, m->ws,
        t.events());
 }
 
@@ -1133,7 +1338,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     GemmEpilogue head;
     head.site = 1;
     head.norm = &nf;
-    gemm(s, m->logits, m->ldv, E.data, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
+    const WeightUse wh(m, m->wte);
+    gemm(s, m->logits, m->ldv, wh.ptr, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
          t.events());
   }
   const int64_t nf = M * c.d_ff;
@@ -1409,7 +1615,32 @@ int mft_model_destroy(mft_model m) {
                     m->weff_mem, m->tables};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
+    ShardStore& sh = m->sh;
+    if (sh.copy) (void)hipStreamSynchronize(sh.copy);
+    for (auto& e : sh.ents) {
+      if (e.ready) (void)hipEventDestroy(e.ready);
+      if (e.used) (void)hipEventDestroy(e.used);
+    }
+    if (sh.copy) (void)hipStreamDestroy(sh.copy);
+    if (sh.pool) (void)hipFree(sh.pool);
+    if (sh.host) (void)hipHostFree(sh.host);
     delete m;
+  });
+}
+
+int mft_model_shard_stats(mft_model m, int64_t* loads, int64_t* hits, int64_t* budget) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    if (loads) *loads = m->sh.loads;
+    if (hits) *hits = m->sh.hits;
+    if (budget) *budget = m->sh.budget;
+  });
+}
+
+int mft_model_shard_reset(mft_model m) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    shard_reset(m);
   });
 }
 
@@ -1443,13 +1674,17 @@ int mft_model_param_info(mft_model m, int i, const char** name, int* ndim, int64
 int mft_model_init_params(mft_model m, uint64_t seed, float std, float a_std, float b_std) {
   return guarded([&] {
     if (!m) throw Error(MFT_EINVAL, "null model");
+    shard_reset(m);  // streamed tensors are generated in the pool, then copied to the host store
     for (size_t i = 0; i < m->P.size(); ++i) {
       Param& p = m->P[i];
       const uint64_t ps = seed * 0x100000001b3ull + i * 0x9e3779b97f4a7c15ull;
+      void* dst = p.shard >= 0 ? static_cast<void*>(m->sh.pool) : p.data;
       switch (p.init) {
         case INIT_NORMAL:
-          if (p.f16) fill_normal_f16(m->stream, static_cast<uint16_t*>(p.data), p.numel, ps, std);
-          else fill_normal(m->stream, static_cast<float*>(p.data), p.numel, ps, std, 0.f);
+          if (p.f16) fill_normal_f16(m->stream, static_cast<uint16_t*>(dst), p.numel, ps, std);
+          else fill_normal(m->stream, static_cast<float*>(dst), p.numel, ps, std, 0.f);
+          if (p.shard >= 0)
+            MFT_HIP(hipMemcpyAsync(p.data, dst, (size_t)p.numel * (p.f16 ? 2 : 4), hipMemcpyDeviceToHost, m->stream));
           break;
         case INIT_ONE: fill_const(m->stream, static_cast<float*>(p.data), p.numel, 1.f); break;
         case INIT_ZERO: fill_const(m->stream, static_cast<float*>(p.data), p.numel, 0.f); break;
@@ -1547,6 +1782,9 @@ int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps, flo
 int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, const int32_t* labels,
                          int n_micro, int seqs_per_micro, int S, float upstream, float lr, float b1,
                          float b2, float eps, float wd, float clip, int use_graph) {
+  // a streamed (sharded) model's pool addresses change from step to step:
+  // no captured graph
+  if (m && m->sh.budget > 0) use_graph = 0;
   return guarded([&] {
     if (!m || !ids || !labels) throw Error(MFT_EINVAL, "null argument");
     const int nseq = n_micro * seqs_per_micro;

@@ -74,6 +74,8 @@ class Model:
             raise ValueError(f"{name}: expected {n} elements, got {a.size}")
         call("mft_memcpy_h2d", self._handle(), C.c_void_p(p["data"]), a.ctypes.data_as(C.c_void_p),
              a.nbytes)
+        if self.cfg.shard_budget > 0 and not p["trainable"]:
+            call("mft_model_shard_reset", self.h)  # drop stale HBM copies of streamed tensors
 
     def get(self, name: str, grad: bool = False):
         import numpy as np
@@ -126,6 +128,12 @@ class Model:
         call("mft_model_train_step", self.h, _dev(ids, torch.int32, "ids"),
              _dev(mask, torch.float32, "mask"), _dev(labels, torch.int32, "labels"), n_micro,
              seqs_per_micro, S, upstream, lr, b1, b2, eps, wd, clip, int(graph))
+
+    def shard_stats(self):
+        """(loads, hits, budget) of the shard store (zeros when not sharded)."""
+        lo, hi, bu = C.c_int64(), C.c_int64(), C.c_int64()
+        call("mft_model_shard_stats", self.h, C.byref(lo), C.byref(hi), C.byref(bu))
+        return lo.value, hi.value, bu.value
 
     def set_training(self, on: bool):
         """Training forwards apply LoRA dropout; evaluation forwards do not."""
