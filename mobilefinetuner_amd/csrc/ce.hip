@@ -67,10 +67,15 @@ __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2)
 
 // One workgroup per logits row.  The row is walked as an aligned float4 body
 // (rows start at any 4-byte offset when V is odd) plus a scalar head and
-// tail; each thread keeps U float4 loads in flight per step and folds each
-// group of 4·U values into its running pair with one rescale.  The gradient
-// sweep re-reads the row (from L2 / MALL) and writes dlogits in place.
-template <int BLOCK>
+// tail.  The first H·BLOCK float4 of the body stay in registers from the
+// statistics sweep to the gradient sweep (each thread issues its H loads at
+// once), so only the rest of the row is read twice: a row of up to
+// 4·H·BLOCK values (GPT-2's 50257 with H = 13) moves through HBM once
+// each way.  The rest is streamed with U float4 loads in flight per thread,
+// each group of 4·U values folded into the thread's running (max, Σ) pair
+// with one rescale, and re-read by the gradient sweep, which writes dlogits
+// in place.
+template <int BLOCK, int H>
 __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S,
     int64_t V, int64_t ld, int ignore_index, float upstream, int64_t norm_count,
@@ -97,7 +102,29 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
 
   float m = -FLT_MAX, sum = 0.f;
   for (int64_t j = tid; j < head; j += BLOCK) merge_ms(m, sum, x[j] * kLog2e, 1.f);
-  for (int64_t b = tid; b < n4; b += (int64_t)BLOCK * U) {
+  // held part: float4 q = tid + BLOCK·i, i < H
+  floatx4 hv[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const int64_t q = tid + (int64_t)BLOCK * i;
+    hv[i] = q < n4 ? x4[q] : floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+  {
+    float mx = m;
+#pragma unroll
+    for (int i = 0; i < H; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = fmaxf(mx, hv[i][e] * kLog2e);
+    float acc = sum * __builtin_amdgcn_exp2f(m - mx);
+#pragma unroll
+    for (int i = 0; i < H; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc += __builtin_amdgcn_exp2f(fmaf(hv[i][e], kLog2e, -mx));
+    sum = acc;
+    m = mx;
+  }
+  const int64_t rest0 = (int64_t)BLOCK * H;  // first streamed float4
+  for (int64_t b = rest0 + tid; b < n4; b += (int64_t)BLOCK * U) {
     floatx4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -149,7 +176,19 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     dx[j] = (j == label ? p - 1.f : p) * g;
   }
   floatx4* d4 = reinterpret_cast<floatx4*>(dx + head);
-  for (int64_t b = tid; b < n4; b += (int64_t)BLOCK * U) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const int64_t q = tid + (int64_t)BLOCK * i;
+    if (q >= n4) continue;
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(hv[i][e], kLog2e, -lse2));
+      o[e] = (head + 4 * q + e == label ? p - 1.f : p) * g;
+    }
+    d4[q] = o;
+  }
+  for (int64_t b = rest0 + tid; b < n4; b += (int64_t)BLOCK * U) {
     floatx4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -203,8 +242,14 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   hipLaunchKernelGGL(ce_count_kernel, dim3(1), dim3(1024), 0, s, labels, B, S, V, ignore_index, count_scratch,
                      bad_label);
   MFT_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ce_row_kernel<1024>, dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V, ld,
-                     ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
+  // rows of up to 13·4096 values are held whole in registers (GPT-2's
+  // 50257); wider rows keep their first 16·4096 values there
+  if (V <= 13 * 4096)
+    hipLaunchKernelGGL((ce_row_kernel<1024, 13>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
+                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
+  else
+    hipLaunchKernelGGL((ce_row_kernel<1024, 16>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
+                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,
                      (const int64_t*)count_scratch, n_valid);
