@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=1235)
     ap.add_argument("--lr", type=float, default=2e-4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-api-bench", action="store_true",
+                    help="skip the operators-API driver-loop line (GPT-2 small only)")
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--graph", action="store_true",
@@ -191,6 +193,18 @@ def main():
         sys.exit(2)
     if args.op:
         return op_bench(args)
+    # The operators API (the boundary the reference's drivers compile
+    # against) timed by its own driver-loop program, run as a child process
+    # before this process touches the GPU.
+    api = None
+    exe = os.path.join(ROOT, "mobilefinetuner_amd", "bin", "api_bench")
+    if args.config == "gpt2s" and not args.no_api_bench and os.path.exists(exe):
+        import subprocess
+        r = subprocess.run([exe, "4", "128", "1", str(max(args.steps, 5)), str(max(args.warmup, 1))],
+                           capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError("api_bench failed: " + r.stderr[-2000:])
+        api = json.loads(r.stdout.strip().splitlines()[-1])
     import torch
 
     from mobilefinetuner_amd.configs import CONFIGS, step_flops
@@ -292,6 +306,8 @@ def main():
         result["breakdown"] = br
     else:
         result["roofline"] = None
+    if api is not None:
+        result["operators_api"] = api
     if mc.shard_budget > 0:
         loads, hits, budget = model.shard_stats()
         result["shard_store"] = {"budget_bytes": budget, "loads": loads, "hits": hits}
