@@ -33,6 +33,10 @@ size_t dtype_size(DType t);
 
 class Tensor;
 using TensorPtr = std::shared_ptr<Tensor>;
+// One host mirror shared by views that tile a device range (a model's LoRA
+// parameter or gradient arena): the first host access copies the whole
+// range once, and host edits go back in one copy before the next device use.
+struct MirrorGroup;
 
 namespace autograd {
 class Node;
@@ -48,6 +52,11 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
   // last dimension's rows are `pitch` elements apart (pitch >= last dim).
   static TensorPtr view(std::vector<int64_t> shape, DType dtype, void* device_ptr, int64_t pitch,
                         std::shared_ptr<void> owner);
+  // A mirror group over device bytes [base, base + bytes), and a contiguous
+  // view inside it whose host copy is the group's.
+  static std::shared_ptr<MirrorGroup> mirror_group(void* base, size_t bytes);
+  static TensorPtr view(std::vector<int64_t> shape, DType dtype, void* device_ptr, std::shared_ptr<void> owner,
+                        std::shared_ptr<MirrorGroup> group);
   ~Tensor();
   Tensor(const Tensor&) = delete;
   Tensor& operator=(const Tensor&) = delete;
@@ -64,12 +73,12 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
   template <class T>
   T* data() {
     sync_host(true);
-    return reinterpret_cast<T*>(host_.data());
+    return reinterpret_cast<T*>(host_ptr());
   }
   template <class T>
   const T* data() const {
     sync_host(false);
-    return reinterpret_cast<const T*>(host_.data());
+    return reinterpret_cast<const T*>(host_ptr());
   }
   // Device pointer (pending host edits are copied back first).  The const
   // form does not mark the device copy as changed.
@@ -96,12 +105,17 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
 
   // Device memory owner of a view (the model whose arena it points into).
   const std::shared_ptr<void>& owner() const { return owner_; }
+  // Mirror group of a grouped view (null otherwise) and the view's byte
+  // offset in it.
+  const std::shared_ptr<MirrorGroup>& mirror() const { return group_; }
+  size_t mirror_offset() const { return group_off_; }
 
  private:
   Tensor() = default;
   void init_shape(std::vector<int64_t> shape, DType dtype, Device device);
   void sync_host(bool will_write) const;
   void upload_if_dirty() const;
+  char* host_ptr() const;
 
   std::vector<int64_t> shape_;
   int64_t numel_ = 0;
@@ -114,6 +128,8 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
   // host mirror: 0 = stale, 1 = equal to the device, 2 = newer than the device
   mutable std::vector<char> host_;
   mutable int host_state_ = 0;
+  std::shared_ptr<MirrorGroup> group_;  // shared host mirror (grouped views)
+  size_t group_off_ = 0;
 
   bool requires_grad_ = false;
   bool retain_grad_ = false;

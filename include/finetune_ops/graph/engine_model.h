@@ -95,6 +95,7 @@ class EngineModel {
   int last_S_ = 0;  // sequence length of the last forward
   std::shared_ptr<EngineState> st_;
   std::vector<TensorPtr> views_, grad_views_;  // parameter / gradient views, created on demand
+  std::shared_ptr<MirrorGroup> lora_pg_, lora_gg_;  // host mirrors of the LoRA parameter / gradient arenas
   std::map<std::string, TensorPtr> pending_;  // assigned before the engine exists
 };
 

@@ -39,9 +39,14 @@ class Adam {
 
  private:
   struct State;
+  struct GroupState;
   AdamConfig cfg_;
   int t_ = 0;
   std::unordered_map<const Tensor*, std::unique_ptr<State>> state_;
+  // moments of parameters that tile a mirror group (a model's LoRA arena)
+  // live in one arena per group: per-tensor states are views into it, and a
+  // step over every member of the group is one launch
+  std::unordered_map<const MirrorGroup*, std::unique_ptr<GroupState>> gstate_;
 };
 
 }  // namespace ops

@@ -10,6 +10,7 @@
 #include <cstring>
 #include <fstream>
 #include <functional>
+#include <map>
 #include <stdexcept>
 #include <string>
 #include <sys/stat.h>
@@ -118,7 +119,72 @@ Tensor::~Tensor() {
   if (owns_ && dev_) (void)hipFree(dev_);
 }
 
+struct MirrorGroup {
+  char* dev = nullptr;
+  size_t bytes = 0;
+  std::vector<char> host;
+  int state = 0;    // 0 = stale, 1 = equal to the device, 2 = newer than the device
+  int members = 0;  // views created in the group
+  // zero_grad() requests not yet applied on the device: byte offset → bytes.
+  // They run at the group's next device or host access, as one fill over the
+  // whole range when every member asked (the drivers' zero_grad loop).
+  std::map<size_t, size_t> zeros;
+};
+
+namespace {
+void flush_zeros(MirrorGroup& g) {
+  if (g.zeros.empty()) return;
+  if ((int)g.zeros.size() == g.members) {
+    mft_check(mft_fill(detail::handle(), reinterpret_cast<float*>(g.dev), (int64_t)(g.bytes / 4), 0.f), "mft_fill");
+  } else {
+    for (const auto& z : g.zeros)
+      mft_check(mft_fill(detail::handle(), reinterpret_cast<float*>(g.dev + z.first), (int64_t)(z.second / 4), 0.f),
+                "mft_fill");
+  }
+  g.zeros.clear();
+  g.state = 0;
+}
+}  // namespace
+
+std::shared_ptr<MirrorGroup> Tensor::mirror_group(void* base, size_t bytes) {
+  auto g = std::make_shared<MirrorGroup>();
+  g->dev = static_cast<char*>(base);
+  g->bytes = bytes;
+  return g;
+}
+
+TensorPtr Tensor::view(std::vector<int64_t> shape, DType dtype, void* device_ptr, std::shared_ptr<void> owner,
+                       std::shared_ptr<MirrorGroup> group) {
+  const int64_t last = shape.empty() ? 1 : shape.back();
+  TensorPtr t = view(std::move(shape), dtype, device_ptr, last, std::move(owner));
+  if (group) {
+    const char* p = static_cast<const char*>(device_ptr);
+    if (p < group->dev || p + (size_t)t->numel_ * dtype_size(dtype) > group->dev + group->bytes)
+      throw std::invalid_argument("Tensor::view: outside its mirror group");
+    t->group_off_ = (size_t)(p - group->dev);
+    ++group->members;
+    t->group_ = std::move(group);
+  }
+  return t;
+}
+
+char* Tensor::host_ptr() const { return group_ ? group_->host.data() + group_off_ : host_.data(); }
+
 void Tensor::sync_host(bool will_write) const {
+  if (group_) {
+    MirrorGroup& g = *group_;
+    flush_zeros(g);
+    if (g.host.size() != g.bytes) {
+      g.host.assign(g.bytes, 0);
+      g.state = 0;
+    }
+    if (g.state == 0 && g.bytes > 0) {
+      hip_check(hipMemcpy(g.host.data(), g.dev, g.bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+      g.state = 1;
+    }
+    if (will_write) g.state = 2;
+    return;
+  }
   const size_t esz = dtype_size(dtype_);
   if (host_.size() != (size_t)numel_ * esz) {
     host_.assign((size_t)numel_ * esz, 0);
@@ -138,6 +204,14 @@ void Tensor::sync_host(bool will_write) const {
 }
 
 void Tensor::upload_if_dirty() const {
+  if (group_) {
+    flush_zeros(*group_);
+    if (group_->state == 2) {
+      hip_check(hipMemcpy(group_->dev, group_->host.data(), group_->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+      group_->state = 1;
+    }
+    return;
+  }
   if (host_state_ != 2) return;
   const size_t esz = dtype_size(dtype_);
   const int64_t row = shape_.empty() ? 1 : shape_.back();
@@ -160,12 +234,23 @@ const void* Tensor::device_data() const {
   return dev_;
 }
 
-void Tensor::mark_device_written() { host_state_ = 0; }
+void Tensor::mark_device_written() {
+  // grouped views: callers take device_data() before a kernel writes, which
+  // flushes any host edits of the group, so the whole mirror is now stale
+  if (group_) group_->state = 0;
+  else host_state_ = 0;
+}
 
 void Tensor::zero_grad() {
   if (!grad_) return;
   if (grad_->dtype() != kFloat32) throw std::runtime_error("zero_grad: float32 gradients only");
   if (!grad_->contiguous()) throw std::runtime_error("zero_grad: strided gradient");
+  if (const auto& g = grad_->group_) {  // deferred: one fill for the whole group when every member asks
+    grad_->upload_if_dirty();           // host edits of other members reach the device first
+    g->zeros[grad_->group_off_] = (size_t)grad_->numel() * 4;
+    g->state = 0;
+    return;
+  }
   mft_check(mft_fill(detail::handle(), static_cast<float*>(grad_->device_data()), grad_->numel(), 0.f), "mft_fill");
   grad_->mark_device_written();
 }
@@ -762,12 +847,20 @@ struct Adam::State {
   TensorPtr m, v;
 };
 
+struct Adam::GroupState {
+  std::weak_ptr<MirrorGroup> group;
+  TensorPtr m, v;  // one float per byte/4 of the group
+};
+
 Adam::Adam(const AdamConfig& cfg) : cfg_(cfg) {}
 Adam::~Adam() = default;
 
 void Adam::step(const std::vector<TensorPtr>& params, const std::vector<TensorPtr>& grads) {
   if (params.size() != grads.size()) throw std::invalid_argument("Adam::step: params and grads differ in length");
   ++t_;
+  // Moment storage: a parameter inside a mirror group takes views into the
+  // group's moment arena; others own theirs.
+  std::vector<State*> sts(params.size(), nullptr);
   for (size_t i = 0; i < params.size(); ++i) {
     const TensorPtr& p = params[i];
     const TensorPtr& g = grads[i];
@@ -779,11 +872,59 @@ void Adam::step(const std::vector<TensorPtr>& params, const std::vector<TensorPt
     if (!st || st->owner.lock() != p || st->m->numel() != p->numel()) {
       st = std::make_unique<State>();
       st->owner = p;
-      st->m = new_f32(p->shape());
-      st->v = new_f32(p->shape());
+      if (const auto& grp = p->mirror()) {
+        auto& gs = gstate_[grp.get()];
+        if (!gs || gs->group.lock() != grp) {
+          gs = std::make_unique<GroupState>();
+          gs->group = grp;
+          gs->m = new_f32({(int64_t)(grp->bytes / 4)});
+          gs->v = new_f32({(int64_t)(grp->bytes / 4)});
+        }
+        char* mb = static_cast<char*>(gs->m->device_data()) + p->mirror_offset();
+        char* vb = static_cast<char*>(gs->v->device_data()) + p->mirror_offset();
+        st->m = Tensor::view(p->shape(), kFloat32, mb, p->shape().empty() ? 1 : p->shape().back(), gs->m);
+        st->v = Tensor::view(p->shape(), kFloat32, vb, p->shape().empty() ? 1 : p->shape().back(), gs->v);
+      } else {
+        st->m = new_f32(p->shape());
+        st->v = new_f32(p->shape());
+      }
     }
+    sts[i] = st.get();
+  }
+  // Every member of one parameter group, each with its gradient at the same
+  // offset of one gradient group (the LoRA parameters and gradients of a
+  // model, as get_lora_parameters() and their grad() hand them out): one
+  // update over the whole arenas (padding between tensors has zero
+  // gradient and stays zero).
+  const MirrorGroup* pg = params.empty() || !params[0] ? nullptr : params[0]->mirror().get();
+  const MirrorGroup* gg = grads.empty() || !grads[0] ? nullptr : grads[0]->mirror().get();
+  bool fused = pg && gg && pg->bytes == gg->bytes && (int)params.size() == pg->members;
+  if (fused) {
+    std::unordered_set<size_t> offs;
+    for (size_t i = 0; i < params.size() && fused; ++i)
+      fused = params[i] && grads[i] && params[i]->mirror().get() == pg && grads[i]->mirror().get() == gg &&
+              params[i]->mirror_offset() == grads[i]->mirror_offset() &&
+              offs.insert(params[i]->mirror_offset()).second;
+  }
+  if (fused) {
+    GroupState& gs = *gstate_[pg];
+    float* pd = static_cast<float*>(params[0]->device_data());  // flushes host edits of either group
+    float* gd = static_cast<float*>(grads[0]->device_data());
+    pd -= params[0]->mirror_offset() / 4;
+    gd -= grads[0]->mirror_offset() / 4;
+    mft_check(mft_adam_step(detail::handle(), pd, gd, static_cast<float*>(gs.m->device_data()),
+                            static_cast<float*>(gs.v->device_data()), (int64_t)(pg->bytes / 4), cfg_.learning_rate,
+                            cfg_.beta1, cfg_.beta2, cfg_.epsilon, cfg_.weight_decay, t_, nullptr, 0),
+              "mft_adam_step");
+    params[0]->mark_device_written();
+    return;
+  }
+  for (size_t i = 0; i < params.size(); ++i) {
+    if (!sts[i]) continue;
+    const TensorPtr& p = params[i];
+    const TensorPtr& g = grads[i];
     mft_check(mft_adam_step(detail::handle(), static_cast<float*>(p->device_data()), static_cast<float*>(g->device_data()),
-                            static_cast<float*>(st->m->device_data()), static_cast<float*>(st->v->device_data()),
+                            static_cast<float*>(sts[i]->m->device_data()), static_cast<float*>(sts[i]->v->device_data()),
                             p->numel(), cfg_.learning_rate, cfg_.beta1, cfg_.beta2, cfg_.epsilon, cfg_.weight_decay, t_,
                             nullptr, 0),
               "mft_adam_step");

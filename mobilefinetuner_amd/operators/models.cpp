@@ -108,6 +108,9 @@ struct ModelLossNode : autograd::Node {
                   "hipMemcpy2D");
         autograd::accumulate_grad(lg, g);
       }
+    // gradients edited through host views go back before the backward adds to them
+    for (auto& w : st->grad_views)
+      if (auto gv = w.lock()) (void)gv->device_data();
     mft_check(mft_model_backward(st->m, ctx.mask ? static_cast<const float*>(ctx.mask->device_data()) : nullptr, ctx.B,
                                  ctx.S),
               "mft_model_backward");
@@ -221,6 +224,8 @@ void EngineModel::ensure_engine() {
   st->grad_views.assign(n, {});
   views_.assign(n, nullptr);
   grad_views_.assign(n, nullptr);
+  lora_pg_.reset();
+  lora_gg_.reset();
   st_ = st;
   // LoRA adapters not assigned below start as PEFT does: A small random, B zero.
   std::mt19937 rng(1234);
@@ -271,6 +276,8 @@ void EngineModel::attach_lora(int r, float alpha, int mask) {
     st_.reset();
     views_.clear();
     grad_views_.clear();
+    lora_pg_.reset();
+    lora_gg_.reset();
   }
   lora_r_ = r;
   lora_alpha_ = alpha;
@@ -373,14 +380,36 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
 std::vector<TensorPtr> EngineModel::parameters() {
   ensure_engine();
   std::vector<TensorPtr> out;
+  // The LoRA parameters and their gradients each tile one device arena: each
+  // arena gets one host mirror, so the drivers' host loops over
+  // p->grad()->data<float>() cost one copy each way per step, not one per tensor.
+  if (!lora_pg_) {
+    char *plo = nullptr, *phi = nullptr, *glo = nullptr, *ghi = nullptr;
+    for (const auto& r : st_->recs) {
+      if (!r.trainable) continue;
+      size_t b = 4;
+      for (int64_t d : r.shape) b *= (size_t)d;
+      char* pd = static_cast<char*>(r.data);
+      char* gd = reinterpret_cast<char*>(r.grad);
+      if (!plo || pd < plo) plo = pd;
+      if (!phi || pd + b > phi) phi = pd + b;
+      if (!glo || gd < glo) glo = gd;
+      if (!ghi || gd + b > ghi) ghi = gd + b;
+    }
+    if (plo) {
+      lora_pg_ = Tensor::mirror_group(plo, (size_t)(phi - plo));
+      lora_gg_ = Tensor::mirror_group(glo, (size_t)(ghi - glo));
+    }
+  }
   for (size_t i = 0; i < st_->recs.size(); ++i) {
     if (!views_[i]) {
       const auto& r = st_->recs[i];
       const int64_t last = r.shape.empty() ? 1 : r.shape.back();
-      views_[i] = Tensor::view(r.shape, r.f16 ? kFloat16 : kFloat32, r.data, last, st_);
+      views_[i] = r.trainable ? Tensor::view(r.shape, kFloat32, r.data, st_, lora_pg_)
+                              : Tensor::view(r.shape, r.f16 ? kFloat16 : kFloat32, r.data, last, st_);
       st_->views[i] = views_[i];
       if (r.trainable) {
-        grad_views_[i] = Tensor::view(r.shape, kFloat32, r.grad, last, st_);
+        grad_views_[i] = Tensor::view(r.shape, kFloat32, r.grad, st_, lora_gg_);
         st_->grad_views[i] = grad_views_[i];
         views_[i]->set_requires_grad(true);
         views_[i]->set_grad(grad_views_[i]);
