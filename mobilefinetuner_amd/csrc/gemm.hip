@@ -48,10 +48,35 @@ struct GemmParams {
   int M, N, K;
   int k_chunk;       // K range per split (multiple of BK)
   int tiles_m, tiles_n, tiles_per_xcd;
+  int splits;        // split-K count (the grid is 1-D; see tile_of)
+  int spread;        // 1: every K-slice over all 8 XCDs (tuning comparison)
   float* partial;    // split-K: [splits][M][N] raw accumulators
   int b_vec;         // B rows allow 128-bit (fp32) / 64-bit (fp16) loads
   GemmEpilogue ep;
 };
+
+// Workgroup → (tile, split) of a 1-D grid.  Workgroup L runs on XCD L % 8
+// (round-robin dispatch), each XCD with its own L2.  With s ≤ 8 splits, the
+// s K-slices take 8/s XCDs each and their tiles are cut into contiguous
+// ranges among those XCDs, M-fastest, so an XCD reads whole column bands of
+// B and the A rows of only its own K-slice (a split-K launch that spread
+// every slice over every XCD would fetch the whole of A into each of the 8
+// L2s).  With `spread` (used for s > 8) every K-slice covers all 8 XCDs.
+// Host side: tiles_per_xcd = ceil(tiles / (8/s)), or ceil(tiles/8) spread.
+__device__ __forceinline__ bool tile_of(const GemmParams& p, int& tile, int& split) {
+  const int L = blockIdx.x, xcd = L % 8, idx = L / 8;
+  const int tiles = p.tiles_m * p.tiles_n;
+  if (p.spread) {
+    const int per = 8 * p.tiles_per_xcd, r = L % per;
+    split = L / per;
+    tile = (r % 8) * p.tiles_per_xcd + r / 8;
+  } else {  // s ≤ 8
+    const int g = 8 / p.splits;  // XCDs per split
+    split = xcd / g;
+    tile = (xcd % g) * p.tiles_per_xcd + idx;
+  }
+  return tile < tiles && split < p.splits;
+}
 
 // Bias, residual and β·C; the rank-r term is accumulated on the matrix
 // cores before the epilogue.
@@ -92,17 +117,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   constexpr int SMEM = (KW > 1 && 4 * 4096 > 2 * STAGE) ? 4 * 4096 : 2 * STAGE;
   __shared__ __attribute__((aligned(16))) float smem[SMEM];
 
-  // XCD-aware tile order: workgroup ids are dispatched round-robin over the
-  // 8 XCDs, so tile = (id % 8) * tiles_per_xcd + id / 8 gives every XCD a
-  // contiguous run of tiles (m fastest): the workgroups sharing a B column
-  // panel share one XCD's L2.
-  const int wg = blockIdx.x;
-  const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
-  if (tile >= p.tiles_m * p.tiles_n) return;
+  // XCD-aware tile order (tile_of): every XCD takes a contiguous run of
+  // tiles (m fastest), so the workgroups sharing a B column panel share one
+  // XCD's L2.
+  int tile, split;
+  if (!tile_of(p, tile, split)) return;
   const int tm_idx = tile % p.tiles_m;
   const int tn_idx = tile / p.tiles_m;
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-  const int split = blockIdx.y;
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg + BK - 1) / BK;
@@ -409,13 +431,11 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
   static_assert(BK % 16 == 0 && A_ITEMS >= 1 && B_ITEMS >= 1, "tile config");
   __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
 
-  const int wg = blockIdx.x;
-  const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
-  if (tile >= p.tiles_m * p.tiles_n) return;
+  int tile, split;
+  if (!tile_of(p, tile, split)) return;
   const int tm_idx = tile % p.tiles_m;
   const int tn_idx = tile / p.tiles_m;
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-  const int split = blockIdx.y;
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg + BK - 1) / BK;
@@ -753,13 +773,11 @@ __global__ __launch_bounds__(256) void gemm_p_kernel(GemmParams p) {
   static_assert(A_ITEMS >= 1 && B_ITEMS >= 1 && (Q == 2 || Q == 4), "tile config");
   __shared__ __attribute__((aligned(16))) float smem[3 * STAGE];
 
-  const int wg = blockIdx.x;
-  const int tile = (wg % 8) * p.tiles_per_xcd + wg / 8;
-  if (tile >= p.tiles_m * p.tiles_n) return;
+  int tile, split;
+  if (!tile_of(p, tile, split)) return;
   const int tm_idx = tile % p.tiles_m;
   const int tn_idx = tile / p.tiles_m;
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-  const int split = blockIdx.y;
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
@@ -1063,13 +1081,31 @@ void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, 
   else launch_p_rank<BM, BK, SITE, false>(s, p, grid, b_nk, b_f16);
 }
 
+// The 1-D grid of tile_of for `splits` K-slices.
+dim3 xcd_grid(GemmParams& p, int splits) {
+  static const int spread = [] {  // tuning hook: MFT_GEMM_SPREAD=1 spreads every K-slice over all XCDs
+    const char* e = getenv("MFT_GEMM_SPREAD");
+    return e ? atoi(e) : 0;
+  }();
+  const int tiles = p.tiles_m * p.tiles_n;
+  p.splits = splits;
+  // vocabulary-deep reductions (the LM head's dH, 16 splits) measured 1.4%
+  // faster with every slice over all XCDs; layer GEMMs keep one K-slice per
+  // XCD group (43% less L2 fetch on GPT-2 small, same time)
+  p.spread = spread || splits > 8;
+  if (p.spread) {
+    p.tiles_per_xcd = (int)cdiv(tiles, 8);
+    return dim3((unsigned)(p.tiles_per_xcd * 8 * splits), 1);
+  }
+  p.tiles_per_xcd = (int)cdiv(tiles, 8 / splits);
+  return dim3((unsigned)(p.tiles_per_xcd * 8), 1);
+}
+
 template <int BM, int BK>
 void launch_q(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, 64);
-  const int tiles = p.tiles_m * p.tiles_n;
-  p.tiles_per_xcd = (int)cdiv(tiles, 8);
-  const dim3 grid(p.tiles_per_xcd * 8, splits);
+  const dim3 grid = xcd_grid(p, splits);
   // The pipelined kernel takes whole BK-deep panels in every split (and
   // the rank-r panel); gemm_q_kernel covers K tails.  Tuning hook:
   // MFT_GEMM_PIPE=0 keeps gemm_q_kernel everywhere.
@@ -1093,9 +1129,7 @@ template <int BM, int BN, int BK>
 void launch_tile(hipStream_t s, GemmParams& p, bool b_nk, bool b_f16, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, BN);
-  const int tiles = p.tiles_m * p.tiles_n;
-  p.tiles_per_xcd = (int)cdiv(tiles, 8);
-  const dim3 grid(p.tiles_per_xcd * 8, splits);
+  const dim3 grid = xcd_grid(p, splits);
   if (p.ep.site == 1) launch_variant<BM, BN, BK, 1>(s, p, grid, b_nk, b_f16);
   else launch_variant<BM, BN, BK, 0>(s, p, grid, b_nk, b_f16);
   MFT_LAUNCH_CHECK();
