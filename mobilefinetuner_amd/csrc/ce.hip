@@ -214,6 +214,93 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
   }
 }
 
+// Rows whose base-2 softmax statistics the LM-head GEMM wrote per 64-column
+// block (stats[row·stats_ld + j] = (max, Σ)): the row's log-sum-exp is merged
+// from those pairs, so the gradient sweep is the only pass over the logits —
+// each value read once and its dlogit written in place.
+template <int BLOCK>
+__global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
+    const float* logits, const int32_t* __restrict__ labels, int B, int S, int64_t V, int64_t ld,
+    int ignore_index, float upstream, int64_t norm_count, const int64_t* __restrict__ cnt, float* dlogits,
+    float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld) {
+  constexpr int NW = BLOCK / 64, U = 4;
+  __shared__ float sm[NW], ss[NW];
+  const int64_t row = blockIdx.x;
+  const int s = (int)(row % S);
+  const int label = (s + 1 < S) ? labels[row + 1] : ignore_index;
+  const float* x = logits + row * ld;
+  float* dx = dlogits ? dlogits + row * ld : nullptr;
+  const int tid = threadIdx.x;
+  if (label == ignore_index || label < 0 || (int64_t)label >= V) {
+    if (dx)
+      for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
+    if (tid == 0) row_nll[row] = 0.f;
+    return;
+  }
+  const float xl = x[label];  // read before any thread writes (dx may alias x)
+  const int64_t nb = (V + 63) / 64;
+  const float2* st = stats + row * stats_ld;
+  float m = -FLT_MAX, sum = 0.f;
+  for (int64_t j = tid; j < nb; j += BLOCK) {
+    const float2 p = st[j];
+    merge_ms(m, sum, p.x, p.y);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64);
+    const float s2 = __shfl_xor(sum, off, 64);
+    merge_ms(m, sum, m2, s2);
+  }
+  const int w = tid >> 6;
+  if ((tid & 63) == 0) {
+    sm[w] = m;
+    ss[w] = sum;
+  }
+  __syncthreads();
+  m = sm[0];
+  sum = ss[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) merge_ms(m, sum, sm[i], ss[i]);
+  const float lse2 = m + __builtin_amdgcn_logf(sum);
+  if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
+  if (!dx) return;
+  const int64_t n = norm_count > 0 ? norm_count : *cnt;
+  const float g = n > 0 ? upstream / (float)n : 0.f;
+  const int64_t head = std::min<int64_t>((4 - (((uintptr_t)x >> 2) & 3)) & 3, V);
+  const int64_t n4 = (V - head) / 4;
+  const int64_t tail0 = head + 4 * n4;
+  const floatx4* x4 = reinterpret_cast<const floatx4*>(x + head);
+  floatx4* d4 = reinterpret_cast<floatx4*>(dx + head);
+  for (int64_t j = tid; j < head; j += BLOCK) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(x[j], kLog2e, -lse2));
+    dx[j] = (j == label ? p - 1.f : p) * g;
+  }
+  for (int64_t b = tid; b < n4; b += (int64_t)BLOCK * U) {
+    floatx4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = b + (int64_t)u * BLOCK;
+      if (q < n4) v[u] = x4[q];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = b + (int64_t)u * BLOCK;
+      if (q >= n4) continue;
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(v[u][e], kLog2e, -lse2));
+        o[e] = (head + 4 * q + e == label ? p - 1.f : p) * g;
+      }
+      d4[q] = o;
+    }
+  }
+  for (int64_t j = tail0 + tid; j < V; j += BLOCK) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(x[j], kLog2e, -lse2));
+    dx[j] = (j == label ? p - 1.f : p) * g;
+  }
+}
+
 __global__ __launch_bounds__(256) void ce_sum_kernel(const float* __restrict__ row_nll,
                                                      int64_t rows, double* loss_sum,
                                                      const int64_t* cnt, int64_t* n_valid) {
@@ -235,7 +322,8 @@ __global__ __launch_bounds__(256) void ce_sum_kernel(const float* __restrict__ r
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
-                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label) {
+                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label,
+                const float2* row_stats, int64_t stats_ld) {
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
@@ -243,8 +331,14 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                      bad_label);
   MFT_LAUNCH_CHECK();
   // rows of up to 13·4096 values are held whole in registers (GPT-2's
-  // 50257); wider rows keep their first 16·4096 values there
-  if (V <= 13 * 4096)
+  // 50257); wider rows take the LM head's row statistics when it wrote them
+  // (one sweep), else keep their first 16·4096 values in registers
+  if (row_stats && V > 13 * 4096) {
+    MFT_CHECK_ARG(stats_ld >= cdiv(V, 64), "row statistics pitch");
+    hipLaunchKernelGGL((ce_row_stats_kernel<1024>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
+                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll,
+                       row_stats, stats_ld);
+  } else if (V <= 13 * 4096)
     hipLaunchKernelGGL((ce_row_kernel<1024, 13>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
                        ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
   else

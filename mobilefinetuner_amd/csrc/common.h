@@ -119,9 +119,18 @@ struct GemmEpilogue {
   // separately named (otherwise identical) kernel instantiation so kernel
   // traces and counter profiles attribute the two apart.
   int site = 0;
+  // LM head (128×128 plan only): per row and 64-column block of C, the
+  // base-2 softmax statistics (max of C·log2e, Σ 2^(C·log2e − max)) of the
+  // stored values, at stats[row·stats_ld + n/64]; the cross-entropy then
+  // reads the logits once.
+  float2* stats = nullptr;
+  int64_t stats_ld = 0;
   // Host-side only: row norm of the finished output (never read by kernels).
   const RowNorm* norm = nullptr;
 };
+// Whether gemm() runs an M×N×K product (the LM head's logits) on the
+// 128×128 kernel, the one that can emit row statistics.
+bool gemm_wide_plan(int M, int N);
 
 // Device scratch handed to launchers (split-K partials, rank-r temporaries).
 struct Scratch {
@@ -282,7 +291,8 @@ size_t attn_bwd_scratch_floats(const AttnArgs& a);
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
-                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label = nullptr);
+                float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label = nullptr,
+                const float2* row_stats = nullptr, int64_t stats_ld = 0);
 
 void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n);
 void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n);

@@ -151,6 +151,13 @@ struct mft_model_s {
   float *h_final = nullptr, *hf = nullptr, *fmean = nullptr, *frstd = nullptr;
   float* logits = nullptr;
   int64_t ldv = 0;  // logits row stride: vocab rounded up to 4 (zeroed padding)
+  // Per-row softmax statistics of the logits, one (max, Σ) pair per 64
+  // columns, written by the LM head's GEMM for vocabularies too wide for the
+  // cross-entropy to hold a row in registers; stats_fresh says the last
+  // forward wrote them for the logits now in place.
+  float2* row_stats = nullptr;
+  int64_t stats_ld = 0;
+  bool stats_fresh = false;
   // dh, dh2: residual-stream gradients entering a layer's MLP and attention
   // blocks (alternating, so norm backward passes run out of place)
   float *dh = nullptr, *dh2 = nullptr, *dtmp = nullptr, *dn = nullptr, *datt = nullptr;
@@ -681,6 +688,10 @@ void alloc_acts(mft_model_s* m) {
     m->fmean = b.f(M);
     m->ldv = (c.vocab + 3) / 4 * 4;
     m->logits = b.f(M * m->ldv);
+    if (c.vocab > 13 * 4096 && gemm_wide_plan((int)M, (int)c.vocab)) {
+      m->stats_ld = cdiv(c.vocab, 64);
+      m->row_stats = reinterpret_cast<float2*>(b.f(2 * M * m->stats_ld));
+    }
     m->dh = b.f(M * d);
     m->dh2 = b.f(M * d);
     m->dtmp = b.f(M * d);
@@ -1275,6 +1286,11 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
   GemmEpilogue head;
   head.site = 1;
+  m->stats_fresh = m->row_stats && gemm_wide_plan((int)M, (int)c.vocab);
+  if (m->stats_fresh) {
+    head.stats = m->row_stats;
+    head.stats_ld = m->stats_ld;
+  }
   gemm(s, m->hf, d, wh.ptr, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, head, m->ws,
        t.events());
 }
@@ -1290,7 +1306,8 @@ void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs,
     t.begin();
     ce_fwd_bwd(m->stream, lg, labels + row0, seqs, S, c.vocab, m->ldv, -100, upstream, 0,
                m->d_loss + m->n_micro_pending, m->d_cnt + m->n_micro_pending, backward ? lg : nullptr,
-               m->row_nll + row0, m->d_tmpcnt, m->d_err + 1);
+               m->row_nll + row0, m->d_tmpcnt, m->d_err + 1,
+               m->stats_fresh ? m->row_stats + row0 * m->stats_ld : nullptr, m->stats_ld);
     t.end();
     m->n_micro_pending++;
   }

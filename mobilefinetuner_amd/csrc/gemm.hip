@@ -26,6 +26,7 @@
 // half h of a 32×32 tile supplies k = kw·KS + h·KS/2 + j for its KS/2 MFMAs
 // (A and B permuted identically, so the sum is unchanged).  Interior tiles
 // take an unchecked load path; edge tiles check every element.
+#include <cfloat>
 #include <cstdio>
 #include <cstdlib>
 #include <type_traits>
@@ -54,6 +55,39 @@ struct GemmParams {
   int b_vec;         // B rows allow 128-bit (fp32) / 64-bit (fp16) loads
   GemmEpilogue ep;
 };
+
+constexpr float kLog2eG = 1.4426950408889634f;
+
+// Softmax statistics of one logits row segment of 64 values held in LDS
+// (row-major, 16-byte aligned): (max t, Σ 2^(t − max)) with t = value·log2e.
+// Entries past the matrix edge hold −FLT_MAX (their terms flush to 0; the
+// first entry is always inside).  The max runs over the raw values (scaling
+// by log2e is monotonic) as IEEE maximum, which needs no canonicalised
+// operands.
+__device__ __forceinline__ float2 row_stats64(const float* row) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  float v[64];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const float4 t = r4[q];
+    v[4 * q] = t.x;
+    v[4 * q + 1] = t.y;
+    v[4 * q + 2] = t.z;
+    v[4 * q + 3] = t.w;
+  }
+  float mx = v[0];
+#pragma unroll
+  for (int c = 1; c + 1 < 64; c += 2) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(v[c], v[c + 1]));
+  mx = __builtin_elementwise_maximum(mx, v[63]);
+  const float ml = mx * kLog2eG;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; c += 2) {
+    s0 += __builtin_amdgcn_exp2f(fmaf(v[c], kLog2eG, -ml));
+    s1 += __builtin_amdgcn_exp2f(fmaf(v[c + 1], kLog2eG, -ml));
+  }
+  return make_float2(ml, s0 + s1);
+}
 
 // Workgroup → (tile, split) of a 1-D grid.  Workgroup L runs on XCD L % 8
 // (round-robin dispatch), each XCD with its own L2.  With s ≤ 8 splits, the
@@ -380,6 +414,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       }
     }
     return;
+  }
+
+  // Row statistics of the LM head's logits for the cross-entropy: one
+  // (max, Σ) pair per row and 64-column block of the values stored below
+  // (the LM head's epilogue adds nothing); a block wholly past N writes none.
+  // Each wave transposes its 64×64 sub-tile through its own region of the
+  // (now idle) LDS ring, row pitch 68 floats, so lane L reads row L whole
+  // with conflict-free 128-bit reads and reduces it alone; a wave's LDS
+  // operations complete in issue order, so no barrier is needed.
+  if constexpr (SITE == 1 && BM == 128 && BN == 128) {
+    constexpr int SP = 68;
+    static_assert(4 * 64 * SP <= SMEM, "LDS ring too small for the statistics transpose");
+    const int nb = n0 + wn;
+    if (p.ep.stats && !split_out && nb < p.N) {
+      float* ws = smem + wave * 64 * SP;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const bool in = nb + b * 32 + li < p.N;
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            ws[(a * 32 + 8 * (e >> 2) + 4 * lh + (e & 3)) * SP + b * 32 + li] = in ? acc[a][b][e] : -FLT_MAX;
+      }
+      const float2 st = row_stats64(ws + lane * SP);
+      const int m = m0 + wm + lane;
+      if (m < p.M) p.ep.stats[(int64_t)m * p.ep.stats_ld + nb / 64] = st;
+    }
   }
 
   // Output: lane (li, lh) of a 32×32 tile holds column li, rows
@@ -1159,7 +1221,7 @@ int plan_bk(int bm, int bn) { return ((bm == 64 || bm == 128) && bn == 64) || bn
 // in total (a 576-workgroup plan, one full round plus an eighth of a
 // second, was the costliest miss of the previous rule).
 Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
-  if (cdiv(M, 128) * cdiv(N, 128) >= 1024) return {128, 128, 1};
+  if (gemm_wide_plan(M, N)) return {128, 128, 1};
   if (K >= 16384) {
     const int64_t tiles = cdiv(M, 64) * cdiv(N, 64);
     int sp = 1;
@@ -1192,6 +1254,8 @@ Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
 }
 
 }  // namespace
+
+bool gemm_wide_plan(int M, int N) { return cdiv(M, 128) * cdiv(N, 128) >= 1024; }
 
 void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb, bool b_nk,
           bool b_f16, float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep,
@@ -1233,7 +1297,7 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   // (bm×bn ∈ {128×128, 64×128, 64×64}, or "64,0,s" for the quadrant kernel);
   // same arithmetic, other tiling.
   static const char* forced = getenv("MFT_GEMM_PLAN");
-  if (forced) {
+  if (forced && !ep.stats) {
     int bm = 0, bn = 0, sp = 0;
     if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
@@ -1264,9 +1328,14 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   // tiles, 36 of them in a fourth round), the trailing column tiles become
   // an unsplit 32-row-tile launch instead, which spreads that work over the
   // whole GPU for a fraction of a round.  Plain epilogues only (bias allowed).
+  MFT_CHECK_ARG(!ep.stats || (pl.bm == 128 && pl.bn == 128 && ep.site == 1 && ep.stats_ld >= cdiv(N, 64)),
+                "row statistics need the 128x128 LM-head plan");
+  MFT_CHECK_ARG(!ep.stats || (!ep.bias && !ep.resid && ep.beta == 0.f && !ep.gelu_out && !ep.gelu_grad_of &&
+                              !ep.P && !(ep.norm && ep.norm->kind != NORM_NONE)),
+                "row statistics describe plain logits (no epilogue terms)");
   int n_main = 0;
   if (pl.bm == 128 && pl.bn == 128 && !forced && !nm && ep.P == nullptr && !ep.resid && ep.beta == 0.f &&
-      !ep.gelu_out && !ep.gelu_grad_of) {
+      !ep.gelu_out && !ep.gelu_grad_of && !ep.stats) {
     const int64_t tm = cdiv(M, 128), tn = cdiv(N, 128), tiles = tm * tn;
     const int64_t rem = tiles % 512;
     if (tiles > 512 && rem > 0 && rem * 4 <= 512) n_main = (int)((tn - cdiv(rem, tm)) * 128);
@@ -1275,6 +1344,7 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   int splits = pl.splits;
   p.k_chunk = (int)(cdiv(cdiv(K, splits), bk) * bk);
   splits = (int)cdiv(K, p.k_chunk);
+  MFT_CHECK_ARG(!ep.stats || splits == 1, "row statistics need an unsplit K");
   if (splits > 1) p.partial = ws.ptr;
 
   // Timing: events recorded by the dispatch itself, except under stream

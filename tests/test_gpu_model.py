@@ -46,6 +46,14 @@ SMALL = {
     "qwen2-qv": (qwen2(2, 256, 4, 2, 64, 384, vocab=601, name="qwen-qv", lora_mask=0b0101), 2, 48, 1),
     "gemma3-qv": (gemma3(2, 128, 2, 1, 256, 256, vocab=509, name="gemma-qv", sliding_window=24,
                          query_pre_attn_scalar=256, lora_mask=0b0000101), 2, 32, 1),
+    # A vocabulary wider than 13·4096 on a 128×128-tiled LM head: the GEMM
+    # writes per-64-column softmax statistics and the cross-entropy takes its
+    # log-sum-exp from them (one sweep over the logits).  70001 leaves a
+    # ragged last column block; 53672 (= 419·128 + 40) a last tile whose
+    # first 64-column block is ragged and whose second lies wholly past the
+    # vocabulary; two micro-batches offset the statistics rows.
+    "qwen2-wide-vocab": (qwen2(1, 128, 2, 1, 64, 256, vocab=70001, name="qwen-wv"), 2, 96, 2),
+    "gpt2-wide-vocab": (gpt2(1, 128, 2, vocab=53672, max_pos=128, name="gpt2-wv"), 2, 96, 2),
 }
 
 
