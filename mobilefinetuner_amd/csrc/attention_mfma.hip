@@ -957,17 +957,20 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short(AttnP p) {
 }
 
 // dK/dV role: workgroup = one 16-key tile of one QUERY head; waves take the
-// query tiles that see it round-robin.  K, V of the tile stay in registers
+// query tiles that see it round-robin.  K, V of the tile are read from
+// global memory once per workgroup (staged in LDS) and stay in registers
 // (B operands of S = Q·Kᵀ and dP = dO·Vᵀ); per query tile a wave reads Q,
-// dO, O rows (A operands, and delta) and Q, dO by column (B operands of
-// dK += dSᵀ·Q, dV += Pᵀ·dO).  The partials [key 4g+v][d 16c+i] are summed
-// over the waves through LDS; GQA groups > 1 write per-query-head partials.
+// dO, O rows (A operands, and delta) and turns its Q and dO rows into the
+// column operands of dK += dSᵀ·Q, dV += Pᵀ·dO through its own LDS slot.  The
+// partials [key 4g+v][d 16c+i] are summed over the waves through the same
+// slots; GQA groups > 1 write per-query-head partials.
 template <int HD, int NW>
 __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, float* smem) {
   constexpr int NC = HD / 16;
   constexpr int PO = HD + 4;
-  float* Dk = smem;               // [NW][16][PO]
-  float* Dv = Dk + NW * 16 * PO;  // [NW][16][PO]
+  float* Dk = smem;               // [NW][16][PO]: wave w's Q transpose slot, then its dK partial
+  float* Dv = Dk + NW * 16 * PO;  // [NW][16][PO]: wave w's dO transpose slot, then its dV partial
+  float* KV = Dv + NW * 16 * PO;  // [2][16][PO]: the tile's K and V rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -986,23 +989,10 @@ __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, flo
   const int qt_hi = (p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1) / 16;
 
   const float qk2 = p.scale * kLog2e;
-  floatx4 kreg[NC], vreg[NC], dkacc[NC], dvacc[NC];
-  {
-    const int64_t row = tok0 + min(kj, p.S - 1);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int64_t off = (int64_t)kh * HD + 16 * c + 4 * lg;
-      kreg[c] = *reinterpret_cast<const floatx4*>(p.k + row * p.k_rs + off) * qk2;
-      vreg[c] = *reinterpret_cast<const floatx4*>(p.v + row * p.v_rs + off);
-      dkacc[c] = dvacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
   const int64_t lrow0 = ((int64_t)b * p.Hq + h) * p.S;
-  // one query tile's operands: Q, dO, O rows (128-bit), Q and dO columns,
-  // lse of query q0 + i
+  // one query tile's operands: Q, dO, O rows (128-bit), lse of query q0 + i
   struct QTile {
     floatx4 qa[NC], ga[NC], oa[NC];
-    float qb[NC][4], gb[NC][4];
     float lse;
   };
   auto load = [&](int qt, QTile& T) {
@@ -1015,18 +1005,58 @@ __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, flo
       T.ga[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
       T.oa[c] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int64_t r2 = tok0 + min(q0 + 4 * lg + t, p.S - 1);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        T.qb[c][t] = p.q[r2 * p.q_rs + (int64_t)h * HD + 16 * c + li];
-        T.gb[c][t] = p.dout[r2 * p.do_rs + (int64_t)h * HD + 16 * c + li];
-      }
-    }
     T.lse = p.lse[lrow0 + min(q0 + li, p.S - 1)];
   };
-  auto compute = [&](int qt, const QTile& T) {
+  // K, V rows of the tile (rows past S clamped; their keys are masked):
+  // one 128-bit item per thread and tensor per pass, issued together with
+  // the wave's first query tile
+  constexpr int KV_IT = 16 * (HD / 4) / (64 * NW);
+  static_assert(KV_IT >= 1 && KV_IT * 64 * NW == 16 * (HD / 4), "K/V staging shape");
+  floatx4 kx[KV_IT], vx[KV_IT];
+#pragma unroll
+  for (int u = 0; u < KV_IT; ++u) {
+    const int f = tid + 64 * NW * u, r = f / (HD / 4), c4 = f % (HD / 4);
+    const int64_t row = tok0 + min(k0 + r, p.S - 1);
+    kx[u] = *reinterpret_cast<const floatx4*>(p.k + row * p.k_rs + (int64_t)kh * HD + 4 * c4);
+    vx[u] = *reinterpret_cast<const floatx4*>(p.v + row * p.v_rs + (int64_t)kh * HD + 4 * c4);
+  }
+  QTile cur;
+  int qt = qt_lo + w;
+  if (qt <= qt_hi) load(qt, cur);
+#pragma unroll
+  for (int u = 0; u < KV_IT; ++u) {
+    const int f = tid + 64 * NW * u, r = f / (HD / 4), c4 = f % (HD / 4);
+    *reinterpret_cast<floatx4*>(KV + r * PO + 4 * c4) = kx[u];
+    *reinterpret_cast<floatx4*>(KV + (16 + r) * PO + 4 * c4) = vx[u];
+  }
+  __syncthreads();
+  floatx4 kreg[NC], vreg[NC], dkacc[NC], dvacc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    kreg[c] = *reinterpret_cast<const floatx4*>(KV + li * PO + 16 * c + 4 * lg) * qk2;
+    vreg[c] = *reinterpret_cast<const floatx4*>(KV + (16 + li) * PO + 16 * c + 4 * lg);
+    dkacc[c] = dvacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Q and dO by column (rows 4g + t, column 16c + i): the wave's rows
+  // written to its LDS slots and read back transposed (a wave's LDS
+  // operations complete in issue order, so the slots need no barrier)
+  float* sq = Dk + w * 16 * PO;
+  float* sg = Dv + w * 16 * PO;
+  auto cols = [&](const QTile& T, float (&qb)[NC][4], float (&gb)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      *reinterpret_cast<floatx4*>(sq + li * PO + 16 * c + 4 * lg) = T.qa[c];
+      *reinterpret_cast<floatx4*>(sg + li * PO + 16 * c + 4 * lg) = T.ga[c];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        qb[c][t] = sq[(4 * lg + t) * PO + 16 * c + li];
+        gb[c][t] = sg[(4 * lg + t) * PO + 16 * c + li];
+      }
+  };
+  auto compute = [&](int qt, const QTile& T, const float (&qb)[NC][4], const float (&gb)[NC][4]) {
     const int q0 = 16 * qt;
     const float l2 = T.lse * kLog2e;  // query q0 + li
     float dl = 0.f;
@@ -1058,17 +1088,18 @@ __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, flo
     for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        dvacc[c] = mfma4(pv[t], T.gb[c][t], dvacc[c]);
-        dkacc[c] = mfma4(ds[t], T.qb[c][t], dkacc[c]);
+        dvacc[c] = mfma4(pv[t], gb[c][t], dvacc[c]);
+        dkacc[c] = mfma4(ds[t], qb[c][t], dkacc[c]);
       }
   };
   // One tile of operands in registers at a time: holding the next tile's
-  // loads in flight as well (two tiles of registers) halves the waves per
-  // SIMD and measured slower at GPT-2's shapes.
-  for (int qt = qt_lo + w; qt <= qt_hi; qt += NW) {
-    QTile cur;
-    load(qt, cur);
-    compute(qt, cur);
+  // loads in flight as well (two tiles of registers) lowers the waves per
+  // SIMD below what the launch needs to be resident at once.
+  for (; qt <= qt_hi; qt += NW) {
+    float qb[NC][4], gb[NC][4];
+    cols(cur, qb, gb);
+    compute(qt, cur, qb, gb);
+    if (qt + NW <= qt_hi) load(qt + NW, cur);
   }
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -1098,16 +1129,18 @@ __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, flo
 }
 
 // dQ role: workgroup = one 16-query tile of one head; waves take its visible
-// key tiles round-robin.  Q, dO of the tile stay in registers (B operands of
+// key tiles round-robin.  Q, dO, O of the tile are read from global memory
+// once per workgroup (staged in LDS); Q, dO stay in registers (B operands of
 // Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ, so a lane owns one query's softmax row); per
-// key tile a wave reads K, V rows (A operands) and K by column (B operand of
-// dQ += dS·K).  The partials [query 4g+v][d 16c+i] are summed over the
-// waves through LDS.
+// key tile a wave reads K, V rows (A operands) and turns its K rows into the
+// column operand of dQ += dS·K through its own LDS slot.  The partials
+// [query 4g+v][d 16c+i] are summed over the waves through the same slots.
 template <int HD, int NW>
 __device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float* smem) {
   constexpr int NC = HD / 16;
   constexpr int PO = HD + 4;
-  float* Dq = smem;  // [NW][16][PO]
+  float* Dq = smem;                // [NW][16][PO]: wave w's K transpose slot, then its dQ partial
+  float* QG = Dq + NW * 16 * PO;   // [3][16][PO]: the tile's Q, dO and O rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -1130,24 +1163,11 @@ __device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float
   const float qk2 = p.scale * kLog2e;
   const float* kbase = p.k + (int64_t)kh * HD;
   const float* vbase = p.v + (int64_t)kh * HD;
-  floatx4 qreg[NC], greg[NC], dqacc[NC], orow[NC];
-  {
-    const int64_t row = tok0 + min(qi, p.S - 1);
-    const int64_t off = (int64_t)h * HD + 4 * lg;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qreg[c] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off + 16 * c);
-      greg[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
-      orow[c] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
-      dqacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
   const float lse_q = p.lse[((int64_t)b * p.Hq + h) * p.S + min(qi, p.S - 1)];
   float dl = 0.f, l2 = 0.f;  // delta and lse·log2(e) of query qi (formed below)
-  // one key tile's operands: K, V rows (128-bit) and K columns
+  // one key tile's operands: K, V rows (128-bit)
   struct KTile {
     floatx4 ka[NC], va[NC];
-    float kb[NC][4];
   };
   auto load = [&](int kt, KTile& T) {
     const int64_t row = tok0 + min(16 * kt + li, p.S - 1);
@@ -1156,14 +1176,54 @@ __device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float
       T.ka[c] = *reinterpret_cast<const floatx4*>(kbase + row * p.k_rs + 16 * c + 4 * lg);
       T.va[c] = *reinterpret_cast<const floatx4*>(vbase + row * p.v_rs + 16 * c + 4 * lg);
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float* kr = kbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.k_rs + li;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) T.kb[c][t] = kr[16 * c];
-    }
   };
-  auto compute = [&](int kt, const KTile& T) {
+  // Q, dO, O rows of the tile (rows past S clamped; they are not stored):
+  // one 128-bit item per thread and tensor per pass, issued together with
+  // the wave's first key tile
+  constexpr int QG_IT = 16 * (HD / 4) / (64 * NW);
+  static_assert(QG_IT >= 1 && QG_IT * 64 * NW == 16 * (HD / 4), "Q/dO/O staging shape");
+  floatx4 qx[QG_IT], gx[QG_IT], ox[QG_IT];
+#pragma unroll
+  for (int u = 0; u < QG_IT; ++u) {
+    const int f = tid + 64 * NW * u, r = f / (HD / 4), c4 = f % (HD / 4);
+    const int64_t row = tok0 + min(q0 + r, p.S - 1);
+    const int64_t off = (int64_t)h * HD + 4 * c4;
+    qx[u] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off);
+    gx[u] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off);
+    ox[u] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off);
+  }
+  KTile cur;
+  int kt = kt_lo + w;
+  if (kt <= kt_hi) load(kt, cur);
+#pragma unroll
+  for (int u = 0; u < QG_IT; ++u) {
+    const int f = tid + 64 * NW * u, r = f / (HD / 4), c4 = f % (HD / 4);
+    *reinterpret_cast<floatx4*>(QG + r * PO + 4 * c4) = qx[u];
+    *reinterpret_cast<floatx4*>(QG + (16 + r) * PO + 4 * c4) = gx[u];
+    *reinterpret_cast<floatx4*>(QG + (32 + r) * PO + 4 * c4) = ox[u];
+  }
+  __syncthreads();
+  floatx4 qreg[NC], greg[NC], dqacc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    qreg[c] = *reinterpret_cast<const floatx4*>(QG + li * PO + 16 * c + 4 * lg);
+    greg[c] = *reinterpret_cast<const floatx4*>(QG + (16 + li) * PO + 16 * c + 4 * lg);
+    const floatx4 orow = *reinterpret_cast<const floatx4*>(QG + (32 + li) * PO + 16 * c + 4 * lg);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dl = fmaf(greg[c][e], orow[e], dl);
+    dqacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  // K by column (rows 4g + t, column 16c + i) through the wave's LDS slot
+  float* sk = Dq + w * 16 * PO;
+  auto cols = [&](const KTile& T, float (&kb)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) *reinterpret_cast<floatx4*>(sk + li * PO + 16 * c + 4 * lg) = T.ka[c];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kb[c][t] = sk[(4 * lg + t) * PO + 16 * c + li];
+  };
+  auto compute = [&](int kt, const KTile& T, const float (&kb)[NC][4]) {
     floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -1186,24 +1246,18 @@ __device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], T.kb[c][t], dqacc[c]);
+      for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], kb[c][t], dqacc[c]);
   };
-  // the first key tile's loads go out with the query rows' (before delta is
-  // formed); each later tile's after the previous one is multiplied (one
-  // tile of registers, as in the dK/dV role)
-  KTile cur;
-  int kt = kt_lo + w;
-  if (kt <= kt_hi) load(kt, cur);
+  // each later key tile's loads go out after the previous one is multiplied
+  // (one tile of registers, as in the dK/dV role)
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    qreg[c] *= qk2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) dl = fmaf(greg[c][e], orow[c][e], dl);
-  }
+  for (int c = 0; c < NC; ++c) qreg[c] *= qk2;
   dl = add_xor32(add_xor16(dl));
   l2 = lse_q * kLog2e;
   for (; kt <= kt_hi; kt += NW) {
-    compute(kt, cur);
+    float kb[NC][4];
+    cols(cur, kb);
+    compute(kt, cur, kb);
     if (kt + NW <= kt_hi) load(kt + NW, cur);
   }
 #pragma unroll
@@ -1404,7 +1458,8 @@ void fwd_short_launch(hipStream_t s, AttnP& p) {
 template <int HD>
 void bwd_short_launch(hipStream_t s, AttnP& p) {
   constexpr int NW = kShortWaves;
-  const size_t lds = sizeof(float) * 2 * NW * 16 * (HD + 4);
+  // dK/dV role: 2·NW wave slots + K, V rows; dQ role: NW slots + Q, dO, O rows
+  const size_t lds = sizeof(float) * std::max(2 * NW + 2, NW + 3) * 16 * (HD + 4);
   auto kern = attn_bwd_short<HD, NW>;
   set_lds(kern, lds);
   const int tiles = (int)(cdiv(p.S, 16) * p.Hq * p.B);
