@@ -10,6 +10,8 @@
 // the matrix cores, one launch for both gradients of a layer, with M split
 // over the waves of a workgroup and summed in wave order (deterministic, no
 // atomics, no second pass).
+#include <type_traits>
+
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -322,12 +324,26 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
 // remaining values to the partner lane), after which value v sits in lanes
 // with lane >> (6 − log2(RW·r)) == v.
 //
-// Outer role (out(j,c) (+)= s·Σ_m P[m,j]·X[m,c]): 256 columns per workgroup
-// (four per lane, so a wave reads 1 KB of a row), the rows split over the
-// four waves; P's row is uniform across the wave.  Wave partials are added
-// through LDS in wave order (deterministic), column runs per XCD.
+// Outer role (out(j,c) (+)= s·Σ_m P[m,j]·X[m,c]): 64 columns per workgroup
+// (one per lane: at the benchmark shapes a 768-wide product then spans 12
+// workgroups instead of 3), the rows split over the four waves and read in
+// chunks of 16 rows in flight; P's row is uniform across the wave.  Wave
+// partials are added through LDS in wave order (deterministic), column runs
+// per XCD.
+// Job tables hold generic pointers; loads through them are marked global
+// (vector memory instructions instead of flat ones), and a row that is the
+// same for the whole wave is read through the scalar cache.
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ T lds_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 constexpr int kBatchThreads = 256;
-constexpr int kBatchCols = 256;
+constexpr int kBatchCols = 64;
 
 template <int R>
 constexpr int batch_rows_per_wave() { return R <= 16 ? 4 : 2; }
@@ -358,11 +374,11 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
   for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
     floatx4 xv[RW];
 #pragma unroll
-    for (int q = 0; q < RW; ++q) xv[q] = *reinterpret_cast<const floatx4*>(xr[q] + k);
+    for (int q = 0; q < RW; ++q) xv[q] = ldg(reinterpret_cast<const floatx4*>(xr[q] + k));
     if (jb.y_rk) {  // Y [r, K]
 #pragma unroll
       for (int j = 0; j < R; ++j) {
-        const floatx4 y = *reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + k);
+        const floatx4 y = ldg(reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + k));
 #pragma unroll
         for (int q = 0; q < RW; ++q)
 #pragma unroll
@@ -374,7 +390,7 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int jq = 0; jq < R / 4; ++jq) {
-          const floatx4 y = yp[t * (R / 4) + jq];
+          const floatx4 y = ldg(yp + t * (R / 4) + jq);
 #pragma unroll
           for (int q = 0; q < RW; ++q)
 #pragma unroll
@@ -427,41 +443,55 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
 
 template <int R>
 __device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, float* lds) {
+  constexpr int CPL = kBatchCols / 64;  // columns per lane
+  typedef float colv __attribute__((ext_vector_type(CPL)));
   const int blk = (raw % 8) * (jb.blocks / 8) + raw / 8;
   const int c0 = blk * kBatchCols;
   if (c0 >= jb.K) return;  // whole workgroup, before any barrier
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = c0 + 4 * lane;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = c0 + CPL * lane;
   const bool cok = c < jb.K;  // C is a multiple of 4 (checked on the host)
   const int per = (M + 3) / 4;
   const int mb = w * per, me = min(M, mb + per);
-  float acc[R][4];
+  float acc[R][CPL];
 #pragma unroll
   for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[j][e] = 0.f;
+    for (int e = 0; e < CPL; ++e) acc[j][e] = 0.f;
   const float* xp = jb.X + (cok ? c : 0);
-#pragma unroll 4
-  for (int m = mb; m < me; ++m) {
-    const floatx4 x = *reinterpret_cast<const floatx4*>(xp + (int64_t)m * jb.ldx);
-    const floatx4* pp = reinterpret_cast<const floatx4*>(jb.Y + (int64_t)m * R);
+  // rows in chunks of CH, every row load of a chunk issued before its first
+  // use (a wave's rows are one chain of chunk latencies); P's row is the
+  // same for the whole wave and comes through the scalar cache
+  auto rows = [&](int m, auto nc) {
+    constexpr int NCH = decltype(nc)::value;
+    colv xs[NCH];
 #pragma unroll
-    for (int jq = 0; jq < R / 4; ++jq) {
-      const floatx4 pv = pp[jq];
+    for (int u = 0; u < NCH; ++u) xs[u] = ldg(reinterpret_cast<const colv*>(xp + (int64_t)(m + u) * jb.ldx));
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+    for (int u = 0; u < NCH; ++u) {
+      const floatx4* pp = reinterpret_cast<const floatx4*>(jb.Y + (int64_t)(m + u) * R);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[4 * jq + e][t] = fmaf(pv[e], x[t], acc[4 * jq + e][t]);
+      for (int jq = 0; jq < R / 4; ++jq) {
+        const floatx4 pv = lds_uniform(pp + jq);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int t = 0; t < CPL; ++t) acc[4 * jq + e][t] = fmaf(pv[e], xs[u][t], acc[4 * jq + e][t]);
+      }
     }
-  }
-  // wave-ordered sum through LDS: lds[j][256 columns]
+  };
+  constexpr int CH = 16 / CPL;
+  int m = mb;
+  for (; m + CH <= me; m += CH) rows(m, std::integral_constant<int, CH>{});
+  for (; m < me; ++m) rows(m, std::integral_constant<int, 1>{});
+  // wave-ordered sum through LDS: lds[j][kBatchCols columns]
   for (int q = 0; q < 4; ++q) {
     if (w == q) {
 #pragma unroll
       for (int j = 0; j < R; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float& d = lds[j * kBatchCols + 4 * lane + e];
+        for (int e = 0; e < CPL; ++e) {
+          float& d = lds[j * kBatchCols + CPL * lane + e];
           d = q == 0 ? acc[j][e] : d + acc[j][e];
         }
     }
@@ -471,9 +501,9 @@ __device__ __forceinline__ void batch_outer(const RankJob& jb, int raw, int M, f
 #pragma unroll
   for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < CPL; ++e) {
       float* out = jb.out + (int64_t)j * jb.osj + (int64_t)(c + e) * jb.osc;
-      const float v = lds[j * kBatchCols + 4 * lane + e];
+      const float v = lds[j * kBatchCols + CPL * lane + e];
       *out = jb.accumulate ? fmaf(jb.scale, v, *out) : jb.scale * v;
     }
 }
