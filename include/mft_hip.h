@@ -51,6 +51,14 @@ void*       mft_get_stream(mft_handle h);
 int         mft_synchronize(mft_handle h);
 const char* mft_last_error(void);
 const char* mft_version(void);
+/* Debug mode: with on != 0 every kernel launch is followed by a device
+ * synchronisation, and an execution error is reported (MFT_EHIP, message
+ * naming the source line of the launch) by the call that made it.  Also set
+ * by MFT_SYNC_CHECK=1 in the environment at library load.  A captured
+ * training-step graph is not used while it is on (steps run eagerly).
+ * No counterpart in the reference (it runs on the CPU); the debug build mode
+ * for the GPU path. */
+int         mft_set_sync_check(int on);
 /* Device memory helpers for hosts without their own allocator (the C++
  * operators layer, ctypes tests). */
 int mft_malloc(void** ptr, size_t bytes);

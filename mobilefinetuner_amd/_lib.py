@@ -47,6 +47,7 @@ _SIGS = {
     "mft_synchronize": (_I, [_P]),
     "mft_last_error": (C.c_char_p, []),
     "mft_version": (C.c_char_p, []),
+    "mft_set_sync_check": (_I, [_I]),
     "mft_malloc": (_I, [C.POINTER(_P), C.c_size_t]),
     "mft_free": (_I, [_P]),
     "mft_memcpy_h2d": (_I, [_P, _P, _P, C.c_size_t]),

@@ -3,6 +3,7 @@
 // the handle's stream and converts C++ exceptions into status codes plus a
 // thread-local message.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -23,6 +24,18 @@ struct HandleScratch {
 }  // namespace
 
 void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+int g_sync_check = [] {
+  const char* e = getenv("MFT_SYNC_CHECK");
+  return e && atoi(e) != 0 ? 1 : 0;
+}();
+
+void sync_check(const char* file, int line) {
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess)
+    throw Error(MFT_EHIP, std::string("sync check after the launch at ") + file + ":" + std::to_string(line) +
+                              ": " + hipGetErrorString(e));
+}
 
 }  // namespace mft
 
@@ -73,6 +86,10 @@ void require_handle(mft_handle h) {
 extern "C" {
 
 const char* mft_last_error(void) { return mft::g_last_error.c_str(); }
+
+int mft_set_sync_check(int on) {
+  return guarded([&] { mft::g_sync_check = on ? 1 : 0; });
+}
 const char* mft_version(void) { return "mft_hip 0.1 gfx950"; }
 
 int mft_create(mft_handle* out, void* stream) {

@@ -37,8 +37,17 @@ void set_last_error(const std::string& msg);
       throw ::mft::Error(MFT_EHIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
-// Kernel launch error check (catches invalid launch configurations).
-#define MFT_LAUNCH_CHECK() MFT_HIP(hipGetLastError())
+// Kernel launch error check (catches invalid launch configurations).  In
+// sync-check mode (mft_set_sync_check, or MFT_SYNC_CHECK=1 in the
+// environment) every check also waits for the device and reports an
+// execution error with the launch site that precedes it.
+extern int g_sync_check;
+void sync_check(const char* file, int line);
+#define MFT_LAUNCH_CHECK()                                   \
+  do {                                                       \
+    MFT_HIP(hipGetLastError());                              \
+    if (::mft::g_sync_check) ::mft::sync_check(__FILE__, __LINE__); \
+  } while (0)
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

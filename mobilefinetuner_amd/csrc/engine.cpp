@@ -1799,9 +1799,10 @@ int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps, flo
 int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, const int32_t* labels,
                          int n_micro, int seqs_per_micro, int S, float upstream, float lr, float b1,
                          float b2, float eps, float wd, float clip, int use_graph) {
-  // a streamed (sharded) model's pool addresses change from step to step:
-  // no captured graph
-  if (m && m->sh.budget > 0) use_graph = 0;
+  // no captured graph for a streamed (sharded) model, whose pool addresses
+  // change from step to step, or in sync-check mode, whose device waits
+  // cannot be captured
+  if (m && (m->sh.budget > 0 || g_sync_check)) use_graph = 0;
   return guarded([&] {
     if (!m || !ids || !labels) throw Error(MFT_EINVAL, "null argument");
     const int nseq = n_micro * seqs_per_micro;

@@ -616,6 +616,89 @@ static void test_gemma_trainer() {
   orc_model_destroy(om);
 }
 
+// Checkpoint and resume as the reference drivers do them (main.cpp:143-150,
+// 241-262): a run writes checkpoint-<step> every save_every steps; a run that
+// stops after the step-2 save is restarted from that file — base weights
+// from the model files, LoRA A/B through load_safetensors +
+// attach_from_state, a fresh optimizer and schedule.  The restored adapters
+// must equal the ones the first run held at the save bit for bit, and two
+// further trainer steps from them must match the oracle started from the
+// same adapters with a fresh AdamW.
+static void test_gemma_resume() {
+  const GemmaTextConfig cfg = tiny_gemma();
+  const std::string dir = "/tmp/mft_resume_" + std::to_string(getpid());
+  std::vector<std::string> names;
+  std::vector<std::vector<float>> at_save;
+  {
+    GemmaModel model(cfg);
+    GemmaLoraInjector injector;
+    injector.inject(model, GemmaLoraSpec::full_attn_mlp());
+    orc_model* om = tiny_gemma_oracle(0x7f);
+    init_both(model, om, 33);
+    orc_model_destroy(om);
+    SyntheticLM train(8, 9), eval(2, 10);
+    GemmaTrainerConfig tc;
+    tc.learning_rate = 1e-3f;
+    tc.micro_batch_size = 2;
+    tc.max_steps = 2;
+    tc.save_every = 2;
+    tc.warmup_ratio = 0.f;
+    tc.output_dir = dir;
+    GemmaLoRATrainer trainer(model, injector, train, eval, tc);
+    trainer.train();
+    for (auto& name : model.parameter_names())
+      if (name.find(".lora_") != std::string::npos) {
+        names.push_back(name);
+        at_save.push_back(host_copy(model.get_parameter(name)));
+      }
+  }  // the first run ends after its step-2 save
+  const std::string ckpt = dir + "/checkpoint-2/gemma_lora.safetensors";
+  check("resume checkpoint-2 written", std::filesystem::exists(ckpt) ? 0.0 : 1.0, 0.0);
+  GemmaModel model(cfg);
+  GemmaLoraInjector injector;
+  injector.inject(model, GemmaLoraSpec::full_attn_mlp());
+  orc_model* om = tiny_gemma_oracle(0x7f);
+  init_both(model, om, 33);  // the base weights, as loaded from the model files
+  LoraState st = LoraSaver::load_safetensors(ckpt);
+  check("resume checkpoint compatible", st.compatible_with(model) ? 0.0 : 1.0, 0.0);
+  LoraSaver::attach_from_state(model, st);
+  double worst = 0;
+  for (size_t i = 0; i < names.size(); ++i) {
+    const auto got = host_copy(model.get_parameter(names[i]));
+    worst = std::max(worst, rel_l2(got.data(), at_save[i].data(), (int64_t)got.size()));
+    std::memcpy(orc_model_param_data(om, oracle_index(om, names[i])), at_save[i].data(), at_save[i].size() * 4);
+  }
+  check("resume adapters restored bit for bit", worst, 0.0);
+  SyntheticLM train(8, 9), eval(2, 10), replay(8, 9);
+  GemmaTrainerConfig tc;
+  tc.learning_rate = 1e-3f;
+  tc.micro_batch_size = 2;
+  tc.max_steps = 2;
+  tc.warmup_ratio = 0.5f;
+  tc.output_dir = dir;
+  GemmaLoRATrainer trainer(model, injector, train, eval, tc);
+  trainer.train();
+  const auto& hist = trainer.history();
+  check("resumed run ran 2 steps", std::abs((int)hist.size() - 2), 0);
+  std::vector<float> mask(2 * 12, 1.f);
+  for (int step = 1; step <= (int)hist.size(); ++step) {
+    auto ids = replay.take(2, true);
+    const float loss = orc_model_fwd_bwd(om, ids.data(), mask.data(), ids.data(), 2, 12, 1.f);
+    orc_model_opt_step(om, trainer.lr_at(step), 0.9f, 0.999f, 1e-8f, 0.f, 1.f);
+    check("resumed step" + std::to_string(step) + " loss", std::abs(hist[step - 1].loss - loss) / loss, 1e-4);
+  }
+  std::vector<float> got, want;
+  for (auto& name : names) {
+    const auto g = host_copy(model.get_parameter(name));
+    const float* o = static_cast<const float*>(orc_model_param_data(om, oracle_index(om, name)));
+    got.insert(got.end(), g.begin(), g.end());
+    want.insert(want.end(), o, o + g.size());
+  }
+  check("resumed LoRA params after 2 more steps", rel_l2(got.data(), want.data(), (int64_t)got.size()), 1e-5);
+  orc_model_destroy(om);
+  std::filesystem::remove_all(dir);
+}
+
 // The Gemma driver's alignment-mode API: block handles and debug_params,
 // dumps, dlogits through retain_grad, and the layout ops it applies.
 static void test_gemma_debug_api() {
@@ -807,6 +890,7 @@ int main() {
     test_gemma(false);
     test_gemma(true);
     test_gemma_trainer();
+    test_gemma_resume();
     test_gemma_debug_api();
     MemoryManager::instance().force_cleanup();
   } catch (const std::exception& e) {

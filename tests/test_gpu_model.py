@@ -373,3 +373,29 @@ def test_graph_replay_equals_eager_steps():
             assert rel_err(b, a) < 1e-6, p["name"]
     for eng in models:
         eng.close()
+
+
+def test_sync_check_mode_gives_the_same_steps():
+    """Debug build mode (mft_set_sync_check): every launch is followed by a
+    device wait and error check, a requested graph step runs eagerly, and the
+    steps are bit-identical to the normal eager steps."""
+    from mobilefinetuner_amd._lib import call
+    mc = SMALL["gpt2"][0]
+    B, S = 2, 48
+    ids = torch.from_numpy(np.random.default_rng(21).integers(0, mc.vocab, (B * S,)).astype(np.int32)).cuda()
+    out = []
+    for mode in (0, 1):
+        eng = Model(mc, B * S)
+        for n, v in param_values(eng.params, seed=4).items():
+            eng.set_param(n, v)
+        call("mft_set_sync_check", mode)
+        try:
+            for _ in range(2):
+                eng.train_step(ids, ids, S=S, lr=1e-3, clip=1.0, graph=True)
+            out.append((eng.read_stats(), {p["name"]: eng.get(p["name"]) for p in eng.params if p["trainable"]}))
+        finally:
+            call("mft_set_sync_check", 0)
+        eng.close()
+    assert out[0][0] == out[1][0], (out[0][0], out[1][0])
+    for n in out[0][1]:
+        assert np.array_equal(out[0][1][n], out[1][1][n]), n

@@ -23,5 +23,6 @@ def test_cpp_operator_api_matches_oracle():
     for tag in ("ops chain dA", "gpt2 step1", "qwen2 step1", "qwen2-dropout step1", "gemma3 step1", "gemma3-fp16w step1",
                 "gpt2 checkpoint logits equal", "qwen2 checkpoint logits equal",
                 "gemma trainer step3 loss", "gemma trainer LoRA params after 3 steps",
+                "resume adapters restored bit for bit", "resumed LoRA params after 2 more steps",
                 "gemma retain_grad dlogits", "layout matmul"):
         assert any(tag in ln for ln in r.stdout.splitlines()), tag
