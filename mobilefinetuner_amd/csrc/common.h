@@ -344,6 +344,33 @@ void rmsnorm_fwd_seg(hipStream_t s, const float* x, int64_t x_ld, const float* w
 void rmsnorm_bwd_seg(hipStream_t s, const float* dy, int64_t dy_ld, const float* x, int64_t x_ld, const float* w,
                      const float* rstd, int64_t M, int64_t C, int seg, bool unit_offset, float* dx, int64_t dx_ld);
 void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm& nm);
+// RoPE angle table: tab[p·hd/2 + i] = (cos, sin)(p·θ^(−2i/hd)) for positions
+// p < npos, computed in double and rounded to float (the values the
+// per-element rope computes).
+void rope_table(hipStream_t s, double theta, int hd, int npos, float2* tab);
+// The head rows of q or k around attention: row r = (token t, head h) at
+// t·ld + h·hd (a strided view of a fused q|k|v buffer works).  With a norm
+// (w != null, Gemma3's per-head RMSNorm with the (1 + w) scale): x is the
+// projection output the norm reads (forward) or its input saved for the
+// backward, rstd its per-row 1/rms.
+struct HeadRows {
+  const float* in = nullptr;
+  int64_t in_ld = 0;
+  float* out = nullptr;
+  int64_t out_ld = 0;
+  int H = 0;
+  const float* w = nullptr;
+  float* rstd = nullptr;
+  const float* x = nullptr;
+  int64_t x_ld = 0;
+};
+// Forward: out = RoPE(RMSNorm(in)) (RoPE(in) without a norm; out may alias
+// in), q and k rows in one launch; position of token t is t mod S.
+void qk_rope_fwd(hipStream_t s, const HeadRows& q, const HeadRows& k, int64_t M, int S, int hd, float eps,
+                 const float2* tab, int npos);
+// Backward: out = RMSNormᵀ(RoPE⁻¹(in)) (RoPE⁻¹(in) without a norm).
+void qk_rope_bwd(hipStream_t s, const HeadRows& q, const HeadRows& k, int64_t M, int S, int hd,
+                 const float2* tab, int npos);
 // Split-K reduction (partials [splits][M][N], summed in split order) + the
 // GEMM epilogue + the row norm in one pass.  Returns false, launching
 // nothing, when the shape or alignment does not fit the fused kernel.

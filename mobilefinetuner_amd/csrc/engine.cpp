@@ -165,6 +165,9 @@ struct mft_model_s {
   float *dact = nullptr, *dgate = nullptr, *dup = nullptr;
   float *dtq = nullptr, *dtk = nullptr;
   float* row_nll = nullptr;
+  // RoPE angle tables (cos, sin) for positions [0, max_tokens): global θ and
+  // (Gemma3) the local layers' θ
+  float2* rope_tab[2] = {nullptr, nullptr};
   Scratch ws;
   // Merged LoRA weights and batched rank-r work.  With `merged`, every LoRA
   // linear multiplies by W_eff = W + s·Aᵀ·Bᵀ (rebuilt by one launch at the
@@ -707,6 +710,10 @@ void alloc_acts(mft_model_s* m) {
     m->dgate = b.f(M * ff);
     m->dup = b.f(M * ff);
     m->row_nll = b.f(M);
+    if (!gpt2) {
+      m->rope_tab[0] = reinterpret_cast<float2*>(b.f(M * hd));  // M positions × hd/2 pairs
+      if (gemma) m->rope_tab[1] = reinterpret_cast<float2*>(b.f(M * hd));
+    }
     const int64_t wide = std::max<int64_t>({d, ff, H * hd, 3 * d});
     const int64_t wsf = std::max<int64_t>(
         M * std::max<int64_t>(r, 1) + 16 * std::max<int64_t>(r, 1) * wide + 8 * M * wide,
@@ -728,6 +735,9 @@ void alloc_acts(mft_model_s* m) {
   // logits padding columns are never written and must stay finite (they are
   // read, times zero rows of E, by the LM-head backward's vector loads).
   MFT_HIP(hipMemset(m->logits, 0, sizeof(float) * (size_t)M * m->ldv));
+  if (m->rope_tab[0]) rope_table(m->stream, c.rope_theta, (int)hd, (int)M, m->rope_tab[0]);
+  if (m->rope_tab[1]) rope_table(m->stream, c.rope_local_theta, (int)hd, (int)M, m->rope_tab[1]);
+  MFT_HIP(hipStreamSynchronize(m->stream));
   void* sc = nullptr;
   MFT_HIP(hipMalloc(&sc, 4096));
   MFT_HIP(hipMemset(sc, 0, 4096));
@@ -1241,25 +1251,29 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       ep.bias = pd<float>(m, L.lin[T_Q].b);
       Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
       gemm(s, a.n1, d, L.lin[T_Q].weff, nt, false, false, a.qkv, nt, (int)M, nt, d, ep, m->ws, t.events());
-      if (gemma) {
-        rmsnorm_fwd_seg(s, a.qraw, nt, pd<float>(m, L.qn), M * H, hd, H, c.norm_eps, true, a.q, H * hd, a.qrs);
-        rmsnorm_fwd_seg(s, a.kraw, nt, pd<float>(m, L.kn), M * Hk, hd, Hk, c.norm_eps, true, a.k, Hk * hd, a.krs);
-      }
     } else {
-      if (gemma) {
-        lin_fwd(m, L.lin[T_Q], a.n1, M, a.qraw, a.xa[T_Q], nullptr);
-        lin_fwd(m, L.lin[T_K], a.n1, M, a.kraw, a.xa[T_K], nullptr);
-        rmsnorm_fwd(s, a.qraw, pd<float>(m, L.qn), M * H, hd, c.norm_eps, true, a.q, a.qrs);
-        rmsnorm_fwd(s, a.kraw, pd<float>(m, L.kn), M * Hk, hd, c.norm_eps, true, a.k, a.krs);
-      } else {
-        lin_fwd(m, L.lin[T_Q], a.n1, M, a.q, a.xa[T_Q], nullptr);
-        lin_fwd(m, L.lin[T_K], a.n1, M, a.k, a.xa[T_K], nullptr);
-      }
+      lin_fwd(m, L.lin[T_Q], a.n1, M, gemma ? a.qraw : a.q, a.xa[T_Q], nullptr);
+      lin_fwd(m, L.lin[T_K], a.n1, M, gemma ? a.kraw : a.k, a.xa[T_K], nullptr);
       lin_fwd(m, L.lin[T_V], a.n1, M, a.v, a.xa[T_V], nullptr);
     }
-    const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
-    rope(s, a.q, a.qs, nseq, S, H, hd, th, false);
-    rope(s, a.k, a.ks, nseq, S, Hk, hd, th, false);
+    {
+      // Gemma3's per-head q/k RMSNorms and RoPE (in place for Qwen2), q and
+      // k rows in one launch
+      const int64_t raw_ld = m->fuse_qkv ? m->nqkv : 0;
+      HeadRows hq, hk;
+      hq.H = (int)H;
+      hk.H = (int)Hk;
+      if (gemma) {
+        hq.in = a.qraw; hq.in_ld = raw_ld ? raw_ld : H * hd; hq.w = pd<float>(m, L.qn); hq.rstd = a.qrs;
+        hk.in = a.kraw; hk.in_ld = raw_ld ? raw_ld : Hk * hd; hk.w = pd<float>(m, L.kn); hk.rstd = a.krs;
+      } else {
+        hq.in = a.q; hq.in_ld = a.qs;
+        hk.in = a.k; hk.in_ld = a.ks;
+      }
+      hq.out = a.q; hq.out_ld = a.qs;
+      hk.out = a.k; hk.out_ld = a.ks;
+      qk_rope_fwd(s, hq, hk, M, S, hd, c.norm_eps, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
+    }
     attention_fwd(m, a, li, mask, nseq, S);
     if (gemma) {
       lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr);
@@ -1428,12 +1442,22 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
                  m->ws);
         t.end();
       }
-      const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
-      rope(s, dq, qld, nseq, S, H, hd, th, true);
-      rope(s, dk, kld, nseq, S, Hk, hd, th, true);
-      if (gemma) {
-        rmsnorm_bwd_seg(s, dq, qld, a.qraw, nt, pd<float>(m, L.qn), a.qrs, M * H, hd, H, true, a.DY[T_Q], nt);
-        rmsnorm_bwd_seg(s, dk, kld, a.kraw, nt, pd<float>(m, L.kn), a.krs, M * Hk, hd, Hk, true, a.DY[T_K], nt);
+      {
+        // RoPE's inverse (in place for Qwen2), then Gemma3's q/k norm
+        // backward into the fused gradient; q and k rows in one launch
+        HeadRows hq, hk;
+        hq.H = (int)H;
+        hk.H = (int)Hk;
+        hq.in = dq; hq.in_ld = qld;
+        hk.in = dk; hk.in_ld = kld;
+        if (gemma) {
+          hq.out = a.DY[T_Q]; hq.out_ld = nt; hq.w = pd<float>(m, L.qn); hq.rstd = a.qrs; hq.x = a.qraw; hq.x_ld = nt;
+          hk.out = a.DY[T_K]; hk.out_ld = nt; hk.w = pd<float>(m, L.kn); hk.rstd = a.krs; hk.x = a.kraw; hk.x_ld = nt;
+        } else {
+          hq.out = dq; hq.out_ld = qld;
+          hk.out = dk; hk.out_ld = kld;
+        }
+        qk_rope_bwd(s, hq, hk, M, S, hd, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
       }
       if (need_dx) {
         GemmEpilogue ep;
@@ -1455,18 +1479,27 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
                (int64_t)Hk * hd, dv, (int64_t)Hk * hd, m->ws);
       t.end();
     }
-    const double th = layer_local(c, li) ? c.rope_local_theta : c.rope_theta;
-    rope(s, dq, (int64_t)H * hd, nseq, S, H, hd, th, true);
-    rope(s, dk, (int64_t)Hk * hd, nseq, S, Hk, hd, th, true);
     const float* dqx = dq;
     const float* dkx = dk;
-    if (gemma) {
-      float* tq = dyb(li, T_Q, m->dtq);
-      float* tk = dyb(li, T_K, m->dtk);
-      rmsnorm_bwd(s, dq, a.qraw, pd<float>(m, L.qn), a.qrs, M * H, hd, true, tq, nullptr);
-      rmsnorm_bwd(s, dk, a.kraw, pd<float>(m, L.kn), a.krs, M * Hk, hd, true, tk, nullptr);
-      dqx = tq;
-      dkx = tk;
+    {
+      // RoPE's inverse (in place for Qwen2), then Gemma3's q/k norm
+      // backward; q and k rows in one launch
+      HeadRows hq, hk;
+      hq.H = (int)H;
+      hk.H = (int)Hk;
+      hq.in = dq; hq.in_ld = (int64_t)H * hd;
+      hk.in = dk; hk.in_ld = (int64_t)Hk * hd;
+      hq.out = dq; hq.out_ld = hq.in_ld;
+      hk.out = dk; hk.out_ld = hk.in_ld;
+      if (gemma) {
+        float* tq = dyb(li, T_Q, m->dtq);
+        float* tk = dyb(li, T_K, m->dtk);
+        hq.out = tq; hq.w = pd<float>(m, L.qn); hq.rstd = a.qrs; hq.x = a.qraw; hq.x_ld = hq.in_ld;
+        hk.out = tk; hk.w = pd<float>(m, L.kn); hk.rstd = a.krs; hk.x = a.kraw; hk.x_ld = hk.in_ld;
+        dqx = tq;
+        dkx = tk;
+      }
+      qk_rope_bwd(s, hq, hk, M, S, hd, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
     }
     // dn = dq·Wqᵀ + dk·Wkᵀ + dv·Wvᵀ accumulated in the GEMM epilogues, the
     // input norm's backward fused into the last one.

@@ -296,6 +296,134 @@ __global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy,
   rms_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, w, rstd[r], unit_offset, dx + o, resid ? resid + o : nullptr);
 }
 
+// ---- q/k head rows: per-head RMSNorm + RoPE in one pass -------------------
+// One wave per head row of hd = 64·E values, lane l holding values
+// [l·E, l·E + E): the RoPE partner of value i < hd/2 is i + hd/2, held by
+// lane l ^ 32 at the same slot, so the rotation is one lane exchange.  The
+// angles come from the table (no transcendental per element).  Rows of q
+// come first, then rows of k.
+__global__ void rope_table_kernel(double theta, int hd, int npos, float2* __restrict__ tab) {
+  const int half = hd / 2;
+  const int64_t n = (int64_t)npos * half;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(idx % half), p = (int)(idx / half);
+    const double inv = pow(theta, -2.0 * i / (double)hd);
+    double sn, cs;
+    sincos((double)p * inv, &sn, &cs);
+    tab[idx] = make_float2((float)cs, (float)sn);
+  }
+}
+
+template <int E>
+struct HeadVec {
+  float v[E];
+};
+
+template <int E>
+__device__ __forceinline__ HeadVec<E> load_head(const float* p) {
+  HeadVec<E> r;
+  if constexpr (E == 4) {
+    const floatx4 t = *reinterpret_cast<const floatx4*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.v[e] = t[e];
+  } else if constexpr (E == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+  } else {
+    r.v[0] = *p;
+  }
+  return r;
+}
+
+template <int E>
+__device__ __forceinline__ void store_head(float* p, const HeadVec<E>& r) {
+  if constexpr (E == 4) {
+    *reinterpret_cast<floatx4*>(p) = floatx4{r.v[0], r.v[1], r.v[2], r.v[3]};
+  } else if constexpr (E == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
+  } else {
+    *p = r.v[0];
+  }
+}
+
+// x rotated by the angle of (pos, slot): lanes < 32 hold the first half
+// (x1), lanes ≥ 32 the second (x2); out1 = x1·c − x2·s, out2 = x2·c + x1·s
+// (sign of s flipped for the inverse).
+template <int E>
+__device__ __forceinline__ void rotate(HeadVec<E>& r, const float2* __restrict__ trow, int lane, bool inverse) {
+  const bool upper = lane >= 32;
+  const int i0 = (lane & 31) * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float other = __shfl_xor(r.v[e], 32, 64);
+    const float2 cs = trow[i0 + e];
+    const float sn = inverse ? -cs.y : cs.y;
+    const float x1 = upper ? other : r.v[e], x2 = upper ? r.v[e] : other;
+    r.v[e] = upper ? x2 * cs.x + x1 * sn : x1 * cs.x - x2 * sn;
+  }
+}
+
+template <int E, bool NORM>
+__global__ __launch_bounds__(256) void qk_rope_fwd_kernel(HeadRows q, HeadRows k, int64_t M, int S, float eps,
+                                                          const float2* __restrict__ tab) {
+  constexpr int HD = 64 * E, HALF = HD / 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nq = M * q.H;
+  if (row >= nq + M * k.H) return;  // whole wave
+  const bool isq = row < nq;
+  const HeadRows& hr = isq ? q : k;
+  const int64_t r = isq ? row : row - nq;
+  const int64_t t = r / hr.H;
+  const int h = (int)(r % hr.H);
+  HeadVec<E> v = load_head<E>(hr.in + t * hr.in_ld + (int64_t)h * HD + lane * E);
+  if constexpr (NORM) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) s = fmaf(v.v[e], v.v[e], s);
+    const float rs = rsqrtf(wsum(s) / (float)HD + eps);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v.v[e] = v.v[e] * rs * (1.f + hr.w[lane * E + e]);
+    if (lane == 0) hr.rstd[r] = rs;
+  }
+  rotate<E>(v, tab + (int64_t)(t % S) * HALF, lane, false);
+  store_head<E>(hr.out + t * hr.out_ld + (int64_t)h * HD + lane * E, v);
+}
+
+template <int E, bool NORM>
+__global__ __launch_bounds__(256) void qk_rope_bwd_kernel(HeadRows q, HeadRows k, int64_t M, int S,
+                                                          const float2* __restrict__ tab) {
+  constexpr int HD = 64 * E, HALF = HD / 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nq = M * q.H;
+  if (row >= nq + M * k.H) return;  // whole wave
+  const bool isq = row < nq;
+  const HeadRows& hr = isq ? q : k;
+  const int64_t r = isq ? row : row - nq;
+  const int64_t t = r / hr.H;
+  const int h = (int)(r % hr.H);
+  HeadVec<E> g = load_head<E>(hr.in + t * hr.in_ld + (int64_t)h * HD + lane * E);
+  rotate<E>(g, tab + (int64_t)(t % S) * HALF, lane, true);
+  if constexpr (NORM) {
+    const HeadVec<E> x = load_head<E>(hr.x + t * hr.x_ld + (int64_t)h * HD + lane * E);
+    const float rs = hr.rstd[r];
+    float xh[E];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      g.v[e] *= 1.f + hr.w[lane * E + e];  // dy·w'
+      xh[e] = x.v[e] * rs;                 // x̂
+      s = fmaf(g.v[e], xh[e], s);
+    }
+    s = wsum(s) / (float)HD;
+#pragma unroll
+    for (int e = 0; e < E; ++e) g.v[e] = rs * (g.v[e] - xh[e] * s);
+  }
+  store_head<E>(hr.out + t * hr.out_ld + (int64_t)h * HD + lane * E, g);
+}
+
 // ---- split-K reduction + GEMM epilogue + norm ------------------------------
 // Each row group finishes one row of C: the partials are summed in split
 // order and the epilogue (bias, residual, beta·C, GELU') applied exactly as
@@ -491,6 +619,66 @@ void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm
     case NORM_RMS_BWD: return rmsnorm_bwd(s, c, nm.x, nm.w, nm.rstd, M, C, nm.unit_offset != 0, nm.y, nm.resid);
     default: MFT_CHECK_ARG(false, "unknown norm kind");
   }
+}
+
+void rope_table(hipStream_t s, double theta, int hd, int npos, float2* tab) {
+  MFT_CHECK_ARG(hd % 2 == 0 && npos > 0 && tab, "rope table: bad shape");
+  const int64_t n = (int64_t)npos * (hd / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 4096)), dim3(256), 0, s,
+                     theta, hd, npos, tab);
+  MFT_LAUNCH_CHECK();
+}
+
+namespace {
+void check_heads(const HeadRows& r, int hd, bool fwd) {
+  const int E = hd / 64;
+  MFT_CHECK_ARG(r.H > 0 && r.in && r.out && r.in_ld >= (int64_t)r.H * hd && r.out_ld >= (int64_t)r.H * hd,
+                "q/k head rows: bad shape");
+  MFT_CHECK_ARG(r.in_ld % E == 0 && r.out_ld % E == 0 && ((uintptr_t)r.in % (4 * E)) == 0 &&
+                    ((uintptr_t)r.out % (4 * E)) == 0,
+                "q/k head rows: rows must be aligned to the lane vector");
+  if (r.w) {
+    MFT_CHECK_ARG(r.rstd != nullptr, "q/k head norm: rstd required");
+    if (!fwd)
+      MFT_CHECK_ARG(r.x && r.x_ld >= (int64_t)r.H * hd && r.x_ld % E == 0 && ((uintptr_t)r.x % (4 * E)) == 0,
+                    "q/k head norm backward: saved input rows required");
+  }
+}
+}  // namespace
+
+#define MFT_QK_DISPATCH(KERNEL, NORM, ...)                                                                    \
+  do {                                                                                                        \
+    if (hd == 64) hipLaunchKernelGGL((KERNEL<1, NORM>), __VA_ARGS__);                                          \
+    else if (hd == 128) hipLaunchKernelGGL((KERNEL<2, NORM>), __VA_ARGS__);                                    \
+    else hipLaunchKernelGGL((KERNEL<4, NORM>), __VA_ARGS__);                                                   \
+  } while (0)
+
+void qk_rope_fwd(hipStream_t s, const HeadRows& q, const HeadRows& k, int64_t M, int S, int hd, float eps,
+                 const float2* tab, int npos) {
+  MFT_CHECK_ARG(hd == 64 || hd == 128 || hd == 256, "q/k head rows: head_dim must be 64, 128 or 256");
+  MFT_CHECK_ARG(M > 0 && S > 0 && M % S == 0 && S <= npos && tab, "q/k head rows: positions past the RoPE table");
+  MFT_CHECK_ARG((q.w == nullptr) == (k.w == nullptr), "q/k head rows: both or neither normalised");
+  check_heads(q, hd, true);
+  check_heads(k, hd, true);
+  const int64_t rows = M * (q.H + k.H);
+  const dim3 grid((unsigned)cdiv(rows, 4)), block(256);
+  if (q.w) MFT_QK_DISPATCH(qk_rope_fwd_kernel, true, grid, block, 0, s, q, k, M, S, eps, tab);
+  else MFT_QK_DISPATCH(qk_rope_fwd_kernel, false, grid, block, 0, s, q, k, M, S, eps, tab);
+  MFT_LAUNCH_CHECK();
+}
+
+void qk_rope_bwd(hipStream_t s, const HeadRows& q, const HeadRows& k, int64_t M, int S, int hd, const float2* tab,
+                 int npos) {
+  MFT_CHECK_ARG(hd == 64 || hd == 128 || hd == 256, "q/k head rows: head_dim must be 64, 128 or 256");
+  MFT_CHECK_ARG(M > 0 && S > 0 && M % S == 0 && S <= npos && tab, "q/k head rows: positions past the RoPE table");
+  MFT_CHECK_ARG((q.w == nullptr) == (k.w == nullptr), "q/k head rows: both or neither normalised");
+  check_heads(q, hd, false);
+  check_heads(k, hd, false);
+  const int64_t rows = M * (q.H + k.H);
+  const dim3 grid((unsigned)cdiv(rows, 4)), block(256);
+  if (q.w) MFT_QK_DISPATCH(qk_rope_bwd_kernel, true, grid, block, 0, s, q, k, M, S, tab);
+  else MFT_QK_DISPATCH(qk_rope_bwd_kernel, false, grid, block, 0, s, q, k, M, S, tab);
+  MFT_LAUNCH_CHECK();
 }
 
 bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, float* C, int64_t ldc,
