@@ -319,6 +319,19 @@ void set_hparams(hipStream_t s, float* hp, float lr, float b1, float b2, float e
                  float max_norm, double* ss, int* tstep);
 void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t n);
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out);
+// The step engine's optimizer in two launches: opt_partials writes one
+// Σg² partial per workgroup (kOptBlocks of them, fixed order, no atomics)
+// and, given hp_args (the eager step), the hyper-parameters and the step
+// count as set_hparams does; adam_partials sums the partials in a fixed
+// order in every workgroup, clips and applies Adam as adam_step_dev.
+constexpr int kOptBlocks = 256;
+struct HpArgs {
+  float lr, b1, b2, eps, wd, max_norm;
+};
+void opt_partials(hipStream_t s, const float* g, int64_t n, double* partials, const HpArgs* hp_args, float* hp,
+                  int* tstep);
+void adam_partials(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n, const float* hp,
+                   const int* tstep, const double* partials, float* clip_out, bool zero_grad);
 void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,
                 float* norm);
 void layernorm_fwd(hipStream_t s, const float* x, const float* g,

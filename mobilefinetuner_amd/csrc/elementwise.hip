@@ -353,6 +353,71 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g,
   if (threadIdx.x == 0) atomicAdd(out, red[0] + red[1] + red[2] + red[3]);
 }
 
+__global__ __launch_bounds__(256) void opt_partials_kernel(const float* __restrict__ g, int64_t n,
+                                                           double* __restrict__ partials, HpArgs a, int write_hp,
+                                                           float* __restrict__ hp, int* __restrict__ tstep) {
+  __shared__ double red[4];
+  if (write_hp && blockIdx.x == 0 && threadIdx.x == 0) {
+    hp[0] = a.lr; hp[1] = a.b1; hp[2] = a.b2; hp[3] = a.eps; hp[4] = a.wd; hp[5] = a.max_norm;
+    *tstep += 1;
+  }
+  double s = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const double x = g[i];
+    s += x * x;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partials[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Adam with the clip factor from kOptBlocks Σg² partials, summed by every
+// workgroup in the same order (one per thread, then a fixed tree).
+__global__ __launch_bounds__(256) void adam_partials_kernel(float* __restrict__ p, float* __restrict__ g,
+                                                            float* __restrict__ m, float* __restrict__ v, int64_t n,
+                                                            const float* __restrict__ hp,
+                                                            const int* __restrict__ tstep,
+                                                            const double* __restrict__ partials,
+                                                            float* __restrict__ out, int zero_grad) {
+  static_assert(kOptBlocks == 256, "one partial per thread");
+  __shared__ double red[4];
+  double ps = partials[threadIdx.x];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ps;
+  __syncthreads();
+  const double ss = (red[0] + red[1]) + (red[2] + red[3]);
+  const float lr = hp[0], b1 = hp[1], b2 = hp[2], eps = hp[3], wd = hp[4], max_norm = hp[5];
+  const int t = *tstep;
+  const double bc1 = 1.0 - pow((double)b1, (double)t);
+  const double bc2 = 1.0 - pow((double)b2, (double)t);
+  float nv = (float)sqrt(ss);
+  float cs = 1.f;
+  if (max_norm > 0.f && nv > max_norm) {
+    cs = max_norm / (nv + 1e-6f);
+    nv = max_norm;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    out[0] = cs;
+    out[1] = nv;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float gi = g[i] * cs;
+    const float mi = b1 * m[i] + (1.f - b1) * gi;
+    const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
+    m[i] = mi;
+    v[i] = vi;
+    const double mh = mi / bc1, vh = vi / bc2;
+    double pi = p[i];
+    if (wd != 0.f) pi -= (double)lr * wd * pi;
+    pi -= (double)lr * mh / (sqrt(vh) + eps);
+    p[i] = (float)pi;
+    if (zero_grad) g[i] = 0.f;
+  }
+}
+
 __global__ void clip_kernel(const double* ss, float max_norm, float* scale,
                             float* norm) {
   float nv = (float)sqrt(*ss);
@@ -588,6 +653,20 @@ void add_out(hipStream_t s, float* out, const float* a, const float* b, int64_t 
 void sumsq(hipStream_t s, const float* g, int64_t n, double* out) {
   if (n <= 0) return;
   hipLaunchKernelGGL(sumsq_kernel, dim3(grid_for(n, 256, 1024)), dim3(256), 0, s, g, n, out);
+  MFT_LAUNCH_CHECK();
+}
+void opt_partials(hipStream_t s, const float* g, int64_t n, double* partials, const HpArgs* hp_args, float* hp,
+                  int* tstep) {
+  const HpArgs a = hp_args ? *hp_args : HpArgs{};
+  hipLaunchKernelGGL(opt_partials_kernel, dim3(kOptBlocks), dim3(256), 0, s, g, n, partials, a, hp_args ? 1 : 0, hp,
+                     tstep);
+  MFT_LAUNCH_CHECK();
+}
+void adam_partials(hipStream_t s, float* p, float* g, float* m, float* v, int64_t n, const float* hp,
+                   const int* tstep, const double* partials, float* clip_out, bool zero_grad) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(adam_partials_kernel, dim3(grid_for(n, 256, 2048)), dim3(256), 0, s, p, g, m, v, n, hp, tstep,
+                     partials, clip_out, zero_grad ? 1 : 0);
   MFT_LAUNCH_CHECK();
 }
 void clip_scale(hipStream_t s, const double* ss, float max_norm, float* scale,

@@ -199,6 +199,7 @@ struct mft_model_s {
   int64_t* d_cnt = nullptr;
   int64_t* d_tmpcnt = nullptr;
   double* d_sumsq = nullptr;
+  double* d_partials = nullptr;  // kOptBlocks Σg² partials of the optimizer
   float* d_clip = nullptr;  // [0] scale, [1] norm
   float* d_hp = nullptr;    // {lr, b1, b2, eps, wd, max_norm}
   int* d_t = nullptr;       // Adam step count (advanced on the device)
@@ -739,8 +740,8 @@ void alloc_acts(mft_model_s* m) {
   if (m->rope_tab[1]) rope_table(m->stream, c.rope_local_theta, (int)hd, (int)M, m->rope_tab[1]);
   MFT_HIP(hipStreamSynchronize(m->stream));
   void* sc = nullptr;
-  MFT_HIP(hipMalloc(&sc, 4096));
-  MFT_HIP(hipMemset(sc, 0, 4096));
+  MFT_HIP(hipMalloc(&sc, 4096 + kOptBlocks * sizeof(double)));
+  MFT_HIP(hipMemset(sc, 0, 4096 + kOptBlocks * sizeof(double)));
   m->d_loss = reinterpret_cast<double*>(sc);                               // 64 doubles
   m->d_cnt = reinterpret_cast<int64_t*>(static_cast<char*>(sc) + 512);     // 64 int64
   m->d_tmpcnt = reinterpret_cast<int64_t*>(static_cast<char*>(sc) + 1024);
@@ -750,6 +751,7 @@ void alloc_acts(mft_model_s* m) {
   m->d_t = reinterpret_cast<int*>(static_cast<char*>(sc) + 2048);
   m->d_err = reinterpret_cast<int*>(static_cast<char*>(sc) + 2304);
   m->d_drop_step = reinterpret_cast<int*>(static_cast<char*>(sc) + 2560);
+  m->d_partials = reinterpret_cast<double*>(static_cast<char*>(sc) + 4096);
   MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
@@ -1513,20 +1515,21 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
   run_batch(m, m->da_batch, M);   // dA += s·Uᵀ·x of every LoRA linear
 }
 
-// Hyper-parameters reach the device as kernel arguments of a one-block
-// kernel launched ahead of the optimizer (or of the captured step graph), so
-// no host buffer is read by the device.
+// Hyper-parameters reach the device as kernel arguments: of the optimizer's
+// first launch in an eager step, of a one-block kernel launched ahead of a
+// captured step graph's replay — no host buffer is read by the device.
 void upload_hparams(mft_model_s* m, float lr, float b1, float b2, float eps, float wd, float clip) {
   set_hparams(m->stream, m->d_hp, lr, b1, b2, eps, wd, clip, m->d_sumsq, m->d_t);
 }
 
-// clip_and_get_grad_norm + Adam::step + zero_grad on the flat LoRA arrays;
-// reads d_hp / d_t only, so it can live inside a captured graph.  Follows
-// upload_hparams, which advanced d_t and cleared d_sumsq.
-void opt_device(mft_model_s* m) {
+// clip_and_get_grad_norm + Adam::step + zero_grad on the flat LoRA arrays
+// in two launches.  With hp (an eager step) the first launch also writes the
+// hyper-parameters and advances d_t; without (a captured graph, or after an
+// explicit upload_hparams) it reads d_hp / d_t only.
+void opt_device(mft_model_s* m, const HpArgs* hp = nullptr) {
   const hipStream_t s = m->stream;
-  sumsq(s, m->lora_g, m->lora_n, m->d_sumsq);
-  adam_step_dev(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, m->d_hp, m->d_t, m->d_sumsq, m->d_clip,
+  opt_partials(s, m->lora_g, m->lora_n, m->d_partials, hp, m->d_hp, m->d_t);
+  adam_partials(s, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->lora_n, m->d_hp, m->d_t, m->d_partials, m->d_clip,
                 true);
 }
 
@@ -1823,8 +1826,8 @@ int mft_model_backward(mft_model m, const float* mask, int nseq, int S) {
 int mft_model_opt_step(mft_model m, float lr, float b1, float b2, float eps, float wd, float clip) {
   return guarded([&] {
     if (!m) throw Error(MFT_EINVAL, "null model");
-    upload_hparams(m, lr, b1, b2, eps, wd, clip);
-    opt_device(m);
+    const HpArgs hp{lr, b1, b2, eps, wd, clip};
+    opt_device(m, &hp);
     m->adam_t++;
   });
 }
@@ -1848,8 +1851,8 @@ int mft_model_train_step(mft_model m, const int32_t* ids, const float* mask, con
       forward(m, ids, mask, nseq, S, m->training, n_micro);
       cross_entropy(m, labels, n_micro, seqs_per_micro, S, upstream, true);
       backward(m, mask, nseq, S);
-      upload_hparams(m, lr, b1, b2, eps, wd, clip);
-      opt_device(m);
+      const HpArgs hp{lr, b1, b2, eps, wd, clip};
+      opt_device(m, &hp);
       m->adam_t++;
       return;
     }
