@@ -19,38 +19,6 @@
 namespace mft {
 namespace {
 
-// Counts the valid shifted targets: label != ignore_index and inside
-// [0, V) — the same test ce_row_kernel applies, so an out-of-range label is
-// excluded from both the loss and its normaliser (and flagged in *bad).
-// One workgroup: the count is stored, not accumulated, so no clearing
-// launch precedes it.
-__global__ __launch_bounds__(1024) void ce_count_kernel(const int32_t* __restrict__ labels,
-                                                        int B, int S, int64_t V, int ignore_index,
-                                                        int64_t* cnt, int* bad) {
-  __shared__ int red[16];
-  int c = 0;
-  bool out_of_range = false;
-  const int64_t total = (int64_t)B * S;
-  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
-    const int s = (int)(i % S);
-    if (s + 1 >= S) continue;
-    const int lab = labels[i + 1];
-    if (lab == ignore_index) continue;
-    if (lab >= 0 && (int64_t)lab < V) c++;
-    else out_of_range = true;
-  }
-  if (out_of_range && bad) atomicOr(bad, 1);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int64_t v = 0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) v += red[w];
-    *cnt = v;
-  }
-}
-
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -65,6 +33,47 @@ __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2)
   m = mm;
 }
 
+// The micro-batch's valid shifted targets, counted by every row workgroup:
+// position s < S−1 whose next label is neither ignore_index nor outside
+// [0, V) — the test the row itself applies, so an out-of-range label is
+// excluded from both the loss and its normaliser (and flagged in *bad).
+// This thread's share over i = tid, tid + BLOCK, …; `oor` is set when the
+// share met an out-of-range label.  The loads are independent of the row's,
+// so they overlap its reads.  The count is stored (by workgroup 0), not
+// accumulated, so no clearing launch precedes it.
+__device__ __forceinline__ int count_share(const int32_t* __restrict__ labels, int B, int S, int64_t V,
+                                           int ignore_index, int tid, int block, bool& oor) {
+  int c = 0;
+  const int64_t total = (int64_t)B * S;
+  for (int64_t i = tid; i < total; i += block) {
+    const int s = (int)(i % S);
+    if (s + 1 >= S) continue;
+    const int lab = labels[i + 1];
+    if (lab == ignore_index) continue;
+    if (lab >= 0 && (int64_t)lab < V) c++;
+    else oor = true;
+  }
+  return c;
+}
+
+// Workgroup 0 publishes the count (for the loss sum) and the bad-label flag.
+// red: NW ints of LDS; a full workgroup reduction with its own barrier, for a
+// workgroup whose row takes no other reduction.
+template <int NW>
+__device__ __forceinline__ void publish_count(int c, bool oor, int* red, int64_t* cnt, int* bad) {
+  if (blockIdx.x != 0) return;
+  if (oor && bad) atomicOr(bad, 1);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t v = 0;
+    for (int w = 0; w < NW; ++w) v += red[w];
+    *cnt = v;
+  }
+}
+
 // One workgroup per logits row.  The row is walked as an aligned float4 body
 // (rows start at any 4-byte offset when V is odd) plus a scalar head and
 // tail.  The first H·BLOCK float4 of the body stay in registers from the
@@ -75,25 +84,32 @@ __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2)
 // each group of 4·U values folded into the thread's running (max, Σ) pair
 // with one rescale, and re-read by the gradient sweep, which writes dlogits
 // in place.
+// The micro-batch's target count is formed in every workgroup beside the
+// row's statistics (workgroup 0 stores it in *cnt and raises *bad).
 template <int BLOCK, int H>
 __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S,
     int64_t V, int64_t ld, int ignore_index, float upstream, int64_t norm_count,
-    const int64_t* __restrict__ cnt, float* dlogits, float* __restrict__ row_nll) {
+    int64_t* __restrict__ cnt, int* bad, float* dlogits, float* __restrict__ row_nll) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
+  __shared__ int sc[NW];
   const int64_t row = blockIdx.x;
   const int s = (int)(row % S);
   const int label = (s + 1 < S) ? labels[row + 1] : ignore_index;
   const float* x = logits + row * ld;
   float* dx = dlogits ? dlogits + row * ld : nullptr;
   const int tid = threadIdx.x;
+  bool oor = false;
+  int c = count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
   if (label == ignore_index || label < 0 || (int64_t)label >= V) {
+    publish_count<NW>(c, oor, sc, cnt, bad);
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
     return;
   }
+  if (blockIdx.x == 0 && oor && bad) atomicOr(bad, 1);
   const float xl = x[label];  // read before any thread writes (dx may alias x)
   const int64_t head = std::min<int64_t>((4 - (((uintptr_t)x >> 2) & 3)) & 3, V);
   const int64_t n4 = (V - head) / 4;
@@ -153,21 +169,28 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float m2 = __shfl_xor(m, off, 64);
     const float s2 = __shfl_xor(sum, off, 64);
     merge_ms(m, sum, m2, s2);
+    c += __shfl_xor(c, off, 64);
   }
   const int w = tid >> 6;
   if ((tid & 63) == 0) {
     sm[w] = m;
     ss[w] = sum;
+    sc[w] = c;
   }
   __syncthreads();
   m = sm[0];
   sum = ss[0];
+  int64_t n_valid = sc[0];
 #pragma unroll
-  for (int i = 1; i < NW; ++i) merge_ms(m, sum, sm[i], ss[i]);
+  for (int i = 1; i < NW; ++i) {
+    merge_ms(m, sum, sm[i], ss[i]);
+    n_valid += sc[i];
+  }
+  if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
   const float lse2 = m + __builtin_amdgcn_logf(sum);  // log2 Σ 2^t (sum ≥ 1)
   if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
   if (!dx) return;
-  const int64_t n = norm_count > 0 ? norm_count : *cnt;
+  const int64_t n = norm_count > 0 ? norm_count : n_valid;
   const float g = n > 0 ? upstream / (float)n : 0.f;
   // dlogits = (softmax − onehot(label))·g; every element is read before the
   // same thread writes it.
@@ -221,22 +244,27 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
 template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S, int64_t V, int64_t ld,
-    int ignore_index, float upstream, int64_t norm_count, const int64_t* __restrict__ cnt, float* dlogits,
+    int ignore_index, float upstream, int64_t norm_count, int64_t* __restrict__ cnt, int* bad, float* dlogits,
     float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
+  __shared__ int sc[NW];
   const int64_t row = blockIdx.x;
   const int s = (int)(row % S);
   const int label = (s + 1 < S) ? labels[row + 1] : ignore_index;
   const float* x = logits + row * ld;
   float* dx = dlogits ? dlogits + row * ld : nullptr;
   const int tid = threadIdx.x;
+  bool oor = false;
+  int c = count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
   if (label == ignore_index || label < 0 || (int64_t)label >= V) {
+    publish_count<NW>(c, oor, sc, cnt, bad);
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
     return;
   }
+  if (blockIdx.x == 0 && oor && bad) atomicOr(bad, 1);
   const float xl = x[label];  // read before any thread writes (dx may alias x)
   const int64_t nb = (V + 63) / 64;
   const float2* st = stats + row * stats_ld;
@@ -250,21 +278,28 @@ __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     const float m2 = __shfl_xor(m, off, 64);
     const float s2 = __shfl_xor(sum, off, 64);
     merge_ms(m, sum, m2, s2);
+    c += __shfl_xor(c, off, 64);
   }
   const int w = tid >> 6;
   if ((tid & 63) == 0) {
     sm[w] = m;
     ss[w] = sum;
+    sc[w] = c;
   }
   __syncthreads();
   m = sm[0];
   sum = ss[0];
+  int64_t n_valid = sc[0];
 #pragma unroll
-  for (int i = 1; i < NW; ++i) merge_ms(m, sum, sm[i], ss[i]);
+  for (int i = 1; i < NW; ++i) {
+    merge_ms(m, sum, sm[i], ss[i]);
+    n_valid += sc[i];
+  }
+  if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
   const float lse2 = m + __builtin_amdgcn_logf(sum);
   if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
   if (!dx) return;
-  const int64_t n = norm_count > 0 ? norm_count : *cnt;
+  const int64_t n = norm_count > 0 ? norm_count : n_valid;
   const float g = n > 0 ? upstream / (float)n : 0.f;
   const int64_t head = std::min<int64_t>((4 - (((uintptr_t)x >> 2) & 3)) & 3, V);
   const int64_t n4 = (V - head) / 4;
@@ -327,23 +362,20 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
-  hipLaunchKernelGGL(ce_count_kernel, dim3(1), dim3(1024), 0, s, labels, B, S, V, ignore_index, count_scratch,
-                     bad_label);
-  MFT_LAUNCH_CHECK();
   // rows of up to 13·4096 values are held whole in registers (GPT-2's
   // 50257); wider rows take the LM head's row statistics when it wrote them
   // (one sweep), else keep their first 16·4096 values in registers
   if (row_stats && V > 13 * 4096) {
     MFT_CHECK_ARG(stats_ld >= cdiv(V, 64), "row statistics pitch");
     hipLaunchKernelGGL((ce_row_stats_kernel<1024>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll,
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll,
                        row_stats, stats_ld);
   } else if (V <= 13 * 4096)
     hipLaunchKernelGGL((ce_row_kernel<1024, 13>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll);
   else
     hipLaunchKernelGGL((ce_row_kernel<1024, 16>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, (const int64_t*)count_scratch, dlogits, row_nll);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,
                      (const int64_t*)count_scratch, n_valid);

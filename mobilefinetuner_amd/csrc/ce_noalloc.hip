@@ -55,7 +55,7 @@ extern "C" int mft_ce_fwd_bwd_noalloc(mft_handle h, const float* logits, const i
                                        " rows exceeds the no-allocation maximum of " +
                                        std::to_string(mft::kCeNoAllocMaxRows));
     char* base = mft::scratch_on_current_device();
-    int64_t* cnt = reinterpret_cast<int64_t*>(base);  // zeroed by a fill kernel inside ce_fwd_bwd
+    int64_t* cnt = reinterpret_cast<int64_t*>(base);  // stored (not accumulated) inside ce_fwd_bwd
     float* nll = row_nll ? row_nll : reinterpret_cast<float*>(base + 256);
     mft::ce_fwd_bwd(h->stream, logits, labels, B, S, V, V, ignore_index, upstream, norm_count, loss_sum, n_valid,
                     dlogits, nll, cnt);

@@ -410,6 +410,13 @@ void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
 void embed(hipStream_t s, const int32_t* ids, int64_t M, int S,
            const void* wte, int64_t V, bool w_f16, const float* wpe, int64_t C,
            float scale, float* out, int* bad);
+// embed() followed by row_norm(x, nm) (LayerNorm or RMSNorm forward) in one
+// launch; workgroup 0 also zeroes `zero` (nzero 8-byte words, nullable).
+// Returns false, launching nothing, when the row layout does not allow it
+// (C % 4, C > 4096, unaligned rows).
+bool embed_norm(hipStream_t s, const int32_t* ids, int64_t M, int S, const void* wte, int64_t V, bool w_f16,
+                const float* wpe, int64_t C, float scale, float* x, int* bad, const RowNorm& nm, void* zero,
+                int nzero);
 void add_inplace(hipStream_t s, float* a, const float* b, int64_t n);
 void fill_normal(hipStream_t s, float* p, int64_t n, uint64_t seed, float std,
                  float mean);

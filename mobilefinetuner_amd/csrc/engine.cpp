@@ -132,6 +132,10 @@ struct ShardStore {
   int64_t loads = 0, hits = 0;
 };
 
+// Loss and count slots of a step: 64 doubles then 64 int64 (8-byte words).
+constexpr int kStatWords = 128;
+static_assert(sizeof(double) == 8 && sizeof(int64_t) == 8, "stat slots");
+
 struct mft_model_s {
   mft_model_cfg c{};
   ShardStore sh;
@@ -200,6 +204,7 @@ struct mft_model_s {
   int64_t* d_tmpcnt = nullptr;
   double* d_sumsq = nullptr;
   double* d_partials = nullptr;  // kOptBlocks Σg² partials of the optimizer
+  bool zero_pending = false;      // the loss/count slots are cleared by the next forward's first launch
   float* d_clip = nullptr;  // [0] scale, [1] norm
   float* d_hp = nullptr;    // {lr, b1, b2, eps, wd, max_norm}
   int* d_t = nullptr;       // Adam step count (advanced on the device)
@@ -1199,11 +1204,6 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   m->last_rows = M;
   shard_begin(m);
   merge_lora(m);  // A, B (or W) may have changed since the last forward
-  {
-    const WeightUse we(m, m->wte);
-    embed(s, ids, M, S, we.ptr, c.vocab, E.f16, gpt2 ? pd<float>(m, m->wpe) : nullptr, d,
-          gemma ? std::sqrt((float)d) : 1.f, m->A[0].x, m->d_err);
-  }
   // Input norm of layer li (li == n_layer: the final norm).  GPT-2 and Qwen2
   // run it inside the GEMM that produced its input (the previous layer's
   // residual-fused down projection); Gemma3's post-norms sit in between.
@@ -1233,11 +1233,27 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     nm.rstd = a.rstd2;
     return nm;
   };
+  // The embedding gather and layer 0's input norm run as one launch, which
+  // also clears the step's loss and count slots when a step begins.
+  bool first_norm = false;
+  {
+    const WeightUse we(m, m->wte);
+    const float* wpe = gpt2 ? pd<float>(m, m->wpe) : nullptr;
+    const float scale = gemma ? std::sqrt((float)d) : 1.f;
+    void* zero = m->zero_pending ? static_cast<void*>(m->d_loss) : nullptr;
+    first_norm = embed_norm(s, ids, M, S, we.ptr, c.vocab, E.f16, wpe, d, scale, m->A[0].x, m->d_err, norm1(0),
+                            zero, kStatWords);
+    if (!first_norm) {
+      if (zero) fill_const(s, static_cast<float*>(zero), 2 * kStatWords, 0.f);
+      embed(s, ids, M, S, we.ptr, c.vocab, E.f16, wpe, d, scale, m->A[0].x, m->d_err);
+    }
+    m->zero_pending = false;
+  }
   for (int li = 0; li < c.n_layer; ++li) {
     const Layer& L = m->L[li];
     Acts& a = m->A[li];
     float* hout = li + 1 < c.n_layer ? m->A[li + 1].x : m->h_final;
-    if (li == 0 || gemma) row_norm(s, a.x, M, d, norm1(li));
+    if ((li == 0 && !first_norm) || (li > 0 && gemma)) row_norm(s, a.x, M, d, norm1(li));
     const RowNorm n2 = norm2(li), nx = norm1(li + 1);
     if (gpt2) {
       lin_fwd(m, L.lin[G_ATTN], a.n1, M, a.q, a.xa[G_ATTN], nullptr);
@@ -1533,12 +1549,11 @@ void opt_device(mft_model_s* m, const HpArgs* hp = nullptr) {
                 true);
 }
 
+// The 64 per-micro loss sums (doubles) and the 64 counts (int64) that follow
+// them are cleared by the step's first launch (the forward's embedding).
 void zero_stats(mft_model_s* m, int n_micro) {
-  // the 64 per-micro loss sums (doubles) and the 64 counts (int64) that
-  // follow them: one launch over both arrays
   (void)n_micro;
-  static_assert(sizeof(double) == 8 && sizeof(int64_t) == 8, "stat slots");
-  fill_const(m->stream, reinterpret_cast<float*>(m->d_loss), (512 + 512) / 4, 0.f);
+  m->zero_pending = true;
 }
 
 void drop_graph(mft_model_s* m) {

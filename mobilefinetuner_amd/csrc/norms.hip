@@ -531,6 +531,80 @@ dim3 row_grid(int64_t M, const RowShape& sh) { return dim3((unsigned)cdiv(M, 4 /
     else hipLaunchKernelGGL((KERNEL<4, 4>), __VA_ARGS__);                     \
   } while (0)
 
+// ---- embedding gather + the first layer's input norm ----------------------
+// Row r: e = wte[ids[r]]·scale (+ wpe[r mod S]) is stored as the residual
+// stream x (an id outside [0, V) stores a zero row and raises *bad), then
+// normalised from registers into nm.y, exactly as embed() followed by
+// row_norm().  Workgroup 0 also clears `zero` (nzero 8-byte words: the
+// step's loss and count slots), so neither needs a launch of its own.
+template <int NV, int RW, int KIND, bool F16>
+__global__ __launch_bounds__(256) void embed_norm_vec(const int32_t* __restrict__ ids, int64_t M, int S,
+                                                      const void* __restrict__ wte, int64_t V,
+                                                      const float* __restrict__ wpe, int C, float scale,
+                                                      float* __restrict__ x, int* bad, RowNorm nm,
+                                                      unsigned long long* zero, int nzero) {
+  __shared__ float red[4][4];
+  if (zero && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < nzero; i += 256) zero[i] = 0ull;
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
+  const int64_t id = ids[r];
+  const bool ok = id >= 0 && id < V;
+  const int C4 = C / 4;
+  const int64_t pos = r % S;
+  floatx4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int q = pl.gl + 64 * RW * i;
+    v[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (q >= C4 || !ok) continue;
+    floatx4 e;
+    if constexpr (F16) e = widen4(reinterpret_cast<const uint2*>(wte)[id * C4 + q]);
+    else e = reinterpret_cast<const floatx4*>(wte)[id * C4 + q];
+    const floatx4 p = wpe ? reinterpret_cast<const floatx4*>(wpe)[pos * C4 + q] : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float t = e[k] * scale;
+      if (wpe) t += p[k];
+      v[i][k] = t;
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int q = pl.gl + 64 * RW * i;
+      if (q < C4) reinterpret_cast<floatx4*>(x)[r * C4 + q] = v[i];
+    }
+    if (!ok && bad && pl.gl == 0) atomicOr(bad, 1);
+  }
+  if constexpr (KIND == NORM_LN_FWD)
+    ln_fwd_row<NV, RW>(v, C, pl, valid, red, nm.w, nm.b, nm.eps, nm.y + r * C, nm.mean ? nm.mean + r : nullptr,
+                       nm.rstd ? nm.rstd + r : nullptr);
+  else
+    rms_fwd_row<NV, RW>(v, C, pl, valid, red, nm.w, nm.eps, nm.unit_offset, nm.y + r * C,
+                        nm.rstd ? nm.rstd + r : nullptr);
+}
+
+template <int KIND, bool F16>
+void embed_norm_launch(hipStream_t s, const RowShape& sh, const int32_t* ids, int64_t M, int S, const void* wte,
+                       int64_t V, const float* wpe, int C, float scale, float* x, int* bad, const RowNorm& nm,
+                       unsigned long long* zero, int nzero) {
+  const dim3 grid = row_grid(M, sh), block(256);
+#define MFT_EMBED_NORM(NV, RW)                                                                                       \
+  hipLaunchKernelGGL((embed_norm_vec<NV, RW, KIND, F16>), grid, block, 0, s, ids, M, S, wte, V, wpe, C, scale, x, bad, \
+                     nm, zero, nzero)
+  if (sh.rw == 1) MFT_EMBED_NORM(1, 1);
+  else if (sh.rw == 2) MFT_EMBED_NORM(1, 2);
+  else if (sh.nv == 1) MFT_EMBED_NORM(1, 4);
+  else if (sh.nv == 2) MFT_EMBED_NORM(2, 4);
+  else if (sh.nv == 3) MFT_EMBED_NORM(3, 4);
+  else MFT_EMBED_NORM(4, 4);
+#undef MFT_EMBED_NORM
+  MFT_LAUNCH_CHECK();
+}
+
 template <int KIND>
 void splitk_norm_launch(hipStream_t s, const RowShape& sh, const float* partial, int splits, int M, int N, float* C,
                         const GemmEpilogue& ep, const RowNorm& nm) {
@@ -679,6 +753,23 @@ void qk_rope_bwd(hipStream_t s, const HeadRows& q, const HeadRows& k, int64_t M,
   if (q.w) MFT_QK_DISPATCH(qk_rope_bwd_kernel, true, grid, block, 0, s, q, k, M, S, tab);
   else MFT_QK_DISPATCH(qk_rope_bwd_kernel, false, grid, block, 0, s, q, k, M, S, tab);
   MFT_LAUNCH_CHECK();
+}
+
+bool embed_norm(hipStream_t s, const int32_t* ids, int64_t M, int S, const void* wte, int64_t V, bool w_f16,
+                const float* wpe, int64_t C, float scale, float* x, int* bad, const RowNorm& nm, void* zero,
+                int nzero) {
+  if (M <= 0 || S <= 0 || V <= 0 || (nm.kind != NORM_LN_FWD && nm.kind != NORM_RMS_FWD)) return false;
+  if (!vec_ok(C, {wpe, x, nm.w, nm.b, nm.y, w_f16 ? nullptr : wte}) || ((uintptr_t)wte & 7)) return false;
+  const RowShape sh = row_shape(C);
+  unsigned long long* z = static_cast<unsigned long long*>(zero);
+  if (nm.kind == NORM_LN_FWD) {
+    if (w_f16) embed_norm_launch<NORM_LN_FWD, true>(s, sh, ids, M, S, wte, V, wpe, (int)C, scale, x, bad, nm, z, nzero);
+    else embed_norm_launch<NORM_LN_FWD, false>(s, sh, ids, M, S, wte, V, wpe, (int)C, scale, x, bad, nm, z, nzero);
+  } else {
+    if (w_f16) embed_norm_launch<NORM_RMS_FWD, true>(s, sh, ids, M, S, wte, V, wpe, (int)C, scale, x, bad, nm, z, nzero);
+    else embed_norm_launch<NORM_RMS_FWD, false>(s, sh, ids, M, S, wte, V, wpe, (int)C, scale, x, bad, nm, z, nzero);
+  }
+  return true;
 }
 
 bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, float* C, int64_t ldc,
