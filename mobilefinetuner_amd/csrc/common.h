@@ -91,9 +91,12 @@ __device__ __forceinline__ float __attribute__((ext_vector_type(4))) unstash_f16
 //   NORM_LN_BWD / NORM_RMS_BWD: C is the gradient of the norm's output for
 //     input rows x (with the stored mean / rstd); y = resid + ∂x (resid may
 //     be null or alias y).  skip_c: C itself is not needed afterwards.
+//   NORM_RMS_RES_RMS (Gemma3's sandwich: post-norm, residual add, the next
+//     pre-norm): y = resid + C row · rstd · (w + unit_offset), rstd stored;
+//     y2 = y · rstd2 · (w2 + unit_offset), rstd2 stored.
 // With split-K the reduction, the epilogue and the norm run as one pass
 // (the row is finished in registers); otherwise the norm runs after the GEMM.
-enum { NORM_NONE = 0, NORM_LN_FWD, NORM_RMS_FWD, NORM_LN_BWD, NORM_RMS_BWD };
+enum { NORM_NONE = 0, NORM_LN_FWD, NORM_RMS_FWD, NORM_LN_BWD, NORM_RMS_BWD, NORM_RMS_RES_RMS };
 struct RowNorm {
   int kind = NORM_NONE;
   const float* w = nullptr;
@@ -106,6 +109,9 @@ struct RowNorm {
   const float* x = nullptr;
   const float* resid = nullptr;
   bool skip_c = false;
+  const float* w2 = nullptr;  // NORM_RMS_RES_RMS: the second norm
+  float* y2 = nullptr;
+  float* rstd2 = nullptr;
 };
 
 struct GemmEpilogue {

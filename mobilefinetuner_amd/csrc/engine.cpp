@@ -1220,6 +1220,22 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     nm.rstd = fin ? m->frstd : m->A[li].rstd1;
     return nm;
   };
+  // Gemma3's sandwich after a sublayer: y = resid + RMSNorm_w(C) (rstd kept),
+  // then the norm `next` of y (pre-FFN norm, next input norm or final norm).
+  auto sandwich = [&](int w, const float* resid, float* y, float* rstd, const RowNorm& next) {
+    RowNorm nm;
+    nm.kind = NORM_RMS_RES_RMS;
+    nm.w = pd<float>(m, w);
+    nm.eps = c.norm_eps;
+    nm.unit_offset = 1;
+    nm.resid = resid;
+    nm.y = y;
+    nm.rstd = rstd;
+    nm.w2 = next.w;
+    nm.y2 = next.y;
+    nm.rstd2 = next.rstd;
+    return nm;
+  };
   auto norm2 = [&](int li) {  // the pre-MLP norm of layer li
     RowNorm nm;
     Acts& a = m->A[li];
@@ -1253,7 +1269,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     const Layer& L = m->L[li];
     Acts& a = m->A[li];
     float* hout = li + 1 < c.n_layer ? m->A[li + 1].x : m->h_final;
-    if ((li == 0 && !first_norm) || (li > 0 && gemma)) row_norm(s, a.x, M, d, norm1(li));
+    if (li == 0 && !first_norm) row_norm(s, a.x, M, d, norm1(li));
     const RowNorm n2 = norm2(li), nx = norm1(li + 1);
     if (gpt2) {
       lin_fwd(m, L.lin[G_ATTN], a.n1, M, a.q, a.xa[G_ATTN], nullptr);
@@ -1293,26 +1309,22 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       qk_rope_fwd(s, hq, hk, M, S, hd, c.norm_eps, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
     }
     attention_fwd(m, a, li, mask, nseq, S);
-    if (gemma) {
-      lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr);
-      rmsnorm_fwd(s, a.o, pd<float>(m, L.pan), M, d, c.norm_eps, true, m->dtmp, a.ors);
-      add_out(s, a.hmid, a.x, m->dtmp, M * d);
-      rmsnorm_fwd(s, a.hmid, pd<float>(m, L.n2w), M, d, c.norm_eps, gemma, a.n2, a.rstd2);
+    if (gemma) {  // post-attention norm, residual add and pre-FFN norm in the o projection's epilogue
+      const RowNorm sw = sandwich(L.pan, a.x, a.hmid, a.ors, norm2(li));
+      lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr, nullptr, &sw);
     } else {
       lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x, nullptr, &n2);  // residual + norm fused
     }
     lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
     lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
     glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
-    if (gemma) {
-      lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr);
-      rmsnorm_fwd(s, a.mo, pd<float>(m, L.pfn), M, d, c.norm_eps, true, m->dtmp, a.mrs);
-      add_out(s, hout, a.hmid, m->dtmp, M * d);
+    if (gemma) {  // post-FFN norm, residual add and the next input norm in the down projection's epilogue
+      const RowNorm sw = sandwich(L.pfn, a.hmid, hout, a.mrs, norm1(li + 1));
+      lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr, nullptr, &sw);
     } else {
       lin_fwd(m, L.lin[T_DOWN], a.act, M, hout, a.xa[T_DOWN], a.hmid, nullptr, &nx);  // residual + norm fused
     }
   }
-  if (gemma) row_norm(s, m->h_final, M, d, norm1(c.n_layer));
   // LM head: logits = hf · Eᵀ, E [V, d] is the [N, K] operand.
   const WeightUse wh(m, m->wte);
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);

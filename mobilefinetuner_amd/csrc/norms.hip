@@ -222,6 +222,55 @@ __device__ __forceinline__ void rms_bwd_row(floatx4 (&gv)[NV], floatx4 (&xv)[NV]
   }
 }
 
+// Gemma3's sandwich: y = resid + v·rstd·(off + w), then y2 = y·rstd2·(off +
+// w2), with the arithmetic of rms_fwd_row followed by an elementwise add and
+// a second rms_fwd_row.
+// xres: the row of nm.resid (loaded by the caller with the row itself).
+template <int NV, int RW>
+__device__ __forceinline__ void rms_res_rms_row(const floatx4 (&v)[NV], const floatx4 (&xres)[NV], int C,
+                                                const Place<RW>& pl, bool valid, float (*red)[4], const RowNorm& nm,
+                                                int64_t r) {
+  const int C4 = C / 4;
+  const float off = nm.unit_offset ? 1.f : 0.f;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s = fmaf(v[i][e], v[i][e], s);
+  const float rs = rsqrtf(row_sum<RW>(s, red, pl.wave) / (float)C + nm.eps);
+  floatx4 h[NV];
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int qi = pl.gl + 64 * RW * i;
+    h[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (qi >= C4) continue;
+    const floatx4 wv = reinterpret_cast<const floatx4*>(nm.w)[qi];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[i][e] = xres[i][e] + v[i][e] * rs * (off + wv[e]);
+      s2 = fmaf(h[i][e], h[i][e], s2);
+    }
+  }
+  const float rs2 = rsqrtf(row_sum<RW>(s2, red + 2, pl.wave) / (float)C + nm.eps);
+  if (!valid) return;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int qi = pl.gl + 64 * RW * i;
+    if (qi >= C4) continue;
+    const floatx4 wv = reinterpret_cast<const floatx4*>(nm.w2)[qi];
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = h[i][e] * rs2 * (off + wv[e]);
+    reinterpret_cast<floatx4*>(nm.y + r * C)[qi] = h[i];
+    reinterpret_cast<floatx4*>(nm.y2 + r * C)[qi] = o;
+  }
+  if (pl.gl == 0) {
+    if (nm.rstd) nm.rstd[r] = rs;
+    if (nm.rstd2) nm.rstd2[r] = rs2;
+  }
+}
+
 // ---- standalone launches: 4 / RW rows per 256-thread workgroup -------------
 template <int NV, int RW>
 __global__ __launch_bounds__(256) void ln_fwd_vec(const float* __restrict__ x, const float* __restrict__ g,
@@ -294,6 +343,19 @@ __global__ __launch_bounds__(256) void rms_bwd_vec(const float* __restrict__ dy,
   load_row<NV, RW>(x + seg_off(r, seg, x_ld, C), C / 4, pl.gl, xv);
   const int64_t o = seg_off(r, seg, dx_ld, C);
   rms_bwd_row<NV, RW>(gv, xv, C, pl, valid, red, w, rstd[r], unit_offset, dx + o, resid ? resid + o : nullptr);
+}
+
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void rms_res_rms_vec(const float* __restrict__ x, int64_t M, int C, RowNorm nm) {
+  __shared__ float red[4][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
+  floatx4 v[NV], xres[NV];
+  load_row<NV, RW>(nm.resid + r * C, C / 4, pl.gl, xres);
+  load_row<NV, RW>(x + r * C, C / 4, pl.gl, v);
+  rms_res_rms_row<NV, RW>(v, xres, C, pl, valid, red, nm, r);
 }
 
 // ---- q/k head rows: per-head RMSNorm + RoPE in one pass -------------------
@@ -445,6 +507,7 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
   constexpr bool BWD = KIND == NORM_LN_BWD || KIND == NORM_RMS_BWD;
   floatx4 xv[NV], rv[NV];
   if constexpr (BWD) load_row<NV, RW>(nm.x + r * C, C4, pl.gl, xv);
+  if constexpr (KIND == NORM_RMS_RES_RMS) load_row<NV, RW>(nm.resid + r * C, C4, pl.gl, xv);
   if (ep.resid) load_row<NV, RW>(ep.resid + r * C, C4, pl.gl, rv);
   floatx4 v[NV];
   load_row<NV, RW>(partial + r * C, C4, pl.gl, v);
@@ -495,6 +558,8 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
   } else if constexpr (KIND == NORM_LN_BWD) {
     ln_bwd_row<NV, RW>(v, xv, C, pl, valid, red, nm.w, nm.mean[r], nm.rstd[r], nm.y + r * C,
                        nm.resid ? nm.resid + r * C : nullptr);
+  } else if constexpr (KIND == NORM_RMS_RES_RMS) {
+    rms_res_rms_row<NV, RW>(v, xv, C, pl, valid, red, nm, r);
   } else {
     rms_bwd_row<NV, RW>(v, xv, C, pl, valid, red, nm.w, nm.rstd[r], nm.unit_offset, nm.y + r * C,
                         nm.resid ? nm.resid + r * C : nullptr);
@@ -686,6 +751,20 @@ void rmsnorm_bwd_seg(hipStream_t s, const float* dy, int64_t dy_ld, const float*
 }
 
 void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm& nm) {
+  if (nm.kind == NORM_RMS_RES_RMS) {
+    MFT_CHECK_ARG(M > 0 && C > 0 && nm.resid && nm.y && nm.y2 && nm.w && nm.w2, "sandwich norm: missing operand");
+    if (vec_ok(C, {c, nm.w, nm.w2, nm.resid, nm.y, nm.y2})) {
+      const RowShape sh = row_shape(C);
+      MFT_ROW_DISPATCH(sh, rms_res_rms_vec, row_grid(M, sh), dim3(256), 0, s, c, M, (int)C, nm);
+      MFT_LAUNCH_CHECK();
+      return;
+    }
+    // row-loop fallback: the same three steps as separate launches
+    rmsnorm_fwd(s, c, nm.w, M, C, nm.eps, nm.unit_offset != 0, nm.y, nm.rstd);
+    add_inplace(s, nm.y, nm.resid, M * C);
+    rmsnorm_fwd(s, nm.y, nm.w2, M, C, nm.eps, nm.unit_offset != 0, nm.y2, nm.rstd2);
+    return;
+  }
   switch (nm.kind) {
     case NORM_LN_FWD: return layernorm_fwd(s, c, nm.w, nm.b, M, C, nm.eps, nm.y, nm.mean, nm.rstd);
     case NORM_RMS_FWD: return rmsnorm_fwd(s, c, nm.w, M, C, nm.eps, nm.unit_offset != 0, nm.y, nm.rstd);
@@ -775,7 +854,8 @@ bool embed_norm(hipStream_t s, const int32_t* ids, int64_t M, int S, const void*
 bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, float* C, int64_t ldc,
                  const GemmEpilogue& ep, const RowNorm& nm) {
   if (ldc != N || splits < 1 || M <= 0) return false;
-  if (!vec_ok(N, {partial, C, ep.bias, ep.resid, ep.gelu_out, ep.gelu_grad_of, nm.w, nm.b, nm.y, nm.x, nm.resid}))
+  if (!vec_ok(N, {partial, C, ep.bias, ep.resid, ep.gelu_out, ep.gelu_grad_of, nm.w, nm.b, nm.y, nm.x, nm.resid,
+                  nm.w2, nm.y2}))
     return false;
   const RowShape sh = row_shape(N);
   switch (nm.kind) {
@@ -783,6 +863,9 @@ bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, 
     case NORM_RMS_FWD: splitk_norm_launch<NORM_RMS_FWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
     case NORM_LN_BWD: splitk_norm_launch<NORM_LN_BWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
     case NORM_RMS_BWD: splitk_norm_launch<NORM_RMS_BWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
+    case NORM_RMS_RES_RMS:
+      splitk_norm_launch<NORM_RMS_RES_RMS>(s, sh, partial, splits, M, N, C, ep, nm);
+      return true;
     default: return false;
   }
 }
