@@ -94,9 +94,12 @@ __device__ __forceinline__ float __attribute__((ext_vector_type(4))) unstash_f16
 //   NORM_RMS_RES_RMS (Gemma3's sandwich: post-norm, residual add, the next
 //     pre-norm): y = resid + C row · rstd · (w + unit_offset), rstd stored;
 //     y2 = y · rstd2 · (w2 + unit_offset), rstd2 stored.
+//   NORM_RMS_BWD_POST (its backward): y as NORM_RMS_BWD, then y2 = the
+//     gradient of the post-norm's input for its input rows x2 (w2, stored
+//     rstd2) given output gradient y.
 // With split-K the reduction, the epilogue and the norm run as one pass
 // (the row is finished in registers); otherwise the norm runs after the GEMM.
-enum { NORM_NONE = 0, NORM_LN_FWD, NORM_RMS_FWD, NORM_LN_BWD, NORM_RMS_BWD, NORM_RMS_RES_RMS };
+enum { NORM_NONE = 0, NORM_LN_FWD, NORM_RMS_FWD, NORM_LN_BWD, NORM_RMS_BWD, NORM_RMS_RES_RMS, NORM_RMS_BWD_POST };
 struct RowNorm {
   int kind = NORM_NONE;
   const float* w = nullptr;
@@ -109,9 +112,10 @@ struct RowNorm {
   const float* x = nullptr;
   const float* resid = nullptr;
   bool skip_c = false;
-  const float* w2 = nullptr;  // NORM_RMS_RES_RMS: the second norm
+  const float* w2 = nullptr;  // NORM_RMS_RES_RMS / NORM_RMS_BWD_POST: the second norm
   float* y2 = nullptr;
   float* rstd2 = nullptr;
+  const float* x2 = nullptr;  // NORM_RMS_BWD_POST: the second norm's input rows
 };
 
 struct GemmEpilogue {

@@ -1391,11 +1391,24 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     nm.skip_c = true;
     return nm;
   };
+  // Gemma3: extend a norm backward with that of the post-norm whose output
+  // fed it through the residual stream: layer li's post-attention norm
+  // (attn) or post-FFN norm; its input gradient is the o or down projection's dY.
+  auto post_bwd = [&](RowNorm nm, int li, bool attn) {
+    const Acts& pa = m->A[li];
+    nm.kind = NORM_RMS_BWD_POST;
+    nm.x2 = attn ? pa.o : pa.mo;
+    nm.w2 = pd<float>(m, attn ? m->L[li].pan : m->L[li].pfn);
+    nm.rstd2 = attn ? pa.ors : pa.mrs;
+    nm.y2 = dyb(li, attn ? T_O : T_DOWN, m->dtmp);
+    return nm;
+  };
   {
     // dhf = dlogits · E, E [V, d] is the [K, N] operand; the final norm's
     // backward runs in its epilogue.
     Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
-    const RowNorm nf = norm_bwd(m->h_final, m->nfw, gpt2 ? m->fmean : nullptr, m->frstd, res_in(top), nullptr);
+    RowNorm nf = norm_bwd(m->h_final, m->nfw, gpt2 ? m->fmean : nullptr, m->frstd, res_in(top), nullptr);
+    if (gemma) nf = post_bwd(nf, top, false);  // + the top layer's post-FFN norm backward
     GemmEpilogue head;
     head.site = 1;
     head.norm = &nf;
@@ -1410,21 +1423,22 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     float* rin = res_in(li);
     float* rmid = res_mid(li);
     const bool need_dx = li > 0;
-    const RowNorm nb2 = norm_bwd(a.hmid, L.n2w, gpt2 ? a.mean2 : nullptr, a.rstd2, rmid, rin);
+    RowNorm nb2 = norm_bwd(a.hmid, L.n2w, gpt2 ? a.mean2 : nullptr, a.rstd2, rmid, rin);
     float* rnext = need_dx ? res_in(li - 1) : nullptr;
-    const RowNorm nb1 = norm_bwd(a.x, L.n1w, gpt2 ? a.mean1 : nullptr, a.rstd1, rnext, rmid);
+    RowNorm nb1 = norm_bwd(a.x, L.n1w, gpt2 ? a.mean1 : nullptr, a.rstd1, rnext, rmid);
+    if (gemma) {
+      nb2 = post_bwd(nb2, li, true);                  // + this layer's post-attention norm backward
+      if (need_dx) nb1 = post_bwd(nb1, li - 1, false);  // + the next lower layer's post-FFN norm backward
+    }
     // ---- MLP block ----
     if (gpt2) {
       float* dgate = dyb(li, G_FC, m->dgate);
       lin_bwd(m, L.lin[G_FC2], rin, a.act, a.xa[G_FC2], M, dgate, a.gate);  // GELU' fused
       lin_bwd(m, L.lin[G_FC], dgate, a.n2, a.xa[G_FC], M, m->dn, nullptr, &nb2);  // LN backward fused
     } else {
-      const float* dmo = rin;
-      if (gemma) {
-        float* t = dyb(li, T_DOWN, m->dtmp);
-        rmsnorm_bwd(s, rin, a.mo, pd<float>(m, L.pfn), a.mrs, M, d, true, t, nullptr);
-        dmo = t;
-      }
+      // Gemma3: the post-FFN norm's backward ran with the norm backward that
+      // produced rin (the layer above's, or the LM head's final norm)
+      const float* dmo = gemma ? dyb(li, T_DOWN, m->dtmp) : rin;
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
       float* dgate = dyb(li, T_GATE, m->dgate);
       float* dup = dyb(li, T_UP, m->dup);
@@ -1433,12 +1447,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dn, nullptr, &nb2, 1.f);  // dn += ...; norm fused
     }
     // ---- attention block ----
-    const float* dox = rmid;
-    if (gemma) {
-      float* t = dyb(li, T_O, m->dtmp);
-      rmsnorm_bwd(s, rmid, a.o, pd<float>(m, L.pan), a.ors, M, d, true, t, nullptr);
-      dox = t;
-    }
+    // Gemma3: the post-attention norm's backward ran with the pre-FFN norm's
+    const float* dox = gemma ? dyb(li, T_O, m->dtmp) : rmid;
     lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};

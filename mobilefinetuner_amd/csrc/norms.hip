@@ -271,6 +271,63 @@ __device__ __forceinline__ void rms_res_rms_row(const floatx4 (&v)[NV], const fl
   }
 }
 
+// Backward of an RMSNorm whose input came out of a post-norm: stage 1 is
+// rms_bwd_row with the residual (y = resid + ∂x over rows x with w, rstd[r]);
+// stage 2 is rms_bwd_row of y over the post-norm's input rows x2 (w2,
+// rstd2[r], no residual) into y2.  gv: the incoming gradient; xv, x2v, rv:
+// the rows of x, x2 and resid (all overwritten).
+template <int NV, int RW>
+__device__ __forceinline__ void rms_bwd_post_row(floatx4 (&gv)[NV], floatx4 (&xv)[NV], floatx4 (&x2v)[NV],
+                                                 const floatx4 (&rv)[NV], int C, const Place<RW>& pl, bool valid,
+                                                 float (*red)[4], const RowNorm& nm, int64_t r) {
+  const int C4 = C / 4;
+  const float off = nm.unit_offset ? 1.f : 0.f;
+  const float rs = nm.rstd[r];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int qi = pl.gl + 64 * RW * i;
+    if (qi >= C4) continue;
+    const floatx4 wv = reinterpret_cast<const floatx4*>(nm.w)[qi];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gv[i][e] *= off + wv[e];
+      xv[i][e] *= rs;
+      s = fmaf(gv[i][e], xv[i][e], s);
+    }
+  }
+  s = row_sum<RW>(s, red, pl.wave) / (float)C;
+  const float rs2 = nm.rstd2[r];
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int qi = pl.gl + 64 * RW * i;
+    if (qi >= C4) continue;
+    const floatx4 w2 = reinterpret_cast<const floatx4*>(nm.w2)[qi];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float y = rs * (gv[i][e] - xv[i][e] * s);
+      if (nm.resid) y += rv[i][e];
+      gv[i][e] = y;  // stage 1's output, kept for the store
+      xv[i][e] = y * (off + w2[e]);
+      x2v[i][e] *= rs2;
+      s2 = fmaf(xv[i][e], x2v[i][e], s2);
+    }
+  }
+  s2 = row_sum<RW>(s2, red + 2, pl.wave) / (float)C;
+  if (!valid) return;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int qi = pl.gl + 64 * RW * i;
+    if (qi >= C4) continue;
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = rs2 * (xv[i][e] - x2v[i][e] * s2);
+    reinterpret_cast<floatx4*>(nm.y + r * C)[qi] = gv[i];
+    reinterpret_cast<floatx4*>(nm.y2 + r * C)[qi] = o;
+  }
+}
+
 // ---- standalone launches: 4 / RW rows per 256-thread workgroup -------------
 template <int NV, int RW>
 __global__ __launch_bounds__(256) void ln_fwd_vec(const float* __restrict__ x, const float* __restrict__ g,
@@ -508,6 +565,12 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
   floatx4 xv[NV], rv[NV];
   if constexpr (BWD) load_row<NV, RW>(nm.x + r * C, C4, pl.gl, xv);
   if constexpr (KIND == NORM_RMS_RES_RMS) load_row<NV, RW>(nm.resid + r * C, C4, pl.gl, xv);
+  floatx4 x2v[KIND == NORM_RMS_BWD_POST ? NV : 1], nrv[KIND == NORM_RMS_BWD_POST ? NV : 1];
+  if constexpr (KIND == NORM_RMS_BWD_POST) {
+    load_row<NV, RW>(nm.x + r * C, C4, pl.gl, xv);
+    load_row<NV, RW>(nm.x2 + r * C, C4, pl.gl, x2v);
+    if (nm.resid) load_row<NV, RW>(nm.resid + r * C, C4, pl.gl, nrv);
+  }
   if (ep.resid) load_row<NV, RW>(ep.resid + r * C, C4, pl.gl, rv);
   floatx4 v[NV];
   load_row<NV, RW>(partial + r * C, C4, pl.gl, v);
@@ -560,6 +623,8 @@ __global__ __launch_bounds__(256) void splitk_norm_vec(const float* __restrict__
                        nm.resid ? nm.resid + r * C : nullptr);
   } else if constexpr (KIND == NORM_RMS_RES_RMS) {
     rms_res_rms_row<NV, RW>(v, xv, C, pl, valid, red, nm, r);
+  } else if constexpr (KIND == NORM_RMS_BWD_POST) {
+    rms_bwd_post_row<NV, RW>(v, xv, x2v, nrv, C, pl, valid, red, nm, r);
   } else {
     rms_bwd_row<NV, RW>(v, xv, C, pl, valid, red, nm.w, nm.rstd[r], nm.unit_offset, nm.y + r * C,
                         nm.resid ? nm.resid + r * C : nullptr);
@@ -765,6 +830,11 @@ void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm
     rmsnorm_fwd(s, nm.y, nm.w2, M, C, nm.eps, nm.unit_offset != 0, nm.y2, nm.rstd2);
     return;
   }
+  if (nm.kind == NORM_RMS_BWD_POST) {  // the two backward passes as two launches
+    rmsnorm_bwd(s, c, nm.x, nm.w, nm.rstd, M, C, nm.unit_offset != 0, nm.y, nm.resid);
+    rmsnorm_bwd(s, nm.y, nm.x2, nm.w2, nm.rstd2, M, C, nm.unit_offset != 0, nm.y2, nullptr);
+    return;
+  }
   switch (nm.kind) {
     case NORM_LN_FWD: return layernorm_fwd(s, c, nm.w, nm.b, M, C, nm.eps, nm.y, nm.mean, nm.rstd);
     case NORM_RMS_FWD: return rmsnorm_fwd(s, c, nm.w, M, C, nm.eps, nm.unit_offset != 0, nm.y, nm.rstd);
@@ -855,7 +925,7 @@ bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, 
                  const GemmEpilogue& ep, const RowNorm& nm) {
   if (ldc != N || splits < 1 || M <= 0) return false;
   if (!vec_ok(N, {partial, C, ep.bias, ep.resid, ep.gelu_out, ep.gelu_grad_of, nm.w, nm.b, nm.y, nm.x, nm.resid,
-                  nm.w2, nm.y2}))
+                  nm.w2, nm.y2, nm.x2}))
     return false;
   const RowShape sh = row_shape(N);
   switch (nm.kind) {
@@ -865,6 +935,9 @@ bool splitk_norm(hipStream_t s, const float* partial, int splits, int M, int N, 
     case NORM_RMS_BWD: splitk_norm_launch<NORM_RMS_BWD>(s, sh, partial, splits, M, N, C, ep, nm); return true;
     case NORM_RMS_RES_RMS:
       splitk_norm_launch<NORM_RMS_RES_RMS>(s, sh, partial, splits, M, N, C, ep, nm);
+      return true;
+    case NORM_RMS_BWD_POST:
+      splitk_norm_launch<NORM_RMS_BWD_POST>(s, sh, partial, splits, M, N, C, ep, nm);
       return true;
     default: return false;
   }
