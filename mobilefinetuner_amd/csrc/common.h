@@ -414,6 +414,13 @@ void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
              int act, float* out);
 void glu_bwd(hipStream_t s, const float* dout, const float* gate,
              const float* up, int64_t n, int act, float* dgate, float* dup);
+// The same over [rows, cols] views whose gate/up (and dgate/dup) rows are
+// ld_gu apart (a fused gate|up projection: ld_gu = 2·cols); out and dout
+// are [rows, cols] arrays.
+void glu_fwd_rows(hipStream_t s, const float* gate, const float* up, int64_t rows, int64_t cols, int64_t ld_gu,
+                  int act, float* out);
+void glu_bwd_rows(hipStream_t s, const float* dout, const float* gate, const float* up, int64_t rows,
+                  int64_t cols, int64_t ld_gu, int act, float* dgate, float* dup);
 void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,
           double theta, bool inverse);
 // Ids outside [0, V) give zero rows and set *bad (device int, nullable).

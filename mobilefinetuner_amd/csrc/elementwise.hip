@@ -124,29 +124,39 @@ __device__ __forceinline__ float silu_grad(float x) {
   return s * (1.f + x * (1.f - s));
 }
 
+// Element i of a [rows, cols] view: gate/up (and dgate/dup) rows ld_gu
+// apart, out/dout rows cols apart (ld_gu == cols: one flat array).
+__device__ __forceinline__ int64_t gu_index(int64_t i, int64_t cols, int64_t ld_gu) {
+  if (ld_gu == cols) return i;
+  const int64_t r = i / cols;
+  return r * ld_gu + (i - r * cols);
+}
+
 __global__ void glu_fwd_kernel(const float* __restrict__ gate,
-                               const float* __restrict__ up, int64_t n, int act,
+                               const float* __restrict__ up, int64_t n, int64_t cols, int64_t ld_gu, int act,
                                float* __restrict__ out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const float a = act == 0 ? gelu_tanh(gate[i]) : silu(gate[i]);
-    out[i] = up ? a * up[i] : a;
+    const int64_t j = gu_index(i, cols, ld_gu);
+    const float a = act == 0 ? gelu_tanh(gate[j]) : silu(gate[j]);
+    out[i] = up ? a * up[j] : a;
   }
 }
 
 __global__ void glu_bwd_kernel(const float* __restrict__ dout,
                                const float* __restrict__ gate,
-                               const float* __restrict__ up, int64_t n, int act,
+                               const float* __restrict__ up, int64_t n, int64_t cols, int64_t ld_gu, int act,
                                float* __restrict__ dgate, float* __restrict__ dup) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const float gv = gate[i];
+    const int64_t j = gu_index(i, cols, ld_gu);
+    const float gv = gate[j];
     const float a = act == 0 ? gelu_tanh(gv) : silu(gv);
     const float da = act == 0 ? gelu_tanh_grad(gv) : silu_grad(gv);
-    const float u = up ? up[i] : 1.f;
+    const float u = up ? up[j] : 1.f;
     const float d = dout[i];
-    dgate[i] = d * u * da;
-    if (up && dup) dup[i] = d * a;
+    dgate[j] = d * u * da;
+    if (up && dup) dup[j] = d * a;
   }
 }
 
@@ -572,14 +582,27 @@ void rmsnorm_bwd_rowloop(hipStream_t s, const float* dy, const float* x,
 }
 void glu_fwd(hipStream_t s, const float* gate, const float* up, int64_t n,
              int act, float* out) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(glu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, act, out);
-  MFT_LAUNCH_CHECK();
+  glu_fwd_rows(s, gate, up, 1, n, n, act, out);
 }
 void glu_bwd(hipStream_t s, const float* dout, const float* gate,
              const float* up, int64_t n, int act, float* dgate, float* dup) {
+  glu_bwd_rows(s, dout, gate, up, 1, n, n, act, dgate, dup);
+}
+void glu_fwd_rows(hipStream_t s, const float* gate, const float* up, int64_t rows, int64_t cols, int64_t ld_gu,
+                  int act, float* out) {
+  const int64_t n = rows * cols;
   if (n <= 0) return;
-  hipLaunchKernelGGL(glu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, dout, gate, up, n, act, dgate, dup);
+  MFT_CHECK_ARG(ld_gu >= cols, "glu: gate/up row pitch below the row length");
+  hipLaunchKernelGGL(glu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, cols, ld_gu, act, out);
+  MFT_LAUNCH_CHECK();
+}
+void glu_bwd_rows(hipStream_t s, const float* dout, const float* gate, const float* up, int64_t rows,
+                  int64_t cols, int64_t ld_gu, int act, float* dgate, float* dup) {
+  const int64_t n = rows * cols;
+  if (n <= 0) return;
+  MFT_CHECK_ARG(ld_gu >= cols, "glu: gate/up row pitch below the row length");
+  hipLaunchKernelGGL(glu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, dout, gate, up, n, cols, ld_gu, act, dgate,
+                     dup);
   MFT_LAUNCH_CHECK();
 }
 void rope(hipStream_t s, float* x, int64_t rs, int B, int S, int H, int hd,

@@ -75,6 +75,7 @@ struct Acts {
   float* DY[T_MAX];  // dY of each LoRA linear, kept until the end of the backward
   int64_t dy_ld[T_MAX];  // row pitch of DY[t] (N, or the fused q|k|v width)
   float *qkv, *dyqkv;    // fused q|k|v projection output and its gradient (fuse_qkv)
+  float *gu, *dygu;      // fused gate|up projection output [M, 2·ff] and its gradient (fuse_gu)
   float *att, *lse, *o, *ors, *hmid, *n2, *mean2, *rstd2;
   float *gate, *up, *act, *mo, *mrs;
 };
@@ -223,6 +224,9 @@ struct mft_model_s {
   // q|k|v forward and one for its dX, over a W_eff block [d, nqkv]
   bool fuse_qkv = false;
   int nqkv = 0;
+  // gate|up as one projection (column blocks of one [d, 2·ff] W_eff) and
+  // one dX GEMM, when both are merged LoRA linears without bias
+  bool fuse_gu = false;
   // operator-level split points: shape of the forward whose activations are
   // kept (0 = none) and whether its logits buffer now holds dlogits
   int api_nseq = 0, api_S = 0;
@@ -606,9 +610,21 @@ bool qkv_fusable(const mft_model_s* m) {
   return true;
 }
 
+// gate and up fuse into one projection when both are merged LoRA linears
+// without bias (their W_eff become column blocks of one array).
+bool gu_fusable(const mft_model_s* m) {
+  if (m->c.arch == MFT_ARCH_GPT2 || !lora_merge(m)) return false;
+  for (const auto& L : m->L) {
+    const Linear &g = L.lin[T_GATE], &u = L.lin[T_UP];
+    if (g.A < 0 || u.A < 0 || g.b >= 0 || u.b >= 0 || g.K != u.K || g.N != u.N) return false;
+  }
+  return true;
+}
+
 void alloc_acts(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
   m->fuse_qkv = qkv_fusable(m);
+  m->fuse_gu = gu_fusable(m);
   m->nqkv = c.n_head * c.head_dim + 2 * c.n_kv_head * c.head_dim;
   const int64_t M = m->max_tokens;
   const int64_t d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim, ff = c.d_ff, r = c.lora_r;
@@ -672,6 +688,10 @@ void alloc_acts(mft_model_s* m) {
           if (m->fuse_qkv && t < 3) {  // views of the fused gradient
             a.DY[t] = a.dyqkv + (t == 0 ? 0 : H * hd + (t - 1) * Hk * hd);
             a.dy_ld[t] = m->nqkv;
+          } else if (m->fuse_gu && (t == T_GATE || t == T_UP)) {
+            if (t == T_GATE) a.dygu = b.f(M * 2 * ff);
+            a.DY[t] = a.dygu + (t == T_GATE ? 0 : ff);
+            a.dy_ld[t] = 2 * ff;
           } else if (keep_dy) {
             a.DY[t] = b.f(M * L.lin[t].N);
             a.dy_ld[t] = L.lin[t].N;
@@ -685,8 +705,14 @@ void alloc_acts(mft_model_s* m) {
       a.n2 = b.f(M * d);
       a.rstd2 = b.f(M);
       if (gpt2) a.mean2 = b.f(M);
-      a.gate = b.f(M * ff);
-      if (!gpt2) a.up = b.f(M * ff);
+      if (m->fuse_gu) {
+        a.gu = b.f(M * 2 * ff);
+        a.gate = a.gu;
+        a.up = a.gu + ff;
+      } else {
+        a.gate = b.f(M * ff);
+        if (!gpt2) a.up = b.f(M * ff);
+      }
       a.act = b.f(M * ff);
       a.mo = b.f(M * d);
       if (gemma) a.mrs = b.f(M);
@@ -797,6 +823,10 @@ void build_lora_tables(mft_model_s* m) {
         if (t == 0) weff_floats += ((size_t)l.K * m->nqkv + 63) / 64 * 64;  // one [d, nqkv] block
         continue;
       }
+      if (m->fuse_gu && (t == T_GATE || t == T_UP)) {
+        if (t == T_GATE) weff_floats += ((size_t)l.K * 2 * l.N + 63) / 64 * 64;  // one [d, 2·ff] block
+        continue;
+      }
       weff_floats += ((size_t)l.K * l.N + 63) / 64 * 64;
     }
   if (!panel && hipMalloc(&m->weff_mem, weff_floats * sizeof(float)) != hipSuccess)
@@ -884,6 +914,14 @@ void build_lora_tables(mft_model_s* m) {
           l.weff = L.lin[t - 1].weff + L.lin[t - 1].N;
         }
         l.weff_ld = m->nqkv;
+      } else if (m->fuse_gu && (t == T_GATE || t == T_UP)) {  // column block of the layer's [d, 2·ff] W_eff
+        if (t == T_GATE) {
+          l.weff = static_cast<float*>(m->weff_mem) + woff;
+          woff += ((size_t)l.K * 2 * l.N + 63) / 64 * 64;
+        } else {
+          l.weff = L.lin[T_GATE].weff + L.lin[T_GATE].N;
+        }
+        l.weff_ld = 2 * l.N;
       } else {
         l.weff = static_cast<float*>(m->weff_mem) + woff;
         woff += ((size_t)l.K * l.N + 63) / 64 * 64;
@@ -1315,9 +1353,17 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     } else {
       lin_fwd(m, L.lin[T_O], a.att, M, a.hmid, a.xa[T_O], a.x, nullptr, &n2);  // residual + norm fused
     }
-    lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
-    lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
-    glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
+    if (m->fuse_gu) {  // gate|up = n2·W_eff[d, 2·ff] in one GEMM
+      const int n2f = 2 * c.d_ff;
+      Timed t(m, CLS_LINEAR, 2.0 * M * n2f * d);
+      gemm(s, a.n2, d, L.lin[T_GATE].weff, n2f, false, false, a.gu, n2f, (int)M, n2f, d, GemmEpilogue(), m->ws,
+           t.events());
+      glu_fwd_rows(s, a.gate, a.up, M, c.d_ff, n2f, gemma ? 0 : 1, a.act);
+    } else {
+      lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
+      lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
+      glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
+    }
     if (gemma) {  // post-FFN norm, residual add and the next input norm in the down projection's epilogue
       const RowNorm sw = sandwich(L.pfn, a.hmid, hout, a.mrs, norm1(li + 1));
       lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr, nullptr, &sw);
@@ -1440,11 +1486,22 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       // produced rin (the layer above's, or the LM head's final norm)
       const float* dmo = gemma ? dyb(li, T_DOWN, m->dtmp) : rin;
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
-      float* dgate = dyb(li, T_GATE, m->dgate);
-      float* dup = dyb(li, T_UP, m->dup);
-      glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, dgate, dup);
-      lin_bwd(m, L.lin[T_GATE], dgate, a.n2, a.xa[T_GATE], M, m->dn);
-      lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dn, nullptr, &nb2, 1.f);  // dn += ...; norm fused
+      if (m->fuse_gu) {
+        // dgate|dup in the fused [M, 2·ff] gradient, then one GEMM gives
+        // dn = dgu·W_eff[d, 2·ff]ᵀ with the pre-FFN norm's backward fused
+        const int n2f = 2 * c.d_ff;
+        glu_bwd_rows(s, m->dact, a.gate, a.up, M, c.d_ff, n2f, gemma ? 0 : 1, a.DY[T_GATE], a.DY[T_UP]);
+        GemmEpilogue ep;
+        ep.norm = &nb2;
+        Timed t(m, CLS_LINEAR, 2.0 * M * n2f * d);
+        gemm(s, a.dygu, n2f, L.lin[T_GATE].weff, n2f, true, false, m->dn, d, (int)M, d, n2f, ep, m->ws, t.events());
+      } else {
+        float* dgate = dyb(li, T_GATE, m->dgate);
+        float* dup = dyb(li, T_UP, m->dup);
+        glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, dgate, dup);
+        lin_bwd(m, L.lin[T_GATE], dgate, a.n2, a.xa[T_GATE], M, m->dn);
+        lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dn, nullptr, &nb2, 1.f);  // dn += ...; norm fused
+      }
     }
     // ---- attention block ----
     // Gemma3: the post-attention norm's backward ran with the pre-FFN norm's
@@ -1992,8 +2049,8 @@ int mft_model_activation(mft_model m, int layer, const char* name, const float**
       else if (n == "o_proj" && gemma) set(a.o, d, d);
       else if (n == "mid") set(a.hmid, d, d);
       else if (n == "norm2") set(a.n2, d, d);
-      else if (n == "gate") set(a.gate, c.d_ff, c.d_ff);
-      else if (n == "up" && !gpt2) set(a.up, c.d_ff, c.d_ff);
+      else if (n == "gate") set(a.gate, c.d_ff, m->fuse_gu ? 2 * c.d_ff : c.d_ff);
+      else if (n == "up" && !gpt2) set(a.up, c.d_ff, m->fuse_gu ? 2 * c.d_ff : c.d_ff);
       else if (n == "act") set(a.act, c.d_ff, c.d_ff);
       else if (n == "down_proj" && gemma) set(a.mo, d, d);
       else if (n == "out") set(layer + 1 < c.n_layer ? m->A[layer + 1].x : m->h_final, d, d);
