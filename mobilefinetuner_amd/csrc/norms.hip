@@ -415,6 +415,21 @@ __global__ __launch_bounds__(256) void rms_res_rms_vec(const float* __restrict__
   rms_res_rms_row<NV, RW>(v, xres, C, pl, valid, red, nm, r);
 }
 
+template <int NV, int RW>
+__global__ __launch_bounds__(256) void rms_bwd_post_vec(const float* __restrict__ dy, int64_t M, int C, RowNorm nm) {
+  __shared__ float red[4][4];
+  const Place<RW> pl;
+  const int64_t row = (int64_t)blockIdx.x * (4 / RW) + pl.grp;
+  const bool valid = row < M;
+  const int64_t r = valid ? row : M - 1;
+  floatx4 gv[NV], xv[NV], x2v[NV], rv[NV];
+  load_row<NV, RW>(nm.x + r * C, C / 4, pl.gl, xv);
+  load_row<NV, RW>(nm.x2 + r * C, C / 4, pl.gl, x2v);
+  if (nm.resid) load_row<NV, RW>(nm.resid + r * C, C / 4, pl.gl, rv);
+  load_row<NV, RW>(dy + r * C, C / 4, pl.gl, gv);
+  rms_bwd_post_row<NV, RW>(gv, xv, x2v, rv, C, pl, valid, red, nm, r);
+}
+
 // ---- q/k head rows: per-head RMSNorm + RoPE in one pass -------------------
 // One wave per head row of hd = 64·E values, lane l holding values
 // [l·E, l·E + E): the RoPE partner of value i < hd/2 is i + hd/2, held by
@@ -830,7 +845,16 @@ void row_norm(hipStream_t s, const float* c, int64_t M, int64_t C, const RowNorm
     rmsnorm_fwd(s, nm.y, nm.w2, M, C, nm.eps, nm.unit_offset != 0, nm.y2, nm.rstd2);
     return;
   }
-  if (nm.kind == NORM_RMS_BWD_POST) {  // the two backward passes as two launches
+  if (nm.kind == NORM_RMS_BWD_POST) {
+    MFT_CHECK_ARG(M > 0 && C > 0 && nm.x && nm.x2 && nm.y && nm.y2 && nm.w && nm.w2 && nm.rstd && nm.rstd2,
+                  "post-norm backward: missing operand");
+    if (vec_ok(C, {c, nm.x, nm.x2, nm.w, nm.w2, nm.resid, nm.y, nm.y2})) {
+      const RowShape sh = row_shape(C);
+      MFT_ROW_DISPATCH(sh, rms_bwd_post_vec, row_grid(M, sh), dim3(256), 0, s, c, M, (int)C, nm);
+      MFT_LAUNCH_CHECK();
+      return;
+    }
+    // row-loop fallback: the two backward passes as two launches
     rmsnorm_bwd(s, c, nm.x, nm.w, nm.rstd, M, C, nm.unit_offset != 0, nm.y, nm.resid);
     rmsnorm_bwd(s, nm.y, nm.x2, nm.w2, nm.rstd2, M, C, nm.unit_offset != 0, nm.y2, nullptr);
     return;
