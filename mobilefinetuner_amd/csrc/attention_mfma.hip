@@ -956,6 +956,136 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short(AttnP p) {
   }
 }
 
+// Forward at head_dim 256 (Gemma-3): the same tiling and arithmetic as
+// attn_fwd_short, with the workgroup's 16 query rows staged once in LDS and
+// read as MFMA operands 16 dims at a time (holding them in registers, with
+// the K and V tiles and the O accumulator, would not fit two waves per
+// SIMD), and the key tile's K and V rows loaded per tile without a prefetch
+// set.  The waves' partial O rows are merged through the same LDS, after a
+// barrier that ends every wave's reads of the staged queries.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn_fwd_short256(AttnP p) {
+  constexpr int HD = 256, NC = HD / 16, PO = HD + 4;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Qs = smem;               // [16][PO] during the key loop
+  float* Os = smem;               // [NW][16][PO] after it
+  float* Ms = Os + NW * 16 * PO;  // [NW][16]
+  float* Ls = Ms + NW * 16;       // [NW][16]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int nqt = (p.S + 15) / 16;
+  const int hb = blockIdx.x % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int qt = nqt - 1 - (int)blockIdx.x / (p.Hq * p.B);  // heaviest (last) tiles first
+  const int q0 = 16 * qt;
+  const int kh = h / (p.Hq / p.Hkv);
+  const int qi = q0 + li;
+  const bool qok = qi < p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const int64_t tok0 = (int64_t)b * p.S;
+  const int qlast = min(q0 + 15, p.S - 1);
+  const int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
+  const int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  const int jhi = qok ? (p.causal ? qi : p.S - 1) : -1;  // keys visible to query qi
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
+
+  const float qscale = p.scale * kLog2e;  // scores in base-2 units
+  for (int f = tid; f < 16 * (HD / 4); f += 64 * NW) {
+    const int r = f / (HD / 4), c4 = f % (HD / 4), q = q0 + r;
+    const floatx4 x = *reinterpret_cast<const floatx4*>(p.q + (tok0 + min(q, p.S - 1)) * p.q_rs + (int64_t)h * HD + 4 * c4);
+    *reinterpret_cast<floatx4*>(&Qs[r * PO + 4 * c4]) = q < p.S ? x * qscale : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  floatx4 oacc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -INFINITY, lrow = 0.f;
+  const float* kbase = p.k + (int64_t)kh * HD;
+  const float* vbase = p.v + (int64_t)kh * HD;
+  const float* qrow = Qs + li * PO + 4 * lg;
+  for (int kt = kt_lo + w; kt <= kt_hi; kt += NW) {
+    floatx4 kc[NC];
+    float vc[NC][4];
+    const float* krow = kbase + (tok0 + min(16 * kt + li, p.S - 1)) * p.k_rs + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kc[c] = *reinterpret_cast<const floatx4*>(krow + 16 * c);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float* vrow = vbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.v_rs + li;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) vc[c][t] = vrow[16 * c];
+    }
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const floatx4 qv = *reinterpret_cast<const floatx4*>(qrow + 16 * c);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s = mfma4(kc[c][t], qv[t], s);
+    }
+    // lane holds S[query qi][key j0 + v]
+    const int j0 = 16 * kt + 4 * lg;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = j0 + v;
+      bool ok = (j >= jlo) & (j <= jhi) & (j < p.S);
+      if (kpb) ok = ok & (kpb[min(j, p.S - 1)] > 0.5f);
+      s[v] = ok ? s[v] : -INFINITY;
+    }
+    float mloc = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mloc = max_xor32(max_xor16(mloc));
+    const float mnew = fmaxf(mrow, mloc);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;  // nothing visible yet: exact zeros, no NaN
+    const float corr = fast_exp2(mrow - mref);
+    floatx4 pr;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) pr[v] = fast_exp2(s[v] - mref);
+    const float lsum = add_xor32(add_xor16((pr[0] + pr[1]) + (pr[2] + pr[3])));
+    lrow = lrow * corr + lsum;
+    mrow = mnew;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float cv = __shfl(corr, 4 * lg + v, 64);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) oacc[c][v] *= cv;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) oacc[c] = mfma4(pr[t], vc[c][t], oacc[c]);
+  }
+  __syncthreads();  // the staged queries are read by every wave before Os overwrites them
+  if (lg == 0) {
+    Ms[w * 16 + li] = mrow;
+    Ls[w * 16 + li] = lrow;
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Os[(w * 16 + 4 * lg + v) * PO + 16 * c + li] = oacc[c][v];
+  __syncthreads();
+  for (int f = tid; f < 16 * (HD / 4); f += 64 * NW) {
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    const int gq = q0 + r;
+    if (gq >= p.S) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) M = fmaxf(M, Ms[u * 16 + r]);
+    const float Mref = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    floatx4 o = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float wgt = fast_exp2(Ms[u * 16 + r] - Mref);
+      L += Ls[u * 16 + r] * wgt;
+      o += *reinterpret_cast<const floatx4*>(&Os[(u * 16 + r) * PO + 4 * c4]) * wgt;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *reinterpret_cast<floatx4*>(p.out + (tok0 + gq) * p.out_rs + (int64_t)h * HD + 4 * c4) = o * inv;
+    if (c4 == 0) p.lse_out[((int64_t)b * p.Hq + h) * p.S + gq] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
+  }
+}
+
 // dK/dV role: workgroup = one 16-key tile of one QUERY head; waves take the
 // query tiles that see it round-robin.  K, V of the tile are read from
 // global memory once per workgroup (staged in LDS) and stay in registers
@@ -1455,6 +1585,26 @@ void fwd_short_launch(hipStream_t s, AttnP& p) {
   MFT_LAUNCH_CHECK();
 }
 
+// The head_dim-256 forward at S ≤ 256 (its backward keeps the blocked
+// kernels).  Tuning hook: MFT_ATTN_SHORT256=0 keeps the blocked forward.
+bool use_short256_fwd(const AttnArgs& a) {
+  static const int mode = [] {
+    const char* e = getenv("MFT_ATTN_SHORT256");
+    return e ? atoi(e) : 1;
+  }();
+  return mode != 0 && a.hd == 256 && a.S <= 256;
+}
+
+void fwd_short256_launch(hipStream_t s, AttnP& p) {
+  constexpr int NW = kShortWaves, PO = 256 + 4;
+  const size_t lds = sizeof(float) * (NW * 16 * PO + 2 * NW * 16);
+  auto kern = attn_fwd_short256<NW>;
+  set_lds(kern, lds);
+  const dim3 grid((unsigned)(cdiv(p.S, 16) * p.Hq * p.B));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, s, p);
+  MFT_LAUNCH_CHECK();
+}
+
 template <int HD>
 void bwd_short_launch(hipStream_t s, AttnP& p) {
   constexpr int NW = kShortWaves;
@@ -1496,7 +1646,7 @@ AttnP make(const AttnArgs& a) {
 }  // namespace
 
 size_t attn_fwd_scratch_floats(const AttnArgs& a) {
-  if (use_short(a)) return 0;
+  if (use_short(a) || use_short256_fwd(a)) return 0;
   const FwdPlan pl = fwd_plan(a);
   if (pl.nch == 1) return 0;
   return (size_t)a.B * a.Hq * pl.nch * a.S * (size_t)(a.hd + 2);
@@ -1518,6 +1668,10 @@ void attn_fwd(hipStream_t s, const AttnArgs& a, float* o, int64_t o_rs, float* l
   p.lse_out = lse;
   if (use_short(a)) {
     a.hd == 64 ? fwd_short_launch<64>(s, p) : fwd_short_launch<128>(s, p);
+    return;
+  }
+  if (use_short256_fwd(a)) {
+    fwd_short256_launch(s, p);
     return;
   }
   const FwdPlan pl = fwd_plan(a);

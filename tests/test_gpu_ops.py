@@ -195,6 +195,7 @@ ATTN = [
     (2, 14, 2, 160, 64, 0, True),     # Qwen-style GQA 7:1, padding mask
     (2, 4, 1, 96, 256, 0, False),     # Gemma hd=256, GQA 4:1
     (1, 4, 1, 200, 256, 64, False),   # Gemma sliding window
+    (2, 4, 1, 144, 256, 0, True),     # hd=256 short-sequence forward: padding mask, GQA 4:1
     (1, 4, 2, 77, 128, 0, True),      # hd=128, ragged S
     (2, 4, 2, 200, 64, 48, True),     # short-sequence kernels: sliding window, padding, GQA
     # grids large enough for the 4- and 2-wave workgroup variants
