@@ -160,6 +160,54 @@ __global__ void glu_bwd_kernel(const float* __restrict__ dout,
   }
 }
 
+// 128-bit forms: one run of 4 consecutive elements of a row per thread
+// (cols % 4 == 0, every operand 16-byte aligned and n/4 < 2^31, checked on
+// the host), the run's row found with one 32-bit division.
+typedef float glux4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int64_t gu_run(unsigned q, unsigned cq, unsigned ldq) {
+  if (ldq == cq) return q;
+  const unsigned r = q / cq;
+  return (int64_t)r * ldq + (q - r * cq);
+}
+
+__global__ __launch_bounds__(256) void glu_fwd_vec(const glux4* __restrict__ gate, const glux4* __restrict__ up,
+                                                   unsigned nq, unsigned cq, unsigned ldq, int act,
+                                                   glux4* __restrict__ out) {
+  const unsigned q = blockIdx.x * 256u + threadIdx.x;
+  if (q >= nq) return;
+  const int64_t j = gu_run(q, cq, ldq);
+  const glux4 g = gate[j];
+  const glux4 u = up ? up[j] : glux4{1.f, 1.f, 1.f, 1.f};
+  glux4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (act == 0 ? gelu_tanh(g[e]) : silu(g[e])) * u[e];
+  out[q] = o;
+}
+
+__global__ __launch_bounds__(256) void glu_bwd_vec(const glux4* __restrict__ dout, const glux4* __restrict__ gate,
+                                                   const glux4* __restrict__ up, unsigned nq, unsigned cq,
+                                                   unsigned ldq, int act, glux4* __restrict__ dgate,
+                                                   glux4* __restrict__ dup) {
+  const unsigned q = blockIdx.x * 256u + threadIdx.x;
+  if (q >= nq) return;
+  const int64_t j = gu_run(q, cq, ldq);
+  const glux4 d = dout[q];
+  const glux4 g = gate[j];
+  const glux4 u = up ? up[j] : glux4{1.f, 1.f, 1.f, 1.f};
+  glux4 dg, du;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float gv = g[e];
+    const float a = act == 0 ? gelu_tanh(gv) : silu(gv);
+    const float da = act == 0 ? gelu_tanh_grad(gv) : silu_grad(gv);
+    dg[e] = d[e] * u[e] * da;
+    du[e] = d[e] * a;
+  }
+  dgate[j] = dg;
+  if (up && dup) dup[j] = du;
+}
+
 // ---- RoPE (HF rotate_half) ---------------------------------------------------
 __global__ void rope_kernel(float* x, int64_t rs, int B, int S, int H, int hd,
                             double theta, int inverse) {
@@ -588,11 +636,27 @@ void glu_bwd(hipStream_t s, const float* dout, const float* gate,
              const float* up, int64_t n, int act, float* dgate, float* dup) {
   glu_bwd_rows(s, dout, gate, up, 1, n, n, act, dgate, dup);
 }
+// The 128-bit GLU kernels' preconditions (null operands pass).
+static bool glu_vec_ok(int64_t n, int64_t cols, int64_t ld_gu, std::initializer_list<const void*> ptrs) {
+  if (cols % 4 != 0 || ld_gu % 4 != 0 || n / 4 >= ((int64_t)1 << 31)) return false;
+  for (const void* p : ptrs)
+    if (((uintptr_t)p & 15) != 0) return false;
+  return true;
+}
+
 void glu_fwd_rows(hipStream_t s, const float* gate, const float* up, int64_t rows, int64_t cols, int64_t ld_gu,
                   int act, float* out) {
   const int64_t n = rows * cols;
   if (n <= 0) return;
   MFT_CHECK_ARG(ld_gu >= cols, "glu: gate/up row pitch below the row length");
+  if (glu_vec_ok(n, cols, ld_gu, {gate, up, out})) {
+    const unsigned nq = (unsigned)(n / 4);
+    hipLaunchKernelGGL(glu_fwd_vec, dim3(cdiv(nq, 256)), dim3(256), 0, s, reinterpret_cast<const glux4*>(gate),
+                       reinterpret_cast<const glux4*>(up), nq, (unsigned)(cols / 4), (unsigned)(ld_gu / 4), act,
+                       reinterpret_cast<glux4*>(out));
+    MFT_LAUNCH_CHECK();
+    return;
+  }
   hipLaunchKernelGGL(glu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, cols, ld_gu, act, out);
   MFT_LAUNCH_CHECK();
 }
@@ -601,6 +665,15 @@ void glu_bwd_rows(hipStream_t s, const float* dout, const float* gate, const flo
   const int64_t n = rows * cols;
   if (n <= 0) return;
   MFT_CHECK_ARG(ld_gu >= cols, "glu: gate/up row pitch below the row length");
+  if (glu_vec_ok(n, cols, ld_gu, {dout, gate, up, dgate, dup})) {
+    const unsigned nq = (unsigned)(n / 4);
+    hipLaunchKernelGGL(glu_bwd_vec, dim3(cdiv(nq, 256)), dim3(256), 0, s, reinterpret_cast<const glux4*>(dout),
+                       reinterpret_cast<const glux4*>(gate), reinterpret_cast<const glux4*>(up), nq,
+                       (unsigned)(cols / 4), (unsigned)(ld_gu / 4), act, reinterpret_cast<glux4*>(dgate),
+                       reinterpret_cast<glux4*>(dup));
+    MFT_LAUNCH_CHECK();
+    return;
+  }
   hipLaunchKernelGGL(glu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, dout, gate, up, n, cols, ld_gu, act, dgate,
                      dup);
   MFT_LAUNCH_CHECK();
