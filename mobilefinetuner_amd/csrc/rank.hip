@@ -370,7 +370,9 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
 #pragma unroll
     for (int j = 0; j < R; ++j) acc[q][j] = 0.f;
   // K is a multiple of 4 (checked on the host), so a 4-vector never crosses a row.
-#pragma unroll 2
+  // The K-split form unrolls deeper: its few workgroups (one job of 4-row
+  // groups) leave the loads of several steps to cover the memory latency.
+#pragma unroll(KS == 1 ? 2 : 4)
   for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
     floatx4 xv[RW];
 #pragma unroll
