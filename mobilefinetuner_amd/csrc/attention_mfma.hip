@@ -1543,8 +1543,12 @@ BwdPlan bwd_plan(const AttnArgs& a) {
   const int bkv = a.hd == 64 ? Cfg<64>::DQBKV : a.hd == 128 ? Cfg<128>::DQBKV : Cfg<256>::DQBKV;
   const int64_t waves = launch_waves(a, nw);
   const int nqb = (int)cdiv(a.S, bq), nkb = (int)cdiv(a.S, bkv);
-  const int pq = chunk_blocks(a, waves, nqb, kMaxBwdChunks, "MFT_ATTN_BWD_BPC");
-  const int pk = chunk_blocks(a, waves, nkb, kMaxBwdChunks, "MFT_ATTN_BWD_BPC");
+  // head_dim 256: two waves per workgroup already give the launch its
+  // waves; a dK/dV split beyond two chunks and any dQ split cost more in
+  // partial rows and their sums than they return (Gemma-3 at S = 256)
+  const int maxq = a.hd == 256 ? 2 : kMaxBwdChunks, maxk = a.hd == 256 ? 1 : kMaxBwdChunks;
+  const int pq = chunk_blocks(a, waves, nqb, maxq, "MFT_ATTN_BWD_BPC");
+  const int pk = chunk_blocks(a, waves, nkb, maxk, "MFT_ATTN_BWD_BPC");
   BwdPlan pl{nw, 1, a.S, 1, a.S};
   if (pq) { pl.nqc = (int)cdiv(nqb, pq); pl.cq = pq * bq; }
   if (pk) { pl.nkc = (int)cdiv(nkb, pk); pl.ckq = pk * bkv; }
