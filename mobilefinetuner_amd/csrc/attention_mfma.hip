@@ -1530,8 +1530,9 @@ FwdPlan fwd_plan(const AttnArgs& a) {
 }
 
 // Backward splits (dK/dV over query chunks, dQ over key chunks), at most
-// kMaxBwdChunks each: every chunk costs a partial row per (token, head).
-constexpr int kMaxBwdChunks = 4;
+// kMaxBwdChunks each: every chunk costs a partial row per (token, head), and
+// at Qwen2's S = 1024 two chunks measured faster than four.
+constexpr int kMaxBwdChunks = 2;
 
 struct BwdPlan {
   int nw, nqc, cq, nkc, ckq;
@@ -1543,10 +1544,9 @@ BwdPlan bwd_plan(const AttnArgs& a) {
   const int bkv = a.hd == 64 ? Cfg<64>::DQBKV : a.hd == 128 ? Cfg<128>::DQBKV : Cfg<256>::DQBKV;
   const int64_t waves = launch_waves(a, nw);
   const int nqb = (int)cdiv(a.S, bq), nkb = (int)cdiv(a.S, bkv);
-  // head_dim 256: two waves per workgroup already give the launch its
-  // waves; a dK/dV split beyond two chunks and any dQ split cost more in
-  // partial rows and their sums than they return (Gemma-3 at S = 256)
-  const int maxq = a.hd == 256 ? 2 : kMaxBwdChunks, maxk = a.hd == 256 ? 1 : kMaxBwdChunks;
+  // head_dim 256: a dQ split costs more in partial rows and their sums than
+  // it returns (Gemma-3 at S = 256)
+  const int maxq = kMaxBwdChunks, maxk = a.hd == 256 ? 1 : kMaxBwdChunks;
   const int pq = chunk_blocks(a, waves, nqb, maxq, "MFT_ATTN_BWD_BPC");
   const int pk = chunk_blocks(a, waves, nkb, maxk, "MFT_ATTN_BWD_BPC");
   BwdPlan pl{nw, 1, a.S, 1, a.S};
