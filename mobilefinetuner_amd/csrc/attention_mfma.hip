@@ -107,6 +107,9 @@ __device__ __forceinline__ void stage_pair(StageDst d1, const float* src1, int64
   constexpr int ITEMS = TOTAL / NT;
   constexpr int CH = ITEMS < 512 / HD ? ITEMS : 512 / HD;
   static_assert(ITEMS % CH == 0, "staging batch");
+  // both tensors through buffer resources at the sequence's first row
+  const __amdgpu_buffer_rsrc_t rs_1 = buf_rsrc(src1 + (int64_t)b * S * rs1 + (int64_t)h1 * HD);
+  const __amdgpu_buffer_rsrc_t rs_2 = buf_rsrc(src2 + (int64_t)b * S * rs2 + (int64_t)h2 * HD);
 #pragma unroll
   for (int base = 0; base < ITEMS; base += CH) {
     floatx4 v1[CH], v2[CH];
@@ -115,11 +118,9 @@ __device__ __forceinline__ void stage_pair(StageDst d1, const float* src1, int64
       const int f = tid + NT * (base + c);
       int r, c4;
       stage_item<HD, ROWS, T1>(f, r, c4);
-      const int64_t row1 = (int64_t)b * S + min(r0 + r, S - 1);
-      v1[c] = *reinterpret_cast<const floatx4*>(src1 + row1 * rs1 + (int64_t)h1 * HD + 4 * c4);
+      v1[c] = buf_load4(rs_1, (uint32_t)(((int64_t)min(r0 + r, S - 1) * rs1 + 4 * c4) * 4), 0);
       stage_item<HD, ROWS, T2>(f, r, c4);
-      const int64_t row2 = (int64_t)b * S + min(r0 + r, S - 1);
-      v2[c] = *reinterpret_cast<const floatx4*>(src2 + row2 * rs2 + (int64_t)h2 * HD + 4 * c4);
+      v2[c] = buf_load4(rs_2, (uint32_t)(((int64_t)min(r0 + r, S - 1) * rs2 + 4 * c4) * 4), 0);
     }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -856,17 +857,19 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short(AttnP p) {
     }
   }
   float mrow = -INFINITY, lrow = 0.f;
-  const float* kbase = p.k + (int64_t)kh * HD;
-  const float* vbase = p.v + (int64_t)kh * HD;
+  // K and V of this sequence and KV head through buffer resources (32-bit
+  // per-lane offsets; a sequence's rows span well under 4 GiB)
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k + tok0 * p.k_rs + (int64_t)kh * HD);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(p.v + tok0 * p.v_rs + (int64_t)kh * HD);
   auto load = [&](int kt, floatx4 (&kr)[NC], float (&vr)[NC][4]) {
-    const float* krow = kbase + (tok0 + min(16 * kt + li, p.S - 1)) * p.k_rs + 4 * lg;
+    const uint32_t ko = (uint32_t)(((int64_t)min(16 * kt + li, p.S - 1) * p.k_rs + 4 * lg) * 4);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kr[c] = *reinterpret_cast<const floatx4*>(krow + 16 * c);
+    for (int c = 0; c < NC; ++c) kr[c] = buf_load4(rk, ko + 64u * c, 0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float* vrow = vbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.v_rs + li;
+      const uint32_t vo = (uint32_t)(((int64_t)min(16 * kt + 4 * lg + t, p.S - 1) * p.v_rs + li) * 4);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) vr[c][t] = vrow[16 * c];
+      for (int c = 0; c < NC; ++c) vr[c][t] = buf_load1(rv, vo + 64u * c, 0);
     }
   };
   floatx4 kc[NC];
@@ -1001,20 +1004,20 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short256(AttnP p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   float mrow = -INFINITY, lrow = 0.f;
-  const float* kbase = p.k + (int64_t)kh * HD;
-  const float* vbase = p.v + (int64_t)kh * HD;
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k + tok0 * p.k_rs + (int64_t)kh * HD);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(p.v + tok0 * p.v_rs + (int64_t)kh * HD);
   const float* qrow = Qs + li * PO + 4 * lg;
   for (int kt = kt_lo + w; kt <= kt_hi; kt += NW) {
     floatx4 kc[NC];
     float vc[NC][4];
-    const float* krow = kbase + (tok0 + min(16 * kt + li, p.S - 1)) * p.k_rs + 4 * lg;
+    const uint32_t ko = (uint32_t)(((int64_t)min(16 * kt + li, p.S - 1) * p.k_rs + 4 * lg) * 4);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kc[c] = *reinterpret_cast<const floatx4*>(krow + 16 * c);
+    for (int c = 0; c < NC; ++c) kc[c] = buf_load4(rk, ko + 64u * c, 0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float* vrow = vbase + (tok0 + min(16 * kt + 4 * lg + t, p.S - 1)) * p.v_rs + li;
+      const uint32_t vo = (uint32_t)(((int64_t)min(16 * kt + 4 * lg + t, p.S - 1) * p.v_rs + li) * 4);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) vc[c][t] = vrow[16 * c];
+      for (int c = 0; c < NC; ++c) vc[c][t] = buf_load1(rv, vo + 64u * c, 0);
     }
     floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1125,17 +1128,22 @@ __device__ __forceinline__ void attn_bwd_short_dkdv(const AttnP& p, int bid, flo
     floatx4 qa[NC], ga[NC], oa[NC];
     float lse;
   };
+  // Q, dO, O of this sequence and query head through buffer resources
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc(p.q + tok0 * p.q_rs + (int64_t)h * HD);
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(p.dout + tok0 * p.do_rs + (int64_t)h * HD);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(p.o + tok0 * p.o_rs + (int64_t)h * HD);
   auto load = [&](int qt, QTile& T) {
     const int q0 = 16 * qt;
-    const int64_t row = tok0 + min(q0 + li, p.S - 1);
-    const int64_t off = (int64_t)h * HD + 4 * lg;
+    const int64_t r = min(q0 + li, p.S - 1);
+    const uint32_t oq = (uint32_t)((r * p.q_rs + 4 * lg) * 4), og = (uint32_t)((r * p.do_rs + 4 * lg) * 4),
+                   oo = (uint32_t)((r * p.o_rs + 4 * lg) * 4);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      T.qa[c] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off + 16 * c);
-      T.ga[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
-      T.oa[c] = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
+      T.qa[c] = buf_load4(rq, oq + 64u * c, 0);
+      T.ga[c] = buf_load4(rg, og + 64u * c, 0);
+      T.oa[c] = buf_load4(ro, oo + 64u * c, 0);
     }
-    T.lse = p.lse[lrow0 + min(q0 + li, p.S - 1)];
+    T.lse = p.lse[lrow0 + r];
   };
   // K, V rows of the tile (rows past S clamped; their keys are masked):
   // one 128-bit item per thread and tensor per pass, issued together with
@@ -1299,12 +1307,15 @@ __device__ __forceinline__ void attn_bwd_short_dq(const AttnP& p, int bid, float
   struct KTile {
     floatx4 ka[NC], va[NC];
   };
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + tok0 * p.k_rs);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + tok0 * p.v_rs);
   auto load = [&](int kt, KTile& T) {
-    const int64_t row = tok0 + min(16 * kt + li, p.S - 1);
+    const int64_t r = min(16 * kt + li, p.S - 1);
+    const uint32_t ko = (uint32_t)((r * p.k_rs + 4 * lg) * 4), vo = (uint32_t)((r * p.v_rs + 4 * lg) * 4);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      T.ka[c] = *reinterpret_cast<const floatx4*>(kbase + row * p.k_rs + 16 * c + 4 * lg);
-      T.va[c] = *reinterpret_cast<const floatx4*>(vbase + row * p.v_rs + 16 * c + 4 * lg);
+      T.ka[c] = buf_load4(rk, ko + 64u * c, 0);
+      T.va[c] = buf_load4(rv, vo + 64u * c, 0);
     }
   };
   // Q, dO, O rows of the tile (rows past S clamped; they are not stored):

@@ -83,6 +83,27 @@ __device__ __forceinline__ float __attribute__((ext_vector_type(4))) unstash_f16
   return widen4(uint2{__float_as_uint(v[0]), __float_as_uint(v[1])});
 }
 
+// Raw buffer resource over [base, base + 4 GiB): a load takes a 32-bit
+// per-lane byte offset (one VGPR) plus a wave-uniform offset (an SGPR)
+// instead of a 64-bit address pair and its 64-bit arithmetic — on the
+// operand loads of the GEMM and attention loops that issue cost showed as
+// matrix-core idle time.  No range checking is relied on: every offset the
+// kernels form stays inside its operand.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ float __attribute__((ext_vector_type(4))) buf_load4(__amdgpu_buffer_rsrc_t r,
+                                                                              uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float __attribute__((ext_vector_type(4))),
+                            __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint2 buf_load2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
 // ---- launchers shared by the C-ABI and the step engine ----------------------
 // A row norm applied to the finished rows of a GEMM output C[M,N] (N = the
 // normalised width, ldc = N):

@@ -56,19 +56,6 @@ struct GemmParams {
   GemmEpilogue ep;
 };
 
-// Raw buffer resource over [base, base + 4 GiB): loads take a 32-bit byte
-// offset per lane plus a wave-uniform offset; no range checking is relied
-// on (every offset formed by the kernels stays inside its operand).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
-}
-__device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ uint2 buf_load2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-}
-
 constexpr float kLog2eG = 1.4426950408889634f;
 
 // Softmax statistics of one logits row segment of 64 values held in LDS
@@ -661,37 +648,40 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmParams p) {
     // here and a panel adds one uniform offset (clamped to the last panel,
     // so the prefetches past the end stay in bounds; those panels are
     // stored as zeros).  No per-element masks in the loop.
-    const float* a_ptr[A_ITEMS];
-    const char* b_ptr[B_ITEMS];
     constexpr int BES = B_F16 ? 2 : 4;
+    // buffer resources at the tile's first row / column and kbeg (as in
+    // gemm_p_kernel): 32-bit per-lane offsets, panel offsets in SGPRs
+    const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(p.A + (int64_t)m0 * p.lda + kbeg);
+    const __amdgpu_buffer_rsrc_t rsb =
+        buf_rsrc(static_cast<const char*>(p.B) + (B_NK ? (int64_t)n0 * p.ldb + kbeg : (int64_t)kbeg * p.ldb + n0) * BES);
+    uint32_t a_off[A_ITEMS], b_off[B_ITEMS];
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-      a_ptr[it] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + kq;
+      a_off[it] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + kq) * 4);
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
       const int flat = tid + 256 * it;
       if constexpr (B_NK) {
         const int row = flat / (BK / 4), kq = (flat % (BK / 4)) * 4;
-        b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)min(n0 + row, p.N - 1) * p.ldb + kq) * BES;
+        b_off[it] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + kq) * BES);
       } else {
         const int k = flat / (BN / 4), nq = (flat % (BN / 4)) * 4;
-        const int gn = n0 + nq < p.N ? n0 + nq : 0;
-        b_ptr[it] = static_cast<const char*>(p.B) + ((int64_t)k * p.ldb + gn) * BES;
+        b_off[it] = (uint32_t)(((int64_t)k * p.ldb + (n0 + nq < p.N ? nq : 0)) * BES);
       }
     }
     auto load_fast = [&](auto sc, int k0) {
       constexpr int S = decltype(sc)::value;
-      const int kc = min(k0, kend - BK);
+      const int kc = min(k0, kend - BK) - kbeg;
 #pragma unroll
-      for (int it = 0; it < A_ITEMS; ++it) ra_set[S][it] = *reinterpret_cast<const floatx4*>(a_ptr[it] + kc);
-      const int64_t boff = (B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES;
+      for (int it = 0; it < A_ITEMS; ++it) ra_set[S][it] = buf_load4(rsa, a_off[it], (uint32_t)kc * 4u);
+      const uint32_t boff = (uint32_t)((B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * BES);
 #pragma unroll
       for (int it = 0; it < B_ITEMS; ++it) {
-        if constexpr (B_F16) rb_set[S][it] = stash_f16(*reinterpret_cast<const uint2*>(b_ptr[it] + boff));
-        else rb_set[S][it] = *reinterpret_cast<const floatx4*>(b_ptr[it] + boff);
+        if constexpr (B_F16) rb_set[S][it] = stash_f16(buf_load2u(rsb, b_off[it], boff));
+        else rb_set[S][it] = buf_load4(rsb, b_off[it], boff);
       }
     };
     auto store_fast = [&](auto sc, int k0) {
@@ -1365,10 +1355,10 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   p.k_chunk = (int)(cdiv(cdiv(K, splits), bk) * bk);
   splits = (int)cdiv(K, p.k_chunk);
   MFT_CHECK_ARG(!ep.stats || splits == 1, "row statistics need an unsplit K");
-  // The pipelined kernels address a tile's K-slice through 32-bit buffer
+  // The whole-panel kernels address a tile's K-slice through 32-bit buffer
   // offsets from the tile's first row / column.
   MFT_CHECK_ARG(((int64_t)128 * lda + p.k_chunk) * 4 < (int64_t(1) << 32) &&
-                    (b_nk ? (int64_t)64 * p.ldb + p.k_chunk : (int64_t)p.k_chunk * p.ldb + 64) * (b_f16 ? 2 : 4) <
+                    (b_nk ? (int64_t)128 * p.ldb + p.k_chunk : (int64_t)p.k_chunk * p.ldb + 128) * (b_f16 ? 2 : 4) <
                         (int64_t(1) << 32),
                 "GEMM operand too large for 32-bit buffer offsets");
   if (splits > 1) p.partial = ws.ptr;
