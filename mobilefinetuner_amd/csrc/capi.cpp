@@ -7,6 +7,8 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -30,11 +32,49 @@ int g_sync_check = [] {
   return e && atoi(e) != 0 ? 1 : 0;
 }();
 
+// Streams the library launches on (handles, models, their copy and capture
+// streams), reference-counted.  The sync check waits for these streams only,
+// and not at all while any of them is being captured into a graph: a device
+// or stream wait inside a capture would invalidate it.  (So the mode reports
+// nothing for launches made under capture; they run when the graph does.)
+std::mutex g_streams_mu;
+std::vector<std::pair<hipStream_t, int>> g_streams;
+
+void register_stream(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);
+  for (auto& e : g_streams)
+    if (e.first == s) {
+      ++e.second;
+      return;
+    }
+  g_streams.emplace_back(s, 1);
+}
+
+void unregister_stream(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);
+  for (size_t i = 0; i < g_streams.size(); ++i)
+    if (g_streams[i].first == s) {
+      if (--g_streams[i].second == 0) g_streams.erase(g_streams.begin() + (std::ptrdiff_t)i);
+      return;
+    }
+}
+
 void sync_check(const char* file, int line) {
-  const hipError_t e = hipDeviceSynchronize();
-  if (e != hipSuccess)
-    throw Error(MFT_EHIP, std::string("sync check after the launch at ") + file + ":" + std::to_string(line) +
-                              ": " + hipGetErrorString(e));
+  std::vector<hipStream_t> streams;
+  {
+    std::lock_guard<std::mutex> lock(g_streams_mu);
+    for (const auto& e : g_streams) streams.push_back(e.first);
+  }
+  for (hipStream_t s : streams) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone) return;
+  }
+  for (hipStream_t s : streams) {
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+      throw Error(MFT_EHIP, std::string("sync check after the launch at ") + file + ":" + std::to_string(line) +
+                                ": " + hipGetErrorString(e));
+  }
 }
 
 }  // namespace mft
@@ -97,6 +137,7 @@ int mft_create(mft_handle* out, void* stream) {
     if (!out) throw mft::Error(MFT_EINVAL, "null out");
     HandleImpl* hi = new HandleImpl();
     hi->h.stream = reinterpret_cast<hipStream_t>(stream);
+    mft::register_stream(hi->h.stream);
     MFT_HIP(hipGetDevice(&hi->h.device));
     int ncu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, hi->h.device) == hipSuccess && ncu > 0)
@@ -113,6 +154,7 @@ int mft_destroy(mft_handle h) {
       (void)hipStreamSynchronize(h->stream);
       (void)hipFree(hi->scratch.ptr);
     }
+    mft::unregister_stream(h->stream);
     delete hi;
   });
 }
@@ -120,6 +162,8 @@ int mft_destroy(mft_handle h) {
 int mft_set_stream(mft_handle h, void* stream) {
   return guarded([&] {
     require_handle(h);
+    mft::register_stream(reinterpret_cast<hipStream_t>(stream));
+    mft::unregister_stream(h->stream);
     h->stream = reinterpret_cast<hipStream_t>(stream);
   });
 }

@@ -1,6 +1,9 @@
 // ce.hip — shifted LM cross-entropy over the full vocabulary, forward and
 // backward in one pass structure:
-//   1. count the valid targets (label != ignore_index, shifted by one),
+//   1. count the valid targets (label != ignore_index, shifted by one) —
+//      inside every row workgroup for up to kCountInRowMax rows, else once
+//      by a one-workgroup launch ahead of the rows (per-row counting reads
+//      the whole label array once per row: rows² work),
 //   2. one workgroup per logits row: online max/sum-exp over V in registers
 //      (base 2 on x·log2e; each thread keeps its own running max and
 //      rescaled sum over 128-bit loads, merged by a wave64 shuffle tree and
@@ -74,6 +77,26 @@ __device__ __forceinline__ void publish_count(int c, bool oor, int* red, int64_t
   }
 }
 
+// The micro-batch's valid-target count formed once (batches above
+// kCountInRowMax rows): one workgroup strides the labels, stores the count
+// in *cnt and raises *bad for an out-of-range label.
+__global__ __launch_bounds__(1024) void ce_count_kernel(const int32_t* __restrict__ labels, int B, int S,
+                                                        int64_t V, int ignore_index, int64_t* cnt, int* bad) {
+  __shared__ int red[16];
+  bool oor = false;
+  int c = count_share(labels, B, S, V, ignore_index, threadIdx.x, 1024, oor);
+  if (oor && bad) atomicOr(bad, 1);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t v = 0;
+    for (int w = 0; w < 16; ++w) v += red[w];
+    *cnt = v;
+  }
+}
+
 // One workgroup per logits row.  The row is walked as an aligned float4 body
 // (rows start at any 4-byte offset when V is odd) plus a scalar head and
 // tail.  The first H·BLOCK float4 of the body stay in registers from the
@@ -85,12 +108,13 @@ __device__ __forceinline__ void publish_count(int c, bool oor, int* red, int64_t
 // with one rescale, and re-read by the gradient sweep, which writes dlogits
 // in place.
 // The micro-batch's target count is formed in every workgroup beside the
-// row's statistics (workgroup 0 stores it in *cnt and raises *bad).
+// row's statistics (workgroup 0 stores it in *cnt and raises *bad), or, with
+// `counted`, read from *cnt where ce_count_kernel stored it.
 template <int BLOCK, int H>
 __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S,
     int64_t V, int64_t ld, int ignore_index, float upstream, int64_t norm_count,
-    int64_t* __restrict__ cnt, int* bad, float* dlogits, float* __restrict__ row_nll) {
+    int64_t* __restrict__ cnt, int* bad, float* dlogits, float* __restrict__ row_nll, int counted) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
   __shared__ int sc[NW];
@@ -101,9 +125,9 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
   float* dx = dlogits ? dlogits + row * ld : nullptr;
   const int tid = threadIdx.x;
   bool oor = false;
-  int c = count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
+  int c = counted ? 0 : count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
   if (label == ignore_index || label < 0 || (int64_t)label >= V) {
-    publish_count<NW>(c, oor, sc, cnt, bad);
+    if (!counted) publish_count<NW>(c, oor, sc, cnt, bad);
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
@@ -186,7 +210,8 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     merge_ms(m, sum, sm[i], ss[i]);
     n_valid += sc[i];
   }
-  if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
+  if (counted) n_valid = *cnt;
+  else if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
   const float lse2 = m + __builtin_amdgcn_logf(sum);  // log2 Σ 2^t (sum ≥ 1)
   if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
   if (!dx) return;
@@ -245,7 +270,7 @@ template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S, int64_t V, int64_t ld,
     int ignore_index, float upstream, int64_t norm_count, int64_t* __restrict__ cnt, int* bad, float* dlogits,
-    float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld) {
+    float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld, int counted) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
   __shared__ int sc[NW];
@@ -256,9 +281,9 @@ __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
   float* dx = dlogits ? dlogits + row * ld : nullptr;
   const int tid = threadIdx.x;
   bool oor = false;
-  int c = count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
+  int c = counted ? 0 : count_share(labels, B, S, V, ignore_index, tid, BLOCK, oor);
   if (label == ignore_index || label < 0 || (int64_t)label >= V) {
-    publish_count<NW>(c, oor, sc, cnt, bad);
+    if (!counted) publish_count<NW>(c, oor, sc, cnt, bad);
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
@@ -295,7 +320,8 @@ __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     merge_ms(m, sum, sm[i], ss[i]);
     n_valid += sc[i];
   }
-  if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
+  if (counted) n_valid = *cnt;
+  else if (blockIdx.x == 0 && tid == 0) *cnt = n_valid;
   const float lse2 = m + __builtin_amdgcn_logf(sum);
   if (tid == 0) row_nll[row] = lse2 * kLn2 - xl;
   if (!dx) return;
@@ -362,6 +388,16 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
+  // Up to kCountInRowMax rows every row workgroup counts the targets beside
+  // its own statistics (no launch of its own); beyond, a count launch forms it
+  // once (per-row counting grows with rows²: 4.3G label reads at 65536 rows).
+  constexpr int64_t kCountInRowMax = 4096;
+  const int counted = rows > kCountInRowMax ? 1 : 0;
+  if (counted) {
+    hipLaunchKernelGGL(ce_count_kernel, dim3(1), dim3(1024), 0, s, labels, B, S, V, ignore_index, count_scratch,
+                       bad_label);
+    MFT_LAUNCH_CHECK();
+  }
   // rows of up to 13·4096 values are held whole in registers (GPT-2's
   // 50257); wider rows take the LM head's row statistics when it wrote them
   // (one sweep), else keep their first 16·4096 values in registers
@@ -369,13 +405,13 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
     MFT_CHECK_ARG(stats_ld >= cdiv(V, 64), "row statistics pitch");
     hipLaunchKernelGGL((ce_row_stats_kernel<1024>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
                        ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll,
-                       row_stats, stats_ld);
+                       row_stats, stats_ld, counted);
   } else if (V <= 13 * 4096)
     hipLaunchKernelGGL((ce_row_kernel<1024, 13>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted);
   else
     hipLaunchKernelGGL((ce_row_kernel<1024, 16>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted);
   MFT_LAUNCH_CHECK();
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,
                      (const int64_t*)count_scratch, n_valid);

@@ -39,10 +39,15 @@ void set_last_error(const std::string& msg);
 
 // Kernel launch error check (catches invalid launch configurations).  In
 // sync-check mode (mft_set_sync_check, or MFT_SYNC_CHECK=1 in the
-// environment) every check also waits for the device and reports an
-// execution error with the launch site that precedes it.
+// environment) every check also waits for the library's streams and reports
+// an execution error with the launch site that precedes it — except while
+// one of them is being captured into a graph, where waiting would break the
+// capture.
 extern int g_sync_check;
 void sync_check(const char* file, int line);
+// Streams the sync check waits for (every stream the library launches on).
+void register_stream(hipStream_t s);
+void unregister_stream(hipStream_t s);
 #define MFT_LAUNCH_CHECK()                                   \
   do {                                                       \
     MFT_HIP(hipGetLastError());                              \

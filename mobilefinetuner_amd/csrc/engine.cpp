@@ -131,6 +131,9 @@ struct ShardStore {
   uint64_t clock = 0;
   std::vector<int> seq, prev;  // entries in use order: this pass and the previous one
   int64_t loads = 0, hits = 0;
+  // error of a prefetch issued from a use's release (reported by the next use)
+  int deferred_code = 0;
+  std::string deferred;
 };
 
 // Loss and count slots of a step: 64 doubles then 64 int64 (8-byte words).
@@ -234,6 +237,7 @@ struct mft_model_s {
   int64_t last_rows = 0;  // token rows of the last forward (activation accessor)
   // captured train-step graph
   hipStream_t cap_stream = nullptr;
+  bool stream_registered = false;  // m->stream is in the sync check's stream list
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   bool capturing = false;
@@ -391,6 +395,7 @@ void alloc_params(mft_model_s* m) {
       throw Error(MFT_ENOMEM, "shard store pool (" + std::to_string(budget) + " bytes)");
     sh.free_blocks[0] = budget;
     MFT_HIP(hipStreamCreateWithFlags(&sh.copy, hipStreamNonBlocking));
+    register_stream(sh.copy);
     for (auto& e : sh.ents) {
       MFT_HIP(hipEventCreateWithFlags(&e.ready, hipEventDisableTiming));
       MFT_HIP(hipEventCreateWithFlags(&e.used, hipEventDisableTiming));
@@ -455,8 +460,9 @@ void shard_free(ShardStore& sh, int64_t off, int64_t bytes) {
 
 // Makes entry i resident: evicts the least recently used entries no launch
 // holds until a first-fit block is free, then copies the tensor on the copy
-// stream, behind the last uses of every evicted block.
-void shard_load(mft_model_s* m, int i) {
+// stream, behind the last uses of every evicted block.  When nothing more can
+// be evicted, a prefetch returns false (the use will load it); a use throws.
+bool shard_load(mft_model_s* m, int i, bool prefetch = false) {
   ShardStore& sh = m->sh;
   const size_t need = shard_round(sh.ents[i].bytes);
   int64_t off;
@@ -466,7 +472,10 @@ void shard_load(mft_model_s* m, int i) {
       const ShardStore::Entry& c = sh.ents[j];
       if (j != i && c.off >= 0 && !c.held && (v < 0 || c.last < sh.ents[v].last)) v = j;
     }
-    if (v < 0) throw Error(MFT_EINVAL, "shard budget too small for the tensors one launch uses");
+    if (v < 0) {
+      if (prefetch) return false;
+      throw Error(MFT_EINVAL, "shard budget too small for the tensors one launch uses");
+    }
     ShardStore::Entry& ev = sh.ents[v];
     if (ev.used_valid) MFT_HIP(hipStreamWaitEvent(sh.copy, ev.used, 0));
     shard_free(sh, ev.off, (int64_t)shard_round(ev.bytes));
@@ -478,6 +487,7 @@ void shard_load(mft_model_s* m, int i) {
   MFT_HIP(hipEventRecord(e.ready, sh.copy));
   e.ready_valid = true;
   ++sh.loads;
+  return true;
 }
 
 // Device address of frozen parameter p for the next launch on the model's
@@ -494,6 +504,11 @@ struct WeightUse {
       return;
     }
     ShardStore& sh = m->sh;
+    if (sh.deferred_code) {  // a prefetch issued after an earlier use failed
+      const int code = sh.deferred_code;
+      sh.deferred_code = 0;
+      throw Error(code, "shard store prefetch failed: " + sh.deferred);
+    }
     ShardStore::Entry& e = sh.ents[i];
     e.held = true;
     e.last = ++sh.clock;
@@ -517,9 +532,17 @@ struct WeightUse {
       ShardStore::Entry& n = sh.ents[sh.prev[pos]];
       if (n.off < 0 && !n.held) {
         n.last = ++sh.clock;
+        // A budget that cannot hold it now makes the prefetch a no-op; any
+        // other failure (a HIP copy, event or wait error) is kept and thrown
+        // by the next use, since a destructor cannot throw.
         try {
-          shard_load(m, sh.prev[pos]);
-        } catch (...) {
+          (void)shard_load(m, sh.prev[pos], true);
+        } catch (const Error& err) {
+          sh.deferred_code = err.code;
+          sh.deferred = err.what();
+        } catch (const std::exception& err) {
+          sh.deferred_code = MFT_EHIP;
+          sh.deferred = err.what();
         }
       }
     }
@@ -784,6 +807,7 @@ void alloc_acts(mft_model_s* m) {
   m->d_drop_step = reinterpret_cast<int*>(static_cast<char*>(sc) + 2560);
   m->d_partials = reinterpret_cast<double*>(static_cast<char*>(sc) + 4096);
   MFT_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
+  register_stream(m->cap_stream);
   MFT_HIP(hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming));
   MFT_HIP(hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming));
 }
@@ -1734,6 +1758,8 @@ int mft_model_create(mft_model* out, const mft_model_cfg* cfg, int64_t max_token
     try {
       m->c = *cfg;
       m->stream = reinterpret_cast<hipStream_t>(stream);
+      register_stream(m->stream);
+      m->stream_registered = true;
       m->max_tokens = max_tokens;
       build_params(m);
       assign_dropout_streams(m);
@@ -1754,7 +1780,11 @@ int mft_model_destroy(mft_model m) {
     (void)hipStreamSynchronize(m->stream);
     if (m->cap_stream) (void)hipStreamSynchronize(m->cap_stream);
     drop_graph(m);
-    if (m->cap_stream) (void)hipStreamDestroy(m->cap_stream);
+    if (m->stream_registered) unregister_stream(m->stream);
+    if (m->cap_stream) {
+      unregister_stream(m->cap_stream);
+      (void)hipStreamDestroy(m->cap_stream);
+    }
     if (m->ev_in) (void)hipEventDestroy(m->ev_in);
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
@@ -1768,7 +1798,10 @@ int mft_model_destroy(mft_model m) {
       if (e.ready) (void)hipEventDestroy(e.ready);
       if (e.used) (void)hipEventDestroy(e.used);
     }
-    if (sh.copy) (void)hipStreamDestroy(sh.copy);
+    if (sh.copy) {
+      unregister_stream(sh.copy);
+      (void)hipStreamDestroy(sh.copy);
+    }
     if (sh.pool) (void)hipFree(sh.pool);
     if (sh.host) (void)hipHostFree(sh.host);
     delete m;

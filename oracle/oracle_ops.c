@@ -8,6 +8,7 @@
 #include <dlfcn.h>
 #include <math.h>
 #include <omp.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -340,12 +341,20 @@ void orc_attn_bwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
    * each unit keeps its own fp64 dK/dV partial [S, hd], summed afterwards
    * over the chunks and the heads of each GQA group in a fixed order (the
    * result does not depend on the thread count). */
-  const int QC = 64;
+  /* The partials take 16·B·Hq·nch·S·hd bytes: chunks of 64 queries, made
+   * longer (fewer partials) while that would exceed 1 GiB. */
+  const size_t part = (size_t)S * hd;
+  int QC = 64;
+  while (QC < S && (double)B * Hq * ((S + QC - 1) / QC) * part * 16.0 > (double)(1 << 30)) QC *= 2;
   const int nch = (S + QC - 1) / QC;
   const int64_t units = (int64_t)B * Hq * nch;
-  const size_t part = (size_t)S * hd;
   double* dKp = (double*)calloc((size_t)units * part, sizeof(double));
   double* dVp = (double*)calloc((size_t)units * part, sizeof(double));
+  if (!dKp || !dVp) {
+    fprintf(stderr, "orc_attn_bwd: cannot allocate %.2f GiB of fp64 dK/dV partials (B=%d Hq=%d S=%d hd=%d)\n",
+            2.0 * (double)units * part * 8.0 / (double)(1 << 30), B, Hq, S, hd);
+    abort();
+  }
 #pragma omp parallel
   {
     double* P = (double*)malloc(sizeof(double) * (size_t)S);

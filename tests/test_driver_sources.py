@@ -4,7 +4,13 @@ Qwen2.5 (WikiText) and Gemma-3 270M / 1B training programs.  Their data
 layer and tokenizers are outside this build; tests/driver_stubs declares the
 names those drivers use from them (WikiText2Dataset, WT2Config, the BPE and
 Gemma tokenizers) and nothing else.  g++ -fsyntax-only, CPU only; skipped
-where the reference tree is not present."""
+where the reference tree is not present.
+
+The link test goes one step further: each driver is compiled to an object
+and linked into an executable against libfinetune_ops.so, with the stub
+definitions of tests/driver_stubs/stub_defs.cpp (they throw if called) for
+the out-of-scope data layer and tokenizers, so a header declaration without
+a definition in the library fails the link."""
 import os
 import shutil
 import subprocess
@@ -31,5 +37,40 @@ def test_reference_driver_compiles_against_headers(src):
         pytest.skip(f"{src} not in the reference tree")
     r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
                         "-I", os.path.join(ROOT, "tests", "driver_stubs"), path],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+
+
+LIB_DIR = os.path.join(ROOT, "mobilefinetuner_amd")
+
+
+@pytest.fixture(scope="module")
+def stub_obj(tmp_path_factory):
+    out = str(tmp_path_factory.mktemp("stubs") / "stub_defs.o")
+    r = subprocess.run(["g++", "-std=c++17", "-c", "-fPIC", "-I", os.path.join(ROOT, "include"),
+                        "-I", os.path.join(ROOT, "tests", "driver_stubs"),
+                        os.path.join(ROOT, "tests", "driver_stubs", "stub_defs.cpp"), "-o", out],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    return out
+
+
+@pytest.mark.skipif(not os.path.isdir(REF), reason="reference tree not present")
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not installed")
+@pytest.mark.skipif(not os.path.exists(os.path.join(LIB_DIR, "libfinetune_ops.so")),
+                    reason="libfinetune_ops.so not built")
+@pytest.mark.parametrize("src", DRIVERS)
+def test_reference_driver_links_against_library(src, stub_obj, tmp_path):
+    path = os.path.join(REF, src)
+    if not os.path.exists(path):
+        pytest.skip(f"{src} not in the reference tree")
+    obj = str(tmp_path / "driver.o")
+    r = subprocess.run(["g++", "-std=c++17", "-c", "-I", os.path.join(ROOT, "include"),
+                        "-I", os.path.join(ROOT, "tests", "driver_stubs"), path, "-o", obj],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    exe = str(tmp_path / "driver")
+    r = subprocess.run(["g++", obj, stub_obj, "-o", exe, "-L", LIB_DIR, "-lfinetune_ops",
+                        "-Wl,-rpath-link," + LIB_DIR, "-Wl,-rpath-link,/opt/rocm/lib", "-Wl,--no-undefined"],
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-4000:]

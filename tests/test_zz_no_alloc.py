@@ -40,8 +40,10 @@ def _run(name, logits, labels, B, S, up, keep_nll):
 @pytest.mark.parametrize("keep_nll", [False, True])
 def test_noalloc_ce_equals_allocating_entry_point(keep_nll):
     rng = np.random.default_rng(31)
-    # second call smaller: stale scratch from the first must not leak into it
-    for B, S, V, up in ((4, 128, 50257, 1.0), (2, 33, 3001, 0.5)):
+    # each call smaller than the one before it in its pair: stale scratch must
+    # not leak into it; the last pair runs the maximum row count (65536, the
+    # separately counted targets) and then a count-in-row-workgroup batch
+    for B, S, V, up in ((4, 128, 50257, 1.0), (2, 33, 3001, 0.5), (16, 4096, 64, 1.0), (2, 1000, 77, 0.5)):
         print(f"ce noalloc B={B} S={S} V={V} keep_nll={keep_nll}", flush=True)
         logits = torch.from_numpy((rng.standard_normal((B * S, V)) * 2).astype(np.float32)).cuda()
         lab = rng.integers(0, V, (B, S)).astype(np.int32)
