@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <fstream>
 #include <functional>
 #include <map>
@@ -82,13 +83,114 @@ void Tensor::init_shape(std::vector<int64_t> shape, DType dtype, Device device) 
   pitch_ = shape_.empty() ? 1 : shape_.back();
 }
 
+// Device blocks of the tensors this library allocates come from a cache:
+// a freed block is kept on a free list of its rounded size and handed to the
+// next tensor of that size, instead of hipFree (which waits for the device)
+// and hipMalloc on every temporary of a training step (input ids, masks,
+// loss scalars, upstream gradients).  All of this library's work runs on the
+// null stream, in order, so a block reused by a later tensor is only touched
+// after the earlier tensor's queued work.  MemoryManager::clear_unused_memory
+// and force_cleanup return the cached blocks to the device.
+namespace {
+struct DevCache {
+  std::mutex mu;
+  std::unordered_map<size_t, std::vector<void*>> free;  // rounded bytes → blocks
+};
+DevCache& dev_cache() {
+  static DevCache* c = new DevCache();  // never destroyed: tensors may outlive static destruction
+  return *c;
+}
+size_t round_block(size_t b) {
+  if (b <= (size_t(1) << 20)) {
+    size_t r = 256;
+    while (r < b) r <<= 1;
+    return r;
+  }
+  const size_t g = size_t(2) << 20;
+  return (b + g - 1) / g * g;
+}
+void* dev_alloc(size_t bytes) {
+  const size_t rb = round_block(bytes);
+  {
+    DevCache& c = dev_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto it = c.free.find(rb);
+    if (it != c.free.end() && !it->second.empty()) {
+      void* p = it->second.back();
+      it->second.pop_back();
+      return p;
+    }
+  }
+  void* p = nullptr;
+  hip_check(hipMalloc(&p, rb), "hipMalloc");
+  return p;
+}
+void dev_release(void* p, size_t bytes) {
+  DevCache& c = dev_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.free[round_block(bytes)].push_back(p);
+}
+void dev_cache_clear() {
+  DevCache& c = dev_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  for (auto& e : c.free)
+    for (void* p : e.second) (void)hipFree(p);
+  c.free.clear();
+}
+}  // namespace
+
+// Host data of small tensors (token ids, masks, labels, scalars) goes to
+// the device through a ring of pinned staging slots with asynchronous copies
+// on the null stream, so building a step's inputs does not wait for the
+// device; a slot is reused once its previous copy has completed.
+namespace {
+struct StageRing {
+  static constexpr int kSlots = 64;
+  static constexpr size_t kSlotBytes = size_t(64) << 10;
+  std::mutex mu;
+  char* host = nullptr;
+  hipEvent_t ev[kSlots] = {};
+  bool used[kSlots] = {};
+  int next = 0;
+};
+StageRing& stage_ring() {
+  static StageRing* r = new StageRing();  // never destroyed (outlives static destruction)
+  return *r;
+}
+// Copies `bytes` (≤ kSlotBytes) from host memory to dst asynchronously;
+// false when the staging ring cannot be set up (the caller copies directly).
+bool stage_upload(void* dst, const void* src, size_t bytes) {
+  StageRing& r = stage_ring();
+  if (bytes > StageRing::kSlotBytes) return false;
+  std::lock_guard<std::mutex> lock(r.mu);
+  if (!r.host) {
+    if (hipHostMalloc(reinterpret_cast<void**>(&r.host), StageRing::kSlots * StageRing::kSlotBytes,
+                      hipHostMallocDefault) != hipSuccess) {
+      r.host = nullptr;
+      return false;
+    }
+    for (auto& e : r.ev) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+  }
+  const int i = r.next;
+  r.next = (r.next + 1) % StageRing::kSlots;
+  if (r.used[i]) hip_check(hipEventSynchronize(r.ev[i]), "hipEventSynchronize");
+  char* slot = r.host + (size_t)i * StageRing::kSlotBytes;
+  std::memcpy(slot, src, bytes);
+  hip_check(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, nullptr), "hipMemcpyAsync H2D");
+  hip_check(hipEventRecord(r.ev[i], nullptr), "hipEventRecord");
+  r.used[i] = true;
+  return true;
+}
+}  // namespace
+
 Tensor::Tensor(std::vector<int64_t> shape, DType dtype, Device device) {
   init_shape(std::move(shape), dtype, device);
   const size_t bytes = (size_t)numel_ * dtype_size(dtype_);
   if (bytes) {
-    hip_check(hipMalloc(&dev_, bytes), "hipMalloc");
+    dev_ = dev_alloc(bytes);
     owns_ = true;
-    hip_check(hipMemset(dev_, 0, bytes), "hipMemset");
+    hip_check(hipMemsetAsync(dev_, 0, bytes, nullptr), "hipMemsetAsync");
   }
 }
 
@@ -97,9 +199,16 @@ Tensor::Tensor(std::vector<int64_t> shape, const void* data, DType dtype, Device
   const size_t bytes = (size_t)numel_ * dtype_size(dtype_);
   if (bytes) {
     if (!data) throw std::invalid_argument("Tensor: null data");
-    hip_check(hipMalloc(&dev_, bytes), "hipMalloc");
+    dev_ = dev_alloc(bytes);
     owns_ = true;
-    hip_check(hipMemcpy(dev_, data, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    if (stage_upload(dev_, data, bytes)) {
+      // small host-built tensors keep their host copy: the host checks of
+      // ids and labels (check_ids, check_labels) then read no device memory
+      host_.assign(static_cast<const char*>(data), static_cast<const char*>(data) + bytes);
+      host_state_ = 1;
+    } else {
+      hip_check(hipMemcpy(dev_, data, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    }
   }
 }
 
@@ -116,22 +225,39 @@ TensorPtr Tensor::view(std::vector<int64_t> shape, DType dtype, void* device_ptr
 }
 
 Tensor::~Tensor() {
-  if (owns_ && dev_) (void)hipFree(dev_);
+  if (owns_ && dev_) dev_release(dev_, (size_t)numel_ * dtype_size(dtype_));
 }
 
 struct MirrorGroup {
   char* dev = nullptr;
   size_t bytes = 0;
-  std::vector<char> host;
-  int state = 0;    // 0 = stale, 1 = equal to the device, 2 = newer than the device
+  // Host copy in pinned memory (allocated at the first host access): the
+  // drivers' per-step gradient reads and writes move at DMA rate, and a copy
+  // can be queued behind the kernels that produce the data.
+  char* host = nullptr;
+  hipEvent_t arrive = nullptr;  // end of the queued device→host copy (state 3)
+  // 0 = stale, 1 = equal to the device, 2 = newer than the device,
+  // 3 = a device→host copy is queued (equal to the device once `arrive` fires)
+  int state = 0;
   int members = 0;  // views created in the group
   // zero_grad() requests not yet applied on the device: byte offset → bytes.
   // They run at the group's next device or host access, as one fill over the
   // whole range when every member asked (the drivers' zero_grad loop).
   std::map<size_t, size_t> zeros;
+  ~MirrorGroup() {
+    if (arrive) (void)hipEventDestroy(arrive);
+    if (host) (void)hipHostFree(host);
+  }
 };
 
 namespace {
+void ensure_host(MirrorGroup& g) {
+  if (g.host || g.bytes == 0) return;
+  hip_check(hipHostMalloc(reinterpret_cast<void**>(&g.host), g.bytes, hipHostMallocDefault), "hipHostMalloc");
+  std::memset(g.host, 0, g.bytes);
+  g.state = 0;
+}
+
 void flush_zeros(MirrorGroup& g) {
   if (g.zeros.empty()) return;
   if ((int)g.zeros.size() == g.members) {
@@ -145,6 +271,25 @@ void flush_zeros(MirrorGroup& g) {
   g.state = 0;
 }
 }  // namespace
+
+namespace detail {
+// Queues the copy of t's mirror group into its pinned host buffer behind the
+// work already on the stream (the engine's backward), so a host read that
+// follows waits for the kernels only, not for a copy started after them.
+// Groupless tensors are left alone.
+void prefetch_host(const TensorPtr& t) {
+  if (!t || !t->mirror()) return;
+  MirrorGroup& g = *t->mirror();
+  flush_zeros(g);
+  ensure_host(g);
+  if (g.state != 0 || g.bytes == 0) return;  // already equal, newer on the host, or queued
+  if (!g.arrive) hip_check(hipEventCreateWithFlags(&g.arrive, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipMemcpyAsync(g.host, g.dev, g.bytes, hipMemcpyDeviceToHost, nullptr), "hipMemcpyAsync D2H");
+  hip_check(hipEventRecord(g.arrive, nullptr), "hipEventRecord");
+  g.state = 3;
+}
+
+}  // namespace detail
 
 std::shared_ptr<MirrorGroup> Tensor::mirror_group(void* base, size_t bytes) {
   auto g = std::make_shared<MirrorGroup>();
@@ -168,18 +313,19 @@ TensorPtr Tensor::view(std::vector<int64_t> shape, DType dtype, void* device_ptr
   return t;
 }
 
-char* Tensor::host_ptr() const { return group_ ? group_->host.data() + group_off_ : host_.data(); }
+char* Tensor::host_ptr() const { return group_ ? group_->host + group_off_ : host_.data(); }
 
 void Tensor::sync_host(bool will_write) const {
   if (group_) {
     MirrorGroup& g = *group_;
     flush_zeros(g);
-    if (g.host.size() != g.bytes) {
-      g.host.assign(g.bytes, 0);
-      g.state = 0;
+    ensure_host(g);
+    if (g.state == 3) {
+      hip_check(hipEventSynchronize(g.arrive), "hipEventSynchronize");
+      g.state = 1;
     }
     if (g.state == 0 && g.bytes > 0) {
-      hip_check(hipMemcpy(g.host.data(), g.dev, g.bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+      hip_check(hipMemcpy(g.host, g.dev, g.bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
       g.state = 1;
     }
     if (will_write) g.state = 2;
@@ -207,7 +353,7 @@ void Tensor::upload_if_dirty() const {
   if (group_) {
     flush_zeros(*group_);
     if (group_->state == 2) {
-      hip_check(hipMemcpy(group_->dev, group_->host.data(), group_->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+      hip_check(hipMemcpy(group_->dev, group_->host, group_->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
       group_->state = 1;
     }
     return;
@@ -246,7 +392,13 @@ void Tensor::zero_grad() {
   if (grad_->dtype() != kFloat32) throw std::runtime_error("zero_grad: float32 gradients only");
   if (!grad_->contiguous()) throw std::runtime_error("zero_grad: strided gradient");
   if (const auto& g = grad_->group_) {  // deferred: one fill for the whole group when every member asks
-    grad_->upload_if_dirty();           // host edits of other members reach the device first
+    // host edits of other members reach the device first (without applying
+    // the zero requests already pending: those wait for the rest of the
+    // group, so the drivers' zero_grad loop costs one fill)
+    if (g->state == 2) {
+      hip_check(hipMemcpy(g->dev, g->host, g->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+      g->state = 1;
+    }
     g->zeros[grad_->group_off_] = (size_t)grad_->numel() * 4;
     g->state = 0;
     return;
@@ -939,8 +1091,8 @@ MemoryManager& MemoryManager::instance() {
   return m;
 }
 
-void MemoryManager::force_cleanup() { hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
-void MemoryManager::clear_unused_memory() { force_cleanup(); }
+void MemoryManager::force_cleanup() { dev_cache_clear(); }
+void MemoryManager::clear_unused_memory() { dev_cache_clear(); }
 void MemoryManager::cleanup_dead_references() {}
 
 void MemoryManager::print_memory_stats() const {

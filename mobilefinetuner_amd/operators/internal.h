@@ -16,6 +16,9 @@ void hip_check(hipError_t e, const char* what);
 void mft_check(int rc, const char* what);
 mft_handle handle();
 float read_scalar(const TensorPtr& t);
+// Queues a device→host copy of t's mirror group behind the stream's work
+// (the engine backward's gradients, read by the drivers' clip loop next).
+void prefetch_host(const TensorPtr& t);
 TensorPtr make_loss(double loss_sum, int64_t n_valid, bool sum);
 bool parse_reduction(const std::string& r);
 

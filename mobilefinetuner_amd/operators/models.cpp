@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <fstream>
 #include <random>
 #include <sstream>
@@ -73,8 +74,11 @@ void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int 
   mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
                          reinterpret_cast<double*>(p), reinterpret_cast<int64_t*>(p + 8)),
             "mft_model_ce");
-  hip_check(hipMemcpy(ls, p, 8, hipMemcpyDeviceToHost), "hipMemcpy D2H");
-  hip_check(hipMemcpy(nv, p + 8, 8, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  if (!ls && !nv) return;
+  char buf[16];  // loss sum and count are adjacent: one read-back
+  hip_check(hipMemcpy(buf, p, 16, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  if (ls) std::memcpy(ls, buf, 8);
+  if (nv) std::memcpy(nv, buf + 8, 8);
 }
 
 // loss = lm_cross_entropy(model.forward(...)); its backward turns the
@@ -92,9 +96,7 @@ struct ModelLossNode : autograd::Node {
     if (st->generation != ctx.generation)
       throw std::runtime_error("backward: the model ran another forward since this loss was computed");
     const float up = detail::read_scalar(g);
-    double ls;
-    int64_t nv;
-    model_ce(st.get(), ctx, labels, ignore, up, sum, true, &ls, &nv);
+    model_ce(st.get(), ctx, labels, ignore, up, sum, true, nullptr, nullptr);  // the loss was read at the forward
     // logits->retain_grad(): the gradient the CE just wrote over the logits
     // buffer is copied out before the backward consumes it
     if (auto lg = logits.lock())
@@ -116,6 +118,13 @@ struct ModelLossNode : autograd::Node {
               "mft_model_backward");
     for (auto& w : st->grad_views)
       if (auto gv = w.lock()) gv->mark_device_written();
+    // the drivers read the gradients next (their clip loop): queue the copy
+    // to the host now, behind the backward
+    for (auto& w : st->grad_views)
+      if (auto gv = w.lock()) {
+        detail::prefetch_host(gv);
+        break;  // one group holds them all
+      }
     return {};
   }
 };
