@@ -57,8 +57,12 @@ struct GemmaTrainerConfig {
   float max_grad_norm = 1.0f;
   float weight_decay = 0.0f;
   float adam_beta1 = 0.9f, adam_beta2 = 0.999f, adam_eps = 1e-8f;
-  // Embedding dumps of the reference's debugging aids; accepted, not written
-  // (the embedding is frozen, so every dump would be the loaded table).
+  // Embedding dump (gemma_3_270m_lora_finetune/src/main.cpp:205-207,
+  // 283-284, 688-690): at step dump_embedding_step (1-indexed) the trainer
+  // writes the first micro-batch's scaled token embeddings (the model's
+  // hidden_states_emb, [B, S, hidden], a leading 1 dropped) and its token ids
+  // as embedding_step<N>.npy and input_ids_step<N>.npy into
+  // dump_embedding_dir ("./debug" when empty).
   bool dump_embedding = false;
   int dump_embedding_step = 1;
   std::string dump_embedding_dir;
@@ -122,6 +126,7 @@ class GemmaLoRATrainer {
   const std::vector<TrainerStepLog>& history() const { return history_; }
 
  private:
+  void dump_embedding_output(int step, const TrainerBatch& b);
   GemmaModel& model_;
   GemmaLoraInjector& injector_;
   std::unique_ptr<BatchSource> train_, eval_;

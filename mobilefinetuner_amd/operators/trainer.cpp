@@ -75,6 +75,22 @@ float GemmaLoRATrainer::lr_at(int step) const {
   return (float)(base * (1.0 - progress));
 }
 
+void GemmaLoRATrainer::dump_embedding_output(int step, const TrainerBatch& b) {
+  const std::string dir = cfg_.dump_embedding_dir.empty() ? std::string("./debug") : cfg_.dump_embedding_dir;
+  auto acts = model_.debug_tensors();
+  auto it = acts.find("hidden_states_emb");
+  if (it == acts.end() || !it->second) throw std::runtime_error("dump_embedding: the model kept no embedding output");
+  const TensorPtr& e = it->second;
+  std::vector<int64_t> shp = e->shape();
+  if (!shp.empty() && shp[0] == 1) shp.erase(shp.begin());
+  const std::string tag = "_step" + std::to_string(step) + ".npy";
+  detail::write_npy(dir + "/embedding" + tag, static_cast<const Tensor&>(*e).data<float>(), shp, false);
+  std::vector<int64_t> ishp = b.input_ids->shape();
+  if (!ishp.empty() && ishp[0] == 1) ishp.erase(ishp.begin());
+  detail::write_npy(dir + "/input_ids" + tag, static_cast<const Tensor&>(*b.input_ids).data<int32_t>(), ishp, true);
+  std::printf("[Trainer] step %d: embedding dump written to %s\n", step, dir.c_str());
+}
+
 void GemmaLoRATrainer::train() {
   auto params = model_.get_lora_parameters();
   if (params.empty()) throw std::runtime_error("GemmaLoRATrainer::train: the model has no LoRA adapters (inject first)");
@@ -101,6 +117,7 @@ void GemmaLoRATrainer::train() {
       TrainerBatch b = train_->next_batch(cfg_.micro_batch_size, true);
       if (!b.input_ids) throw std::runtime_error("GemmaLoRATrainer::train: the training data yielded no batch");
       auto logits = model_.forward(b.input_ids, b.attention_mask);
+      if (cfg_.dump_embedding && step == cfg_.dump_embedding_step && a == 0) dump_embedding_output(step, b);
       auto loss = lm_cross_entropy(logits, b.labels, -100, "mean");
       loss_sum += loss->data<float>()[0];
       mul(loss, 1.0f / (float)accum)->backward();

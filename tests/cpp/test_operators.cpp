@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <iterator>
 #include <fstream>
 #include <cstdio>
 #include <cstring>
@@ -42,6 +43,28 @@
 using namespace ops;
 
 static int g_fail = 0;
+
+// Minimal .npy (format 1.0, little-endian) readers for the dumps the API writes.
+static std::vector<char> npy_payload(const std::string& path) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) return {};
+  std::vector<char> all((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+  if (all.size() < 10) return {};
+  const size_t hlen = (size_t)(unsigned char)all[8] | ((size_t)(unsigned char)all[9] << 8);
+  return std::vector<char>(all.begin() + 10 + (std::ptrdiff_t)hlen, all.end());
+}
+static std::vector<float> read_npy_f32(const std::string& path) {
+  const auto p = npy_payload(path);
+  std::vector<float> v(p.size() / 4);
+  std::memcpy(v.data(), p.data(), v.size() * 4);
+  return v;
+}
+static std::vector<int32_t> read_npy_i32(const std::string& path) {
+  const auto p = npy_payload(path);
+  std::vector<int32_t> v(p.size() / 4);
+  std::memcpy(v.data(), p.data(), v.size() * 4);
+  return v;
+}
 
 static double rel_l2(const float* a, const float* b, int64_t n) {
   double num = 0, den = 0;
@@ -575,6 +598,9 @@ static void test_gemma_trainer() {
   tc.eval_steps = 3;
   tc.eval_batches = 2;
   tc.output_dir = "/tmp/mft_trainer_test";
+  tc.dump_embedding = true;  // step 2's first micro-batch
+  tc.dump_embedding_step = 2;
+  tc.dump_embedding_dir = tc.output_dir + "/emb";
   GemmaLoRATrainer trainer(model, injector, train, eval, tc);
   check("gemma trainer total steps", std::abs(trainer.total_steps() - 3), 0);
   check("gemma trainer warmup steps", std::abs(trainer.warmup_steps() - 1), 0);
@@ -610,6 +636,27 @@ static void test_gemma_trainer() {
     want.insert(want.end(), o, o + t->numel());
   }
   check("gemma trainer LoRA params after 3 steps", rel_l2(got.data(), want.data(), (int64_t)got.size()), 1e-5);
+  {
+    // the embedding dump of step 2: sequences 4 and 5 of the stream (steps
+    // take 2 micro-batches of 2), each row wte[id]·√hidden (HF Gemma3's
+    // scaled embedding; the table is frozen, so it is the initial one)
+    SyntheticLM again(10, 5);
+    (void)again.take(4, true);
+    const std::vector<int32_t> ids = again.take(2, true);
+    const std::vector<float> emb = read_npy_f32(tc.dump_embedding_dir + "/embedding_step2.npy");
+    const std::vector<int32_t> got_ids = read_npy_i32(tc.dump_embedding_dir + "/input_ids_step2.npy");
+    const int d = cfg.hidden_size;
+    auto wte = model.get_parameter("embed_tokens.weight");
+    const float* w = static_cast<const Tensor&>(*wte).data<float>();
+    const float sc = std::sqrt((float)d);
+    std::vector<float> want_e(ids.size() * (size_t)d);
+    for (size_t r = 0; r < ids.size(); ++r)
+      for (int c = 0; c < d; ++c) want_e[r * d + c] = w[(size_t)ids[r] * d + c] * sc;
+    check("gemma trainer embedding dump ids", got_ids == ids ? 0.0 : 1.0, 0);
+    check("gemma trainer embedding dump size", std::abs((double)emb.size() - (double)want_e.size()), 0);
+    if (emb.size() == want_e.size())
+      check("gemma trainer embedding dump values", rel_l2(emb.data(), want_e.data(), (int64_t)emb.size()), 0);
+  }
   trainer.save_lora(tc.output_dir + "/gemma_lora.safetensors");
   std::ifstream saved(tc.output_dir + "/gemma_lora.safetensors", std::ios::binary);
   check("gemma trainer adapter written", saved.good() ? 0.0 : 1.0, 0);
