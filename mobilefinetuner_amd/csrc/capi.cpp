@@ -221,7 +221,7 @@ int mft_lora_linear_fwd(mft_handle h, const float* x, int64_t M, int64_t K,
     if (M <= 0 || K <= 0 || N <= 0) throw mft::Error(MFT_EINVAL, "mft_lora_linear_fwd: empty shape");
     if (w_dtype != MFT_F32 && w_dtype != MFT_F16) throw mft::Error(MFT_EINVAL, "bad w_dtype");
     if ((A == nullptr) != (B == nullptr)) throw mft::Error(MFT_EINVAL, "A and B must both be set or both NULL");
-    const size_t ws = (size_t)16 * M * N * sizeof(float);
+    const size_t ws = (size_t)16 * M * N * sizeof(float) + (size_t)M * sizeof(float) + 512;
     mft::Scratch s{reinterpret_cast<float*>(scratch(h, ws)), ws};
     mft::lora_linear_fwd(h->stream, x, M, K, W, w_dtype == MFT_F16, N, bias, A, B, A ? r : 0, scale,
                          y, xa, resid, s);
@@ -239,7 +239,7 @@ int mft_lora_linear_bwd(mft_handle h, const float* dy, const float* x,
     if (w_dtype != MFT_F32 && w_dtype != MFT_F16) throw mft::Error(MFT_EINVAL, "bad w_dtype");
     if ((A == nullptr) != (B == nullptr)) throw mft::Error(MFT_EINVAL, "A and B must both be set or both NULL");
     const size_t ws = mft::lora_bwd_scratch_floats(M, K, N, A ? r : 0) * sizeof(float) +
-                      (size_t)16 * M * K * sizeof(float);
+                      (size_t)16 * M * K * sizeof(float) + (size_t)M * sizeof(float) + 512;
     mft::Scratch s{reinterpret_cast<float*>(scratch(h, ws)), ws};
     mft::lora_linear_bwd(h->stream, dy, x, W, w_dtype == MFT_F16, A, B, xa, M, K, N, A ? r : 0, scale,
                          dx, dA, dB, accumulate != 0, dx_accumulate != 0, s);

@@ -173,6 +173,18 @@ struct GemmEpilogue {
   // Host-side only: row norm of the finished output (never read by kernels).
   const RowNorm* norm = nullptr;
 };
+// Row scales of an fp32 operand x [M,K] for the fp16 matrix-core GEMM:
+// inv_s[m] = 2^(⌊log2 max|x_m|⌋ − 14) (1 for a zero or non-finite maximum;
+// at most 2^126 below), so that x_m/inv_s[m] splits into two fp16 values per
+// element without leaving fp16's range.
+__device__ __forceinline__ float row_inv_scale(float mx) {
+  int e = 0;
+  if (mx > 0.f && mx <= 3.402823466e38f) e = min(14 - ilogbf(mx), 126);  // ilogb ≤ 127: e ≥ −113
+  return __int_as_float((127 - e) << 23);
+}
+void row_scales(hipStream_t s, const float* x, int64_t ldx, int M, int K, float* inv_s);
+// Shapes gemm_h takes (K in whole 32-deep panels; 8-wide column chunks of a [K,N] B).
+bool gemm_h_ok(int N, int K, bool b_nk, int r);
 // Whether gemm() runs an M×N×K product (the LM head's logits) on the
 // 128×128 kernel, the one that can emit row statistics.
 bool gemm_wide_plan(int M, int N);
@@ -220,6 +232,17 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B,
           int64_t ldb, bool b_nk, bool b_f16, float* C, int64_t ldc, int M,
           int N, int K, const GemmEpilogue& ep, Scratch ws = Scratch(),
           const KernelEvents* ev = nullptr);
+// C[M,N] = A·op(B) (+ epilogue, as gemm()) on the fp16 matrix cores: A fp32
+// with its row scales (row_scales; null: rows used unscaled), split into two
+// fp16 values per element in the tile load; B fp16 [N,K] (b_nk) or [K,N].
+void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, const uint16_t* B, int64_t ldb, bool b_nk,
+            float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws = Scratch(),
+            const KernelEvents* ev = nullptr);
+// C = x·op(W) for fp16 W: row_scales into the front of ws, then gemm_h.
+// Returns false (nothing launched) when the shape, alignment or workspace
+// does not fit; the caller then runs gemm() with W widened.
+bool gemm_f16w(hipStream_t s, const float* x, int64_t ldx, const void* W, int64_t ldw, bool b_nk, float* C,
+               int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws, const KernelEvents* ev = nullptr);
 // out[M,r] = X[M,K] · Y with Y(k,j) = Y[k*ysk + j*ysj]
 void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y,
                int64_t ysk, int64_t ysj, int M, int K, int r, float* out);
@@ -267,6 +290,7 @@ struct RankJob {
   float* out;
   int64_t osj, osc;
   float scale;
+  float* inv_s;  // projection: when set, also the row scales of X (row_scales) for the fp16 GEMM
 };
 int rank_outer_blocks(int C);
 // Runs jobs[0, njobs) (the first nproj are projections) over M rows.

@@ -58,6 +58,10 @@ struct Linear {
   // gradient group); -1 when another linear of the group runs it
   int xa_batch = -1, u_batch = -1;
   float* u = nullptr;  // U = dY·B of this linear (panel path)
+  // row scales of this linear's GEMM input (x forward, dY backward) for the
+  // fp16 matrix-core GEMM, written by the batched rank-r launches (panel path)
+  const float* rs_fwd = nullptr;
+  const float* rs_bwd = nullptr;
 };
 
 
@@ -191,6 +195,11 @@ struct mft_model_s {
   // input / gradient group of a layer (q|k|v, o, gate|up, down); dB and dA
   // from two whole-model launches at the end of the backward.
   bool panel = false;
+  // Row scales for the fp16 matrix-core GEMMs of fp16-stored W: one
+  // [max_tokens] slot per linear of a layer (written by the batched rank-r
+  // launches, read by the GEMMs that follow them), then one for GEMMs whose
+  // input no batched launch reads.
+  float* rscale = nullptr;
   void* weff_mem = nullptr;
   void* tables = nullptr;  // device: MergeJob[n_merge], then RankJob[]
   const MergeJob* d_merge = nullptr;
@@ -913,9 +922,19 @@ void build_lora_tables(mft_model_s* m) {
           if (l.A < 0 || group(t) != g) continue;
           if (first < 0) first = t;
           const int64_t dld = a.dy_ld[t];
-          gx.push_back(proj_job(lora_x(m, li, t), l.K, l.K, static_cast<const float*>(m->P[l.A].data), true,
-                                a.xa[t]));
-          gu.push_back(proj_job(a.DY[t], dld, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]));
+          // with fp16 W: the group's first projection also writes the row
+          // scales of the shared input, every dY projection those of its dY
+          float* slot_f = m->rscale ? m->rscale + (int64_t)first * m->max_tokens : nullptr;
+          float* slot_b = m->rscale ? m->rscale + (int64_t)t * m->max_tokens : nullptr;
+          RankJob jx = proj_job(lora_x(m, li, t), l.K, l.K, static_cast<const float*>(m->P[l.A].data), true,
+                                a.xa[t]);
+          if (t == first) jx.inv_s = slot_f;
+          gx.push_back(jx);
+          RankJob ju = proj_job(a.DY[t], dld, l.N, static_cast<const float*>(m->P[l.B].data), false, a.U[t]);
+          ju.inv_s = slot_b;
+          gu.push_back(ju);
+          l.rs_fwd = slot_f;
+          l.rs_bwd = slot_b;
           db_jobs.push_back(outer_job(a.xa[t], a.DY[t], dld, l.N, m->P[l.B].grad, 1, r));
           da_jobs.push_back(outer_job(a.U[t], lora_x(m, li, t), l.K, l.K, m->P[l.A].grad, l.K, 1));
         }
@@ -987,6 +1006,14 @@ void build_lora_tables(mft_model_s* m) {
   for (auto& p : pend) m->batches.push_back({d_rank + p.off, p.njobs, p.nproj, p.outer_blocks, p.work});
   m->merged = !panel;
   m->panel = panel;
+}
+
+// Row-scale slots for the fp16 matrix-core GEMMs (models with fp16-stored W).
+void alloc_row_scales(mft_model_s* m) {
+  bool any_f16 = false;
+  for (const Param& p : m->P) any_f16 = any_f16 || p.f16;
+  if (any_f16 && hipMalloc(&m->rscale, (size_t)(T_MAX + 1) * m->max_tokens * sizeof(float)) != hipSuccess)
+    throw Error(MFT_ENOMEM, "row scales");
 }
 
 // ---- timing helpers -------------------------------------------------------------
@@ -1065,6 +1092,34 @@ DropStream drop_stream(const mft_model_s* m) {
 
 void run_batch(mft_model_s* m, int idx, int64_t M);
 
+// C = x·op(W) (+ epilogue) for a linear's frozen W.  fp16-stored W runs on
+// the fp16 matrix cores with x's row scales from inv_s (written by the
+// batched rank-r launch that read x) or, when null, from a row_scales launch
+// timed with the linear class.  Tuning hook: MFT_GEMM_F16=0 keeps fp16 W on
+// the fp32 kernels (widened in the tile load).
+void lin_gemm(mft_model_s* m, const float* x, int64_t ldx, const Param& W, const void* wptr, int64_t ldw, bool b_nk,
+              float* C, int64_t ldc, int64_t M, int N, int K, const GemmEpilogue& ep, Scratch ws,
+              const KernelEvents* ev, const float* inv_s) {
+  static const int f16_mode = [] {
+    const char* e = getenv("MFT_GEMM_F16");
+    return e ? atoi(e) : 1;
+  }();
+  if (W.f16 && f16_mode && m->rscale && gemm_h_ok(N, K, b_nk, ep.r) && ldx % 4 == 0 && ldx >= K &&
+      ((uintptr_t)x & 15) == 0 && ldw % 8 == 0 && ((uintptr_t)wptr & 15) == 0) {
+    if (!inv_s) {
+      float* slot = m->rscale + (int64_t)T_MAX * m->max_tokens;
+      Timed ts(m, CLS_LINEAR, 0.0);
+      ts.begin();
+      row_scales(m->stream, x, ldx, (int)M, K, slot);
+      ts.end();
+      inv_s = slot;
+    }
+    gemm_h(m->stream, x, ldx, inv_s, static_cast<const uint16_t*>(wptr), ldw, b_nk, C, ldc, (int)M, N, K, ep, ws, ev);
+    return;
+  }
+  gemm(m->stream, x, ldx, wptr, ldw, b_nk, W.f16, C, ldc, (int)M, N, K, ep, ws, ev);
+}
+
 // y = x·W (+ LoRA) + bias (+ resid); with gelu_out, y keeps the
 // pre-activation and gelu_out receives GELU(y) (GPT-2 c_fc).
 void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* y, float* xa,
@@ -1092,7 +1147,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     ep.qsj = 1;
     ep.lscale = lscale(m);
     Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
-    gemm(m->stream, x, l.K, wu.ptr, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+    lin_gemm(m, x, l.K, W, wu.ptr, l.N, false, y, l.N, M, l.N, l.K, ep, m->ws, t.events(), l.rs_fwd);
     return;
   }
   if (lora) {
@@ -1114,7 +1169,7 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
     ep.lscale = lscale(m);
   }
   Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.N * r);
-  gemm(m->stream, x, l.K, wu.ptr, l.N, false, W.f16, y, l.N, (int)M, l.N, l.K, ep, m->ws, t.events());
+  lin_gemm(m, x, l.K, W, wu.ptr, l.N, false, y, l.N, M, l.N, l.K, ep, m->ws, t.events(), nullptr);
 }
 
 // dx = dy·Wᵀ (+ LoRA) (+ beta·dx); with gelu_grad_of = the pre-activation
@@ -1152,7 +1207,7 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
       ep.qsj = l.K;
       ep.lscale = lscale(m);
       Timed t(m, CLS_LINEAR, 2.0 * M * l.N * l.K + 2.0 * M * l.K * r);
-      gemm(m->stream, dy, l.N, wu.ptr, l.N, true, W.f16, dx, l.K, (int)M, l.K, l.N, ep, m->ws, t.events());
+      lin_gemm(m, dy, l.N, W, wu.ptr, l.N, true, dx, l.K, M, l.K, l.N, ep, m->ws, t.events(), l.rs_bwd);
     }
     return;
   }
@@ -1765,6 +1820,7 @@ int mft_model_create(mft_model* out, const mft_model_cfg* cfg, int64_t max_token
       assign_dropout_streams(m);
       alloc_params(m);
       alloc_acts(m);
+      alloc_row_scales(m);
       build_lora_tables(m);
     } catch (...) {
       mft_model_destroy(m);
@@ -1789,7 +1845,7 @@ int mft_model_destroy(mft_model m) {
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
     void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss,
-                    m->weff_mem, m->tables};
+                    m->weff_mem, m->tables, m->rscale};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     ShardStore& sh = m->sh;

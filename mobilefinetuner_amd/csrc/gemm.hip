@@ -97,7 +97,8 @@ __device__ __forceinline__ float2 row_stats64(const float* row) {
 // every slice over every XCD would fetch the whole of A into each of the 8
 // L2s).  With `spread` (used for s > 8) every K-slice covers all 8 XCDs.
 // Host side: tiles_per_xcd = ceil(tiles / (8/s)), or ceil(tiles/8) spread.
-__device__ __forceinline__ bool tile_of(const GemmParams& p, int& tile, int& split) {
+template <class Params>
+__device__ __forceinline__ bool tile_of(const Params& p, int& tile, int& split) {
   const int L = blockIdx.x, xcd = L % 8, idx = L / 8;
   const int tiles = p.tiles_m * p.tiles_n;
   if (p.spread) {
@@ -1092,6 +1093,322 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// ---- fp16 matrix-core path ---------------------------------------------------
+// Frozen W stored as fp16 is exact in fp16, so y = x·W can run on the fp16
+// matrix cores (v_mfma_f32_16x16x32_f16: 8× the fp32 MFMA rate) once the fp32
+// operand x is carried by two fp16 values.  Row m of x is scaled by
+// s_m = 2^(14 − ⌊log2 max|x_m|⌋), so that max|x_m·s_m| ∈ [2^14, 2^15) sits
+// inside fp16's range, and split into hi = fp16(x·s) and lo = fp16(x·s − hi),
+// both rounded to nearest even (x·s and x·s − hi are exact in fp32).  The
+// pair keeps x·s to within 2^-22·|x·s| (or 2^-25 absolute where lo is
+// subnormal, far below the row maximum): 22 of fp32's 24 significand bits.
+// Products of fp16 values are exact in fp32 and the matrix cores accumulate
+// in fp32, so diag(1/s)·(hi·W + lo·W) differs from the fp32 product by a few
+// units of 2^-22 relative.  The GEMM splits its A tiles while staging them
+// into LDS; the row scales come from a pass that already reads every row
+// (the rank-r projections of the LoRA branch, rank_batch) or from
+// row_scale_kernel.  inv_s[m] = 1/s_m is a power of two.
+// inv_s[m] of rows x[m, 0:K) (K a multiple of 4), one workgroup per row.
+// fmaxf drops NaN operands; NaN and ±inf entries pass through the split
+// unchanged (their rows' products are NaN / inf as in fp32).
+__global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ x, int64_t ldx, int K,
+                                                        float* __restrict__ inv_s) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const float* xr = x + (int64_t)m * ldx;
+  float mx = 0.f;
+  for (int k = 4 * tid; k < K; k += 1024) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(xr + k);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  if (tid == 0) inv_s[m] = row_inv_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+
+struct GemmHParams {
+  const float* A;      // fp32 [M][lda]
+  const float* inv_s;  // [M] row scales 1/s_m (powers of two), or null (s = 1)
+  const uint16_t* B;   // fp16 [N][ldb] (B_NK) or [K][ldb]
+  float* C;
+  int64_t lda, ldb, ldc;
+  int M, N, K;
+  int k_chunk;
+  int tiles_m, tiles_n, tiles_per_xcd;
+  int splits, spread;
+  float* partial;
+  GemmEpilogue ep;
+};
+
+// C = diag(inv_s)·(hi + lo)·op(B) (+ the rank-r panel and epilogue of
+// gemm_p_kernel), hi/lo the fp16 split of diag(s)·A made while A's fp32
+// panel is staged into LDS.  Workgroup tile BM×BN, four waves as 2×2, each
+// owning (BM/2)×(BN/2) outputs as 16×16 tiles; K in panels of 32 (one
+// v_mfma_f32_16x16x32_f16 k-block: lane l holds row l%16, k 8(l/16)..+7 of
+// each operand).  LDS per stage: the hi and lo A planes [BM][32] and B as
+// [BN][32] (B_NK) or [32][BN] (k-major, as W [K,N] is stored): k-major B
+// fragments come out of LDS through ds_read_b64_tr_b16, which hands lane
+// 4a+e of every 16-lane group element e of the 8-byte rows addressed by
+// lanes a, a+4, a+8, a+12 — lanes addressing rows k..k+3 at columns
+// n0 + 4·(0..3) give each lane four consecutive k of its own column, so W
+// needs no transposed copy.  Pipeline as in gemm_p_kernel: a three-stage
+// LDS ring stored two steps ahead, global loads four steps ahead in two
+// register sets, fragments of the next stage read at the top of each step,
+// one barrier per step.  Row pitches: 40 halves (A, [N,K] B: 16-byte
+// fragment reads conflict-free over 8 lanes), BN + 16 halves (k-major B:
+// the four rows of a 16-lane transposed read fall in disjoint banks).
+template <int BM, int BN, bool B_NK, bool RANK>
+__global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
+  constexpr int BK = 32;
+  constexpr int TA = BM / 32, TB = BN / 32;  // 16×16 tiles per wave along M and N
+  constexpr int PA = BK + 8;
+  constexpr int PT = BN + 16;
+  constexpr int A_PL = BM * PA;
+  constexpr int B_PL = B_NK ? BN * PA : BK * PT;
+  constexpr int STAGE = 2 * A_PL + B_PL;  // halves
+  constexpr int A_ITEMS = BM * BK / 4 / 256;  // 16-byte fp32 chunks of A per thread
+  constexpr int B_ITEMS = BN * BK / 8 / 256;  // 16-byte fp16 chunks of B per thread
+  constexpr int N_ST = A_ITEMS + B_ITEMS;     // global loads per panel
+  constexpr int N_WR = 2 * A_ITEMS + B_ITEMS; // LDS stores per panel
+  static_assert(A_ITEMS >= 1 && B_ITEMS >= 1 && TA >= 1 && TB >= 1, "tile config");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[3 * STAGE];
+
+  int tile, split;
+  if (!tile_of(p, tile, split)) return;
+  const int tm_idx = tile % p.tiles_m;
+  const int tn_idx = tile / p.tiles_m;
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int kbeg = split * p.k_chunk;
+  const int kend = min(p.K, kbeg + p.k_chunk);
+  const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
+  const int odd = nk & 1;
+  const int T = nk + odd;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * (BN / 2);
+  const int li = lane & 15, lg = lane >> 4;
+
+  floatx4 acc[TA][TB];
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int b = 0; b < TB; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // buffer resources based at the tile's first row / column of its K-slice
+  const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(p.A + (int64_t)m0 * p.lda + kbeg);
+  const __amdgpu_buffer_rsrc_t rsb =
+      buf_rsrc(p.B + (B_NK ? (int64_t)n0 * p.ldb + kbeg : (int64_t)kbeg * p.ldb + n0));
+  uint32_t a_off[A_ITEMS], b_off[B_ITEMS];
+  int a_lds[A_ITEMS], b_lds[B_ITEMS];  // LDS offsets (halves) within a stage
+  float a_sc[A_ITEMS];                 // s_m of each A chunk's row
+#pragma unroll
+  for (int it = 0; it < A_ITEMS; ++it) {
+    const int flat = tid + 256 * it;
+    const int row = flat / 8, kq = (flat % 8) * 4;
+    const int mr = min(m0 + row, p.M - 1);
+    a_off[it] = (uint32_t)(((int64_t)(mr - m0) * p.lda + kq) * 4);
+    a_lds[it] = row * PA + kq;
+    a_sc[it] = p.inv_s ? 1.f / p.inv_s[mr] : 1.f;  // exact: a power of two
+  }
+#pragma unroll
+  for (int it = 0; it < B_ITEMS; ++it) {
+    const int flat = tid + 256 * it;
+    if constexpr (B_NK) {
+      const int row = flat / 4, kq = (flat % 4) * 8;
+      b_off[it] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + kq) * 2);
+      b_lds[it] = 2 * A_PL + row * PA + kq;
+    } else {
+      const int k = flat / (BN / 8), nq = (flat % (BN / 8)) * 8;
+      b_off[it] = (uint32_t)(((int64_t)k * p.ldb + (n0 + nq < p.N ? nq : 0)) * 2);
+      b_lds[it] = 2 * A_PL + k * PT + nq;
+    }
+  }
+
+  floatx4 rs[2][N_ST];  // register staging sets (16-byte chunks as floats)
+  auto gload = [&](auto sc, int j) {
+    constexpr int S = decltype(sc)::value;
+    const int kc = min(max(j - odd, 0), nk - 1) * BK;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) rs[S][it] = buf_load4(rsa, a_off[it], (uint32_t)kc * 4u);
+    const uint32_t boff = (uint32_t)((B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * 2);
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) rs[S][A_ITEMS + it] = buf_load4(rsb, b_off[it], boff);
+  };
+  auto lstore = [&](auto sc, int stage) {
+    constexpr int S = decltype(sc)::value;
+    uint16_t* st = smem + stage * STAGE;
+#pragma unroll
+    for (int it = 0; it < A_ITEMS; ++it) {
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float y = rs[S][it][t] * a_sc[it];
+        const _Float16 yh = (_Float16)y;
+        h[t] = __builtin_bit_cast(uint16_t, yh);
+        l[t] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)yh));
+      }
+      *reinterpret_cast<uint2*>(st + a_lds[it]) = uint2{h[0] | h[1] << 16, h[2] | h[3] << 16};
+      *reinterpret_cast<uint2*>(st + A_PL + a_lds[it]) = uint2{l[0] | l[1] << 16, l[2] | l[3] << 16};
+    }
+#pragma unroll
+    for (int it = 0; it < B_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + b_lds[it]) = rs[S][A_ITEMS + it];
+  };
+  struct Frags {
+    halfx8 h[TA], l[TA], b[TB];
+  };
+  auto read_frags = [&](Frags& f, int stage) {
+    const uint16_t* st = smem + stage * STAGE;
+#pragma unroll
+    for (int a = 0; a < TA; ++a) {
+      const int o = (wm + 16 * a + li) * PA + 8 * lg;
+      f.h[a] = *reinterpret_cast<const halfx8*>(st + o);
+      f.l[a] = *reinterpret_cast<const halfx8*>(st + A_PL + o);
+    }
+    const uint16_t* bs = st + 2 * A_PL;
+    if constexpr (B_NK) {
+#pragma unroll
+      for (int b = 0; b < TB; ++b) f.b[b] = *reinterpret_cast<const halfx8*>(bs + (wn + 16 * b + li) * PA + 8 * lg);
+    } else {
+      const int r = 8 * lg + (li >> 2);
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        const int c = wn + 16 * b + 4 * (li & 3);
+        const shortx4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(bs + r * PT + c));
+        const shortx4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(bs + (r + 4) * PT + c));
+        f.b[b] = __builtin_bit_cast(halfx8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+  };
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+      for (int b = 0; b < TB; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.h[a], f.b[b], acc[a][b], 0, 0, 0);
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+      for (int b = 0; b < TB; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.l[a], f.b[b], acc[a][b], 0, 0, 0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  constexpr int N_RD = 2 * TA + (B_NK ? TB : 2 * TB);  // LDS read instructions per read_frags
+  constexpr int N_MF = 2 * TA * TB;                     // MFMAs per step
+  Frags F[2];
+  int s_nxt = 1, s_st = 2;  // stages of entries j+1, j+2 (wave-uniform); entry j sits in the third
+  auto step = [&](auto sc, int j) {
+    constexpr int S = decltype(sc)::value;
+    read_frags(F[S ^ 1], s_nxt);  // entry j+1, visible since the last barrier
+    lstore(sc, s_st);             // entry j+2, loaded two steps ago
+    gload(sc, j + 4);             // into the same register set
+    mfmas(F[S]);
+    __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
+    if constexpr (N_MF >= N_WR + N_ST) {
+#pragma unroll
+      for (int i = 0; i < N_WR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < N_ST; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, N_MF - N_WR - N_ST, 0);
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x200, N_WR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, N_ST, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, N_MF, 0);
+    }
+    __syncthreads();
+    const int t = s_nxt;  // the stage of entry j (just multiplied) takes entry j+3
+    s_nxt = s_st;
+    s_st = (t + 2) % 3;
+  };
+  gload(I0{}, 0);
+  gload(I1{}, 1);
+  if (odd) {  // the virtual entry 0: a stage of zeros
+    for (int i = tid; i < STAGE / 8; i += 256) reinterpret_cast<floatx4*>(smem)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    lstore(I0{}, 0);
+  }
+  lstore(I1{}, 1);
+  gload(I0{}, 2);
+  gload(I1{}, 3);
+  __syncthreads();
+  read_frags(F[0], 0);
+  for (int j = 0; j < T; j += 2) {
+    step(I0{}, j);
+    step(I1{}, j + 1);
+  }
+
+  // undo the row scale
+  if (p.inv_s) {
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float f = p.inv_s[min(m0 + wm + 16 * a + 4 * lg + v, p.M - 1)];
+#pragma unroll
+        for (int b = 0; b < TB; ++b) acc[a][b][v] *= f;
+      }
+  }
+
+  // Rank-r LoRA term in fp32 (v_mfma_f32_16x16x4_f32), split 0 only, staged
+  // in the ring's LDS after the last step's barrier.
+  if (RANK && split == 0) {
+    const int r = p.ep.r, rp = (r + 3) & ~3, pr = rp + 1;
+    float* Ps = reinterpret_cast<float*>(smem);
+    float* Qs = Ps + BM * pr;
+    for (int i = tid; i < BM * rp; i += 256) {
+      const int row = i / rp, j = i % rp, m = m0 + row;
+      Ps[row * pr + j] = (m < p.M && j < r) ? p.ep.P[(int64_t)m * r + j] : 0.f;
+    }
+    for (int i = tid; i < BN * rp; i += 256) {
+      const int col = i / rp, j = i % rp, n = n0 + col;
+      Qs[col * pr + j] = (n < p.N && j < r) ? p.ep.lscale * p.ep.Q[(int64_t)n * p.ep.qsn + (int64_t)j * p.ep.qsj] : 0.f;
+    }
+    __syncthreads();
+    for (int t = 0; t < rp / 4; ++t) {
+      float fp[TA], fq[TB];
+#pragma unroll
+      for (int a = 0; a < TA; ++a) fp[a] = Ps[(wm + 16 * a + li) * pr + 4 * t + lg];
+#pragma unroll
+      for (int b = 0; b < TB; ++b) fq[b] = Qs[(wn + 16 * b + li) * pr + 4 * t + lg];
+#pragma unroll
+      for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int b = 0; b < TB; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fp[a], fq[b], acc[a][b], 0, 0, 0);
+    }
+  }
+
+  const bool split_out = p.partial != nullptr;
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int b = 0; b < TB; ++b) {
+      const int n = n0 + wn + 16 * b + li;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm + 16 * a + 4 * lg + v;
+        if (m >= p.M) continue;
+        if (split_out)
+          p.partial[((int64_t)split * p.M + m) * p.N + n] = acc[a][b][v];
+        else
+          epilogue_store(p.ep, acc[a][b][v], m, n, p.C, p.ldc);
+      }
+    }
+}
+
 // Launch of the GEMM kernel proper.  With timing events set, the dispatch
 // itself records them (hipExtLaunchKernel: the timestamps bracket the
 // kernel's execution), so timing adds no event packets to the stream and the
@@ -1101,8 +1418,8 @@ thread_local const KernelEvents* t_gemm_events = nullptr;
 thread_local hipEvent_t t_tail_start = nullptr, t_tail_stop = nullptr;
 namespace {
 
-template <typename Kern>
-void launch_gemm_kernel(Kern kernel, dim3 grid, dim3 block, hipStream_t s, const GemmParams& p) {
+template <typename Kern, class Params>
+void launch_gemm_kernel(Kern kernel, dim3 grid, dim3 block, hipStream_t s, const Params& p) {
   if (t_gemm_events)
     hipExtLaunchKernelGGL(kernel, grid, block, 0, s, t_gemm_events->start, t_gemm_events->stop, 0, p);
   else
@@ -1154,7 +1471,8 @@ void launch_p_variant(hipStream_t s, const GemmParams& p, dim3 grid, bool b_nk, 
 }
 
 // The 1-D grid of tile_of for `splits` K-slices.
-dim3 xcd_grid(GemmParams& p, int splits) {
+template <class Params>
+dim3 xcd_grid(Params& p, int splits) {
   static const int spread = [] {  // tuning hook: MFT_GEMM_SPREAD=1 spreads every K-slice over all XCDs
     const char* e = getenv("MFT_GEMM_SPREAD");
     return e ? atoi(e) : 0;
@@ -1263,6 +1581,101 @@ Plan plan_gemm(int M, int N, int K, size_t ws_bytes) {
   return best;
 }
 
+// After the main launch: the split-K reduction with the epilogue (and the
+// row norm, fused into it where splitk_norm can), or the row norm alone.
+void gemm_finish(hipStream_t s, int splits, bool dispatch_events, const KernelEvents* ev, const float* partial,
+                 int M, int N, float* C, int64_t ldc, const GemmEpilogue& ep, const RowNorm* nm) {
+  MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
+  if (splits > 1) {
+    // The split-K reduction (with the epilogue and, when fused, the row
+    // norm) belongs to the GEMM's time: bracket it with the tail events.
+    const bool tail = ev && ev->tail_start && ev->tail_stop;
+    if (tail) {
+      ev->tail_used = true;
+      if (dispatch_events) {
+        t_tail_start = ev->tail_start;
+        t_tail_stop = ev->tail_stop;
+      } else {
+        MFT_HIP(hipEventRecord(ev->tail_start, s));
+      }
+    }
+    struct TailReset {
+      ~TailReset() { t_tail_start = t_tail_stop = nullptr; }
+    } tail_reset;
+    const bool fused = nm && splitk_norm(s, partial, splits, M, N, C, ldc, ep, *nm);
+    if (!fused) {
+      MFT_LAUNCH_TAIL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256),
+                      0, s, partial, splits, M, N, C, ldc, ep);
+    }
+    t_tail_start = t_tail_stop = nullptr;
+    if (tail && !dispatch_events) MFT_HIP(hipEventRecord(ev->tail_stop, s));
+    MFT_LAUNCH_CHECK();
+    if (!fused && nm) row_norm(s, C, M, N, *nm);
+  } else if (nm) {
+    row_norm(s, C, M, N, *nm);
+  }
+}
+
+
+// ---- fp16 matrix-core GEMM launch ----
+template <int BM, int BN, bool RANK>
+void launch_h_rank(hipStream_t s, GemmHParams& p, bool b_nk, int splits) {
+  p.tiles_m = (int)cdiv(p.M, BM);
+  p.tiles_n = (int)cdiv(p.N, BN);
+  const dim3 grid = xcd_grid(p, splits), block(256);
+  if (b_nk) launch_gemm_kernel(gemm_h_kernel<BM, BN, true, RANK>, grid, block, s, p);
+  else launch_gemm_kernel(gemm_h_kernel<BM, BN, false, RANK>, grid, block, s, p);
+  MFT_LAUNCH_CHECK();
+}
+template <int BM, int BN>
+void launch_h(hipStream_t s, GemmHParams& p, bool b_nk, int splits) {
+  if (p.ep.P != nullptr) launch_h_rank<BM, BN, true>(s, p, b_nk, splits);
+  else launch_h_rank<BM, BN, false>(s, p, b_nk, splits);
+}
+
+// Tile shape and split-K of the fp16 GEMM.  A panel step's time is the
+// larger of a per-shape latency floor and the step's operand bytes (fp32 A,
+// fp16 B) times the workgroups resident at once over an effective L2 rate;
+// a launch runs ceil(workgroups / capacity) rounds of k_chunk/32 steps
+// (capacity = 256 CUs × 1, 2 or 3 workgroups of the 128×128, 64×128 and
+// 64×64 tiles, from their LDS rings), plus 5 µs per launch and, split, 2 µs
+// plus the partials at 3 MB/µs.  Fitted to MI355X sweeps of the Gemma-3 1B
+// linear shapes (M = 1024, 18 plans each), it picks within 6% of the best
+// measured plan in total; K-slices deeper than 1024 measured slower than
+// the model says (the fp32 A rows of a deep slice fall out of L2), so deep
+// reductions split until a slice is at most 1024 deep.
+struct PlanH {
+  int bm, bn, splits;
+};
+PlanH plan_gemm_h(int M, int N, int K, size_t ws_bytes) {
+  struct Shape {
+    int bm, bn, occ;
+    double lat_us;
+  };
+  static const Shape shapes[] = {{128, 128, 1, 1.0}, {64, 128, 2, 0.4}, {64, 64, 3, 0.3}};
+  PlanH best{64, 64, 1};
+  double best_t = 1e30;
+  for (const Shape& sh : shapes) {
+    const int64_t tiles = cdiv(M, sh.bm) * cdiv(N, sh.bn);
+    for (int sp : {1, 2, 3, 4, 6, 8}) {
+      const int64_t kc = cdiv(cdiv(K, sp), 32) * 32;
+      if (cdiv(K, kc) != sp) continue;
+      if (sp > 1 && (kc < 128 || (size_t)sp * M * N * sizeof(float) > ws_bytes)) continue;
+      if (K >= 4096 && kc > 1024 && sp < 8) continue;
+      const int64_t wgs = tiles * sp, cap = 256 * sh.occ;
+      const double conc = (double)std::min<int64_t>(wgs, cap);
+      const double step_bytes = sh.bm * 32.0 * 4 + sh.bn * 32.0 * 2;
+      const double tau = std::max(sh.lat_us, conc * step_bytes / 11e6);  // µs per panel step
+      double t = 5.0 + (double)cdiv(wgs, cap) * (double)(kc / 32) * tau;
+      if (sp > 1) t += 2.0 + sp * (double)M * N * 8 / 3e6;
+      if (t < best_t) {
+        best_t = t;
+        best = {sh.bm, sh.bn, sp};
+      }
+    }
+  }
+  return best;
+}
 }  // namespace
 
 bool gemm_wide_plan(int M, int N) { return cdiv(M, 128) * cdiv(N, 128) >= 1024; }
@@ -1410,35 +1823,92 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   t_gemm_events = nullptr;
   if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
 
-  MFT_CHECK_ARG(!nm || ldc == N, "a row norm needs ldc == N");
-  if (splits > 1) {
-    // The split-K reduction (with the epilogue and, when fused, the row
-    // norm) belongs to the GEMM's time: bracket it with the tail events.
-    const bool tail = ev && ev->tail_start && ev->tail_stop;
-    if (tail) {
-      ev->tail_used = true;
-      if (dispatch_events) {
-        t_tail_start = ev->tail_start;
-        t_tail_stop = ev->tail_stop;
-      } else {
-        MFT_HIP(hipEventRecord(ev->tail_start, s));
-      }
-    }
-    struct TailReset {
-      ~TailReset() { t_tail_start = t_tail_stop = nullptr; }
-    } tail_reset;
-    const bool fused = nm && splitk_norm(s, ws.ptr, splits, M, N, C, ldc, ep, *nm);
-    if (!fused) {
-      MFT_LAUNCH_TAIL(splitk_reduce_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)std::min(M, 65535)), dim3(256),
-                      0, s, (const float*)ws.ptr, splits, M, N, C, ldc, ep);
-    }
-    t_tail_start = t_tail_stop = nullptr;
-    if (tail && !dispatch_events) MFT_HIP(hipEventRecord(ev->tail_stop, s));
-    MFT_LAUNCH_CHECK();
-    if (!fused && nm) row_norm(s, C, M, N, *nm);
-  } else if (nm) {
-    row_norm(s, C, M, N, *nm);
+  gemm_finish(s, splits, dispatch_events, ev, ws.ptr, M, N, C, ldc, ep, nm);
+}
+
+
+void row_scales(hipStream_t s, const float* x, int64_t ldx, int M, int K, float* inv_s) {
+  MFT_CHECK_ARG(M > 0 && K > 0 && K % 4 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0, "row_scales shape");
+  hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)M), dim3(256), 0, s, x, ldx, K, inv_s);
+  MFT_LAUNCH_CHECK();
+}
+
+bool gemm_h_ok(int N, int K, bool b_nk, int r) { return K % 32 == 0 && (b_nk || N % 8 == 0) && r <= 32; }
+
+void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, const uint16_t* B, int64_t ldb, bool b_nk,
+            float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws, const KernelEvents* ev) {
+  MFT_CHECK_ARG(M > 0 && N > 0 && K > 0, "empty GEMM");
+  MFT_CHECK_ARG(gemm_h_ok(N, K, b_nk, ep.r), "fp16 GEMM takes K % 32 == 0, N % 8 == 0 for [K,N] B, r <= 32");
+  MFT_CHECK_ARG(A && lda >= K && lda % 4 == 0, "lda must be a multiple of 4 and >= K");
+  MFT_CHECK_ARG(b_nk ? ldb >= K : ldb >= N, "ldb too small");
+  MFT_CHECK_ARG(ldb % 8 == 0, "ldb must be a multiple of 8");
+  MFT_CHECK_ARG(ldc >= N, "ldc must be >= N");
+  MFT_CHECK_ARG((((uintptr_t)A | (uintptr_t)B) & 15) == 0, "GEMM operands must be 16-byte aligned");
+  MFT_CHECK_ARG(!ep.stats, "row statistics need the fp32 LM-head plan");
+  GemmHParams p{};
+  p.A = A; p.inv_s = inv_s; p.B = B; p.C = C;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K;
+  p.ep = ep;
+  p.partial = nullptr;
+  PlanH pl = plan_gemm_h(M, N, K, ws.ptr ? ws.bytes : 0);
+  // Tuning hook: MFT_GEMMH_PLAN="bm,bn,splits" forces the launch shape.
+  static const char* forced = getenv("MFT_GEMMH_PLAN");
+  if (forced) {
+    int bm = 0, bn = 0, sp = 0;
+    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
+        ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
+        (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
+      pl = {bm, bn, sp};
   }
+  const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
+  // as in gemm(): a row norm rides in the split-K reduction for free
+  if (nm && !forced && pl.splits == 1 && K >= 512 && N % 4 == 0 && N <= 4096 && ldc == N &&
+      (size_t)2 * M * N * sizeof(float) <= ws.bytes)
+    pl.splits = 2;
+  int splits = pl.splits;
+  p.k_chunk = (int)(cdiv(cdiv(K, splits), 32) * 32);
+  splits = (int)cdiv(K, p.k_chunk);
+  MFT_CHECK_ARG(((int64_t)pl.bm * p.lda + p.k_chunk) * 4 < (int64_t(1) << 32) &&
+                    (b_nk ? (int64_t)pl.bn * p.ldb + p.k_chunk : (int64_t)p.k_chunk * p.ldb + pl.bn) * 2 <
+                        (int64_t(1) << 32),
+                "GEMM operand too large for 32-bit buffer offsets");
+  if (splits > 1) p.partial = ws.ptr;
+
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (ev) MFT_HIP(hipStreamIsCapturing(s, &cap));
+  const bool dispatch_events = ev && ev->start && ev->stop && cap == hipStreamCaptureStatusNone;
+  if (ev && ev->start && !dispatch_events) MFT_HIP(hipEventRecord(ev->start, s));
+  t_gemm_events = dispatch_events ? ev : nullptr;
+  if (pl.bm == 128) launch_h<128, 128>(s, p, b_nk, splits);
+  else if (pl.bn == 128) launch_h<64, 128>(s, p, b_nk, splits);
+  else launch_h<64, 64>(s, p, b_nk, splits);
+  t_gemm_events = nullptr;
+  if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
+  gemm_finish(s, splits, dispatch_events, ev, ws.ptr, M, N, C, ldc, ep, nm);
+}
+
+
+bool gemm_f16w(hipStream_t s, const float* x, int64_t ldx, const void* W, int64_t ldw, bool b_nk, float* C,
+               int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws, const KernelEvents* ev) {
+  static const int mode = [] {  // tuning hook: MFT_GEMM_F16=0 keeps fp16 W on the fp32 kernels
+    const char* e = getenv("MFT_GEMM_F16");
+    return e ? atoi(e) : 1;
+  }();
+  if (!mode || ep.stats || !gemm_h_ok(N, K, b_nk, ep.r) || ldx % 4 != 0 || ldx < K || ((uintptr_t)x & 15) != 0 ||
+      ldw % 8 != 0 || ((uintptr_t)W & 15) != 0)
+    return false;
+  const size_t need = ((size_t)M * sizeof(float) + 255) / 256 * 256;
+  const size_t pad = ws.ptr ? (256 - ((uintptr_t)ws.ptr & 255)) & 255 : 0;
+  if (!ws.ptr || ws.bytes < need + pad) return false;
+  char* base = reinterpret_cast<char*>(ws.ptr) + pad;
+  float* inv_s = reinterpret_cast<float*>(base);
+  row_scales(s, x, ldx, M, K, inv_s);
+  Scratch rest;
+  rest.ptr = reinterpret_cast<float*>(base + need);
+  rest.bytes = ws.bytes - need - pad;
+  gemm_h(s, x, ldx, inv_s, static_cast<const uint16_t*>(W), ldw, b_nk, C, ldc, M, N, K, ep, rest, ev);
+  return true;
 }
 
 }  // namespace mft

@@ -38,7 +38,8 @@ void lora_linear_fwd(hipStream_t s, const float* x, int64_t M, int64_t K,
     ep.qsj = 1;
     ep.lscale = scale;
   }
-  gemm(s, x, K, W, N, /*b_nk=*/false, w_f16, y, N, (int)M, (int)N, (int)K, ep, ws, ev);
+  if (!(w_f16 && gemm_f16w(s, x, K, W, N, /*b_nk=*/false, y, N, (int)M, (int)N, (int)K, ep, ws, ev)))
+    gemm(s, x, K, W, N, /*b_nk=*/false, w_f16, y, N, (int)M, (int)N, (int)K, ep, ws, ev);
 }
 
 void lora_linear_bwd(hipStream_t s, const float* dy, const float* x,
@@ -70,7 +71,8 @@ void lora_linear_bwd(hipStream_t s, const float* dy, const float* x,
       ep.lscale = scale;
     }
     // dx[M,K] = dy[M,N] · Wᵀ: W [K,N] is the [N_out=K, K_red=N] operand.
-    gemm(s, dy, N, W, N, /*b_nk=*/true, w_f16, dx, K, (int)M, (int)K, (int)N, ep, rest, ev);
+    if (!(w_f16 && gemm_f16w(s, dy, N, W, N, /*b_nk=*/true, dx, K, (int)M, (int)K, (int)N, ep, rest, ev)))
+      gemm(s, dy, N, W, N, /*b_nk=*/true, w_f16, dx, K, (int)M, (int)K, (int)N, ep, rest, ev);
   }
   if (lora) {
     // dA(j,k) = s·Σ_m U[m,j]·x[m,k] → dA[j*K + k];  dB(n,j) = s·Σ_m xa[m,j]·dy[m,n] → dB[n*r + j]

@@ -365,10 +365,13 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
 #pragma unroll
   for (int q = 0; q < RW; ++q) xr[q] = jb.X + (int64_t)min(m0 + q, M - 1) * jb.ldx;
   float acc[RW][R];
+  float mx[RW];  // max |x| of each row (row scales for the fp16 GEMM, when asked for)
 #pragma unroll
-  for (int q = 0; q < RW; ++q)
+  for (int q = 0; q < RW; ++q) {
+    mx[q] = 0.f;
 #pragma unroll
     for (int j = 0; j < R; ++j) acc[q][j] = 0.f;
+  }
   // K is a multiple of 4 (checked on the host), so a 4-vector never crosses a row.
   // The K-split form unrolls deeper: its few workgroups (one job of 4-row
   // groups) leave the loads of several steps to cover the memory latency.
@@ -376,7 +379,10 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
   for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
     floatx4 xv[RW];
 #pragma unroll
-    for (int q = 0; q < RW; ++q) xv[q] = ldg(reinterpret_cast<const floatx4*>(xr[q] + k));
+    for (int q = 0; q < RW; ++q) {
+      xv[q] = ldg(reinterpret_cast<const floatx4*>(xr[q] + k));
+      mx[q] = fmaxf(mx[q], fmaxf(fmaxf(fabsf(xv[q][0]), fabsf(xv[q][1])), fmaxf(fabsf(xv[q][2]), fabsf(xv[q][3]))));
+    }
     if (jb.y_rk) {  // Y [r, K]
 #pragma unroll
       for (int j = 0; j < R; ++j) {
@@ -425,13 +431,29 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
   }
   constexpr int SH = V == 64 ? 0 : V == 32 ? 1 : V == 16 ? 2 : V == 8 ? 3 : V == 4 ? 4 : 5;
   const int vi = lane >> SH;
+  if (jb.inv_s) {  // uniform per job
+#pragma unroll
+    for (int q = 0; q < RW; ++q)
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) mx[q] = fmaxf(mx[q], __shfl_xor(mx[q], d, 64));
+  }
   if constexpr (KS == 1) {
     if ((lane & ((1 << SH) - 1)) == 0) {
       const int q = vi / R, j = vi % R, m = m0 + q;
       if (m < M) jb.out[(int64_t)m * R + j] = v[0];
     }
+    if (jb.inv_s && lane < RW && m0 + lane < M) {
+      float t = mx[0];
+#pragma unroll
+      for (int q = 1; q < RW; ++q) t = lane == q ? mx[q] : t;
+      jb.inv_s[m0 + lane] = row_inv_scale(t);
+    }
   } else {
     if ((lane & ((1 << SH) - 1)) == 0) lds[w * V + vi] = v[0];
+    if (jb.inv_s && lane == 0) {
+#pragma unroll
+      for (int q = 0; q < RW; ++q) lds[KS * V + w * RW + q] = mx[q];
+    }
     __syncthreads();
     if (w == 0 && lane < V) {
       float t = lds[lane];
@@ -439,6 +461,12 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
       for (int u = 1; u < KS; ++u) t += lds[u * V + lane];
       const int q = lane / R, j = lane % R, m = m0 + q;
       if (m < M) jb.out[(int64_t)m * R + j] = t;
+    }
+    if (jb.inv_s && w == 0 && lane < RW && m0 + lane < M) {
+      float t = lds[KS * V + lane];
+#pragma unroll
+      for (int u = 1; u < KS; ++u) t = fmaxf(t, lds[KS * V + u * RW + lane]);
+      jb.inv_s[m0 + lane] = row_inv_scale(t);
     }
   }
 }

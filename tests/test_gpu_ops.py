@@ -115,6 +115,61 @@ def test_lora_linear_fp16_weight(M, K, N):
     assert rel_err(h(dB), dB_ref) < TOL
 
 
+def row_rel_err(a, b):
+    """Largest per-row relative error (rows of any magnitude count alike)."""
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    num = np.linalg.norm(a64 - b64, axis=1)
+    den = np.linalg.norm(b64, axis=1)
+    return float(np.max(np.where(den > 0, num / np.maximum(den, 1e-300), num)))
+
+
+F16_MMA_SHAPES = [
+    (128, 1152, 1024),  # Gemma-3 1B q projection / dX of o
+    (77, 96, 200),      # ragged M and N, three 32-deep panels (odd count)
+    (256, 6912, 1152),  # down projection: split-K
+    (64, 256, 2304),
+]
+
+
+@pytest.mark.parametrize("M,K,N", F16_MMA_SHAPES)
+def test_lora_linear_fp16_matrix_cores_rows_of_any_scale(M, K, N):
+    """fp16 W on the fp16 matrix cores: x (forward) and dY (dX) are split
+    per row into fp16 hi/lo planes with a power-of-two row scale.  Rows span
+    1e-30 .. 1e8 (gradients are tiny, activations are not) and one row is
+    zero, so a missing or wrong row scale shows as a row far off; every row is
+    held to 2e-5 relative against the oracle (double accumulation) on the same
+    fp16 values: the pair keeps 22 significand bits, and fp32 accumulation
+    over K = 6912 alone is a few 1e-6."""
+    print(f"fp16 matrix-core linear M={M} K={K} N={N}", flush=True)
+    r = 8
+    rng = np.random.default_rng(M + K + N)
+    mags = 10.0 ** rng.uniform(-30, 8, size=(M, 1))
+    mags[M // 2] = 0.0
+    x = (rn(M, K) * mags).astype(np.float32)
+    dy = (rn(M, N) * mags[::-1]).astype(np.float32)
+    A, B = rn(r, K, std=1 / 8), rn(N, r, std=0.02)
+    Wf = rn(K, N, std=0.02).astype(np.float16).astype(np.float32)
+    W16 = Wf.astype(np.float16)
+    y_ref, xa_ref = O.lora_linear_fwd(x, Wf, None, A, B, 4.0)
+    y, xa = ops.lora_linear_fwd(g(x), g(W16), None, g(A), g(B), 4.0)
+    assert row_rel_err(h(y), y_ref) < 2e-5
+    assert np.all(h(y)[M // 2] == 0.0)
+    dx_ref, _, _ = O.lora_linear_bwd(dy, x, Wf, A, B, xa_ref, 4.0)
+    dx, _, _ = ops.lora_linear_bwd(g(dy), g(x), g(W16), g(A), g(B), xa, 4.0)
+    assert row_rel_err(h(dx), dx_ref) < 2e-5
+
+
+def test_lora_linear_fp16_k_tail_takes_widened_path():
+    """K = 132 is not a whole number of 32-deep panels: the fp16-W linear
+    runs the fp32 kernels with W widened in the tile load instead, same bar."""
+    M, K, N, r = 50, 132, 96, 4
+    x, A, B = rn(M, K), rn(r, K, std=1 / 8), rn(N, r, std=0.02)
+    W16 = rn(K, N, std=0.02).astype(np.float16)
+    y_ref, _ = O.lora_linear_fwd(x, W16.astype(np.float32), None, A, B, 2.0)
+    y, _ = ops.lora_linear_fwd(g(x), g(W16), None, g(A), g(B), 2.0)
+    assert rel_err(h(y), y_ref) < TOL
+
+
 def test_lm_head_fp16_vocab_gemms():
     """Gemma-3 1B's LM head with the tied embedding E [V, d] stored as fp16
     (config 5): logits = h·Eᵀ runs the 128×128 kernel with an [N, K] fp16
