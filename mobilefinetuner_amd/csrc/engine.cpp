@@ -1092,23 +1092,29 @@ DropStream drop_stream(const mft_model_s* m) {
 
 void run_batch(mft_model_s* m, int idx, int64_t M);
 
+// Whether C = x·op(W) runs on the fp16 matrix cores (lin_gemm).
 // C = x·op(W) (+ epilogue) for a linear's frozen W.  fp16-stored W runs on
 // the fp16 matrix cores with x's row scales from inv_s (written by the
 // batched rank-r launch that read x) or, when null, from a row_scales launch
 // timed with the linear class.  Tuning hook: MFT_GEMM_F16=0 keeps fp16 W on
 // the fp32 kernels (widened in the tile load).
-void lin_gemm(mft_model_s* m, const float* x, int64_t ldx, const Param& W, const void* wptr, int64_t ldw, bool b_nk,
-              float* C, int64_t ldc, int64_t M, int N, int K, const GemmEpilogue& ep, Scratch ws,
-              const KernelEvents* ev, const float* inv_s) {
+bool f16_path(const mft_model_s* m, const Param& W, const float* x, int64_t ldx, const void* wptr, int64_t ldw,
+              bool b_nk, int N, int K, int r) {
   static const int f16_mode = [] {
     const char* e = getenv("MFT_GEMM_F16");
     return e ? atoi(e) : 1;
   }();
-  if (W.f16 && f16_mode && m->rscale && gemm_h_ok(N, K, b_nk, ep.r) && ldx % 4 == 0 && ldx >= K &&
-      ((uintptr_t)x & 15) == 0 && ldw % 8 == 0 && ((uintptr_t)wptr & 15) == 0) {
+  return W.f16 && f16_mode && m->rscale && gemm_h_ok(N, K, b_nk, r) && ldx % 4 == 0 && ldx >= K &&
+         ((uintptr_t)x & 15) == 0 && ldw % 8 == 0 && ((uintptr_t)wptr & 15) == 0;
+}
+
+void lin_gemm(mft_model_s* m, const float* x, int64_t ldx, const Param& W, const void* wptr, int64_t ldw, bool b_nk,
+              float* C, int64_t ldc, int64_t M, int N, int K, const GemmEpilogue& ep, Scratch ws,
+              const KernelEvents* ev, const float* inv_s, int cls = CLS_LINEAR) {
+  if (f16_path(m, W, x, ldx, wptr, ldw, b_nk, N, K, ep.r)) {
     if (!inv_s) {
       float* slot = m->rscale + (int64_t)T_MAX * m->max_tokens;
-      Timed ts(m, CLS_LINEAR, 0.0);
+      Timed ts(m, cls, 0.0);
       ts.begin();
       row_scales(m->stream, x, ldx, (int)M, K, slot);
       ts.end();
@@ -1455,13 +1461,15 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   Timed t(m, CLS_LMHEAD, 2.0 * M * c.vocab * d);
   GemmEpilogue head;
   head.site = 1;
-  m->stats_fresh = m->row_stats && gemm_wide_plan((int)M, (int)c.vocab);
+  // fp16 E: the fp16 matrix cores (any tile plan there emits the row statistics)
+  const bool h16 = f16_path(m, E, m->hf, d, wh.ptr, d, true, (int)c.vocab, d, 0);
+  m->stats_fresh = m->row_stats && (h16 || gemm_wide_plan((int)M, (int)c.vocab));
   if (m->stats_fresh) {
     head.stats = m->row_stats;
     head.stats_ld = m->stats_ld;
   }
-  gemm(s, m->hf, d, wh.ptr, d, true, E.f16, m->logits, m->ldv, (int)M, (int)c.vocab, d, head, m->ws,
-       t.events());
+  lin_gemm(m, m->hf, d, E, wh.ptr, d, true, m->logits, m->ldv, M, (int)c.vocab, d, head, m->ws, t.events(), nullptr,
+           CLS_LMHEAD);
 }
 
 void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs, int S,
@@ -1538,8 +1546,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     head.site = 1;
     head.norm = &nf;
     const WeightUse wh(m, m->wte);
-    gemm(s, m->logits, m->ldv, wh.ptr, d, false, E.f16, m->dn, d, (int)M, d, (int)c.vocab, head, m->ws,
-         t.events());
+    lin_gemm(m, m->logits, m->ldv, E, wh.ptr, d, false, m->dn, d, M, d, (int)c.vocab, head, m->ws, t.events(),
+             nullptr, CLS_LMHEAD);
   }
   const int64_t nf = M * c.d_ff;
   for (int li = top; li >= 0; --li) {

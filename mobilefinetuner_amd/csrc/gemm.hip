@@ -1391,6 +1391,35 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   }
 
   const bool split_out = p.partial != nullptr;
+  // Row statistics of the LM head's logits for the cross-entropy, as in
+  // gemm_kernel's: each wave's (BM/2)×64 sub-tile is one 64-column block;
+  // the wave transposes it through its own region of the idle LDS ring (row
+  // pitch 68 floats) and lane L < BM/2 reduces row L alone (row_stats64);
+  // a block wholly past N writes none.
+  if constexpr (BN == 128) {
+    constexpr int SP = 68;
+    static_assert(4 * (BM / 2) * SP * 4 <= 3 * STAGE * 2, "LDS ring too small for the statistics transpose");
+    const int nb = n0 + wn;
+    if (p.ep.stats && !split_out) {  // uniform over the workgroup
+      __syncthreads();  // every wave is done with the ring
+    }
+    if (p.ep.stats && !split_out && nb < p.N) {
+      float* ws = reinterpret_cast<float*>(smem) + wave * (BM / 2) * SP;
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        const bool in = nb + 16 * b + li < p.N;
+#pragma unroll
+        for (int a = 0; a < TA; ++a)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) ws[(16 * a + 4 * lg + v) * SP + 16 * b + li] = in ? acc[a][b][v] : -FLT_MAX;
+      }
+      if (lane < BM / 2) {
+        const float2 st = row_stats64(ws + lane * SP);
+        const int m = m0 + wm + lane;
+        if (m < p.M) p.ep.stats[(int64_t)m * p.ep.stats_ld + nb / 64] = st;
+      }
+    }
+  }
 #pragma unroll
   for (int a = 0; a < TA; ++a)
 #pragma unroll
@@ -1647,7 +1676,7 @@ void launch_h(hipStream_t s, GemmHParams& p, bool b_nk, int splits) {
 struct PlanH {
   int bm, bn, splits;
 };
-PlanH plan_gemm_h(int M, int N, int K, size_t ws_bytes) {
+PlanH plan_gemm_h(int M, int N, int K, size_t ws_bytes, bool stats) {
   struct Shape {
     int bm, bn, occ;
     double lat_us;
@@ -1656,10 +1685,12 @@ PlanH plan_gemm_h(int M, int N, int K, size_t ws_bytes) {
   PlanH best{64, 64, 1};
   double best_t = 1e30;
   for (const Shape& sh : shapes) {
+    if (stats && sh.bn != 128) continue;  // row statistics: 64-column blocks per wave, unsplit K
     const int64_t tiles = cdiv(M, sh.bm) * cdiv(N, sh.bn);
-    for (int sp : {1, 2, 3, 4, 6, 8}) {
+    for (int sp : {1, 2, 3, 4, 6, 8, 16, 32}) {
       const int64_t kc = cdiv(cdiv(K, sp), 32) * 32;
       if (cdiv(K, kc) != sp) continue;
+      if (stats && sp > 1) continue;
       if (sp > 1 && (kc < 128 || (size_t)sp * M * N * sizeof(float) > ws_bytes)) continue;
       if (K >= 4096 && kc > 1024 && sp < 8) continue;
       const int64_t wgs = tiles * sp, cap = 256 * sh.occ;
@@ -1844,26 +1875,28 @@ void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, cons
   MFT_CHECK_ARG(ldb % 8 == 0, "ldb must be a multiple of 8");
   MFT_CHECK_ARG(ldc >= N, "ldc must be >= N");
   MFT_CHECK_ARG((((uintptr_t)A | (uintptr_t)B) & 15) == 0, "GEMM operands must be 16-byte aligned");
-  MFT_CHECK_ARG(!ep.stats, "row statistics need the fp32 LM-head plan");
+  MFT_CHECK_ARG(!ep.stats || (ep.stats_ld >= cdiv(N, 64) && !ep.bias && !ep.resid && ep.beta == 0.f && !ep.gelu_out &&
+                              !ep.gelu_grad_of && !ep.P && !(ep.norm && ep.norm->kind != NORM_NONE)),
+                "row statistics describe plain logits (no epilogue terms)");
   GemmHParams p{};
   p.A = A; p.inv_s = inv_s; p.B = B; p.C = C;
   p.lda = lda; p.ldb = ldb; p.ldc = ldc;
   p.M = M; p.N = N; p.K = K;
   p.ep = ep;
   p.partial = nullptr;
-  PlanH pl = plan_gemm_h(M, N, K, ws.ptr ? ws.bytes : 0);
+  PlanH pl = plan_gemm_h(M, N, K, ws.ptr ? ws.bytes : 0, ep.stats != nullptr);
   // Tuning hook: MFT_GEMMH_PLAN="bm,bn,splits" forces the launch shape.
   static const char* forced = getenv("MFT_GEMMH_PLAN");
-  if (forced) {
+  if (forced && !ep.stats) {
     int bm = 0, bn = 0, sp = 0;
-    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
+    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 && sp <= 64 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
   }
   const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
   // as in gemm(): a row norm rides in the split-K reduction for free
-  if (nm && !forced && pl.splits == 1 && K >= 512 && N % 4 == 0 && N <= 4096 && ldc == N &&
+  if (nm && !forced && !ep.stats && pl.splits == 1 && K >= 512 && N % 4 == 0 && N <= 4096 && ldc == N &&
       (size_t)2 * M * N * sizeof(float) <= ws.bytes)
     pl.splits = 2;
   int splits = pl.splits;
