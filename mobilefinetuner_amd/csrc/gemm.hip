@@ -1128,6 +1128,20 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
   if (tid == 0) inv_s[m] = row_inv_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
 }
 
+// hi/lo split of two fp32 values x0, x1 scaled by s, packed two fp16 per
+// register: hi = fp16(x·s), lo = fp16(x·s − hi), both rounded to nearest
+// even from the exact fp32 value (the fma forms x·s − hi exactly).  Four
+// mixed-precision fmas write each half in place (mixlo keeps the high half,
+// mixhi the low), instead of converts plus shift-and-or packing.
+__device__ __forceinline__ void split2_f16(float x0, float x1, float s, uint32_t& hi, uint32_t& lo) {
+  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
+      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(hi), "=&v"(lo)
+      : "v"(x0), "v"(x1), "v"(s));
+}
+
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
@@ -1163,7 +1177,7 @@ struct GemmHParams {
 // one barrier per step.  Row pitches: 40 halves (A, [N,K] B: 16-byte
 // fragment reads conflict-free over 8 lanes), BN + 16 halves (k-major B:
 // the four rows of a 16-lane transposed read fall in disjoint banks).
-template <int BM, int BN, bool B_NK, bool RANK>
+template <int BM, int BN, bool B_NK, bool RANK, int PIPE>
 __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   constexpr int BK = 32;
   constexpr int TA = BM / 32, TB = BN / 32;  // 16×16 tiles per wave along M and N
@@ -1187,8 +1201,8 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
-  const int odd = nk & 1;
-  const int T = nk + odd;
+  const int pad = (PIPE - nk % PIPE) % PIPE;  // leading zero entries: the step loop runs PIPE steps per iteration
+  const int T = nk + pad;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -1231,10 +1245,10 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     }
   }
 
-  floatx4 rs[2][N_ST];  // register staging sets (16-byte chunks as floats)
+  floatx4 rs[PIPE][N_ST];  // register staging sets (16-byte chunks as floats); entry e in set e % PIPE
   auto gload = [&](auto sc, int j) {
     constexpr int S = decltype(sc)::value;
-    const int kc = min(max(j - odd, 0), nk - 1) * BK;
+    const int kc = min(max(j - pad, 0), nk - 1) * BK;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) rs[S][it] = buf_load4(rsa, a_off[it], (uint32_t)kc * 4u);
     const uint32_t boff = (uint32_t)((B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * 2);
@@ -1246,16 +1260,11 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     uint16_t* st = smem + stage * STAGE;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
-      uint32_t h[4], l[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float y = rs[S][it][t] * a_sc[it];
-        const _Float16 yh = (_Float16)y;
-        h[t] = __builtin_bit_cast(uint16_t, yh);
-        l[t] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)yh));
-      }
-      *reinterpret_cast<uint2*>(st + a_lds[it]) = uint2{h[0] | h[1] << 16, h[2] | h[3] << 16};
-      *reinterpret_cast<uint2*>(st + A_PL + a_lds[it]) = uint2{l[0] | l[1] << 16, l[2] | l[3] << 16};
+      uint2 h, l;
+      split2_f16(rs[S][it][0], rs[S][it][1], a_sc[it], h.x, l.x);
+      split2_f16(rs[S][it][2], rs[S][it][3], a_sc[it], h.y, l.y);
+      *reinterpret_cast<uint2*>(st + a_lds[it]) = h;
+      *reinterpret_cast<uint2*>(st + A_PL + a_lds[it]) = l;
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) *reinterpret_cast<floatx4*>(st + b_lds[it]) = rs[S][A_ITEMS + it];
@@ -1298,17 +1307,21 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
 
   constexpr int N_RD = 2 * TA + (B_NK ? TB : 2 * TB);  // LDS read instructions per read_frags
   constexpr int N_MF = 2 * TA * TB;                     // MFMAs per step
-  Frags F[2];
+  Frags F[PIPE];                                        // entry e's fragments in F[e % PIPE]
   int s_nxt = 1, s_st = 2;  // stages of entries j+1, j+2 (wave-uniform); entry j sits in the third
-  auto step = [&](auto sc, int j) {
-    constexpr int S = decltype(sc)::value;
-    read_frags(F[S ^ 1], s_nxt);  // entry j+1, visible since the last barrier
-    lstore(sc, s_st);             // entry j+2, loaded two steps ago
-    gload(sc, j + 4);             // into the same register set
-    mfmas(F[S]);
+  // Step j (fc = j % PIPE, sc = (j + 2) % PIPE): read entry j+1's fragments,
+  // store entry j+2 (loaded PIPE steps ago) and load entry j+2+PIPE into its
+  // register set, multiply entry j.
+  auto step = [&](auto fc, auto sc, int j) {
+    constexpr int FC = decltype(fc)::value;
+    read_frags(F[(FC + 1) % PIPE], s_nxt);  // entry j+1, visible since the last barrier
+    lstore(sc, s_st);
+    gload(sc, j + 2 + PIPE);
+    mfmas(F[FC]);
     __builtin_amdgcn_sched_group_barrier(0x100, N_RD, 0);
     if constexpr (N_MF >= N_WR + N_ST) {
 #pragma unroll
@@ -1332,21 +1345,34 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     s_nxt = s_st;
     s_st = (t + 2) % 3;
   };
+  // Prologue: entries 0 .. PIPE-1 into their sets, entries 0 and 1 stored
+  // (zero stages for leading pad entries), then entries PIPE, PIPE+1.
+  auto zero_stage = [&](int stage) {
+    for (int i = tid; i < STAGE / 8; i += 256)
+      reinterpret_cast<floatx4*>(smem + stage * STAGE)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  };
   gload(I0{}, 0);
   gload(I1{}, 1);
-  if (odd) {  // the virtual entry 0: a stage of zeros
-    for (int i = tid; i < STAGE / 8; i += 256) reinterpret_cast<floatx4*>(smem)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  } else {
-    lstore(I0{}, 0);
-  }
-  lstore(I1{}, 1);
-  gload(I0{}, 2);
-  gload(I1{}, 3);
+  if constexpr (PIPE == 3) gload(I2{}, 2);
+  if (pad > 0) zero_stage(0);
+  else lstore(I0{}, 0);
+  if (pad > 1) zero_stage(1);
+  else lstore(I1{}, 1);
+  gload(I0{}, PIPE);
+  gload(I1{}, PIPE + 1);
   __syncthreads();
   read_frags(F[0], 0);
-  for (int j = 0; j < T; j += 2) {
-    step(I0{}, j);
-    step(I1{}, j + 1);
+  if constexpr (PIPE == 2) {
+    for (int j = 0; j < T; j += 2) {
+      step(I0{}, I0{}, j);
+      step(I1{}, I1{}, j + 1);
+    }
+  } else {
+    for (int j = 0; j < T; j += 3) {
+      step(I0{}, I2{}, j);
+      step(I1{}, I0{}, j + 1);
+      step(I2{}, I1{}, j + 2);
+    }
   }
 
   // undo the row scale
@@ -1652,8 +1678,17 @@ void launch_h_rank(hipStream_t s, GemmHParams& p, bool b_nk, int splits) {
   p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, BN);
   const dim3 grid = xcd_grid(p, splits), block(256);
-  if (b_nk) launch_gemm_kernel(gemm_h_kernel<BM, BN, true, RANK>, grid, block, s, p);
-  else launch_gemm_kernel(gemm_h_kernel<BM, BN, false, RANK>, grid, block, s, p);
+  static const int pipe = [] {  // tuning hook: MFT_GEMMH_PIPE = 2 or 3 register staging sets
+    const char* e = getenv("MFT_GEMMH_PIPE");
+    return e && atoi(e) == 2 ? 2 : 3;
+  }();
+  if (pipe == 3) {
+    if (b_nk) launch_gemm_kernel(gemm_h_kernel<BM, BN, true, RANK, 3>, grid, block, s, p);
+    else launch_gemm_kernel(gemm_h_kernel<BM, BN, false, RANK, 3>, grid, block, s, p);
+  } else {
+    if (b_nk) launch_gemm_kernel(gemm_h_kernel<BM, BN, true, RANK, 2>, grid, block, s, p);
+    else launch_gemm_kernel(gemm_h_kernel<BM, BN, false, RANK, 2>, grid, block, s, p);
+  }
   MFT_LAUNCH_CHECK();
 }
 template <int BM, int BN>
