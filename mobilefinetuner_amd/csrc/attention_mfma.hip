@@ -1427,6 +1427,303 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_short(AttnP p, int n_dkdv) {
   else attn_bwd_short_dq<HD, NW>(p, bid - n_dkdv, smem);
 }
 
+// ------------------------------------------------------------------------------
+// Short sequences at head_dim 256: the head dimension split over the waves.
+// ------------------------------------------------------------------------------
+// At head_dim 256 a lane of attn_bwd_short's roles would hold K, V, dK, dV
+// and a query tile's Q, dO, O rows at once (about 576 VGPRs).  Here each of
+// the four waves of a workgroup owns one 64-wide slice D_w of the head
+// dimension for the whole tile loop, and all waves walk the same inner
+// tiles: per inner tile every wave forms its partial S and dP (and delta)
+// over D_w with its slice of the operands in registers, the partials go
+// through LDS, and each wave sums the four in wave order (every wave gets
+// the same bits, so P and dS agree across the workgroup) before
+// accumulating its own slice of dK/dV (or dQ).  The exchange buffers
+// alternate with the tile's parity, so one barrier per tile both publishes
+// this tile's partials and (being after the previous tile's reads) frees
+// the buffer written next.  delta = rowsum(dO∘O) is formed from the O rows
+// the kernel reads anyway; the dQ role owns its query tile's dQ whole (no
+// partial rows, no sum pass).  Column operands (Q, dO rows for dK/dV, K
+// rows for dQ) are transposed through a wave-private LDS slot, as in
+// attn_bwd_short.
+constexpr int kS256W = 4;                     // waves per workgroup: one 64-dim slice each
+constexpr int kS256X = 2 * 256 + 16;          // exchange record per wave: S, dP (as [lane][v]), delta
+constexpr int kS256TP = 256 / kS256W + 4;     // transposition slot pitch
+constexpr size_t kS256Lds = sizeof(float) * (2 * kS256W * kS256X + kS256W * 2 * 16 * kS256TP);
+
+// dK/dV role: workgroup = one 16-key tile of one query head.
+__device__ __forceinline__ void attn_bwd_s256_dkdv(const AttnP& p, int bid, float* smem) {
+  constexpr int HD = 256, NW = kS256W, DW = HD / NW, NC = DW / 16, TP = kS256TP, XS = kS256X;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int d0 = DW * w;
+  float* X = smem;                                     // [2][NW][XS]
+  float* sq = smem + 2 * NW * XS + w * 2 * 16 * TP;    // this wave's Q slot [16][TP]
+  float* sg = sq + 16 * TP;                            // and dO slot
+  const int hb = bid % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  const int grp = p.Hq / p.Hkv;
+  const int kh = h / grp;
+  const int kt = bid / (p.Hq * p.B);  // heaviest (first) key tiles first
+  const int k0 = 16 * kt;
+  const int kj = k0 + li;  // this lane's key (S column)
+  const int64_t tok0 = (int64_t)b * p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const bool kvalid = kj < p.S && (!kpb || kpb[min(kj, p.S - 1)] > 0.5f);
+  const int klast = min(k0 + 15, p.S - 1);
+  const int qt_lo = (p.causal ? k0 : 0) / 16;
+  const int qt_hi = (p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1) / 16;
+  const float qk2 = p.scale * kLog2e;
+  const int64_t lrow0 = ((int64_t)b * p.Hq + h) * p.S;
+
+  // this wave's slice of the tile's K (scaled by scale·log2e) and V rows
+  floatx4 kreg[NC], vreg[NC], dkacc[NC], dvacc[NC];
+  {
+    const int64_t row = tok0 + min(kj, p.S - 1);
+    const float* kr = p.k + row * p.k_rs + (int64_t)kh * HD + d0 + 4 * lg;
+    const float* vr = p.v + row * p.v_rs + (int64_t)kh * HD + d0 + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      kreg[c] = *reinterpret_cast<const floatx4*>(kr + 16 * c) * qk2;
+      vreg[c] = *reinterpret_cast<const floatx4*>(vr + 16 * c);
+      dkacc[c] = dvacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  struct QTile {
+    floatx4 qa[NC], ga[NC], oa[NC];
+    float lse;
+  };
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc(p.q + tok0 * p.q_rs + (int64_t)h * HD + d0);
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(p.dout + tok0 * p.do_rs + (int64_t)h * HD + d0);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(p.o + tok0 * p.o_rs + (int64_t)h * HD + d0);
+  auto load = [&](int qt, QTile& T) {
+    const int64_t r = min(16 * qt + li, p.S - 1);
+    const uint32_t oq = (uint32_t)((r * p.q_rs + 4 * lg) * 4), og = (uint32_t)((r * p.do_rs + 4 * lg) * 4),
+                   oo = (uint32_t)((r * p.o_rs + 4 * lg) * 4);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      T.qa[c] = buf_load4(rq, oq + 64u * c, 0);
+      T.ga[c] = buf_load4(rg, og + 64u * c, 0);
+      T.oa[c] = buf_load4(ro, oo + 64u * c, 0);
+    }
+    T.lse = p.lse[lrow0 + r];
+  };
+  QTile cur, nxt;
+  if (qt_lo <= qt_hi) load(qt_lo, cur);
+  int par = 0;
+  for (int qt = qt_lo; qt <= qt_hi; ++qt, par ^= 1) {
+    if (qt < qt_hi) load(qt + 1, nxt);
+    floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+    float dl = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s4 = mfma4(cur.qa[c][t], kreg[c][t], s4);
+        dp4 = mfma4(cur.ga[c][t], vreg[c][t], dp4);
+        dl = fmaf(cur.ga[c][t], cur.oa[c][t], dl);
+      }
+    dl = add_xor32(add_xor16(dl));  // delta of query q0 + li over this slice
+    float* xw = X + (par * NW + w) * XS;
+    *reinterpret_cast<floatx4*>(xw + 4 * lane) = s4;
+    *reinterpret_cast<floatx4*>(xw + 256 + 4 * lane) = dp4;
+    if (lg == 0) xw[512 + li] = dl;
+    // Q, dO by column (rows 4g + t, column 16c + i) through the wave's slots
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      *reinterpret_cast<floatx4*>(sq + li * TP + 16 * c + 4 * lg) = cur.qa[c];
+      *reinterpret_cast<floatx4*>(sg + li * TP + 16 * c + 4 * lg) = cur.ga[c];
+    }
+    float qb[NC][4], gb[NC][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        qb[c][t] = sq[(4 * lg + t) * TP + 16 * c + li];
+        gb[c][t] = sg[(4 * lg + t) * TP + 16 * c + li];
+      }
+    const float l2 = cur.lse * kLog2e;  // query q0 + li
+    __syncthreads();
+    floatx4 S = floatx4{0.f, 0.f, 0.f, 0.f}, dP = floatx4{0.f, 0.f, 0.f, 0.f}, D = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float* xu = X + (par * NW + u) * XS;
+      S += *reinterpret_cast<const floatx4*>(xu + 4 * lane);
+      dP += *reinterpret_cast<const floatx4*>(xu + 256 + 4 * lane);
+      D += *reinterpret_cast<const floatx4*>(xu + 512 + 4 * lg);
+    }
+    // S[q0 + 4g + v][key kj]: P = 2^(S₂ − lse₂), dS/scale = P∘(dP − delta)
+    const int q0 = 16 * qt;
+    floatx4 pv, ds;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int qv = q0 + 4 * lg + v;
+      const float l2v = __shfl(l2, 4 * lg + v, 64);
+      const bool ok = kvalid & (qv < p.S) & (!p.causal | (qv >= kj)) & ((p.window <= 0) | (qv - kj < p.window));
+      pv[v] = fast_exp2(ok ? S[v] - l2v : -INFINITY);
+      ds[v] = pv[v] * (dP[v] - D[v]);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        dvacc[c] = mfma4(pv[t], gb[c][t], dvacc[c]);
+        dkacc[c] = mfma4(ds[t], qb[c][t], dkacc[c]);
+      }
+    if (qt < qt_hi) cur = nxt;
+  }
+  // dK, dV [key k0 + 4g + v][dim d0 + 16c + i] of this wave's slice
+  const bool direct = grp == 1;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int gk = k0 + 4 * lg + v;
+    if (gk >= p.S) continue;
+    const int64_t tok = tok0 + gk;
+    float* dkr = (direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + (tok * p.Hq + h) * HD) + d0 + li;
+    float* dvr = (direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD) + d0 + li;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      dkr[16 * c] = dkacc[c][v] * p.scale;
+      dvr[16 * c] = dvacc[c][v];
+    }
+  }
+}
+
+// dQ role: workgroup = one 16-query tile of one head.
+__device__ __forceinline__ void attn_bwd_s256_dq(const AttnP& p, int bid, float* smem) {
+  constexpr int HD = 256, NW = kS256W, DW = HD / NW, NC = DW / 16, TP = kS256TP, XS = kS256X;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int d0 = DW * w;
+  float* X = smem;                                   // [2][NW][XS]
+  float* sk = smem + 2 * NW * XS + w * 2 * 16 * TP;  // this wave's K slot [16][TP]
+  const int hb = bid % (p.Hq * p.B);
+  const int h = hb % p.Hq, b = hb / p.Hq;
+  // Lightest (first) query tiles first: the launch fits the GPU at once and
+  // its second half lands on the CUs of the first, so dQ tile j shares a CU
+  // with dK/dV key tile j (heaviest first) — a causal pair sums to S/16 + 1
+  // inner tiles wherever it lands, and a heavy tile finishes alone on its CU.
+  const int qt = bid / (p.Hq * p.B);
+  const int q0 = 16 * qt;
+  const int kh = h / (p.Hq / p.Hkv);
+  const int qi = q0 + li;
+  const bool qok = qi < p.S;
+  const int64_t tok0 = (int64_t)b * p.S;
+  const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
+  const int qlast = min(q0 + 15, p.S - 1);
+  const int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
+  const int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  const int jhi = qok ? (p.causal ? qi : p.S - 1) : -1;
+  const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
+  const float qk2 = p.scale * kLog2e;
+
+  // this wave's slice of the tile's Q (scaled) and dO rows (B operands of
+  // Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ: the lane owns query qi), delta over the slice
+  floatx4 qreg[NC], greg[NC], dqacc[NC];
+  float dl = 0.f;
+  {
+    const int64_t row = tok0 + min(qi, p.S - 1);
+    const int64_t off = (int64_t)h * HD + d0 + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qreg[c] = *reinterpret_cast<const floatx4*>(p.q + row * p.q_rs + off + 16 * c) * qk2;
+      greg[c] = *reinterpret_cast<const floatx4*>(p.dout + row * p.do_rs + off + 16 * c);
+      const floatx4 orow = *reinterpret_cast<const floatx4*>(p.o + row * p.o_rs + off + 16 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dl = fmaf(greg[c][e], orow[e], dl);
+      dqacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  const float l2 = p.lse[((int64_t)b * p.Hq + h) * p.S + min(qi, p.S - 1)] * kLog2e;
+  struct KTile {
+    floatx4 ka[NC], va[NC];
+  };
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k + tok0 * p.k_rs + (int64_t)kh * HD + d0);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(p.v + tok0 * p.v_rs + (int64_t)kh * HD + d0);
+  auto load = [&](int kt, KTile& T) {
+    const int64_t r = min(16 * kt + li, p.S - 1);
+    const uint32_t ko = (uint32_t)((r * p.k_rs + 4 * lg) * 4), vo = (uint32_t)((r * p.v_rs + 4 * lg) * 4);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      T.ka[c] = buf_load4(rk, ko + 64u * c, 0);
+      T.va[c] = buf_load4(rv, vo + 64u * c, 0);
+    }
+  };
+  KTile cur, nxt;
+  if (kt_lo <= kt_hi) load(kt_lo, cur);
+  // delta of query qi: the four slices' sums through the first exchange
+  // buffer, summed in wave order (the first tile's barrier orders them)
+  dl = add_xor32(add_xor16(dl));
+  float dfull = 0.f;
+  int par = 0;
+  for (int kt = kt_lo; kt <= kt_hi; ++kt, par ^= 1) {
+    if (kt < kt_hi) load(kt + 1, nxt);
+    floatx4 s4 = floatx4{0.f, 0.f, 0.f, 0.f}, dp4 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s4 = mfma4(cur.ka[c][t], qreg[c][t], s4);
+        dp4 = mfma4(cur.va[c][t], greg[c][t], dp4);
+      }
+    float* xw = X + (par * NW + w) * XS;
+    *reinterpret_cast<floatx4*>(xw + 4 * lane) = s4;
+    *reinterpret_cast<floatx4*>(xw + 256 + 4 * lane) = dp4;
+    if (kt == kt_lo && lg == 0) xw[512 + li] = dl;
+    // K by column (rows 4g + t, column 16c + i) through the wave's slot
+#pragma unroll
+    for (int c = 0; c < NC; ++c) *reinterpret_cast<floatx4*>(sk + li * TP + 16 * c + 4 * lg) = cur.ka[c];
+    float kb[NC][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kb[c][t] = sk[(4 * lg + t) * TP + 16 * c + li];
+    __syncthreads();
+    floatx4 S = floatx4{0.f, 0.f, 0.f, 0.f}, dP = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float* xu = X + (par * NW + u) * XS;
+      S += *reinterpret_cast<const floatx4*>(xu + 4 * lane);
+      dP += *reinterpret_cast<const floatx4*>(xu + 256 + 4 * lane);
+      if (kt == kt_lo) dfull += xu[512 + li];
+    }
+    // Sᵀ[key 16kt + 4g + v][query qi]
+    floatx4 ds;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = 16 * kt + 4 * lg + v;
+      bool ok = (j >= jlo) & (j <= jhi) & (j < p.S);
+      if (kpb) ok = ok & (kpb[min(j, p.S - 1)] > 0.5f);
+      const float pp = fast_exp2(ok ? S[v] - l2 : -INFINITY);
+      ds[v] = pp * (dP[v] - dfull);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], kb[c][t], dqacc[c]);
+    if (kt < kt_hi) cur = nxt;
+  }
+  // dQ [query q0 + 4g + v][dim d0 + 16c + i] of this wave's slice
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int gq = q0 + 4 * lg + v;
+    if (gq >= p.S) continue;
+    float* dqr = p.dq + (tok0 + gq) * p.dq_rs + (int64_t)h * HD + d0 + li;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) dqr[16 * c] = dqacc[c][v] * p.scale;
+  }
+}
+
+// Both roles in one launch: blocks [0, n_dkdv) are dK/dV tiles, the rest dQ tiles.
+__global__ __launch_bounds__(64 * kS256W) void attn_bwd_short256(AttnP p, int n_dkdv) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int bid = (int)blockIdx.x;
+  if (bid < n_dkdv) attn_bwd_s256_dkdv(p, bid, smem);
+  else attn_bwd_s256_dq(p, bid - n_dkdv, smem);
+}
+
 template <typename K>
 void set_lds(K kernel, size_t bytes) {
   MFT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -1620,6 +1917,29 @@ void fwd_short256_launch(hipStream_t s, AttnP& p) {
   MFT_LAUNCH_CHECK();
 }
 
+// The head_dim-256 backward at S ≤ 256 (attn_bwd_short256).  Tuning hook:
+// MFT_ATTN_SHORT256_BWD=0 keeps the blocked kernels.
+bool use_short256_bwd(const AttnArgs& a) {
+  static const int mode = [] {
+    const char* e = getenv("MFT_ATTN_SHORT256_BWD");
+    return e ? atoi(e) : 1;
+  }();
+  return mode != 0 && a.hd == 256 && a.S <= 256;
+}
+
+void bwd_short256_launch(hipStream_t s, AttnP& p) {
+  set_lds(attn_bwd_short256, kS256Lds);
+  const int tiles = (int)(cdiv(p.S, 16) * p.Hq * p.B);
+  hipLaunchKernelGGL(attn_bwd_short256, dim3((unsigned)(2 * tiles)), dim3(64 * kS256W), kS256Lds, s, p, tiles);
+  MFT_LAUNCH_CHECK();
+  if (p.Hq != p.Hkv) {
+    const int64_t total = (int64_t)p.B * p.S * p.Hkv * (256 / 4);
+    hipLaunchKernelGGL(attn_partial_sum_kernel<256>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
+                       dim3(256), 0, s, p, 16);
+    MFT_LAUNCH_CHECK();
+  }
+}
+
 template <int HD>
 void bwd_short_launch(hipStream_t s, AttnP& p) {
   constexpr int NW = kShortWaves;
@@ -1733,6 +2053,14 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
       p.pdv = p.pdk + rows * a.hd;
     }
     a.hd == 64 ? bwd_short_launch<64>(s, p) : bwd_short_launch<128>(s, p);
+    return;
+  }
+  if (short_ok && use_short256_bwd(a)) {  // delta formed in-kernel; GQA partials after the delta rows
+    if (a.Hq != a.Hkv) {
+      p.pdk = ws.ptr + (rows + 3) / 4 * 4;
+      p.pdv = p.pdk + rows * a.hd;
+    }
+    bwd_short256_launch(s, p);
     return;
   }
   const BwdPlan pl = bwd_plan(a);

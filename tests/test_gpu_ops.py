@@ -257,6 +257,10 @@ ATTN = [
     (8, 16, 4, 256, 64, 0, False),    # 4 waves / workgroup, GQA 4:1
     (4, 8, 2, 500, 128, 0, True),     # 2 waves / workgroup, ragged S, padding mask
     (4, 8, 2, 512, 256, 128, False),  # 2 waves / workgroup, hd=256 sliding window
+    # hd=256 at S <= 256: the short backward (head dimension split over the waves)
+    (4, 4, 1, 256, 256, 0, False),    # Gemma-3 270M attention shape
+    (1, 2, 2, 33, 256, 0, True),      # one query head per KV head (no partial rows), ragged S, padding
+    (2, 8, 2, 256, 256, 32, False),   # two KV heads of four query heads each, sliding window 32
 ]
 
 
@@ -281,6 +285,24 @@ def test_attention_fwd_bwd(B, Hq, Hkv, S, hd, window, pad):
                                         True, window, kpad)
     dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, True,
                               window, g(kpad) if pad else None)
+    assert rel_err(h(dq), dq_ref) < TOL
+    assert rel_err(h(dk), dk_ref) < TOL
+    assert rel_err(h(dv), dv_ref) < TOL
+
+
+def test_attention_hd256_short_non_causal():
+    """Non-causal attention at head_dim 256 and S <= 256 (every query tile of
+    the short backward sees every key tile), GQA 4:1, padding mask."""
+    B, Hq, Hkv, S, hd = 2, 4, 1, 80, 256
+    q, k, v, dout = rn(B * S, Hq * hd), rn(B * S, Hkv * hd), rn(B * S, Hkv * hd), rn(B * S, Hq * hd)
+    kpad = np.ones((B, S), np.float32)
+    kpad[1, S - 9:] = 0
+    scale = hd ** -0.5
+    o_ref, lse_ref = O.attn_fwd(q, k, v, B, Hq, Hkv, S, hd, scale, False, 0, kpad)
+    o, lse = ops.attn_fwd(g(q), g(k), g(v), B, Hq, Hkv, S, hd, scale, False, 0, g(kpad))
+    assert rel_err(h(o), o_ref) < TOL
+    dq_ref, dk_ref, dv_ref = O.attn_bwd(q, k, v, o_ref, dout, lse_ref, B, Hq, Hkv, S, hd, scale, False, 0, kpad)
+    dq, dk, dv = ops.attn_bwd(g(q), g(k), g(v), o, g(dout), lse, B, Hq, Hkv, S, hd, scale, False, 0, g(kpad))
     assert rel_err(h(dq), dq_ref) < TOL
     assert rel_err(h(dk), dk_ref) < TOL
     assert rel_err(h(dv), dv_ref) < TOL
