@@ -71,6 +71,10 @@ _SIGS = {
     "orc_model_fwd_bwd": (_F, [_P, _P, _P, _P, _I, _I, _F]),
     "orc_model_forward": (_F, [_P, _P, _P, _P, _I, _I, _P]),
     "orc_model_opt_step": (_F, [_P, _F, _F, _F, _F, _F, _F]),
+    "orc_model_set_retain": (None, [_P, C.c_uint64]),
+    "orc_model_retained": (_P, [_P, _I, C.c_char_p, _I, C.POINTER(_L)]),
+    "orc_attn_probs": (None, [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _F, _I, _I, _P,
+                              _P, _P, _P, _P]),
 }
 
 
@@ -328,6 +332,23 @@ class OracleModel:
 
     def opt_step(self, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0):
         return lib().orc_model_opt_step(self.h, lr, b1, b2, eps, wd, clip)
+
+    def set_retain(self, layers):
+        """Keep the activations and activation gradients of `layers` in
+        later steps (oracle.h: orc_model_set_retain)."""
+        mask = 0
+        for l in layers:
+            mask |= 1 << l
+        lib().orc_model_set_retain(self.h, mask)
+
+    def retained(self, layer, name, grad=True):
+        """A kept activation (grad=False) or activation gradient as a copy:
+        [B*S, width], or [B, Hq, S, S] for "scores" / "probs"; None if absent."""
+        n = C.c_int64()
+        addr = lib().orc_model_retained(self.h, layer, name.encode(), 1 if grad else 0, C.byref(n))
+        if not addr:
+            return None
+        return np.ctypeslib.as_array((C.c_float * n.value).from_address(addr)).copy()
 
 
 def dropout_mask(seed, step, lid, shape, p):

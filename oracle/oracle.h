@@ -150,6 +150,13 @@ typedef struct {
   uint64_t dropout_seed;
 } orc_model_cfg;
 
+/* Scores / probabilities of one attention and their gradients in closed
+ * form, [B, Hq, S, S] each (NULL outputs skipped; dout NULL: no gradients). */
+void orc_attn_probs(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
+                    const float* v, int64_t v_rs, const float* dout, int64_t do_rs,
+                    int B, int Hq, int Hkv, int S, int hd, float scale, int causal,
+                    int window, const float* kpad, float* scores, float* probs,
+                    float* dprobs, float* dscores);
 typedef struct orc_model orc_model;
 orc_model* orc_model_create(const orc_model_cfg* cfg);
 void       orc_model_destroy(orc_model* m);
@@ -169,6 +176,17 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
 /* Forward only; writes logits [B*S, V] when logits != NULL; returns loss. */
 float orc_model_forward(orc_model* m, const int32_t* ids, const float* mask,
                         const int32_t* labels, int B, int S, float* logits);
+/* Retained intermediates (the Gemma driver's alignment dump,
+ * gemma_3_270m_lora_finetune/src/main.cpp:547-657): with bit l of layer_mask
+ * set, later forwards keep layer l's activations and backwards its
+ * activation gradients, until the next forward.  Names per layer: "x",
+ * "norm1", "q_proj", "k_proj", "v", "q_normed", "k_normed" (after the q/k
+ * norms, before RoPE), "q", "k" (after RoPE), "attn", "o_proj", "mid",
+ * "norm2", "gate", "up", "gate_act", "act", "down_proj", "out" — token-major
+ * [B·S, width] — and "scores", "probs" [B, Hq, S, S]; layer −1: "embed".
+ * orc_model_retained returns the kept buffer (NULL if absent) and its size. */
+void orc_model_set_retain(orc_model* m, uint64_t layer_mask);
+const float* orc_model_retained(const orc_model* m, int layer, const char* name, int grad, int64_t* n);
 /* clip + Adam on the LoRA params, then zero grads (main.cpp:489-505). */
 float orc_model_opt_step(orc_model* m, float lr, float b1, float b2, float eps,
                          float wd, float clip);

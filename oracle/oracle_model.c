@@ -70,6 +70,15 @@ struct orc_model {
   int B, S;
   float** act;
   int nact;
+  /* retained intermediates (orc_model_set_retain) */
+  uint64_t retain;
+  struct kept {
+    int layer, grad;
+    char name[16];
+    float* data;
+    int64_t n;
+  } * kept;
+  int nkept;
 };
 
 static void* xmalloc(size_t n) {
@@ -202,8 +211,46 @@ static void free_acts(orc_model* m) {
   m->nact = 0;
 }
 
+static void clear_kept(orc_model* m) {
+  for (int i = 0; i < m->nkept; ++i) free(m->kept[i].data);
+  free(m->kept);
+  m->kept = NULL;
+  m->nkept = 0;
+}
+
+void orc_model_set_retain(orc_model* m, uint64_t layer_mask) { m->retain = layer_mask; }
+
+const float* orc_model_retained(const orc_model* m, int layer, const char* name, int grad, int64_t* n) {
+  for (int i = 0; i < m->nkept; ++i)
+    if (m->kept[i].layer == layer && m->kept[i].grad == grad && !strcmp(m->kept[i].name, name)) {
+      if (n) *n = m->kept[i].n;
+      return m->kept[i].data;
+    }
+  if (n) *n = 0;
+  return NULL;
+}
+
+static int keeps(const orc_model* m, int layer) {
+  return layer >= 0 && layer < 64 && ((m->retain >> layer) & 1);
+}
+
+/* Copies rows x cols of src (rows ld apart) as retained (layer, name, grad). */
+static void keep(orc_model* m, int layer, const char* name, int grad, const float* src, int64_t rows,
+                 int64_t cols, int64_t ld) {
+  float* d = (float*)xmalloc(sizeof(float) * (size_t)(rows * cols));
+  for (int64_t r = 0; r < rows; ++r) memcpy(d + r * cols, src + r * ld, sizeof(float) * (size_t)cols);
+  m->kept = (struct kept*)realloc(m->kept, sizeof(struct kept) * (size_t)(m->nkept + 1));
+  struct kept* k = &m->kept[m->nkept++];
+  k->layer = layer;
+  k->grad = grad;
+  snprintf(k->name, sizeof(k->name), "%s", name);
+  k->data = d;
+  k->n = rows * cols;
+}
+
 void orc_model_destroy(orc_model* m) {
   if (!m) return;
+  clear_kept(m);
   for (int i = 0; i < m->np; ++i) {
     free(m->p[i].data); free(m->p[i].grad); free(m->p[i].m); free(m->p[i].v);
   }
@@ -403,9 +450,14 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
               e->is_f16 ? (const uint16_t*)e->data : NULL,
               gpt2 ? P(m, m->wpe) : NULL, d, sc, h);
   }
+  if (m->retain) {
+    clear_kept(m);
+    if (keeps(m, 0)) keep(m, -1, "embed", 0, h, M, d, d);
+  }
   for (int li = 0; li < c->n_layer; ++li) {
     olayer* L = &m->L[li];
     lcache* C = &cache[li];
+    const int kp = keeps(m, li);
     memset(C, 0, sizeof(*C));
     C->x = h;
     C->n1 = F(m, M * d);
@@ -431,6 +483,10 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
         C->qrs = F(m, M * H); C->krs = F(m, M * Hk);
         orc_rmsnorm_fwd(C->qraw, P(m, L->qn), M * H, hd, c->norm_eps, 1, C->q, C->qrs);
         orc_rmsnorm_fwd(C->kraw, P(m, L->kn), M * Hk, hd, c->norm_eps, 1, C->k, C->krs);
+        if (kp) {
+          keep(m, li, "q_normed", 0, C->q, M, (int64_t)H * hd, (int64_t)H * hd);
+          keep(m, li, "k_normed", 0, C->k, M, (int64_t)Hk * hd, (int64_t)Hk * hd);
+        }
       }
       double th = layer_is_local(c, li) ? c->rope_local_theta : c->rope_theta;
       orc_rope(C->q, C->qs, B, S, H, hd, th, 0);
@@ -441,6 +497,17 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
     int win = layer_is_local(c, li) ? c->sliding_window : 0;
     orc_attn_fwd(C->q, C->qs, C->k, C->ks, C->v, C->vs, B, H, Hk, S, hd,
                  attn_scale(c), 1, win, mask, C->att, (int64_t)H * hd, C->lse);
+    if (kp) {
+      const int64_t ns = (int64_t)B * H * S * S;
+      float* sc = (float*)xmalloc(sizeof(float) * (size_t)ns);
+      float* pr = (float*)xmalloc(sizeof(float) * (size_t)ns);
+      orc_attn_probs(C->q, C->qs, C->k, C->ks, C->v, C->vs, NULL, 0, B, H, Hk, S, hd, attn_scale(c), 1, win,
+                     mask, sc, pr, NULL, NULL);
+      keep(m, li, "scores", 0, sc, 1, ns, ns);
+      keep(m, li, "probs", 0, pr, 1, ns, ns);
+      free(sc);
+      free(pr);
+    }
     float* hmid = F(m, M * d);
     const olinear* lo = gpt2 ? &L->lin[G_PROJ] : &L->lin[T_O];
     C->o = F(m, M * d);
@@ -485,6 +552,33 @@ static void forward_all(orc_model* m, const int32_t* ids, const float* mask,
       for (int64_t i = 0; i < M * d; ++i) hout[i] = hmid[i] + mn[i];
     } else {
       for (int64_t i = 0; i < M * d; ++i) hout[i] = hmid[i] + C->mo[i];
+    }
+    if (kp) {
+      const int64_t qw = (int64_t)H * hd, kw = (int64_t)Hk * hd, ff = c->d_ff;
+      keep(m, li, "x", 0, C->x, M, d, d);
+      keep(m, li, "norm1", 0, C->n1, M, d, d);
+      if (!gpt2) {
+        keep(m, li, "q_proj", 0, gemma ? C->qraw : C->q, M, qw, qw);
+        keep(m, li, "k_proj", 0, gemma ? C->kraw : C->k, M, kw, kw);
+      }
+      keep(m, li, "q", 0, C->q, M, qw, C->qs);
+      keep(m, li, "k", 0, C->k, M, kw, C->ks);
+      keep(m, li, "v", 0, C->v, M, kw, C->vs);
+      keep(m, li, "attn", 0, C->att, M, qw, qw);
+      keep(m, li, "o_proj", 0, C->o, M, d, d);
+      keep(m, li, "mid", 0, C->hmid, M, d, d);
+      keep(m, li, "norm2", 0, C->n2, M, d, d);
+      keep(m, li, "gate", 0, C->gate, M, ff, ff);
+      if (C->up) keep(m, li, "up", 0, C->up, M, ff, ff);
+      keep(m, li, "act", 0, C->act, M, ff, ff);
+      keep(m, li, "down_proj", 0, C->mo, M, d, d);
+      keep(m, li, "out", 0, hout, M, d, d);
+      if (C->up) {  /* the activation of gate alone */
+        float* ga = (float*)xmalloc(sizeof(float) * (size_t)(M * ff));
+        orc_glu_fwd(C->gate, NULL, M * ff, gemma ? 0 : 1, ga);
+        keep(m, li, "gate_act", 0, ga, M, ff, ff);
+        free(ga);
+      }
     }
     h = hout;
   }
@@ -571,12 +665,16 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
   for (int li = c->n_layer - 1; li >= 0; --li) {
     olayer* L = &m->L[li];
     lcache* C = &cache[li];
+    const int kp = keeps(m, li);
+    const int64_t qw = (int64_t)H * hd, kw = (int64_t)Hk * hd, ff = c->d_ff;
+    if (kp) keep(m, li, "out", 1, dh, M, d, d);
     /* ---- MLP block: hout = hmid + [postnorm](mlp(n2)) ---- */
     const float* dmo = dh;
     if (gemma) {
       orc_rmsnorm_bwd(dh, C->mo, P(m, L->pfn), C->mrs, M, d, 1, dtmp, 0);
       dmo = dtmp;
     }
+    if (kp) keep(m, li, "down_proj", 1, dmo, M, d, d);
     if (gpt2) {
       lin_bwd(m, &L->lin[G_FC2], dmo, C->act, C->xa[G_FC2], C->xd[G_FC2], M, dact);
       orc_glu_bwd(dact, C->gate, NULL, nf, 0, dgate, NULL);
@@ -585,11 +683,22 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
     } else {
       lin_bwd(m, &L->lin[T_DOWN], dmo, C->act, C->xa[T_DOWN], C->xd[T_DOWN], M, dact);
       orc_glu_bwd(dact, C->gate, C->up, nf, gemma ? 0 : 1, dgate, dup);
+      if (kp) {
+        keep(m, li, "act", 1, dact, M, ff, ff);
+        keep(m, li, "gate", 1, dgate, M, ff, ff);
+        keep(m, li, "up", 1, dup, M, ff, ff);
+        float* dga = (float*)xmalloc(sizeof(float) * (size_t)nf);  /* d(gate_act) = dact∘up */
+        for (int64_t i = 0; i < nf; ++i) dga[i] = dact[i] * C->up[i];
+        keep(m, li, "gate_act", 1, dga, M, ff, ff);
+        free(dga);
+      }
       lin_bwd(m, &L->lin[T_GATE], dgate, C->n2, C->xa[T_GATE], C->xd[T_GATE], M, dn);
       lin_bwd(m, &L->lin[T_UP], dup, C->n2, C->xa[T_UP], C->xd[T_UP], M, dtmp);
       add_into(dn, dtmp, M * d);
+      if (kp) keep(m, li, "norm2", 1, dn, M, d, d);
       orc_rmsnorm_bwd(dn, C->hmid, P(m, L->n2w), C->rstd2, M, d, gemma, dh, 1);
     }
+    if (kp) keep(m, li, "mid", 1, dh, M, d, d);
     /* dh now holds d(hmid).  ---- attention block ---- */
     const float* dox = dh;
     if (gemma) {
@@ -599,7 +708,21 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
     lin_bwd(m, gpt2 ? &L->lin[G_PROJ] : &L->lin[T_O], dox, C->att,
             C->xa[gpt2 ? G_PROJ : T_O], C->xd[gpt2 ? G_PROJ : T_O], M, datt);
     int win = layer_is_local(c, li) ? c->sliding_window : 0;
-    const int need_dx = li > 0; /* nothing trainable below layer 0 */
+    /* nothing trainable below layer 0 (its input gradient only when retained) */
+    const int need_dx = li > 0 || kp;
+    if (kp) {
+      keep(m, li, "o_proj", 1, dox, M, d, d);
+      keep(m, li, "attn", 1, datt, M, qw, qw);
+      const int64_t ns = (int64_t)B * H * S * S;
+      float* dpr = (float*)xmalloc(sizeof(float) * (size_t)ns);
+      float* dsc = (float*)xmalloc(sizeof(float) * (size_t)ns);
+      orc_attn_probs(C->q, C->qs, C->k, C->ks, C->v, C->vs, datt, qw, B, H, Hk, S, hd, attn_scale(c), 1, win,
+                     mask, NULL, NULL, dpr, dsc);
+      keep(m, li, "probs", 1, dpr, 1, ns, ns);
+      keep(m, li, "scores", 1, dsc, 1, ns, ns);
+      free(dpr);
+      free(dsc);
+    }
     if (gpt2) {
       orc_attn_bwd(C->q, C->qs, C->k, C->ks, C->v, C->vs, C->att, (int64_t)H * hd,
                    datt, (int64_t)H * hd, C->lse, B, H, Hk, S, hd, attn_scale(c), 1,
@@ -612,9 +735,18 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
                    datt, (int64_t)H * hd, C->lse, B, H, Hk, S, hd, attn_scale(c), 1,
                    win, mask, dq, (int64_t)H * hd, dk, (int64_t)Hk * hd, dv,
                    (int64_t)Hk * hd);
+      if (kp) {
+        keep(m, li, "q", 1, dq, M, qw, qw);
+        keep(m, li, "k", 1, dk, M, kw, kw);
+        keep(m, li, "v", 1, dv, M, kw, kw);
+      }
       double th = layer_is_local(c, li) ? c->rope_local_theta : c->rope_theta;
       orc_rope(dq, (int64_t)H * hd, B, S, H, hd, th, 1);
       orc_rope(dk, (int64_t)Hk * hd, B, S, Hk, hd, th, 1);
+      if (kp && gemma) {
+        keep(m, li, "q_normed", 1, dq, M, qw, qw);
+        keep(m, li, "k_normed", 1, dk, M, kw, kw);
+      }
       if (gemma) {
         float* t1 = F(m, M * H * hd);
         float* t2 = F(m, M * Hk * hd);
@@ -623,13 +755,22 @@ float orc_model_fwd_bwd(orc_model* m, const int32_t* ids, const float* mask,
         memcpy(dq, t1, sizeof(float) * (size_t)(M * H * hd));
         memcpy(dk, t2, sizeof(float) * (size_t)(M * Hk * hd));
       }
+      if (kp) {
+        keep(m, li, "q_proj", 1, dq, M, qw, qw);
+        keep(m, li, "k_proj", 1, dk, M, kw, kw);
+      }
       lin_bwd(m, &L->lin[T_Q], dq, C->n1, C->xa[T_Q], C->xd[T_Q], M, need_dx ? dn1 : NULL);
       lin_bwd(m, &L->lin[T_K], dk, C->n1, C->xa[T_K], C->xd[T_K], M, need_dx ? dtmp : NULL);
       if (need_dx) add_into(dn1, dtmp, M * d);
       lin_bwd(m, &L->lin[T_V], dv, C->n1, C->xa[T_V], C->xd[T_V], M, need_dx ? dtmp : NULL);
       if (need_dx) {
         add_into(dn1, dtmp, M * d);
+        if (kp) keep(m, li, "norm1", 1, dn1, M, d, d);
         orc_rmsnorm_bwd(dn1, C->x, P(m, L->n1w), C->rstd1, M, d, gemma, dh, 1);
+        if (kp) {
+          keep(m, li, "x", 1, dh, M, d, d);
+          if (li == 0) keep(m, -1, "embed", 1, dh, M, d, d);
+        }
       }
     }
   }

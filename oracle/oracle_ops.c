@@ -329,6 +329,60 @@ void orc_attn_fwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
   }
 }
 
+/* Scores, probabilities and their gradients of one attention in closed form
+ * (the dense softmax-attention backward; the alignment dump's attn_scores /
+ * attn_probs, gemma_3_270m_lora_finetune/src/main.cpp:579-580,599-657):
+ * scores[b,h,i,j] = scale·q_i·k_j (−FLT_MAX where masked), probs = softmax
+ * over j, dprobs = dO_i·v_j, dscores = probs∘(dprobs − Σ_j probs·dprobs).
+ * Outputs [B, Hq, S, S]; any output may be NULL (dprobs/dscores need dout). */
+void orc_attn_probs(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
+                    const float* v, int64_t v_rs, const float* dout, int64_t do_rs,
+                    int B, int Hq, int Hkv, int S, int hd, float scale, int causal,
+                    int window, const float* kpad, float* scores, float* probs,
+                    float* dprobs, float* dscores) {
+  const int grp = Hq / Hkv;
+#pragma omp parallel
+  {
+    double* sc = (double*)malloc(sizeof(double) * (size_t)S);
+    double* dp = (double*)malloc(sizeof(double) * (size_t)S);
+#pragma omp for collapse(3) schedule(dynamic, 16)
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < Hq; ++h)
+        for (int i = 0; i < S; ++i) {
+          const int kh = h / grp;
+          const float* qi = q + ((int64_t)b * S + i) * q_rs + (int64_t)h * hd;
+          const double mx = attn_scores(qi, k, k_rs, b, kh, S, hd, scale, causal, window, kpad, i, sc);
+          const int64_t row = (((int64_t)b * Hq + h) * S + i) * S;
+          if (scores)
+            for (int j = 0; j < S; ++j) scores[row + j] = sc[j] == -INFINITY ? -3.402823466e38f : (float)sc[j];
+          double sum = 0.0;
+          for (int j = 0; j < S; ++j) {
+            sc[j] = (mx == -INFINITY || sc[j] == -INFINITY) ? 0.0 : exp(sc[j] - mx);
+            sum += sc[j];
+          }
+          for (int j = 0; j < S; ++j) sc[j] = sum > 0.0 ? sc[j] / sum : 0.0;
+          if (probs)
+            for (int j = 0; j < S; ++j) probs[row + j] = (float)sc[j];
+          if (!dout) continue;
+          const float* gi = dout + ((int64_t)b * S + i) * do_rs + (int64_t)h * hd;
+          double delta = 0.0;
+          for (int j = 0; j < S; ++j) {
+            const float* vj = v + ((int64_t)b * S + j) * v_rs + (int64_t)kh * hd;
+            double a = 0.0;
+            for (int d = 0; d < hd; ++d) a += (double)gi[d] * vj[d];
+            dp[j] = a;
+            delta += sc[j] * a;
+          }
+          for (int j = 0; j < S; ++j) {
+            if (dprobs) dprobs[row + j] = (float)dp[j];
+            if (dscores) dscores[row + j] = (float)(sc[j] * (dp[j] - delta));
+          }
+        }
+    free(sc);
+    free(dp);
+  }
+}
+
 void orc_attn_bwd(const float* q, int64_t q_rs, const float* k, int64_t k_rs,
                   const float* v, int64_t v_rs, const float* o, int64_t o_rs,
                   const float* dout, int64_t do_rs, const float* lse, int B,
