@@ -168,6 +168,25 @@ int mft_model_activation(mft_model m, int layer, const char* name,
                          const float** ptr, int64_t* rows, int64_t* cols,
                          int64_t* ld);
 
+/* Alignment-dump debug mode (the Gemma driver's --align_dump_grads,
+ * gemma_3_270m_lora_finetune/src/main.cpp:547-657; the reference model
+ * retains these gradients by default, main.cpp:328-330): with bit l of
+ * layer_mask set, later forwards also keep layer l's "q_normed", "k_normed"
+ * (q/k after Gemma3's norms, before RoPE), "gate_act" (GELU(gate)), "scores"
+ * and "probs" (the attention's scaled scores, −FLT_MAX where masked, and
+ * softmax, [B·Hq·S rows, S]) for mft_model_activation, and later backwards
+ * keep the gradients of every named activation of the layer (those of
+ * mft_model_activation, layer −1 "embed" for layer 0's input) for
+ * mft_model_activation_grad, until the next forward.  Costs extra launches
+ * and memory; 0 (the default) turns it off.  Gemma3 models only; not while
+ * a step graph is captured. */
+int mft_model_set_retain(mft_model m, uint64_t layer_mask);
+/* A retained activation gradient: device pointer to `rows` rows of `cols`
+ * floats, `ld` apart, valid until the next forward.  MFT_EINVAL when the
+ * last backward kept none of that name. */
+int mft_model_activation_grad(mft_model m, int layer, const char* name, const float** ptr, int64_t* rows,
+                              int64_t* cols, int64_t* ld);
+
 /* ---- measurement ----------------------------------------------------------
  * When enabled, HIP events are recorded on the model's stream around every
  * launch of a kernel class; mft_model_timing returns the summed duration

@@ -98,6 +98,9 @@ _SIGS = {
     "mft_model_train_step": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _F, _F, _F, _F, _F, _F, _I]),
     "mft_model_read_stats": (_I, [_P, C.POINTER(_F), C.POINTER(_L), C.POINTER(_F)]),
     "mft_model_activation": (_I, [_P, _I, C.c_char_p, C.POINTER(_P), C.POINTER(_L), C.POINTER(_L), C.POINTER(_L)]),
+    "mft_model_activation_grad": (_I, [_P, _I, C.c_char_p, C.POINTER(_P), C.POINTER(_L), C.POINTER(_L),
+                                       C.POINTER(_L)]),
+    "mft_model_set_retain": (_I, [_P, C.c_uint64]),
     "mft_model_set_timing": (_I, [_P, _I]),
     "mft_model_set_training": (_I, [_P, _I]),
     "mft_model_shard_stats": (_I, [_P, C.POINTER(_L), C.POINTER(_L), C.POINTER(_L)]),

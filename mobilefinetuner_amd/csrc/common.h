@@ -426,6 +426,24 @@ void rope_table(hipStream_t s, double theta, int hd, int npos, float2* tab);
 // (w != null, Gemma3's per-head RMSNorm with the (1 + w) scale): x is the
 // projection output the norm reads (forward) or its input saved for the
 // backward, rstd its per-row 1/rms.
+// ---- alignment-dump debug mode (debug.hip) ------------------------------------
+// Dense attention scores / probabilities [B, Hq, S, S] and their gradients
+// of one layer (token-major q/k/v/o/dout rows; lse from the forward); any
+// output may be null, gradients need dout, v and o.
+struct DebugAttn {
+  const float *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *dout = nullptr, *lse = nullptr;
+  const float* kpad = nullptr;
+  int64_t q_rs = 0, k_rs = 0, v_rs = 0, o_rs = 0, do_rs = 0;
+  int B = 0, Hq = 0, Hkv = 0, S = 0, hd = 0, causal = 1, window = 0;
+  float scale = 1.f;
+  float *scores = nullptr, *probs = nullptr, *dprobs = nullptr, *dscores = nullptr;
+};
+void debug_attn(hipStream_t s, const DebugAttn& a);
+// out = a∘b and out = GELU(x) (tanh form) over rows × cols.
+void debug_mul(hipStream_t s, const float* a, int64_t lda, const float* b, int64_t ldb, float* out, int64_t ldo,
+               int64_t rows, int64_t cols);
+void debug_gelu(hipStream_t s, const float* x, int64_t ldx, float* out, int64_t ldo, int64_t rows, int64_t cols);
+
 struct HeadRows {
   const float* in = nullptr;
   int64_t in_ld = 0;

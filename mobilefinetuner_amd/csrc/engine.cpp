@@ -195,6 +195,18 @@ struct mft_model_s {
   // input / gradient group of a layer (q|k|v, o, gate|up, down); dB and dA
   // from two whole-model launches at the end of the backward.
   bool panel = false;
+  // Alignment-dump debug mode: layers whose activations and activation
+  // gradients are retained (bit l = layer l), and the retained copies keyed
+  // by (layer, name): activations a forward does not keep as they are
+  // (q/k before RoPE, GELU(gate), attention scores and probabilities) and
+  // every activation gradient the backward forms.
+  uint64_t retain = 0;
+  struct Kept {
+    float* p = nullptr;
+    int64_t rows = 0, cols = 0;
+    size_t cap = 0;
+  };
+  std::map<std::pair<int, std::string>, Kept> kept_act, kept_grad;
   // Row scales for the fp16 matrix-core GEMMs of fp16-stored W: one
   // [max_tokens] slot per linear of a layer (written by the batched rank-r
   // launches, read by the GEMMs that follow them), then one for GEMMs whose
@@ -1092,6 +1104,75 @@ DropStream drop_stream(const mft_model_s* m) {
 
 void run_batch(mft_model_s* m, int idx, int64_t M);
 
+// ---- alignment-dump debug mode ------------------------------------------------
+bool keeps(const mft_model_s* m, int li) { return li >= 0 && li < 64 && ((m->retain >> li) & 1); }
+
+// Device buffer of the retained (layer, name) activation or gradient,
+// rows × cols floats (grown on demand; debug mode only, never captured).
+float* kept_buf(mft_model_s* m, bool grad, int layer, const char* name, int64_t rows, int64_t cols) {
+  auto& k = (grad ? m->kept_grad : m->kept_act)[{layer, name}];
+  const size_t need = (size_t)(rows * cols) * sizeof(float);
+  if (k.cap < need) {
+    if (k.p) MFT_HIP(hipFree(k.p));
+    k.p = nullptr;
+    k.cap = 0;
+    if (hipMalloc(&k.p, need) != hipSuccess) throw Error(MFT_ENOMEM, "retained debug tensor");
+    k.cap = need;
+  }
+  k.rows = rows;
+  k.cols = cols;
+  return k.p;
+}
+
+void keep_copy(mft_model_s* m, bool grad, int layer, const char* name, const float* src, int64_t rows, int64_t cols,
+               int64_t ld) {
+  float* d = kept_buf(m, grad, layer, name, rows, cols);
+  MFT_HIP(hipMemcpy2DAsync(d, cols * sizeof(float), src, ld * sizeof(float), cols * sizeof(float), rows,
+                           hipMemcpyDeviceToDevice, m->stream));
+}
+
+// q and k rows before RoPE (after Gemma3's q/k norms) of layer li, from the
+// rows after it: RoPE⁻¹ of a copy (activations: of a.q/a.k; gradients: of dq/dk).
+void keep_pre_rope(mft_model_s* m, bool grad, int li, const float* q, int64_t q_ld, const float* k, int64_t k_ld,
+                   int64_t M, int S) {
+  const mft_model_cfg& c = m->c;
+  const int64_t qw = (int64_t)c.n_head * c.head_dim, kw = (int64_t)c.n_kv_head * c.head_dim;
+  keep_copy(m, grad, li, "q_normed", q, M, qw, q_ld);
+  keep_copy(m, grad, li, "k_normed", k, M, kw, k_ld);
+  HeadRows hq, hk;
+  hq.H = c.n_head;
+  hk.H = c.n_kv_head;
+  hq.in = hq.out = kept_buf(m, grad, li, "q_normed", M, qw);
+  hk.in = hk.out = kept_buf(m, grad, li, "k_normed", M, kw);
+  hq.in_ld = hq.out_ld = qw;
+  hk.in_ld = hk.out_ld = kw;
+  qk_rope_bwd(m->stream, hq, hk, M, S, c.head_dim, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
+}
+
+// Scores and probabilities of layer li (forward), or their gradients from
+// dO = datt (backward), as dense [B, Hq, S, S] tensors.
+void keep_attention(mft_model_s* m, const Acts& a, int li, const float* mask, int nseq, int S, const float* datt) {
+  const mft_model_cfg& c = m->c;
+  DebugAttn g;
+  g.q = a.q; g.k = a.k; g.v = a.v; g.o = a.att; g.lse = a.lse; g.kpad = mask;
+  g.q_rs = a.qs; g.k_rs = a.ks; g.v_rs = a.vs; g.o_rs = (int64_t)c.n_head * c.head_dim;
+  g.B = nseq; g.Hq = c.n_head; g.Hkv = c.n_kv_head; g.S = S; g.hd = c.head_dim;
+  g.causal = 1;
+  g.window = layer_local(c, li) ? c.sliding_window : 0;
+  g.scale = attn_scale(c);
+  const int64_t rows = (int64_t)nseq * c.n_head * S;
+  if (datt) {
+    g.dout = datt;
+    g.do_rs = (int64_t)c.n_head * c.head_dim;
+    g.dprobs = kept_buf(m, true, li, "probs", rows, S);
+    g.dscores = kept_buf(m, true, li, "scores", rows, S);
+  } else {
+    g.scores = kept_buf(m, false, li, "scores", rows, S);
+    g.probs = kept_buf(m, false, li, "probs", rows, S);
+  }
+  debug_attn(m->stream, g);
+}
+
 // Whether C = x·op(W) runs on the fp16 matrix cores (lin_gemm).
 // C = x·op(W) (+ epilogue) for a linear's frozen W.  fp16-stored W runs on
 // the fp16 matrix cores with x's row scales from inv_s (written by the
@@ -1432,6 +1513,10 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       qk_rope_fwd(s, hq, hk, M, S, hd, c.norm_eps, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
     }
     attention_fwd(m, a, li, mask, nseq, S);
+    if (gemma && keeps(m, li)) {  // alignment-dump debug mode
+      keep_pre_rope(m, false, li, a.q, a.qs, a.k, a.ks, M, S);
+      keep_attention(m, a, li, mask, nseq, S, nullptr);
+    }
     if (gemma) {  // post-attention norm, residual add and pre-FFN norm in the o projection's epilogue
       const RowNorm sw = sandwich(L.pan, a.x, a.hmid, a.ors, norm2(li));
       lin_fwd(m, L.lin[T_O], a.att, M, a.o, a.xa[T_O], nullptr, nullptr, &sw);
@@ -1449,6 +1534,9 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
       glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
     }
+    if (gemma && keeps(m, li))  // GELU(gate) alone (alignment-dump debug mode)
+      debug_gelu(s, a.gate, m->fuse_gu ? 2 * c.d_ff : c.d_ff, kept_buf(m, false, li, "gate_act", M, c.d_ff), c.d_ff,
+                 M, c.d_ff);
     if (gemma) {  // post-FFN norm, residual add and the next input norm in the down projection's epilogue
       const RowNorm sw = sandwich(L.pfn, a.hmid, hout, a.mrs, norm1(li + 1));
       lin_fwd(m, L.lin[T_DOWN], a.act, M, a.mo, a.xa[T_DOWN], nullptr, nullptr, &sw);
@@ -1555,13 +1643,23 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     Acts& a = m->A[li];
     float* rin = res_in(li);
     float* rmid = res_mid(li);
-    const bool need_dx = li > 0;
+    // alignment-dump debug mode (Gemma3): this layer's activation gradients
+    // are kept, including its input's (formed at layer 0 too), and the fused
+    // norm backwards also store the GEMM output they consume (d(norm output))
+    const bool kp = gemma && keeps(m, li);
+    const int64_t qw = (int64_t)H * hd, kw = (int64_t)Hk * hd, ffw = c.d_ff;
+    const bool need_dx = li > 0 || kp;
     RowNorm nb2 = norm_bwd(a.hmid, L.n2w, gpt2 ? a.mean2 : nullptr, a.rstd2, rmid, rin);
     float* rnext = need_dx ? res_in(li - 1) : nullptr;
     RowNorm nb1 = norm_bwd(a.x, L.n1w, gpt2 ? a.mean1 : nullptr, a.rstd1, rnext, rmid);
     if (gemma) {
-      nb2 = post_bwd(nb2, li, true);                  // + this layer's post-attention norm backward
-      if (need_dx) nb1 = post_bwd(nb1, li - 1, false);  // + the next lower layer's post-FFN norm backward
+      nb2 = post_bwd(nb2, li, true);                            // + this layer's post-attention norm backward
+      if (li > 0) nb1 = post_bwd(nb1, li - 1, false);           // + the next lower layer's post-FFN norm backward
+    }
+    if (kp) {
+      nb1.skip_c = nb2.skip_c = false;
+      keep_copy(m, true, li, "out", rin, M, d, d);
+      keep_copy(m, true, li, "down_proj", dyb(li, T_DOWN, m->dtmp), M, d, d);
     }
     // ---- MLP block ----
     if (gpt2) {
@@ -1573,11 +1671,20 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       // produced rin (the layer above's, or the LM head's final norm)
       const float* dmo = gemma ? dyb(li, T_DOWN, m->dtmp) : rin;
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
+      if (kp) {
+        keep_copy(m, true, li, "act", m->dact, M, ffw, ffw);
+        debug_mul(s, m->dact, ffw, a.up, m->fuse_gu ? 2 * ffw : ffw, kept_buf(m, true, li, "gate_act", M, ffw), ffw,
+                  M, ffw);  // d(GELU(gate)) = d(act)∘up
+      }
       if (m->fuse_gu) {
         // dgate|dup in the fused [M, 2·ff] gradient, then one GEMM gives
         // dn = dgu·W_eff[d, 2·ff]ᵀ with the pre-FFN norm's backward fused
         const int n2f = 2 * c.d_ff;
         glu_bwd_rows(s, m->dact, a.gate, a.up, M, c.d_ff, n2f, gemma ? 0 : 1, a.DY[T_GATE], a.DY[T_UP]);
+        if (kp) {
+          keep_copy(m, true, li, "gate", a.DY[T_GATE], M, ffw, n2f);
+          keep_copy(m, true, li, "up", a.DY[T_UP], M, ffw, n2f);
+        }
         GemmEpilogue ep;
         ep.norm = &nb2;
         Timed t(m, CLS_LINEAR, 2.0 * M * n2f * d);
@@ -1586,14 +1693,27 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
         float* dgate = dyb(li, T_GATE, m->dgate);
         float* dup = dyb(li, T_UP, m->dup);
         glu_bwd(s, m->dact, a.gate, a.up, nf, gemma ? 0 : 1, dgate, dup);
+        if (kp) {
+          keep_copy(m, true, li, "gate", dgate, M, ffw, ffw);
+          keep_copy(m, true, li, "up", dup, M, ffw, ffw);
+        }
         lin_bwd(m, L.lin[T_GATE], dgate, a.n2, a.xa[T_GATE], M, m->dn);
         lin_bwd(m, L.lin[T_UP], dup, a.n2, a.xa[T_UP], M, m->dn, nullptr, &nb2, 1.f);  // dn += ...; norm fused
       }
     }
+    if (kp) {
+      keep_copy(m, true, li, "norm2", m->dn, M, d, d);
+      keep_copy(m, true, li, "mid", rmid, M, d, d);
+    }
     // ---- attention block ----
     // Gemma3: the post-attention norm's backward ran with the pre-FFN norm's
     const float* dox = gemma ? dyb(li, T_O, m->dtmp) : rmid;
+    if (kp) keep_copy(m, true, li, "o_proj", dox, M, d, d);
     lin_bwd(m, gpt2 ? L.lin[G_PROJ] : L.lin[T_O], dox, a.att, a.xa[gpt2 ? G_PROJ : T_O], M, m->datt);
+    if (kp) {
+      keep_copy(m, true, li, "attn", m->datt, M, qw, qw);
+      keep_attention(m, a, li, mask, nseq, S, m->datt);
+    }
     AttnArgs g{a.q, a.k, a.v, a.qs, a.ks, a.vs, nseq, H, Hk, S, hd, attn_scale(c), 1,
                layer_local(c, li) ? c.sliding_window : 0, mask};
     // algorithmic: dV, dP, dQ, dK (the recomputed scores are not counted), causal half
@@ -1626,6 +1746,12 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
                  m->ws);
         t.end();
       }
+      if (kp) {
+        keep_copy(m, true, li, "q", dq, M, qw, qld);
+        keep_copy(m, true, li, "k", dk, M, kw, kld);
+        keep_copy(m, true, li, "v", a.DY[T_V], M, kw, nt);
+        keep_pre_rope(m, true, li, dq, qld, dk, kld, M, S);
+      }
       {
         // RoPE's inverse (in place for Qwen2), then Gemma3's q/k norm
         // backward into the fused gradient; q and k rows in one launch
@@ -1643,12 +1769,21 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
         }
         qk_rope_bwd(s, hq, hk, M, S, hd, m->rope_tab[layer_local(c, li) ? 1 : 0], (int)m->max_tokens);
       }
+      if (kp) {
+        keep_copy(m, true, li, "q_proj", a.DY[T_Q], M, qw, nt);
+        keep_copy(m, true, li, "k_proj", a.DY[T_K], M, kw, nt);
+      }
       if (need_dx) {
         GemmEpilogue ep;
         ep.norm = &nb1;
         Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
         gemm(s, a.dyqkv, nt, L.lin[T_Q].weff, nt, true, false, m->dn, d, (int)M, d, (int)nt, ep, m->ws,
              t.events());
+      }
+      if (kp) {
+        keep_copy(m, true, li, "norm1", m->dn, M, d, d);
+        keep_copy(m, true, li, "x", rnext, M, d, d);
+        if (li == 0) keep_copy(m, true, -1, "embed", rnext, M, d, d);
       }
       continue;
     }
@@ -1662,6 +1797,12 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       attn_bwd(s, g, a.att, (int64_t)H * hd, m->datt, (int64_t)H * hd, a.lse, dq, (int64_t)H * hd, dk,
                (int64_t)Hk * hd, dv, (int64_t)Hk * hd, m->ws);
       t.end();
+    }
+    if (kp) {
+      keep_copy(m, true, li, "q", dq, M, qw, qw);
+      keep_copy(m, true, li, "k", dk, M, kw, kw);
+      keep_copy(m, true, li, "v", dv, M, kw, kw);
+      keep_pre_rope(m, true, li, dq, qw, dk, kw, M, S);
     }
     const float* dqx = dq;
     const float* dkx = dk;
@@ -1687,10 +1828,19 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     }
     // dn = dq·Wqᵀ + dk·Wkᵀ + dv·Wvᵀ accumulated in the GEMM epilogues, the
     // input norm's backward fused into the last one.
+    if (kp) {
+      keep_copy(m, true, li, "q_proj", dqx, M, qw, qw);
+      keep_copy(m, true, li, "k_proj", dkx, M, kw, kw);
+    }
     float* dn = need_dx ? m->dn : nullptr;
     lin_bwd(m, L.lin[T_Q], dqx, a.n1, a.xa[T_Q], M, dn);
     lin_bwd(m, L.lin[T_K], dkx, a.n1, a.xa[T_K], M, dn, nullptr, nullptr, 1.f);
     lin_bwd(m, L.lin[T_V], dv, a.n1, a.xa[T_V], M, dn, nullptr, need_dx ? &nb1 : nullptr, 1.f);
+    if (kp) {
+      keep_copy(m, true, li, "norm1", m->dn, M, d, d);
+      keep_copy(m, true, li, "x", rnext, M, d, d);
+      if (li == 0) keep_copy(m, true, -1, "embed", rnext, M, d, d);
+    }
   }
   run_batch(m, m->udb_batch, M);  // merged: U = dY·B and dB += s·dYᵀ·xa of every LoRA linear
   run_batch(m, m->db_batch, M);   // panel: dB += s·dYᵀ·xa of every LoRA linear
@@ -1852,6 +2002,9 @@ int mft_model_destroy(mft_model m) {
     if (m->ev_in) (void)hipEventDestroy(m->ev_in);
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     for (auto e : m->ev_pool) (void)hipEventDestroy(e);
+    for (auto* km : {&m->kept_act, &m->kept_grad})
+      for (auto& kv : *km)
+        if (kv.second.p) (void)hipFree(kv.second.p);
     void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss,
                     m->weff_mem, m->tables, m->rscale};
     for (void* b : bufs)
@@ -2152,11 +2305,45 @@ int mft_model_activation(mft_model m, int layer, const char* name, const float**
       else if (n == "down_proj" && gemma) set(a.mo, d, d);
       else if (n == "out") set(layer + 1 < c.n_layer ? m->A[layer + 1].x : m->h_final, d, d);
     }
+    if (!p) {  // the alignment-dump debug mode's extra activations
+      auto it = m->kept_act.find({layer, n});
+      if (it != m->kept_act.end() && it->second.p) {
+        *ptr = it->second.p;
+        if (rows) *rows = it->second.rows;
+        if (cols) *cols = it->second.cols;
+        if (ld) *ld = it->second.cols;
+        return;
+      }
+    }
     if (!p) throw Error(MFT_EINVAL, "mft_model_activation: this model keeps no activation '" + n + "'");
     *ptr = p;
     if (rows) *rows = m->last_rows;
     if (cols) *cols = w;
     if (ld) *ld = pitch;
+  });
+}
+
+int mft_model_set_retain(mft_model m, uint64_t layer_mask) {
+  return guarded([&] {
+    if (!m) throw Error(MFT_EINVAL, "null model");
+    if (layer_mask && m->c.arch != MFT_ARCH_GEMMA3)
+      throw Error(MFT_EINVAL, "mft_model_set_retain: the alignment dump's retention serves Gemma3 models");
+    if (m->capturing) throw Error(MFT_EINVAL, "mft_model_set_retain: not while a step graph is being captured");
+    m->retain = layer_mask;
+  });
+}
+
+int mft_model_activation_grad(mft_model m, int layer, const char* name, const float** ptr, int64_t* rows,
+                              int64_t* cols, int64_t* ld) {
+  return guarded([&] {
+    if (!m || !name || !ptr) throw Error(MFT_EINVAL, "null argument");
+    auto it = m->kept_grad.find({layer, name});
+    if (it == m->kept_grad.end() || !it->second.p)
+      throw Error(MFT_EINVAL, std::string("mft_model_activation_grad: no retained gradient '") + name + "'");
+    *ptr = it->second.p;
+    if (rows) *rows = it->second.rows;
+    if (cols) *cols = it->second.cols;
+    if (ld) *ld = it->second.cols;
   });
 }
 

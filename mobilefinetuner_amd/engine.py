@@ -146,6 +146,33 @@ class Model:
         call("mft_model_read_stats", self.h, C.byref(loss), C.byref(n), C.byref(gn))
         return loss.value, n.value, gn.value
 
+    # --- alignment-dump debug mode (tests) ---
+    def set_retain(self, layers):
+        """Keep the activations and activation gradients of `layers` in later
+        steps (mft_engine.h: mft_model_set_retain); [] turns it off."""
+        mask = 0
+        for l in layers:
+            mask |= 1 << l
+        call("mft_model_set_retain", self.h, C.c_uint64(mask))
+
+    def _kept(self, fn, layer, name):
+        import numpy as np
+        p, rows, cols, ld = C.c_void_p(), C.c_int64(), C.c_int64(), C.c_int64()
+        call(fn, self.h, layer, name.encode(), C.byref(p), C.byref(rows), C.byref(cols), C.byref(ld))
+        torch.cuda.synchronize()
+        n = (rows.value - 1) * ld.value + cols.value
+        flat = np.empty(n, np.float32)
+        call("mft_memcpy_d2h", self._handle(), flat.ctypes.data_as(C.c_void_p), p, flat.nbytes)
+        return np.lib.stride_tricks.as_strided(flat, (rows.value, cols.value), (ld.value * 4, 4)).copy()
+
+    def activation(self, layer, name):
+        """A kept activation of the last forward as [rows, cols] (mft_model_activation)."""
+        return self._kept("mft_model_activation", layer, name)
+
+    def activation_grad(self, layer, name):
+        """A retained activation gradient of the last backward (mft_model_activation_grad)."""
+        return self._kept("mft_model_activation_grad", layer, name)
+
     # --- timing ---
     def set_timing(self, on: bool):
         call("mft_model_set_timing", self.h, int(on))
