@@ -82,7 +82,9 @@ class EngineModel {
  protected:
   void attach_lora(int r, float alpha, int mask);
   virtual std::string normalise_name(const std::string& name) const { return name; }
-  // Called at the end of every forward (debug dumps).
+  // Called at the start (engine settings for this forward) and at the end
+  // (debug dumps) of every forward.
+  virtual void before_forward() {}
   virtual void after_forward() {}
   void ensure_engine();
 

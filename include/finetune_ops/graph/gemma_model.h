@@ -51,9 +51,10 @@ class GemmaModel : public EngineModel {
  public:
   explicit GemmaModel(const GemmaTextConfig& cfg);
   const GemmaTextConfig& config() const { return cfg_; }
-  // Gradients of intermediate activations are not kept by the fused engine;
-  // the switch is accepted for source compatibility.
-  void set_debug_retain_grads(bool) {}
+  // Whether the alignment dump (enable_debug_dump) also keeps the gradients
+  // of the dumped layers' activations for debug_tensors()[...]->grad(); on
+  // by default, as in the reference (main.cpp:328-330 turns it off).
+  void set_debug_retain_grads(bool on);
   // Handles on layer i's LoRA linears (rebuilt when the adapters change).
   GemmaBlock& get_block(int i);
 
@@ -63,11 +64,12 @@ class GemmaModel : public EngineModel {
   // files named <activation>_l<layer>.npy (hidden_states_emb.npy for the
   // scaled embedding), shaped [B, S, C] without a leading batch of one.
   void enable_debug_dump(const std::string& dir, const std::vector<int>& layers);
-  // The same activations of the last forward as tensors (views valid until
-  // the next forward), keyed as the dumps are named without ".npy".  The
-  // fused engine keeps no gradients of intermediates and never forms the
-  // [S, S] attention scores or probabilities, so those keys are absent and
-  // the tensors carry no grad().
+  // The same activations of the last forward as tensors (valid until the
+  // next forward), keyed as the dumps are named without ".npy": token-major
+  // [B, S, C], q/k norm and RoPE outputs head-major [B, H, S, hd],
+  // attn_scores / attn_probs [B, Hq, S, S].  While gradients are retained,
+  // q/k before RoPE, gate_act and the scores / probabilities exist too, and
+  // after a backward every tensor carries its gradient in grad().
   std::unordered_map<std::string, TensorPtr> debug_tensors();
   // Writes layer i's norm weights (input_layernorm, post_attention_layernorm,
   // pre_feedforward_layernorm, post_feedforward_layernorm, q_norm, k_norm) to
@@ -84,6 +86,8 @@ class GemmaModel : public EngineModel {
   std::string dump_dir_;
   std::vector<int> dump_layers_;
   bool dump_ = false;
+  bool retain_grads_ = true;
+  void before_forward() override;
   void after_forward() override;
 };
 

@@ -1396,6 +1396,7 @@ void attention_fwd(mft_model_s* m, Acts& a, int li, const float* mask, int nseq,
 // sequences each); with LoRA dropout each draws its own masks.
 void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S, bool train, int n_fwd) {
   const mft_model_cfg& c = m->c;
+  for (auto& kv : m->kept_grad) kv.second.rows = 0;  // retained gradients belong to one step
   m->fwd_dropout = train && c.lora_dropout > 0.f && c.lora_r > 0 && c.lora_mask != 0;
   m->drop_n_fwd = n_fwd;
   m->drop_rows = (int64_t)(nseq / n_fwd) * S;
@@ -2338,7 +2339,7 @@ int mft_model_activation_grad(mft_model m, int layer, const char* name, const fl
   return guarded([&] {
     if (!m || !name || !ptr) throw Error(MFT_EINVAL, "null argument");
     auto it = m->kept_grad.find({layer, name});
-    if (it == m->kept_grad.end() || !it->second.p)
+    if (it == m->kept_grad.end() || !it->second.p || it->second.rows == 0)
       throw Error(MFT_EINVAL, std::string("mft_model_activation_grad: no retained gradient '") + name + "'");
     *ptr = it->second.p;
     if (rows) *rows = it->second.rows;

@@ -361,6 +361,7 @@ TensorPtr EngineModel::forward(const TensorPtr& ids, const TensorPtr& mask) {
   // training forward (LoRA dropout) iff gradients are being recorded
   mft_check(mft_model_set_training(st_->m, autograd::Engine::instance().is_enabled() ? 1 : 0),
             "mft_model_set_training");
+  before_forward();
   mft_check(mft_model_forward_train(st_->m, static_cast<const int32_t*>(ids->device_data()),
                                     mask ? static_cast<const float*>(mask->device_data()) : nullptr, B, S),
             "mft_model_forward_train");
@@ -731,31 +732,78 @@ GemmaBlock& GemmaModel::get_block(int i) {
 }
 
 namespace {
-// (dump name, engine activation name) pairs of a Gemma layer.
-const char* const kGemmaDumps[][2] = {
-    {"hidden_before_attn", "x"},     {"hidden_after_attn_norm", "norm1"}, {"q_proj_out", "q_proj"},
-    {"k_proj_out", "k_proj"},        {"v_proj_out", "v"},                 {"q_rotary_out", "q"},
-    {"k_rotary_out", "k"},           {"attn_context", "attn"},           {"attn_out_raw", "o_proj"},
-    {"hidden_after_attn", "mid"},    {"hidden_before_mlp_norm", "mid"},  {"hidden_after_mlp_norm", "norm2"},
-    {"gate_proj_out", "gate"},       {"up_proj_out", "up"},              {"mlp_prod", "act"},
-    {"down_proj_out", "down_proj"},  {"hidden_after_mlp", "out"}};
+// (dump name, engine activation name, layout) of a Gemma layer's debug
+// tensors: token-major [B, S, C] (T), head-major [B, H, S, hd] of the query
+// (Q) or key (K) heads, or [B, Hq, S, S] (A).  The norm / RoPE outputs are
+// head-major as the driver's analytical gradients multiply them with the
+// [B, H, S, S] score gradients (main.cpp:615-651).  q/k before RoPE, GELU(gate),
+// scores and probabilities exist while the dump retains gradients.
+struct DumpKey {
+  const char* dump;
+  const char* act;
+  char layout;
+};
+const DumpKey kGemmaDumps[] = {
+    {"hidden_before_attn", "x", 'T'},       {"hidden_after_attn_norm", "norm1", 'T'},
+    {"q_proj_out", "q_proj", 'T'},          {"k_proj_out", "k_proj", 'T'},
+    {"v_proj_out", "v", 'T'},               {"q_norm_out", "q_normed", 'Q'},
+    {"k_norm_out", "k_normed", 'K'},        {"q_norm_out_pre_rope", "q_normed", 'Q'},
+    {"k_norm_out_pre_rope", "k_normed", 'K'}, {"q_rotary_out", "q", 'Q'},
+    {"k_rotary_out", "k", 'K'},             {"attn_context", "attn", 'T'},
+    {"attn_scores", "scores", 'A'},         {"attn_probs", "probs", 'A'},
+    {"attn_out_raw", "o_proj", 'T'},        {"hidden_after_attn", "mid", 'T'},
+    {"hidden_before_mlp_norm", "mid", 'T'}, {"hidden_after_mlp_norm", "norm2", 'T'},
+    {"gate_proj_out", "gate", 'T'},         {"gate_act", "gate_act", 'T'},
+    {"up_proj_out", "up", 'T'},             {"mlp_prod", "act", 'T'},
+    {"down_proj_out", "down_proj", 'T'},    {"hidden_after_mlp", "out", 'T'}};
 }  // namespace
+
+void GemmaModel::set_debug_retain_grads(bool on) { retain_grads_ = on; }
+
+void GemmaModel::before_forward() {
+  uint64_t mask = 0;
+  if (dump_ && retain_grads_) {
+    const int n = std::min(cfg_.num_hidden_layers, 64);
+    if (dump_layers_.empty()) mask = n == 64 ? ~0ull : (1ull << n) - 1;
+    for (int l : dump_layers_)
+      if (l >= 0 && l < 64) mask |= 1ull << l;
+  }
+  mft_check(mft_model_set_retain(st_->m, mask), "mft_model_set_retain");
+}
 
 std::unordered_map<std::string, TensorPtr> GemmaModel::debug_tensors() {
   std::unordered_map<std::string, TensorPtr> out;
   if (!st_) return out;
-  const float* p = nullptr;
-  int64_t rows = 0, cols = 0, ld = 0;
-  auto add = [&](const std::string& key, int layer, const char* act) {
-    if (mft_model_activation(st_->m, layer, act, &p, &rows, &cols, &ld) != 0) return;
-    const int64_t S = last_S_ > 0 ? last_S_ : rows;
-    out[key] = Tensor::view({rows / S, S, cols}, kFloat32, const_cast<float*>(p), ld, st_);
+  const int64_t S = last_S_;
+  const int64_t hd = cfg_.head_dim;
+  // engine rows [rows, cols] (rows ld apart) as a tensor of the key's layout
+  auto shaped = [&](const float* p, int64_t rows, int64_t cols, int64_t ld, char layout) -> TensorPtr {
+    const int64_t s = S > 0 ? S : rows;
+    if (layout == 'A') return Tensor::view({rows / (cfg_.num_attention_heads * s), cfg_.num_attention_heads, s, s},
+                                           kFloat32, const_cast<float*>(p), ld, st_);
+    if (layout == 'T') return Tensor::view({rows / s, s, cols}, kFloat32, const_cast<float*>(p), ld, st_);
+    // [B, S, H, hd] rows → a head-major [B, H, S, hd] copy
+    const int64_t B = rows / s, H = cols / hd;
+    auto t = std::make_shared<Tensor>(std::vector<int64_t>{B, H, s, hd}, kFloat32, kGPU);
+    const int64_t shape[4] = {B, H, s, hd}, strides[4] = {s * ld, hd, ld, 1};
+    mft_check(mft_strided_copy(detail::handle(), p, static_cast<float*>(t->device_data()), 4, shape, strides),
+              "mft_strided_copy");
+    return t;
   };
-  add("hidden_states_emb", -1, "embed");
+  auto add = [&](const std::string& key, int layer, const char* act, char layout) {
+    const float* p = nullptr;
+    int64_t rows = 0, cols = 0, ld = 0;
+    if (mft_model_activation(st_->m, layer, act, &p, &rows, &cols, &ld) != 0) return;
+    TensorPtr t = shaped(p, rows, cols, ld, layout);
+    if (mft_model_activation_grad(st_->m, layer, act, &p, &rows, &cols, &ld) == 0)
+      t->set_grad(shaped(p, rows, cols, ld, layout));
+    out[key] = t;
+  };
+  add("hidden_states_emb", -1, "embed", 'T');
   for (int l = 0; l < cfg_.num_hidden_layers; ++l) {
     if (!dump_layers_.empty() && std::find(dump_layers_.begin(), dump_layers_.end(), l) == dump_layers_.end())
       continue;
-    for (const auto& d : kGemmaDumps) add(std::string(d[0]) + "_l" + std::to_string(l), l, d[1]);
+    for (const auto& d : kGemmaDumps) add(std::string(d.dump) + "_l" + std::to_string(l), l, d.act, d.layout);
   }
   return out;
 }

@@ -748,6 +748,88 @@ static void test_gemma_resume() {
 
 // The Gemma driver's alignment-mode API: block handles and debug_params,
 // dumps, dlogits through retain_grad, and the layout ops it applies.
+// The align dump's gradients (gemma_3_270m_lora_finetune/src/main.cpp:547-657)
+// after forward + lm_cross_entropy + backward on `ids` ([1, S]): every dumped
+// tensor's grad() against the oracle's retained intermediates of the same
+// step (oracle.h: orc_model_set_retain), and the driver's analytical
+// attention gradients (dMat = dScores·scale, dQ = dMat·repeat_kv(K),
+// dK = dMatᵀ·Q, dV = Pᵀ·dContext) against the oracle's d(q), d(k), d(v).
+static void check_align_grads(GemmaModel& model, orc_model* om,
+                              std::unordered_map<std::string, TensorPtr>& dbg, const std::vector<int32_t>& ids,
+                              const GemmaTextConfig& cfg) {
+  const int S = (int)ids.size(), H = cfg.num_attention_heads, Hk = cfg.num_key_value_heads, hd = cfg.head_dim;
+  orc_model_set_retain(om, (1ull << 0) | (1ull << 2));
+  std::vector<float> mask(S, 1.f);
+  orc_model_fwd_bwd(om, ids.data(), mask.data(), ids.data(), 1, S, 1.f);
+  // token-major [S, H·hd] oracle rows → head-major [H, S, hd]
+  auto head = [&](const float* t, int heads) {
+    std::vector<float> o((size_t)heads * S * hd);
+    for (int s = 0; s < S; ++s)
+      for (int h = 0; h < heads; ++h)
+        for (int e = 0; e < hd; ++e) o[((size_t)h * S + s) * hd + e] = t[((size_t)s * heads + h) * hd + e];
+    return o;
+  };
+  const char* keys[][3] = {{"hidden_before_attn", "x", "T"},      {"hidden_after_attn_norm", "norm1", "T"},
+                           {"q_proj_out", "q_proj", "T"},         {"k_proj_out", "k_proj", "T"},
+                           {"v_proj_out", "v", "T"},              {"q_norm_out", "q_normed", "Q"},
+                           {"k_norm_out_pre_rope", "k_normed", "K"}, {"q_rotary_out", "q", "Q"},
+                           {"k_rotary_out", "k", "K"},            {"attn_context", "attn", "T"},
+                           {"attn_scores", "scores", "A"},        {"attn_probs", "probs", "A"},
+                           {"attn_out_raw", "o_proj", "T"},       {"hidden_after_attn", "mid", "T"},
+                           {"hidden_after_mlp_norm", "norm2", "T"}, {"gate_proj_out", "gate", "T"},
+                           {"gate_act", "gate_act", "T"},         {"up_proj_out", "up", "T"},
+                           {"mlp_prod", "act", "T"},              {"down_proj_out", "down_proj", "T"},
+                           {"hidden_after_mlp", "out", "T"}};
+  for (int layer : {0, 2}) {
+    const std::string L = "_l" + std::to_string(layer);
+    for (const auto& k : keys) {
+      auto it = dbg.find(k[0] + L);
+      int64_t n = 0;
+      const float* ref = orc_model_retained(om, layer, k[1], 1, &n);
+      if (it == dbg.end() || !it->second->grad() || !ref) {
+        check(std::string("align grad present ") + k[0] + L, 1.0, 0);
+        continue;
+      }
+      std::vector<float> want(ref, ref + n);
+      if (k[2][0] == 'Q') want = head(ref, H);
+      if (k[2][0] == 'K') want = head(ref, Hk);
+      auto g = it->second->grad();
+      check(std::string("align grad ") + k[0] + L,
+            g->numel() == (int64_t)want.size() ? rel_l2(g->data<float>(), want.data(), want.size()) : 1.0, 1e-4);
+    }
+  }
+  {
+    int64_t n = 0;
+    const float* ref = orc_model_retained(om, -1, "embed", 1, &n);
+    auto e = dbg["hidden_states_emb"];
+    check("align grad hidden_states_emb",
+          ref && e->grad() ? rel_l2(e->grad()->data<float>(), ref, (size_t)n) : 1.0, 1e-4);
+  }
+  // the driver's analytical attention gradients (main.cpp:599-657)
+  for (int layer : {0, 2}) {
+    const std::string L = "_l" + std::to_string(layer);
+    const float qk_scale = std::pow(cfg.query_pre_attn_scalar, -0.5f);
+    auto dMat = mul(dbg["attn_scores" + L]->grad(), qk_scale);
+    auto k_full = repeat_kv_heads(dbg["k_rotary_out" + L], H / Hk);
+    auto dQ = matmul(dMat, k_full);                            // [1, H, S, hd]
+    auto dK = matmul(transpose(dMat, -2, -1), dbg["q_rotary_out" + L]);  // per query head
+    auto G = dbg["attn_context" + L]->grad();                  // [1, S, H·hd]
+    auto Gh = permute(reshape(G, {1, S, H, hd}), {0, 2, 1, 3});
+    auto dV = matmul(transpose(dbg["attn_probs" + L], -2, -1), Gh);
+    int64_t n = 0;
+    auto want_q = head(orc_model_retained(om, layer, "q", 1, &n), H);
+    check("align analytical dq" + L, rel_l2(dQ->data<float>(), want_q.data(), want_q.size()), 1e-4);
+    for (const char* which : {"k", "v"}) {
+      auto want = head(orc_model_retained(om, layer, which, 1, &n), Hk);
+      const float* per = (which[0] == 'k' ? dK : dV)->data<float>();  // [H, S, hd]: sum each KV head's group
+      std::vector<float> sum(want.size(), 0.f);
+      for (int h = 0; h < H; ++h)
+        for (size_t i = 0; i < (size_t)S * hd; ++i) sum[(size_t)(h / (H / Hk)) * S * hd + i] += per[(size_t)h * S * hd + i];
+      check(std::string("align analytical d") + which + L, rel_l2(sum.data(), want.data(), want.size()), 1e-4);
+    }
+  }
+}
+
 static void test_gemma_debug_api() {
   const GemmaTextConfig cfg = tiny_gemma();
   GemmaModel model(cfg);
@@ -766,6 +848,10 @@ static void test_gemma_debug_api() {
   for (int64_t i = 0; i < A->numel(); ++i) a[i] = 0.01f * (float)((i % 7) - 3);
   const float* back = static_cast<const Tensor&>(*model.get_parameter("layers.1.self_attn.q_proj.lora_A")).data<float>();
   check("gemma debug_params write-through", std::abs(back[5] - 0.01f * 2.f), 0);
+  {  // the oracle gets the same LoRA-A, for the gradient checks below
+    const int oi = oracle_index(om, "layers.1.self_attn.q_proj.lora_A");
+    std::memcpy(orc_model_param_data(om, oi), a, A->numel() * 4);
+  }
   const std::string dir = "/tmp/mft_align_dump";
   model.enable_debug_dump(dir, {0, 2});
   model.dump_layer_norm_weights(0, dir);
@@ -786,7 +872,9 @@ static void test_gemma_debug_api() {
   auto dbg = model.debug_tensors();
   check("gemma debug tensors present",
         dbg.count("q_rotary_out_l0") && dbg.count("attn_context_l2") && dbg.count("hidden_states_emb") &&
-                !dbg.count("attn_scores_l0") && !dbg.count("q_rotary_out_l1") ? 0.0 : 1.0, 0);
+                dbg.count("attn_scores_l0") && dbg.count("attn_probs_l2") && dbg.count("q_norm_out_pre_rope_l0") &&
+                dbg.count("gate_act_l2") && !dbg.count("q_rotary_out_l1") ? 0.0 : 1.0, 0);
+  check_align_grads(model, om, dbg, ids, cfg);
   for (const char* f : {"/hidden_states_emb.npy", "/q_rotary_out_l0.npy", "/mlp_prod_l2.npy", "/layer0_q_norm.npy"}) {
     std::ifstream in(dir + f, std::ios::binary);
     char magic[6] = {0};

@@ -24,5 +24,7 @@ def test_cpp_operator_api_matches_oracle():
                 "gpt2 checkpoint logits equal", "qwen2 checkpoint logits equal",
                 "gemma trainer step3 loss", "gemma trainer LoRA params after 3 steps",
                 "resume adapters restored bit for bit", "resumed LoRA params after 2 more steps",
-                "gemma retain_grad dlogits", "layout matmul", "gemma trainer embedding dump values"):
+                "gemma retain_grad dlogits", "layout matmul", "gemma trainer embedding dump values",
+                "align grad attn_scores_l0", "align grad q_rotary_out_l2", "align grad hidden_states_emb",
+                "align analytical dq_l0", "align analytical dv_l2"):
         assert any(tag in ln for ln in r.stdout.splitlines()), tag
