@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "LoRA fwd+bwd tokens/sec at 1 GPU; LoRA-linear & attention % of MFMA peak"
 PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense fp32 matrix
+PEAK_FP16_MFMA = 2500.0  # TFLOP/s, MI355X dense fp16 matrix (fp16-stored W runs its GEMMs here)
 PEAK_HBM = 8000.0        # GB/s, MI355X HBM3E
 
 
@@ -284,13 +285,24 @@ def main():
             return t_ms, work, n
         t_ms, work, n = cls(CLS_LINEAR)
         ach = work / (t_ms / 1000.0) / 1e12 if t_ms > 0 else 0.0
+        # fp16-stored W: the linear and LM-head GEMMs run on the fp16 matrix
+        # cores (fp32 operand split into hi + lo fp16 halves, two fp16 products
+        # per fp32 product), so their peak is the fp16 one; the fp32 fraction
+        # is reported beside it.  Work is counted once (2·M·N·K per GEMM).
+        peak_mm = PEAK_FP16_MFMA if mc.w_fp16 else PEAK_FP32_MFMA
+        kname = ("linear-layer GEMMs (gemm_h_kernel: fp16 W on fp16 MFMA, fp32 operand as hi+lo fp16, "
+                 "rank-r panel on fp32 MFMA; fwd + dX) with their split-K reductions" if mc.w_fp16 else
+                 "linear-layer GEMMs (gemm_p_kernel / gemm_q_kernel, fwd + dX, merged LoRA "
+                 "weights) with their split-K reductions")
         result["roofline"] = {
-            "kernel": "linear-layer GEMMs (gemm_p_kernel / gemm_q_kernel, fwd + dX, merged LoRA "
-                      "weights) with their split-K reductions", "bound": "mfma",
-            "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-            "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic_bytes(args.config),
+            "kernel": kname, "bound": "mfma",
+            "achieved": round(ach, 2), "peak": peak_mm, "unit": "TFLOP/s",
+            "frac": round(ach / peak_mm, 4), "traffic": traffic_bytes(args.config),
             "launches": n, "avg_launch_us": round(1000.0 * t_ms / max(n, 1), 2),
             "timed_steps": tsteps, "ms_per_step_with_events": round(ms_timed, 4)}
+        if mc.w_fp16:
+            result["roofline"].update({"peak_fp32": PEAK_FP32_MFMA,
+                                       "frac_of_fp32_peak": round(ach / PEAK_FP32_MFMA, 4)})
         br = {}
         for name, c, unit in (("lm_head_gemm", CLS_LMHEAD, "TFLOP/s"), ("attention", CLS_ATTN, "TFLOP/s"),
                               ("cross_entropy", CLS_CE, "GB/s"), ("lora_rank_r", CLS_RANK, "GB/s")):
@@ -298,9 +310,10 @@ def main():
             if n == 0:
                 continue
             rate = work / (t_ms / 1000.0) / (1e9 if unit == "GB/s" else 1e12)
-            peak = PEAK_HBM if unit == "GB/s" else PEAK_FP32_MFMA
+            peak = PEAK_HBM if unit == "GB/s" else (
+                peak_mm if c == CLS_LMHEAD else PEAK_FP32_MFMA)
             br[name] = {"ms_per_step": round(t_ms / tsteps, 4), "achieved": round(rate, 2),
-                        "unit": unit, "frac_of_peak": round(rate / peak, 4), "launches": n}
+                        "unit": unit, "frac_of_peak": round(rate / peak, 4), "peak": peak, "launches": n}
         lin_ms = model.timing(CLS_LINEAR)[0]
         br["linear_gemm"] = {"ms_per_step": round(lin_ms / tsteps, 4)}
         result["breakdown"] = br

@@ -88,6 +88,9 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
   bool contiguous() const { return shape_.empty() || pitch_ == shape_.back(); }
   // Called after a kernel wrote the device copy: the host mirror is stale.
   void mark_device_written();
+  // The host copy is at least as new as the device copy: data() reads no
+  // device memory (and waits for nothing).
+  bool host_current() const;
 
   // ---- autograd ----
   bool requires_grad() const { return requires_grad_; }
@@ -121,8 +124,12 @@ class Tensor : public std::enable_shared_from_this<Tensor> {
   int64_t numel_ = 0;
   DType dtype_ = kFloat32;
   Device device_ = kCPU;
-  void* dev_ = nullptr;
+  mutable void* dev_ = nullptr;
   bool owns_ = false;
+  // host-built tensors of at most kLazyBytes: the device block is taken
+  // (and the host values copied there) at the first device_data()
+  static constexpr size_t kLazyBytes = 64;
+  mutable bool lazy_dev_ = false;
   int64_t pitch_ = 0;
   std::shared_ptr<void> owner_;
   // host mirror: 0 = stale, 1 = equal to the device, 2 = newer than the device

@@ -120,7 +120,8 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask,
  * ignore_index); with backward != 0 it also overwrites the logits with
  * dlogits = upstream·(softmax − onehot)/norm (norm = norm_count if > 0, else
  * the valid count), after which mft_model_backward accumulates the LoRA
- * gradients.  Asynchronous. */
+ * gradients.  loss_sum and n_valid may both be NULL (dlogits only; nothing
+ * is summed).  Asynchronous. */
 int mft_model_forward_train(mft_model m, const int32_t* ids, const float* mask,
                             int nseq, int S);
 int mft_model_logits(mft_model m, float** logits, int64_t* ld);

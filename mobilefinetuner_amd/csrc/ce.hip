@@ -413,6 +413,7 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
     hipLaunchKernelGGL((ce_row_kernel<1024, 16>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
                        ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted);
   MFT_LAUNCH_CHECK();
+  if (!loss_sum && !n_valid) return;  // dlogits only
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,
                      (const int64_t*)count_scratch, n_valid);
   MFT_LAUNCH_CHECK();

@@ -51,7 +51,7 @@ mft_handle handle() {
 float read_scalar(const TensorPtr& t) {
   if (!t || t->numel() != 1) throw std::runtime_error("expected a one-element tensor");
   if (t->dtype() != kFloat32) throw std::runtime_error("expected a float32 tensor");
-  return t->data<float>()[0];
+  return static_cast<const Tensor&>(*t).data<float>()[0];
 }
 
 }  // namespace detail
@@ -199,6 +199,15 @@ Tensor::Tensor(std::vector<int64_t> shape, const void* data, DType dtype, Device
   const size_t bytes = (size_t)numel_ * dtype_size(dtype_);
   if (bytes) {
     if (!data) throw std::invalid_argument("Tensor: null data");
+    if (device == kCPU && bytes <= kLazyBytes) {
+      // scalars and other tiny host-built values (a loss, a backward seed,
+      // an upstream gradient) stay on the host until a kernel needs them
+      host_.assign(static_cast<const char*>(data), static_cast<const char*>(data) + bytes);
+      host_state_ = 2;
+      lazy_dev_ = true;
+      owns_ = true;
+      return;
+    }
     dev_ = dev_alloc(bytes);
     owns_ = true;
     if (stage_upload(dev_, data, bytes)) {
@@ -236,8 +245,11 @@ struct MirrorGroup {
   // can be queued behind the kernels that produce the data.
   char* host = nullptr;
   hipEvent_t arrive = nullptr;  // end of the queued device→host copy (state 3)
+  hipEvent_t depart = nullptr;  // end of the queued host→device copy (state 4)
   // 0 = stale, 1 = equal to the device, 2 = newer than the device,
-  // 3 = a device→host copy is queued (equal to the device once `arrive` fires)
+  // 3 = a device→host copy is queued (equal to the device once `arrive` fires),
+  // 4 = a host→device copy is queued: equal to the device, but the host copy
+  //     is read by that copy until `depart` fires (host writes wait for it)
   int state = 0;
   int members = 0;  // views created in the group
   // zero_grad() requests not yet applied on the device: byte offset → bytes.
@@ -245,7 +257,9 @@ struct MirrorGroup {
   // whole range when every member asked (the drivers' zero_grad loop).
   std::map<size_t, size_t> zeros;
   ~MirrorGroup() {
+    if (depart) (void)hipEventSynchronize(depart);  // a queued upload may still read `host`
     if (arrive) (void)hipEventDestroy(arrive);
+    if (depart) (void)hipEventDestroy(depart);
     if (host) (void)hipHostFree(host);
   }
 };
@@ -320,8 +334,8 @@ void Tensor::sync_host(bool will_write) const {
     MirrorGroup& g = *group_;
     flush_zeros(g);
     ensure_host(g);
-    if (g.state == 3) {
-      hip_check(hipEventSynchronize(g.arrive), "hipEventSynchronize");
+    if (g.state == 3 || (g.state == 4 && will_write)) {
+      hip_check(hipEventSynchronize(g.state == 3 ? g.arrive : g.depart), "hipEventSynchronize");
       g.state = 1;
     }
     if (g.state == 0 && g.bytes > 0) {
@@ -350,11 +364,25 @@ void Tensor::sync_host(bool will_write) const {
 }
 
 void Tensor::upload_if_dirty() const {
+  if (lazy_dev_) {
+    const size_t bytes = host_.size();
+    dev_ = dev_alloc(bytes);
+    lazy_dev_ = false;
+    if (!stage_upload(dev_, host_.data(), bytes))
+      hip_check(hipMemcpy(dev_, host_.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    host_state_ = 1;
+    return;
+  }
   if (group_) {
-    flush_zeros(*group_);
-    if (group_->state == 2) {
-      hip_check(hipMemcpy(group_->dev, group_->host, group_->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
-      group_->state = 1;
+    MirrorGroup& g = *group_;
+    flush_zeros(g);
+    if (g.state == 2) {
+      // queued behind the stream's work, ahead of the kernel that asked: the
+      // pinned host copy stays untouched until `depart` (sync_host waits)
+      if (!g.depart) hip_check(hipEventCreateWithFlags(&g.depart, hipEventDisableTiming), "hipEventCreate");
+      hip_check(hipMemcpyAsync(g.dev, g.host, g.bytes, hipMemcpyHostToDevice, nullptr), "hipMemcpyAsync H2D");
+      hip_check(hipEventRecord(g.depart, nullptr), "hipEventRecord");
+      g.state = 4;
     }
     return;
   }
@@ -378,6 +406,11 @@ void* Tensor::device_data() {
 const void* Tensor::device_data() const {
   upload_if_dirty();
   return dev_;
+}
+
+bool Tensor::host_current() const {
+  if (group_) return group_->state == 1 || group_->state == 2 || group_->state == 4;
+  return host_state_ != 0 && host_.size() == (size_t)numel_ * dtype_size(dtype_);
 }
 
 void Tensor::mark_device_written() {
@@ -536,10 +569,21 @@ void require_f32(const TensorPtr& t, const char* what) {
 
 TensorPtr new_f32(const std::vector<int64_t>& shape) { return std::make_shared<Tensor>(shape, kFloat32, kGPU); }
 
+// s·a computed on the host for a one-element float32 tensor whose host copy
+// is current (a loss, a backward seed, the upstream gradient of a loss
+// scale): no kernel, no copy, no wait.  The product is the one fp32 multiply
+// the device's scale kernel performs.  Null otherwise.
+TensorPtr host_scaled(const TensorPtr& a, float s) {
+  if (a->numel() != 1 || a->dtype() != kFloat32 || !a->host_current()) return nullptr;
+  const float v = static_cast<const Tensor&>(*a).data<float>()[0] * s;
+  return std::make_shared<Tensor>(a->shape(), &v, kFloat32, kCPU);
+}
+
 struct MulNode : Node {
   float s;
   const char* name() const override { return "MulBackward"; }
   std::vector<TensorPtr> apply(const TensorPtr& g) override {
+    if (auto h = host_scaled(g, s)) return {h};
     auto out = new_f32(g->shape());
     mft_check(mft_scale(detail::handle(), fptr(g), g->numel(), s, static_cast<float*>(out->device_data())), "mft_scale");
     return {out};
@@ -611,8 +655,12 @@ struct AttnNode : Node {
 
 TensorPtr mul(const TensorPtr& a, float s) {
   require_f32(a, "mul");
-  auto out = new_f32(a->shape());
-  mft_check(mft_scale(detail::handle(), fptr(a), a->numel(), s, static_cast<float*>(out->device_data())), "mft_scale");
+  TensorPtr out = host_scaled(a, s);
+  if (!out) {
+    out = new_f32(a->shape());
+    mft_check(mft_scale(detail::handle(), fptr(a), a->numel(), s, static_cast<float*>(out->device_data())),
+              "mft_scale");
+  }
   auto n = std::make_shared<MulNode>();
   n->s = s;
   n->inputs = {a};

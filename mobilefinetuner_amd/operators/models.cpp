@@ -69,12 +69,17 @@ const int32_t* labels_ptr(const TensorPtr& labels) { return static_cast<const in
 // zeroed first, read back after the launch).
 void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int ignore, float upstream, bool sum,
               bool backward, double* ls, int64_t* nv) {
+  if (!ls && !nv) {  // dlogits only: no loss slots to clear or read
+    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
+                           nullptr, nullptr),
+              "mft_model_ce");
+    return;
+  }
   auto stats = std::make_shared<Tensor>(std::vector<int64_t>{4}, kFloat32, kGPU);
   char* p = static_cast<char*>(stats->device_data());
   mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
                          reinterpret_cast<double*>(p), reinterpret_cast<int64_t*>(p + 8)),
             "mft_model_ce");
-  if (!ls && !nv) return;
   char buf[16];  // loss sum and count are adjacent: one read-back
   hip_check(hipMemcpy(buf, p, 16, hipMemcpyDeviceToHost), "hipMemcpy D2H");
   if (ls) std::memcpy(ls, buf, 8);
