@@ -238,6 +238,24 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B,
 void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, const uint16_t* B, int64_t ldb, bool b_nk,
             float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws = Scratch(),
             const KernelEvents* ev = nullptr);
+// Column-segmented gemm_h: one launch computes C_g = A·op(B_g) (+ the
+// rank-r panel lscale·P_g·Q_g) for every segment g over the shared fp32 input
+// A — the q, k and v (or gate and up) projections of one input.  The
+// epilogue's r / qsn / qsj / lscale apply to every segment; no bias,
+// residual, beta, GELU, norm or statistics; K is not split.  Returns false
+// (nothing launched) when the segments' widths do not fit a tile plan.
+struct GemmHSegmentArg {
+  const uint16_t* B;
+  int64_t ldb;
+  int N;
+  float* C;
+  int64_t ldc;
+  const float* P;
+  const float* Q;
+};
+bool gemm_h_segments(hipStream_t s, const float* A, int64_t lda, const float* inv_s, bool b_nk,
+                     const GemmHSegmentArg* seg, int nseg, int M, int K, const GemmEpilogue& ep,
+                     const KernelEvents* ev = nullptr);
 // C = x·op(W) for fp16 W: row_scales into the front of ws, then gemm_h.
 // Returns false (nothing launched) when the shape, alignment or workspace
 // does not fit; the caller then runs gemm() with W widened.

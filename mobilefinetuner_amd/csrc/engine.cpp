@@ -1259,6 +1259,44 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
   lin_gemm(m, x, l.K, W, wu.ptr, l.N, false, y, l.N, M, l.N, l.K, ep, m->ws, t.events(), nullptr);
 }
 
+// Rank-r panel path: the projections ts[0..nt) of one shared input x (q|k|v,
+// gate|up) as one column-segmented fp16 launch, after the group's batched
+// x·Aᵀ projections (which also write x's row scales).  False, with nothing
+// launched, when a member does not qualify (no LoRA, a bias, a streamed
+// weight, a shape the fp16 kernel or a 64-wide tile does not take).
+bool lin_fwd_group(mft_model_s* m, const Layer& L, const int* ts, int nt, const float* x, int64_t M,
+                   float* const* ys, const Acts& a) {
+  static const bool on = [] {  // tuning hook: MFT_GROUP_FWD=0 keeps one launch per projection
+    const char* e = getenv("MFT_GROUP_FWD");
+    return !e || atoi(e) != 0;
+  }();
+  if (!on || !m->panel || nt < 2 || nt > 3) return false;
+  const Linear& l0 = L.lin[ts[0]];
+  const int K = l0.K, r = m->c.lora_r;
+  GemmHSegmentArg seg[3];
+  double work = 0.0;
+  for (int i = 0; i < nt; ++i) {
+    const Linear& l = L.lin[ts[i]];
+    const Param& W = m->P[l.W];
+    if (l.A < 0 || l.b >= 0 || l.K != K || l.N % 64 != 0 || W.shard >= 0 || l.rs_fwd != l0.rs_fwd || !l.rs_fwd ||
+        !f16_path(m, W, x, K, W.data, l.N, false, l.N, K, r))
+      return false;
+    seg[i] = GemmHSegmentArg{static_cast<const uint16_t*>(W.data), l.N, l.N, ys[i], l.N, a.xa[ts[i]],
+                             static_cast<const float*>(m->P[l.B].data)};
+    work += 2.0 * M * l.N * K + 2.0 * M * l.N * r;
+  }
+  run_batch(m, l0.xa_batch, M);
+  GemmEpilogue ep;
+  ep.r = r;
+  ep.qsn = r;
+  ep.qsj = 1;
+  ep.lscale = lscale(m);
+  Timed t(m, CLS_LINEAR, work);
+  MFT_CHECK_ARG(gemm_h_segments(m->stream, x, K, l0.rs_fwd, false, seg, nt, (int)M, K, ep, t.events()),
+                "segmented projection launch");
+  return true;
+}
+
 // dx = dy·Wᵀ (+ LoRA) (+ beta·dx); with gelu_grad_of = the pre-activation
 // that fed a GELU into this layer, dx is the gradient of that pre-activation
 // instead; norm: the backward of the norm that produced x, applied to dx.
@@ -1491,9 +1529,13 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
       Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
       gemm(s, a.n1, d, L.lin[T_Q].weff, nt, false, false, a.qkv, nt, (int)M, nt, d, ep, m->ws, t.events());
     } else {
-      lin_fwd(m, L.lin[T_Q], a.n1, M, gemma ? a.qraw : a.q, a.xa[T_Q], nullptr);
-      lin_fwd(m, L.lin[T_K], a.n1, M, gemma ? a.kraw : a.k, a.xa[T_K], nullptr);
-      lin_fwd(m, L.lin[T_V], a.n1, M, a.v, a.xa[T_V], nullptr);
+      static const int qkv[3] = {T_Q, T_K, T_V};
+      float* const ys[3] = {gemma ? a.qraw : a.q, gemma ? a.kraw : a.k, a.v};
+      if (!lin_fwd_group(m, L, qkv, 3, a.n1, M, ys, a)) {
+        lin_fwd(m, L.lin[T_Q], a.n1, M, ys[0], a.xa[T_Q], nullptr);
+        lin_fwd(m, L.lin[T_K], a.n1, M, ys[1], a.xa[T_K], nullptr);
+        lin_fwd(m, L.lin[T_V], a.n1, M, ys[2], a.xa[T_V], nullptr);
+      }
     }
     {
       // Gemma3's per-head q/k RMSNorms and RoPE (in place for Qwen2), q and
@@ -1531,8 +1573,12 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
            t.events());
       glu_fwd_rows(s, a.gate, a.up, M, c.d_ff, n2f, gemma ? 0 : 1, a.act);
     } else {
-      lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
-      lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
+      static const int gu[2] = {T_GATE, T_UP};
+      float* const ys[2] = {a.gate, a.up};
+      if (!lin_fwd_group(m, L, gu, 2, a.n2, M, ys, a)) {
+        lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
+        lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
+      }
       glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
     }
     if (gemma && keeps(m, li))  // GELU(gate) alone (alignment-dump debug mode)

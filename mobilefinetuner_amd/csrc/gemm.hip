@@ -29,6 +29,7 @@
 #include <cfloat>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include <hip/hip_ext.h>
@@ -1146,6 +1147,20 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
+// A column segment of a segmented launch: output columns [n0, next n0) of
+// the launch take their own B, C and rank-r panel (P, Q) — the q, k and v
+// (or gate and up) projections of one shared input in one launch.
+struct GemmHSegment {
+  int n0;
+  const uint16_t* B;
+  int64_t ldb;
+  float* C;
+  int64_t ldc;
+  const float* P;
+  const float* Q;
+};
+constexpr int kMaxGemmHSegments = 3;
+
 struct GemmHParams {
   const float* A;      // fp32 [M][lda]
   const float* inv_s;  // [M] row scales 1/s_m (powers of two), or null (s = 1)
@@ -1158,6 +1173,8 @@ struct GemmHParams {
   int splits, spread;
   float* partial;
   GemmEpilogue ep;
+  int nseg;  // > 1: column segments (unsplit K, every segment a whole number of BN-wide tiles)
+  GemmHSegment seg[kMaxGemmHSegments];
 };
 
 // C = diag(inv_s)·(hi + lo)·op(B) (+ the rank-r panel and epilogue of
@@ -1197,7 +1214,26 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   if (!tile_of(p, tile, split)) return;
   const int tm_idx = tile % p.tiles_m;
   const int tn_idx = tile / p.tiles_m;
-  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int m0 = tm_idx * BM;
+  int n0 = tn_idx * BN;
+  static_assert(kMaxGemmHSegments == 3, "segment selects below");
+  if (p.nseg > 1) {  // the tile's column segment (uniform): its operands, columns relative to it
+    // selects over constant indices only: a computed index into the kernel
+    // arguments would copy them to scratch memory
+    const int g = p.nseg > 2 && n0 >= p.seg[2].n0 ? 2 : n0 >= p.seg[1].n0 ? 1 : 0;
+#define MFT_SEG(f) (g == 0 ? p.seg[0].f : g == 1 ? p.seg[1].f : p.seg[2].f)
+    const int nb = MFT_SEG(n0);
+    const int ne = g == 0 ? p.seg[1].n0 : g == 1 && p.nseg > 2 ? p.seg[2].n0 : p.N;
+    p.B = MFT_SEG(B);
+    p.ldb = MFT_SEG(ldb);
+    p.C = MFT_SEG(C);
+    p.ldc = MFT_SEG(ldc);
+    p.ep.P = MFT_SEG(P);
+    p.ep.Q = MFT_SEG(Q);
+#undef MFT_SEG
+    n0 -= nb;
+    p.N = ne - nb;
+  }
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nk = (kend - kbeg) / BK;  // whole panels (checked on the host)
@@ -1746,6 +1782,19 @@ PlanH plan_gemm_h(int M, int N, int K, size_t ws_bytes, bool stats) {
 
 bool gemm_wide_plan(int M, int N) { return cdiv(M, 128) * cdiv(N, 128) >= 1024; }
 
+// Tuning hooks MFT_GEMM_PLAN / MFT_GEMMH_PLAN: "bm,bn,splits" forces every
+// launch; "M,N,K:bm,bn,splits;..." forces the listed shapes only.  Returns
+// false when the variable forces nothing for this shape.
+static bool forced_plan(const char* env, int M, int N, int K, int& bm, int& bn, int& sp) {
+  if (!env) return false;
+  if (!strchr(env, ':')) return sscanf(env, "%d,%d,%d", &bm, &bn, &sp) == 3;
+  for (const char* e = env; e && *e; e = strchr(e, ';') ? strchr(e, ';') + 1 : nullptr) {
+    int m = 0, n = 0, k = 0;
+    if (sscanf(e, "%d,%d,%d:%d,%d,%d", &m, &n, &k, &bm, &bn, &sp) == 6 && m == M && n == N && k == K) return true;
+  }
+  return false;
+}
+
 void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb, bool b_nk,
           bool b_f16, float* C, int64_t ldc, int M, int N, int K, const GemmEpilogue& ep,
           Scratch ws, const KernelEvents* ev) {
@@ -1782,13 +1831,14 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   }
 
   Plan pl = plan_gemm(M, N, K, ws.ptr ? ws.bytes : 0);
-  // Tuning hook: MFT_GEMM_PLAN="bm,bn,splits" forces the launch shape
+  // Tuning hook: MFT_GEMM_PLAN="bm,bn,splits" (or per shape, "M,N,K:bm,bn,splits;...") forces the launch shape
   // (bm×bn ∈ {128×128, 64×128, 64×64}, or "64,0,s" for the quadrant kernel);
   // same arithmetic, other tiling.
-  static const char* forced = getenv("MFT_GEMM_PLAN");
+  static const char* forced_env = getenv("MFT_GEMM_PLAN");
+  int bm = 0, bn = 0, sp = 0;
+  const bool forced = forced_plan(forced_env, M, N, K, bm, bn, sp);
   if (forced && !ep.stats) {
-    int bm = 0, bn = 0, sp = 0;
-    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 &&
+    if (sp >= 1 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64) ||
          ((bm == 32 || bm == 64 || bm == 128) && (bn == 0 || bn == 1))) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
@@ -1833,6 +1883,8 @@ void gemm(hipStream_t s, const float* A, int64_t lda, const void* B, int64_t ldb
   int splits = pl.splits;
   p.k_chunk = (int)(cdiv(cdiv(K, splits), bk) * bk);
   splits = (int)cdiv(K, p.k_chunk);
+  static const bool log_plans = getenv("MFT_GEMM_PLAN_LOG") != nullptr;  // tuning hook: print each launch's plan
+  if (log_plans) fprintf(stderr, "gemm %d,%d,%d:%d,%d,%d norm=%d main=%d\n", M, N, K, pl.bm, pl.bn, splits, nm ? 1 : 0, n_main);
   MFT_CHECK_ARG(!ep.stats || splits == 1, "row statistics need an unsplit K");
   // The whole-panel kernels address a tile's K-slice through 32-bit buffer
   // offsets from the tile's first row / column.
@@ -1920,11 +1972,12 @@ void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, cons
   p.ep = ep;
   p.partial = nullptr;
   PlanH pl = plan_gemm_h(M, N, K, ws.ptr ? ws.bytes : 0, ep.stats != nullptr);
-  // Tuning hook: MFT_GEMMH_PLAN="bm,bn,splits" forces the launch shape.
-  static const char* forced = getenv("MFT_GEMMH_PLAN");
+  // Tuning hook: MFT_GEMMH_PLAN="bm,bn,splits" (or per shape, "M,N,K:bm,bn,splits;...") forces the launch shape.
+  static const char* forced_env = getenv("MFT_GEMMH_PLAN");
+  int bm = 0, bn = 0, sp = 0;
+  const bool forced = forced_plan(forced_env, M, N, K, bm, bn, sp);
   if (forced && !ep.stats) {
-    int bm = 0, bn = 0, sp = 0;
-    if (sscanf(forced, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1 && sp <= 64 &&
+    if (sp >= 1 && sp <= 64 &&
         ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
         (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
       pl = {bm, bn, sp};
@@ -1937,6 +1990,8 @@ void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, cons
   int splits = pl.splits;
   p.k_chunk = (int)(cdiv(cdiv(K, splits), 32) * 32);
   splits = (int)cdiv(K, p.k_chunk);
+  static const bool log_plans = getenv("MFT_GEMM_PLAN_LOG") != nullptr;
+  if (log_plans) fprintf(stderr, "gemm_h %d,%d,%d:%d,%d,%d norm=%d\n", M, N, K, pl.bm, pl.bn, splits, nm ? 1 : 0);
   MFT_CHECK_ARG(((int64_t)pl.bm * p.lda + p.k_chunk) * 4 < (int64_t(1) << 32) &&
                     (b_nk ? (int64_t)pl.bn * p.ldb + p.k_chunk : (int64_t)p.k_chunk * p.ldb + pl.bn) * 2 <
                         (int64_t(1) << 32),
@@ -1956,6 +2011,64 @@ void gemm_h(hipStream_t s, const float* A, int64_t lda, const float* inv_s, cons
   gemm_finish(s, splits, dispatch_events, ev, ws.ptr, M, N, C, ldc, ep, nm);
 }
 
+bool gemm_h_segments(hipStream_t s, const float* A, int64_t lda, const float* inv_s, bool b_nk,
+                     const GemmHSegmentArg* seg, int nseg, int M, int K, const GemmEpilogue& ep,
+                     const KernelEvents* ev) {
+  MFT_CHECK_ARG(seg && nseg >= 2 && nseg <= kMaxGemmHSegments && M > 0 && K > 0, "segmented GEMM: 2 or 3 segments");
+  MFT_CHECK_ARG(A && lda >= K && lda % 4 == 0 && ((uintptr_t)A & 15) == 0, "segmented GEMM: A");
+  MFT_CHECK_ARG(!ep.bias && !ep.resid && ep.beta == 0.f && !ep.gelu_out && !ep.gelu_grad_of && !ep.stats &&
+                    !(ep.norm && ep.norm->kind != NORM_NONE),
+                "segmented GEMM: plain outputs plus the rank-r panel only");
+  int N = 0;
+  bool all64 = true, all128 = true;
+  for (int g = 0; g < nseg; ++g) {
+    const GemmHSegmentArg& a = seg[g];
+    MFT_CHECK_ARG(a.B && a.C && a.N > 0 && gemm_h_ok(a.N, K, b_nk, ep.r) && a.ldb % 8 == 0 &&
+                      (b_nk ? a.ldb >= K : a.ldb >= a.N) && a.ldc >= a.N && ((uintptr_t)a.B & 15) == 0,
+                  "segmented GEMM: segment shape");
+    MFT_CHECK_ARG((ep.r > 0) == (a.P != nullptr && a.Q != nullptr), "segmented GEMM: rank panel per segment");
+    all64 = all64 && a.N % 64 == 0;
+    all128 = all128 && a.N % 128 == 0;
+    N += a.N;
+  }
+  PlanH pl = plan_gemm_h(M, N, K, 0, false);  // no workspace: unsplit
+  static const char* forced_env = getenv("MFT_GEMMH_PLAN");
+  int bm = 0, bn = 0, sp = 0;
+  if (forced_plan(forced_env, M, N, K, bm, bn, sp) && sp == 1 &&
+      ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)))
+    pl = {bm, bn, 1};
+  if (pl.bn == 128 && !all128) pl = {64, 64, 1};
+  if (!all64) return false;
+  GemmHParams p{};
+  p.A = A; p.inv_s = inv_s; p.B = seg[0].B; p.C = seg[0].C;
+  p.lda = lda; p.ldb = seg[0].ldb; p.ldc = seg[0].ldc;
+  p.M = M; p.N = N; p.K = K;
+  p.ep = ep;
+  p.ep.P = seg[0].P;  // selects the rank-panel kernel; each tile takes its segment's panel
+  p.ep.Q = seg[0].Q;
+  p.partial = nullptr;
+  p.k_chunk = K;
+  p.nseg = nseg;
+  for (int g = 0, n0 = 0; g < nseg; n0 += seg[g].N, ++g) {
+    p.seg[g] = GemmHSegment{n0, seg[g].B, seg[g].ldb, seg[g].C, seg[g].ldc, seg[g].P, seg[g].Q};
+    MFT_CHECK_ARG((b_nk ? (int64_t)pl.bn * seg[g].ldb + K : (int64_t)K * seg[g].ldb + pl.bn) * 2 < (int64_t(1) << 32),
+                  "GEMM operand too large for 32-bit buffer offsets");
+  }
+  MFT_CHECK_ARG(((int64_t)pl.bm * lda + K) * 4 < (int64_t(1) << 32), "GEMM operand too large for 32-bit buffer offsets");
+  static const bool log_plans = getenv("MFT_GEMM_PLAN_LOG") != nullptr;
+  if (log_plans) fprintf(stderr, "gemm_h_seg %d,%d,%d:%d,%d,1 nseg=%d\n", M, N, K, pl.bm, pl.bn, nseg);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (ev) MFT_HIP(hipStreamIsCapturing(s, &cap));
+  const bool dispatch_events = ev && ev->start && ev->stop && cap == hipStreamCaptureStatusNone;
+  if (ev && ev->start && !dispatch_events) MFT_HIP(hipEventRecord(ev->start, s));
+  t_gemm_events = dispatch_events ? ev : nullptr;
+  if (pl.bm == 128) launch_h<128, 128>(s, p, b_nk, 1);
+  else if (pl.bn == 128) launch_h<64, 128>(s, p, b_nk, 1);
+  else launch_h<64, 64>(s, p, b_nk, 1);
+  t_gemm_events = nullptr;
+  if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
+  return true;
+}
 
 bool gemm_f16w(hipStream_t s, const float* x, int64_t ldx, const void* W, int64_t ldw, bool b_nk, float* C,
                int64_t ldc, int M, int N, int K, const GemmEpilogue& ep, Scratch ws, const KernelEvents* ev) {
