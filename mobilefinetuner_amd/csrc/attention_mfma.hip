@@ -1465,15 +1465,26 @@ __device__ __forceinline__ void attn_bwd_s256_dkdv(const AttnP& p, int bid, floa
   const int h = hb % p.Hq, b = hb / p.Hq;
   const int grp = p.Hq / p.Hkv;
   const int kh = h / grp;
-  const int kt = bid / (p.Hq * p.B);  // heaviest (first) key tiles first
+  // With query chunks (nqc > 1, cq = 16·CH queries each) the unit is (key
+  // tile, chunk): the last chunk of every key tile first (causal: the
+  // fullest), then the earlier chunks, each heaviest key tile first.
+  const int nt = (p.S + 15) / 16;
+  const int item = bid / (p.Hq * p.B);
+  const int kt = item % nt;
+  const int qc = p.nqc > 1 ? p.nqc - 1 - item / nt : 0;
   const int k0 = 16 * kt;
   const int kj = k0 + li;  // this lane's key (S column)
   const int64_t tok0 = (int64_t)b * p.S;
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
   const bool kvalid = kj < p.S && (!kpb || kpb[min(kj, p.S - 1)] > 0.5f);
   const int klast = min(k0 + 15, p.S - 1);
-  const int qt_lo = (p.causal ? k0 : 0) / 16;
-  const int qt_hi = (p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1) / 16;
+  int qt_lo = (p.causal ? k0 : 0) / 16;
+  int qt_hi = (p.window > 0 ? min(p.S - 1, klast + p.window - 1) : p.S - 1) / 16;
+  if (p.nqc > 1) {  // this chunk's query tiles; an empty chunk is never read back
+    qt_lo = max(qt_lo, qc * (p.cq / 16));
+    qt_hi = min(qt_hi, (qc + 1) * (p.cq / 16) - 1);
+    if (qt_lo > qt_hi) return;  // whole workgroup, before any barrier
+  }
   const float qk2 = p.scale * kLog2e;
   const int64_t lrow0 = ((int64_t)b * p.Hq + h) * p.S;
 
@@ -1573,15 +1584,17 @@ __device__ __forceinline__ void attn_bwd_s256_dkdv(const AttnP& p, int bid, floa
       }
     if (qt < qt_hi) cur = nxt;
   }
-  // dK, dV [key k0 + 4g + v][dim d0 + 16c + i] of this wave's slice
-  const bool direct = grp == 1;
+  // dK, dV [key k0 + 4g + v][dim d0 + 16c + i] of this wave's slice; partial
+  // rows [chunk][B·S][Hq][HD] for GQA groups or query chunks
+  const bool direct = grp == 1 && p.nqc <= 1;
+  const int64_t prow = (int64_t)qc * p.B * p.S;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int gk = k0 + 4 * lg + v;
     if (gk >= p.S) continue;
     const int64_t tok = tok0 + gk;
-    float* dkr = (direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + (tok * p.Hq + h) * HD) + d0 + li;
-    float* dvr = (direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + (tok * p.Hq + h) * HD) + d0 + li;
+    float* dkr = (direct ? p.dk + tok * p.dk_rs + (int64_t)kh * HD : p.pdk + ((prow + tok) * p.Hq + h) * HD) + d0 + li;
+    float* dvr = (direct ? p.dv + tok * p.dv_rs + (int64_t)kh * HD : p.pdv + ((prow + tok) * p.Hq + h) * HD) + d0 + li;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       dkr[16 * c] = dkacc[c][v] * p.scale;
@@ -1605,7 +1618,12 @@ __device__ __forceinline__ void attn_bwd_s256_dq(const AttnP& p, int bid, float*
   // its second half lands on the CUs of the first, so dQ tile j shares a CU
   // with dK/dV key tile j (heaviest first) — a causal pair sums to S/16 + 1
   // inner tiles wherever it lands, and a heavy tile finishes alone on its CU.
-  const int qt = bid / (p.Hq * p.B);
+  // With key chunks (nkc > 1, ckq = 16·CH keys each) the unit is (query
+  // tile, chunk), the first chunks first.
+  const int nt = (p.S + 15) / 16;
+  const int item = bid / (p.Hq * p.B);
+  const int qt = item % nt;
+  const int kc = p.nkc > 1 ? item / nt : 0;
   const int q0 = 16 * qt;
   const int kh = h / (p.Hq / p.Hkv);
   const int qi = q0 + li;
@@ -1613,8 +1631,13 @@ __device__ __forceinline__ void attn_bwd_s256_dq(const AttnP& p, int bid, float*
   const int64_t tok0 = (int64_t)b * p.S;
   const float* kpb = p.kpad ? p.kpad + (int64_t)b * p.S : nullptr;
   const int qlast = min(q0 + 15, p.S - 1);
-  const int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
-  const int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  int kt_hi = (p.causal ? qlast : p.S - 1) / 16;
+  int kt_lo = p.window > 0 ? max(0, q0 - p.window + 1) / 16 : 0;
+  if (p.nkc > 1) {  // this chunk's key tiles; an empty chunk is never read back
+    kt_lo = max(kt_lo, kc * (p.ckq / 16));
+    kt_hi = min(kt_hi, (kc + 1) * (p.ckq / 16) - 1);
+    if (kt_lo > kt_hi) return;  // whole workgroup, before any barrier
+  }
   const int jhi = qok ? (p.causal ? qi : p.S - 1) : -1;
   const int jlo = p.window > 0 ? qi - p.window + 1 : 0;
   const float qk2 = p.scale * kLog2e;
@@ -1705,14 +1728,22 @@ __device__ __forceinline__ void attn_bwd_s256_dq(const AttnP& p, int bid, float*
       for (int t = 0; t < 4; ++t) dqacc[c] = mfma4(ds[t], kb[c][t], dqacc[c]);
     if (kt < kt_hi) cur = nxt;
   }
-  // dQ [query q0 + 4g + v][dim d0 + 16c + i] of this wave's slice
+  // dQ [query q0 + 4g + v][dim d0 + 16c + i] of this wave's slice (with key
+  // chunks: the unscaled partial row [chunk][B·S][Hq][HD], summed and scaled
+  // by attn_dq_sum_kernel)
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int gq = q0 + 4 * lg + v;
     if (gq >= p.S) continue;
-    float* dqr = p.dq + (tok0 + gq) * p.dq_rs + (int64_t)h * HD + d0 + li;
+    if (p.nkc > 1) {
+      float* dqr = p.pdq + (((int64_t)kc * p.B * p.S + tok0 + gq) * p.Hq + h) * HD + d0 + li;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) dqr[16 * c] = dqacc[c][v] * p.scale;
+      for (int c = 0; c < NC; ++c) dqr[16 * c] = dqacc[c][v];
+    } else {
+      float* dqr = p.dq + (tok0 + gq) * p.dq_rs + (int64_t)h * HD + d0 + li;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) dqr[16 * c] = dqacc[c][v] * p.scale;
+    }
   }
 }
 
@@ -1927,15 +1958,41 @@ bool use_short256_bwd(const AttnArgs& a) {
   return mode != 0 && a.hd == 256 && a.S <= 256;
 }
 
+// Causal chains longer than s256_chunk_tiles() tiles (16 rows each) are cut
+// into chunks — the dK/dV role's query range, the dQ role's key range — so
+// no workgroup runs more than that many dependent tile steps; the chunks'
+// partial rows are summed in chunk order by attn_partial_sum_kernel /
+// attn_dq_sum_kernel.  Tuning hook: MFT_ATTN_S256_CHUNK = tiles per chunk
+// (0: unsplit).
+int s256_chunk_tiles() {
+  static const int t = [] {
+    const char* e = getenv("MFT_ATTN_S256_CHUNK");
+    return e ? atoi(e) : 8;
+  }();
+  return t;
+}
+
 void bwd_short256_launch(hipStream_t s, AttnP& p) {
   set_lds(attn_bwd_short256, kS256Lds);
-  const int tiles = (int)(cdiv(p.S, 16) * p.Hq * p.B);
-  hipLaunchKernelGGL(attn_bwd_short256, dim3((unsigned)(2 * tiles)), dim3(64 * kS256W), kS256Lds, s, p, tiles);
+  const int nt = (int)cdiv(p.S, 16);
+  const int ch = s256_chunk_tiles();
+  const int nch = ch > 0 && nt > ch ? std::min<int>((int)cdiv(nt, ch), kMaxBwdChunks) : 1;
+  const int ctiles = (int)cdiv(nt, nch);  // tiles per chunk
+  p.nqc = p.nkc = nch;
+  p.cq = p.ckq = 16 * ctiles;
+  const int tiles = (int)(nt * p.Hq * p.B);
+  hipLaunchKernelGGL(attn_bwd_short256, dim3((unsigned)(2 * tiles * nch)), dim3(64 * kS256W), kS256Lds, s, p,
+                     tiles * nch);
   MFT_LAUNCH_CHECK();
-  if (p.Hq != p.Hkv) {
+  if (p.Hq != p.Hkv || nch > 1) {
     const int64_t total = (int64_t)p.B * p.S * p.Hkv * (256 / 4);
     hipLaunchKernelGGL(attn_partial_sum_kernel<256>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
                        dim3(256), 0, s, p, 16);
+    MFT_LAUNCH_CHECK();
+  }
+  if (nch > 1) {
+    const int64_t total = (int64_t)p.B * p.S * p.Hq * (256 / 4);
+    hipLaunchKernelGGL(attn_dq_sum_kernel<256>, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, 16);
     MFT_LAUNCH_CHECK();
   }
 }
@@ -2055,11 +2112,12 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs, co
     a.hd == 64 ? bwd_short_launch<64>(s, p) : bwd_short_launch<128>(s, p);
     return;
   }
-  if (short_ok && use_short256_bwd(a)) {  // delta formed in-kernel; GQA partials after the delta rows
-    if (a.Hq != a.Hkv) {
-      p.pdk = ws.ptr + (rows + 3) / 4 * 4;
-      p.pdv = p.pdk + rows * a.hd;
-    }
+  if (short_ok && use_short256_bwd(a)) {  // delta formed in-kernel; partials after the delta rows
+    // dK, dV per (query chunk, query head), then dQ per key chunk: at most
+    // kMaxBwdChunks each (attn_bwd_scratch_floats)
+    p.pdk = ws.ptr + (rows + 3) / 4 * 4;
+    p.pdv = p.pdk + kMaxBwdChunks * rows * a.hd;
+    p.pdq = p.pdv + kMaxBwdChunks * rows * a.hd;
     bwd_short256_launch(s, p);
     return;
   }
@@ -2094,6 +2152,7 @@ size_t attn_bwd_scratch_floats(const AttnArgs& a) {
   const BwdPlan pl = bwd_plan(a);
   const size_t rows = (size_t)a.B * a.S * a.Hq;
   size_t n = (rows + 3) / 4 * 4;  // covers the short kernels' need too
+  if (use_short256_bwd(a)) return n + 3 * (size_t)kMaxBwdChunks * rows * (size_t)a.hd;
   if (a.Hq != a.Hkv || pl.nqc > 1) n += 2 * (size_t)pl.nqc * rows * (size_t)a.hd;
   if (pl.nkc > 1) n += (size_t)pl.nkc * rows * (size_t)a.hd;
   return n;
