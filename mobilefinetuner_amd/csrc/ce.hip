@@ -114,7 +114,8 @@ template <int BLOCK, int H>
 __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S,
     int64_t V, int64_t ld, int ignore_index, float upstream, int64_t norm_count,
-    int64_t* __restrict__ cnt, int* bad, float* dlogits, float* __restrict__ row_nll, int counted) {
+    int64_t* __restrict__ cnt, int* bad, float* dlogits, float* __restrict__ row_nll, int counted,
+    float* __restrict__ dl_inv_s) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
   __shared__ int sc[NW];
@@ -131,6 +132,7 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
+    if (dx && dl_inv_s && tid == 0) dl_inv_s[row] = 1.f;  // a zero row
     return;
   }
   if (blockIdx.x == 0 && oor && bad) atomicOr(bad, 1);
@@ -217,6 +219,13 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(
   if (!dx) return;
   const int64_t n = norm_count > 0 ? norm_count : n_valid;
   const float g = n > 0 ? upstream / (float)n : 0.f;
+  if (dl_inv_s && tid == 0) {
+    // row scale of the dlogits for the fp16 GEMM that consumes them, from a
+    // bound on the row's max |dlogit| = |g|·max(max_j p_j, 1 − p_label)
+    const float pmax = __builtin_amdgcn_exp2f(m - lse2);
+    const float plab = __builtin_amdgcn_exp2f(fmaf(xl, kLog2e, -lse2));
+    dl_inv_s[row] = row_inv_scale(fabsf(g) * fmaxf(pmax, 1.f - plab));
+  }
   // dlogits = (softmax − onehot(label))·g; every element is read before the
   // same thread writes it.
   for (int64_t j = tid; j < head; j += BLOCK) {
@@ -270,7 +279,8 @@ template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     const float* logits, const int32_t* __restrict__ labels, int B, int S, int64_t V, int64_t ld,
     int ignore_index, float upstream, int64_t norm_count, int64_t* __restrict__ cnt, int* bad, float* dlogits,
-    float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld, int counted) {
+    float* __restrict__ row_nll, const float2* __restrict__ stats, int64_t stats_ld, int counted,
+    float* __restrict__ dl_inv_s) {
   constexpr int NW = BLOCK / 64, U = 4;
   __shared__ float sm[NW], ss[NW];
   __shared__ int sc[NW];
@@ -287,6 +297,7 @@ __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
     if (dx)
       for (int64_t j = tid; j < V; j += BLOCK) dx[j] = 0.f;
     if (tid == 0) row_nll[row] = 0.f;
+    if (dx && dl_inv_s && tid == 0) dl_inv_s[row] = 1.f;  // a zero row
     return;
   }
   if (blockIdx.x == 0 && oor && bad) atomicOr(bad, 1);
@@ -327,6 +338,13 @@ __global__ __launch_bounds__(BLOCK) void ce_row_stats_kernel(
   if (!dx) return;
   const int64_t n = norm_count > 0 ? norm_count : n_valid;
   const float g = n > 0 ? upstream / (float)n : 0.f;
+  if (dl_inv_s && tid == 0) {
+    // row scale of the dlogits for the fp16 GEMM that consumes them, from a
+    // bound on the row's max |dlogit| = |g|·max(max_j p_j, 1 − p_label)
+    const float pmax = __builtin_amdgcn_exp2f(m - lse2);
+    const float plab = __builtin_amdgcn_exp2f(fmaf(xl, kLog2e, -lse2));
+    dl_inv_s[row] = row_inv_scale(fabsf(g) * fmaxf(pmax, 1.f - plab));
+  }
   const int64_t head = std::min<int64_t>((4 - (((uintptr_t)x >> 2) & 3)) & 3, V);
   const int64_t n4 = (V - head) / 4;
   const int64_t tail0 = head + 4 * n4;
@@ -384,7 +402,8 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
                 float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label,
-                const float2* row_stats, int64_t stats_ld) {
+                const float2* row_stats, int64_t stats_ld, float* dl_inv_s) {
+  if (!dlogits) dl_inv_s = nullptr;
   MFT_CHECK_ARG(B > 0 && S > 0 && V > 0 && ld >= V, "empty or bad row stride");
   MFT_CHECK_ARG(count_scratch && row_nll, "scratch required");
   const int64_t rows = (int64_t)B * S;
@@ -405,13 +424,15 @@ void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
     MFT_CHECK_ARG(stats_ld >= cdiv(V, 64), "row statistics pitch");
     hipLaunchKernelGGL((ce_row_stats_kernel<1024>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
                        ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll,
-                       row_stats, stats_ld, counted);
+                       row_stats, stats_ld, counted, dl_inv_s);
   } else if (V <= 13 * 4096)
     hipLaunchKernelGGL((ce_row_kernel<1024, 13>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted,
+                       dl_inv_s);
   else
     hipLaunchKernelGGL((ce_row_kernel<1024, 16>), dim3((unsigned)rows), dim3(1024), 0, s, logits, labels, B, S, V,
-                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted);
+                       ld, ignore_index, upstream, norm_count, count_scratch, bad_label, dlogits, row_nll, counted,
+                       dl_inv_s);
   MFT_LAUNCH_CHECK();
   if (!loss_sum && !n_valid) return;  // dlogits only
   hipLaunchKernelGGL(ce_sum_kernel, dim3(1), dim3(256), 0, s, (const float*)row_nll, rows, loss_sum,

@@ -373,13 +373,15 @@ void attn_bwd(hipStream_t s, const AttnArgs& a, const float* o, int64_t o_rs,
 size_t attn_bwd_scratch_floats(const AttnArgs& a);
 
 // logits rows have stride ld (>= V); dlogits (may alias logits) uses the same.
+// dl_inv_s (nullable; with dlogits): per row, the row_inv_scale of a bound on
+// the row's max |dlogit|, for the fp16 matrix-core GEMM that reads dlogits.
 // A target is valid iff label != ignore_index and 0 <= label < V; other
 // labels count as ignored, and set *bad_label (device int, nullable) to 1.
 void ce_fwd_bwd(hipStream_t s, const float* logits, const int32_t* labels,
                 int B, int S, int64_t V, int64_t ld, int ignore_index, float upstream,
                 int64_t norm_count, double* loss_sum, int64_t* n_valid,
                 float* dlogits, float* row_nll, int64_t* count_scratch, int* bad_label = nullptr,
-                const float2* row_stats = nullptr, int64_t stats_ld = 0);
+                const float2* row_stats = nullptr, int64_t stats_ld = 0, float* dl_inv_s = nullptr);
 
 void dequant_f16(hipStream_t s, const uint16_t* src, float* dst, int64_t n);
 void quant_f16(hipStream_t s, const float* src, uint16_t* dst, int64_t n);

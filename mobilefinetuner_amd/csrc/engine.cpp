@@ -212,6 +212,10 @@ struct mft_model_s {
   // launches, read by the GEMMs that follow them), then one for GEMMs whose
   // input no batched launch reads.
   float* rscale = nullptr;
+  // row scales of the dlogits, written by the CE backward for the LM head's
+  // dH GEMM on the fp16 path (fresh until that GEMM reads them)
+  float* dl_rscale = nullptr;
+  bool dl_rs_fresh = false;
   void* weff_mem = nullptr;
   void* tables = nullptr;  // device: MergeJob[n_merge], then RankJob[]
   const MergeJob* d_merge = nullptr;
@@ -1024,8 +1028,9 @@ void build_lora_tables(mft_model_s* m) {
 void alloc_row_scales(mft_model_s* m) {
   bool any_f16 = false;
   for (const Param& p : m->P) any_f16 = any_f16 || p.f16;
-  if (any_f16 && hipMalloc(&m->rscale, (size_t)(T_MAX + 1) * m->max_tokens * sizeof(float)) != hipSuccess)
+  if (any_f16 && hipMalloc(&m->rscale, (size_t)(T_MAX + 2) * m->max_tokens * sizeof(float)) != hipSuccess)
     throw Error(MFT_ENOMEM, "row scales");
+  if (m->rscale) m->dl_rscale = m->rscale + (int64_t)(T_MAX + 1) * m->max_tokens;
 }
 
 // ---- timing helpers -------------------------------------------------------------
@@ -1435,6 +1440,7 @@ void attention_fwd(mft_model_s* m, Acts& a, int li, const float* mask, int nseq,
 void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, int S, bool train, int n_fwd) {
   const mft_model_cfg& c = m->c;
   for (auto& kv : m->kept_grad) kv.second.rows = 0;  // retained gradients belong to one step
+  m->dl_rs_fresh = false;                              // new logits: no dlogits scales yet
   m->fwd_dropout = train && c.lora_dropout > 0.f && c.lora_r > 0 && c.lora_mask != 0;
   m->drop_n_fwd = n_fwd;
   m->drop_rows = (int64_t)(nseq / n_fwd) * S;
@@ -1619,8 +1625,10 @@ void cross_entropy(mft_model_s* m, const int32_t* labels, int n_micro, int seqs,
     ce_fwd_bwd(m->stream, lg, labels + row0, seqs, S, c.vocab, m->ldv, -100, upstream, 0,
                m->d_loss + m->n_micro_pending, m->d_cnt + m->n_micro_pending, backward ? lg : nullptr,
                m->row_nll + row0, m->d_tmpcnt, m->d_err + 1,
-               m->stats_fresh ? m->row_stats + row0 * m->stats_ld : nullptr, m->stats_ld);
+               m->stats_fresh ? m->row_stats + row0 * m->stats_ld : nullptr, m->stats_ld,
+               backward && m->dl_rscale ? m->dl_rscale + row0 : nullptr);
     t.end();
+    if (backward && m->dl_rscale) m->dl_rs_fresh = true;
     m->n_micro_pending++;
   }
 }
@@ -1682,7 +1690,8 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
     head.norm = &nf;
     const WeightUse wh(m, m->wte);
     lin_gemm(m, m->logits, m->ldv, E, wh.ptr, d, false, m->dn, d, M, d, (int)c.vocab, head, m->ws, t.events(),
-             nullptr, CLS_LMHEAD);
+             m->dl_rs_fresh ? m->dl_rscale : nullptr, CLS_LMHEAD);
+    m->dl_rs_fresh = false;
   }
   const int64_t nf = M * c.d_ff;
   for (int li = top; li >= 0; --li) {
@@ -2198,8 +2207,12 @@ int mft_model_ce(mft_model m, const int32_t* labels, int nseq, int S, int ignore
       throw Error(MFT_EINVAL, "mft_model_ce: no forward of this shape is pending");
     if (m->api_dlogits) throw Error(MFT_EINVAL, "mft_model_ce: the logits were already turned into dlogits");
     ce_fwd_bwd(m->stream, m->logits, labels, nseq, S, m->c.vocab, m->ldv, ignore_index, upstream, norm_count,
-               loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt, m->d_err + 1);
-    if (backward) m->api_dlogits = true;
+               loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt, m->d_err + 1, nullptr, 0,
+               backward && m->dl_rscale ? m->dl_rscale : nullptr);
+    if (backward) {
+      m->api_dlogits = true;
+      m->dl_rs_fresh = m->dl_rscale != nullptr;
+    }
   });
 }
 
