@@ -256,6 +256,22 @@ struct GemmHSegmentArg {
 bool gemm_h_segments(hipStream_t s, const float* A, int64_t lda, const float* inv_s, bool b_nk,
                      const GemmHSegmentArg* seg, int nseg, int M, int K, const GemmEpilogue& ep,
                      const KernelEvents* ev = nullptr);
+// K-segmented gemm_h over [N,K] B: C = Σ_g A[:, k0_g : k0_g + K_g]·B_gᵀ
+// (+ Σ_g lscale·P_g·Q_g, ep.r per segment), with A's column blocks scaled by
+// the largest of the segments' row scales — the dX of the q, k and v (or gate
+// and up) projections, their dY side by side in A.  The epilogue, split-K and
+// a row norm as in gemm_h.  Segments' K in whole 32-deep panels; nseg·r ≤ 32.
+struct GemmHKSegmentArg {
+  const uint16_t* B;  // fp16 [N][ldb]
+  int64_t ldb;
+  int K;
+  const float* inv_s;  // row scales of A's column block
+  const float* P;
+  const float* Q;
+};
+void gemm_h_ksegments(hipStream_t s, const float* A, int64_t lda, const GemmHKSegmentArg* seg, int nseg, float* C,
+                      int64_t ldc, int M, int N, const GemmEpilogue& ep, Scratch ws,
+                      const KernelEvents* ev = nullptr);
 // C = x·op(W) for fp16 W: row_scales into the front of ws, then gemm_h.
 // Returns false (nothing launched) when the shape, alignment or workspace
 // does not fit; the caller then runs gemm() with W widened.

@@ -255,6 +255,13 @@ struct mft_model_s {
   // gate|up as one projection (column blocks of one [d, 2·ff] W_eff) and
   // one dX GEMM, when both are merged LoRA linears without bias
   bool fuse_gu = false;
+  // fp16-W rank-r panel path with LoRA on all of q, k, v (gate and up): one
+  // column-segmented launch for their forward, one K-segmented launch for
+  // their dX (each projection keeps its own W), with the fused layouts below
+  bool seg_qkv = false, seg_gu = false;
+  // fused activation layouts: q|k|v outputs and their dY as column blocks of
+  // one [M, nqkv] buffer, gate|up of one [M, 2·ff] (fuse_* or seg_*)
+  bool lay_qkv = false, lay_gu = false;
   // operator-level split points: shape of the forward whose activations are
   // kept (0 = none) and whether its logits buffer now holds dlogits
   int api_nseq = 0, api_S = 0;
@@ -669,11 +676,38 @@ bool gu_fusable(const mft_model_s* m) {
   return true;
 }
 
+// The rank-r panel path's segmented launches (gemm_h_segments forward,
+// gemm_h_ksegments dX) for linears t0 .. t0+n-1 of every layer: each a LoRA
+// linear over fp16 W resident in HBM (no shard store), no bias, one input
+// width, output widths in 64-column tiles, and n·r ≤ 32 for the dX's rank
+// panels.  Tuning hook: MFT_GROUP_FWD=0 keeps one launch per projection.
+bool segment_fusable(const mft_model_s* m, int t0, int n) {
+  static const bool on = [] {
+    const char* e = getenv("MFT_GROUP_FWD");
+    return !e || atoi(e) != 0;
+  }();
+  const mft_model_cfg& c = m->c;
+  if (!on || c.arch == MFT_ARCH_GPT2 || !lora_batched(m) || lora_merge(m) || c.shard_budget > 0 ||
+      n * c.lora_r > 32)
+    return false;
+  for (const auto& L : m->L)
+    for (int t = t0; t < t0 + n; ++t) {
+      const Linear& l = L.lin[t];
+      if (l.A < 0 || l.b >= 0 || !m->P[l.W].f16 || l.K != L.lin[t0].K || l.N % 64 != 0 || l.K % 32 != 0)
+        return false;
+    }
+  return true;
+}
+
 void alloc_acts(mft_model_s* m) {
   const mft_model_cfg& c = m->c;
   m->fuse_qkv = qkv_fusable(m);
   m->fuse_gu = gu_fusable(m);
   m->nqkv = c.n_head * c.head_dim + 2 * c.n_kv_head * c.head_dim;
+  m->seg_qkv = segment_fusable(m, T_Q, 3);
+  m->seg_gu = segment_fusable(m, T_GATE, 2);
+  m->lay_qkv = m->fuse_qkv || m->seg_qkv;
+  m->lay_gu = m->fuse_gu || m->seg_gu;
   const int64_t M = m->max_tokens;
   const int64_t d = c.d, H = c.n_head, Hk = c.n_kv_head, hd = c.head_dim, ff = c.d_ff, r = c.lora_r;
   const bool gpt2 = c.arch == MFT_ARCH_GPT2, gemma = c.arch == MFT_ARCH_GEMMA3;
@@ -692,7 +726,7 @@ void alloc_acts(mft_model_s* m) {
         a.k = a.q + d;
         a.v = a.q + 2 * d;
         a.qs = a.ks = a.vs = 3 * d;
-      } else if (m->fuse_qkv) {
+      } else if (m->lay_qkv) {
         // one [M, nqkv] projection output: q|k|v (Qwen2), qraw|kraw|v (Gemma3)
         const int64_t nq = H * hd, nk = Hk * hd, nt = m->nqkv;
         a.qkv = b.f(M * nt);
@@ -733,10 +767,10 @@ void alloc_acts(mft_model_s* m) {
           if (c.lora_dropout > 0.f) L.lin[t].xd = b.f(M * L.lin[t].K);
           a.xa[t] = b.f(M * r);
           a.U[t] = b.f(M * r);
-          if (m->fuse_qkv && t < 3) {  // views of the fused gradient
+          if (m->lay_qkv && t < 3) {  // views of the fused gradient
             a.DY[t] = a.dyqkv + (t == 0 ? 0 : H * hd + (t - 1) * Hk * hd);
             a.dy_ld[t] = m->nqkv;
-          } else if (m->fuse_gu && (t == T_GATE || t == T_UP)) {
+          } else if (m->lay_gu && (t == T_GATE || t == T_UP)) {
             if (t == T_GATE) a.dygu = b.f(M * 2 * ff);
             a.DY[t] = a.dygu + (t == T_GATE ? 0 : ff);
             a.dy_ld[t] = 2 * ff;
@@ -753,7 +787,7 @@ void alloc_acts(mft_model_s* m) {
       a.n2 = b.f(M * d);
       a.rstd2 = b.f(M);
       if (gpt2) a.mean2 = b.f(M);
-      if (m->fuse_gu) {
+      if (m->lay_gu) {
         a.gu = b.f(M * 2 * ff);
         a.gate = a.gu;
         a.up = a.gu + ff;
@@ -1270,12 +1304,8 @@ void lin_fwd(mft_model_s* m, const Linear& l, const float* x, int64_t M, float* 
 // launched, when a member does not qualify (no LoRA, a bias, a streamed
 // weight, a shape the fp16 kernel or a 64-wide tile does not take).
 bool lin_fwd_group(mft_model_s* m, const Layer& L, const int* ts, int nt, const float* x, int64_t M,
-                   float* const* ys, const Acts& a) {
-  static const bool on = [] {  // tuning hook: MFT_GROUP_FWD=0 keeps one launch per projection
-    const char* e = getenv("MFT_GROUP_FWD");
-    return !e || atoi(e) != 0;
-  }();
-  if (!on || !m->panel || nt < 2 || nt > 3) return false;
+                   float* const* ys, int64_t ldy, const Acts& a) {
+  if (!m->panel || nt < 2 || nt > 3) return false;
   const Linear& l0 = L.lin[ts[0]];
   const int K = l0.K, r = m->c.lora_r;
   GemmHSegmentArg seg[3];
@@ -1286,8 +1316,8 @@ bool lin_fwd_group(mft_model_s* m, const Layer& L, const int* ts, int nt, const 
     if (l.A < 0 || l.b >= 0 || l.K != K || l.N % 64 != 0 || W.shard >= 0 || l.rs_fwd != l0.rs_fwd || !l.rs_fwd ||
         !f16_path(m, W, x, K, W.data, l.N, false, l.N, K, r))
       return false;
-    seg[i] = GemmHSegmentArg{static_cast<const uint16_t*>(W.data), l.N, l.N, ys[i], l.N, a.xa[ts[i]],
-                             static_cast<const float*>(m->P[l.B].data)};
+    seg[i] = GemmHSegmentArg{static_cast<const uint16_t*>(W.data), l.N, l.N, ys[i], ldy > 0 ? ldy : l.N,
+                             a.xa[ts[i]], static_cast<const float*>(m->P[l.B].data)};
     work += 2.0 * M * l.N * K + 2.0 * M * l.N * r;
   }
   run_batch(m, l0.xa_batch, M);
@@ -1300,6 +1330,33 @@ bool lin_fwd_group(mft_model_s* m, const Layer& L, const int* ts, int nt, const 
   MFT_CHECK_ARG(gemm_h_segments(m->stream, x, K, l0.rs_fwd, false, seg, nt, (int)M, K, ep, t.events()),
                 "segmented projection launch");
   return true;
+}
+
+// Rank-r panel path: dX of the projections ts[0..nt) of one input, whose dY
+// are column blocks of dy (pitch ldy), as one K-segmented fp16 launch after
+// the group's batched U = dY·B projections (which write each dY block's row
+// scales); dx null: the projections only (their dA still needs U).
+void lin_bwd_group(mft_model_s* m, const Layer& L, const int* ts, int nt, const float* dy, int64_t ldy, int64_t M,
+                   float* dx, const GemmEpilogue& ep_in) {
+  const Linear& l0 = L.lin[ts[0]];
+  run_batch(m, l0.u_batch, M);
+  if (!dx) return;
+  const int r = m->c.lora_r;
+  GemmHKSegmentArg seg[3];
+  double work = 0.0;
+  for (int i = 0; i < nt; ++i) {
+    const Linear& l = L.lin[ts[i]];
+    seg[i] = GemmHKSegmentArg{static_cast<const uint16_t*>(m->P[l.W].data), l.N, l.N, l.rs_bwd, l.u,
+                              static_cast<const float*>(m->P[l.A].data)};
+    work += 2.0 * M * l.N * l.K + 2.0 * M * l.K * r;
+  }
+  GemmEpilogue ep = ep_in;
+  ep.r = r;
+  ep.qsn = 1;
+  ep.qsj = l0.K;
+  ep.lscale = lscale(m);
+  Timed t(m, CLS_LINEAR, work);
+  gemm_h_ksegments(m->stream, dy, ldy, seg, nt, dx, l0.K, (int)M, l0.K, ep, m->ws, t.events());
 }
 
 // dx = dy·Wᵀ (+ LoRA) (+ beta·dx); with gelu_grad_of = the pre-activation
@@ -1537,7 +1594,9 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     } else {
       static const int qkv[3] = {T_Q, T_K, T_V};
       float* const ys[3] = {gemma ? a.qraw : a.q, gemma ? a.kraw : a.k, a.v};
-      if (!lin_fwd_group(m, L, qkv, 3, a.n1, M, ys, a)) {
+      const bool grouped = lin_fwd_group(m, L, qkv, 3, a.n1, M, ys, m->lay_qkv ? m->nqkv : 0, a);
+      MFT_CHECK_ARG(grouped || !m->seg_qkv, "segmented q|k|v projection did not qualify");
+      if (!grouped) {
         lin_fwd(m, L.lin[T_Q], a.n1, M, ys[0], a.xa[T_Q], nullptr);
         lin_fwd(m, L.lin[T_K], a.n1, M, ys[1], a.xa[T_K], nullptr);
         lin_fwd(m, L.lin[T_V], a.n1, M, ys[2], a.xa[T_V], nullptr);
@@ -1546,7 +1605,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     {
       // Gemma3's per-head q/k RMSNorms and RoPE (in place for Qwen2), q and
       // k rows in one launch
-      const int64_t raw_ld = m->fuse_qkv ? m->nqkv : 0;
+      const int64_t raw_ld = m->lay_qkv ? m->nqkv : 0;
       HeadRows hq, hk;
       hq.H = (int)H;
       hk.H = (int)Hk;
@@ -1581,14 +1640,17 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
     } else {
       static const int gu[2] = {T_GATE, T_UP};
       float* const ys[2] = {a.gate, a.up};
-      if (!lin_fwd_group(m, L, gu, 2, a.n2, M, ys, a)) {
+      const bool grouped = lin_fwd_group(m, L, gu, 2, a.n2, M, ys, m->lay_gu ? 2 * c.d_ff : 0, a);
+      MFT_CHECK_ARG(grouped || !m->seg_gu, "segmented gate|up projection did not qualify");
+      if (!grouped) {
         lin_fwd(m, L.lin[T_GATE], a.n2, M, a.gate, a.xa[T_GATE], nullptr);
         lin_fwd(m, L.lin[T_UP], a.n2, M, a.up, a.xa[T_UP], nullptr);
       }
-      glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
+      if (m->lay_gu) glu_fwd_rows(s, a.gate, a.up, M, c.d_ff, 2 * c.d_ff, gemma ? 0 : 1, a.act);
+      else glu_fwd(s, a.gate, a.up, M * c.d_ff, gemma ? 0 : 1, a.act);
     }
     if (gemma && keeps(m, li))  // GELU(gate) alone (alignment-dump debug mode)
-      debug_gelu(s, a.gate, m->fuse_gu ? 2 * c.d_ff : c.d_ff, kept_buf(m, false, li, "gate_act", M, c.d_ff), c.d_ff,
+      debug_gelu(s, a.gate, m->lay_gu ? 2 * c.d_ff : c.d_ff, kept_buf(m, false, li, "gate_act", M, c.d_ff), c.d_ff,
                  M, c.d_ff);
     if (gemma) {  // post-FFN norm, residual add and the next input norm in the down projection's epilogue
       const RowNorm sw = sandwich(L.pfn, a.hmid, hout, a.mrs, norm1(li + 1));
@@ -1729,12 +1791,13 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
       lin_bwd(m, L.lin[T_DOWN], dmo, a.act, a.xa[T_DOWN], M, m->dact);
       if (kp) {
         keep_copy(m, true, li, "act", m->dact, M, ffw, ffw);
-        debug_mul(s, m->dact, ffw, a.up, m->fuse_gu ? 2 * ffw : ffw, kept_buf(m, true, li, "gate_act", M, ffw), ffw,
+        debug_mul(s, m->dact, ffw, a.up, m->lay_gu ? 2 * ffw : ffw, kept_buf(m, true, li, "gate_act", M, ffw), ffw,
                   M, ffw);  // d(GELU(gate)) = d(act)∘up
       }
-      if (m->fuse_gu) {
+      if (m->lay_gu) {
         // dgate|dup in the fused [M, 2·ff] gradient, then one GEMM gives
-        // dn = dgu·W_eff[d, 2·ff]ᵀ with the pre-FFN norm's backward fused
+        // dn = dgu·W_eff[d, 2·ff]ᵀ (panel path: over the two W as K segments)
+        // with the pre-FFN norm's backward fused
         const int n2f = 2 * c.d_ff;
         glu_bwd_rows(s, m->dact, a.gate, a.up, M, c.d_ff, n2f, gemma ? 0 : 1, a.DY[T_GATE], a.DY[T_UP]);
         if (kp) {
@@ -1743,8 +1806,14 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
         }
         GemmEpilogue ep;
         ep.norm = &nb2;
-        Timed t(m, CLS_LINEAR, 2.0 * M * n2f * d);
-        gemm(s, a.dygu, n2f, L.lin[T_GATE].weff, n2f, true, false, m->dn, d, (int)M, d, n2f, ep, m->ws, t.events());
+        if (m->fuse_gu) {
+          Timed t(m, CLS_LINEAR, 2.0 * M * n2f * d);
+          gemm(s, a.dygu, n2f, L.lin[T_GATE].weff, n2f, true, false, m->dn, d, (int)M, d, n2f, ep, m->ws,
+               t.events());
+        } else {
+          static const int gu[2] = {T_GATE, T_UP};
+          lin_bwd_group(m, L, gu, 2, a.dygu, n2f, M, m->dn, ep);
+        }
       } else {
         float* dgate = dyb(li, T_GATE, m->dgate);
         float* dup = dyb(li, T_UP, m->dup);
@@ -1787,10 +1856,11 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
               need_dx ? &nb1 : nullptr);  // LN backward fused
       continue;
     }
-    if (m->fuse_qkv) {
+    if (m->lay_qkv) {
       // dq|dk|dv land in the fused [M, nqkv] gradient (Gemma3: dq, dk first
       // through RoPE's inverse and the q/k norms' backward), then one GEMM
-      // gives dn = dqkv·W_eff[d, nqkv]ᵀ with the input norm's backward fused.
+      // gives dn = dqkv·W_eff[d, nqkv]ᵀ (panel path: over the three W as K
+      // segments) with the input norm's backward fused.
       const int64_t nt = m->nqkv;
       float* dq = gemma ? m->dq : a.DY[T_Q];
       float* dk = gemma ? m->dk : a.DY[T_K];
@@ -1829,7 +1899,12 @@ void backward(mft_model_s* m, const float* mask, int nseq, int S) {
         keep_copy(m, true, li, "q_proj", a.DY[T_Q], M, qw, nt);
         keep_copy(m, true, li, "k_proj", a.DY[T_K], M, kw, nt);
       }
-      if (need_dx) {
+      if (m->seg_qkv) {
+        GemmEpilogue ep;
+        ep.norm = &nb1;
+        static const int qkv[3] = {T_Q, T_K, T_V};
+        lin_bwd_group(m, L, qkv, 3, a.dyqkv, nt, M, need_dx ? m->dn : nullptr, ep);
+      } else if (need_dx) {
         GemmEpilogue ep;
         ep.norm = &nb1;
         Timed t(m, CLS_LINEAR, 2.0 * M * nt * d);
@@ -2353,14 +2428,14 @@ int mft_model_activation(mft_model m, int layer, const char* name, const float**
       else if (n == "q") set(a.q, hq, a.qs);
       else if (n == "k") set(a.k, hk, a.ks);
       else if (n == "v") set(a.v, hk, a.vs);
-      else if (n == "q_proj" && gemma) set(a.qraw, hq, m->fuse_qkv ? m->nqkv : hq);
-      else if (n == "k_proj" && gemma) set(a.kraw, hk, m->fuse_qkv ? m->nqkv : hk);
+      else if (n == "q_proj" && gemma) set(a.qraw, hq, m->lay_qkv ? m->nqkv : hq);
+      else if (n == "k_proj" && gemma) set(a.kraw, hk, m->lay_qkv ? m->nqkv : hk);
       else if (n == "attn") set(a.att, hq, hq);
       else if (n == "o_proj" && gemma) set(a.o, d, d);
       else if (n == "mid") set(a.hmid, d, d);
       else if (n == "norm2") set(a.n2, d, d);
-      else if (n == "gate") set(a.gate, c.d_ff, m->fuse_gu ? 2 * c.d_ff : c.d_ff);
-      else if (n == "up" && !gpt2) set(a.up, c.d_ff, m->fuse_gu ? 2 * c.d_ff : c.d_ff);
+      else if (n == "gate") set(a.gate, c.d_ff, m->lay_gu ? 2 * c.d_ff : c.d_ff);
+      else if (n == "up" && !gpt2) set(a.up, c.d_ff, m->lay_gu ? 2 * c.d_ff : c.d_ff);
       else if (n == "act") set(a.act, c.d_ff, c.d_ff);
       else if (n == "down_proj" && gemma) set(a.mo, d, d);
       else if (n == "out") set(layer + 1 < c.n_layer ? m->A[layer + 1].x : m->h_final, d, d);

@@ -1160,6 +1160,18 @@ struct GemmHSegment {
   const float* Q;
 };
 constexpr int kMaxGemmHSegments = 3;
+// A K segment of a K-segmented launch ([N,K] B only): reduction indices
+// [k0, next k0) take their own B (fp16 [N][ldb]), the row scales of their A
+// columns and their rank-r panel — dX = Σ_g dY_g·W_gᵀ over the q, k and v (or
+// gate and up) projections, whose dY are column blocks of one A.
+struct GemmHKSegment {
+  int k0;
+  const uint16_t* B;
+  int64_t ldb;
+  const float* inv_s;
+  const float* P;
+  const float* Q;
+};
 
 struct GemmHParams {
   const float* A;      // fp32 [M][lda]
@@ -1175,6 +1187,8 @@ struct GemmHParams {
   GemmEpilogue ep;
   int nseg;  // > 1: column segments (unsplit K, every segment a whole number of BN-wide tiles)
   GemmHSegment seg[kMaxGemmHSegments];
+  int nkseg;  // > 1: K segments (B_NK; every segment a whole number of 32-deep panels)
+  GemmHKSegment kseg[kMaxGemmHSegments];
 };
 
 // C = diag(inv_s)·(hi + lo)·op(B) (+ the rank-r panel and epilogue of
@@ -1255,7 +1269,23 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(p.A + (int64_t)m0 * p.lda + kbeg);
   const __amdgpu_buffer_rsrc_t rsb =
       buf_rsrc(p.B + (B_NK ? (int64_t)n0 * p.ldb + kbeg : (int64_t)kbeg * p.ldb + n0));
+  // K segments: every segment's B based at the tile's first column (its own
+  // pitch); a panel takes the segment holding its first k (selects over
+  // constant indices keep the kernel arguments in scalar registers)
+  static_assert(kMaxGemmHSegments == 3, "K-segment selects below");
+  const bool kseg = B_NK && p.nkseg > 1;
+
+  const int64_t kldb1 = p.kseg[1].ldb, kldb2 = p.kseg[2].ldb;
+  const int kk1 = p.kseg[1].k0, kk2 = p.kseg[2].k0;
+  // 1/s_m of row m: with K segments the largest of the segments' scales
+  // (their A blocks share one row scale, so the products sum in one accumulator)
+  auto row_isc = [&](int m) {
+    if (!kseg) return p.inv_s[m];
+    float v = fmaxf(p.kseg[0].inv_s[m], p.kseg[1].inv_s[m]);
+    return p.nkseg > 2 ? fmaxf(v, p.kseg[2].inv_s[m]) : v;
+  };
   uint32_t a_off[A_ITEMS], b_off[B_ITEMS];
+  int b_row[B_ITEMS], b_kq[B_ITEMS];   // [N,K] B chunk: row within the tile, k within the panel
   int a_lds[A_ITEMS], b_lds[B_ITEMS];  // LDS offsets (halves) within a stage
   float a_sc[A_ITEMS];                 // s_m of each A chunk's row
 #pragma unroll
@@ -1265,14 +1295,16 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     const int mr = min(m0 + row, p.M - 1);
     a_off[it] = (uint32_t)(((int64_t)(mr - m0) * p.lda + kq) * 4);
     a_lds[it] = row * PA + kq;
-    a_sc[it] = p.inv_s ? 1.f / p.inv_s[mr] : 1.f;  // exact: a power of two
+    a_sc[it] = p.inv_s ? 1.f / row_isc(mr) : 1.f;  // exact: a power of two
   }
 #pragma unroll
   for (int it = 0; it < B_ITEMS; ++it) {
     const int flat = tid + 256 * it;
     if constexpr (B_NK) {
       const int row = flat / 4, kq = (flat % 4) * 8;
-      b_off[it] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + kq) * 2);
+      b_row[it] = min(n0 + row, p.N - 1) - n0;
+      b_kq[it] = kq;
+      b_off[it] = (uint32_t)(((int64_t)b_row[it] * p.ldb + kq) * 2);
       b_lds[it] = 2 * A_PL + row * PA + kq;
     } else {
       const int k = flat / (BN / 8), nq = (flat % (BN / 8)) * 8;
@@ -1287,9 +1319,28 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     const int kc = min(max(j - pad, 0), nk - 1) * BK;
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) rs[S][it] = buf_load4(rsa, a_off[it], (uint32_t)kc * 4u);
-    const uint32_t boff = (uint32_t)((B_NK ? (int64_t)kc : (int64_t)kc * p.ldb) * 2);
+    if constexpr (B_NK) {
+      // selects only (no branch): the panel's segment — always 0 without K
+      // segments, where segment 0's B is the whole of B
+      const int kg = kbeg + kc;  // the panel's first k in the whole reduction
+      const int g = !kseg ? 0 : p.nkseg > 2 && kg >= kk2 ? 2 : kg >= kk1 ? 1 : 0;
+      // the pointer is selected, then made a resource (selecting among three
+      // resources, or among pointers computed ahead of the loop, puts them in
+      // scratch memory)
+      const __amdgpu_buffer_rsrc_t rb = buf_rsrc(
+          g == 0 ? (kseg ? p.kseg[0].B + (int64_t)n0 * p.kseg[0].ldb : p.B + (int64_t)n0 * p.ldb)
+                 : g == 1 ? p.kseg[1].B + (int64_t)n0 * kldb1 : p.kseg[2].B + (int64_t)n0 * kldb2);
+      const int64_t ldb = g == 1 ? kldb1 : kldb2;
+      const uint32_t boff = (uint32_t)(kg - (g == 0 ? 0 : g == 1 ? kk1 : kk2)) * 2u;
 #pragma unroll
-    for (int it = 0; it < B_ITEMS; ++it) rs[S][A_ITEMS + it] = buf_load4(rsb, b_off[it], boff);
+      for (int it = 0; it < B_ITEMS; ++it)
+        rs[S][A_ITEMS + it] =
+            buf_load4(rb, g == 0 ? b_off[it] : (uint32_t)(((int64_t)b_row[it] * ldb + b_kq[it]) * 2), boff);
+    } else {
+      const uint32_t boff = (uint32_t)((int64_t)kc * p.ldb * 2);
+#pragma unroll
+      for (int it = 0; it < B_ITEMS; ++it) rs[S][A_ITEMS + it] = buf_load4(rsb, b_off[it], boff);
+    }
   };
   auto lstore = [&](auto sc, int stage) {
     constexpr int S = decltype(sc)::value;
@@ -1417,7 +1468,7 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
     for (int a = 0; a < TA; ++a)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float f = p.inv_s[min(m0 + wm + 16 * a + 4 * lg + v, p.M - 1)];
+        const float f = row_isc(min(m0 + wm + 16 * a + 4 * lg + v, p.M - 1));
 #pragma unroll
         for (int b = 0; b < TB; ++b) acc[a][b][v] *= f;
       }
@@ -1426,16 +1477,24 @@ __global__ __launch_bounds__(256) void gemm_h_kernel(GemmHParams p) {
   // Rank-r LoRA term in fp32 (v_mfma_f32_16x16x4_f32), split 0 only, staged
   // in the ring's LDS after the last step's barrier.
   if (RANK && split == 0) {
-    const int r = p.ep.r, rp = (r + 3) & ~3, pr = rp + 1;
+    // with K segments the panels of the segments side by side: rank index
+    // j = g·r + jj takes segment g's P[m][jj] and Q(n, jj)
+    const int r = p.ep.r, rt = kseg ? p.nkseg * r : r, rp = (rt + 3) & ~3, pr = rp + 1;
+    const float *kP0 = p.kseg[0].P, *kP1 = p.kseg[1].P, *kP2 = p.kseg[2].P;
+    const float *kQ0 = p.kseg[0].Q, *kQ1 = p.kseg[1].Q, *kQ2 = p.kseg[2].Q;
     float* Ps = reinterpret_cast<float*>(smem);
     float* Qs = Ps + BM * pr;
     for (int i = tid; i < BM * rp; i += 256) {
       const int row = i / rp, j = i % rp, m = m0 + row;
-      Ps[row * pr + j] = (m < p.M && j < r) ? p.ep.P[(int64_t)m * r + j] : 0.f;
+      const int g = j / r, jj = j % r;
+      const float* P = !kseg ? p.ep.P : g == 0 ? kP0 : g == 1 ? kP1 : kP2;
+      Ps[row * pr + j] = (m < p.M && j < rt) ? P[(int64_t)m * r + jj] : 0.f;
     }
     for (int i = tid; i < BN * rp; i += 256) {
       const int col = i / rp, j = i % rp, n = n0 + col;
-      Qs[col * pr + j] = (n < p.N && j < r) ? p.ep.lscale * p.ep.Q[(int64_t)n * p.ep.qsn + (int64_t)j * p.ep.qsj] : 0.f;
+      const int g = j / r, jj = j % r;
+      const float* Q = !kseg ? p.ep.Q : g == 0 ? kQ0 : g == 1 ? kQ1 : kQ2;
+      Qs[col * pr + j] = (n < p.N && j < rt) ? p.ep.lscale * Q[(int64_t)n * p.ep.qsn + (int64_t)jj * p.ep.qsj] : 0.f;
     }
     __syncthreads();
     for (int t = 0; t < rp / 4; ++t) {
@@ -2068,6 +2127,67 @@ bool gemm_h_segments(hipStream_t s, const float* A, int64_t lda, const float* in
   t_gemm_events = nullptr;
   if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
   return true;
+}
+
+void gemm_h_ksegments(hipStream_t s, const float* A, int64_t lda, const GemmHKSegmentArg* seg, int nseg, float* C,
+                      int64_t ldc, int M, int N, const GemmEpilogue& ep, Scratch ws, const KernelEvents* ev) {
+  MFT_CHECK_ARG(seg && nseg >= 2 && nseg <= kMaxGemmHSegments && M > 0 && N > 0, "K-segmented GEMM: 2 or 3 segments");
+  MFT_CHECK_ARG(A && lda % 4 == 0 && ((uintptr_t)A & 15) == 0, "K-segmented GEMM: A");
+  MFT_CHECK_ARG(ldc >= N && nseg * ep.r <= 32, "K-segmented GEMM: ldc or rank");
+  MFT_CHECK_ARG(!ep.stats && !ep.gelu_out && !ep.gelu_grad_of, "K-segmented GEMM: no statistics or GELU terms");
+  int K = 0;
+  for (int g = 0; g < nseg; ++g) {
+    const GemmHKSegmentArg& a = seg[g];
+    MFT_CHECK_ARG(a.B && a.inv_s && a.K > 0 && a.K % 32 == 0 && a.ldb >= a.K && a.ldb % 8 == 0 &&
+                      ((uintptr_t)a.B & 15) == 0,
+                  "K-segmented GEMM: segment shape");
+    MFT_CHECK_ARG((ep.r > 0) == (a.P != nullptr && a.Q != nullptr), "K-segmented GEMM: rank panel per segment");
+    K += a.K;
+  }
+  MFT_CHECK_ARG(lda >= K, "K-segmented GEMM: lda < K");
+  GemmHParams p{};
+  p.A = A; p.inv_s = seg[0].inv_s; p.B = seg[0].B; p.C = C;
+  p.lda = lda; p.ldb = seg[0].ldb; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K;
+  p.ep = ep;
+  p.ep.P = seg[0].P;  // selects the rank-panel kernel; the panel reads every segment's P, Q
+  p.ep.Q = seg[0].Q;
+  p.partial = nullptr;
+  p.nkseg = nseg;
+  for (int g = 0, k0 = 0; g < nseg; k0 += seg[g].K, ++g)
+    p.kseg[g] = GemmHKSegment{k0, seg[g].B, seg[g].ldb, seg[g].inv_s, seg[g].P, seg[g].Q};
+  for (int g = nseg; g < kMaxGemmHSegments; ++g) p.kseg[g] = p.kseg[nseg - 1];  // never selected
+  PlanH pl = plan_gemm_h(M, N, K, ws.ptr ? ws.bytes : 0, false);
+  static const char* forced_env = getenv("MFT_GEMMH_PLAN");
+  int bm = 0, bn = 0, sp = 0;
+  const bool forced = forced_plan(forced_env, M, N, K, bm, bn, sp);
+  if (forced && sp >= 1 && sp <= 64 && ((bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64)) &&
+      (sp == 1 || (size_t)sp * M * N * sizeof(float) <= ws.bytes))
+    pl = {bm, bn, sp};
+  const RowNorm* nm = ep.norm && ep.norm->kind != NORM_NONE ? ep.norm : nullptr;
+  if (nm && !forced && pl.splits == 1 && K >= 512 && N % 4 == 0 && N <= 4096 && ldc == N &&
+      (size_t)2 * M * N * sizeof(float) <= ws.bytes)
+    pl.splits = 2;  // a row norm rides in the split-K reduction
+  p.k_chunk = (int)(cdiv(cdiv(K, pl.splits), 32) * 32);
+  const int splits = (int)cdiv(K, p.k_chunk);
+  for (int g = 0; g < nseg; ++g)
+    MFT_CHECK_ARG(((int64_t)pl.bn * seg[g].ldb + seg[g].K) * 2 < (int64_t(1) << 32),
+                  "GEMM operand too large for 32-bit buffer offsets");
+  MFT_CHECK_ARG(((int64_t)pl.bm * lda + p.k_chunk) * 4 < (int64_t(1) << 32), "GEMM operand too large for 32-bit buffer offsets");
+  if (splits > 1) p.partial = ws.ptr;
+  static const bool log_plans = getenv("MFT_GEMM_PLAN_LOG") != nullptr;
+  if (log_plans) fprintf(stderr, "gemm_h_kseg %d,%d,%d:%d,%d,%d nseg=%d norm=%d\n", M, N, K, pl.bm, pl.bn, splits, nseg, nm ? 1 : 0);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (ev) MFT_HIP(hipStreamIsCapturing(s, &cap));
+  const bool dispatch_events = ev && ev->start && ev->stop && cap == hipStreamCaptureStatusNone;
+  if (ev && ev->start && !dispatch_events) MFT_HIP(hipEventRecord(ev->start, s));
+  t_gemm_events = dispatch_events ? ev : nullptr;
+  if (pl.bm == 128) launch_h<128, 128>(s, p, true, splits);
+  else if (pl.bn == 128) launch_h<64, 128>(s, p, true, splits);
+  else launch_h<64, 64>(s, p, true, splits);
+  t_gemm_events = nullptr;
+  if (ev && ev->stop && !dispatch_events) MFT_HIP(hipEventRecord(ev->stop, s));
+  gemm_finish(s, splits, dispatch_events, ev, ws.ptr, M, N, C, ldc, ep, nm);
 }
 
 bool gemm_f16w(hipStream_t s, const float* x, int64_t ldx, const void* W, int64_t ldw, bool b_nk, float* C,

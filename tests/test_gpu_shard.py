@@ -24,8 +24,12 @@ if not torch.cuda.is_available():
 
 from mobilefinetuner_amd.engine import Model  # noqa: E402
 
-# fp16-stored weights: both the resident and the streamed model take the
-# rank-r panel path, so their steps are the same kernels on the same values.
+# fp16-stored weights: the rank-r panel path.  A model whose weights all stay
+# in HBM runs q|k|v and gate|up as segmented launches (one launch for the
+# three / two projections); the shard store launches each projection on its
+# own (one streamed weight at a time), so bit-for-bit comparisons pit the
+# streamed model against a store whose budget holds every weight (resident
+# after the first use: the same kernels on the same values).
 F16 = gemma3(3, 128, 2, 1, 256, 320, vocab=611, name="gemma-s16", w_fp16=1, sliding_window=24,
              query_pre_attn_scalar=256)
 
@@ -53,28 +57,38 @@ def steps(eng, ids, S, n, lr=1e-3):
 def test_streamed_steps_equal_resident_steps_bit_for_bit():
     B, S = 2, 32
     print("shard store: gemma3 fp16 W, budget 1.3x the largest tensor", flush=True)
-    ref = Model(F16, B * S)
-    sizes = streamed(ref)
+    hbm = Model(F16, B * S)  # every weight in HBM, no store
+    sizes = streamed(hbm)
     budget = int(max(sizes) * 1.3)
     assert budget < sum(sizes)
+    ref = Model(dataclasses.replace(F16, shard_budget=2 * sum(sizes)), B * S)  # the store, everything fits
     sh = Model(dataclasses.replace(F16, shard_budget=budget), B * S)
-    vals = param_values(ref.params, seed=3)
+    vals = param_values(hbm.params, seed=3)
     for n, v in vals.items():
+        hbm.set_param(n, v)
         ref.set_param(n, v)
         sh.set_param(n, v)
     rng = np.random.default_rng(4)
     ids = [torch.from_numpy(rng.integers(0, F16.vocab, (B * S,)).astype(np.int32)).cuda() for _ in range(3)]
     la = steps(ref, ids, S, 3)
     lb = steps(sh, ids, S, 3)
+    lh = steps(hbm, ids, S, 3)
     assert la == lb, (la, lb)
     for p in ref.params:
         if p["trainable"]:
             assert np.array_equal(ref.get(p["name"]), sh.get(p["name"])), p["name"]
+            # the store-free model's segmented launches sum in another order
+            assert rel_err(hbm.get(p["name"]), sh.get(p["name"])) < 1e-5, p["name"]
+    for (x, _, _), (y, _, _) in zip(lh, lb):
+        assert abs(x - y) <= 1e-5 * abs(y), (lh, lb)
+    loads_ref, _, _ = ref.shard_stats()
+    assert loads_ref == len(sizes), loads_ref  # the roomy store loaded each weight once
     loads, hits, bud = sh.shard_stats()
     # every tensor is used at least twice per step; with room for about one
     # tensor most uses have to stream
     assert bud == budget & ~255 and loads > 2 * len(sizes), (loads, hits, bud)
-    assert ref.shard_stats() == (0, 0, 0)
+    assert hbm.shard_stats() == (0, 0, 0)
+    hbm.close()
     ref.close()
     sh.close()
 
