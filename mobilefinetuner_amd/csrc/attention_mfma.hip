@@ -1007,18 +1007,25 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short256(AttnP p) {
   const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k + tok0 * p.k_rs + (int64_t)kh * HD);
   const __amdgpu_buffer_rsrc_t rv = buf_rsrc(p.v + tok0 * p.v_rs + (int64_t)kh * HD);
   const float* qrow = Qs + li * PO + 4 * lg;
-  for (int kt = kt_lo + w; kt <= kt_hi; kt += NW) {
-    floatx4 kc[NC];
-    float vc[NC][4];
+  // K of a key tile: this lane's row slice (S operands); the wave's next K
+  // tile is loaded while the current one is multiplied (its V column slices,
+  // needed only after the softmax, are loaded at the top of the step)
+  auto load_k = [&](int kt, floatx4* k) {
     const uint32_t ko = (uint32_t)(((int64_t)min(16 * kt + li, p.S - 1) * p.k_rs + 4 * lg) * 4);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kc[c] = buf_load4(rk, ko + 64u * c, 0);
+    for (int c = 0; c < NC; ++c) k[c] = buf_load4(rk, ko + 64u * c, 0);
+  };
+  floatx4 kc[NC], kn[NC];
+  if (kt_lo + w <= kt_hi) load_k(kt_lo + w, kc);
+  for (int kt = kt_lo + w; kt <= kt_hi; kt += NW) {
+    float vc[NC][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t vo = (uint32_t)(((int64_t)min(16 * kt + 4 * lg + t, p.S - 1) * p.v_rs + li) * 4);
 #pragma unroll
       for (int c = 0; c < NC; ++c) vc[c][t] = buf_load1(rv, vo + 64u * c, 0);
     }
+    if (kt + NW <= kt_hi) load_k(kt + NW, kn);
     floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1056,6 +1063,9 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_short256(AttnP p) {
     for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int t = 0; t < 4; ++t) oacc[c] = mfma4(pr[t], vc[c][t], oacc[c]);
+    if (kt + NW <= kt_hi)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kc[c] = kn[c];
   }
   __syncthreads();  // the staged queries are read by every wave before Os overwrites them
   if (lg == 0) {
