@@ -327,6 +327,22 @@ struct RankJob {
   float* inv_s;  // projection: when set, also the row scales of X (row_scales) for the fp16 GEMM
 };
 int rank_outer_blocks(int C);
+// Up to three projections out[M,r] = X·Y of one launch, by value (the per-layer
+// batches of the rank-r panel path); inv_s (nullable): the rows' fp16-GEMM scales.
+struct ProjJob {
+  const float* X;
+  int64_t ldx;
+  const float* Y;  // [r][K] (y_rk) or [K][r]
+  int K, y_rk;
+  float* out;
+  float* inv_s;
+};
+constexpr int kMaxProjJobs = 3;
+struct ProjJobs {
+  ProjJob j[kMaxProjJobs];
+  int n;
+};
+void rank_proj_jobs(hipStream_t s, const ProjJobs& jb, int M, int r);
 // Runs jobs[0, njobs) (the first nproj are projections) over M rows.
 void rank_batch(hipStream_t s, const RankJob* jobs, int njobs, int nproj, int outer_blocks, int M, int r);
 

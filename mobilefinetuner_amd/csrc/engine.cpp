@@ -224,6 +224,7 @@ struct mft_model_s {
     const RankJob* jobs;
     int njobs, nproj, outer_blocks;
     double work_per_row;  // HBM bytes per token row (timing)
+    ProjJobs pj;          // pj.n > 0: the same projections by value (one launch of rank_proj_jobs)
   };
   std::vector<Batch> batches;
   int xa_batch = -1, udb_batch = -1, da_batch = -1, db_batch = -1;
@@ -921,6 +922,7 @@ void build_lora_tables(mft_model_s* m) {
     size_t off;
     int njobs, nproj, outer_blocks;
     double work;
+    ProjJobs pj;
   };
   std::vector<Pending> pend;
   auto proj_job = [&](const float* X, int64_t ldx, int K, const float* Y, bool y_rk, float* out) {
@@ -938,7 +940,15 @@ void build_lora_tables(mft_model_s* m) {
   // its index.
   auto add_batch = [&](std::vector<RankJob> proj, std::vector<RankJob> outer) {
     if (proj.empty() && outer.empty()) return -1;
-    Pending p{rj.size(), (int)(proj.size() + outer.size()), (int)proj.size(), 0, 0.0};
+    Pending p{rj.size(), (int)(proj.size() + outer.size()), (int)proj.size(), 0, 0.0, ProjJobs{}};
+    // a few projections of one Y layout and nothing else: also kept by value
+    if (outer.empty() && proj.size() <= (size_t)kMaxProjJobs) {
+      bool same = true;
+      for (auto& j : proj) same = same && j.y_rk == proj[0].y_rk;
+      if (same) {
+        for (auto& j : proj) p.pj.j[p.pj.n++] = ProjJob{j.X, j.ldx, j.Y, j.K, j.y_rk, j.out, j.inv_s};
+      }
+    }
     // timing work in HBM bytes per token row: a projection reads a K-wide
     // row and writes r values; an outer product reads a C-wide row and r values
     for (auto& j : proj) {
@@ -1053,7 +1063,7 @@ void build_lora_tables(mft_model_s* m) {
   m->d_merge = static_cast<const MergeJob*>(m->tables);
   m->n_merge = (int)mj.size();
   m->merge_tiles_total = tiles;
-  for (auto& p : pend) m->batches.push_back({d_rank + p.off, p.njobs, p.nproj, p.outer_blocks, p.work});
+  for (auto& p : pend) m->batches.push_back({d_rank + p.off, p.njobs, p.nproj, p.outer_blocks, p.work, p.pj});
   m->merged = !panel;
   m->panel = panel;
 }
@@ -1454,12 +1464,21 @@ void lin_bwd(mft_model_s* m, const Linear& l, const float* dy, const float* x, c
 }
 
 // One table-driven launch of batched rank-r work (see build_lora_tables).
+// A batch of at most three projections (the rank-r panel path's per-layer
+// groups) runs as one by-value launch, a workgroup per row and job; larger
+// batches and outer products read their job table.  Tuning hook:
+// MFT_PROJ_JOBS=0 keeps every batch on the table kernel.
 void run_batch(mft_model_s* m, int idx, int64_t M) {
   if (idx < 0) return;
+  static const bool by_value = [] {
+    const char* e = getenv("MFT_PROJ_JOBS");
+    return !e || atoi(e) != 0;
+  }();
   const mft_model_s::Batch& b = m->batches[idx];
   Timed t(m, CLS_RANK, b.work_per_row * M);
   t.begin();
-  rank_batch(m->stream, b.jobs, b.njobs, b.nproj, b.outer_blocks, (int)M, m->c.lora_r);
+  if (by_value && b.pj.n > 0) rank_proj_jobs(m->stream, b.pj, (int)M, m->c.lora_r);
+  else rank_batch(m->stream, b.jobs, b.njobs, b.nproj, b.outer_blocks, (int)M, m->c.lora_r);
   t.end();
 }
 

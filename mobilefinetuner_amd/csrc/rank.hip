@@ -100,6 +100,65 @@ __global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restr
   }
 }
 
+// Up to three projection jobs of one launch, passed by value (no job table
+// to read before the first load): workgroup b runs row b % M of job b / M,
+// as rank_proj_vec_kernel with RB = 1, and with inv_s set also writes the
+// row's fp16-GEMM scale row_inv_scale(max_k |X[m,k]|).  The per-layer
+// batches of the rank-r panel path (xa of a group's shared input, U of its
+// dY blocks) take this form.
+template <int R, bool Y_RK>
+__global__ __launch_bounds__(256) void rank_proj_jobs_kernel(ProjJobs jb, int M) {
+  static_assert(kMaxProjJobs == 3, "job selects below");
+  __shared__ float red[4][R];
+  __shared__ float rmx[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = (int)blockIdx.x / M, m = (int)blockIdx.x % M;
+  // selects over constant indices keep the arguments in scalar registers
+  const float* X = g == 0 ? jb.j[0].X : g == 1 ? jb.j[1].X : jb.j[2].X;
+  const int64_t ldx = g == 0 ? jb.j[0].ldx : g == 1 ? jb.j[1].ldx : jb.j[2].ldx;
+  const float* Y = g == 0 ? jb.j[0].Y : g == 1 ? jb.j[1].Y : jb.j[2].Y;
+  const int K = g == 0 ? jb.j[0].K : g == 1 ? jb.j[1].K : jb.j[2].K;
+  float* out = g == 0 ? jb.j[0].out : g == 1 ? jb.j[1].out : jb.j[2].out;
+  float* inv_s = g == 0 ? jb.j[0].inv_s : g == 1 ? jb.j[1].inv_s : jb.j[2].inv_s;
+  float acc[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) acc[q] = 0.f;
+  float mx = 0.f;
+  const float* xr = X + (int64_t)m * ldx;
+  for (int k = tid * 4; k < K; k += 1024) {
+    const floatx4 xv = *reinterpret_cast<const floatx4*>(xr + k);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3]))));
+    if constexpr (Y_RK) {
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        const floatx4 y = *reinterpret_cast<const floatx4*>(Y + (int64_t)j * K + k);
+        acc[j] += xv[0] * y[0] + xv[1] * y[1] + xv[2] * y[2] + xv[3] * y[3];
+      }
+    } else {
+      const float* yk = Y + (int64_t)k * R;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jq = 0; jq < R / 4; ++jq) {
+          const floatx4 y = *reinterpret_cast<const floatx4*>(yk + e * R + 4 * jq);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[4 * jq + u] = fmaf(xv[e], y[u], acc[4 * jq + u]);
+        }
+    }
+  }
+  const float t = wave_reduce_spread<R>(acc, lane);
+  constexpr int SPREAD = 64 / R;
+  if ((lane % SPREAD) == 0) red[wave][lane / SPREAD] = t;
+  if (inv_s) {  // uniform per job
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+    if (lane == 0) rmx[wave] = mx;
+  }
+  __syncthreads();
+  if (tid < R) out[(int64_t)m * R + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+  if (inv_s && tid == 0) inv_s[m] = row_inv_scale(fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3])));
+}
+
 // Generic fallback (any r ≤ 32, any alignment).
 template <int RMAX>
 __global__ __launch_bounds__(256) void rank_proj_scalar_kernel(const float* X, int64_t ldx,
@@ -611,6 +670,32 @@ void rank_batch_launch(hipStream_t s, const RankJob* jobs, int njobs, int nproj,
     case 32: hipLaunchKernelGGL((rank_batch_kernel<32, KS>), grid, block, 0, s, jobs, njobs, nproj, M); break;
     default: MFT_CHECK_ARG(false, "batched rank-r work takes r in {4, 8, 16, 32}");
   }
+  MFT_LAUNCH_CHECK();
+}
+
+void rank_proj_jobs(hipStream_t s, const ProjJobs& jb, int M, int r) {
+  MFT_CHECK_ARG(jb.n >= 1 && jb.n <= kMaxProjJobs && M > 0 && (r == 4 || r == 8 || r == 16 || r == 32),
+                "projection jobs: 1-3 jobs, r in {4, 8, 16, 32}");
+  bool y_rk = jb.j[0].y_rk != 0;
+  for (int g = 0; g < jb.n; ++g) {
+    const ProjJob& j = jb.j[g];
+    MFT_CHECK_ARG(j.X && j.Y && j.out && j.K > 0 && j.K % 4 == 0 && j.ldx % 4 == 0 && aligned16(j.X) &&
+                      aligned16(j.Y) && (j.y_rk != 0) == y_rk,
+                  "projection job: shape, alignment or Y layout");
+  }
+  ProjJobs b = jb;
+  for (int g = jb.n; g < kMaxProjJobs; ++g) b.j[g] = b.j[jb.n - 1];  // never selected
+  const dim3 grid((unsigned)(jb.n * M)), block(256);
+#define MFT_PJ(R)                                                                   \
+  if (y_rk) hipLaunchKernelGGL((rank_proj_jobs_kernel<R, true>), grid, block, 0, s, b, M); \
+  else hipLaunchKernelGGL((rank_proj_jobs_kernel<R, false>), grid, block, 0, s, b, M)
+  switch (r) {
+    case 4: { MFT_PJ(4); } break;
+    case 8: { MFT_PJ(8); } break;
+    case 16: { MFT_PJ(16); } break;
+    default: { MFT_PJ(32); } break;
+  }
+#undef MFT_PJ
   MFT_LAUNCH_CHECK();
 }
 
