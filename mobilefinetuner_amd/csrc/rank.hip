@@ -43,31 +43,27 @@ __device__ __forceinline__ float wave_reduce_spread(float (&v)[NV], int lane) {
   return t;
 }
 
-// out[m, j] = Σ_k X[m,k]·Y(k,j) for RB rows per 256-thread workgroup; every
-// thread takes 128-bit chunks of K for all RB rows (so X is streamed once),
-// the RB·R partial sums are reduced within each wave by recursive halving
-// and across the four waves in LDS.
-// Y_RK: Y stored [R][K] (xa = x·Aᵀ with A [r,K]); otherwise [K][R]
-// (U = dy·B with B [N,r]).
-template <int R, int RB, bool Y_RK>
-__global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restrict__ X, int64_t ldx,
-                                                             const float* __restrict__ Y, int M, int K,
-                                                             float* __restrict__ out) {
-  constexpr int NV = RB * R;
-  __shared__ float red[4][NV];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.x * RB;
-  float acc[NV];
+// acc[i·R + j] += Σ_k X[row i, k]·Y(k, j) over this thread's share of K for
+// the RB rows xr[i], and with MX mx[i] = max |X[row i, k]| over that share.
+// Y_RK: Y stored [R][K] (xa = x·Aᵀ with A [r,K]); thread t takes the 128-bit
+// chunks k = 4t + 1024i and reads each Y row with one 128-bit load per chunk.
+// Otherwise Y is [K][R] (U = dy·B with B [N,r]); thread t takes single
+// columns k = t + 256i, E at a time, so that a wave's Y reads (R contiguous
+// floats per k) are contiguous across lanes.  128-bit X chunks there would
+// put 4R floats between the lanes' Y reads, one cache line per lane per load
+// (2.3x slower at K = 6912, 1.5x at K = 1152).
+template <int R, int RB, bool Y_RK, bool MX>
+__device__ __forceinline__ void proj_accumulate(const float* const (&xr)[RB], const float* __restrict__ Y, int K,
+                                                int tid, float (&acc)[RB * R], float (&mx)[RB]) {
+  if constexpr (Y_RK) {
+    for (int k = tid * 4; k < K; k += 1024) {
+      floatx4 xv[RB];
 #pragma unroll
-  for (int q = 0; q < NV; ++q) acc[q] = 0.f;
-  for (int k = tid * 4; k < K; k += 1024) {
-    floatx4 xv[RB];
-#pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int m = min(m0 + i, M - 1);
-      xv[i] = *reinterpret_cast<const floatx4*>(X + (int64_t)m * ldx + k);
-    }
-    if constexpr (Y_RK) {
+      for (int i = 0; i < RB; ++i) {
+        xv[i] = *reinterpret_cast<const floatx4*>(xr[i] + k);
+        if constexpr (MX)
+          mx[i] = fmaxf(mx[i], fmaxf(fmaxf(fabsf(xv[i][0]), fabsf(xv[i][1])), fmaxf(fabsf(xv[i][2]), fabsf(xv[i][3]))));
+      }
 #pragma unroll
       for (int j = 0; j < R; ++j) {
         const floatx4 y = *reinterpret_cast<const floatx4*>(Y + (int64_t)j * K + k);
@@ -75,44 +71,79 @@ __global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restr
         for (int i = 0; i < RB; ++i)
           acc[i * R + j] += xv[i][0] * y[0] + xv[i][1] * y[1] + xv[i][2] * y[2] + xv[i][3] * y[3];
       }
-    } else {
-      const float* yk = Y + (int64_t)k * R;
+    }
+  } else {
+    constexpr int E = R <= 8 ? 4 : R == 16 ? 2 : 1;
+    for (int k0 = tid; k0 < K; k0 += 256 * E) {
+      float xs[E][RB];
+      floatx4 ys[E][R / 4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int e = 0; e < E; ++e) {
+        const int k = k0 + 256 * e;
+        if (k < K) {
 #pragma unroll
-        for (int jq = 0; jq < R / 4; ++jq) {
-          const floatx4 y = *reinterpret_cast<const floatx4*>(yk + e * R + 4 * jq);
+          for (int i = 0; i < RB; ++i) xs[e][i] = xr[i][k];
 #pragma unroll
-          for (int i = 0; i < RB; ++i)
+          for (int q = 0; q < R / 4; ++q) ys[e][q] = *reinterpret_cast<const floatx4*>(Y + (int64_t)k * R + 4 * q);
+        } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[i * R + 4 * jq + u] = fmaf(xv[i][e], y[u], acc[i * R + 4 * jq + u]);
+          for (int i = 0; i < RB; ++i) xs[e][i] = 0.f;
+#pragma unroll
+          for (int q = 0; q < R / 4; ++q) ys[e][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          if constexpr (MX) mx[i] = fmaxf(mx[i], fabsf(xs[e][i]));
+#pragma unroll
+          for (int q = 0; q < R / 4; ++q)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[i * R + 4 * q + u] = fmaf(xs[e][i], ys[e][q][u], acc[i * R + 4 * q + u]);
         }
     }
   }
-  const float t = wave_reduce_spread<NV>(acc, lane);
-  constexpr int SPREAD = 64 / NV;
+}
+
+// out[m, j] = Σ_k X[m,k]·Y(k,j), one row per 256-thread workgroup; the R
+// partial sums are reduced within each wave by recursive halving and across
+// the four waves in LDS.
+template <int R, bool Y_RK>
+__global__ __launch_bounds__(256) void rank_proj_vec_kernel(const float* __restrict__ X, int64_t ldx,
+                                                             const float* __restrict__ Y, int M, int K,
+                                                             float* __restrict__ out) {
+  __shared__ float red[4][R];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = blockIdx.x;
+  float acc[R], mx[1];
+#pragma unroll
+  for (int q = 0; q < R; ++q) acc[q] = 0.f;
+  const float* const xr[1] = {X + (int64_t)m * ldx};
+  proj_accumulate<R, 1, Y_RK, false>(xr, Y, K, tid, acc, mx);
+  const float t = wave_reduce_spread<R>(acc, lane);
+  constexpr int SPREAD = 64 / R;
   if ((lane % SPREAD) == 0) red[wave][lane / SPREAD] = t;
   __syncthreads();
-  if (tid < NV) {
-    const int i = tid / R, j = tid % R;
-    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-    if (m0 + i < M) out[(int64_t)(m0 + i) * R + j] = v;
-  }
+  if (tid < R) out[(int64_t)m * R + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
 }
 
 // Up to three projection jobs of one launch, passed by value (no job table
-// to read before the first load): workgroup b runs row b % M of job b / M,
-// as rank_proj_vec_kernel with RB = 1, and with inv_s set also writes the
-// row's fp16-GEMM scale row_inv_scale(max_k |X[m,k]|).  The per-layer
-// batches of the rank-r panel path (xa of a group's shared input, U of its
-// dY blocks) take this form.
-template <int R, bool Y_RK>
+// to read before the first load): workgroup b runs RB rows of job b / nb
+// (nb = ⌈M/RB⌉ row blocks per job) with proj_accumulate, and with inv_s set
+// also writes each row's fp16-GEMM scale row_inv_scale(max_k |X[m,k]|).
+// RB = 2 shares each read of Y among two rows (deep K: every workgroup reads
+// all K·r floats of Y).  The per-layer batches of the rank-r panel path (xa
+// of a group's shared input, U of its dY blocks) take this form.
+template <int R, int RB, bool Y_RK>
 __global__ __launch_bounds__(256) void rank_proj_jobs_kernel(ProjJobs jb, int M) {
   static_assert(kMaxProjJobs == 3, "job selects below");
-  __shared__ float red[4][R];
-  __shared__ float rmx[4];
+  constexpr int NV = RB * R;
+  __shared__ float red[4][NV];
+  __shared__ float rmx[4][RB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = (int)blockIdx.x / M, m = (int)blockIdx.x % M;
+  const int nb = (M + RB - 1) / RB;
+  const int g = (int)blockIdx.x / nb, m0 = ((int)blockIdx.x % nb) * RB;
   // selects over constant indices keep the arguments in scalar registers
   const float* X = g == 0 ? jb.j[0].X : g == 1 ? jb.j[1].X : jb.j[2].X;
   const int64_t ldx = g == 0 ? jb.j[0].ldx : g == 1 ? jb.j[1].ldx : jb.j[2].ldx;
@@ -120,43 +151,35 @@ __global__ __launch_bounds__(256) void rank_proj_jobs_kernel(ProjJobs jb, int M)
   const int K = g == 0 ? jb.j[0].K : g == 1 ? jb.j[1].K : jb.j[2].K;
   float* out = g == 0 ? jb.j[0].out : g == 1 ? jb.j[1].out : jb.j[2].out;
   float* inv_s = g == 0 ? jb.j[0].inv_s : g == 1 ? jb.j[1].inv_s : jb.j[2].inv_s;
-  float acc[R];
+  float acc[NV], mx[RB];
 #pragma unroll
-  for (int q = 0; q < R; ++q) acc[q] = 0.f;
-  float mx = 0.f;
-  const float* xr = X + (int64_t)m * ldx;
-  for (int k = tid * 4; k < K; k += 1024) {
-    const floatx4 xv = *reinterpret_cast<const floatx4*>(xr + k);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3]))));
-    if constexpr (Y_RK) {
+  for (int q = 0; q < NV; ++q) acc[q] = 0.f;
+  const float* xr[RB];
 #pragma unroll
-      for (int j = 0; j < R; ++j) {
-        const floatx4 y = *reinterpret_cast<const floatx4*>(Y + (int64_t)j * K + k);
-        acc[j] += xv[0] * y[0] + xv[1] * y[1] + xv[2] * y[2] + xv[3] * y[3];
-      }
-    } else {
-      const float* yk = Y + (int64_t)k * R;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int jq = 0; jq < R / 4; ++jq) {
-          const floatx4 y = *reinterpret_cast<const floatx4*>(yk + e * R + 4 * jq);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) acc[4 * jq + u] = fmaf(xv[e], y[u], acc[4 * jq + u]);
-        }
-    }
+  for (int i = 0; i < RB; ++i) {
+    xr[i] = X + (int64_t)min(m0 + i, M - 1) * ldx;
+    mx[i] = 0.f;
   }
-  const float t = wave_reduce_spread<R>(acc, lane);
-  constexpr int SPREAD = 64 / R;
+  proj_accumulate<R, RB, Y_RK, true>(xr, Y, K, tid, acc, mx);
+  const float t = wave_reduce_spread<NV>(acc, lane);
+  constexpr int SPREAD = 64 / NV;
   if ((lane % SPREAD) == 0) red[wave][lane / SPREAD] = t;
   if (inv_s) {  // uniform per job
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-    if (lane == 0) rmx[wave] = mx;
+    for (int i = 0; i < RB; ++i) {
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], d, 64));
+      if (lane == 0) rmx[wave][i] = mx[i];
+    }
   }
   __syncthreads();
-  if (tid < R) out[(int64_t)m * R + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-  if (inv_s && tid == 0) inv_s[m] = row_inv_scale(fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3])));
+  if (tid < NV) {
+    const int i = tid / R, j = tid % R;
+    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (m0 + i < M) out[(int64_t)(m0 + i) * R + j] = v;
+  }
+  if (inv_s && tid < RB && m0 + tid < M)
+    inv_s[m0 + tid] = row_inv_scale(fmaxf(fmaxf(rmx[0][tid], rmx[1][tid]), fmaxf(rmx[2][tid], rmx[3][tid])));
 }
 
 // Generic fallback (any r ≤ 32, any alignment).
@@ -621,12 +644,12 @@ __global__ __launch_bounds__(kBatchThreads) void rank_batch_kernel(const RankJob
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-template <int R, int RB>
+template <int R>
 void proj_vec(hipStream_t s, const float* X, int64_t ldx, const float* Y, bool y_rk, int M, int K,
               float* out) {
-  const dim3 grid((unsigned)cdiv(M, RB)), block(256);
-  if (y_rk) hipLaunchKernelGGL((rank_proj_vec_kernel<R, RB, true>), grid, block, 0, s, X, ldx, Y, M, K, out);
-  else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, RB, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
+  const dim3 grid((unsigned)M), block(256);
+  if (y_rk) hipLaunchKernelGGL((rank_proj_vec_kernel<R, true>), grid, block, 0, s, X, ldx, Y, M, K, out);
+  else      hipLaunchKernelGGL((rank_proj_vec_kernel<R, false>), grid, block, 0, s, X, ldx, Y, M, K, out);
 }
 
 void outer_launch(hipStream_t s, OuterArgs& a) {
@@ -683,17 +706,23 @@ void rank_proj_jobs(hipStream_t s, const ProjJobs& jb, int M, int r) {
                       aligned16(j.Y) && (j.y_rk != 0) == y_rk,
                   "projection job: shape, alignment or Y layout");
   }
+  int kmax = 0;
+  for (int g = 0; g < jb.n; ++g) kmax = std::max(kmax, jb.j[g].K);
   ProjJobs b = jb;
   for (int g = jb.n; g < kMaxProjJobs; ++g) b.j[g] = b.j[jb.n - 1];  // never selected
-  const dim3 grid((unsigned)(jb.n * M)), block(256);
-#define MFT_PJ(R)                                                                   \
-  if (y_rk) hipLaunchKernelGGL((rank_proj_jobs_kernel<R, true>), grid, block, 0, s, b, M); \
-  else hipLaunchKernelGGL((rank_proj_jobs_kernel<R, false>), grid, block, 0, s, b, M)
+  // two rows per workgroup share the Y reads of deep [K][r] Y (a row per
+  // workgroup otherwise: 2.4 TB/s at K = 6912 with one job, 30% slower at two
+  // rows; [K][r] at K = 6912, two jobs: 22.5 -> 19.2 us)
+  const bool two = !y_rk && kmax > 2048 && r <= 8;
+  const dim3 grid((unsigned)(jb.n * (two ? cdiv(M, 2) : M))), block(256);
+#define MFT_PJ(R, RB)                                                                       \
+  if (y_rk) hipLaunchKernelGGL((rank_proj_jobs_kernel<R, RB, true>), grid, block, 0, s, b, M); \
+  else hipLaunchKernelGGL((rank_proj_jobs_kernel<R, RB, false>), grid, block, 0, s, b, M)
   switch (r) {
-    case 4: { MFT_PJ(4); } break;
-    case 8: { MFT_PJ(8); } break;
-    case 16: { MFT_PJ(16); } break;
-    default: { MFT_PJ(32); } break;
+    case 4: if (two) { MFT_PJ(4, 2); } else { MFT_PJ(4, 1); } break;
+    case 8: if (two) { MFT_PJ(8, 2); } else { MFT_PJ(8, 1); } break;
+    case 16: { MFT_PJ(16, 1); } break;
+    default: { MFT_PJ(32, 1); } break;
   }
 #undef MFT_PJ
   MFT_LAUNCH_CHECK();
@@ -719,11 +748,10 @@ void rank_proj(hipStream_t s, const float* X, int64_t ldx, const float* Y, int64
   const bool vec = (r == 4 || r == 8 || r == 16 || r == 32) && (y_rk || y_kr) && K % 4 == 0 && ldx % 4 == 0 &&
                    aligned16(X) && aligned16(Y);
   if (vec) {
-    // one row per workgroup
-    if (r == 4) proj_vec<4, 1>(s, X, ldx, Y, y_rk, M, K, out);
-    else if (r == 8) proj_vec<8, 1>(s, X, ldx, Y, y_rk, M, K, out);
-    else if (r == 16) proj_vec<16, 1>(s, X, ldx, Y, y_rk, M, K, out);
-    else proj_vec<32, 1>(s, X, ldx, Y, y_rk, M, K, out);
+    if (r == 4) proj_vec<4>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 8) proj_vec<8>(s, X, ldx, Y, y_rk, M, K, out);
+    else if (r == 16) proj_vec<16>(s, X, ldx, Y, y_rk, M, K, out);
+    else proj_vec<32>(s, X, ldx, Y, y_rk, M, K, out);
   } else {
     dim3 grid((unsigned)cdiv(M, 4)), block(256);
     if (r <= 8)       hipLaunchKernelGGL(rank_proj_scalar_kernel<8>, grid, block, 0, s, X, ldx, Y, ysk, ysj, M, K, r, out);
