@@ -244,13 +244,19 @@ struct MirrorGroup {
   // drivers' per-step gradient reads and writes move at DMA rate, and a copy
   // can be queued behind the kernels that produce the data.
   char* host = nullptr;
+  void* host_dev = nullptr;     // `host` as kernels address it (null: copies only)
   hipEvent_t arrive = nullptr;  // end of the queued device→host copy (state 3)
-  hipEvent_t depart = nullptr;  // end of the queued host→device copy (state 4)
+  hipEvent_t depart = nullptr;  // end of the queued work that reads `host` (states 2 and 4)
   // 0 = stale, 1 = equal to the device, 2 = newer than the device,
   // 3 = a device→host copy is queued (equal to the device once `arrive` fires),
   // 4 = a host→device copy is queued: equal to the device, but the host copy
   //     is read by that copy until `depart` fires (host writes wait for it)
   int state = 0;
+  // a queued kernel or copy reads `host` until `depart` fires (host writes wait)
+  bool host_read = false;
+  // host edits not yet on the device when zero_grad() requests arrived: they
+  // go up before the fills unless every member is zeroed
+  bool host_edits = false;
   int members = 0;  // views created in the group
   // zero_grad() requests not yet applied on the device: byte offset → bytes.
   // They run at the group's next device or host access, as one fill over the
@@ -269,7 +275,18 @@ void ensure_host(MirrorGroup& g) {
   if (g.host || g.bytes == 0) return;
   hip_check(hipHostMalloc(reinterpret_cast<void**>(&g.host), g.bytes, hipHostMallocDefault), "hipHostMalloc");
   std::memset(g.host, 0, g.bytes);
+  if (hipHostGetDevicePointer(&g.host_dev, g.host, 0) != hipSuccess) {
+    g.host_dev = nullptr;
+    (void)hipGetLastError();
+  }
   g.state = 0;
+}
+
+// `depart` marks the end of what the stream has queued so far that reads `host`
+void mark_host_read(MirrorGroup& g) {
+  if (!g.depart) hip_check(hipEventCreateWithFlags(&g.depart, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipEventRecord(g.depart, nullptr), "hipEventRecord");
+  g.host_read = true;
 }
 
 void flush_zeros(MirrorGroup& g) {
@@ -277,11 +294,16 @@ void flush_zeros(MirrorGroup& g) {
   if ((int)g.zeros.size() == g.members) {
     mft_check(mft_fill(detail::handle(), reinterpret_cast<float*>(g.dev), (int64_t)(g.bytes / 4), 0.f), "mft_fill");
   } else {
+    if (g.host_edits) {  // the members not zeroed keep their host edits
+      hip_check(hipMemcpyAsync(g.dev, g.host, g.bytes, hipMemcpyHostToDevice, nullptr), "hipMemcpyAsync H2D");
+      mark_host_read(g);
+    }
     for (const auto& z : g.zeros)
       mft_check(mft_fill(detail::handle(), reinterpret_cast<float*>(g.dev + z.first), (int64_t)(z.second / 4), 0.f),
                 "mft_fill");
   }
   g.zeros.clear();
+  g.host_edits = false;
   g.state = 0;
 }
 }  // namespace
@@ -334,6 +356,10 @@ void Tensor::sync_host(bool will_write) const {
     MirrorGroup& g = *group_;
     flush_zeros(g);
     ensure_host(g);
+    if (will_write && g.host_read) {
+      hip_check(hipEventSynchronize(g.depart), "hipEventSynchronize");
+      g.host_read = false;
+    }
     if (g.state == 3 || (g.state == 4 && will_write)) {
       hip_check(hipEventSynchronize(g.state == 3 ? g.arrive : g.depart), "hipEventSynchronize");
       g.state = 1;
@@ -379,9 +405,8 @@ void Tensor::upload_if_dirty() const {
     if (g.state == 2) {
       // queued behind the stream's work, ahead of the kernel that asked: the
       // pinned host copy stays untouched until `depart` (sync_host waits)
-      if (!g.depart) hip_check(hipEventCreateWithFlags(&g.depart, hipEventDisableTiming), "hipEventCreate");
       hip_check(hipMemcpyAsync(g.dev, g.host, g.bytes, hipMemcpyHostToDevice, nullptr), "hipMemcpyAsync H2D");
-      hip_check(hipEventRecord(g.depart, nullptr), "hipEventRecord");
+      mark_host_read(g);
       g.state = 4;
     }
     return;
@@ -428,10 +453,7 @@ void Tensor::zero_grad() {
     // host edits of other members reach the device first (without applying
     // the zero requests already pending: those wait for the rest of the
     // group, so the drivers' zero_grad loop costs one fill)
-    if (g->state == 2) {
-      hip_check(hipMemcpy(g->dev, g->host, g->bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
-      g->state = 1;
-    }
+    if (g->state == 2) g->host_edits = true;  // uploaded at the flush unless every member is zeroed
     g->zeros[grad_->group_off_] = (size_t)grad_->numel() * 4;
     g->state = 0;
     return;
@@ -1108,14 +1130,22 @@ void Adam::step(const std::vector<TensorPtr>& params, const std::vector<TensorPt
   }
   if (fused) {
     GroupState& gs = *gstate_[pg];
-    float* pd = static_cast<float*>(params[0]->device_data());  // flushes host edits of either group
-    float* gd = static_cast<float*>(grads[0]->device_data());
+    float* pd = static_cast<float*>(params[0]->device_data());  // flushes host edits of the parameters
     pd -= params[0]->mirror_offset() / 4;
-    gd -= grads[0]->mirror_offset() / 4;
+    // Gradients edited on the host (the drivers' clip loop scales them in
+    // place) are read by the update straight from the pinned host copy: no
+    // upload, whose copy engine → kernel hand-off alone costs ≈50 µs.  The
+    // device copy stays stale (host-newer state); the drivers' zero_grad()
+    // that follows replaces it without an upload.
+    MirrorGroup& gm = *grads[0]->mirror();
+    const bool from_host = gm.state == 2 && gm.host_dev && gm.zeros.empty();
+    float* gd = from_host ? static_cast<float*>(gm.host_dev)
+                          : static_cast<float*>(grads[0]->device_data()) - grads[0]->mirror_offset() / 4;
     mft_check(mft_adam_step(detail::handle(), pd, gd, static_cast<float*>(gs.m->device_data()),
                             static_cast<float*>(gs.v->device_data()), (int64_t)(pg->bytes / 4), cfg_.learning_rate,
                             cfg_.beta1, cfg_.beta2, cfg_.epsilon, cfg_.weight_decay, t_, nullptr, 0),
               "mft_adam_step");
+    if (from_host) mark_host_read(gm);
     params[0]->mark_device_written();
     return;
   }

@@ -251,6 +251,28 @@ static void driver_loop(const std::string& tag, EngineModel& model, orc_model* o
       std::memcpy(trainable[i]->data<float>(), o, trainable[i]->numel() * sizeof(float));
     }
   }
+  // Host edits of the gradients, then zero_grad() of one member only: the
+  // fill must not lose the other members' edits (they reach the device
+  // first), while a zero_grad() of every member needs no upload.
+  if (trainable.size() >= 2) {
+    for (size_t i = 0; i < trainable.size(); ++i) {
+      float* g = trainable[i]->grad()->data<float>();
+      for (int64_t j = 0; j < trainable[i]->numel(); ++j) g[j] = 0.25f * (float)(i + 1) + 1e-3f * (float)(j % 97);
+    }
+    trainable[0]->zero_grad();
+    auto dev_scaled = mul(trainable[1]->grad(), 2.f);  // reads the device copy
+    const float* d = dev_scaled->data<float>();
+    const float* h = trainable[1]->grad()->data<float>();
+    const float* z = trainable[0]->grad()->data<float>();
+    double e = 0;
+    for (int64_t j = 0; j < trainable[1]->numel(); ++j) {
+      const float want = 0.5f + 1e-3f * (float)(j % 97);
+      e = std::max(e, (double)std::fabs(h[j] - want) + std::fabs(d[j] - 2.f * want));
+    }
+    for (int64_t j = 0; j < trainable[0]->numel(); ++j) e = std::max(e, (double)std::fabs(z[j]));
+    check(tag + " partial zero_grad keeps host edits", e, 0.0);
+    for (auto& p : trainable) p->zero_grad();
+  }
 }
 
 
