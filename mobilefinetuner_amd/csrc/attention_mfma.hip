@@ -579,13 +579,13 @@ __device__ __forceinline__ void attn_bwd_dkdv_role(const AttnP& p, int bid, floa
 // dK/dV[b,s,kh,:] = Σ_{c} Σ_{j<grp} partial[c][b,s,kh·grp+j,:], in (c, j)
 // order over the query chunks c the key's block was given (same range test
 // as the dK/dV kernel; c = 0 only without a split).
+// Workgroup blk of nblk (256 threads) takes a grid-stride share.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_partial_sum_kernel(AttnP p, int bkeys) {
+__device__ __forceinline__ void partial_sum_role(const AttnP& p, int bkeys, int blk, int nblk) {
   const int grp = p.Hq / p.Hkv;
   const int64_t BS = (int64_t)p.B * p.S;
   const int64_t total = BS * p.Hkv * (HD / 4);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t i = (int64_t)blk * 256 + threadIdx.x; i < total; i += (int64_t)nblk * 256) {
     const int c4 = (int)(i % (HD / 4));
     const int64_t r = i / (HD / 4);
     const int kh = (int)(r % p.Hkv);
@@ -624,14 +624,19 @@ __global__ __launch_bounds__(256) void attn_partial_sum_kernel(AttnP p, int bkey
     *reinterpret_cast<floatx4*>(p.dv + tok * p.dv_rs + (int64_t)kh * HD + 4 * c4) = sv;
   }
 }
+template <int HD>
+__global__ __launch_bounds__(256) void attn_partial_sum_kernel(AttnP p, int bkeys) {
+  partial_sum_role<HD>(p, bkeys, blockIdx.x, gridDim.x);
+}
 
 // dQ[b,s,h,:] = scale · Σ_c partial[c][b,s,h,:] over the key chunks c the
 // query's block was given (same range test as the dQ kernel), in c order.
+// Workgroup blk (256 threads) takes 256 consecutive float4 columns.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_dq_sum_kernel(AttnP p, int qblock) {
+__device__ __forceinline__ void dq_sum_role(const AttnP& p, int qblock, int blk) {
   const int64_t BS = (int64_t)p.B * p.S;
   const int64_t total = BS * p.Hq * (HD / 4);
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = (int64_t)blk * 256 + threadIdx.x;
   if (i >= total) return;
   const int c4 = (int)(i % (HD / 4));
   const int64_t r = i / (HD / 4);  // tok·Hq + h
@@ -645,6 +650,17 @@ __global__ __launch_bounds__(256) void attn_dq_sum_kernel(AttnP p, int qblock) {
   for (int c = jmin / p.ckq; c <= jmax / p.ckq; ++c)
     s += *reinterpret_cast<const floatx4*>(p.pdq + (((int64_t)c * BS + tok) * p.Hq + h) * HD + 4 * c4);
   *reinterpret_cast<floatx4*>(p.dq + tok * p.dq_rs + (int64_t)h * HD + 4 * c4) = s * p.scale;
+}
+template <int HD>
+__global__ __launch_bounds__(256) void attn_dq_sum_kernel(AttnP p, int qblock) {
+  dq_sum_role<HD>(p, qblock, blockIdx.x);
+}
+// Both sums of a chunked backward in one launch: workgroups [0, nkv) sum
+// the dK/dV partials, the rest the dQ partials (independent outputs).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_sums_kernel(AttnP p, int bkeys, int qblock, int nkv) {
+  if ((int)blockIdx.x < nkv) partial_sum_role<HD>(p, bkeys, blockIdx.x, nkv);
+  else dq_sum_role<HD>(p, qblock, (int)blockIdx.x - nkv);
 }
 
 // ------------------------------------------------------------------------------
@@ -1994,15 +2010,15 @@ void bwd_short256_launch(hipStream_t s, AttnP& p) {
   hipLaunchKernelGGL(attn_bwd_short256, dim3((unsigned)(2 * tiles * nch)), dim3(64 * kS256W), kS256Lds, s, p,
                      tiles * nch);
   MFT_LAUNCH_CHECK();
-  if (p.Hq != p.Hkv || nch > 1) {
-    const int64_t total = (int64_t)p.B * p.S * p.Hkv * (256 / 4);
-    hipLaunchKernelGGL(attn_partial_sum_kernel<256>, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 4096)),
-                       dim3(256), 0, s, p, 16);
+  const int64_t kv_total = (int64_t)p.B * p.S * p.Hkv * (256 / 4);
+  const int nkv = (int)std::min<int64_t>(cdiv(kv_total, 256), 4096);
+  if (nch > 1) {  // dK/dV and dQ partials, summed in one launch
+    const int64_t q_total = (int64_t)p.B * p.S * p.Hq * (256 / 4);
+    hipLaunchKernelGGL(attn_sums_kernel<256>, dim3((unsigned)(nkv + cdiv(q_total, 256))), dim3(256), 0, s, p, 16, 16,
+                       nkv);
     MFT_LAUNCH_CHECK();
-  }
-  if (nch > 1) {
-    const int64_t total = (int64_t)p.B * p.S * p.Hq * (256 / 4);
-    hipLaunchKernelGGL(attn_dq_sum_kernel<256>, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, 16);
+  } else if (p.Hq != p.Hkv) {
+    hipLaunchKernelGGL(attn_partial_sum_kernel<256>, dim3((unsigned)nkv), dim3(256), 0, s, p, 16);
     MFT_LAUNCH_CHECK();
   }
 }
