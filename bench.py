@@ -190,7 +190,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+                          "(the multi-GPU sharding is a design, not built or run)"}))
         sys.exit(2)
     if args.op:
         return op_bench(args)
