@@ -491,19 +491,46 @@ void shard_free(ShardStore& sh, int64_t off, int64_t bytes) {
   }
 }
 
-// Makes entry i resident: evicts the least recently used entries no launch
-// holds until a first-fit block is free, then copies the tensor on the copy
-// stream, behind the last uses of every evicted block.  When nothing more can
-// be evicted, a prefetch returns false (the use will load it); a use throws.
+// Uses until entry j is next needed, counted from use position pos of the
+// current pass, read off the previous pass's order (a step repeats its use
+// order): positions pos.. of this pass, then the next pass from its start;
+// a large value when the previous pass never used it.
+int64_t shard_next_use(const ShardStore& sh, int j, size_t pos) {
+  const size_t n = sh.prev.size();
+  for (size_t q = pos; q < n; ++q)
+    if (sh.prev[q] == j) return (int64_t)(q - pos);
+  for (size_t q = 0; q < std::min(pos, n); ++q)
+    if (sh.prev[q] == j) return (int64_t)(n - pos + q);
+  return INT64_MAX / 2;
+}
+
+// Makes entry i resident: evicts entries no launch holds until a first-fit
+// block is free — the one needed furthest ahead in the step's use order
+// (Belady's rule over the previous pass's order; least recently used while
+// there is no previous pass) — then copies the tensor on the copy stream,
+// behind the last uses of every evicted block.  When nothing more can be
+// evicted, a prefetch returns false (the use will load it); a use throws.
+// Tuning hook: MFT_SHARD_LRU=1 evicts least recently used entries always.
 bool shard_load(mft_model_s* m, int i, bool prefetch = false) {
+  static const bool lru_only = [] {
+    const char* e = getenv("MFT_SHARD_LRU");
+    return e && atoi(e) != 0;
+  }();
   ShardStore& sh = m->sh;
   const size_t need = shard_round(sh.ents[i].bytes);
+  const size_t pos = sh.seq.size();  // this pass's position of the use being served
   int64_t off;
   while ((off = shard_alloc(sh, need)) < 0) {
     int v = -1;
+    int64_t v_next = -1;
     for (int j = 0; j < (int)sh.ents.size(); ++j) {
       const ShardStore::Entry& c = sh.ents[j];
-      if (j != i && c.off >= 0 && !c.held && (v < 0 || c.last < sh.ents[v].last)) v = j;
+      if (j == i || c.off < 0 || c.held) continue;
+      const int64_t nx = lru_only || sh.prev.empty() ? 0 : shard_next_use(sh, j, pos);
+      if (v < 0 || nx > v_next || (nx == v_next && c.last < sh.ents[v].last)) {
+        v = j;
+        v_next = nx;
+      }
     }
     if (v < 0) {
       if (prefetch) return false;
