@@ -67,6 +67,10 @@ def parse():
                     help="stream the frozen linear weights and the token embedding from pinned host "
                          "memory through an HBM pool of this size (the reference's --shard_budget_mb); "
                          "0 keeps every weight resident")
+    ap.add_argument("--w-fp16", action="store_true",
+                    help="store the frozen weights as fp16 (rounded to nearest even), as the reference's "
+                         "sharder does with --shard_fp16_disk 1; the GEMMs then run on the fp16 matrix cores. "
+                         "Changes the model's numerics: not the fp32 configs' headline")
     return ap.parse_args()
 
 
@@ -213,9 +217,12 @@ def main():
                                             Model)
     rc = CONFIGS[args.config]
     mc = rc.model
-    if args.shard_budget_mb > 0:
+    if args.shard_budget_mb > 0 or args.w_fp16:
         import dataclasses
-        mc = dataclasses.replace(mc, shard_budget=int(args.shard_budget_mb * (1 << 20)))
+        if args.shard_budget_mb > 0:
+            mc = dataclasses.replace(mc, shard_budget=int(args.shard_budget_mb * (1 << 20)))
+        if args.w_fp16:
+            mc = dataclasses.replace(mc, w_fp16=1)
     torch.cuda.set_device(0)
     tokens = rc.tokens_per_step
     model = Model(mc, tokens)

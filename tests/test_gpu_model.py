@@ -40,6 +40,11 @@ SMALL = {
                       query_pre_attn_scalar=256), 2, 40, 1),
     "gemma3-fp16w": (gemma3(2, 128, 2, 1, 256, 320, vocab=611, name="gemma-t16", w_fp16=1,
                             sliding_window=512, query_pre_attn_scalar=256), 2, 32, 2),
+    # fp16-stored W (the reference sharder's --shard_fp16_disk storage) on the
+    # other families: biases, LayerNorm, GELU epilogues and the tied fp16
+    # embedding on the fp16 matrix-core GEMMs.
+    "gpt2-fp16w": (gpt2(2, 256, 4, vocab=1000, max_pos=128, name="gpt2-t16", w_fp16=1), 2, 48, 2),
+    "qwen2-fp16w": (qwen2(2, 256, 4, 2, 64, 384, vocab=997, name="qwen-t16", w_fp16=1), 2, 64, 1),
     # LoRA on q and v only: q, k and v stay separate GEMMs (the fused q|k|v
     # projection needs adapters on all three); Qwen2 with biases, Gemma3 with
     # the per-head q/k norms on unfused buffers.
