@@ -459,15 +459,15 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
   // K is a multiple of 4 (checked on the host), so a 4-vector never crosses a row.
   // The K-split form unrolls deeper: its few workgroups (one job of 4-row
   // groups) leave the loads of several steps to cover the memory latency.
+  if (jb.y_rk) {  // Y [r, K]: a lane takes 4-wide chunks of K, one 128-bit Y load per rank
 #pragma unroll(KS == 1 ? 2 : 4)
-  for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
-    floatx4 xv[RW];
+    for (int k = 4 * lane + (KS == 1 ? 0 : 256 * w); k < K; k += 256 * KS) {
+      floatx4 xv[RW];
 #pragma unroll
-    for (int q = 0; q < RW; ++q) {
-      xv[q] = ldg(reinterpret_cast<const floatx4*>(xr[q] + k));
-      mx[q] = fmaxf(mx[q], fmaxf(fmaxf(fabsf(xv[q][0]), fabsf(xv[q][1])), fmaxf(fabsf(xv[q][2]), fabsf(xv[q][3]))));
-    }
-    if (jb.y_rk) {  // Y [r, K]
+      for (int q = 0; q < RW; ++q) {
+        xv[q] = ldg(reinterpret_cast<const floatx4*>(xr[q] + k));
+        mx[q] = fmaxf(mx[q], fmaxf(fmaxf(fabsf(xv[q][0]), fabsf(xv[q][1])), fmaxf(fabsf(xv[q][2]), fabsf(xv[q][3]))));
+      }
 #pragma unroll
       for (int j = 0; j < R; ++j) {
         const floatx4 y = ldg(reinterpret_cast<const floatx4*>(jb.Y + (int64_t)j * K + k));
@@ -476,17 +476,40 @@ __device__ __forceinline__ void batch_proj(const RankJob& jb, int b, int M, floa
 #pragma unroll
           for (int t = 0; t < 4; ++t) acc[q][j] = fmaf(xv[q][t], y[t], acc[q][j]);
       }
-    } else {  // Y [K, r]: rows k..k+3 are 4·r consecutive floats
-      const floatx4* yp = reinterpret_cast<const floatx4*>(jb.Y + (int64_t)k * R);
+    }
+  } else {
+    // Y [K, r]: a lane takes single columns k, E at a time, so that a wave's
+    // Y reads (r consecutive floats per column) are contiguous across lanes;
+    // with 4-wide chunks the lanes' Y reads would sit 4·r floats apart, a
+    // cache line per lane per load
+    constexpr int E = 4, KSTEP = 64 * KS;
+    for (int k0 = lane + (KS == 1 ? 0 : 64 * w); k0 < K; k0 += KSTEP * E) {
+      float xs[E][RW];
+      floatx4 ys[E][R / 4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int e = 0; e < E; ++e) {
+        const int k = k0 + KSTEP * e;
+        if (k < K) {
 #pragma unroll
-        for (int jq = 0; jq < R / 4; ++jq) {
-          const floatx4 y = ldg(yp + t * (R / 4) + jq);
+          for (int q = 0; q < RW; ++q) xs[e][q] = ldg(xr[q] + k);
 #pragma unroll
-          for (int q = 0; q < RW; ++q)
+          for (int jq = 0; jq < R / 4; ++jq) ys[e][jq] = ldg(reinterpret_cast<const floatx4*>(jb.Y + (int64_t)k * R) + jq);
+        } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[q][4 * jq + e] = fmaf(xv[q][t], y[e], acc[q][4 * jq + e]);
+          for (int q = 0; q < RW; ++q) xs[e][q] = 0.f;
+#pragma unroll
+          for (int jq = 0; jq < R / 4; ++jq) ys[e][jq] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+#pragma unroll
+        for (int q = 0; q < RW; ++q) {
+          mx[q] = fmaxf(mx[q], fabsf(xs[e][q]));
+#pragma unroll
+          for (int jq = 0; jq < R / 4; ++jq)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[q][4 * jq + u] = fmaf(xs[e][q], ys[e][jq][u], acc[q][4 * jq + u]);
         }
     }
   }
