@@ -334,9 +334,9 @@ __global__ __launch_bounds__(64 * kOuterWaves) void rank_outer_mfma(OuterArgs a)
 // ---- batched LoRA work ---------------------------------------------------------
 // W_eff[k][n] = W[k][n] + scale·Σ_j A[j][k]·B[n][j].  A workgroup owns
 // kMergeRows·4 rows × 256 columns of one job; a thread takes kMergeRows rows ×
-// 4 columns (the A values of its rows are wave-uniform, its B rows are 4·R
-// contiguous floats, reused over all its rows).  HBM-bound: reads W once,
-// writes W_eff once.
+// 4 columns (the A values of its rows are wave-uniform, the B values of its
+// columns come from the tile's B rows staged in LDS, reused over all its
+// rows).  HBM-bound: reads W once, writes W_eff once.
 constexpr int kMergeRows = 8;
 template <int R>
 __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restrict__ jobs, int njobs, float scale) {
@@ -351,28 +351,41 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const MergeJob* __restr
   const int tiles_n = (jb.N + 255) / 256;
   const int tt = t - jb.tile0;
   const int k0 = (tt / tiles_n) * (4 * kMergeRows) + kMergeRows * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n = (tt % tiles_n) * 256 + 4 * (threadIdx.x & 63);
-  if (n >= jb.N) return;
+  const int nb = (tt % tiles_n) * 256, n = nb + 4 * (threadIdx.x & 63);
+  const bool nok = n < jb.N;  // N is a multiple of 4
   // All rows' W loads are issued before any is used (rows past K re-read
   // row K-1 and are not stored), so each thread has kMergeRows loads in flight.
   floatx4 w[kMergeRows];
 #pragma unroll
   for (int q = 0; q < kMergeRows; ++q) {
     const int k = min(k0 + q, jb.K - 1);
+    const int64_t at = (int64_t)k * jb.N + (nok ? n : 0);
     if (jb.f16)
-      w[q] = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + (int64_t)k * jb.N + n));
+      w[q] = widen4(*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(jb.W) + at));
     else
-      w[q] = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + (int64_t)k * jb.N + n);
+      w[q] = *reinterpret_cast<const floatx4*>(static_cast<const float*>(jb.W) + at);
   }
+  // The tile's 256 rows of B ([N][R]) are read once, coalesced, and staged
+  // transposed (bt[j][column]); a lane then takes its four columns of rank j
+  // as one 128-bit LDS read (read straight from B, the lanes' four rows sit
+  // 4·R floats apart: a cache line per lane per load).
+  __shared__ float bt[R][256 + 4];
+  for (int f = threadIdx.x; f < 64 * R; f += 256) {
+    const int c = (4 * f) / R, j0 = (4 * f) % R;
+    const floatx4 v = nb + c < jb.N ? *reinterpret_cast<const floatx4*>(jb.B + (int64_t)(nb + c) * R + j0)
+                                    : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bt[j0 + u][c] = v[u];
+  }
+  __syncthreads();
+  if (!nok) return;
   float bv[4][R];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
+  for (int j = 0; j < R; ++j) {
+    const floatx4 b4 = *reinterpret_cast<const floatx4*>(&bt[j][4 * (threadIdx.x & 63)]);
 #pragma unroll
-    for (int j4 = 0; j4 < R / 4; ++j4) {
-      const floatx4 b4 = *reinterpret_cast<const floatx4*>(jb.B + (int64_t)(n + e) * R + 4 * j4);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) bv[e][4 * j4 + u] = b4[u];
-    }
+    for (int e = 0; e < 4; ++e) bv[e][j] = b4[e];
+  }
 #pragma unroll
   for (int q = 0; q < kMergeRows; ++q) {
     const int k = k0 + q;
