@@ -45,6 +45,13 @@ SMALL = {
     # embedding on the fp16 matrix-core GEMMs.
     "gpt2-fp16w": (gpt2(2, 256, 4, vocab=1000, max_pos=128, name="gpt2-t16", w_fp16=1), 2, 48, 2),
     "qwen2-fp16w": (qwen2(2, 256, 4, 2, 64, 384, vocab=997, name="qwen-t16", w_fp16=1), 2, 64, 1),
+    # LoRA ranks other than 8 through the step engine's batched rank-r
+    # kernels (projections, outer products, the merge; on fp16 W the
+    # per-layer projection groups)
+    "gpt2-r16": (gpt2(2, 256, 4, vocab=1000, max_pos=128, name="gpt2-r16", lora_r=16), 2, 48, 1),
+    "qwen2-r32": (qwen2(2, 256, 4, 2, 64, 384, vocab=997, name="qwen-r32", lora_r=32), 2, 64, 1),
+    "gemma3-fp16w-r4": (gemma3(2, 128, 2, 1, 256, 320, vocab=611, name="gemma-t16r4", w_fp16=1, lora_r=4,
+                               sliding_window=512, query_pre_attn_scalar=256), 2, 32, 1),
     # LoRA on q and v only: q, k and v stay separate GEMMs (the fused q|k|v
     # projection needs adapters on all three); Qwen2 with biases, Gemma3 with
     # the per-head q/k norms on unfused buffers.
