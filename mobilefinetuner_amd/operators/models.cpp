@@ -43,8 +43,13 @@ struct EngineState {
   // strong one here would be a cycle through the views' owner pointer)
   std::vector<std::weak_ptr<Tensor>> views, grad_views;
   uint64_t generation = 0;                   // forwards run so far
+  // Pinned (Σ NLL, count) slots the loss launch adds into, read once the
+  // stream has drained: no fill or copy launch around the loss read-back.
+  void* loss_host = nullptr;
+  void* loss_dev = nullptr;  // loss_host as kernels address it
   ~EngineState() {
     if (m) (void)mft_model_destroy(m);
+    if (loss_host) (void)hipHostFree(loss_host);
   }
 };
 
@@ -65,14 +70,33 @@ std::unordered_map<const Tensor*, LogitsCtx>& logits_registry() {
 
 const int32_t* labels_ptr(const TensorPtr& labels) { return static_cast<const int32_t*>(labels->device_data()); }
 
-// Summed NLL and valid count of the engine's current logits (device scalars
-// zeroed first, read back after the launch).
+// Summed NLL and valid count of the engine's current logits (slots zeroed
+// first, read back after the launch).
 void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int ignore, float upstream, bool sum,
               bool backward, double* ls, int64_t* nv) {
   if (!ls && !nv) {  // dlogits only: no loss slots to clear or read
     mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
                            nullptr, nullptr),
               "mft_model_ce");
+    return;
+  }
+  if (!st->loss_host) {
+    hip_check(hipHostMalloc(&st->loss_host, 16, hipHostMallocDefault), "hipHostMalloc");
+    if (hipHostGetDevicePointer(&st->loss_dev, st->loss_host, 0) != hipSuccess) {
+      st->loss_dev = nullptr;
+      (void)hipGetLastError();
+    }
+  }
+  if (st->loss_dev) {
+    // the previous read-back drained the stream, so no launch still writes the slots
+    std::memset(st->loss_host, 0, 16);
+    char* p = static_cast<char*>(st->loss_dev);
+    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
+                           reinterpret_cast<double*>(p), reinterpret_cast<int64_t*>(p + 8)),
+              "mft_model_ce");
+    hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+    if (ls) std::memcpy(ls, st->loss_host, 8);
+    if (nv) std::memcpy(nv, static_cast<const char*>(st->loss_host) + 8, 8);
     return;
   }
   auto stats = std::make_shared<Tensor>(std::vector<int64_t>{4}, kFloat32, kGPU);
