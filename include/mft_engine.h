@@ -117,11 +117,16 @@ int mft_model_forward(mft_model m, const int32_t* ids, const float* mask,
  * logits buffer [nseq*S rows, row pitch ld ≥ vocab].  mft_model_ce adds the
  * summed NLL and the valid-target count of that forward's logits to the
  * DEVICE scalars loss_sum / n_valid (labels: device int32 [nseq*S], HF shift,
- * ignore_index); with backward != 0 it also overwrites the logits with
+ * ignore_index); with backward = 1 it also overwrites the logits with
  * dlogits = upstream·(softmax − onehot)/norm (norm = norm_count if > 0, else
  * the valid count), after which mft_model_backward accumulates the LoRA
- * gradients.  loss_sum and n_valid may both be NULL (dlogits only; nothing
- * is summed).  Asynchronous. */
+ * gradients.  backward = 2 forms those dlogits in a second buffer of the
+ * logits' size (allocated at the first such call) and keeps the logits; a
+ * later backward = 1 call for the same forward with the same upstream and
+ * NULL loss_sum / n_valid then adopts them without a second pass (the two
+ * buffers trade places: mft_model_logits afterwards returns the other one).
+ * loss_sum and n_valid may both be NULL (dlogits only; nothing is summed).
+ * Asynchronous. */
 int mft_model_forward_train(mft_model m, const int32_t* ids, const float* mask,
                             int nseq, int S);
 int mft_model_logits(mft_model m, float** logits, int64_t* ld);

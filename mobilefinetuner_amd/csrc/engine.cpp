@@ -267,6 +267,13 @@ struct mft_model_s {
   // kept (0 = none) and whether its logits buffer now holds dlogits
   int api_nseq = 0, api_S = 0;
   bool api_dlogits = false;
+  // dlogits formed beside the logits by mft_model_ce(backward = 2) for the
+  // pending forward (upstream factor alt_up), adopted by its backward = 1
+  // call: the two buffers trade places
+  float* logits_alt = nullptr;
+  void* logits_alt_mem = nullptr;  // the allocation (either buffer may be the one in use)
+  bool alt_ready = false;
+  float alt_up = 0.f;
   int64_t last_rows = 0;  // token rows of the last forward (activation accessor)
   // captured train-step graph
   hipStream_t cap_stream = nullptr;
@@ -1544,6 +1551,7 @@ void forward(mft_model_s* m, const int32_t* ids, const float* mask, int nseq, in
   const mft_model_cfg& c = m->c;
   for (auto& kv : m->kept_grad) kv.second.rows = 0;  // retained gradients belong to one step
   m->dl_rs_fresh = false;                              // new logits: no dlogits scales yet
+  m->alt_ready = false;
   m->fwd_dropout = train && c.lora_dropout > 0.f && c.lora_r > 0 && c.lora_mask != 0;
   m->drop_n_fwd = n_fwd;
   m->drop_rows = (int64_t)(nseq / n_fwd) * S;
@@ -2183,7 +2191,7 @@ int mft_model_destroy(mft_model m) {
       for (auto& kv : *km)
         if (kv.second.p) (void)hipFree(kv.second.p);
     void* bufs[] = {m->frozen, m->lora_p, m->lora_g, m->lora_m, m->lora_v, m->act_mem, (void*)m->d_loss,
-                    m->weff_mem, m->tables, m->rscale};
+                    m->weff_mem, m->tables, m->rscale, m->logits_alt_mem};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     ShardStore& sh = m->sh;
@@ -2327,11 +2335,36 @@ int mft_model_ce(mft_model m, const int32_t* labels, int nseq, int S, int ignore
     if (nseq != m->api_nseq || S != m->api_S || nseq <= 0)
       throw Error(MFT_EINVAL, "mft_model_ce: no forward of this shape is pending");
     if (m->api_dlogits) throw Error(MFT_EINVAL, "mft_model_ce: the logits were already turned into dlogits");
+    if (backward == 2) {  // the loss, and the dlogits beside the logits
+      if (!m->logits_alt) {
+        const size_t bytes = sizeof(float) * (size_t)m->max_tokens * m->ldv;
+        if (hipMalloc(&m->logits_alt_mem, bytes) != hipSuccess)
+          throw Error(MFT_ENOMEM, "second logits buffer (" + std::to_string(bytes) + " bytes)");
+        m->logits_alt = static_cast<float*>(m->logits_alt_mem);
+        // its padding columns must stay finite, as the logits buffer's
+        MFT_HIP(hipMemsetAsync(m->logits_alt, 0, bytes, m->stream));
+      }
+      ce_fwd_bwd(m->stream, m->logits, labels, nseq, S, m->c.vocab, m->ldv, ignore_index, upstream, norm_count,
+                 loss_sum, n_valid, m->logits_alt, m->row_nll, m->d_tmpcnt, m->d_err + 1, nullptr, 0, m->dl_rscale);
+      m->alt_ready = true;
+      m->alt_up = upstream;
+      return;
+    }
+    if (backward && m->alt_ready && m->alt_up == upstream && !loss_sum && !n_valid) {
+      // adopt the dlogits formed with the loss: no second pass over the logits
+      std::swap(m->logits, m->logits_alt);
+      drop_graph(m);  // a captured step holds the other buffer's address
+      m->alt_ready = false;
+      m->api_dlogits = true;
+      m->dl_rs_fresh = m->dl_rscale != nullptr;
+      return;
+    }
     ce_fwd_bwd(m->stream, m->logits, labels, nseq, S, m->c.vocab, m->ldv, ignore_index, upstream, norm_count,
                loss_sum, n_valid, backward ? m->logits : nullptr, m->row_nll, m->d_tmpcnt, m->d_err + 1, nullptr, 0,
                backward && m->dl_rscale ? m->dl_rscale : nullptr);
     if (backward) {
       m->api_dlogits = true;
+      m->alt_ready = false;
       m->dl_rs_fresh = m->dl_rscale != nullptr;
     }
   });

@@ -47,6 +47,9 @@ struct EngineState {
   // stream has drained: no fill or copy launch around the loss read-back.
   void* loss_host = nullptr;
   void* loss_dev = nullptr;  // loss_host as kernels address it
+  // upstream gradient of the last loss backward: the factor the next loss
+  // forms its dlogits with beside the logits (the drivers' 1/accum repeats)
+  float last_up = 1.f;
   ~EngineState() {
     if (m) (void)mft_model_destroy(m);
     if (loss_host) (void)hipHostFree(loss_host);
@@ -71,12 +74,14 @@ std::unordered_map<const Tensor*, LogitsCtx>& logits_registry() {
 const int32_t* labels_ptr(const TensorPtr& labels) { return static_cast<const int32_t*>(labels->device_data()); }
 
 // Summed NLL and valid count of the engine's current logits (slots zeroed
-// first, read back after the launch).
+// first, read back after the launch).  mode: 0 loss only, 1 dlogits in place
+// of the logits, 2 the loss and the dlogits for `upstream` beside the logits
+// (taken up by the mode-1 call of the backward when its factor matches).
 void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int ignore, float upstream, bool sum,
-              bool backward, double* ls, int64_t* nv) {
+              int mode, double* ls, int64_t* nv) {
   if (!ls && !nv) {  // dlogits only: no loss slots to clear or read
-    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
-                           nullptr, nullptr),
+    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, mode, nullptr,
+                           nullptr),
               "mft_model_ce");
     return;
   }
@@ -91,7 +96,7 @@ void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int 
     // the previous read-back drained the stream, so no launch still writes the slots
     std::memset(st->loss_host, 0, 16);
     char* p = static_cast<char*>(st->loss_dev);
-    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
+    mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, mode,
                            reinterpret_cast<double*>(p), reinterpret_cast<int64_t*>(p + 8)),
               "mft_model_ce");
     hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
@@ -101,7 +106,7 @@ void model_ce(EngineState* st, const LogitsCtx& c, const TensorPtr& labels, int 
   }
   auto stats = std::make_shared<Tensor>(std::vector<int64_t>{4}, kFloat32, kGPU);
   char* p = static_cast<char*>(stats->device_data());
-  mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, backward ? 1 : 0,
+  mft_check(mft_model_ce(st->m, labels_ptr(labels), c.B, c.S, ignore, upstream, sum ? 1 : 0, mode,
                          reinterpret_cast<double*>(p), reinterpret_cast<int64_t*>(p + 8)),
             "mft_model_ce");
   char buf[16];  // loss sum and count are adjacent: one read-back
@@ -125,7 +130,8 @@ struct ModelLossNode : autograd::Node {
     if (st->generation != ctx.generation)
       throw std::runtime_error("backward: the model ran another forward since this loss was computed");
     const float up = detail::read_scalar(g);
-    model_ce(st.get(), ctx, labels, ignore, up, sum, true, nullptr, nullptr);  // the loss was read at the forward
+    st->last_up = up;
+    model_ce(st.get(), ctx, labels, ignore, up, sum, 1, nullptr, nullptr);  // the loss was read at the forward
     // logits->retain_grad(): the gradient the CE just wrote over the logits
     // buffer is copied out before the backward consumes it
     if (auto lg = logits.lock())
@@ -175,9 +181,13 @@ ModelLoss model_loss_hook(const TensorPtr& logits) {
     if (labels->numel() != (int64_t)ctx.B * ctx.S) throw std::invalid_argument("lm_cross_entropy: labels must be [B, S]");
     double ls;
     int64_t nv;
-    model_ce(st.get(), ctx, labels, ignore, 1.f, sum, false, &ls, &nv);
+    // a loss the tape records is most likely backpropagated: its dlogits are
+    // formed in the same pass over the logits, for the factor the last
+    // backward brought (the backward recomputes them if its factor differs)
+    const bool recorded = ctx.trainable && autograd::Engine::instance().is_enabled();
+    model_ce(st.get(), ctx, labels, ignore, recorded ? st->last_up : 1.f, sum, recorded ? 2 : 0, &ls, &nv);
     auto loss = make_loss(ls, nv, sum);
-    if (ctx.trainable && autograd::Engine::instance().is_enabled()) {
+    if (recorded) {
       auto n = std::make_shared<ModelLossNode>();
       n->st = st;
       n->ctx = ctx;
